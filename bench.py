@@ -1,0 +1,242 @@
+"""Benchmark of the quantized-linear forward path on one MI355X.
+
+Prints ONE JSON line.  ``value`` is the headline W4A16 g128 GEMV at M=1
+(K=N=4096, the BASELINE metric's first figure) in TB/s of algorithmic bytes,
+with the weights rotated over >= 64 distinct copies (>= 571 MB) so the 256 MB
+Infinity Cache cannot serve them; inputs are resident in HBM before timing.
+The other legs of the metric (W8A8 int8 GEMM TOPS at M=4096, the W8A8 sweep,
+W4A16 M=16, the Mixtral-shaped MoE chain) are reported under ``legs``, each
+with its own roofline fraction.  Timing uses HIP events recorded on the stream
+the kernels are launched on (torch's current stream), bracketed by
+``torch.cuda.synchronize()``.
+
+``cpu_baseline``: the oracle's restatement of the reference CPU fake-quant
+forward (``F.linear`` on AWQ pseudo-quantized fp16 weights) timed on this
+host's cores for a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, published (POPS x 1000)
+FP16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 MFMA, published
+
+METRIC = "qlinear HBM TB/s (W4A16, M=1) & int8 TOPS (W8A8, M=4096); 7B decode tok/s"
+
+
+def _log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _time_launches(fn, n_launch, warmup):
+    """Average wall time per launch over n_launch back-to-back launches (ms), HIP events
+    on the current stream."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(n_launch):
+        fn(i)
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n_launch
+
+
+def _roof(bound, achieved, peak, unit, traffic=None):
+    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def leg_w4a16(ops, m, n, k, steps, warmup, copies=64, g=128):
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).half()
+    packed, s, z, _ = ops.w4_quantize_awq(w, g, True, return_deq=False)
+    del w
+    pk = [packed.clone() for _ in range(copies)]
+    sc = [s.clone() for _ in range(copies)]
+    zr = [z.clone() for _ in range(copies)]
+    gx = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(m, k, generator=gx, device="cuda").half()
+    y = ops.w4a16_gemm(x, pk[0], sc[0], zr[0], g, None)
+    ms = _time_launches(lambda i: ops.w4a16_gemm(x, pk[i % copies], sc[i % copies], zr[i % copies], g, None),
+                        steps, warmup)
+    nbytes = n * k // 2 + 2 * n * (k // g) * 2 + m * k * 2 + m * n * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del pk, sc, zr
+    torch.cuda.empty_cache()
+    return {"m": m, "n": n, "k": k, "group": g, "ms_per_call": ms, "bytes_per_call": nbytes,
+            "tb_s": gbs / 1000.0, "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s"),
+            "weight_copies": copies}, y
+
+
+def leg_w8a8(ops, m, n, k, steps, warmup):
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).half()
+    qw, sw, _ = ops.w8_quantize_per_channel(w, "export")
+    del w
+    copies = max(1, min(16, int(600e6 // (n * k))))  # rotate weights past the Infinity Cache when HBM-bound
+    qws = [qw.clone() for _ in range(copies)] if m <= 256 else [qw]
+    gx = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(m, k, generator=gx, device="cuda")
+    idx = torch.randperm(k, generator=torch.Generator().manual_seed(2))[: max(1, round(k * 0.01))]
+    x[:, idx.cuda()] *= 20
+    x = x.half()
+    q, st = ops.quant_per_token_i8(x)
+    nc = len(qws)
+    ms = _time_launches(lambda i: ops.w8a8_gemm(q, st, qws[i % nc], sw, None, torch.float16), steps, warmup)
+    ms_q = _time_launches(lambda i: ops.quant_per_token_i8(x), steps, warmup)
+    ops_count = 2.0 * m * n * k
+    nbytes = n * k + m * k + m * n * 2 + 4 * n + 4 * m
+    tops = ops_count / (ms * 1e-3) / 1e12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {"m": m, "n": n, "k": k, "ms_gemm": ms, "ms_quant": ms_q, "ms_e2e": ms + ms_q, "tops": tops,
+           "tops_e2e": ops_count / ((ms + ms_q) * 1e-3) / 1e12, "gb_s": gbs, "weight_copies": nc}
+    if m >= 1024:
+        out["roofline"] = _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS")
+    elif m <= 16:
+        out["roofline"] = _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s")
+    else:
+        out["roofline"] = _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s")
+        out["roofline_mfma"] = _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS")
+    del qws
+    torch.cuda.empty_cache()
+    return out
+
+
+def leg_moe(ops, steps, warmup, t=512, h=4096, inter=14336, e=8, top_k=2):
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    q13 = torch.empty((e, 2 * inter, h), dtype=torch.int8, device="cuda")
+    s13 = torch.empty((e, 2 * inter), dtype=torch.float32, device="cuda")
+    q2 = torch.empty((e, h, inter), dtype=torch.int8, device="cuda")
+    s2 = torch.empty((e, h), dtype=torch.float32, device="cuda")
+    for i in range(e):
+        w = (torch.randn(2 * inter, h, generator=gen, device="cuda") * 0.02).half()
+        q13[i], s13[i], _ = ops.w8_quantize_per_channel(w, "export")
+        w = (torch.randn(h, inter, generator=gen, device="cuda") * 0.02).half()
+        q2[i], s2[i], _ = ops.w8_quantize_per_channel(w, "export")
+    del w
+    gx = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(t, h, generator=gx, device="cuda").half()
+    logits = torch.randn(t, e, generator=torch.Generator().manual_seed(3)).float()
+    p = torch.softmax(logits, dim=-1)
+    tw, ids = torch.topk(p, top_k, dim=-1)
+    tw = (tw / tw.sum(-1, keepdim=True)).float().cuda()
+    ids = ids.to(torch.int32).cuda()
+    ms = _time_launches(lambda i: ops.moe_w8a8_forward(x, ids, tw, q13, s13, q2, s2), steps, warmup)
+    wbytes = e * (2 * inter * h + h * inter)
+    ops_count = 2.0 * t * top_k * (2 * inter * h + h * inter)
+    gbs = wbytes / (ms * 1e-3) / 1e9
+    tops = ops_count / (ms * 1e-3) / 1e12
+    return {"tokens": t, "experts": e, "top_k": top_k, "hidden": h, "inter": inter, "ms_chain": ms,
+            "weight_bytes": wbytes, "gb_s": gbs, "tops": tops,
+            "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s"),
+            "roofline_mfma": _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS")}
+
+
+def cpu_baseline_w4a16(m=1, n=4096, k=4096, g=128, budget_s=12.0):
+    """Oracle restatement of the reference CPU path: AWQ pseudo-quantized fp16 weight, then
+    F.linear (fp32 accumulate).  Timed per call on the host, bounded sample."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import quant as O
+    gen = torch.Generator().manual_seed(1)
+    w = (torch.randn(n, k, generator=gen) * 0.02).half().numpy()
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(0)).half().numpy()
+    t0 = time.perf_counter()
+    deq, _, _, _ = O.pseudo_quantize_tensor(w, 4, True, g)
+    t_deq = time.perf_counter() - t0
+    O.w4a16_linear(x, deq)
+    n_calls, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n_calls < 2000:
+        O.w4a16_linear(x, deq)
+        n_calls += 1
+    per = (time.perf_counter() - t0) / n_calls
+    nbytes = n * k // 2 + 2 * n * (k // g) * 2 + m * k * 2 + m * n * 2
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return {"value": round(nbytes / per / 1e12, 6), "unit": "TB/s", "cores": cores, "kind": "port",
+            "sample": f"{n_calls} calls of oracle w4a16_linear (numpy fp32 BLAS on fp16 AWQ-dequantized "
+                      f"weights) at M={m}, K=N={k}, g={g}; {per * 1e3:.3f} ms/call; AWQ dequant "
+                      f"{t_deq:.2f} s once (excluded)",
+            "ms_per_call": per * 1e3}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--legs", default="w4,w8,moe")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see DESIGN.md for how the kernels would shard)", file=sys.stderr)
+        sys.exit(2)
+    from mindpipe_amd import ops
+
+    legs = set(args.legs.split(","))
+    steps, warmup = args.steps, args.warmup
+    torch.cuda.init()
+    dev = torch.cuda.get_device_properties(0)
+    _log(f"device {dev.name} CUs={dev.multi_processor_count}")
+    out_legs = {}
+    _log("leg w4a16 M=1")
+    head, _ = leg_w4a16(ops, 1, 4096, 4096, steps, warmup)
+    if "w4" in legs:
+        _log("leg w4a16 M=16")
+        out_legs["w4a16_m16_k4096_n4096"], _ = leg_w4a16(ops, 16, 4096, 4096, steps, warmup)
+        _log("leg w4a16 70B shapes")
+        out_legs["w4a16_m1_k8192_n28672"], _ = leg_w4a16(ops, 1, 28672, 8192, max(20, steps // 4), warmup // 2, copies=8)
+        out_legs["w4a16_m1_k28672_n8192"], _ = leg_w4a16(ops, 1, 8192, 28672, max(20, steps // 4), warmup // 2, copies=8)
+    if "w8" in legs:
+        for m in (4096, 256, 16, 1):
+            _log(f"leg w8a8 M={m}")
+            out_legs[f"w8a8_m{m}_k4096_n11008"] = leg_w8a8(ops, m, 11008, 4096,
+                                                            max(10, steps // (10 if m >= 4096 else 2)), warmup // 2)
+    if "moe" in legs:
+        _log("leg moe")
+        out_legs["moe_w8a8_mixtral_t512"] = leg_moe(ops, max(5, steps // 20), max(2, warmup // 4))
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log("cpu baseline")
+        cpu = cpu_baseline_w4a16()
+    w8 = out_legs.get("w8a8_m4096_k4096_n11008")
+    res = {
+        "metric": METRIC,
+        "value": round(head["tb_s"], 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(head["ms_per_call"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4xf16->f32",
+        "data": "synthetic",
+        "config": {"workload": "W4A16 g128 asym GEMV, M=1, K=N=4096, fp16 activations, 64 rotated weight copies",
+                   "m": 1, "k": 4096, "n": 4096, "group_size": 128},
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "int8_tops_m4096": round(w8["tops"], 2) if w8 else None,
+        "legs": out_legs,
+        "device": dev.name,
+    }
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

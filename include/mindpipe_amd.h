@@ -1,0 +1,175 @@
+/*
+ * mindpipe_amd: MI355X (gfx950) quantized-linear forward path, C ABI.
+ *
+ * Every entry point takes raw device pointers, sizes and a HIP stream, launches
+ * asynchronously on that stream, never allocates, never synchronises, and
+ * returns 0 on success or one of the MP_ERR_* codes below (mp_strerror gives
+ * the text).  Shapes are validated on the host before any launch.  Tensors are
+ * dense row-major; "[N,K]" means N rows of K contiguous elements.
+ *
+ * Layouts are the reference's on-disk / module layouts, unchanged:
+ *   - W4 packed  : int32 [N, ceil(K/8)], column k in nibble k%8 of word k/8
+ *                  (algorithm/quantization/exporters/vllm.py:89-111);
+ *                  stored nibble u = int4 + 8 for the signed (GPTQ) export,
+ *                  u = q for AWQ asymmetric codes.
+ *   - W4 scales  : fp16 [N, K/g]; zeros fp16 [N, K/g] (AWQ, quantizer.py:63-105)
+ *                  or NULL meaning the symmetric zero point 8.
+ *   - W8 weight  : int8 [N, K] + fp32 per-row scale [N]
+ *                  (export_fp16_to_ascend_w8a8_dynamic_probe.py:175-195;
+ *                  runtime weight_scale_fp32, vllm_ascend.patch:4030-4031).
+ *   - MoE weights: gate_up int8 [E, 2I, H], down int8 [E, H, I] with per-row
+ *                  fp32 scales [E, 2I] / [E, H] (fake_quant.py:124-160 layout).
+ */
+#ifndef MINDPIPE_AMD_H
+#define MINDPIPE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *mp_stream_t; /* identical to hipStream_t */
+
+enum mp_status {
+  MP_OK = 0,
+  MP_ERR_SHAPE = 1,    /* a size or group size the entry point cannot take */
+  MP_ERR_DTYPE = 2,    /* unsupported dtype enum */
+  MP_ERR_ALIGN = 3,    /* pointer not aligned as the kernel needs (16 B) */
+  MP_ERR_HIP = 4,      /* a HIP launch failed */
+  MP_ERR_ARG = 5,      /* NULL where a buffer is required, bad enum */
+  MP_ERR_WORKSPACE = 6 /* workspace smaller than mp_*_workspace_bytes */
+};
+
+enum mp_dtype { MP_F16 = 0, MP_BF16 = 1, MP_F32 = 2 };
+
+/* Scale rule of the int8 quantizers.
+ * MP_SCALE_FP32 : s = fp32(absmax)/127, q = rint(x/s)   (runtime npu_dynamic_quant
+ *                 contract, vllm_ascend.patch:1741, and the W8 export rule with
+ *                 its 1e-8 clamp).
+ * MP_SCALE_FP16 : fp16 arithmetic of quantize_*_absmax (fake_quant.py:10-31):
+ *                 s = h(h(max(absmax,1e-5))/127), q = rint(h(x/s)).          */
+enum mp_scale_rule { MP_SCALE_FP32 = 0, MP_SCALE_FP16 = 1 };
+
+const char *mp_strerror(int status);
+int mp_abi_version(void);
+
+/* ---------------------------------------------------------------- W4 (AWQ / GPTQ) */
+
+/* AWQ pseudo_quantize_tensor(w, n_bit=4, zero_point, q_group_size=g,
+ * get_scale_zp=True) in fp16 arithmetic; replaces
+ * algorithm/quantization/ptq/awq/source/awq/quantize/quantizer.py:63-105.
+ * w fp16 [N,K].  Effective group = g if g > 0 and K % g == 0, else K (per row,
+ * quantizer.py:67-68).  Outputs: packed int32 [N, ceil(K/8)] (u = q when
+ * zero_point, u = q + 8 when symmetric), scales fp16 [N, K/g_eff], zeros fp16
+ * [N, K/g_eff] (zero_point only; pass NULL when symmetric), w_deq fp16 [N,K]
+ * (optional, NULL to skip) = the tensor the reference returns. */
+int mp_w4_quantize_awq(const void *w, int64_t n, int64_t k, int group_size, int zero_point,
+                       int32_t *packed, void *scales, void *zeros, void *w_deq, mp_stream_t stream);
+
+/* GPTQ symmetric round-to-nearest group quantizer in fp32: Quantizer.find_params
+ * (perchannel, sym) per group + quantize_with_qint and the signed export
+ * q - 8; replaces algorithm/quantization/ptq/gptq/source/quant.py:13-17,44-82
+ * and gptq.py:157-161 (without the Hessian error feedback).  w fp32 or fp16
+ * [N,K] (w_dtype), K % g == 0.  Outputs (each optional): int_weight int8 [N,K]
+ * in [-8,7], packed int32 [N, ceil(K/8)] in the pack_int4_for_vllm layout,
+ * scale fp16 [N, K/g] (required). */
+int mp_w4_quantize_gptq_rtn(const void *w, int w_dtype, int64_t n, int64_t k, int group_size,
+                            int8_t *int_weight, int32_t *packed, void *scale, mp_stream_t stream);
+
+/* pack_int4_for_vllm (algorithm/quantization/exporters/vllm.py:89-111):
+ * int8 [N,K] in [-8,7] -> int32 [N, ceil(K/8)], K zero-padded.  Values out of
+ * range are counted into *bad_count (device int32, caller zeroes it); the
+ * caller raises like the reference's ValueError when it is non-zero. */
+int mp_pack_int4(const int8_t *int_weight, int64_t n, int64_t k, int32_t *packed, int32_t *bad_count,
+                 mp_stream_t stream);
+
+/* Inverse of mp_pack_int4 (tests/test_vllm_real_quant_export.py:23-27). */
+int mp_unpack_int4(const int32_t *packed, int64_t n, int64_t k, int8_t *int_weight, mp_stream_t stream);
+
+/* Y[M,N] = X[M,K] . dequant(W)^T (+ bias[N]); dequant(w) = (u - z) * s with z
+ * from zeros (or 8 when zeros == NULL).  Replaces the fp16 F.linear on AWQ
+ * pseudo-quantized weights (quantizer.py:108-130 + the HF forward) and the
+ * vLLM compressed-tensors WNA16 kernel the export targets
+ * (scripts/repro/evaluate_vllm_real_int4_ppl.py:48-76).  x, bias, y fp16
+ * (x_dtype MP_F16); K % 8 == 0, K % g == 0.  M <= 64 runs the streaming
+ * (decode) kernel, larger M the tiled (prefill) kernel. */
+int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n,
+                  const void *scales, const void *zeros, int group_size, const void *bias, void *y,
+                  int x_dtype, mp_stream_t stream);
+
+/* ---------------------------------------------------------------- W8A8 (SmoothQuant) */
+
+/* Per-token dynamic symmetric int8 quant of x [M,K] (fp16/bf16/fp32).
+ * MP_SCALE_FP32: replaces torch_npu.npu_dynamic_quant (vllm_ascend.patch:3950),
+ *   scale fp32 [M].
+ * MP_SCALE_FP16: codes of quantize_activation_per_token_absmax
+ *   (fake_quant.py:22-31), scale fp16 [M] (x must be fp16). */
+int mp_quant_per_token_i8(const void *x, int64_t m, int64_t k, int x_dtype, int8_t *q, void *scale,
+                          int scale_rule, mp_stream_t stream);
+
+/* Per-output-channel symmetric int8 weight quant of w [N,K] (fp16/bf16).
+ * MP_SCALE_FP32: quantize_weight_per_channel
+ *   (scripts/repro/export_fp16_to_ascend_w8a8_dynamic_probe.py:175-195),
+ *   scale_f32 [N] and scale_src [N] in the source dtype (optional).
+ * MP_SCALE_FP16: quantize_weight_per_channel_absmax (fake_quant.py:10-19),
+ *   scale_f32 [N] holds the fp16 scale value exactly; scale_src fp16 [N].
+ * Rows holding a non-finite value are counted into *bad_count (optional). */
+int mp_w8_quantize_per_channel(const void *w, int64_t n, int64_t k, int w_dtype, int8_t *q,
+                               float *scale_f32, void *scale_src, int scale_rule, int32_t *bad_count,
+                               mp_stream_t stream);
+
+/* Y[M,N] = ((int32 acc = Qx . Qw^T) * s_tok[m]) * s_ch[n] (+ bias[n]) rounded to
+ * out_dtype (fp16/bf16/fp32).  Replaces torch_npu.npu_quant_matmul
+ * (vllm_ascend.patch:4007-4015).  qx int8 [M,K], w int8 [N,K], K % 16 == 0. */
+int mp_w8a8_gemm(const int8_t *qx, const float *s_tok, const int8_t *w, const float *s_ch,
+                 const void *bias, int bias_dtype, void *y, int out_dtype, int64_t m, int64_t n,
+                 int64_t k, mp_stream_t stream);
+
+/* ---------------------------------------------------------------- W8A8 MoE */
+
+/* Routing + per-token quant (replaces npu_moe_init_routing_quant,
+ * vllm_ascend.patch:2369-2379).  topk_ids int32 [T, top_k] in [0,E).
+ * Outputs: routed int8 [T*top_k, H] (token copies sorted by expert, stable in
+ * (token, slot) order), routed_scale fp32 [T*top_k], row_of_slot int32
+ * [T*top_k] (row in routed for assignment t*top_k+j), group_offsets int64
+ * [E+1] (cumulative endpoints, offsets[0] = 0).  workspace >=
+ * mp_moe_route_workspace_bytes(T, H, E). */
+size_t mp_moe_route_workspace_bytes(int64_t t, int64_t h, int n_experts);
+int mp_moe_permute_quant(const void *x, int x_dtype, int64_t t, int64_t h, const int32_t *topk_ids,
+                         int top_k, int n_experts, int8_t *routed, float *routed_scale,
+                         int32_t *row_of_slot, int64_t *group_offsets, void *workspace,
+                         size_t workspace_bytes, mp_stream_t stream);
+
+/* GMM1 + SwiGLU + per-row requant (replaces npu_grouped_matmul_swiglu_quant,
+ * vllm_ascend.patch:2391-2398, and the C++ loop-out bridge
+ * acceleration/custom_ops/qwen2_5_vl/aclnn_grouped_swiglu_out_bridge.cpp:157-273).
+ * For routed row r of expert e: g = (Qx_r . W13_e^T) * sx_r * s13_e (fp32),
+ * h = silu(g[:I]) * g[I:], then h -> int8 q_out [R, I] + fp32 s_out [R].
+ * No limit on I (the CANN op rejects 2I > 10240, moe_mlp.py patch). */
+size_t mp_moe_gmm1_workspace_bytes(int64_t rows, int64_t inter);
+int mp_i8_gemm_swiglu_requant(const int8_t *routed, const float *routed_scale, const int8_t *w13,
+                              const float *s13, const int64_t *group_offsets, int n_experts,
+                              int64_t rows, int64_t h, int64_t inter, int8_t *q_out, float *s_out,
+                              void *workspace, size_t workspace_bytes, mp_stream_t stream);
+
+/* GMM2: Y_r = (Qh_r . W2_e^T) * sh_r * s2_e -> out_dtype [R, N] (fp32 for the
+ * combine).  Replaces npu_grouped_matmul with per_token_scale
+ * (vllm_ascend.patch:2401-2412). */
+int mp_w8a8_grouped_gemm(const int8_t *q, const float *s, const int8_t *w, const float *s_w,
+                         const int64_t *group_offsets, int n_experts, int64_t rows, int64_t n,
+                         int64_t k, void *y, int out_dtype, mp_stream_t stream);
+
+/* out[t] = sum_j topk_w[t,j] * y[row_of_slot[t*top_k+j]] in fp32, rounded once
+ * (replaces npu_moe_token_unpermute, vllm_ascend.patch:2415-2419).  y fp32
+ * [R, H]; topk_w fp32 [T, top_k]; out fp16/bf16/fp32 [T, H]. */
+int mp_moe_unpermute_combine(const float *y, const int32_t *row_of_slot, const float *topk_w,
+                             int64_t t, int top_k, int64_t h, void *out, int out_dtype,
+                             mp_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINDPIPE_AMD_H */

@@ -1,0 +1,258 @@
+// W8A8 MoE chain for gfx950: routing (stable counting sort by expert) fused
+// with the per-token int8 quant, GMM1 + SwiGLU + requant, GMM2, and the
+// weighted un-permute.  The two grouped GEMMs use the tiled int8 MFMA kernel
+// of w8a8.hip with a grouped row schedule.
+#include "i8_gemm.h"
+
+namespace {
+
+constexpr int kMaxExperts = 1024;
+
+// Single-workgroup stable counting sort of the T*top_k assignments by expert.
+// Writes group_offsets [E+1] and row_of_slot [T*top_k].  Assignment a =
+// t*top_k + j keeps (t, j) order inside its expert, so the routed layout is
+// deterministic.  One wave does the placement; rank within a 64-assignment
+// batch comes from a ballot over lanes holding the same expert.
+__global__ __launch_bounds__(256) void moe_route_kernel(const int32_t *__restrict__ ids, int64_t n_assign,
+                                                       int n_experts, int64_t *__restrict__ offsets,
+                                                       int32_t *__restrict__ row_of_slot,
+                                                       int32_t *__restrict__ invalid) {
+  __shared__ int counts[kMaxExperts];
+  __shared__ int cursor[kMaxExperts];
+  for (int e = threadIdx.x; e < n_experts; e += blockDim.x) counts[e] = 0;
+  __syncthreads();
+  for (int64_t a = threadIdx.x; a < n_assign; a += blockDim.x) {
+    const int e = ids[a];
+    if (e >= 0 && e < n_experts) atomicAdd(&counts[e], 1);
+    else if (invalid) atomicAdd(invalid, 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t run = 0;
+    offsets[0] = 0;
+    for (int e = 0; e < n_experts; ++e) {
+      cursor[e] = static_cast<int>(run);
+      run += counts[e];
+      offsets[e + 1] = run;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  for (int64_t base = 0; base < n_assign; base += 64) {
+    const int64_t a = base + lane;
+    const bool valid = a < n_assign;
+    const int e = valid ? ids[a] : -1;
+    const bool ok = valid && e >= 0 && e < n_experts;
+    // rank among lower lanes with the same expert
+    int rank = 0, total = 0;
+    for (int l = 0; l < 64; ++l) {
+      const int el = __shfl(e, l, 64);
+      const int same = (el == e) && ok;
+      rank += same && (l < lane);
+      total += same;
+    }
+    const int pos = ok ? cursor[e] + rank : -1;
+    if (valid) row_of_slot[a] = pos;
+    // the last lane of each expert in this batch advances the cursor
+    __builtin_amdgcn_wave_barrier();
+    if (ok && rank == total - 1) cursor[e] += total;
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// Per-token quant of x[t] written to every routed row that copies it.  One
+// workgroup per assignment; the activation row is re-read from L2 per copy.
+__global__ __launch_bounds__(256) void moe_permute_quant_kernel(const void *__restrict__ x, int x_dtype,
+                                                               int64_t h, int top_k,
+                                                               const int32_t *__restrict__ row_of_slot,
+                                                               int8_t *__restrict__ routed,
+                                                               float *__restrict__ routed_scale) {
+  __shared__ float wmax[4];
+  const int64_t a = blockIdx.x;
+  const int64_t t = a / top_k;
+  const int r = row_of_slot[a];
+  if (r < 0) return;
+  const int tid = threadIdx.x;
+  float amax = 0.f;
+  for (int64_t c = tid; c < h; c += 256) amax = fmaxf(amax, fabsf(mp_load_as_f32(x, t * h + c, x_dtype)));
+  amax = mp_wave_max(amax);
+  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float s = amax / 127.0f;
+  if (tid == 0) routed_scale[r] = s;
+  for (int64_t c = tid; c < h; c += 256) {
+    const float v = mp_load_as_f32(x, t * h + c, x_dtype);
+    float q = (s == 0.f) ? 0.f : rintf(v / s);
+    q = fminf(fmaxf(q, -127.f), 127.f);
+    routed[static_cast<int64_t>(r) * h + c] = static_cast<int8_t>(static_cast<int>(q));
+  }
+}
+
+// Requant of the SwiGLU output: per routed row, abs-max over the GMM1
+// workgroups' partial maxima, then q = rint(h / (amax / 127)).
+__global__ __launch_bounds__(256) void moe_requant_kernel(const float *__restrict__ hbuf, const float *__restrict__ part,
+                                                         int n_partial, int64_t inter, int8_t *__restrict__ q,
+                                                         float *__restrict__ s_out) {
+  __shared__ float wmax[4];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  float amax = 0.f;
+  for (int i = tid; i < n_partial; i += 256) amax = fmaxf(amax, part[r * n_partial + i]);
+  amax = mp_wave_max(amax);
+  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float s = amax / 127.0f;
+  if (tid == 0) s_out[r] = s;
+  for (int64_t c = tid; c < inter; c += 256) {
+    float v = (s == 0.f) ? 0.f : rintf(hbuf[r * inter + c] / s);
+    v = fminf(fmaxf(v, -127.f), 127.f);
+    q[r * inter + c] = static_cast<int8_t>(static_cast<int>(v));
+  }
+}
+
+__global__ void moe_combine_kernel(const float *__restrict__ y, const int32_t *__restrict__ row_of_slot,
+                                   const float *__restrict__ w, int64_t t_count, int top_k, int64_t h,
+                                   void *__restrict__ out, int out_dtype) {
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= t_count * h) return;
+  const int64_t t = tid / h, c = tid % h;
+  float acc = 0.f;
+  for (int j = 0; j < top_k; ++j) {
+    const int r = row_of_slot[t * top_k + j];
+    if (r < 0) continue;
+    acc = mp_add(acc, mp_mul(w[t * top_k + j], y[static_cast<int64_t>(r) * h + c]));
+  }
+  mp_store_from_f32(out, tid, out_dtype, acc);
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+extern "C" size_t mp_moe_route_workspace_bytes(int64_t t, int64_t h, int n_experts) {
+  (void)t;
+  (void)h;
+  (void)n_experts;
+  return 256;  // invalid-id counter (kept for future multi-workgroup routing)
+}
+
+extern "C" int mp_moe_permute_quant(const void *x, int x_dtype, int64_t t, int64_t h, const int32_t *topk_ids,
+                                    int top_k, int n_experts, int8_t *routed, float *routed_scale,
+                                    int32_t *row_of_slot, int64_t *group_offsets, void *workspace,
+                                    size_t workspace_bytes, mp_stream_t stream) {
+  if (!x || !topk_ids || !routed || !routed_scale || !row_of_slot || !group_offsets) return MP_ERR_ARG;
+  if (x_dtype != MP_F16 && x_dtype != MP_BF16 && x_dtype != MP_F32) return MP_ERR_DTYPE;
+  if (t < 0 || h <= 0 || top_k <= 0 || n_experts <= 0 || n_experts > kMaxExperts) return MP_ERR_SHAPE;
+  if (t * top_k > INT32_MAX) return MP_ERR_SHAPE;
+  if (workspace && workspace_bytes < mp_moe_route_workspace_bytes(t, h, n_experts)) return MP_ERR_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t n_assign = t * top_k;
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 0, s, topk_ids, n_assign, n_experts, group_offsets,
+                     row_of_slot, static_cast<int32_t *>(workspace));
+  MP_CHECK_LAUNCH();
+  if (n_assign == 0) return MP_OK;
+  hipLaunchKernelGGL(moe_permute_quant_kernel, dim3(static_cast<unsigned>(n_assign)), dim3(256), 0, s, x, x_dtype, h,
+                     top_k, row_of_slot, routed, routed_scale);
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+static int64_t gmm1_partials(int64_t inter) { return 2 * mp_cdiv(inter, 64); }
+
+extern "C" size_t mp_moe_gmm1_workspace_bytes(int64_t rows, int64_t inter) {
+  const size_t hbytes = static_cast<size_t>(rows) * static_cast<size_t>(inter) * sizeof(float);
+  const size_t pbytes = static_cast<size_t>(rows) * static_cast<size_t>(gmm1_partials(inter)) * sizeof(float);
+  return ((hbytes + 255) & ~static_cast<size_t>(255)) + pbytes;
+}
+
+extern "C" int mp_i8_gemm_swiglu_requant(const int8_t *routed, const float *routed_scale, const int8_t *w13,
+                                         const float *s13, const int64_t *group_offsets, int n_experts,
+                                         int64_t rows, int64_t h, int64_t inter, int8_t *q_out, float *s_out,
+                                         void *workspace, size_t workspace_bytes, mp_stream_t stream) {
+  if (!routed || !routed_scale || !w13 || !s13 || !group_offsets || !q_out || !s_out || !workspace)
+    return MP_ERR_ARG;
+  if (rows < 0 || h <= 0 || inter <= 0 || n_experts <= 0 || n_experts > kMaxExperts) return MP_ERR_SHAPE;
+  if (h % 64 != 0 || h > (1 << 17)) return MP_ERR_SHAPE;
+  if (workspace_bytes < mp_moe_gmm1_workspace_bytes(rows, inter)) return MP_ERR_WORKSPACE;
+  if (rows == 0) return MP_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  float *hbuf = static_cast<float *>(workspace);
+  const size_t hbytes = static_cast<size_t>(rows) * static_cast<size_t>(inter) * sizeof(float);
+  float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + ((hbytes + 255) & ~static_cast<size_t>(255)));
+  mp_i8_args a{};
+  a.a = routed;
+  a.s_a = routed_scale;
+  a.b = w13;
+  a.s_b = s13;
+  a.y = hbuf;
+  a.out_dtype = MP_F32;
+  a.amax_partial = part;
+  a.n_partial = static_cast<int>(gmm1_partials(inter));
+  a.offsets = group_offsets;
+  a.n_experts = n_experts;
+  a.rows = rows;
+  a.n = inter;
+  a.k = h;
+  a.ldy = inter;
+  int rc = mp_launch_i8_gemm(a, MP_EPI_SWIGLU, s);
+  if (rc != MP_OK) return rc;
+  hipLaunchKernelGGL(moe_requant_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, hbuf, part,
+                     a.n_partial, inter, q_out, s_out);
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+extern "C" int mp_w8a8_grouped_gemm(const int8_t *q, const float *s, const int8_t *w, const float *s_w,
+                                    const int64_t *group_offsets, int n_experts, int64_t rows, int64_t n,
+                                    int64_t k, void *y, int out_dtype, mp_stream_t stream) {
+  if (!q || !s || !w || !s_w || !group_offsets || !y) return MP_ERR_ARG;
+  if (out_dtype != MP_F32 && out_dtype != MP_F16 && out_dtype != MP_BF16) return MP_ERR_DTYPE;
+  if (rows < 0 || n <= 0 || k <= 0 || n_experts <= 0 || n_experts > kMaxExperts) return MP_ERR_SHAPE;
+  if (k % 64 != 0 || k > (1 << 17)) return MP_ERR_SHAPE;
+  if (rows == 0) return MP_OK;
+  mp_i8_args a{};
+  a.a = q;
+  a.s_a = s;
+  a.b = w;
+  a.s_b = s_w;
+  a.y = y;
+  a.out_dtype = out_dtype;
+  a.offsets = group_offsets;
+  a.n_experts = n_experts;
+  a.rows = rows;
+  a.n = n;
+  a.k = k;
+  a.ldy = n;
+  return mp_launch_i8_gemm(a, out_dtype == MP_F32 ? MP_EPI_F32 : MP_EPI_DENSE, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int mp_moe_unpermute_combine(const float *y, const int32_t *row_of_slot, const float *topk_w, int64_t t,
+                                        int top_k, int64_t h, void *out, int out_dtype, mp_stream_t stream) {
+  if (!y || !row_of_slot || !topk_w || !out) return MP_ERR_ARG;
+  if (out_dtype != MP_F32 && out_dtype != MP_F16 && out_dtype != MP_BF16) return MP_ERR_DTYPE;
+  if (t < 0 || top_k <= 0 || h <= 0) return MP_ERR_SHAPE;
+  if (t == 0) return MP_OK;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3(static_cast<unsigned>(mp_cdiv(t * h, 256))), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), y, row_of_slot, topk_w, t, top_k, h, out, out_dtype);
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+// ---------------------------------------------------------------- misc
+extern "C" const char *mp_strerror(int status) {
+  switch (status) {
+    case MP_OK: return "ok";
+    case MP_ERR_SHAPE: return "mindpipe_amd: unsupported shape or group size";
+    case MP_ERR_DTYPE: return "mindpipe_amd: unsupported dtype";
+    case MP_ERR_ALIGN: return "mindpipe_amd: pointer alignment (16 bytes required)";
+    case MP_ERR_HIP: return "mindpipe_amd: HIP kernel launch failed";
+    case MP_ERR_ARG: return "mindpipe_amd: missing buffer or bad enum argument";
+    case MP_ERR_WORKSPACE: return "mindpipe_amd: workspace too small";
+    default: return "mindpipe_amd: unknown status";
+  }
+}
+
+extern "C" int mp_abi_version(void) { return 1; }

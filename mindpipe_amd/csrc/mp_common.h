@@ -1,0 +1,77 @@
+// Shared helpers for the gfx950 kernels of mindpipe_amd.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+#include "../../include/mindpipe_amd.h"
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f16_t __attribute__((ext_vector_type(16)));
+typedef int i4_t __attribute__((ext_vector_type(4)));
+typedef int i16_t __attribute__((ext_vector_type(16)));
+
+#define MP_CHECK_LAUNCH()                      \
+  do {                                         \
+    if (hipGetLastError() != hipSuccess)       \
+      return MP_ERR_HIP;                       \
+  } while (0)
+
+static inline bool mp_aligned(const void *p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+static inline int64_t mp_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- scalar conversions (round to nearest even everywhere)
+__device__ __forceinline__ float mp_h2f(uint16_t b) {
+  return __half2float(__ushort_as_half(b));
+}
+__device__ __forceinline__ uint16_t mp_f2h(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+// fp32 -> fp16 -> fp32: the value PyTorch keeps after a half op.
+__device__ __forceinline__ float mp_rh(float f) { return __half2float(__float2half_rn(f)); }
+
+__device__ __forceinline__ float mp_bf2f(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ uint16_t mp_f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float mp_load_as_f32(const void *p, int64_t i, int dtype) {
+  if (dtype == MP_F16) return mp_h2f(static_cast<const uint16_t *>(p)[i]);
+  if (dtype == MP_BF16) return mp_bf2f(static_cast<const uint16_t *>(p)[i]);
+  return static_cast<const float *>(p)[i];
+}
+
+__device__ __forceinline__ void mp_store_from_f32(void *p, int64_t i, int dtype, float v) {
+  if (dtype == MP_F16) static_cast<uint16_t *>(p)[i] = mp_f2h(v);
+  else if (dtype == MP_BF16) static_cast<uint16_t *>(p)[i] = mp_f2bf(v);
+  else static_cast<float *>(p)[i] = v;
+}
+
+// ---- wave64 reductions (DPP-backed shuffles)
+__device__ __forceinline__ float mp_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float mp_wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Uniform-order float multiply/add that the compiler may not contract into an
+// FMA: the W8A8 epilogue is specified as (acc * s_tok) * s_ch + bias with
+// three separate roundings.
+__device__ __forceinline__ float mp_mul(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float mp_add(float a, float b) { return __fadd_rn(a, b); }

@@ -1,0 +1,555 @@
+// W4A16 group-quantized linear for gfx950: AWQ/GPTQ quantizers, the int4 pack
+// format, the streaming decode GEMV (M <= 64) and the tiled prefill GEMM.
+//
+// Weight format (unchanged from the reference export, exporters/vllm.py:89-111):
+// packed int32 [N, ceil(K/8)], column k in nibble k%8 of word k/8, plus fp16
+// scales [N, K/g] and fp16 zeros [N, K/g] (AWQ) or an implicit zero point 8
+// (GPTQ symmetric export, stored nibble = int + 8).
+#include "mp_common.h"
+
+namespace {
+
+constexpr uint32_t kMagic = 0x64006400u;  // fp16 1024.0 in both halves
+
+// Eight nibbles of one packed word -> fp16 (1024 + u) in the order
+// [k0, k4, k1, k5, k2, k6, k3, k7]: the "or 1024" trick turns a 4-bit integer
+// into an fp16 bit pattern with one AND-OR per pair.
+__device__ __forceinline__ h8_t dq_magic(uint32_t w) {
+  union {
+    uint32_t u[4];
+    h8_t h;
+  } r;
+  r.u[0] = (w & 0x000F000Fu) | kMagic;
+  r.u[1] = ((w >> 4) & 0x000F000Fu) | kMagic;
+  r.u[2] = ((w >> 8) & 0x000F000Fu) | kMagic;
+  r.u[3] = ((w >> 12) & 0x000F000Fu) | kMagic;
+  return r.h;
+}
+
+// Natural-order 8 halves (x0..x7 in 4 dwords) -> [x0,x4,x1,x5,x2,x6,x3,x7],
+// the order dq_magic produces, so that the MFMA pairs x_k with w_k.
+__device__ __forceinline__ h8_t perm_to_magic(uint4 d) {
+  union {
+    uint32_t u[4];
+    h8_t h;
+  } r;
+  r.u[0] = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
+  r.u[1] = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
+  r.u[2] = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
+  r.u[3] = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
+  return r.h;
+}
+
+// Inverse of the magic order: [k0,k4,k1,k5,k2,k6,k3,k7] -> natural order.
+__device__ __forceinline__ uint4 magic_to_natural(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  uint4 d;
+  d.x = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+  d.y = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+  d.z = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+  d.w = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
+  return d;
+}
+
+// ------------------------------------------------------------------ quantizers
+
+// One wave per quantization group (row segment of g elements).  fp16
+// arithmetic restated as fp32 op + one rounding, as PyTorch does for half
+// tensors; quantizer.py:63-105.
+__global__ __launch_bounds__(256) void awq_quantize_kernel(
+    const uint16_t *__restrict__ w, int64_t n_rows, int64_t k, int gs, int n_groups, int zero_point,
+    uint32_t *__restrict__ packed, int64_t kw, uint16_t *__restrict__ scales,
+    uint16_t *__restrict__ zeros, uint16_t *__restrict__ wdeq) {
+  const int lane = threadIdx.x & 63;
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (grp >= n_rows * n_groups) return;
+  const int64_t row = grp / n_groups;
+  const int gi = static_cast<int>(grp % n_groups);
+  const int64_t e0 = static_cast<int64_t>(gi) * gs;
+  const uint16_t *src = w + row * k + e0;
+
+  float mx = -INFINITY, mn = INFINITY;
+  for (int i = lane; i < gs; i += 64) {
+    const float v = mp_h2f(src[i]);
+    mx = fmaxf(mx, zero_point ? v : fabsf(v));
+    mn = fminf(mn, v);
+  }
+  mx = mp_wave_max(mx);
+  mn = mp_wave_min(mn);
+
+  float s, z, qmin, qmax;
+  if (zero_point) {
+    float d = mp_rh(mx - mn);
+    if (d < 1e-5f) d = mp_rh(1e-5f);
+    s = mp_rh(d / 15.0f);
+    z = -rintf(mp_rh(mn / s));
+    if (z < 0.0f) z = 0.0f;   // keeps -0.0 like torch.clamp_
+    if (z > 15.0f) z = 15.0f;
+    qmin = 0.0f;
+    qmax = 15.0f;
+  } else {
+    float a = mx;
+    if (a < 1e-5f) a = mp_rh(1e-5f);
+    s = mp_rh(a / 7.0f);
+    z = 0.0f;
+    qmin = -8.0f;
+    qmax = 7.0f;
+  }
+  if (lane == 0) {
+    scales[row * n_groups + gi] = mp_f2h(s);
+    if (zero_point) zeros[row * n_groups + gi] = mp_f2h(z);
+  }
+  // pass 2: one packed word (8 consecutive columns) per lane iteration
+  const int nwords = (gs + 7) / 8;
+  for (int c = lane; c < nwords; c += 64) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int idx = 8 * c + j;
+      if (idx >= gs) break;
+      const float v = mp_h2f(src[idx]);
+      const float t = rintf(mp_rh(v / s));
+      float q = mp_rh(t + z);
+      if (q < qmin) q = qmin;
+      if (q > qmax) q = qmax;
+      const float deq = mp_rh(mp_rh(q - z) * s);
+      if (wdeq) wdeq[row * k + e0 + idx] = mp_f2h(deq);
+      const uint32_t u = static_cast<uint32_t>(static_cast<int>(q) + (zero_point ? 0 : 8));
+      word |= u << (4 * j);
+    }
+    packed[row * kw + e0 / 8 + c] = word;
+  }
+}
+
+// GPTQ symmetric RTN, fp32 math; one thread per (row, group).
+__global__ void gptq_rtn_kernel(const void *__restrict__ w, int w_dtype, int64_t n_rows, int64_t k,
+                                int gs, int8_t *__restrict__ iw, uint32_t *__restrict__ packed,
+                                int64_t kw, uint16_t *__restrict__ scale) {
+  const int n_groups = static_cast<int>(k / gs);
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= n_rows * n_groups) return;
+  const int64_t row = tid / n_groups;
+  const int gi = static_cast<int>(tid % n_groups);
+  const int64_t base = row * k + static_cast<int64_t>(gi) * gs;
+  float xmin = 0.0f, xmax = 0.0f;
+  for (int i = 0; i < gs; ++i) {
+    const float v = mp_load_as_f32(w, base + i, w_dtype);
+    xmin = fminf(xmin, v);
+    xmax = fmaxf(xmax, v);
+  }
+  xmax = fmaxf(fabsf(xmin), xmax);
+  if (xmin < 0.0f) xmin = -xmax;
+  if (xmin == 0.0f && xmax == 0.0f) {
+    xmin = -1.0f;
+    xmax = 1.0f;
+  }
+  const float s = (xmax - xmin) / 15.0f;
+  scale[row * n_groups + gi] = mp_f2h(s);
+  uint32_t word = 0;
+  for (int i = 0; i < gs; ++i) {
+    const float v = mp_load_as_f32(w, base + i, w_dtype);
+    float q = rintf(v / s) + 8.0f;
+    q = fminf(fmaxf(q, 0.0f), 15.0f);
+    const int u = static_cast<int>(q);
+    if (iw) iw[base + i] = static_cast<int8_t>(u - 8);
+    const int64_t col = static_cast<int64_t>(gi) * gs + i;
+    word |= static_cast<uint32_t>(u) << (4 * (col & 7));
+    if ((col & 7) == 7 || i == gs - 1) {
+      if (packed) packed[row * kw + col / 8] = word;
+      word = 0;
+    }
+  }
+}
+
+__global__ void pack_int4_kernel(const int8_t *__restrict__ iw, int64_t n_rows, int64_t k,
+                                 uint32_t *__restrict__ packed, int64_t kw, int32_t *__restrict__ bad) {
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= n_rows * kw) return;
+  const int64_t row = tid / kw, c = tid % kw;
+  uint32_t word = 0;
+  int nbad = 0;
+  for (int j = 0; j < 8; ++j) {
+    const int64_t col = c * 8 + j;
+    if (col >= k) break;
+    const int v = iw[row * k + col];
+    nbad += (v < -8 || v > 7);
+    word |= (static_cast<uint32_t>(v + 8) & 0xFu) << (4 * j);
+  }
+  packed[tid] = word;
+  if (nbad && bad) atomicAdd(bad, nbad);
+}
+
+__global__ void unpack_int4_kernel(const uint32_t *__restrict__ packed, int64_t n_rows, int64_t k,
+                                   int64_t kw, int8_t *__restrict__ iw) {
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= n_rows * k) return;
+  const int64_t row = tid / k, col = tid % k;
+  const uint32_t word = packed[row * kw + col / 8];
+  iw[tid] = static_cast<int8_t>(static_cast<int>((word >> (4 * (col & 7))) & 0xFu) - 8);
+}
+
+// ------------------------------------------------------------------ decode GEMV (M <= 64)
+//
+// Work split: one workgroup of 8 waves per 16 output columns; the 8 waves
+// split K into contiguous runs of 128-column blocks and are summed through LDS
+// at the end.  Per 128-column block a lane loads 16 B of packed weights (32
+// columns of one output row, all in one quantization group), so a wave load
+// instruction covers 16 rows x 64 B.  MFMA f32_16x16x32_f16 does the
+// multiply-reduce: B = weights (column n = lane%16), A = activations (row m =
+// lane%16).  The weights enter the MFMA as (1024 + u) straight from the bit
+// trick; a second MFMA against ones gives sum(x) per row, and
+//   sum_k x_k (u_k - z) s = s * (acc - (1024 + z) * sum_k x_k)
+// removes the offset per group in fp32, so dequantisation costs two VALU ops
+// per weight pair.
+constexpr int kSkinnyWaves = 8;
+
+template <int MT>
+__global__ __launch_bounds__(512) void w4a16_skinny_kernel(
+    const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
+    const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups, int gs,
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
+  __shared__ float red[kSkinnyWaves][MT][4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n = blockIdx.x * 16 + (lane & 15);
+  const int nn = n < n_cols ? n : n_cols - 1;
+  const int kq = lane >> 4;
+  const int kw = k >> 3;
+  const int nblk = k >> 7;
+  const int bpg = gs >> 7;
+  const int b_begin = (nblk * wave) / kSkinnyWaves;
+  const int b_end = (nblk * (wave + 1)) / kSkinnyWaves;
+
+  const uint32_t *wrow = wq + static_cast<int64_t>(nn) * kw + 4 * kq;
+  const uint16_t *srow = sc + static_cast<int64_t>(nn) * n_groups;
+  const uint16_t *zrow = zr ? zr + static_cast<int64_t>(nn) * n_groups : nullptr;
+
+  const uint16_t *xrow[MT];
+  bool xvalid[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = t * 16 + (lane & 15);
+    xvalid[t] = m < m_rows;
+    xrow[t] = x + static_cast<int64_t>(xvalid[t] ? m : 0) * k + 32 * kq;
+  }
+
+  f4_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+  const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  const h8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+
+  constexpr int U = 4;  // blocks whose loads are in flight together
+  for (int b = b_begin; b < b_end; b += U) {
+    uint4 wv[U];
+    float s[U], zc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int bb = (b + u < b_end) ? b + u : b_end - 1;
+      wv[u] = *reinterpret_cast<const uint4 *>(wrow + bb * 16);
+      const int gi = bb / bpg;
+      s[u] = mp_h2f(srow[gi]);
+      zc[u] = 1024.0f + (zrow ? mp_h2f(zrow[gi]) : 8.0f);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (b + u >= b_end) break;
+      const int kb = (b + u) * 128;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        f4_t cg = {0.f, 0.f, 0.f, 0.f};
+        f4_t cs = {0.f, 0.f, 0.f, 0.f};
+        const uint32_t wsel[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          h8_t a = zero8;
+          if (xvalid[t]) a = perm_to_magic(*reinterpret_cast<const uint4 *>(xrow[t] + kb + 8 * q));
+          const h8_t bq = dq_magic(wsel[q]);
+          cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, cg, 0, 0, 0);
+          cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ones, cs, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(s[u], fmaf(-zc[u], cs[i], cg[i]), acc[t][i]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][t][i][lane] = acc[t][i];
+  __syncthreads();
+  for (int o = threadIdx.x; o < MT * 256; o += blockDim.x) {
+    const int t = o >> 8, r = o & 255;
+    const int l = r & 63, i = r >> 6;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSkinnyWaves; ++w) v += red[w][t][i][l];
+    const int m = t * 16 + 4 * (l >> 4) + i;
+    const int col = blockIdx.x * 16 + (l & 15);
+    if (m < m_rows && col < n_cols) {
+      if (bias) v += mp_h2f(bias[col]);
+      y[static_cast<int64_t>(m) * n_cols + col] = mp_f2h(v);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ prefill GEMM (M > 64)
+//
+// 128x128 output tile per workgroup of 4 waves (64x64 each, 2x2 MFMA
+// f32_32x32x16_f16 tiles), BK = 64.  Activations are staged to LDS as is; the
+// packed weights are dequantised by (u - z) * s in fp16 (the exact fp16 values
+// of the reference's pseudo-quantized weight) into LDS.  Double-buffered LDS.
+constexpr int kPBM = 128, kPBN = 128, kPBK = 64, kPLD = kPBK + 8;  // row stride in halves
+
+__global__ __launch_bounds__(256) void w4a16_prefill_kernel(
+    const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
+    const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups, int gs,
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
+  __shared__ __attribute__((aligned(16))) uint16_t sa[2][kPBM * kPLD];
+  __shared__ __attribute__((aligned(16))) uint16_t sb[2][kPBN * kPLD];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * kPBM, n0 = blockIdx.x * kPBN;
+  const int kw = k >> 3;
+
+  // A staging: 128 rows x 64 halves = 1024 chunks of 16 B, 4 per thread
+  // B staging: 128 rows x 8 words = 256 chunks of 16 B (4 words), 1 per thread
+  const int brow = tid >> 1, bhalf = tid & 1;  // each thread: 4 words = 32 columns
+  const int bn = n0 + brow < n_cols ? n0 + brow : n_cols - 1;
+  const uint32_t *bsrc = wq + static_cast<int64_t>(bn) * kw + 4 * bhalf;
+
+  uint4 areg[4];
+  uint4 breg;
+  float bs = 0.f, bz = 0.f;
+
+  auto load_tile = [&](int kt) {
+    const int kb = kt * kPBK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + i * 256;
+      const int r = c >> 3, cc = c & 7;
+      const int m = m0 + r;
+      if (m < m_rows)
+        areg[i] = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(m) * k + kb + cc * 8);
+      else
+        areg[i] = make_uint4(0, 0, 0, 0);
+    }
+    breg = *reinterpret_cast<const uint4 *>(bsrc + kb / 8);
+    const int gi = (kb + 32 * bhalf) / gs;
+    bs = mp_h2f(sc[static_cast<int64_t>(bn) * n_groups + gi]);
+    bz = zr ? mp_h2f(zr[static_cast<int64_t>(bn) * n_groups + gi]) : 8.0f;
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + i * 256;
+      const int r = c >> 3, cc = c & 7;
+      *reinterpret_cast<uint4 *>(&sa[buf][r * kPLD + cc * 8]) = areg[i];
+    }
+    // exact fp16 dequant: (1024+u) - (1024+z) is exact, times s rounds once
+    const __half2 off = __float2half2_rn(1024.0f + bz);
+    const __half2 s2 = __float2half2_rn(bs);
+    const uint32_t wsel[4] = {breg.x, breg.y, breg.z, breg.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t w = wsel[q];
+      uint32_t t[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        __half2 h = __builtin_bit_cast(__half2, ((w >> (4 * j)) & 0x000F000Fu) | kMagic);
+        h = __hmul2(__hsub2(h, off), s2);
+        t[j] = __builtin_bit_cast(uint32_t, h);
+      }
+      const uint4 nat = magic_to_natural(t[0], t[1], t[2], t[3]);
+      *reinterpret_cast<uint4 *>(&sb[buf][brow * kPLD + bhalf * 32 + q * 8]) = nat;
+    }
+  };
+
+  f16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nkt = k / kPBK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nkt) load_tile(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < kPBK / 16; ++ks) {
+      h8_t af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r = wm * 64 + i * 32 + (lane & 31);
+        af[i] = *reinterpret_cast<const h8_t *>(&sa[cur][r * kPLD + ks * 16 + 8 * (lane >> 5)]);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = wn * 64 + j * 32 + (lane & 31);
+        bf[j] = *reinterpret_cast<const h8_t *>(&sb[cur][r * kPLD + ks * 16 + 8 * (lane >> 5)]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nkt) {
+      store_tile(cur ^ 1);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+      if (col >= n_cols) continue;
+      const float b = bias ? mp_h2f(bias[col]) : 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < m_rows) y[static_cast<int64_t>(m) * n_cols + col] = mp_f2h(acc[i][j][r] + b);
+      }
+    }
+}
+
+// ------------------------------------------------------------------ any-shape fallback
+// One thread per output, exact fp16 dequant; used only for shapes the fast
+// kernels do not take (tiny K, K not a multiple of 128 / 64, odd groups).
+__global__ void w4a16_simple_kernel(const uint16_t *__restrict__ x, int64_t m_rows, int64_t k,
+                                    const uint32_t *__restrict__ wq, int64_t n_cols, int64_t kw,
+                                    const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr,
+                                    int n_groups, int gs, const uint16_t *__restrict__ bias,
+                                    uint16_t *__restrict__ y) {
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= m_rows * n_cols) return;
+  const int64_t m = tid / n_cols, n = tid % n_cols;
+  float acc = 0.f;
+  for (int64_t c = 0; c < k; ++c) {
+    const uint32_t u = (wq[n * kw + c / 8] >> (4 * (c & 7))) & 0xFu;
+    const int gi = static_cast<int>(c / gs);
+    const float s = mp_h2f(sc[n * n_groups + gi]);
+    const float z = zr ? mp_h2f(zr[n * n_groups + gi]) : 8.0f;
+    const float w = mp_rh(mp_rh(static_cast<float>(u) - z) * s);
+    acc = fmaf(mp_h2f(x[m * k + c]), w, acc);
+  }
+  if (bias) acc += mp_h2f(bias[n]);
+  y[tid] = mp_f2h(acc);
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+extern "C" int mp_w4_quantize_awq(const void *w, int64_t n, int64_t k, int group_size, int zero_point,
+                                  int32_t *packed, void *scales, void *zeros, void *w_deq,
+                                  mp_stream_t stream) {
+  if (!w || !packed || !scales || (zero_point && !zeros)) return MP_ERR_ARG;
+  if (n <= 0 || k <= 0) return MP_ERR_SHAPE;
+  const int64_t gs = (group_size > 0 && k % group_size == 0) ? group_size : k;
+  if (gs % 8 != 0 && gs != k) return MP_ERR_SHAPE;
+  if (gs > (1 << 30)) return MP_ERR_SHAPE;
+  const int64_t n_groups = k / gs;
+  const int64_t total = n * n_groups;
+  const int64_t kw = mp_cdiv(k, 8);
+  hipLaunchKernelGGL(awq_quantize_kernel, dim3(static_cast<unsigned>(mp_cdiv(total, 4))), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t *>(w), n, k,
+                     static_cast<int>(gs), static_cast<int>(n_groups), zero_point,
+                     reinterpret_cast<uint32_t *>(packed), kw, static_cast<uint16_t *>(scales),
+                     static_cast<uint16_t *>(zeros), static_cast<uint16_t *>(w_deq));
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+extern "C" int mp_w4_quantize_gptq_rtn(const void *w, int w_dtype, int64_t n, int64_t k, int group_size,
+                                       int8_t *int_weight, int32_t *packed, void *scale,
+                                       mp_stream_t stream) {
+  if (!w || !scale) return MP_ERR_ARG;
+  if (w_dtype != MP_F32 && w_dtype != MP_F16 && w_dtype != MP_BF16) return MP_ERR_DTYPE;
+  const int64_t gs = group_size > 0 ? group_size : k;
+  if (n <= 0 || k <= 0 || k % gs != 0) return MP_ERR_SHAPE;
+  const int64_t total = n * (k / gs);
+  const int64_t kw = mp_cdiv(k, 8);
+  if (packed && gs % 8 != 0 && gs != k) return MP_ERR_SHAPE;
+  hipLaunchKernelGGL(gptq_rtn_kernel, dim3(static_cast<unsigned>(mp_cdiv(total, 256))), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), w, w_dtype, n, k, static_cast<int>(gs),
+                     int_weight, reinterpret_cast<uint32_t *>(packed), kw,
+                     static_cast<uint16_t *>(scale));
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+extern "C" int mp_pack_int4(const int8_t *int_weight, int64_t n, int64_t k, int32_t *packed,
+                            int32_t *bad_count, mp_stream_t stream) {
+  if (!int_weight || !packed) return MP_ERR_ARG;
+  if (n < 0 || k < 0) return MP_ERR_SHAPE;
+  const int64_t kw = mp_cdiv(k, 8);
+  if (n * kw == 0) return MP_OK;
+  hipLaunchKernelGGL(pack_int4_kernel, dim3(static_cast<unsigned>(mp_cdiv(n * kw, 256))), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), int_weight, n, k,
+                     reinterpret_cast<uint32_t *>(packed), kw, bad_count);
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+extern "C" int mp_unpack_int4(const int32_t *packed, int64_t n, int64_t k, int8_t *int_weight,
+                              mp_stream_t stream) {
+  if (!int_weight || !packed) return MP_ERR_ARG;
+  if (n < 0 || k < 0) return MP_ERR_SHAPE;
+  if (n * k == 0) return MP_OK;
+  hipLaunchKernelGGL(unpack_int4_kernel, dim3(static_cast<unsigned>(mp_cdiv(n * k, 256))), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint32_t *>(packed), n,
+                     k, mp_cdiv(k, 8), int_weight);
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n,
+                             const void *scales, const void *zeros, int group_size, const void *bias,
+                             void *y, int x_dtype, mp_stream_t stream) {
+  if (!x || !w_packed || !scales || !y) return MP_ERR_ARG;
+  if (x_dtype != MP_F16) return MP_ERR_DTYPE;
+  if (m < 0 || n <= 0 || k <= 0 || group_size <= 0 || k % group_size != 0 || k % 8 != 0)
+    return MP_ERR_SHAPE;
+  if (m == 0) return MP_OK;
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return MP_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int n_groups = static_cast<int>(k / group_size);
+  const auto *xp = static_cast<const uint16_t *>(x);
+  const auto *wp = reinterpret_cast<const uint32_t *>(w_packed);
+  const auto *sp = static_cast<const uint16_t *>(scales);
+  const auto *zp = static_cast<const uint16_t *>(zeros);
+  const auto *bp = static_cast<const uint16_t *>(bias);
+  auto *yp = static_cast<uint16_t *>(y);
+  const bool aligned = mp_aligned(x, 16) && mp_aligned(w_packed, 16);
+  if (m <= 64 && k % 128 == 0 && group_size % 128 == 0 && aligned) {
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(n, 16)));
+    const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
+    if (m <= 16)
+      hipLaunchKernelGGL(w4a16_skinny_kernel<1>, grid, dim3(512), 0, s, xp, mi, ki, wp, ni, sp, zp, n_groups,
+                         group_size, bp, yp);
+    else if (m <= 32)
+      hipLaunchKernelGGL(w4a16_skinny_kernel<2>, grid, dim3(512), 0, s, xp, mi, ki, wp, ni, sp, zp, n_groups,
+                         group_size, bp, yp);
+    else
+      hipLaunchKernelGGL(w4a16_skinny_kernel<4>, grid, dim3(512), 0, s, xp, mi, ki, wp, ni, sp, zp, n_groups,
+                         group_size, bp, yp);
+  } else if (m > 64 && k % kPBK == 0 && group_size % 32 == 0 && aligned) {
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, kPBM)));
+    hipLaunchKernelGGL(w4a16_prefill_kernel, grid, dim3(256), 0, s, xp, static_cast<int>(m),
+                       static_cast<int>(k), wp, static_cast<int>(n), sp, zp, n_groups, group_size, bp, yp);
+  } else {
+    hipLaunchKernelGGL(w4a16_simple_kernel, dim3(static_cast<unsigned>(mp_cdiv(m * n, 256))), dim3(256), 0, s,
+                       xp, m, k, wp, n, mp_cdiv(k, 8), sp, zp, n_groups, group_size, bp, yp);
+  }
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}

@@ -1,0 +1,462 @@
+// W8A8 for gfx950: per-token / per-channel int8 quantizers and the int8 MFMA
+// GEMM with the per-token x per-channel scale epilogue (dense and grouped).
+#include "i8_gemm.h"
+
+namespace {
+
+// ------------------------------------------------------------------ row quantizer
+// One 256-thread workgroup per row.  Pass 1: abs-max; pass 2: codes (the row
+// is re-read from L2).  RULE selects the scale arithmetic (see mp_scale_rule).
+template <int RULE>
+__global__ __launch_bounds__(256) void rowquant_kernel(const void *__restrict__ x, int x_dtype, int64_t k,
+                                                       int8_t *__restrict__ q, float *__restrict__ s_f32,
+                                                       uint16_t *__restrict__ s_src, int s_src_bf16,
+                                                       float min_scale, int32_t *__restrict__ bad) {
+  __shared__ float wmax[4];
+  __shared__ int wbad[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t base = row * k;
+  float amax = 0.f;
+  int nonfinite = 0;
+  for (int64_t c = tid; c < k; c += 256) {
+    const float v = mp_load_as_f32(x, base + c, x_dtype);
+    nonfinite |= !isfinite(v);
+    amax = fmaxf(amax, fabsf(v));
+  }
+  amax = mp_wave_max(amax);
+  const int wb = __any(nonfinite);
+  if ((tid & 63) == 0) {
+    wmax[tid >> 6] = amax;
+    wbad[tid >> 6] = wb;
+  }
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const int row_bad = wbad[0] | wbad[1] | wbad[2] | wbad[3];
+
+  float s;
+  if (RULE == MP_SCALE_FP32) {
+    s = amax / 127.0f;
+    if (s < min_scale) s = min_scale;
+  } else {
+    float a = mp_rh(amax);
+    if (a < 1e-5f) a = mp_rh(1e-5f);
+    s = mp_rh(a / 127.0f);
+  }
+  if (tid == 0) {
+    if (s_f32) s_f32[row] = s;
+    if (s_src) s_src[row] = s_src_bf16 ? mp_f2bf(s) : mp_f2h(s);
+    if (bad && row_bad) atomicAdd(bad, 1);
+  }
+  for (int64_t c = tid; c < k; c += 256) {
+    const float v = mp_load_as_f32(x, base + c, x_dtype);
+    float r;
+    if (RULE == MP_SCALE_FP32) {
+      r = (s == 0.f) ? 0.f : rintf(v / s);
+    } else {
+      r = rintf(mp_rh(v / s));
+    }
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    q[base + c] = static_cast<int8_t>(static_cast<int>(r));
+  }
+}
+
+// ------------------------------------------------------------------ decode GEMV (M <= 64)
+// One workgroup of 8 waves per 16 output columns; the waves split K in
+// 64-byte blocks and are summed exactly (int32) through LDS.  MFMA
+// i32_16x16x64_i8: B = weight rows straight from HBM (16 B per lane), A =
+// int8 activations (row m = lane%16, zero beyond M).
+constexpr int kI8Waves = 8;
+
+template <int MT>
+__global__ __launch_bounds__(512) void i8_skinny_kernel(mp_i8_args p) {
+  __shared__ int red[kI8Waves][MT][4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n_cols = static_cast<int>(p.n);
+  const int k = static_cast<int>(p.k);
+  const int m_rows = static_cast<int>(p.rows);
+  const int n = blockIdx.x * 16 + (lane & 15);
+  const int nn = n < n_cols ? n : n_cols - 1;
+  const int kq = lane >> 4;
+  const int nblk = k >> 6;
+  const int b_begin = (nblk * wave) / kI8Waves;
+  const int b_end = (nblk * (wave + 1)) / kI8Waves;
+  const int8_t *wrow = p.b + static_cast<int64_t>(nn) * k + 16 * kq;
+  const int8_t *arow[MT];
+  bool avalid[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = t * 16 + (lane & 15);
+    avalid[t] = m < m_rows;
+    arow[t] = p.a + static_cast<int64_t>(avalid[t] ? m : 0) * k + 16 * kq;
+  }
+  i4_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = i4_t{0, 0, 0, 0};
+
+  constexpr int U = 4;
+  for (int b = b_begin; b < b_end; b += U) {
+    i4_t wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int bb = (b + u < b_end) ? b + u : b_end - 1;
+      wv[u] = *reinterpret_cast<const i4_t *>(wrow + bb * 64);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (b + u >= b_end) break;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        i4_t a = i4_t{0, 0, 0, 0};
+        if (avalid[t]) a = *reinterpret_cast<const i4_t *>(arow[t] + (b + u) * 64);
+        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wv[u], acc[t], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][t][i][lane] = acc[t][i];
+  __syncthreads();
+  for (int o = threadIdx.x; o < MT * 256; o += blockDim.x) {
+    const int t = o >> 8, r = o & 255;
+    const int l = r & 63, i = r >> 6;
+    int v = 0;
+#pragma unroll
+    for (int w = 0; w < kI8Waves; ++w) v += red[w][t][i][l];
+    const int m = t * 16 + 4 * (l >> 4) + i;
+    const int col = blockIdx.x * 16 + (l & 15);
+    if (m < m_rows && col < n_cols) {
+      float yv = mp_mul(mp_mul(static_cast<float>(v), p.s_a[m]), p.s_b[col]);
+      if (p.bias) yv = mp_add(yv, mp_load_as_f32(p.bias, col, p.bias_dtype));
+      mp_store_from_f32(p.y, static_cast<int64_t>(m) * p.ldy + col, p.out_dtype, yv);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ tiled GEMM
+// BM x BN output tile per workgroup of 4 waves (2 x 2, each (BM/2) x (BN/2)
+// built from MFMA i32_32x32x32_i8 tiles), BK-byte K steps, LDS double buffer
+// with a 16-byte row pad (conflict-free ds_read_b128 for the MFMA fragments).
+// Grouped mode maps blockIdx.y to (expert, row tile) by walking the
+// cumulative row offsets; surplus tiles exit.
+template <int BM, int BN, int BK, int EPI>
+__global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
+  constexpr int LD = BK + 16;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int CA = BM * BK / 16 / 256;  // 16-byte chunks per thread
+  constexpr int CB = BN * BK / 16 / 256;
+  constexpr int CPR = BK / 16;            // chunks per row
+  static_assert(EPI != MP_EPI_SWIGLU || TN == 2, "SwiGLU pairs gate/up in one wave");
+  __shared__ __attribute__((aligned(16))) int8_t sa[2][BM * LD];
+  __shared__ __attribute__((aligned(16))) int8_t sb[2][BN * LD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int64_t row_begin, row_end;
+  int e = 0;
+  if (p.offsets) {
+    int64_t slot = blockIdx.y;
+    bool found = false;
+    for (e = 0; e < p.n_experts; ++e) {
+      const int64_t lo = p.offsets[e], hi = p.offsets[e + 1];
+      const int64_t tiles = (hi - lo + BM - 1) / BM;
+      if (slot < tiles) {
+        row_begin = lo + slot * BM;
+        row_end = hi < row_begin + BM ? hi : row_begin + BM;
+        found = true;
+        break;
+      }
+      slot -= tiles;
+    }
+    if (!found) return;
+  } else {
+    row_begin = static_cast<int64_t>(blockIdx.y) * BM;
+    row_end = p.rows < row_begin + BM ? p.rows : row_begin + BM;
+  }
+  const int64_t k = p.k;
+  const int64_t n_out = p.n;
+  const int64_t nb_rows = (EPI == MP_EPI_SWIGLU) ? 2 * n_out : n_out;  // weight rows per expert
+  const int8_t *bexp = p.b + static_cast<int64_t>(e) * nb_rows * k;
+  const float *sbexp = p.s_b + static_cast<int64_t>(e) * nb_rows;
+  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * ((EPI == MP_EPI_SWIGLU) ? BN / 2 : BN);
+
+  // source rows of this thread's chunks
+  const int8_t *asrc[CA];
+  bool aval[CA];
+#pragma unroll
+  for (int i = 0; i < CA; ++i) {
+    const int c = tid + i * 256;
+    const int64_t r = row_begin + c / CPR;
+    aval[i] = r < row_end;
+    asrc[i] = p.a + (aval[i] ? r : row_begin) * k + (c % CPR) * 16;
+  }
+  const int8_t *bsrc[CB];
+#pragma unroll
+  for (int i = 0; i < CB; ++i) {
+    const int c = tid + i * 256;
+    const int lr = c / CPR;
+    int64_t wr;
+    if (EPI == MP_EPI_SWIGLU) {
+      const int64_t oc = col0 + (lr % (BN / 2));
+      const int64_t occ = oc < n_out ? oc : n_out - 1;
+      wr = (lr < BN / 2) ? occ : n_out + occ;
+    } else {
+      const int64_t oc = col0 + lr;
+      wr = oc < n_out ? oc : n_out - 1;
+    }
+    bsrc[i] = bexp + wr * k + (c % CPR) * 16;
+  }
+
+  i4_t areg[CA], breg[CB];
+  auto load_tile = [&](int64_t kt) {
+    const int64_t off = kt * BK;
+#pragma unroll
+    for (int i = 0; i < CA; ++i)
+      areg[i] = aval[i] ? *reinterpret_cast<const i4_t *>(asrc[i] + off) : i4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < CB; ++i) breg[i] = *reinterpret_cast<const i4_t *>(bsrc[i] + off);
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+      const int c = tid + i * 256;
+      *reinterpret_cast<i4_t *>(&sa[buf][(c / CPR) * LD + (c % CPR) * 16]) = areg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      const int c = tid + i * 256;
+      *reinterpret_cast<i4_t *>(&sb[buf][(c / CPR) * LD + (c % CPR) * 16]) = breg[i];
+    }
+  };
+
+  i16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  // LDS rows read by this lane's fragments
+  int arow_l[TM], brow_l[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) arow_l[i] = (wm * WM + i * 32 + (lane & 31)) * LD + 16 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int lr = (EPI == MP_EPI_SWIGLU) ? (j * (BN / 2) + wn * 32 + (lane & 31))
+                                          : (wn * WN + j * 32 + (lane & 31));
+    brow_l[j] = lr * LD + 16 * (lane >> 5);
+  }
+
+  const int64_t nkt = k / BK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    const int cur = static_cast<int>(kt & 1);
+    if (kt + 1 < nkt) load_tile(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      i4_t af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i4_t *>(&sa[cur][arow_l[i] + ks * 32]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const i4_t *>(&sb[cur][brow_l[j] + ks * 32]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nkt) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- epilogues
+  if (EPI == MP_EPI_SWIGLU) {
+    const int64_t col = col0 + wn * 32 + (lane & 31);
+    const bool cval = col < n_out;
+    const int64_t colc = cval ? col : n_out - 1;
+    const float sg = sbexp[colc], su = sbexp[n_out + colc];
+    float *hbuf = static_cast<float *>(p.y);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = row_begin + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const bool mval = m < row_end;
+        const float sa_m = mval ? p.s_a[m] : 0.f;
+        const float g = mp_mul(mp_mul(static_cast<float>(acc[i][0][r]), sa_m), sg);
+        const float u = mp_mul(mp_mul(static_cast<float>(acc[i][1][r]), sa_m), su);
+        const float den = mp_add(1.0f, expf(-g));
+        const float h = mp_mul(__fdiv_rn(g, den), u);
+        if (mval && cval) hbuf[m * p.ldy + col] = h;
+        float a = (mval && cval) ? fabsf(h) : 0.f;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+        if ((lane & 31) == 0 && mval)
+          p.amax_partial[m * p.n_partial + static_cast<int64_t>(blockIdx.x) * 2 + wn] = a;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = col0 + wn * WN + j * 32 + (lane & 31);
+      if (col >= n_out) continue;
+      const float sb = sbexp[col];
+      const float bv = (EPI == MP_EPI_DENSE && p.bias) ? mp_load_as_f32(p.bias, col, p.bias_dtype) : 0.f;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = row_begin + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (m >= row_end) continue;
+          float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), p.s_a[m]), sb);
+          if (EPI == MP_EPI_DENSE) {
+            if (p.bias) v = mp_add(v, bv);
+            mp_store_from_f32(p.y, m * p.ldy + col, p.out_dtype, v);
+          } else {
+            static_cast<float *>(p.y)[m * p.ldy + col] = v;
+          }
+        }
+    }
+  }
+}
+
+// Any-shape dense fallback: one thread per output.
+__global__ void i8_simple_kernel(mp_i8_args p) {
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= p.rows * p.n) return;
+  const int64_t m = tid / p.n, col = tid % p.n;
+  int acc = 0;
+  for (int64_t c = 0; c < p.k; ++c)
+    acc += static_cast<int>(p.a[m * p.k + c]) * static_cast<int>(p.b[col * p.k + c]);
+  float v = mp_mul(mp_mul(static_cast<float>(acc), p.s_a[m]), p.s_b[col]);
+  if (p.bias) v = mp_add(v, mp_load_as_f32(p.bias, col, p.bias_dtype));
+  mp_store_from_f32(p.y, m * p.ldy + col, p.out_dtype, v);
+}
+
+constexpr int kTBM = 128, kTBN = 128, kTBK = 64;
+
+}  // namespace
+
+// Shared launcher (dense + grouped).
+int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
+  const bool aligned = mp_aligned(a.a, 16) && mp_aligned(a.b, 16);
+  if (a.offsets) {
+    // grouped: tiled kernel only
+    if (a.k % kTBK != 0 || !aligned) return MP_ERR_SHAPE;
+    const int64_t n_tiles =
+        mp_cdiv(a.n, epilogue == MP_EPI_SWIGLU ? kTBN / 2 : kTBN);
+    const int64_t m_slots = mp_cdiv(a.rows, kTBM) + a.n_experts;
+    const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(m_slots));
+    if (epilogue == MP_EPI_SWIGLU)
+      hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_SWIGLU>), grid, dim3(256), 0, stream, a);
+    else if (epilogue == MP_EPI_F32)
+      hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_F32>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_DENSE>), grid, dim3(256), 0, stream, a);
+    MP_CHECK_LAUNCH();
+    return MP_OK;
+  }
+  if (epilogue == MP_EPI_SWIGLU) return MP_ERR_ARG;
+  if (a.rows <= 64 && a.k % 64 == 0 && aligned && epilogue == MP_EPI_DENSE && a.k <= INT32_MAX &&
+      a.n <= INT32_MAX) {
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, 16)));
+    if (a.rows <= 16)
+      hipLaunchKernelGGL(i8_skinny_kernel<1>, grid, dim3(512), 0, stream, a);
+    else if (a.rows <= 32)
+      hipLaunchKernelGGL(i8_skinny_kernel<2>, grid, dim3(512), 0, stream, a);
+    else
+      hipLaunchKernelGGL(i8_skinny_kernel<4>, grid, dim3(512), 0, stream, a);
+  } else if (a.k % kTBK == 0 && aligned) {
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));
+    if (epilogue == MP_EPI_F32)
+      hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_F32>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_DENSE>), grid, dim3(256), 0, stream, a);
+  } else {
+    if (epilogue != MP_EPI_DENSE) return MP_ERR_SHAPE;
+    hipLaunchKernelGGL(i8_simple_kernel, dim3(static_cast<unsigned>(mp_cdiv(a.rows * a.n, 256))), dim3(256), 0,
+                       stream, a);
+  }
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+// ====================================================================== C ABI
+
+extern "C" int mp_quant_per_token_i8(const void *x, int64_t m, int64_t k, int x_dtype, int8_t *q,
+                                     void *scale, int scale_rule, mp_stream_t stream) {
+  if (!x || !q || !scale) return MP_ERR_ARG;
+  if (x_dtype != MP_F16 && x_dtype != MP_BF16 && x_dtype != MP_F32) return MP_ERR_DTYPE;
+  if (m < 0 || k <= 0) return MP_ERR_SHAPE;
+  if (m == 0) return MP_OK;
+  if (m > INT32_MAX) return MP_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (scale_rule == MP_SCALE_FP32) {
+    hipLaunchKernelGGL(rowquant_kernel<MP_SCALE_FP32>, dim3(static_cast<unsigned>(m)), dim3(256), 0, s, x, x_dtype,
+                       k, q, static_cast<float *>(scale), nullptr, 0, 0.0f, nullptr);
+  } else if (scale_rule == MP_SCALE_FP16) {
+    if (x_dtype != MP_F16) return MP_ERR_DTYPE;
+    hipLaunchKernelGGL(rowquant_kernel<MP_SCALE_FP16>, dim3(static_cast<unsigned>(m)), dim3(256), 0, s, x, x_dtype,
+                       k, q, nullptr, static_cast<uint16_t *>(scale), 0, 0.0f, nullptr);
+  } else {
+    return MP_ERR_ARG;
+  }
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+extern "C" int mp_w8_quantize_per_channel(const void *w, int64_t n, int64_t k, int w_dtype, int8_t *q,
+                                          float *scale_f32, void *scale_src, int scale_rule,
+                                          int32_t *bad_count, mp_stream_t stream) {
+  if (!w || !q || !scale_f32) return MP_ERR_ARG;
+  if (w_dtype != MP_F16 && w_dtype != MP_BF16) return MP_ERR_DTYPE;
+  if (n < 0 || k <= 0) return MP_ERR_SHAPE;
+  if (n == 0) return MP_OK;
+  if (n > INT32_MAX) return MP_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (scale_rule == MP_SCALE_FP32) {
+    hipLaunchKernelGGL(rowquant_kernel<MP_SCALE_FP32>, dim3(static_cast<unsigned>(n)), dim3(256), 0, s, w, w_dtype,
+                       k, q, scale_f32, static_cast<uint16_t *>(scale_src), w_dtype == MP_BF16 ? 1 : 0, 1e-8f,
+                       bad_count);
+  } else if (scale_rule == MP_SCALE_FP16) {
+    if (w_dtype != MP_F16) return MP_ERR_DTYPE;
+    hipLaunchKernelGGL(rowquant_kernel<MP_SCALE_FP16>, dim3(static_cast<unsigned>(n)), dim3(256), 0, s, w, w_dtype,
+                       k, q, scale_f32, static_cast<uint16_t *>(scale_src), 0, 0.0f, bad_count);
+  } else {
+    return MP_ERR_ARG;
+  }
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+extern "C" int mp_w8a8_gemm(const int8_t *qx, const float *s_tok, const int8_t *w, const float *s_ch,
+                            const void *bias, int bias_dtype, void *y, int out_dtype, int64_t m, int64_t n,
+                            int64_t k, mp_stream_t stream) {
+  if (!qx || !s_tok || !w || !s_ch || !y) return MP_ERR_ARG;
+  if (out_dtype != MP_F16 && out_dtype != MP_BF16 && out_dtype != MP_F32) return MP_ERR_DTYPE;
+  if (bias && bias_dtype != MP_F16 && bias_dtype != MP_BF16 && bias_dtype != MP_F32) return MP_ERR_DTYPE;
+  if (m < 0 || n <= 0 || k <= 0) return MP_ERR_SHAPE;
+  if (k > (1 << 17)) return MP_ERR_SHAPE;  // int32 accumulator: 127*127*K < 2^31
+  if (m == 0) return MP_OK;
+  mp_i8_args a{};
+  a.a = qx;
+  a.s_a = s_tok;
+  a.b = w;
+  a.s_b = s_ch;
+  a.bias = bias;
+  a.bias_dtype = bias_dtype;
+  a.y = y;
+  a.out_dtype = out_dtype;
+  a.rows = m;
+  a.n = n;
+  a.k = k;
+  a.ldy = n;
+  return mp_launch_i8_gemm(a, MP_EPI_DENSE, reinterpret_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,321 @@
+"""Torch-facing operators over the C ABI.
+
+Each function validates device/dtype/shape/contiguity the way the reference's
+torch extension does with ``TORCH_CHECK`` (``aclnn_grouped_swiglu_out_bridge.cpp:97-109,163-202``),
+allocates outputs with the caching allocator, and launches on the current HIP
+stream.  The functions are also registered as ``torch.ops.mindpipe_amd.*``
+custom ops with fake (meta) implementations so that ``torch.compile`` and graph
+capture see shapes without running kernels (the pattern of the reference's
+``torch.ops.vllm.mindpipe_qwen2_grouped_swiglu_loop_out`` registration,
+``vllm.patch:171-228,291-306``).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import MP_BF16, MP_F16, MP_F32, MP_SCALE_FP16, MP_SCALE_FP32
+
+_DT = {torch.float16: MP_F16, torch.bfloat16: MP_BF16, torch.float32: MP_F32}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, name: str, dtype=None, ndim=None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be on the GPU (mindpipe_amd has no CPU path)")
+    if dtype is not None and t.dtype not in (dtype if isinstance(dtype, tuple) else (dtype,)):
+        raise RuntimeError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise RuntimeError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _dev(t: torch.Tensor):
+    return torch.cuda.device(t.device)
+
+
+# ---------------------------------------------------------------- W4
+def w4_quantize_awq(w: torch.Tensor, group_size: int = 128, zero_point: bool = True,
+                    return_deq: bool = True):
+    """AWQ ``pseudo_quantize_tensor`` on the GPU: returns ``(packed, scales, zeros, w_deq)``."""
+    _need(w, "w", torch.float16, 2)
+    n, k = w.shape
+    g = group_size if (group_size > 0 and k % group_size == 0) else k
+    packed = torch.empty((n, (k + 7) // 8), dtype=torch.int32, device=w.device)
+    scales = torch.empty((n, k // g), dtype=torch.float16, device=w.device)
+    zeros = torch.empty_like(scales) if zero_point else None
+    deq = torch.empty_like(w) if return_deq else None
+    with _dev(w):
+        _lib.check(_lib.load().mp_w4_quantize_awq(
+            w.data_ptr(), n, k, group_size, int(zero_point), packed.data_ptr(), scales.data_ptr(),
+            _ptr(zeros), _ptr(deq), _stream()), "mp_w4_quantize_awq")
+    return packed, scales, zeros, deq
+
+
+def w4_quantize_gptq_rtn(w: torch.Tensor, group_size: int = 128):
+    """GPTQ symmetric RTN group quantizer: returns ``(int_weight int8, packed int32, scale fp16)``."""
+    _need(w, "w", (torch.float32, torch.float16, torch.bfloat16), 2)
+    n, k = w.shape
+    g = group_size if group_size > 0 else k
+    if k % g:
+        raise ValueError("group_size must divide in_features")
+    iw = torch.empty((n, k), dtype=torch.int8, device=w.device)
+    packed = torch.empty((n, (k + 7) // 8), dtype=torch.int32, device=w.device)
+    scale = torch.empty((n, k // g), dtype=torch.float16, device=w.device)
+    with _dev(w):
+        _lib.check(_lib.load().mp_w4_quantize_gptq_rtn(
+            w.data_ptr(), _DT[w.dtype], n, k, g, iw.data_ptr(), packed.data_ptr(), scale.data_ptr(),
+            _stream()), "mp_w4_quantize_gptq_rtn")
+    return iw, packed, scale
+
+
+def pack_int4(int_weight: torch.Tensor) -> torch.Tensor:
+    """``pack_int4_for_vllm`` on the GPU (raises ValueError on out-of-range values)."""
+    if int_weight.dim() != 2:
+        raise ValueError(f"Expected 2D int_weight, got shape {tuple(int_weight.shape)}.")
+    _need(int_weight, "int_weight", torch.int8, 2)
+    n, k = int_weight.shape
+    packed = torch.empty((n, (k + 7) // 8), dtype=torch.int32, device=int_weight.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=int_weight.device)
+    with _dev(int_weight):
+        _lib.check(_lib.load().mp_pack_int4(int_weight.data_ptr(), n, k, packed.data_ptr(), bad.data_ptr(),
+                                            _stream()), "mp_pack_int4")
+    if int(bad.item()) != 0:
+        raise ValueError("int4 weights must be in signed range [-8, 7].")
+    return packed
+
+
+def unpack_int4(packed: torch.Tensor, k: int) -> torch.Tensor:
+    _need(packed, "packed", torch.int32, 2)
+    n = packed.shape[0]
+    if packed.shape[1] != (k + 7) // 8:
+        raise ValueError("packed width does not match k")
+    out = torch.empty((n, k), dtype=torch.int8, device=packed.device)
+    with _dev(packed):
+        _lib.check(_lib.load().mp_unpack_int4(packed.data_ptr(), n, k, out.data_ptr(), _stream()), "mp_unpack_int4")
+    return out
+
+
+@torch.library.custom_op("mindpipe_amd::w4a16_gemm", mutates_args=())
+def w4a16_gemm(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor],
+               group_size: int, bias: Optional[torch.Tensor]) -> torch.Tensor:
+    """``Y = X . dequant(W)^T (+ bias)``; ``x`` fp16 ``[..., K]``; ``w_packed`` int32 ``[N, K/8]``."""
+    _need(x, "x", torch.float16)
+    _need(w_packed, "w_packed", torch.int32, 2)
+    _need(scales, "scales", torch.float16, 2)
+    k = x.shape[-1]
+    n = w_packed.shape[0]
+    if w_packed.shape[1] * 8 != k:
+        raise RuntimeError(f"w_packed {tuple(w_packed.shape)} does not match K={k}")
+    if k % group_size or scales.shape != (n, k // group_size):
+        raise RuntimeError(f"scales {tuple(scales.shape)} do not match N={n}, K={k}, g={group_size}")
+    if zeros is not None:
+        _need(zeros, "zeros", torch.float16, 2)
+        if zeros.shape != scales.shape:
+            raise RuntimeError("zeros must have the shape of scales")
+    if bias is not None:
+        _need(bias, "bias", torch.float16, 1)
+        if bias.shape[0] != n:
+            raise RuntimeError("bias must be [N]")
+    x2 = x.reshape(-1, k)
+    m = x2.shape[0]
+    y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    with _dev(x):
+        _lib.check(_lib.load().mp_w4a16_gemm(
+            x2.data_ptr(), m, k, w_packed.data_ptr(), n, scales.data_ptr(), _ptr(zeros), group_size,
+            _ptr(bias), y.data_ptr(), MP_F16, _stream()), "mp_w4a16_gemm")
+    return y.reshape(*x.shape[:-1], n)
+
+
+@w4a16_gemm.register_fake
+def _(x, w_packed, scales, zeros, group_size, bias):
+    return x.new_empty((*x.shape[:-1], w_packed.shape[0]))
+
+
+# ---------------------------------------------------------------- W8A8
+@torch.library.custom_op("mindpipe_amd::quant_per_token_i8", mutates_args=())
+def quant_per_token_i8(x: torch.Tensor, fp16_scale: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-token dynamic int8 quant: ``(q int8 [..., K], scale [...])``.
+
+    ``fp16_scale=False``: fp32 scale ``absmax/127`` (``npu_dynamic_quant`` contract).
+    ``fp16_scale=True``: fp16 scale and codes of ``quantize_activation_per_token_absmax``.
+    """
+    _need(x, "x", (torch.float16, torch.bfloat16, torch.float32))
+    k = x.shape[-1]
+    x2 = x.reshape(-1, k)
+    m = x2.shape[0]
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    if fp16_scale:
+        if x.dtype != torch.float16:
+            raise RuntimeError("the fp16 scale rule takes fp16 activations")
+        s = torch.empty((m,), dtype=torch.float16, device=x.device)
+    else:
+        s = torch.empty((m,), dtype=torch.float32, device=x.device)
+    with _dev(x):
+        _lib.check(_lib.load().mp_quant_per_token_i8(
+            x2.data_ptr(), m, k, _DT[x.dtype], q.data_ptr(), s.data_ptr(),
+            MP_SCALE_FP16 if fp16_scale else MP_SCALE_FP32, _stream()), "mp_quant_per_token_i8")
+    return q.reshape(x.shape), s.reshape(x.shape[:-1])
+
+
+@quant_per_token_i8.register_fake
+def _(x, fp16_scale=False):
+    return (torch.empty_like(x, dtype=torch.int8),
+            x.new_empty(x.shape[:-1], dtype=torch.float16 if fp16_scale else torch.float32))
+
+
+def w8_quantize_per_channel(w: torch.Tensor, rule: str = "export"):
+    """Per-output-channel int8 weight quant.
+
+    ``rule="export"``: fp32 rule of the Ascend W8A8 export (clamp 1e-8).
+    ``rule="fake"``: fp16 rule of ``quantize_weight_per_channel_absmax``.
+    Returns ``(q int8 [N,K], scale_f32 [N], scale_src [N] in w.dtype)``.
+    """
+    _need(w, "w", (torch.float16, torch.bfloat16), 2)
+    n, k = w.shape
+    q = torch.empty((n, k), dtype=torch.int8, device=w.device)
+    s32 = torch.empty((n,), dtype=torch.float32, device=w.device)
+    ssrc = torch.empty((n,), dtype=w.dtype, device=w.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=w.device)
+    r = MP_SCALE_FP32 if rule == "export" else MP_SCALE_FP16
+    if rule not in ("export", "fake"):
+        raise ValueError(f"unknown rule {rule!r}")
+    with _dev(w):
+        _lib.check(_lib.load().mp_w8_quantize_per_channel(
+            w.data_ptr(), n, k, _DT[w.dtype], q.data_ptr(), s32.data_ptr(), ssrc.data_ptr(), r, bad.data_ptr(),
+            _stream()), "mp_w8_quantize_per_channel")
+    if rule == "export" and int(bad.item()) != 0:
+        raise ValueError("Source weight contains non-finite values")
+    return q, s32, ssrc
+
+
+@torch.library.custom_op("mindpipe_amd::w8a8_gemm", mutates_args=())
+def w8a8_gemm(qx: torch.Tensor, s_tok: torch.Tensor, w: torch.Tensor, s_ch: torch.Tensor,
+              bias: Optional[torch.Tensor], out_dtype: torch.dtype) -> torch.Tensor:
+    """``((Qx . Qw^T) * s_tok) * s_ch (+ bias)`` -> ``out_dtype``; ``qx`` int8 ``[..., K]``, ``w`` int8 ``[N, K]``."""
+    _need(qx, "qx", torch.int8)
+    _need(w, "w", torch.int8, 2)
+    _need(s_tok, "s_tok", torch.float32)
+    _need(s_ch, "s_ch", torch.float32, 1)
+    k = qx.shape[-1]
+    n = w.shape[0]
+    if w.shape[1] != k:
+        raise RuntimeError(f"weight {tuple(w.shape)} does not match K={k}")
+    q2 = qx.reshape(-1, k)
+    m = q2.shape[0]
+    if s_tok.numel() != m or s_ch.numel() != n:
+        raise RuntimeError("scale sizes do not match M / N")
+    if bias is not None:
+        _need(bias, "bias", (torch.float16, torch.bfloat16, torch.float32), 1)
+    y = torch.empty((m, n), dtype=out_dtype, device=qx.device)
+    with _dev(qx):
+        _lib.check(_lib.load().mp_w8a8_gemm(
+            q2.data_ptr(), s_tok.data_ptr(), w.data_ptr(), s_ch.data_ptr(), _ptr(bias),
+            _DT[bias.dtype] if bias is not None else MP_F16, y.data_ptr(), _DT[out_dtype], m, n, k, _stream()),
+            "mp_w8a8_gemm")
+    return y.reshape(*qx.shape[:-1], n)
+
+
+@w8a8_gemm.register_fake
+def _(qx, s_tok, w, s_ch, bias, out_dtype):
+    return qx.new_empty((*qx.shape[:-1], w.shape[0]), dtype=out_dtype)
+
+
+# ---------------------------------------------------------------- MoE
+def moe_permute_quant(x: torch.Tensor, topk_ids: torch.Tensor, n_experts: int):
+    """Routing + per-token quant: ``(routed int8 [T*k,H], routed_scale f32, row_of_slot int32 [T*k],
+    group_offsets int64 [E+1])``.  Rows of ``routed`` past ``group_offsets[-1]`` are unused."""
+    _need(x, "x", (torch.float16, torch.bfloat16, torch.float32), 2)
+    _need(topk_ids, "topk_ids", torch.int32, 2)
+    t, h = x.shape
+    top_k = topk_ids.shape[1]
+    if topk_ids.shape[0] != t:
+        raise RuntimeError("topk_ids must be [T, top_k]")
+    lib = _lib.load()
+    rows = t * top_k
+    routed = torch.empty((rows, h), dtype=torch.int8, device=x.device)
+    rscale = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    row_of_slot = torch.empty((rows,), dtype=torch.int32, device=x.device)
+    offsets = torch.empty((n_experts + 1,), dtype=torch.int64, device=x.device)
+    wsb = lib.mp_moe_route_workspace_bytes(t, h, n_experts)
+    ws = torch.zeros((wsb,), dtype=torch.uint8, device=x.device)
+    with _dev(x):
+        _lib.check(lib.mp_moe_permute_quant(
+            x.data_ptr(), _DT[x.dtype], t, h, topk_ids.data_ptr(), top_k, n_experts, routed.data_ptr(),
+            rscale.data_ptr(), row_of_slot.data_ptr(), offsets.data_ptr(), ws.data_ptr(), wsb, _stream()),
+            "mp_moe_permute_quant")
+    return routed, rscale, row_of_slot, offsets
+
+
+def moe_gmm1_swiglu_quant(routed, rscale, w13, s13, offsets, inter: int):
+    """GMM1 + SwiGLU + requant over expert groups: ``(q int8 [R, I], s f32 [R])``."""
+    _need(routed, "routed", torch.int8, 2)
+    _need(w13, "w13", torch.int8, 3)
+    _need(s13, "s13", torch.float32, 2)
+    _need(offsets, "group_offsets", torch.int64, 1)
+    rows, h = routed.shape
+    e = w13.shape[0]
+    if w13.shape[1] != 2 * inter or w13.shape[2] != h or s13.shape != (e, 2 * inter):
+        raise RuntimeError("w13 must be [E, 2I, H] with s13 [E, 2I]")
+    lib = _lib.load()
+    q = torch.empty((rows, inter), dtype=torch.int8, device=routed.device)
+    s = torch.empty((rows,), dtype=torch.float32, device=routed.device)
+    wsb = lib.mp_moe_gmm1_workspace_bytes(rows, inter)
+    ws = torch.empty((wsb,), dtype=torch.uint8, device=routed.device)
+    with _dev(routed):
+        _lib.check(lib.mp_i8_gemm_swiglu_requant(
+            routed.data_ptr(), rscale.data_ptr(), w13.data_ptr(), s13.data_ptr(), offsets.data_ptr(), e, rows, h,
+            inter, q.data_ptr(), s.data_ptr(), ws.data_ptr(), wsb, _stream()), "mp_i8_gemm_swiglu_requant")
+    return q, s
+
+
+def moe_gmm2(q, s, w2, s2, offsets, out_dtype=torch.float32):
+    _need(q, "q", torch.int8, 2)
+    _need(w2, "w2", torch.int8, 3)
+    _need(s2, "s2", torch.float32, 2)
+    rows, k = q.shape
+    e, n, k2 = w2.shape
+    if k2 != k or s2.shape != (e, n):
+        raise RuntimeError("w2 must be [E, H, I] with s2 [E, H]")
+    y = torch.empty((rows, n), dtype=out_dtype, device=q.device)
+    with _dev(q):
+        _lib.check(_lib.load().mp_w8a8_grouped_gemm(
+            q.data_ptr(), s.data_ptr(), w2.data_ptr(), s2.data_ptr(), offsets.data_ptr(), e, rows, n, k,
+            y.data_ptr(), _DT[out_dtype], _stream()), "mp_w8a8_grouped_gemm")
+    return y
+
+
+def moe_unpermute_combine(y, row_of_slot, topk_w, out_dtype=torch.float16):
+    _need(y, "y", torch.float32, 2)
+    _need(topk_w, "topk_weights", torch.float32, 2)
+    t, top_k = topk_w.shape
+    h = y.shape[1]
+    out = torch.empty((t, h), dtype=out_dtype, device=y.device)
+    with _dev(y):
+        _lib.check(_lib.load().mp_moe_unpermute_combine(
+            y.data_ptr(), row_of_slot.data_ptr(), topk_w.data_ptr(), t, top_k, h, out.data_ptr(), _DT[out_dtype],
+            _stream()), "mp_moe_unpermute_combine")
+    return out
+
+
+def moe_w8a8_forward(x, topk_ids, topk_w, w13, s13, w2, s2, out_dtype=None):
+    """Whole W8A8 MoE chain (routing quant -> GMM1+SwiGLU+requant -> GMM2 -> combine)."""
+    e = w13.shape[0]
+    inter = w2.shape[2]
+    routed, rscale, row_of_slot, offsets = moe_permute_quant(x, topk_ids.to(torch.int32).contiguous(), e)
+    q, s = moe_gmm1_swiglu_quant(routed, rscale, w13, s13, offsets, inter)
+    y = moe_gmm2(q, s, w2, s2, offsets)
+    return moe_unpermute_combine(y, row_of_slot, topk_w.to(torch.float32).contiguous(),
+                                 out_dtype or x.dtype)
