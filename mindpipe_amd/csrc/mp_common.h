@@ -73,5 +73,22 @@ __device__ __forceinline__ float mp_wave_min(float v) {
 // Uniform-order float multiply/add that the compiler may not contract into an
 // FMA: the W8A8 epilogue is specified as (acc * s_tok) * s_ch + bias with
 // three separate roundings.
-__device__ __forceinline__ float mp_mul(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float mp_add(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float mp_mul(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float mp_add(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
+// Workgroup barrier that waits only for this wave's LDS traffic (lgkmcnt),
+// not for outstanding global loads, so weight prefetches stay in flight
+// across it.  The "memory" clobber keeps the compiler from moving LDS
+// accesses across the barrier.
+__device__ __forceinline__ void mp_lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// LDS budget (bytes) for an activation chunk staged by the decode kernels.
+constexpr int kMpXLdsBudget = 60 * 1024;

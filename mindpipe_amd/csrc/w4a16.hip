@@ -189,101 +189,139 @@ __global__ void unpack_int4_kernel(const uint32_t *__restrict__ packed, int64_t 
 
 // ------------------------------------------------------------------ decode GEMV (M <= 64)
 //
-// Work split: one workgroup of 8 waves per 16 output columns; the 8 waves
-// split K into contiguous runs of 128-column blocks and are summed through LDS
-// at the end.  Per 128-column block a lane loads 16 B of packed weights (32
-// columns of one output row, all in one quantization group), so a wave load
-// instruction covers 16 rows x 64 B.  MFMA f32_16x16x32_f16 does the
-// multiply-reduce: B = weights (column n = lane%16), A = activations (row m =
-// lane%16).  The weights enter the MFMA as (1024 + u) straight from the bit
-// trick; a second MFMA against ones gives sum(x) per row, and
-//   sum_k x_k (u_k - z) s = s * (acc - (1024 + z) * sum_k x_k)
-// removes the offset per group in fp32, so dequantisation costs two VALU ops
-// per weight pair.
-constexpr int kSkinnyWaves = 8;
-
-template <int MT>
-__global__ __launch_bounds__(512) void w4a16_skinny_kernel(
+// Work split: one workgroup of NW waves per 16 output columns; the waves take
+// 128-column K blocks round-robin and are summed through LDS at the end.  The
+// activations are staged once per workgroup into LDS (in K chunks that fit
+// the LDS budget), already permuted into the order the nibble trick produces,
+// together with the per-block row sums.  Per block a lane loads 16 B of packed
+// weights (32 columns of one output row, all inside one quantization group);
+// a wave load covers 16 rows x 64 B.  MFMA f32_16x16x32_f16 does the
+// multiply-reduce with B = weights (column n = lane%16) and A = activations
+// (row m = lane%16).  Weights enter the MFMA as (1024 + u) straight from the
+// bit trick and the offset is removed per group in fp32:
+//   sum_k x_k (u_k - z) s = s * (acc - (1024 + z) * sum_k x_k),
+// so dequantisation costs two VALU ops per weight pair.  Weight loads are
+// double-buffered, U blocks per buffer.
+template <int MT, int NW>
+__global__ __launch_bounds__(NW * 64) void w4a16_skinny_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups, int gs,
-    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
-  __shared__ float red[kSkinnyWaves][MT][4][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, int cb) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int U = 4;
+  const int xstride = cb * 256 + 16;  // bytes per staged row (16 B skew against bank conflicts)
+  uint8_t *xs = smem;
+  float *xsum = reinterpret_cast<float *>(smem + m_rows * xstride);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int n = blockIdx.x * 16 + (lane & 15);
   const int nn = n < n_cols ? n : n_cols - 1;
   const int kq = lane >> 4;
   const int kw = k >> 3;
   const int nblk = k >> 7;
   const int bpg = gs >> 7;
-  const int b_begin = (nblk * wave) / kSkinnyWaves;
-  const int b_end = (nblk * (wave + 1)) / kSkinnyWaves;
-
   const uint32_t *wrow = wq + static_cast<int64_t>(nn) * kw + 4 * kq;
   const uint16_t *srow = sc + static_cast<int64_t>(nn) * n_groups;
   const uint16_t *zrow = zr ? zr + static_cast<int64_t>(nn) * n_groups : nullptr;
 
-  const uint16_t *xrow[MT];
-  bool xvalid[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const int m = t * 16 + (lane & 15);
-    xvalid[t] = m < m_rows;
-    xrow[t] = x + static_cast<int64_t>(xvalid[t] ? m : 0) * k + 32 * kq;
-  }
-
   f4_t acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
-  const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
   const h8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
 
-  constexpr int U = 4;  // blocks whose loads are in flight together
-  for (int b = b_begin; b < b_end; b += U) {
-    uint4 wv[U];
-    float s[U], zc[U];
+  uint4 wa[U], wb[U];
+  float sa[U], za[U], sb[U], zb[U];
+
+  for (int c0 = 0; c0 < nblk; c0 += cb) {
+    const int cbn = (nblk - c0) < cb ? (nblk - c0) : cb;
+    const int nmine = cbn > wave ? (cbn - wave + NW - 1) / NW : 0;
+    auto issue = [&](uint4 *w, float *s, float *z, int r0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int bb = (b + u < b_end) ? b + u : b_end - 1;
-      wv[u] = *reinterpret_cast<const uint4 *>(wrow + bb * 16);
-      const int gi = bb / bpg;
-      s[u] = mp_h2f(srow[gi]);
-      zc[u] = 1024.0f + (zrow ? mp_h2f(zrow[gi]) : 8.0f);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (b + u >= b_end) break;
-      const int kb = (b + u) * 128;
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        f4_t cg = {0.f, 0.f, 0.f, 0.f};
-        f4_t cs = {0.f, 0.f, 0.f, 0.f};
-        const uint32_t wsel[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          h8_t a = zero8;
-          if (xvalid[t]) a = perm_to_magic(*reinterpret_cast<const uint4 *>(xrow[t] + kb + 8 * q));
-          const h8_t bq = dq_magic(wsel[q]);
-          cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, cg, 0, 0, 0);
-          cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ones, cs, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(s[u], fmaf(-zc[u], cs[i], cg[i]), acc[t][i]);
+      for (int u = 0; u < U; ++u) {
+        int r = r0 + u;
+        r = r < nmine ? r : nmine - 1;
+        const int b = c0 + wave + NW * r;
+        w[u] = *reinterpret_cast<const uint4 *>(wrow + b * 16);
+        const int gi = b / bpg;
+        s[u] = mp_h2f(srow[gi]);
+        z[u] = 1024.0f + (zrow ? mp_h2f(zrow[gi]) : 8.0f);
       }
+    };
+    auto compute = [&](const uint4 *w, const float *s, const float *z, int r0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = r0 + u;
+        if (r >= nmine) break;
+        const int jl = wave + NW * r;
+        const uint32_t wsel[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const int ma = t * 16 + (lane & 15);
+          f4_t cg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            h8_t a = zero8;
+            if (ma < m_rows)
+              a = *reinterpret_cast<const h8_t *>(xs + ma * xstride + (jl * 128 + 32 * kq + 8 * q) * 2);
+            cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, dq_magic(wsel[q]), cg, 0, 0, 0);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int mc = t * 16 + 4 * kq + i;
+            const float xsv = mc < m_rows ? xsum[mc * cb + jl] : 0.f;
+            acc[t][i] = fmaf(s[u], fmaf(-z[u], xsv, cg[i]), acc[t][i]);
+          }
+        }
+      }
+    };
+
+    if (nmine > 0) issue(wa, sa, za, 0);
+    if (c0 > 0) mp_lds_barrier();
+    // stage x[:, chunk] permuted into LDS: pieces of 8 halves
+    const int pieces = m_rows * cbn * 16;
+    for (int p = tid; p < pieces; p += NW * 64) {
+      const int m = p / (cbn * 16), c8 = p % (cbn * 16);
+      const uint4 d = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(m) * k + c0 * 128 + c8 * 8);
+      *reinterpret_cast<h8_t *>(xs + m * xstride + c8 * 16) = perm_to_magic(d);
+    }
+    mp_lds_barrier();
+    for (int t = tid; t < m_rows * cbn; t += NW * 64) {
+      const int m = t / cbn, j = t % cbn;
+      const h8_t *src = reinterpret_cast<const h8_t *>(xs + m * xstride + j * 256);
+      float sum = 0.f;
+#pragma unroll 4
+      for (int c = 0; c < 16; ++c) {
+        const h8_t v = src[c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += static_cast<float>(v[e]);
+      }
+      xsum[m * cb + j] = sum;
+    }
+    mp_lds_barrier();
+
+    for (int r0 = 0; r0 < nmine; r0 += 2 * U) {
+      if (r0 + U < nmine) issue(wb, sb, zb, r0 + U);
+      compute(wa, sa, za, r0);
+      if (r0 + U >= nmine) break;
+      if (r0 + 2 * U < nmine) issue(wa, sa, za, r0 + 2 * U);
+      compute(wb, sb, zb, r0 + U);
     }
   }
 
+  mp_lds_barrier();
+  float *red = reinterpret_cast<float *>(smem);  // [NW][MT][4][64]
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][t][i][lane] = acc[t][i];
-  __syncthreads();
-  for (int o = threadIdx.x; o < MT * 256; o += blockDim.x) {
+    for (int i = 0; i < 4; ++i) red[((wave * MT + t) * 4 + i) * 64 + lane] = acc[t][i];
+  mp_lds_barrier();
+  for (int o = tid; o < MT * 256; o += NW * 64) {
     const int t = o >> 8, r = o & 255;
     const int l = r & 63, i = r >> 6;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < kSkinnyWaves; ++w) v += red[w][t][i][l];
+    for (int w = 0; w < NW; ++w) v += red[((w * MT + t) * 4 + i) * 64 + l];
     const int m = t * 16 + 4 * (l >> 4) + i;
     const int col = blockIdx.x * 16 + (l & 15);
     if (m < m_rows && col < n_cols) {
@@ -515,11 +553,11 @@ extern "C" int mp_unpack_int4(const int32_t *packed, int64_t n, int64_t k, int8_
 extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n,
                              const void *scales, const void *zeros, int group_size, const void *bias,
                              void *y, int x_dtype, mp_stream_t stream) {
-  if (!x || !w_packed || !scales || !y) return MP_ERR_ARG;
   if (x_dtype != MP_F16) return MP_ERR_DTYPE;
   if (m < 0 || n <= 0 || k <= 0 || group_size <= 0 || k % group_size != 0 || k % 8 != 0)
     return MP_ERR_SHAPE;
   if (m == 0) return MP_OK;
+  if (!x || !w_packed || !scales || !y) return MP_ERR_ARG;
   if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return MP_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int n_groups = static_cast<int>(k / group_size);
@@ -531,17 +569,25 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
   auto *yp = static_cast<uint16_t *>(y);
   const bool aligned = mp_aligned(x, 16) && mp_aligned(w_packed, 16);
   if (m <= 64 && k % 128 == 0 && group_size % 128 == 0 && aligned) {
-    const dim3 grid(static_cast<unsigned>(mp_cdiv(n, 16)));
     const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
-    if (m <= 16)
-      hipLaunchKernelGGL(w4a16_skinny_kernel<1>, grid, dim3(512), 0, s, xp, mi, ki, wp, ni, sp, zp, n_groups,
-                         group_size, bp, yp);
-    else if (m <= 32)
-      hipLaunchKernelGGL(w4a16_skinny_kernel<2>, grid, dim3(512), 0, s, xp, mi, ki, wp, ni, sp, zp, n_groups,
-                         group_size, bp, yp);
+    const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    const int nw = mt == 4 ? 4 : 8;
+    const int nblk = ki / 128;
+    int cb = (kMpXLdsBudget / mi - 16) / 260;
+    cb = cb < 1 ? 1 : (cb > nblk ? nblk : cb);
+    size_t smem = static_cast<size_t>(mi) * (cb * 256 + 16) + static_cast<size_t>(mi) * cb * 4;
+    const size_t red = static_cast<size_t>(nw) * mt * 1024;
+    smem = smem > red ? smem : red;
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(n, 16)));
+    if (mt == 1)
+      hipLaunchKernelGGL((w4a16_skinny_kernel<1, 8>), grid, dim3(512), smem, s, xp, mi, ki, wp, ni, sp, zp,
+                         n_groups, group_size, bp, yp, cb);
+    else if (mt == 2)
+      hipLaunchKernelGGL((w4a16_skinny_kernel<2, 8>), grid, dim3(512), smem, s, xp, mi, ki, wp, ni, sp, zp,
+                         n_groups, group_size, bp, yp, cb);
     else
-      hipLaunchKernelGGL(w4a16_skinny_kernel<4>, grid, dim3(512), 0, s, xp, mi, ki, wp, ni, sp, zp, n_groups,
-                         group_size, bp, yp);
+      hipLaunchKernelGGL((w4a16_skinny_kernel<4, 4>), grid, dim3(256), smem, s, xp, mi, ki, wp, ni, sp, zp,
+                         n_groups, group_size, bp, yp, cb);
   } else if (m > 64 && k % kPBK == 0 && group_size % 32 == 0 && aligned) {
     const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, kPBM)));
     hipLaunchKernelGGL(w4a16_prefill_kernel, grid, dim3(256), 0, s, xp, static_cast<int>(m),

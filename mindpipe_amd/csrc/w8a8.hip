@@ -62,17 +62,20 @@ __global__ __launch_bounds__(256) void rowquant_kernel(const void *__restrict__ 
 }
 
 // ------------------------------------------------------------------ decode GEMV (M <= 64)
-// One workgroup of 8 waves per 16 output columns; the waves split K in
-// 64-byte blocks and are summed exactly (int32) through LDS.  MFMA
-// i32_16x16x64_i8: B = weight rows straight from HBM (16 B per lane), A =
-// int8 activations (row m = lane%16, zero beyond M).
-constexpr int kI8Waves = 8;
-
-template <int MT>
-__global__ __launch_bounds__(512) void i8_skinny_kernel(mp_i8_args p) {
-  __shared__ int red[kI8Waves][MT][4][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+// One workgroup of NW waves per 16 output columns; waves take 64-byte K blocks
+// round-robin and are summed exactly (int32) through LDS.  The int8
+// activations are staged once per workgroup into LDS (K chunks within the LDS
+// budget).  MFMA i32_16x16x64_i8: B = weight rows straight from HBM (16 B per
+// lane), A = activations from LDS (row m = lane%16, zero beyond M).  Weight
+// loads are double-buffered, U blocks per buffer.
+template <int MT, int NW>
+__global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int U = 4;
+  const int xstride = cb * 64 + 16;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int n_cols = static_cast<int>(p.n);
   const int k = static_cast<int>(p.k);
   const int m_rows = static_cast<int>(p.rows);
@@ -80,51 +83,68 @@ __global__ __launch_bounds__(512) void i8_skinny_kernel(mp_i8_args p) {
   const int nn = n < n_cols ? n : n_cols - 1;
   const int kq = lane >> 4;
   const int nblk = k >> 6;
-  const int b_begin = (nblk * wave) / kI8Waves;
-  const int b_end = (nblk * (wave + 1)) / kI8Waves;
   const int8_t *wrow = p.b + static_cast<int64_t>(nn) * k + 16 * kq;
-  const int8_t *arow[MT];
-  bool avalid[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const int m = t * 16 + (lane & 15);
-    avalid[t] = m < m_rows;
-    arow[t] = p.a + static_cast<int64_t>(avalid[t] ? m : 0) * k + 16 * kq;
-  }
   i4_t acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = i4_t{0, 0, 0, 0};
+  i4_t wa[U], wb[U];
 
-  constexpr int U = 4;
-  for (int b = b_begin; b < b_end; b += U) {
-    i4_t wv[U];
+  for (int c0 = 0; c0 < nblk; c0 += cb) {
+    const int cbn = (nblk - c0) < cb ? (nblk - c0) : cb;
+    const int nmine = cbn > wave ? (cbn - wave + NW - 1) / NW : 0;
+    auto issue = [&](i4_t *w, int r0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int bb = (b + u < b_end) ? b + u : b_end - 1;
-      wv[u] = *reinterpret_cast<const i4_t *>(wrow + bb * 64);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (b + u >= b_end) break;
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        i4_t a = i4_t{0, 0, 0, 0};
-        if (avalid[t]) a = *reinterpret_cast<const i4_t *>(arow[t] + (b + u) * 64);
-        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wv[u], acc[t], 0, 0, 0);
+      for (int u = 0; u < U; ++u) {
+        int r = r0 + u;
+        r = r < nmine ? r : nmine - 1;
+        w[u] = *reinterpret_cast<const i4_t *>(wrow + (c0 + wave + NW * r) * 64);
       }
+    };
+    auto compute = [&](const i4_t *w, int r0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = r0 + u;
+        if (r >= nmine) break;
+        const int jl = wave + NW * r;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const int ma = t * 16 + (lane & 15);
+          i4_t a = i4_t{0, 0, 0, 0};
+          if (ma < m_rows) a = *reinterpret_cast<const i4_t *>(smem + ma * xstride + jl * 64 + 16 * kq);
+          acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w[u], acc[t], 0, 0, 0);
+        }
+      }
+    };
+    if (nmine > 0) issue(wa, 0);
+    if (c0 > 0) mp_lds_barrier();
+    const int pieces = m_rows * cbn * 4;
+    for (int q = tid; q < pieces; q += NW * 64) {
+      const int m = q / (cbn * 4), c16 = q % (cbn * 4);
+      *reinterpret_cast<i4_t *>(smem + m * xstride + c16 * 16) =
+          *reinterpret_cast<const i4_t *>(p.a + static_cast<int64_t>(m) * k + c0 * 64 + c16 * 16);
+    }
+    mp_lds_barrier();
+    for (int r0 = 0; r0 < nmine; r0 += 2 * U) {
+      if (r0 + U < nmine) issue(wb, r0 + U);
+      compute(wa, r0);
+      if (r0 + U >= nmine) break;
+      if (r0 + 2 * U < nmine) issue(wa, r0 + 2 * U);
+      compute(wb, r0 + U);
     }
   }
+  mp_lds_barrier();
+  int *red = reinterpret_cast<int *>(smem);  // [NW][MT][4][64]
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][t][i][lane] = acc[t][i];
-  __syncthreads();
-  for (int o = threadIdx.x; o < MT * 256; o += blockDim.x) {
+    for (int i = 0; i < 4; ++i) red[((wave * MT + t) * 4 + i) * 64 + lane] = acc[t][i];
+  mp_lds_barrier();
+  for (int o = tid; o < MT * 256; o += NW * 64) {
     const int t = o >> 8, r = o & 255;
     const int l = r & 63, i = r >> 6;
     int v = 0;
 #pragma unroll
-    for (int w = 0; w < kI8Waves; ++w) v += red[w][t][i][l];
+    for (int w = 0; w < NW; ++w) v += red[((w * MT + t) * 4 + i) * 64 + l];
     const int m = t * 16 + 4 * (l >> 4) + i;
     const int col = blockIdx.x * 16 + (l & 15);
     if (m < m_rows && col < n_cols) {
@@ -366,13 +386,22 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
   if (epilogue == MP_EPI_SWIGLU) return MP_ERR_ARG;
   if (a.rows <= 64 && a.k % 64 == 0 && aligned && epilogue == MP_EPI_DENSE && a.k <= INT32_MAX &&
       a.n <= INT32_MAX) {
+    const int mi = static_cast<int>(a.rows);
+    const int mt = mi <= 16 ? 1 : (mi <= 32 ? 2 : 4);
+    const int nw = mt == 4 ? 4 : 8;
+    const int nblk = static_cast<int>(a.k / 64);
+    int cb = (kMpXLdsBudget / mi - 16) / 64;
+    cb = cb < 1 ? 1 : (cb > nblk ? nblk : cb);
+    size_t smem = static_cast<size_t>(mi) * (cb * 64 + 16);
+    const size_t red = static_cast<size_t>(nw) * mt * 1024;
+    smem = smem > red ? smem : red;
     const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, 16)));
-    if (a.rows <= 16)
-      hipLaunchKernelGGL(i8_skinny_kernel<1>, grid, dim3(512), 0, stream, a);
-    else if (a.rows <= 32)
-      hipLaunchKernelGGL(i8_skinny_kernel<2>, grid, dim3(512), 0, stream, a);
+    if (mt == 1)
+      hipLaunchKernelGGL((i8_skinny_kernel<1, 8>), grid, dim3(512), smem, stream, a, cb);
+    else if (mt == 2)
+      hipLaunchKernelGGL((i8_skinny_kernel<2, 8>), grid, dim3(512), smem, stream, a, cb);
     else
-      hipLaunchKernelGGL(i8_skinny_kernel<4>, grid, dim3(512), 0, stream, a);
+      hipLaunchKernelGGL((i8_skinny_kernel<4, 4>), grid, dim3(256), smem, stream, a, cb);
   } else if (a.k % kTBK == 0 && aligned) {
     const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));
     if (epilogue == MP_EPI_F32)
