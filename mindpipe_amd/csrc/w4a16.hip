@@ -189,126 +189,244 @@ __global__ void unpack_int4_kernel(const uint32_t *__restrict__ packed, int64_t 
 
 // ------------------------------------------------------------------ decode GEMV (M <= 64)
 //
-// Work split: one workgroup of NW waves per 16 output columns; the waves take
-// 128-column K blocks round-robin and are summed through LDS at the end.  The
-// activations are staged once per workgroup into LDS (in K chunks that fit
-// the LDS budget), already permuted into the order the nibble trick produces,
-// together with the per-block row sums.  Per block a lane loads 16 B of packed
-// weights (32 columns of one output row, all inside one quantization group);
-// a wave load covers 16 rows x 64 B.  MFMA f32_16x16x32_f16 does the
-// multiply-reduce with B = weights (column n = lane%16) and A = activations
-// (row m = lane%16).  Weights enter the MFMA as (1024 + u) straight from the
-// bit trick and the offset is removed per group in fp32:
-//   sum_k x_k (u_k - z) s = s * (acc - (1024 + z) * sum_k x_k),
-// so dequantisation costs two VALU ops per weight pair.  Weight loads are
-// double-buffered, U blocks per buffer.
-template <int MT, int NW>
-__global__ __launch_bounds__(NW * 64) void w4a16_skinny_kernel(
+// Work split: a workgroup has 8 waves arranged as T = 8/S column tiles of 16
+// output columns, S waves per tile splitting K into contiguous block ranges
+// (a block = 128 K columns = one quantization group at g = 128).  S is chosen
+// on the host so that about 2048 waves stream the weights; S = 1 needs no
+// cross-wave reduction.  The activations are staged once per workgroup into
+// LDS (K chunks within the LDS budget), already permuted into the order the
+// nibble trick produces, with per-(row, block) sums.  Per block a lane loads
+// 16 B of packed weights (32 columns of one output row); a wave load covers 16
+// rows x 64 B.  One 32-bit load brings the fp16 scales (and zeros) of two
+// consecutive blocks.  MFMA f32_16x16x32_f16: B = weights (column n =
+// lane%16), A = activations (row m = lane%16).  Weights enter the MFMA as
+// (1024 + u) from the bit trick; per group
+//   sum_k x_k (u_k - z) s = s * (acc - (1024 + z) * sum_k x_k)
+// removes the offset in fp32.  The hot path is straight-line code (clamped
+// loads, surplus blocks masked by a zero scale): control-flow joins make the
+// compiler wait for every outstanding load.
+
+// (w & mask) | magic with both constants held in VGPRs: the compiler then
+// emits one v_and_or_b32 per nibble pair (with literal operands it needs two
+// instructions, since a gfx9 VOP3 instruction takes one literal / scalar
+// operand).
+__device__ __forceinline__ h8_t dq_magic_fast(uint32_t w, uint32_t mask_v, uint32_t magic_v) {
+  union {
+    uint32_t u[4];
+    h8_t h;
+  } r;
+  r.u[0] = (w & mask_v) | magic_v;
+  r.u[1] = ((w >> 4) & mask_v) | magic_v;
+  r.u[2] = ((w >> 8) & mask_v) | magic_v;
+  r.u[3] = ((w >> 12) & mask_v) | magic_v;
+  return r.h;
+}
+
+// LDS layout of one K chunk (cb blocks), all offsets in bytes:
+//   xs   [M][cb*256 + 16]  activations, permuted to the nibble-trick order
+//   xsum [M][cb]            fp32 per-(row, block) sums
+//   sz   [T*16][cb]         (scale | zero << 16) per (output row, group)
+//   dummy 16 B              sink for masked stores
+constexpr int kDecXPieces = 4;  // 16-B activation pieces staged per thread per chunk
+constexpr int kDecSPieces = 2;  // scale (and zero) pieces staged per thread per chunk
+
+struct DecodeLds {
+  int xstride, xsum_off, sz_off, dummy_off, bytes;
+  __host__ __device__ DecodeLds(int m, int cb, int tiles) {
+    xstride = cb * 256 + 16;
+    xsum_off = m * xstride;
+    sz_off = xsum_off + m * cb * 4;
+    dummy_off = sz_off + tiles * 16 * cb * 4;
+    bytes = dummy_off + 16;
+  }
+};
+
+template <int MT, int S, bool ZP, bool SZ16>
+__global__ __launch_bounds__(512) void w4a16_decode_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
-    const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups, int gs,
+    const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, int cb) {
+  constexpr int NW = 8, T = NW / S, U = 4, NT = NW * 64;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  constexpr int U = 4;
-  const int xstride = cb * 256 + 16;  // bytes per staged row (16 B skew against bank conflicts)
+  const DecodeLds L(m_rows, cb, T);
   uint8_t *xs = smem;
-  float *xsum = reinterpret_cast<float *>(smem + m_rows * xstride);
+  float *xsum = reinterpret_cast<float *>(smem + L.xsum_off);
+  uint32_t *szl = reinterpret_cast<uint32_t *>(smem + L.sz_off);
+  uint8_t *dummy = smem + L.dummy_off;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int n = blockIdx.x * 16 + (lane & 15);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = wave / S, sw = wave % S;
+  const int wg_col0 = blockIdx.x * T * 16;
+  const int n = wg_col0 + tile * 16 + (lane & 15);
   const int nn = n < n_cols ? n : n_cols - 1;
   const int kq = lane >> 4;
   const int kw = k >> 3;
   const int nblk = k >> 7;
-  const int bpg = gs >> 7;
   const uint32_t *wrow = wq + static_cast<int64_t>(nn) * kw + 4 * kq;
-  const uint16_t *srow = sc + static_cast<int64_t>(nn) * n_groups;
-  const uint16_t *zrow = zr ? zr + static_cast<int64_t>(nn) * n_groups : nullptr;
+  const int mlast = m_rows - 1;
+  uint32_t magic_v = kMagic, mask_v = 0x000F000Fu;
+  asm volatile("" : "+v"(magic_v), "+v"(mask_v));  // opaque: keep both constants in VGPRs
 
   f4_t acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
   const h8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-
   uint4 wa[U], wb[U];
-  float sa[U], za[U], sb[U], zb[U];
 
   for (int c0 = 0; c0 < nblk; c0 += cb) {
     const int cbn = (nblk - c0) < cb ? (nblk - c0) : cb;
-    const int nmine = cbn > wave ? (cbn - wave + NW - 1) / NW : 0;
-    auto issue = [&](uint4 *w, float *s, float *z, int r0) {
+    const int lo = (cbn * sw) / S;
+    const int hi = (cbn * (sw + 1)) / S;
+    const int nmine = hi - lo;
+    const int blast = c0 + cbn - 1;
+    auto issue = [&](uint4 *w, int r0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        int r = r0 + u;
-        r = r < nmine ? r : nmine - 1;
-        const int b = c0 + wave + NW * r;
+        int b = c0 + lo + r0 + u;
+        b = b < blast ? b : blast;
         w[u] = *reinterpret_cast<const uint4 *>(wrow + b * 16);
-        const int gi = b / bpg;
-        s[u] = mp_h2f(srow[gi]);
-        z[u] = 1024.0f + (zrow ? mp_h2f(zrow[gi]) : 8.0f);
       }
     };
-    auto compute = [&](const uint4 *w, const float *s, const float *z, int r0) {
+    auto compute = [&](const uint4 *w, int r0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int r = r0 + u;
-        if (r >= nmine) break;
-        const int jl = wave + NW * r;
+        const bool live = r < nmine;
+        int jl = lo + r;
+        jl = jl < cbn - 1 ? jl : cbn - 1;
         const uint32_t wsel[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+        const uint32_t szv = szl[(tile * 16 + (lane & 15)) * cb + jl];
+        const float su = live ? mp_h2f(static_cast<uint16_t>(szv)) : 0.0f;
+        const float zu = 1024.0f + (ZP ? mp_h2f(static_cast<uint16_t>(szv >> 16)) : 8.0f);
+        h8_t bq[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bq[q] = dq_magic_fast(wsel[q], mask_v, magic_v);
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           const int ma = t * 16 + (lane & 15);
+          const int mac = ma < mlast ? ma : mlast;
           f4_t cg = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            h8_t a = zero8;
-            if (ma < m_rows)
-              a = *reinterpret_cast<const h8_t *>(xs + ma * xstride + (jl * 128 + 32 * kq + 8 * q) * 2);
-            cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, dq_magic(wsel[q]), cg, 0, 0, 0);
+            h8_t a = *reinterpret_cast<const h8_t *>(xs + mac * L.xstride + (jl * 128 + 32 * kq + 8 * q) * 2);
+            a = ma < m_rows ? a : zero8;
+            cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[q], cg, 0, 0, 0);
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int mc = t * 16 + 4 * kq + i;
-            const float xsv = mc < m_rows ? xsum[mc * cb + jl] : 0.f;
-            acc[t][i] = fmaf(s[u], fmaf(-z[u], xsv, cg[i]), acc[t][i]);
+            const int mcc = mc < mlast ? mc : mlast;
+            float xsv = xsum[mcc * cb + jl];
+            xsv = mc < m_rows ? xsv : 0.f;
+            acc[t][i] = fmaf(su, fmaf(-zu, xsv, cg[i]), acc[t][i]);
           }
         }
       }
     };
 
-    if (nmine > 0) issue(wa, sa, za, 0);
-    if (c0 > 0) mp_lds_barrier();
-    // stage x[:, chunk] permuted into LDS: pieces of 8 halves
+    // ---- staging loads (activations, then scales / zeros), then the weight
+    // prefetch, so that the LDS writes wait only for the older staging loads
+    // (the host sizes cb so that the pieces fit kDecXPieces / kDecSPieces per thread)
+    constexpr int PMAX = kDecXPieces;
     const int pieces = m_rows * cbn * 16;
-    for (int p = tid; p < pieces; p += NW * 64) {
-      const int m = p / (cbn * 16), c8 = p % (cbn * 16);
-      const uint4 d = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(m) * k + c0 * 128 + c8 * 8);
-      *reinterpret_cast<h8_t *>(xs + m * xstride + c8 * 16) = perm_to_magic(d);
-    }
-    mp_lds_barrier();
-    for (int t = tid; t < m_rows * cbn; t += NW * 64) {
-      const int m = t / cbn, j = t % cbn;
-      const h8_t *src = reinterpret_cast<const h8_t *>(xs + m * xstride + j * 256);
-      float sum = 0.f;
-#pragma unroll 4
-      for (int c = 0; c < 16; ++c) {
-        const h8_t v = src[c];
+    uint4 xv[PMAX];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sum += static_cast<float>(v[e]);
+    for (int i = 0; i < PMAX; ++i) {
+      int p = tid + i * NT;
+      p = p < pieces ? p : pieces - 1;
+      const int m = p / (cbn * 16), c8 = p % (cbn * 16);
+      xv[i] = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(m) * k + c0 * 128 + c8 * 8);
+    }
+    // scale / zero pieces: 8 groups (16 B) or 2 groups (4 B) of one output row
+    constexpr int GPP = SZ16 ? 8 : 2;
+    constexpr int SMAX = kDecSPieces;
+    const int ppr = (cbn + GPP - 1) / GPP;               // pieces per row
+    const int spieces = T * 16 * ppr;
+    uint4 sv[SMAX], zv[SMAX];
+#pragma unroll
+    for (int i = 0; i < SMAX; ++i) {
+      int p = tid + i * NT;
+      p = p < spieces ? p : spieces - 1;
+      const int r = p / ppr, c = p % ppr;
+      int row = wg_col0 + r;
+      row = row < n_cols ? row : n_cols - 1;
+      const int64_t off = static_cast<int64_t>(row) * n_groups + c0 + c * GPP;
+      if (SZ16) {
+        sv[i] = *reinterpret_cast<const uint4 *>(sc + off);
+        zv[i] = ZP ? *reinterpret_cast<const uint4 *>(zr + off) : make_uint4(0, 0, 0, 0);
+      } else {
+        sv[i] = make_uint4(*reinterpret_cast<const uint32_t *>(sc + off), 0u, 0u, 0u);
+        zv[i] = make_uint4(ZP ? *reinterpret_cast<const uint32_t *>(zr + off) : 0u, 0u, 0u, 0u);
       }
-      xsum[m * cb + j] = sum;
+    }
+    issue(wa, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (c0 > 0) mp_lds_barrier();
+#pragma unroll
+    for (int i = 0; i < PMAX; ++i) {
+      const int p = tid + i * NT;
+      const int pc = p < pieces ? p : pieces - 1;
+      const int m = pc / (cbn * 16), c8 = pc % (cbn * 16);
+      uint8_t *dst = p < pieces ? xs + m * L.xstride + c8 * 16 : dummy;
+      const h8_t v = perm_to_magic(xv[i]);
+      *reinterpret_cast<h8_t *>(dst) = v;
+      // per-(row, block) sum: the 16 pieces of a block sit in 16 consecutive lanes
+      float part = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part += static_cast<float>(v[e]);
+      part += __shfl_xor(part, 1, 64);
+      part += __shfl_xor(part, 2, 64);
+      part += __shfl_xor(part, 4, 64);
+      part += __shfl_xor(part, 8, 64);
+      float *sdst = (p < pieces && (c8 & 15) == 0) ? xsum + m * cb + (c8 >> 4) : reinterpret_cast<float *>(dummy);
+      *sdst = part;
+    }
+#pragma unroll
+    for (int i = 0; i < SMAX; ++i) {
+      const int p = tid + i * NT;
+      const int pc = p < spieces ? p : spieces - 1;
+      const int r = pc / ppr, c = pc % ppr;
+      const uint32_t s4[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+      const uint32_t z4[4] = {zv[i].x, zv[i].y, zv[i].z, zv[i].w};
+#pragma unroll
+      for (int e = 0; e < GPP / 2; ++e) {
+        const int j = c * GPP + 2 * e;
+        const bool ok = p < spieces && j < cbn;
+        uint32_t *d = ok ? szl + r * cb + j : reinterpret_cast<uint32_t *>(dummy);
+        d[0] = (s4[e] & 0xFFFFu) | (z4[e] << 16);
+        d = (ok && j + 1 < cbn) ? d + 1 : reinterpret_cast<uint32_t *>(dummy);
+        d[0] = (s4[e] >> 16) | (z4[e] & 0xFFFF0000u);
+      }
     }
     mp_lds_barrier();
 
-    for (int r0 = 0; r0 < nmine; r0 += 2 * U) {
-      if (r0 + U < nmine) issue(wb, sb, zb, r0 + U);
-      compute(wa, sa, za, r0);
-      if (r0 + U >= nmine) break;
-      if (r0 + 2 * U < nmine) issue(wa, sa, za, r0 + 2 * U);
-      compute(wb, sb, zb, r0 + U);
+    const int ngrp = (nmine + U - 1) / U;
+    for (int g = 0; g < ngrp; g += 2) {
+      if (g + 1 < ngrp) issue(wb, (g + 1) * U);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wa, g * U);
+      if (g + 1 >= ngrp) break;
+      if (g + 2 < ngrp) issue(wa, (g + 2) * U);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wb, (g + 1) * U);
     }
   }
 
+  if (S == 1) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = t * 16 + 4 * kq + i;
+        if (m < m_rows && n < n_cols) {
+          float v = acc[t][i];
+          if (bias) v += mp_h2f(bias[n]);
+          y[static_cast<int64_t>(m) * n_cols + n] = mp_f2h(v);
+        }
+      }
+    return;
+  }
   mp_lds_barrier();
   float *red = reinterpret_cast<float *>(smem);  // [NW][MT][4][64]
 #pragma unroll
@@ -316,14 +434,15 @@ __global__ __launch_bounds__(NW * 64) void w4a16_skinny_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[((wave * MT + t) * 4 + i) * 64 + lane] = acc[t][i];
   mp_lds_barrier();
-  for (int o = tid; o < MT * 256; o += NW * 64) {
-    const int t = o >> 8, r = o & 255;
+  for (int o = tid; o < T * MT * 256; o += NT) {
+    const int tl = o / (MT * 256), rem = o % (MT * 256);
+    const int t = rem >> 8, r = rem & 255;
     const int l = r & 63, i = r >> 6;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) v += red[((w * MT + t) * 4 + i) * 64 + l];
+    for (int w = 0; w < S; ++w) v += red[(((tl * S + w) * MT + t) * 4 + i) * 64 + l];
     const int m = t * 16 + 4 * (l >> 4) + i;
-    const int col = blockIdx.x * 16 + (l & 15);
+    const int col = wg_col0 + tl * 16 + (l & 15);
     if (m < m_rows && col < n_cols) {
       if (bias) v += mp_h2f(bias[col]);
       y[static_cast<int64_t>(m) * n_cols + col] = mp_f2h(v);
@@ -567,27 +686,62 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
   const auto *zp = static_cast<const uint16_t *>(zeros);
   const auto *bp = static_cast<const uint16_t *>(bias);
   auto *yp = static_cast<uint16_t *>(y);
-  const bool aligned = mp_aligned(x, 16) && mp_aligned(w_packed, 16);
-  if (m <= 64 && k % 128 == 0 && group_size % 128 == 0 && aligned) {
+  const bool aligned = mp_aligned(x, 16) && mp_aligned(w_packed, 16) && mp_aligned(scales, 4) &&
+                       (zeros == nullptr || mp_aligned(zeros, 4));
+  const int n_groups_i = n_groups;
+  if (m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
     const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
-    const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-    const int nw = mt == 4 ? 4 : 8;
     const int nblk = ki / 128;
-    int cb = (kMpXLdsBudget / mi - 16) / 260;
-    cb = cb < 1 ? 1 : (cb > nblk ? nblk : cb);
-    size_t smem = static_cast<size_t>(mi) * (cb * 256 + 16) + static_cast<size_t>(mi) * cb * 4;
-    const size_t red = static_cast<size_t>(nw) * mt * 1024;
-    smem = smem > red ? smem : red;
-    const dim3 grid(static_cast<unsigned>(mp_cdiv(n, 16)));
-    if (mt == 1)
-      hipLaunchKernelGGL((w4a16_skinny_kernel<1, 8>), grid, dim3(512), smem, s, xp, mi, ki, wp, ni, sp, zp,
-                         n_groups, group_size, bp, yp, cb);
-    else if (mt == 2)
-      hipLaunchKernelGGL((w4a16_skinny_kernel<2, 8>), grid, dim3(512), smem, s, xp, mi, ki, wp, ni, sp, zp,
-                         n_groups, group_size, bp, yp, cb);
-    else
-      hipLaunchKernelGGL((w4a16_skinny_kernel<4, 4>), grid, dim3(256), smem, s, xp, mi, ki, wp, ni, sp, zp,
-                         n_groups, group_size, bp, yp, cb);
+    const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    const int cb_x = kDecXPieces * 512 / (16 * mi);  // blocks whose activations fit the staging registers
+    const bool sz16 = (n_groups_i % 8) == 0 && cb_x >= 8 && mp_aligned(scales, 16) &&
+                      (zeros == nullptr || mp_aligned(zeros, 16));
+    const int gpp = sz16 ? 8 : 2;
+    // waves sharing a 16-column tile: aim for ~2048 streaming waves, >= 4 blocks each
+    const int64_t tiles = mp_cdiv(n, 16);
+    int split = 1;
+    while (split < 8 && tiles * split < 2048 && nblk / (split * 2) >= 4) split *= 2;
+    const int t_per_wg = 8 / split;
+    // chunk: as many blocks as fit the LDS budget, a multiple of the scale piece
+    const int per_block = mi * 260 + t_per_wg * 16 * 4;
+    int cb = (kMpXLdsBudget - 64) / per_block;
+    const int cb_s = kDecSPieces * 512 * gpp / (t_per_wg * 16);            // scale pieces per thread
+    cb = cb < cb_x ? cb : cb_x;
+    cb = cb < cb_s ? cb : cb_s;
+    cb = cb / gpp * gpp;
+    cb = cb < gpp ? gpp : cb;
+    cb = cb > nblk ? nblk : cb;
+    const size_t smem_x = static_cast<size_t>(DecodeLds(mi, cb, t_per_wg).bytes);
+    const size_t red = split > 1 ? static_cast<size_t>(8) * mt * 1024 : 0;
+    const size_t smem = smem_x > red ? smem_x : red;
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(tiles, t_per_wg)));
+#define MP_W4_DEC(MT_, S_, SZ_)                                                                             \
+  do {                                                                                                      \
+    if (zp)                                                                                                 \
+      hipLaunchKernelGGL((w4a16_decode_kernel<MT_, S_, true, SZ_>), grid, dim3(512), smem, s, xp, mi, ki, wp, \
+                         ni, sp, zp, n_groups_i, bp, yp, cb);                                               \
+    else                                                                                                    \
+      hipLaunchKernelGGL((w4a16_decode_kernel<MT_, S_, false, SZ_>), grid, dim3(512), smem, s, xp, mi, ki, wp, \
+                         ni, sp, zp, n_groups_i, bp, yp, cb);                                               \
+  } while (0)
+#define MP_W4_DEC_S(MT_, SZ_)                 \
+  do {                                        \
+    if (split == 1) MP_W4_DEC(MT_, 1, SZ_);      \
+    else if (split == 2) MP_W4_DEC(MT_, 2, SZ_); \
+    else if (split == 4) MP_W4_DEC(MT_, 4, SZ_); \
+    else MP_W4_DEC(MT_, 8, SZ_);                 \
+  } while (0)
+    if (sz16) {
+      if (mt == 1) MP_W4_DEC_S(1, true);
+      else if (mt == 2) MP_W4_DEC_S(2, true);
+      else MP_W4_DEC_S(4, true);
+    } else {
+      if (mt == 1) MP_W4_DEC_S(1, false);
+      else if (mt == 2) MP_W4_DEC_S(2, false);
+      else MP_W4_DEC_S(4, false);
+    }
+#undef MP_W4_DEC_S
+#undef MP_W4_DEC
   } else if (m > 64 && k % kPBK == 0 && group_size % 32 == 0 && aligned) {
     const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, kPBM)));
     hipLaunchKernelGGL(w4a16_prefill_kernel, grid, dim3(256), 0, s, xp, static_cast<int>(m),

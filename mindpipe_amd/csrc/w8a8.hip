@@ -70,12 +70,15 @@ __global__ __launch_bounds__(256) void rowquant_kernel(const void *__restrict__ 
 // loads are double-buffered, U blocks per buffer.
 template <int MT, int NW>
 __global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb) {
+  // Straight-line hot path (clamped loads, masked surplus blocks): control-flow
+  // joins make the compiler wait for every outstanding load.
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int U = 4;
+  constexpr int NT = NW * 64;
   const int xstride = cb * 64 + 16;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_cols = static_cast<int>(p.n);
   const int k = static_cast<int>(p.k);
   const int m_rows = static_cast<int>(p.rows);
@@ -83,6 +86,8 @@ __global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb
   const int nn = n < n_cols ? n : n_cols - 1;
   const int kq = lane >> 4;
   const int nblk = k >> 6;
+  const int mlast = m_rows - 1;
+  uint8_t *dummy = smem + m_rows * xstride;
   const int8_t *wrow = p.b + static_cast<int64_t>(nn) * k + 16 * kq;
   i4_t acc[MT];
 #pragma unroll
@@ -92,44 +97,66 @@ __global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb
   for (int c0 = 0; c0 < nblk; c0 += cb) {
     const int cbn = (nblk - c0) < cb ? (nblk - c0) : cb;
     const int nmine = cbn > wave ? (cbn - wave + NW - 1) / NW : 0;
+    const int rmax = nmine > 0 ? nmine - 1 : 0;
+    const int bmax = c0 + cbn - 1;
     auto issue = [&](i4_t *w, int r0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        int r = r0 + u;
-        r = r < nmine ? r : nmine - 1;
-        w[u] = *reinterpret_cast<const i4_t *>(wrow + (c0 + wave + NW * r) * 64);
+        const int r = (r0 + u) < rmax ? (r0 + u) : rmax;
+        int b = c0 + wave + NW * r;
+        b = b < bmax ? b : bmax;
+        w[u] = *reinterpret_cast<const i4_t *>(wrow + b * 64);
       }
     };
     auto compute = [&](const i4_t *w, int r0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int r = r0 + u;
-        if (r >= nmine) break;
-        const int jl = wave + NW * r;
+        const bool live = r < nmine;
+        int jl = wave + NW * (r < rmax ? r : rmax);
+        jl = jl < cbn - 1 ? jl : cbn - 1;
+        const i4_t wv = live ? w[u] : i4_t{0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           const int ma = t * 16 + (lane & 15);
-          i4_t a = i4_t{0, 0, 0, 0};
-          if (ma < m_rows) a = *reinterpret_cast<const i4_t *>(smem + ma * xstride + jl * 64 + 16 * kq);
-          acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w[u], acc[t], 0, 0, 0);
+          const int mac = ma < mlast ? ma : mlast;
+          i4_t a = *reinterpret_cast<const i4_t *>(smem + mac * xstride + jl * 64 + 16 * kq);
+          a = ma < m_rows ? a : i4_t{0, 0, 0, 0};
+          acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wv, acc[t], 0, 0, 0);
         }
       }
     };
-    if (nmine > 0) issue(wa, 0);
-    if (c0 > 0) mp_lds_barrier();
+    constexpr int PMAX = kMpXLdsBudget / 16 / NT + 1;
     const int pieces = m_rows * cbn * 4;
-    for (int q = tid; q < pieces; q += NW * 64) {
+    i4_t xv[PMAX];
+#pragma unroll
+    for (int i = 0; i < PMAX; ++i) {
+      int q = tid + i * NT;
+      q = q < pieces ? q : pieces - 1;
       const int m = q / (cbn * 4), c16 = q % (cbn * 4);
-      *reinterpret_cast<i4_t *>(smem + m * xstride + c16 * 16) =
-          *reinterpret_cast<const i4_t *>(p.a + static_cast<int64_t>(m) * k + c0 * 64 + c16 * 16);
+      xv[i] = *reinterpret_cast<const i4_t *>(p.a + static_cast<int64_t>(m) * k + c0 * 64 + c16 * 16);
+    }
+    issue(wa, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (c0 > 0) mp_lds_barrier();
+#pragma unroll
+    for (int i = 0; i < PMAX; ++i) {
+      const int q = tid + i * NT;
+      const int qc = q < pieces ? q : pieces - 1;
+      const int m = qc / (cbn * 4), c16 = qc % (cbn * 4);
+      uint8_t *dst = q < pieces ? smem + m * xstride + c16 * 16 : dummy;
+      *reinterpret_cast<i4_t *>(dst) = xv[i];
     }
     mp_lds_barrier();
-    for (int r0 = 0; r0 < nmine; r0 += 2 * U) {
-      if (r0 + U < nmine) issue(wb, r0 + U);
-      compute(wa, r0);
-      if (r0 + U >= nmine) break;
-      if (r0 + 2 * U < nmine) issue(wa, r0 + 2 * U);
-      compute(wb, r0 + U);
+    const int ngrp = (nmine + U - 1) / U;
+    for (int g = 0; g < ngrp; g += 2) {
+      if (g + 1 < ngrp) issue(wb, (g + 1) * U);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wa, g * U);
+      if (g + 1 >= ngrp) break;
+      if (g + 2 < ngrp) issue(wa, (g + 2) * U);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wb, (g + 1) * U);
     }
   }
   mp_lds_barrier();
@@ -139,7 +166,7 @@ __global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[((wave * MT + t) * 4 + i) * 64 + lane] = acc[t][i];
   mp_lds_barrier();
-  for (int o = tid; o < MT * 256; o += NW * 64) {
+  for (int o = tid; o < MT * 256; o += NT) {
     const int t = o >> 8, r = o & 255;
     const int l = r & 63, i = r >> 6;
     int v = 0;
@@ -392,7 +419,7 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
     const int nblk = static_cast<int>(a.k / 64);
     int cb = (kMpXLdsBudget / mi - 16) / 64;
     cb = cb < 1 ? 1 : (cb > nblk ? nblk : cb);
-    size_t smem = static_cast<size_t>(mi) * (cb * 64 + 16);
+    size_t smem = static_cast<size_t>(mi) * (cb * 64 + 16) + 16;
     const size_t red = static_cast<size_t>(nw) * mt * 1024;
     smem = smem > red ? smem : red;
     const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, 16)));
