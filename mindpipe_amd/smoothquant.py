@@ -1,0 +1,323 @@
+"""SmoothQuant W8A8 modules with the reference's API, backed by the gfx950 kernels.
+
+Mirrors ``algorithm/quantization/ptq/smoothquant/source/smoothquant/fake_quant.py``
+(``quantize_weight_per_channel_absmax`` :10-19, ``quantize_activation_per_token_absmax``
+:22-31, ``SmoothQuantLinear`` :38-121, ``SmoothQuantPackedMoeExperts`` :124-198,
+``quantize_llama_like`` / ``quantize_model`` :201-457) and the smoothing helpers of
+``smooth.py:7-25,91-101``.  Same constructor arguments, attribute names and
+``forward`` signatures; the difference is that the weights are held as real int8
+codes with per-row scales and ``forward`` runs the per-token int8 quantizer and the
+int8 MFMA GEMM (or the MoE chain) instead of fake-quant ``F.linear``.
+
+Scale rule (``scale_rule``):
+  * ``"fake"`` (default for the modules): the fp16 arithmetic of the reference's
+    ``quantize_*_absmax`` -- the int8 codes are bit-identical to the codes the
+    reference's fake quantizer rounds to, and outputs match its ``F.linear`` on the
+    fake-quant tensors to fp16 rounding.
+  * ``"export"``: the fp32 rule of the Ascend W8A8 export / runtime
+    (``npu_dynamic_quant`` contract), the one ``runtime.W8A8DynamicLinearMethod`` uses.
+"""
+from __future__ import annotations
+
+from functools import partial
+from typing import List, Optional
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import ops
+
+__all__ = [
+    "quantize_weight_per_channel_absmax",
+    "quantize_activation_per_token_absmax",
+    "SmoothQuantLinear",
+    "SmoothQuantPackedMoeExperts",
+    "quantize_llama_like",
+    "quantize_model",
+    "compute_smooth_scales",
+    "smooth_ln_fcs_llama_like",
+]
+
+
+def _require_gpu(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{what}: mindpipe_amd runs on the GPU only (tensor is on {t.device})")
+
+
+@torch.no_grad()
+def quantize_weight_per_channel_absmax(weight: torch.Tensor, n_bits: int = 8) -> torch.Tensor:
+    """Fake-quantized weight (``q * s`` in fp16), as ``fake_quant.py:10-19`` returns it.
+
+    The codes come from the GPU quantizer (fp16 rule); the returned tensor holds the
+    same values as the reference's (the sign of an exact zero is not carried by int8
+    codes).  ``n_bits >= 16`` returns a copy, like the reference.
+    """
+    if int(n_bits) >= 16:
+        return weight.detach().clone()
+    if int(n_bits) != 8:
+        raise NotImplementedError("mindpipe_amd quantizes weights to 8 bits per channel")
+    _require_gpu(weight, "quantize_weight_per_channel_absmax")
+    shape = weight.shape
+    w2 = weight.detach().reshape(-1, shape[-1]).contiguous()
+    if w2.dtype != torch.float16:
+        raise NotImplementedError("the fp16 fake-quant rule takes fp16 weights")
+    q, s32, _ = ops.w8_quantize_per_channel(w2, "fake")
+    return (q.float() * s32[:, None]).to(weight.dtype).reshape(shape)
+
+
+@torch.no_grad()
+def quantize_activation_per_token_absmax(tensor: torch.Tensor, n_bits: int = 8) -> torch.Tensor:
+    """Fake-quantized activation (``q * s`` in fp16), as ``fake_quant.py:22-31`` returns it."""
+    if int(n_bits) >= 16:
+        return tensor
+    if int(n_bits) != 8:
+        raise NotImplementedError("mindpipe_amd quantizes activations to 8 bits per token")
+    _require_gpu(tensor, "quantize_activation_per_token_absmax")
+    q, s = ops.quant_per_token_i8(tensor.contiguous(), True)
+    return (q.float() * s.float().unsqueeze(-1)).to(tensor.dtype)
+
+
+class SmoothQuantLinear(nn.Module):
+    """W8A8 linear: int8 ``weight [N,K]`` + fp32 ``weight_scale [N]``, per-token int8 activations.
+
+    Constructor and ``from_float`` follow ``fake_quant.py:38-113``.  ``forward`` =
+    per-token int8 quant of ``x`` -> int8 MFMA GEMM with the ``(acc * s_tok) * s_ch
+    (+ bias)`` epilogue -> optional output fake-quant (``quantize_output``, :77-82).
+    """
+
+    def __init__(self, in_features, out_features, bias=True, weight_bits=8, activation_bits=8,
+                 act_quant="per_token", quantize_output=False, dtype=torch.float16, scale_rule="fake"):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.weight_bits = int(weight_bits)
+        self.activation_bits = int(activation_bits)
+        if act_quant != "per_token":
+            raise ValueError(f"Invalid act_quant: {act_quant}")
+        if self.weight_bits < 16 and self.weight_bits != 8:
+            raise NotImplementedError("weight_bits must be 8 (or >= 16 for no quantization)")
+        if self.activation_bits < 16 and self.activation_bits != 8:
+            raise NotImplementedError("activation_bits must be 8 (or >= 16 for no quantization)")
+        if scale_rule not in ("fake", "export"):
+            raise ValueError(f"Invalid scale_rule: {scale_rule}")
+        self.scale_rule = scale_rule
+        self.dtype = dtype
+        wdt = torch.int8 if self.weight_bits < 16 else dtype
+        self.register_buffer("weight", torch.zeros((out_features, in_features), dtype=wdt, requires_grad=False))
+        self.register_buffer("weight_scale", torch.ones((out_features,), dtype=torch.float32))
+        if bias:
+            self.register_buffer("bias", torch.zeros((out_features,), dtype=dtype, requires_grad=False))
+        else:
+            self.register_buffer("bias", None)
+        self.weight_quant_name = "per_channel" if self.weight_bits < 16 else "none"
+        self.act_quant_name = act_quant if self.activation_bits < 16 else "none"
+        self.output_quant_name = self.act_quant_name if quantize_output else "none"
+        self.act_quant = (partial(quantize_activation_per_token_absmax, n_bits=self.activation_bits)
+                          if self.activation_bits < 16 else (lambda t: t))
+
+    @property
+    def quantize_output(self) -> bool:
+        return self.output_quant_name != "none"
+
+    def output_quant(self, y):
+        if self.output_quant_name == "none":
+            return y
+        return quantize_activation_per_token_absmax(y, self.activation_bits)
+
+    def dequantized_weight(self) -> torch.Tensor:
+        """The fake-quant weight the reference module would hold (``q * s``)."""
+        if self.weight_bits >= 16:
+            return self.weight
+        return (self.weight.float() * self.weight_scale[:, None]).to(self.dtype)
+
+    @torch.no_grad()
+    def forward(self, x):
+        _require_gpu(x, "SmoothQuantLinear")
+        if self.weight_bits >= 16:
+            return self.output_quant(F.linear(self.act_quant(x), self.weight, self.bias))
+        if self.activation_bits >= 16:
+            raise NotImplementedError("W8A16 is not a path of this build (weights int8 need int8 activations)")
+        fp16_rule = self.scale_rule == "fake"
+        if fp16_rule and x.dtype != torch.float16:
+            raise NotImplementedError("the fp16 scale rule takes fp16 activations")
+        q, s = ops.quant_per_token_i8(x.contiguous(), fp16_rule)
+        y = ops.w8a8_gemm(q, s.float().contiguous(), self.weight, self.weight_scale, self.bias, x.dtype)
+        return self.output_quant(y)
+
+    @staticmethod
+    def from_float(module, weight_bits=8, activation_bits=8, act_quant="per_token", quantize_output=False,
+                   scale_rule="fake"):
+        assert isinstance(module, nn.Linear)
+        new = SmoothQuantLinear(module.in_features, module.out_features, module.bias is not None,
+                                weight_bits=weight_bits, activation_bits=activation_bits, act_quant=act_quant,
+                                quantize_output=quantize_output, dtype=module.weight.dtype,
+                                scale_rule=scale_rule)
+        new = new.to(device=module.weight.device)
+        if new.weight_bits < 16:
+            _require_gpu(module.weight, "SmoothQuantLinear.from_float")
+            q, s32, _ = ops.w8_quantize_per_channel(module.weight.detach().contiguous(), scale_rule)
+            new.weight = q
+            new.weight_scale = s32
+        else:
+            new.weight = module.weight.detach().clone()
+        if module.bias is not None:
+            new.bias = module.bias.detach().clone()
+        return new
+
+    def __repr__(self):
+        return (f"SmoothQuantLinear({self.in_features}, {self.out_features}, "
+                f"bias={self.bias is not None}, weight_bits={self.weight_bits}, "
+                f"activation_bits={self.activation_bits}, weight_quant={self.weight_quant_name}, "
+                f"act_quant={self.act_quant_name}, output_quant={self.output_quant_name})")
+
+
+def _is_silu(act_fn) -> bool:
+    if isinstance(act_fn, nn.SiLU) or act_fn is F.silu:
+        return True
+    return type(act_fn).__name__ in ("SiLUActivation", "SiLU")
+
+
+class SmoothQuantPackedMoeExperts(nn.Module):
+    """Packed W8A8 experts: ``gate_up_proj`` int8 ``[E,2I,H]``, ``down_proj`` int8 ``[E,H,I]``
+    with per-row fp32 scales; ``forward(hidden_states, top_k_index, top_k_weights)`` as
+    ``fake_quant.py:166-191``.  The chain runs as routing+quant -> grouped GEMM1 +
+    SwiGLU + requant -> grouped GEMM2 -> weighted un-permute (the runtime contract of
+    ``vllm_ascend.patch:2356-2423``); ``act_fn`` must be SiLU (the fused SwiGLU)."""
+
+    def __init__(self, gate_up_proj, down_proj, act_fn, *, weight_bits=8, activation_bits=8, scale_rule="export"):
+        super().__init__()
+        self.num_experts = int(gate_up_proj.shape[0])
+        self.hidden_dim = int(gate_up_proj.shape[2])
+        self.intermediate_dim = int(down_proj.shape[2])
+        self.weight_bits = int(weight_bits)
+        self.activation_bits = int(activation_bits)
+        if self.weight_bits != 8 or self.activation_bits != 8:
+            raise NotImplementedError("the packed MoE path is W8A8")
+        if not _is_silu(act_fn):
+            raise NotImplementedError(f"the fused expert kernel computes SiLU(gate) * up; got {act_fn!r}")
+        self.act_fn = act_fn
+        _require_gpu(gate_up_proj, "SmoothQuantPackedMoeExperts")
+        e, two_i, h = gate_up_proj.shape
+        q13, s13 = self._quant3d(gate_up_proj, scale_rule)
+        q2, s2 = self._quant3d(down_proj, scale_rule)
+        self.register_buffer("gate_up_proj", q13)
+        self.register_buffer("gate_up_scale", s13)
+        self.register_buffer("down_proj", q2)
+        self.register_buffer("down_scale", s2)
+        self.dtype = gate_up_proj.dtype
+
+    @staticmethod
+    def _quant3d(w, rule):
+        e, n, k = w.shape
+        q, s32, _ = ops.w8_quantize_per_channel(w.detach().reshape(e * n, k).contiguous(), rule)
+        return q.reshape(e, n, k), s32.reshape(e, n)
+
+    @staticmethod
+    def from_float(module, weight_bits=8, activation_bits=8, scale_rule="export"):
+        return SmoothQuantPackedMoeExperts(module.gate_up_proj.detach(), module.down_proj.detach(), module.act_fn,
+                                           weight_bits=weight_bits, activation_bits=activation_bits,
+                                           scale_rule=scale_rule)
+
+    @torch.no_grad()
+    def forward(self, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
+                top_k_weights: torch.Tensor) -> torch.Tensor:
+        _require_gpu(hidden_states, "SmoothQuantPackedMoeExperts")
+        return ops.moe_w8a8_forward(hidden_states.contiguous(), top_k_index, top_k_weights, self.gate_up_proj,
+                                    self.gate_up_scale, self.down_proj, self.down_scale,
+                                    out_dtype=hidden_states.dtype)
+
+    def __repr__(self):
+        return (f"SmoothQuantPackedMoeExperts(num_experts={self.num_experts}, "
+                f"hidden_dim={self.hidden_dim}, intermediate_dim={self.intermediate_dim}, "
+                f"weight_bits={self.weight_bits}, activation_bits={self.activation_bits})")
+
+
+_SUPPORTED = {"llama", "qwen2", "qwen3", "qwen3_moe", "mixtral", "mistral", "minicpm"}
+
+
+def _text_layers(model):
+    inner = getattr(model, "model", model)
+    if hasattr(inner, "language_model"):
+        inner = inner.language_model
+    layers = getattr(inner, "layers", None)
+    if layers is None:
+        raise ValueError("model has no decoder layers (expected model.model.layers)")
+    prefix = "model" if hasattr(model, "model") else ""
+    return layers, prefix
+
+
+def _swap(parent, name, qualified, names, **kw):
+    setattr(parent, name, SmoothQuantLinear.from_float(getattr(parent, name), **kw))
+    names.append(qualified)
+
+
+def quantize_llama_like(model, weight_bits=8, activation_bits=8, act_quant="per_token", quantize_bmm_input=True,
+                        scale_rule="fake") -> List[str]:
+    """Module-swap router (``fake_quant.py:226-438``): q/k/v (with output quant when
+    ``quantize_bmm_input``), o, gate/up/down; packed experts become
+    ``SmoothQuantPackedMoeExperts``.  Returns the qualified names, in the reference's order."""
+    model_type = getattr(getattr(model, "config", None), "model_type", None)
+    if model_type not in _SUPPORTED:
+        raise ValueError(f"Unsupported model type: {model_type!r}")
+    layers, prefix = _text_layers(model)
+    names: List[str] = []
+    kw = dict(weight_bits=weight_bits, activation_bits=activation_bits, act_quant=act_quant,
+              scale_rule=scale_rule)
+    for li, layer in enumerate(layers):
+        lp = f"{prefix}.layers.{li}" if prefix else f"layers.{li}"
+        attn = layer.self_attn
+        for p in ("q_proj", "k_proj", "v_proj"):
+            _swap(attn, p, f"{lp}.self_attn.{p}", names, quantize_output=quantize_bmm_input, **kw)
+        _swap(attn, "o_proj", f"{lp}.self_attn.o_proj", names, **kw)
+        mlp = getattr(layer, "mlp", None) or getattr(layer, "block_sparse_moe", None)
+        experts = getattr(mlp, "experts", None)
+        if experts is not None:
+            mlp_name = "mlp" if hasattr(layer, "mlp") else "block_sparse_moe"
+            if isinstance(experts, nn.ModuleList):
+                for ei, ex in enumerate(experts):
+                    for p in ("gate_proj", "up_proj", "down_proj"):
+                        _swap(ex, p, f"{lp}.{mlp_name}.experts.{ei}.{p}", names, **kw)
+            else:
+                mlp.experts = SmoothQuantPackedMoeExperts.from_float(experts, weight_bits=weight_bits,
+                                                                     activation_bits=activation_bits)
+                names.append(f"{lp}.{mlp_name}.experts.gate_up_proj")
+                names.append(f"{lp}.{mlp_name}.experts.down_proj")
+        else:
+            for p in ("gate_proj", "up_proj", "down_proj"):
+                _swap(mlp, p, f"{lp}.mlp.{p}", names, **kw)
+    return names
+
+
+def quantize_model(model, weight_bits=8, activation_bits=8, weight_quant="per_channel", act_quant="per_token",
+                   quantize_bmm_input=True, scale_rule="fake") -> List[str]:
+    """``fake_quant.py:441-457``."""
+    if weight_quant != "per_channel":
+        raise ValueError(f"Invalid weight_quant: {weight_quant}")
+    return quantize_llama_like(model, weight_bits=weight_bits, activation_bits=activation_bits,
+                               act_quant=act_quant, quantize_bmm_input=quantize_bmm_input, scale_rule=scale_rule)
+
+
+@torch.no_grad()
+def compute_smooth_scales(fcs, act_scales: torch.Tensor, alpha: float = 0.5) -> torch.Tensor:
+    """``_compute_smooth_scales`` (``smooth.py:7-25``): ``(a^alpha / w^(1-alpha)).clamp(1e-5)``
+    in the weight dtype, ``w_j = max_n |W_nj|`` over every fc sharing the norm."""
+    if not isinstance(fcs, (list, tuple)):
+        fcs = [fcs]
+    dtype, device = fcs[0].weight.dtype, fcs[0].weight.device
+    a = act_scales.to(device=device, dtype=dtype)
+    wmax = torch.cat([fc.weight.abs().max(dim=0, keepdim=True)[0] for fc in fcs], dim=0)
+    wmax = wmax.max(dim=0)[0].clamp(min=1e-5)
+    return (a.pow(alpha) / wmax.pow(1 - alpha)).clamp(min=1e-5).to(device=device, dtype=dtype)
+
+
+@torch.no_grad()
+def smooth_ln_fcs_llama_like(ln, fcs, act_scales, alpha=0.5):
+    """``smooth.py:91-101``: ``ln.weight /= s``, every fc weight ``*= s`` (column-wise)."""
+    if not isinstance(fcs, (list, tuple)):
+        fcs = [fcs]
+    s = compute_smooth_scales(fcs, act_scales, alpha)
+    ln.weight.div_(s)
+    for fc in fcs:
+        fc.weight.mul_(s.view(1, -1))
+    return s

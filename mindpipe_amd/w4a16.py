@@ -1,0 +1,306 @@
+"""W4A16 group-quantized linear: AWQ / GPTQ quantizers, the vLLM compressed-tensors
+pack format and a real-int4 linear module, backed by the gfx950 kernels.
+
+Mirrors:
+  * ``pseudo_quantize_tensor`` / ``pseudo_quantize_model_weight``
+    (``algorithm/quantization/ptq/awq/source/awq/quantize/quantizer.py:63-130``);
+  * GPTQ's symmetric group quantizer in its round-to-nearest form
+    (``algorithm/quantization/ptq/gptq/source/quant.py:13-17,44-82``, signed export
+    ``gptq.py:157-161``) producing ``RealQuantLinearArtifact`` (``exporters/schema.py:10-20``);
+  * ``pack_int4_for_vllm`` / ``VllmPackedInt4Linear`` / the compression config
+    (``algorithm/quantization/exporters/vllm.py:57-190``), with a working ``forward``;
+  * the export dequant of ``scripts/repro/evaluate_real_quant_export_dequant.py:36-64``.
+"""
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Dict, Iterable, List, Optional
+
+import torch
+from torch import nn
+
+from . import ops
+
+__all__ = [
+    "pseudo_quantize_tensor",
+    "gptq_rtn_quantize",
+    "RealQuantLinearArtifact",
+    "pack_int4_for_vllm",
+    "unpack_int4",
+    "W4A16Linear",
+    "VllmPackedInt4Linear",
+    "build_compression_config",
+    "quantize_model_w4a16",
+    "export_vllm_w4a16",
+    "load_vllm_w4a16",
+]
+
+
+def _gpu(t: torch.Tensor) -> torch.Tensor:
+    if t.is_cuda:
+        return t
+    if not torch.cuda.is_available():
+        raise RuntimeError("mindpipe_amd runs on the GPU only; no GPU is visible")
+    return t.cuda()
+
+
+@dataclass
+class RealQuantLinearArtifact:
+    """Integer weight and qparams of one quantized Linear (``exporters/schema.py:10-20``)."""
+
+    name: str
+    bits: int
+    group_size: int
+    symmetric: bool
+    original_shape: tuple
+    int_weight: torch.Tensor
+    scale: torch.Tensor
+
+
+@torch.no_grad()
+def pseudo_quantize_tensor(w, n_bit=8, zero_point=True, q_group_size=-1, inplace=False, get_scale_zp=False):
+    """AWQ pseudo-quantization on the GPU, same signature and results as the reference.
+
+    Only ``n_bit=4`` is a kernel of this build.  Returns the fp16 dequantized weight
+    (bit-identical to the reference's), plus ``scales``/``zeros`` ``[N, K/g]`` when
+    ``get_scale_zp`` (zero_point only, as in the reference).
+    """
+    if n_bit != 4:
+        raise NotImplementedError("mindpipe_amd implements the 4-bit AWQ quantizer")
+    if get_scale_zp and not zero_point:
+        raise ValueError("get_scale_zp needs zero_point=True (the reference's symmetric branch has no zeros)")
+    src = _gpu(w.detach())
+    shape = src.shape
+    w2 = src.reshape(-1, shape[-1]).contiguous()
+    if w2.dtype != torch.float16:
+        raise NotImplementedError("the AWQ quantizer takes fp16 weights (fp16 arithmetic of the reference)")
+    packed, s, z, deq = ops.w4_quantize_awq(w2, q_group_size, zero_point, return_deq=True)
+    deq = deq.reshape(shape).to(w.device)
+    if inplace:
+        w.data.copy_(deq)
+        deq = w
+    if get_scale_zp:
+        return deq, s.to(w.device), z.to(w.device)
+    return deq
+
+
+@torch.no_grad()
+def gptq_rtn_quantize(name: str, weight: torch.Tensor, bits: int = 4, group_size: int = 128) -> RealQuantLinearArtifact:
+    """GPTQ symmetric group quantizer without Hessian error feedback (its RTN case):
+    ``int_weight`` int8 ``[N,K]`` in ``[-8,7]`` and fp16 ``scale`` ``[N, K/g]``."""
+    if bits != 4:
+        raise NotImplementedError("mindpipe_amd implements the 4-bit GPTQ export")
+    iw, _, scale = ops.w4_quantize_gptq_rtn(_gpu(weight.detach()).contiguous(), group_size)
+    return RealQuantLinearArtifact(name=name, bits=4, group_size=group_size, symmetric=True,
+                                   original_shape=tuple(int(d) for d in weight.shape), int_weight=iw,
+                                   scale=scale)
+
+
+def pack_int4_for_vllm(int_weight: torch.Tensor) -> torch.Tensor:
+    """``exporters/vllm.py:89-111`` on the GPU; returns the packed tensor on the input's device."""
+    if int_weight.ndim != 2:
+        raise ValueError(f"Expected 2D int_weight, got shape {tuple(int_weight.shape)}.")
+    packed = ops.pack_int4(_gpu(int_weight.to(torch.int8)).contiguous())
+    return packed.to(int_weight.device)
+
+
+def unpack_int4(packed: torch.Tensor, columns: int) -> torch.Tensor:
+    return ops.unpack_int4(_gpu(packed).contiguous(), columns).to(packed.device)
+
+
+class W4A16Linear(nn.Module):
+    """Real int4 linear: ``weight_packed`` int32 ``[N, K/8]``, ``weight_scale`` fp16 ``[N, K/g]``,
+    ``weight_zero_point`` fp16 ``[N, K/g]`` (AWQ asymmetric) or ``None`` (symmetric,
+    zero point 8), ``weight_shape`` int64 ``[2]``, ``bias``; ``forward`` runs the W4A16 kernel."""
+
+    def __init__(self, in_features: int, out_features: int, group_size: int = 128, bias: bool = True,
+                 zero_point: bool = True, dtype=torch.float16, device=None):
+        super().__init__()
+        if in_features % 8 or in_features % group_size:
+            raise ValueError("in_features must be a multiple of 8 and of group_size")
+        self.in_features, self.out_features, self.group_size = in_features, out_features, group_size
+        g = in_features // group_size
+        self.register_buffer("weight_packed", torch.zeros((out_features, in_features // 8), dtype=torch.int32, device=device))
+        self.register_buffer("weight_scale", torch.ones((out_features, g), dtype=torch.float16, device=device))
+        self.register_buffer("weight_zero_point", torch.full((out_features, g), 8.0, dtype=torch.float16, device=device)
+                             if zero_point else None)
+        self.register_buffer("weight_shape", torch.tensor([out_features, in_features], dtype=torch.int64))
+        self.register_buffer("bias", torch.zeros(out_features, dtype=dtype, device=device) if bias else None)
+
+    @classmethod
+    @torch.no_grad()
+    def from_float(cls, linear: nn.Linear, group_size: int = 128, zero_point: bool = True) -> "W4A16Linear":
+        w = _gpu(linear.weight.detach()).to(torch.float16).contiguous()
+        n, k = w.shape
+        mod = cls(k, n, group_size, linear.bias is not None, zero_point, device=w.device)
+        packed, s, z, _ = ops.w4_quantize_awq(w, group_size, zero_point, return_deq=False)
+        if s.shape[1] != k // group_size:
+            raise ValueError("group_size must divide in_features")
+        mod.weight_packed.copy_(packed)
+        mod.weight_scale.copy_(s)
+        if zero_point:
+            mod.weight_zero_point.copy_(z)
+        if linear.bias is not None:
+            mod.bias.copy_(linear.bias.detach().to(torch.float16))
+        return mod
+
+    @classmethod
+    def from_artifact(cls, art: RealQuantLinearArtifact, bias: Optional[torch.Tensor] = None) -> "W4A16Linear":
+        n, k = art.original_shape
+        mod = cls(k, n, art.group_size, bias is not None, zero_point=False,
+                  device=torch.device("cuda") if torch.cuda.is_available() else None)
+        mod.weight_packed.copy_(pack_int4_for_vllm(art.int_weight).to(mod.weight_packed.device))
+        mod.weight_scale.copy_(art.scale.to(torch.float16))
+        if bias is not None:
+            mod.bias.copy_(bias)
+        return mod
+
+    def dequantized_weight(self) -> torch.Tensor:
+        """``(u - z) * s`` in fp16 (the reference's pseudo-quantized weight for AWQ codes)."""
+        u = ops.unpack_int4(self.weight_packed, self.in_features).to(torch.int16) + 8
+        s = self.weight_scale.repeat_interleave(self.group_size, dim=1)
+        z = (self.weight_zero_point.repeat_interleave(self.group_size, dim=1) if self.weight_zero_point is not None
+             else torch.full_like(s, 8.0))
+        return ((u.half() - z) * s).half()
+
+    @torch.no_grad()
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not x.is_cuda:
+            raise RuntimeError("W4A16Linear runs on the GPU only")
+        return ops.w4a16_gemm(x.contiguous(), self.weight_packed, self.weight_scale, self.weight_zero_point,
+                              self.group_size, self.bias)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, group_size={self.group_size}, "
+                f"zero_point={self.weight_zero_point is not None}, bias={self.bias is not None}")
+
+
+class VllmPackedInt4Linear(W4A16Linear):
+    """The export module of ``exporters/vllm.py:57-86`` (same buffer names), with a forward."""
+
+    def __init__(self, *, packed_weight, scale, bias, in_features, out_features):
+        g = in_features // scale.shape[1]
+        super().__init__(in_features, out_features, g, bias is not None, zero_point=False,
+                         device=packed_weight.device)
+        self.weight_packed.copy_(packed_weight)
+        self.weight_scale.copy_(scale.to(torch.float16))
+        if bias is not None:
+            self.bias.copy_(bias)
+
+
+def build_compression_config(*, group_size: int, ignored_layers: List[str],
+                             quant_method: str = "compressed-tensors") -> dict:
+    """``_build_compression_config`` (``exporters/vllm.py:139-165``)."""
+    return {
+        "config_groups": {"group_0": {"targets": ["Linear"], "input_activations": None,
+                                      "weights": {"dynamic": False, "group_size": int(group_size), "num_bits": 4,
+                                                  "observer": "minmax", "observer_kwargs": {}, "strategy": "group",
+                                                  "symmetric": True, "type": "int"}}},
+        "format": "pack-quantized",
+        "ignore": list(ignored_layers),
+        "quant_method": quant_method,
+    }
+
+
+def _named_linears(model: nn.Module) -> Dict[str, nn.Linear]:
+    return {n: m for n, m in model.named_modules() if isinstance(m, nn.Linear)}
+
+
+def _set_module(model: nn.Module, name: str, new: nn.Module) -> None:
+    parent_name, _, child = name.rpartition(".")
+    parent = model.get_submodule(parent_name) if parent_name else model
+    setattr(parent, child, new)
+
+
+@torch.no_grad()
+def quantize_model_w4a16(model: nn.Module, group_size: int = 128, zero_point: bool = True,
+                         skip: Iterable[str] = ("lm_head",)) -> List[str]:
+    """Swap every ``nn.Linear`` (except names containing a ``skip`` entry) for a
+    ``W4A16Linear`` holding the AWQ codes ``pseudo_quantize_model_weight`` would round to
+    (``quantizer.py:108-130``); returns the swapped names."""
+    names = []
+    for name, lin in _named_linears(model).items():
+        if any(s in name for s in skip):
+            continue
+        _set_module(model, name, W4A16Linear.from_float(lin, group_size, zero_point))
+        names.append(name)
+    return names
+
+
+@torch.no_grad()
+def export_vllm_w4a16(model: nn.Module, artifacts: Dict[str, RealQuantLinearArtifact], export_dir,
+                      group_size: int) -> dict:
+    """Write a compressed-tensors ``pack-quantized`` checkpoint (``exporters/vllm.py:224-327``):
+    quantized linears become ``<name>.weight_packed / weight_scale / weight_shape (+ bias)``,
+    other tensors are kept; ``config.json`` gets the ``compression_config``."""
+    from safetensors.torch import save_file
+    out = Path(export_dir)
+    out.mkdir(parents=True, exist_ok=True)
+    tensors = {}
+    lin = _named_linears(model)
+    for k_, v in model.state_dict().items():
+        mod_name = k_.rsplit(".", 1)[0]
+        if mod_name in artifacts:
+            continue
+        tensors[k_] = v.detach().cpu().contiguous()
+    for name, art in artifacts.items():
+        if art.int_weight.shape[1] % art.group_size:
+            raise ValueError(f"{name}: in_features must be a multiple of group_size")
+        tensors[f"{name}.weight_packed"] = pack_int4_for_vllm(art.int_weight).cpu()
+        tensors[f"{name}.weight_scale"] = art.scale.detach().cpu().to(torch.float16).contiguous()
+        tensors[f"{name}.weight_shape"] = torch.tensor(list(art.original_shape), dtype=torch.int64)
+        b = getattr(lin.get(name), "bias", None)
+        if b is not None:
+            tensors[f"{name}.bias"] = b.detach().cpu().contiguous()
+    save_file(tensors, str(out / "model.safetensors"))
+    ignored = sorted(n for n in lin if n not in artifacts)
+    cfg_path = out / "config.json"
+    cfg = json.loads(cfg_path.read_text()) if cfg_path.exists() else {}
+    cfg.pop("quantization_config", None)
+    cfg["compression_config"] = build_compression_config(group_size=group_size, ignored_layers=ignored)
+    cfg_path.write_text(json.dumps(cfg, indent=2))
+    return {"backend": "vllm", "quantized_linear_count": len(artifacts), "ignored_layers": ignored,
+            "export_dir": str(out)}
+
+
+@torch.no_grad()
+def load_vllm_w4a16(model: nn.Module, export_dir) -> List[str]:
+    """Load a compressed-tensors ``pack-quantized`` export straight into ``W4A16Linear``
+    modules (no re-quantization); returns the replaced module names."""
+    from safetensors import safe_open
+    path = Path(export_dir)
+    cfg = json.loads((path / "config.json").read_text())["compression_config"]
+    if cfg.get("format") != "pack-quantized":
+        raise ValueError(f"unsupported compression format {cfg.get('format')!r}")
+    g = int(cfg["config_groups"]["group_0"]["weights"]["group_size"])
+    names = []
+    dev = torch.device("cuda")
+    with safe_open(str(path / "model.safetensors"), framework="pt", device="cpu") as f:
+        keys = set(f.keys())
+        for k_ in sorted(keys):
+            if not k_.endswith(".weight_packed"):
+                continue
+            name = k_[: -len(".weight_packed")]
+            n, kk = (int(v) for v in f.get_tensor(f"{name}.weight_shape").tolist())
+            bias = f.get_tensor(f"{name}.bias").to(dev) if f"{name}.bias" in keys else None
+            mod = VllmPackedInt4Linear(packed_weight=f.get_tensor(k_).to(dev),
+                                       scale=f.get_tensor(f"{name}.weight_scale").to(dev),
+                                       bias=bias, in_features=kk, out_features=n)
+            _set_module(model, name, mod)
+            names.append(name)
+        for k_ in keys:
+            if k_.rsplit(".", 1)[0] in names:
+                continue
+            try:
+                t = model.get_parameter(k_)
+            except AttributeError:
+                try:
+                    t = model.get_buffer(k_)
+                except AttributeError:
+                    continue
+            t.data.copy_(f.get_tensor(k_).to(t.device))
+    if g <= 0:
+        raise ValueError("bad group size in compression_config")
+    return names
