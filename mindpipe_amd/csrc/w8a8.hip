@@ -374,6 +374,159 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
   }
 }
 
+// ------------------------------------------------------------------ large-M dense GEMM
+// 256 x 256 output tile per workgroup of 8 waves (2 along M x 4 along N), each
+// wave 128 x 64 = 4 x 2 MFMA i32_32x32x32_i8 tiles (128 accumulator registers,
+// so two waves fit per SIMD).  BK = 64, LDS double buffer (row pitch 80 B:
+// conflict-free ds_read_b128 fragments) and two register stages: K tile kt+2
+// is in flight while tile kt is multiplied and tile kt+1 is written to the
+// other LDS buffer; the LDS-only barrier leaves those loads outstanding.
+// Tiles are assigned XCD-major: the workgroups the dispatcher places on one
+// XCD (id % 8) take a contiguous run of tiles, ordered in 4-row-tile bands, so
+// concurrent tiles share A and B rows in that XCD's L2.
+constexpr int kBigBM = 256, kBigBN = 256, kBigBK = 64, kBigLD = kBigBK + 16, kBigThreads = 512;
+
+__device__ __forceinline__ void big_tile_coords(int id, int tiles_m, int tiles_n, int &tm, int &tn) {
+  const int total = tiles_m * tiles_n;
+  const int per = total / 8, rem = total % 8;
+  const int xcd = id % 8, local = id / 8;
+  const int t = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int band = t / (4 * tiles_n);
+  const int inb = t % (4 * tiles_n);
+  const int rows_in_band = (tiles_m - band * 4) < 4 ? (tiles_m - band * 4) : 4;
+  tm = band * 4 + inb % rows_in_band;
+  tn = inb / rows_in_band;
+}
+
+template <int OUT_DT>
+__global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, int tiles_m, int tiles_n) {
+  constexpr int BM = kBigBM, BN = kBigBN, BK = kBigBK, LD = kBigLD, NT = kBigThreads;
+  constexpr int TM = 4, TN = 2;                // 32x32 tiles per wave
+  constexpr int CPR = BK / 16;                 // 16-byte chunks per tile row
+  constexpr int RPP = NT / CPR;                // tile rows covered per pass (128)
+  constexpr int CA = BM / RPP, CB = BN / RPP;  // passes (2 each)
+  extern __shared__ __attribute__((aligned(16))) int8_t smem_big[];
+  int8_t *sa = smem_big;                // [2][BM*LD]
+  int8_t *sb = smem_big + 2 * BM * LD;  // [2][BN*LD]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  int tm, tn;
+  big_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const int64_t k = p.k;
+
+  // pass i of this thread covers tile row (tid / CPR + i * RPP), bytes (tid % CPR) * 16
+  // of the K step; rows past the matrix are clamped (computed, never stored)
+  const int rloc = tid / CPR, cloc = (tid % CPR) * 16;
+  int aoff[CA], boff[CB];
+#pragma unroll
+  for (int i = 0; i < CA; ++i) {
+    int64_t r = m0 + rloc + i * RPP;
+    r = r < p.rows ? r : p.rows - 1;
+    aoff[i] = static_cast<int>(r - m0);
+  }
+#pragma unroll
+  for (int i = 0; i < CB; ++i) {
+    int64_t c = n0 + rloc + i * RPP;
+    c = c < p.n ? c : p.n - 1;
+    boff[i] = static_cast<int>(c - n0);
+  }
+  const int8_t *abase = p.a + m0 * k + cloc;
+  const int8_t *bbase = p.b + n0 * k + cloc;
+  i4_t ra[CA + CB], rb[CA + CB];
+  auto load_tile = [&](i4_t *r, int64_t kt) {
+    const int64_t off = kt * BK;
+#pragma unroll
+    for (int i = 0; i < CA; ++i) r[i] = *reinterpret_cast<const i4_t *>(abase + static_cast<int64_t>(aoff[i]) * k + off);
+#pragma unroll
+    for (int i = 0; i < CB; ++i) r[CA + i] = *reinterpret_cast<const i4_t *>(bbase + static_cast<int64_t>(boff[i]) * k + off);
+  };
+  auto store_tile = [&](const i4_t *r, int buf) {
+#pragma unroll
+    for (int i = 0; i < CA; ++i)
+      *reinterpret_cast<i4_t *>(&sa[buf * BM * LD + (rloc + i * RPP) * LD + cloc]) = r[i];
+#pragma unroll
+    for (int i = 0; i < CB; ++i)
+      *reinterpret_cast<i4_t *>(&sb[buf * BN * LD + (rloc + i * RPP) * LD + cloc]) = r[CA + i];
+  };
+
+  i16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  const int arow = (wm * 128 + (lane & 31)) * LD + 16 * (lane >> 5);
+  const int brow = (wn * 64 + (lane & 31)) * LD + 16 * (lane >> 5);
+  auto compute = [&](int buf) {
+    const int8_t *ca = sa + buf * BM * LD;
+    const int8_t *cbp = sb + buf * BN * LD;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      i4_t af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i4_t *>(ca + arow + i * 32 * LD + ks * 32);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const i4_t *>(cbp + brow + j * 32 * LD + ks * 32);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // one K32 step of fragments live at a time
+    }
+  };
+
+  // K is a multiple of 2 * BK (host check): the loop body is branch-free; the two
+  // prefetches past the last tile are clamped to it and never multiplied
+  const int64_t nkt = k / BK;
+  load_tile(ra, 0);
+  load_tile(rb, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  store_tile(ra, 0);
+  mp_lds_barrier();
+  for (int64_t kt = 0; kt < nkt; kt += 2) {
+    load_tile(ra, kt + 2 < nkt ? kt + 2 : nkt - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0);
+    store_tile(rb, 1);
+    mp_lds_barrier();
+    load_tile(rb, kt + 3 < nkt ? kt + 3 : nkt - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);
+    store_tile(ra, 0);
+    mp_lds_barrier();
+  }
+
+  // epilogue: (acc * s_tok) * s_ch (+ bias) -> OUT_DT; full tiles skip the row guard
+  const bool full_rows = m0 + BM <= p.rows;
+  const int64_t mbase = m0 + wm * 128 + 4 * (lane >> 5);
+  const bool has_bias = p.bias != nullptr;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+    const bool cval = col < p.n;
+    const int64_t colc = cval ? col : p.n - 1;
+    const float sbv = p.s_b[colc];
+    const float bv = has_bias ? mp_load_as_f32(p.bias, colc, p.bias_dtype) : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = mbase + i * 32 + 8 * (r >> 2) + (r & 3);
+        const int64_t mc = (full_rows || m < p.rows) ? m : p.rows - 1;
+        float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), p.s_a[mc]), sbv);
+        v = has_bias ? mp_add(v, bv) : v;
+        if (cval && (full_rows || m < p.rows)) {
+          if (OUT_DT == MP_F16) static_cast<uint16_t *>(p.y)[m * p.ldy + col] = mp_f2h(v);
+          else if (OUT_DT == MP_BF16) static_cast<uint16_t *>(p.y)[m * p.ldy + col] = mp_f2bf(v);
+          else static_cast<float *>(p.y)[m * p.ldy + col] = v;
+        }
+      }
+  }
+}
+
 // Any-shape dense fallback: one thread per output.
 __global__ void i8_simple_kernel(mp_i8_args p) {
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -429,6 +582,24 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
       hipLaunchKernelGGL((i8_skinny_kernel<2, 8>), grid, dim3(512), smem, stream, a, cb);
     else
       hipLaunchKernelGGL((i8_skinny_kernel<4, 4>), grid, dim3(256), smem, stream, a, cb);
+  } else if (a.rows >= 1024 && a.k % (2 * kBigBK) == 0 && aligned && epilogue == MP_EPI_DENSE) {
+    const int tiles_m = static_cast<int>(mp_cdiv(a.rows, kBigBM));
+    const int tiles_n = static_cast<int>(mp_cdiv(a.n, kBigBN));
+    const size_t smem = static_cast<size_t>(2) * (kBigBM + kBigBN) * kBigLD;
+    const void *fn = a.out_dtype == MP_F16    ? reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F16>)
+                     : a.out_dtype == MP_BF16 ? reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_BF16>)
+                                              : reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F32>);
+    // > 64 KB of dynamic LDS must be allowed per kernel (idempotent, cheap)
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) != hipSuccess)
+      return MP_ERR_HIP;
+    const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
+    const dim3 block(kBigThreads);
+    if (a.out_dtype == MP_F16)
+      hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F16>, grid, block, smem, stream, a, tiles_m, tiles_n);
+    else if (a.out_dtype == MP_BF16)
+      hipLaunchKernelGGL(i8_gemm_big_kernel<MP_BF16>, grid, block, smem, stream, a, tiles_m, tiles_n);
+    else
+      hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F32>, grid, block, smem, stream, a, tiles_m, tiles_n);
   } else if (a.k % kTBK == 0 && aligned) {
     const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));
     if (epilogue == MP_EPI_F32)

@@ -204,7 +204,7 @@ def test_w8_quantize_export_and_fake_rules():
 
 # ------------------------------------------------------------------ W8A8 GEMM
 W8_CASES = [(1, 11008, 4096), (16, 11008, 4096), (5, 1000, 256), (17, 512, 1024), (64, 384, 512), (65, 256, 512),
-            (256, 1000, 1024), (300, 384, 4096), (7, 100, 48)]
+            (256, 1000, 1024), (300, 384, 4096), (7, 100, 48), (1100, 300, 256), (2048, 520, 320)]
 
 
 @pytest.mark.parametrize("m,n,k", W8_CASES)
