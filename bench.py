@@ -73,6 +73,15 @@ def _time_launches(fn, n_launch, warmup, per_graph=None):
     return ms
 
 
+def _traffic(key):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/traffic.json)."""
+    try:
+        with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")) as f:
+            return json.load(f)[key]["bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def _roof(bound, achieved, peak, unit, traffic=None):
     return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
@@ -123,7 +132,8 @@ def leg_w8a8(ops, m, n, k, steps, warmup):
     out = {"m": m, "n": n, "k": k, "ms_gemm": ms, "ms_quant": ms_q, "ms_e2e": ms + ms_q, "tops": tops,
            "tops_e2e": ops_count / ((ms + ms_q) * 1e-3) / 1e12, "gb_s": gbs, "weight_copies": nc}
     if m >= 1024:
-        out["roofline"] = _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS")
+        out["roofline"] = _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS",
+                                _traffic(f"w8a8_gemm_m{m}_k{k}_n{n}"))
     elif m <= 16:
         out["roofline"] = _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s")
     else:
@@ -193,6 +203,33 @@ def cpu_baseline_w4a16(m=1, n=4096, k=4096, g=128, budget_s=12.0):
             "ms_per_call": per * 1e3}
 
 
+def traffic_probe(ops):
+    """Kernel mix for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: a plain 256 MiB
+    device copy (calibration of the counters) and the headline kernels."""
+    src = torch.empty(256 * 1024 * 1024 // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    del src, dst
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    w = (torch.randn(4096, 4096, generator=gen, device="cuda") * 0.02).half()
+    packed, s, z, _ = ops.w4_quantize_awq(w, 128, True, return_deq=False)
+    pk = [packed.clone() for _ in range(64)]
+    sc = [s.clone() for _ in range(64)]
+    zr = [z.clone() for _ in range(64)]
+    x = torch.randn(1, 4096, device="cuda").half()
+    for i in range(128):
+        ops.w4a16_gemm(x, pk[i % 64], sc[i % 64], zr[i % 64], 128, None)
+    qx = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device="cuda")
+    qw = torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device="cuda")
+    st = torch.rand(4096, device="cuda")
+    sw = torch.rand(11008, device="cuda")
+    for _ in range(3):
+        ops.w8a8_gemm(qx, st, qw, sw, None, torch.float16)
+    torch.cuda.synchronize()
+    print("traffic probe done")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,13 +237,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--legs", default="w4,w8,moe")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run the kernel mix profiled for HBM traffic (profiles/traffic.json) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the kernels would shard)", file=sys.stderr)
+              "(the kernels run on one GPU's shard; no collectives are built)", file=sys.stderr)
         sys.exit(2)
     from mindpipe_amd import ops
 
+    if args.traffic_probe:
+        traffic_probe(ops)
+        return
     legs = set(args.legs.split(","))
     steps, warmup = args.steps, args.warmup
     torch.cuda.init()
@@ -215,6 +257,7 @@ def main():
     out_legs = {}
     _log("leg w4a16 M=1")
     head, _ = leg_w4a16(ops, 1, 4096, 4096, steps, warmup)
+    head["roofline"]["traffic"] = _traffic("w4a16_gemv_m1_k4096_n4096")
     if "w4" in legs:
         _log("leg w4a16 M=16")
         out_legs["w4a16_m16_k4096_n4096"], _ = leg_w4a16(ops, 16, 4096, 4096, steps, warmup)
