@@ -174,6 +174,77 @@ def leg_moe(ops, steps, warmup, t=512, h=4096, inter=14336, e=8, top_k=2):
             "roofline_mfma": _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS")}
 
 
+def leg_decoder(cfg_name, batches, prompt, gen_tokens, prefill_batch=1):
+    """Llama-shaped W4A16 stack: prefill tok/s at B=prefill_batch and greedy decode tok/s
+    at each batch size.  For decode the KV cache holds a `prompt`-token context (random
+    values: decode cost does not depend on them); one step is captured in a HIP graph
+    that also feeds the argmax back as the next token, and is replayed gen_tokens times."""
+    from mindpipe_amd.decoder import DecoderConfig, W4Decoder
+    cfg = getattr(DecoderConfig, cfg_name)()
+    out = {"model": cfg_name, "prompt": prompt, "gen_tokens": gen_tokens, "decode": {}}
+    max_len = prompt + gen_tokens
+    kv_per_tok_layer = 2 * cfg.kv_heads * cfg.head_dim * 2
+    for b in batches:
+        model = W4Decoder(cfg, max_batch=b, max_len=max_len)
+        wbytes = model.weight_bytes()
+        if b == prefill_batch:
+            toks = torch.randint(0, cfg.vocab, (b, prompt), device="cuda",
+                                 generator=torch.Generator(device="cuda").manual_seed(4))
+            model.prefill(toks)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            model.prefill(toks)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1)
+            n_params = sum(l[n].n * l[n].k for l in model.layers for n in ("qkv", "o", "gate_up", "down"))
+            lin_flops = 2.0 * b * prompt * n_params
+            out["prefill"] = {"batch": b, "tokens": prompt, "ms": ms, "tok_s": b * prompt / (ms * 1e-3),
+                              "linear_tflops": lin_flops / (ms * 1e-3) / 1e12,
+                              "roofline": _roof("mfma", lin_flops / (ms * 1e-3) / 1e12, FP16_PEAK_TFLOPS, "TFLOP/s")}
+        g = torch.Generator(device="cuda").manual_seed(5)
+        model.k_cache.normal_(0, 1, generator=g)
+        model.v_cache.normal_(0, 1, generator=g)
+        tok = torch.randint(0, cfg.vocab, (b,), device="cuda", generator=g)
+        cur = torch.tensor([prompt], device="cuda", dtype=torch.int64)
+
+        def step():
+            nxt = model.decode_step(tok, cur)
+            tok.copy_(nxt)
+            cur.add_(1)
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        cur.fill_(prompt)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        cur.fill_(prompt)
+        graph.replay()
+        cur.fill_(prompt)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(gen_tokens):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / gen_tokens
+        avg_len = prompt + gen_tokens / 2
+        step_bytes = wbytes + b * max_len * cfg.layers * kv_per_tok_layer  # masked attention reads the full cache
+        alg_bytes = wbytes + b * avg_len * cfg.layers * kv_per_tok_layer
+        out["decode"][str(b)] = {"ms_per_step": ms, "tok_s": b / (ms * 1e-3), "weight_bytes": wbytes,
+                                 "kv_bytes_per_step_read": step_bytes - wbytes,
+                                 "roofline": _roof("hbm", alg_bytes / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s")}
+        del graph, model
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline_w4a16(m=1, n=4096, k=4096, g=128, budget_s=12.0):
     """Oracle restatement of the reference CPU path: AWQ pseudo-quantized fp16 weight, then
     F.linear (fp32 accumulate).  Timed per call on the host, bounded sample."""
@@ -235,7 +306,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--legs", default="w4,w8,moe")
+    ap.add_argument("--legs", default="w4,w8,moe,dec7b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the kernel mix profiled for HBM traffic (profiles/traffic.json) and exit")
@@ -272,6 +343,15 @@ def main():
     if "moe" in legs:
         _log("leg moe")
         out_legs["moe_w8a8_mixtral_t512"] = leg_moe(ops, max(5, steps // 20), max(2, warmup // 4))
+    dec = None
+    if "dec7b" in legs:
+        _log("leg llama-2-7b-shaped W4A16 decode")
+        dec = leg_decoder("llama2_7b", (1, 8, 32), prompt=2048, gen_tokens=256)
+        out_legs["llama2_7b_w4a16"] = dec
+    if "dec70b" in legs:
+        _log("leg llama-3-70b-shaped W4A16 decode")
+        out_legs["llama3_70b_w4a16"] = leg_decoder("llama3_70b", (1, 16, 64), prompt=4096, gen_tokens=64,
+                                                   prefill_batch=0)
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline")
@@ -295,6 +375,7 @@ def main():
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "int8_tops_m4096": round(w8["tops"], 2) if w8 else None,
+        "decode_7b_tok_s": {k: round(v["tok_s"], 1) for k, v in dec["decode"].items()} if dec else None,
         "legs": out_legs,
         "device": dev.name,
     }

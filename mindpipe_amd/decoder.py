@@ -1,0 +1,167 @@
+"""Llama-shaped decoder stack with every linear on the W4A16 kernels (measurement harness).
+
+Used to measure prefill and greedy-decode throughput on the shapes of the W4A16
+workloads: Llama-2-7B (32 layers, hidden 4096, 32 heads, FFN 11008, vocab 32000)
+and Llama-3-70B (80 layers, hidden 8192, 64 q / 8 kv heads, FFN 28672, vocab 128256).
+Weights are random W4 g128 codes with fp16 scales / zeros (a random init of the
+quantized model; no checkpoint is loaded).  q/k/v and gate/up are fused into one
+W4A16 GEMM each (row concatenation of the packed weight is exact).  Attention,
+RMSNorm, RoPE and SwiGLU use PyTorch ops; the KV cache has a fixed capacity and
+attention is masked by the current length, so one decode step is shape-static and
+can be captured into a HIP graph.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+
+
+@dataclass
+class DecoderConfig:
+    layers: int = 32
+    hidden: int = 4096
+    heads: int = 32
+    kv_heads: int = 32
+    ffn: int = 11008
+    vocab: int = 32000
+    group: int = 128
+    rope_theta: float = 10000.0
+    eps: float = 1e-5
+
+    @staticmethod
+    def llama2_7b():
+        return DecoderConfig()
+
+    @staticmethod
+    def llama3_70b():
+        return DecoderConfig(layers=80, hidden=8192, heads=64, kv_heads=8, ffn=28672, vocab=128256,
+                             rope_theta=500000.0)
+
+    @property
+    def head_dim(self):
+        return self.hidden // self.heads
+
+
+class _W4:
+    """Random W4 g128 linear held as packed codes + fp16 scales / zeros."""
+
+    def __init__(self, n, k, group, gen, device):
+        self.n, self.k, self.group = n, k, group
+        self.packed = torch.randint(-2**31, 2**31 - 1, (n, k // 8), generator=gen, device=device, dtype=torch.int32)
+        # dequantised values (u - z) * s with s ~ 0.0027: weights of std ~0.012 over [-0.02, 0.02]
+        self.scales = (torch.rand(n, k // group, generator=gen, device=device) * 0.001 + 0.0022).half()
+        self.zeros = torch.full((n, k // group), 8.0, device=device, dtype=torch.float16)
+
+    def __call__(self, x):
+        return ops.w4a16_gemm(x, self.packed, self.scales, self.zeros, self.group, None)
+
+    def nbytes(self):
+        return self.packed.numel() * 4 + self.scales.numel() * 2 + self.zeros.numel() * 2
+
+
+def _rms(x, w, eps):
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).half() * w
+
+
+class W4Decoder:
+    def __init__(self, cfg: DecoderConfig, max_batch: int, max_len: int, device="cuda", seed: int = 1):
+        self.cfg, self.max_batch, self.max_len = cfg, max_batch, max_len
+        gen = torch.Generator(device=device).manual_seed(seed)
+        h, hd, kvh = cfg.hidden, cfg.head_dim, cfg.kv_heads
+        self.embed = (torch.randn(cfg.vocab, h, generator=gen, device=device) * 0.02).half()
+        self.layers = []
+        for _ in range(cfg.layers):
+            self.layers.append({
+                "ln1": torch.ones(h, device=device, dtype=torch.float16),
+                "ln2": torch.ones(h, device=device, dtype=torch.float16),
+                "qkv": _W4((cfg.heads + 2 * kvh) * hd, h, cfg.group, gen, device),
+                "o": _W4(h, cfg.heads * hd, cfg.group, gen, device),
+                "gate_up": _W4(2 * cfg.ffn, h, cfg.group, gen, device),
+                "down": _W4(h, cfg.ffn, cfg.group, gen, device),
+            })
+        self.norm = torch.ones(h, device=device, dtype=torch.float16)
+        self.lm_head = _W4(cfg.vocab, h, cfg.group, gen, device)
+        # KV cache: K stored [L, B, kvh, hd, T] (keys already transposed for q @ K), V [L, B, kvh, T, hd]
+        self.k_cache = torch.zeros(cfg.layers, max_batch, kvh, hd, max_len, device=device, dtype=torch.float16)
+        self.v_cache = torch.zeros(cfg.layers, max_batch, kvh, max_len, hd, device=device, dtype=torch.float16)
+        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, hd, 2, device=device).float() / hd))
+        t = torch.arange(max_len, device=device).float()
+        freqs = torch.outer(t, inv)
+        self.cos = freqs.cos().half()
+        self.sin = freqs.sin().half()
+
+    def weight_bytes(self):
+        return sum(l[n].nbytes() for l in self.layers for n in ("qkv", "o", "gate_up", "down")) + self.lm_head.nbytes()
+
+    def _rope(self, x, pos):
+        # x [B, heads, T, hd]; pos [T] (or [B, T] for decode)
+        cos = self.cos[pos].unsqueeze(-3) if pos.dim() == 1 else self.cos[pos].unsqueeze(1)
+        sin = self.sin[pos].unsqueeze(-3) if pos.dim() == 1 else self.sin[pos].unsqueeze(1)
+        x1, x2 = x[..., 0::2], x[..., 1::2]
+        out = torch.empty_like(x)
+        out[..., 0::2] = x1 * cos - x2 * sin
+        out[..., 1::2] = x1 * sin + x2 * cos
+        return out
+
+    @torch.no_grad()
+    def prefill(self, tokens):
+        """tokens [B, T] int64; fills the cache at positions [0, T); returns next-token ids [B]."""
+        cfg = self.cfg
+        b, t = tokens.shape
+        hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
+        x = self.embed[tokens]
+        pos = torch.arange(t, device=tokens.device)
+        for li, l in enumerate(self.layers):
+            hn = _rms(x, l["ln1"], cfg.eps)
+            qkv = l["qkv"](hn.reshape(b * t, -1)).reshape(b, t, nh + 2 * kvh, hd).transpose(1, 2)
+            q, k, v = qkv[:, :nh], qkv[:, nh:nh + kvh], qkv[:, nh + kvh:]
+            q, k = self._rope(q, pos), self._rope(k, pos)
+            self.k_cache[li, :b, :, :, :t] = k.transpose(-1, -2)
+            self.v_cache[li, :b, :, :t] = v
+            kk = k.repeat_interleave(nh // kvh, dim=1) if kvh != nh else k
+            vv = v.repeat_interleave(nh // kvh, dim=1) if kvh != nh else v
+            att = torch.nn.functional.scaled_dot_product_attention(q.contiguous(), kk.contiguous(), vv.contiguous(),
+                                                                   is_causal=True)
+            x = x + l["o"](att.transpose(1, 2).reshape(b * t, nh * hd)).reshape(b, t, -1)
+            hn = _rms(x, l["ln2"], cfg.eps)
+            gu = l["gate_up"](hn.reshape(b * t, -1))
+            act = torch.nn.functional.silu(gu[:, :cfg.ffn]) * gu[:, cfg.ffn:]
+            x = x + l["down"](act.contiguous()).reshape(b, t, -1)
+        logits = self.lm_head(_rms(x[:, -1], self.norm, cfg.eps).contiguous())
+        return logits.argmax(-1)
+
+    @torch.no_grad()
+    def decode_step(self, tokens, cur_len):
+        """One greedy step for a batch.  tokens [B] int64 (the last token), cur_len [1]
+        int64 device tensor = position of that token; writes its K/V and returns the next ids."""
+        cfg = self.cfg
+        b = tokens.shape[0]
+        hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
+        grp = nh // kvh
+        x = self.embed[tokens]                                    # [B, H]
+        pos = cur_len.expand(b).unsqueeze(1)                      # [B, 1]
+        mask = (torch.arange(self.max_len, device=tokens.device) > cur_len).to(torch.float16) * -60000.0
+        scale = 1.0 / math.sqrt(hd)
+        for li, l in enumerate(self.layers):
+            hn = _rms(x, l["ln1"], cfg.eps)
+            qkv = l["qkv"](hn).reshape(b, nh + 2 * kvh, 1, hd)
+            q, k, v = qkv[:, :nh], qkv[:, nh:nh + kvh], qkv[:, nh + kvh:]
+            q, k = self._rope(q, pos), self._rope(k, pos)
+            self.k_cache[li, :b].index_copy_(3, cur_len, k.transpose(-1, -2).contiguous())
+            self.v_cache[li, :b].index_copy_(2, cur_len, v.contiguous())
+            qg = q.reshape(b, kvh, grp, hd)                        # heads grouped by kv head
+            s = torch.matmul(qg, self.k_cache[li, :b]) * scale     # [B, kvh, grp, T]
+            p = torch.softmax((s + mask).float(), dim=-1).half()
+            att = torch.matmul(p, self.v_cache[li, :b])            # [B, kvh, grp, hd]
+            x = x + l["o"](att.reshape(b, nh * hd))
+            hn = _rms(x, l["ln2"], cfg.eps)
+            gu = l["gate_up"](hn)
+            act = torch.nn.functional.silu(gu[:, :cfg.ffn]) * gu[:, cfg.ffn:]
+            x = x + l["down"](act.contiguous())
+        logits = self.lm_head(_rms(x, self.norm, cfg.eps).contiguous())
+        return logits.argmax(-1)
