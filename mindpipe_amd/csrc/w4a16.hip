@@ -450,6 +450,175 @@ __global__ __launch_bounds__(512) void w4a16_decode_kernel(
   }
 }
 
+// ------------------------------------------------------------------ batched decode (4 < M <= 64)
+//
+// For small batches the activation bytes per weight byte grow with M, so the
+// activations are not staged per 16-column tile: each wave owns NT column
+// tiles (16 columns each) and a contiguous K range, loads its activation
+// fragments straight from L2 into registers (once per 128-column block, reused
+// by the NT tiles) and gets the per-row block sums from an MFMA against ones.
+// S waves of a workgroup split K; their partial sums meet in LDS.  Scales and
+// zeros come as 32-bit words holding two consecutive groups.
+template <int MT, int NT, int S, bool ZP>
+__global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
+    const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
+    const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
+  constexpr int U = 2;  // blocks per prefetch buffer (even: one scale word per pair)
+  __shared__ float red[S > 1 ? S : 1][MT * NT * 4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kq = lane >> 4;
+  const int kw = k >> 3;
+  const int nblk = k >> 7;
+  const int col0 = blockIdx.x * NT * 16;
+  // contiguous, even-aligned K block range of this wave
+  const int lo = ((nblk * wave) / S) & ~1;
+  const int hi = wave == S - 1 ? nblk : (((nblk * (wave + 1)) / S) & ~1);
+  const int nmine = hi - lo;
+  const int blast = nblk - 1;
+  uint32_t magic_v = kMagic, mask_v = 0x000F000Fu;
+  asm volatile("" : "+v"(magic_v), "+v"(mask_v));
+  const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  const h8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+
+  const uint32_t *wrow[NT];
+  const uint32_t *srow[NT];
+  const uint32_t *zrow[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    int n = col0 + j * 16 + (lane & 15);
+    n = n < n_cols ? n : n_cols - 1;
+    wrow[j] = wq + static_cast<int64_t>(n) * kw + 4 * kq;
+    srow[j] = reinterpret_cast<const uint32_t *>(sc + static_cast<int64_t>(n) * n_groups);
+    zrow[j] = reinterpret_cast<const uint32_t *>(ZP ? zr + static_cast<int64_t>(n) * n_groups : sc);
+  }
+  const uint16_t *xrow[MT];
+  bool xval[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = t * 16 + (lane & 15);
+    xval[t] = m < m_rows;
+    xrow[t] = x + static_cast<int64_t>(xval[t] ? m : 0) * k + 32 * kq;
+  }
+
+  f4_t acc[MT][NT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[t][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint4 wa[U][NT], wb[U][NT];
+  uint32_t sa[NT], za[NT], sb[NT], zb[NT];
+  auto issue = [&](uint4 (*w)[NT], uint32_t *s2, uint32_t *z2, int r0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int b = lo + r0 + u;
+      b = b < blast ? b : blast;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) w[u][j] = *reinterpret_cast<const uint4 *>(wrow[j] + b * 16);
+    }
+    int b0 = lo + r0;
+    b0 = b0 < blast ? b0 : blast - 1;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      s2[j] = srow[j][b0 >> 1];
+      if (ZP) z2[j] = zrow[j][b0 >> 1];
+    }
+  };
+  auto compute = [&](uint4 (*w)[NT], const uint32_t *s2, const uint32_t *z2, int r0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = r0 + u;
+      const bool live = r < nmine;
+      int b = lo + r;
+      b = b < blast ? b : blast;
+      // activation fragments of this block for every m tile, and their row sums
+      h8_t af[MT][4];
+      f4_t cs[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        cs[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint4 d = *reinterpret_cast<const uint4 *>(xrow[t] + b * 128 + 8 * q);
+          h8_t a = perm_to_magic(d);
+          af[t][q] = xval[t] ? a : zero8;
+          cs[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][q], ones, cs[t], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const uint32_t wsel[4] = {w[u][j].x, w[u][j].y, w[u][j].z, w[u][j].w};
+        const int sh = ((b - (lo + r0)) & 1) * 16;
+        const float su = live ? mp_h2f(static_cast<uint16_t>(s2[j] >> sh)) : 0.0f;
+        const float zu = 1024.0f + (ZP ? mp_h2f(static_cast<uint16_t>(z2[j] >> sh)) : 8.0f);
+        h8_t bq[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bq[q] = dq_magic_fast(wsel[q], mask_v, magic_v);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          f4_t cg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][q], bq[q], cg, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t][j][i] = fmaf(su, fmaf(-zu, cs[t][i], cg[i]), acc[t][j][i]);
+        }
+      }
+    }
+  };
+
+  const int ngrp = (nmine + U - 1) / U;
+  issue(wa, sa, za, 0);
+  for (int g = 0; g < ngrp; g += 2) {
+    if (g + 1 < ngrp) issue(wb, sb, zb, (g + 1) * U);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(wa, sa, za, g * U);
+    if (g + 1 >= ngrp) break;
+    if (g + 2 < ngrp) issue(wa, sa, za, (g + 2) * U);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(wb, sb, zb, (g + 1) * U);
+  }
+
+  if (S > 1) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][(t * NT + j) * 4 + i][lane] = acc[t][j][i];
+    __syncthreads();
+    for (int o = threadIdx.x; o < MT * NT * 4 * 64; o += S * 64) {
+      const int slot = o >> 6, l = o & 63;
+      const int t = slot / (NT * 4), j = (slot / 4) % NT, i = slot % 4;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < S; ++w) v += red[w][slot][l];
+      const int m = t * 16 + 4 * (l >> 4) + i;
+      const int col = col0 + j * 16 + (l & 15);
+      if (m < m_rows && col < n_cols) {
+        if (bias) v += mp_h2f(bias[col]);
+        y[static_cast<int64_t>(m) * n_cols + col] = mp_f2h(v);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = t * 16 + 4 * kq + i;
+          const int col = col0 + j * 16 + (lane & 15);
+          if (m < m_rows && col < n_cols) {
+            float v = acc[t][j][i];
+            if (bias) v += mp_h2f(bias[col]);
+            y[static_cast<int64_t>(m) * n_cols + col] = mp_f2h(v);
+          }
+        }
+  }
+}
+
 // ------------------------------------------------------------------ prefill GEMM (M > 64)
 //
 // 128x128 output tile per workgroup of 4 waves (64x64 each, 2x2 MFMA
@@ -604,6 +773,16 @@ __global__ void w4a16_simple_kernel(const uint16_t *__restrict__ x, int64_t m_ro
 
 }  // namespace
 
+// Smallest M routed to the batched decode kernel is M > this value
+// (MP_W4_BATCH_MIN_M overrides it, for measurements).
+static int mp_batch_min_m() {
+  static int v = [] {
+    const char *e = getenv("MP_W4_BATCH_MIN_M");
+    return e ? atoi(e) : 4;
+  }();
+  return v;
+}
+
 // ====================================================================== C ABI
 
 extern "C" int mp_w4_quantize_awq(const void *w, int64_t n, int64_t k, int group_size, int zero_point,
@@ -689,7 +868,55 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
   const bool aligned = mp_aligned(x, 16) && mp_aligned(w_packed, 16) && mp_aligned(scales, 4) &&
                        (zeros == nullptr || mp_aligned(zeros, 4));
   const int n_groups_i = n_groups;
-  if (m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
+  const int batch_min_m = mp_batch_min_m();
+  // batched kernel: small N (activation staging per 16-column tile would dominate) or M >= 32
+  const bool batch_shape = m >= 32 || n <= 16384;
+  if (m > batch_min_m && batch_shape && m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 &&
+      aligned) {
+    const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
+    const int nblk = ki / 128;
+    const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    // column tiles per wave (activation reuse): 4 for 17..32 rows once N is large enough to fill the chip
+    const int nt = (mt == 2 && n >= 8192) ? 4 : 2;
+    const int smax = mt * nt >= 8 ? 8 : 16;            // LDS reduction buffer <= 64 KB
+    const int64_t groups = mp_cdiv(n, 16 * nt);
+    int split = 1;                                     // waves splitting K: ~2048 waves, >= 2 blocks each
+    while (split < smax && groups * split < 2048 && nblk / (split * 2) >= 2) split *= 2;
+    const dim3 grid(static_cast<unsigned>(groups));
+#define MP_W4_BATCH(MT_, NT_, S_)                                                                            \
+  do {                                                                                                       \
+    if (zp)                                                                                                  \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, wp, \
+                         ni, sp, zp, n_groups_i, bp, yp);                                                    \
+    else                                                                                                     \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, wp, \
+                         ni, sp, zp, n_groups_i, bp, yp);                                                    \
+  } while (0)
+    if (mt == 1) {
+      if (split == 1) MP_W4_BATCH(1, 2, 1);
+      else if (split == 2) MP_W4_BATCH(1, 2, 2);
+      else if (split == 4) MP_W4_BATCH(1, 2, 4);
+      else if (split == 8) MP_W4_BATCH(1, 2, 8);
+      else MP_W4_BATCH(1, 2, 16);
+    } else if (mt == 2 && nt == 4) {
+      if (split == 1) MP_W4_BATCH(2, 4, 1);
+      else if (split == 2) MP_W4_BATCH(2, 4, 2);
+      else if (split == 4) MP_W4_BATCH(2, 4, 4);
+      else MP_W4_BATCH(2, 4, 8);
+    } else if (mt == 2) {
+      if (split == 1) MP_W4_BATCH(2, 2, 1);
+      else if (split == 2) MP_W4_BATCH(2, 2, 2);
+      else if (split == 4) MP_W4_BATCH(2, 2, 4);
+      else if (split == 8) MP_W4_BATCH(2, 2, 8);
+      else MP_W4_BATCH(2, 2, 16);
+    } else {
+      if (split == 1) MP_W4_BATCH(4, 2, 1);
+      else if (split == 2) MP_W4_BATCH(4, 2, 2);
+      else if (split == 4) MP_W4_BATCH(4, 2, 4);
+      else MP_W4_BATCH(4, 2, 8);
+    }
+#undef MP_W4_BATCH
+  } else if (m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
     const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
     const int nblk = ki / 128;
     const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
