@@ -773,8 +773,194 @@ __global__ void w4a16_simple_kernel(const uint16_t *__restrict__ x, int64_t m_ro
 
 }  // namespace
 
+
+// ---------------------------------------------------------------- M = 1 GEMV
+// Bandwidth kernel for one activation row.  A wave owns R output rows over all
+// of K; lane l covers K positions [j*2048 + 32 l, +32) of chunk j, so its
+// activation slice is loaded once per chunk and reused by the R rows.  Each
+// 32-bit weight word is dequantised without a shift for half of its nibbles:
+//   (w & 0x000F000F) | 0x6400_6400 -> 1024 + u    (nibbles 0, 4)
+//   (w & 0x00F000F0) | 0x6400_6400 -> 1024 + 16 u (nibbles 1, 5)
+// and the same two masks on w >> 8 for nibbles 2, 6 / 3, 7.  The two scalings
+// go to separate fp32 dot-product chains d0 / d1, so with X0 / X1 the slice
+// sums over the matching positions,
+//   sum_k (u_k - z) x_k = d0 + d1 / 16 - (1024 X0 + 64 X1) - z (X0 + X1).
+// Scale / zero pairs of the R rows x 16 groups are loaded by one coalesced
+// load per 64 entries and handed to the lanes that use them by ds_bpermute.
+// The R per-lane partials are reduced across the wave by a halving butterfly.
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2_t mp_as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+
+template <int R, int C, int S, bool ZP>
+__global__ __launch_bounds__(256) void w4a16_gemv_kernel(
+    const uint16_t *__restrict__ x, int k, const uint32_t *__restrict__ wq, int n_cols,
+    const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
+  constexpr int SZN = R * 16 > 64 ? R * 16 / 64 : 1;  // scale / zero loads per chunk
+  constexpr int LPR = 64 / R;                         // lanes per row after the butterfly
+  constexpr int GPW = 4 / S;                          // row groups per workgroup (S waves split K)
+  __shared__ float red[S > 1 ? 4 : 1][R];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sw = wave % S;
+  const int row0 = (blockIdx.x * GPW + wave / S) * R;
+  if (S == 1 && row0 >= n_cols) return;  // wave-uniform; with S == 1 there is no barrier
+  const int kw = k >> 3;
+  const int nch = (k + 2047) >> 11;
+  uint32_t magic_v = kMagic, m0_v = 0x000F000Fu, m1_v = 0x00F000F0u;
+  asm volatile("" : "+v"(magic_v), "+v"(m0_v), "+v"(m1_v));  // opaque: keep the constants in VGPRs
+
+  const uint32_t *wrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = row0 + r < n_cols ? row0 + r : n_cols - 1;
+    wrow[r] = wq + static_cast<int64_t>(n) * kw;
+  }
+  // scale / zero entry e = lane + 64 i: row e / 16 of the wave, group 16 j + e % 16, read as the
+  // 32-bit word holding groups (2 t, 2 t + 1) (n_groups even, 4-byte aligned rows)
+  const uint32_t *srow[SZN];
+  const uint32_t *zrow[SZN];
+#pragma unroll
+  for (int i = 0; i < SZN; ++i) {
+    const int e = lane + 64 * i;
+    int r = e >> 4;
+    r = r < R ? r : R - 1;
+    const int n = row0 + r < n_cols ? row0 + r : n_cols - 1;
+    srow[i] = reinterpret_cast<const uint32_t *>(sc + static_cast<int64_t>(n) * n_groups);
+    zrow[i] = reinterpret_cast<const uint32_t *>(ZP ? zr + static_cast<int64_t>(n) * n_groups : sc);
+  }
+  const int gpair = (lane & 15) >> 1;
+  // v_perm selector: (s, z) halves of this lane's group -> s in bits 0-15, z in bits 16-31
+  const uint32_t sel = (lane & 1) ? 0x07060302u : 0x05040100u;  // bytes 0-3: s word, 4-7: z word
+
+  struct Stage {
+    uint4 w[R];
+    uint4 xv[4];
+    uint32_t s[SZN], z[SZN];
+  };
+  auto issue = [&](Stage &st, int j) {
+    int kp = j * 2048 + 32 * lane;
+    kp = kp < k ? kp : k - 32;
+#pragma unroll
+    for (int r = 0; r < R; ++r) st.w[r] = *reinterpret_cast<const uint4 *>(wrow[r] + (kp >> 3));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) st.xv[q] = *reinterpret_cast<const uint4 *>(x + kp + 8 * q);
+    int t = 8 * j + gpair;
+    t = t < (n_groups >> 1) ? t : (n_groups >> 1) - 1;
+#pragma unroll
+    for (int i = 0; i < SZN; ++i) {
+      st.s[i] = srow[i][t];
+      st.z[i] = ZP ? zrow[i][t] : 0x48004800u;  // fp16 8.0
+    }
+  };
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  auto compute = [&](const Stage &st, int j) {
+    const bool live = j * 2048 + 32 * lane < k;
+    union {
+      uint32_t u[16];
+      h8_t h[4];
+    } xa;
+    float x0 = 0.f, x1 = 0.f;
+    const h2_t ones = mp_as_h2(0x3C003C00u);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      xa.h[q] = perm_to_magic(st.xv[q]);  // a dead lane (clamped K) is removed by its zero scale
+      x0 = __builtin_amdgcn_fdot2(mp_as_h2(xa.u[4 * q + 0]), ones, x0, false);
+      x1 = __builtin_amdgcn_fdot2(mp_as_h2(xa.u[4 * q + 1]), ones, x1, false);
+      x0 = __builtin_amdgcn_fdot2(mp_as_h2(xa.u[4 * q + 2]), ones, x0, false);
+      x1 = __builtin_amdgcn_fdot2(mp_as_h2(xa.u[4 * q + 3]), ones, x1, false);
+    }
+    const float c_off = fmaf(1024.0f, x0, 64.0f * x1);
+    const float c_sum = x0 + x1;
+    uint32_t szw[SZN];
+#pragma unroll
+    for (int i = 0; i < SZN; ++i) {
+      uint32_t sw = st.s[i], zw = st.z[i];
+      asm volatile("" : "+v"(sw), "+v"(zw));  // keep the combine after the barrier: no early wait
+      szw[i] = __builtin_amdgcn_perm(zw, sw, sel);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      // (s, z) of row r, group 16 j + lane / 4: entry r * 16 + lane / 4
+      const uint32_t v = __shfl(szw[(r * 16) >> 6], ((r * 16) & 63) + (lane >> 2), 64);
+      const float s = live ? mp_h2f(static_cast<uint16_t>(v)) : 0.f;
+      const float z = mp_h2f(static_cast<uint16_t>(v >> 16));
+      const uint32_t wv[4] = {st.w[r].x, st.w[r].y, st.w[r].z, st.w[r].w};
+      float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t w = wv[q], w8 = w >> 8;
+        d0 = __builtin_amdgcn_fdot2(mp_as_h2((w & m0_v) | magic_v), mp_as_h2(xa.u[4 * q + 0]), d0, false);
+        d1 = __builtin_amdgcn_fdot2(mp_as_h2((w & m1_v) | magic_v), mp_as_h2(xa.u[4 * q + 1]), d1, false);
+        d0 = __builtin_amdgcn_fdot2(mp_as_h2((w8 & m0_v) | magic_v), mp_as_h2(xa.u[4 * q + 2]), d0, false);
+        d1 = __builtin_amdgcn_fdot2(mp_as_h2((w8 & m1_v) | magic_v), mp_as_h2(xa.u[4 * q + 3]), d1, false);
+      }
+      acc[r] = fmaf(s, fmaf(d1, 0.0625f, d0) - fmaf(z, c_sum, c_off), acc[r]);
+    }
+  };
+
+  // C chunks per iteration, all issued before any is used; a chunk past the end
+  // re-reads the last one (clamped) and adds nothing (zero scale).  No load
+  // crosses an iteration, so every wait is a partial vmcnt and latency is
+  // hidden by the other waves of the CU.
+  Stage st[C];
+  for (int j = sw * C; j < nch; j += S * C) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) issue(st[c], j + c < nch ? j + c : nch - 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      compute(st[c], j + c);
+      __builtin_amdgcn_sched_barrier(0);  // chunk c + 1's waits stay after chunk c's math
+    }
+  }
+
+  // halving butterfly: after stage b the lane keeps the rows whose index bit matches lane bit (5 - b)
+#pragma unroll
+  for (int c = R, mask = 32; c > 1; c >>= 1, mask >>= 1) {
+    const bool up = (lane & mask) != 0;
+#pragma unroll
+    for (int i = 0; i < c / 2; ++i) {
+      const float send = up ? acc[i] : acc[i + c / 2];
+      const float keep = up ? acc[i + c / 2] : acc[i];
+      acc[i] = keep + __shfl_xor(send, mask, 64);
+    }
+  }
+  float v = acc[0];
+#pragma unroll
+  for (int mask = LPR / 2; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask, 64);
+  if (S > 1) {  // the S waves of a row group add their K parts
+    if ((lane % LPR) == 0) red[wave][lane / LPR] = v;
+    __syncthreads();
+    if (sw != 0) return;
+#pragma unroll
+    for (int t = 1; t < S; ++t) v += red[wave + t][lane / LPR];
+  }
+  const int row = row0 + lane / LPR;
+  if ((lane % LPR) == 0 && row < n_cols) {
+    if (bias) v += mp_h2f(bias[row]);
+    y[row] = mp_f2h(v);
+  }
+}
+
 // Smallest M routed to the batched decode kernel is M > this value
 // (MP_W4_BATCH_MIN_M overrides it, for measurements).
+// Measurement knobs for the one-row GEMV shape choice: MP_W4_GEMV_R (rows per
+// wave), MP_W4_GEMV_C (chunks per iteration), MP_W4_GEMV_S (waves splitting K);
+// MP_W4_GEMV_OFF=1 routes one-row calls to the general decode kernel.
+static int mp_gemv_env(int which) {
+  static const int v[4] = {
+      getenv("MP_W4_GEMV_OFF") ? atoi(getenv("MP_W4_GEMV_OFF")) : 0,
+      getenv("MP_W4_GEMV_R") ? atoi(getenv("MP_W4_GEMV_R")) : 0,
+      getenv("MP_W4_GEMV_C") ? atoi(getenv("MP_W4_GEMV_C")) : 0,
+      getenv("MP_W4_GEMV_S") ? atoi(getenv("MP_W4_GEMV_S")) : 0,
+  };
+  return v[which];
+}
+
 static int mp_batch_min_m() {
   static int v = [] {
     const char *e = getenv("MP_W4_BATCH_MIN_M");
@@ -871,7 +1057,53 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
   const int batch_min_m = mp_batch_min_m();
   // batched kernel: small N (activation staging per 16-column tile would dominate) or M >= 32
   const bool batch_shape = m >= 32 || n <= 16384;
-  if (m > batch_min_m && batch_shape && m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 &&
+  if (m == 1 && mp_gemv_env(0) == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
+    const int ki = static_cast<int>(k), ni = static_cast<int>(n);
+    const int nch = (ki + 2047) / 2048;  // 2048-wide K chunks
+    // measured on the 7B / 70B layer shapes: all chunks up front for short K, two waves
+    // splitting K when the chunk count is a multiple of 4 or the rows alone give under
+    // 2048 waves, else one chunk per iteration
+    int r = 4, c = 1, sk = 1;
+    if (nch <= 2) {
+      c = nch;
+    } else if (nch % 4 == 0) {
+      c = 2;
+      sk = 2;
+    } else if (nch % 2 == 0 && mp_cdiv(n, 4) < 2048) {
+      sk = 2;
+    }
+    if (mp_gemv_env(1) > 0) r = mp_gemv_env(1) >= 8 ? 8 : 4;
+    if (mp_gemv_env(2) > 0) c = mp_gemv_env(2) >= 4 ? 4 : mp_gemv_env(2);
+    if (mp_gemv_env(3) > 0) sk = mp_gemv_env(3) >= 4 ? 4 : mp_gemv_env(3);
+    const int64_t groups = mp_cdiv(n, r);
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(groups, 4 / sk)));
+#define MP_W4_GEMV(R_, C_, S_)                                                                               \
+  do {                                                                                                       \
+    if (zp)                                                                                                  \
+      hipLaunchKernelGGL((w4a16_gemv_kernel<R_, C_, S_, true>), grid, dim3(256), 0, s, xp, ki, wp, ni, sp,  \
+                         zp, n_groups_i, bp, yp);                                                            \
+    else                                                                                                     \
+      hipLaunchKernelGGL((w4a16_gemv_kernel<R_, C_, S_, false>), grid, dim3(256), 0, s, xp, ki, wp, ni, sp, \
+                         zp, n_groups_i, bp, yp);                                                            \
+  } while (0)
+#define MP_W4_GEMV_C(R_, S_)           \
+  do {                                 \
+    if (c == 1) MP_W4_GEMV(R_, 1, S_); \
+    else if (c == 2) MP_W4_GEMV(R_, 2, S_); \
+    else MP_W4_GEMV(R_, 4, S_);        \
+  } while (0)
+#define MP_W4_GEMV_S(R_)               \
+  do {                                 \
+    if (sk == 1) MP_W4_GEMV_C(R_, 1);  \
+    else if (sk == 2) MP_W4_GEMV_C(R_, 2); \
+    else MP_W4_GEMV_C(R_, 4);          \
+  } while (0)
+    if (r == 4) MP_W4_GEMV_S(4);
+    else MP_W4_GEMV_S(8);
+#undef MP_W4_GEMV_S
+#undef MP_W4_GEMV_C
+#undef MP_W4_GEMV
+  } else if (m > batch_min_m && batch_shape && m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 &&
       aligned) {
     const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
     const int nblk = ki / 128;
