@@ -109,6 +109,18 @@ int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t *w_packed, 
 int mp_quant_per_token_i8(const void *x, int64_t m, int64_t k, int x_dtype, int8_t *q, void *scale,
                           int scale_rule, mp_stream_t stream);
 
+/* Fused residual add + RMSNorm (+ per-token dynamic int8 quant) of x [M,H]
+ * (fp16/bf16), replacing torch_npu.npu_add_rms_norm_dynamic_quant and the
+ * npu_add_rms_norm -> npu_dynamic_quant chain of the W8A8 runtime
+ * (vllm_ascend.patch:746-787).  sum = x + residual (fp32; residual may be NULL),
+ * residual_out = sum in the input dtype (optional), y = round(round(sum * rstd)
+ * * weight) (optional), q int8 [M,H] + scale fp32 [M] = per-token quant of y
+ * with the MP_SCALE_FP32 rule of mp_quant_per_token_i8 (optional, both or
+ * neither).  In-place calls (residual_out == residual, y == x) are allowed. */
+int mp_add_rms_norm_quant(const void *x, const void *residual, const void *weight, float eps, int64_t m,
+                          int64_t h, int dtype, void *residual_out, void *y, int8_t *q, float *scale,
+                          mp_stream_t stream);
+
 /* Per-output-channel symmetric int8 weight quant of w [N,K] (fp16/bf16).
  * MP_SCALE_FP32: quantize_weight_per_channel
  *   (scripts/repro/export_fp16_to_ascend_w8a8_dynamic_probe.py:175-195),

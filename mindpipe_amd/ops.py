@@ -176,6 +176,44 @@ def _(x, fp16_scale=False):
             x.new_empty(x.shape[:-1], dtype=torch.float16 if fp16_scale else torch.float32))
 
 
+def add_rms_norm_quant(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor, eps: float,
+                       quant: bool = True, out: bool = False, inplace: bool = False):
+    """Fused residual add + RMSNorm + per-token dynamic int8 quant.
+
+    Returns ``(y, q, scale, residual_sum)``: ``y`` the normalised activations in
+    ``x.dtype`` (``None`` unless ``out`` or not ``quant``), ``q``/``scale`` the
+    int8 codes and fp32 per-token scale of ``y`` (``None`` unless ``quant``) and
+    ``residual_sum = x + residual`` in ``x.dtype`` (``None`` without a residual).
+    ``inplace=True`` writes the sum into ``residual`` and ``y`` into ``x``
+    (the in-place contract of vLLM's fused add-RMSNorm).
+    """
+    _need(x, "x", (torch.float16, torch.bfloat16))
+    _need(weight, "weight", x.dtype, 1)
+    h = x.shape[-1]
+    if weight.shape[0] != h:
+        raise RuntimeError(f"weight {tuple(weight.shape)} does not match H={h}")
+    if residual is not None:
+        _need(residual, "residual", x.dtype)
+        if residual.shape != x.shape:
+            raise RuntimeError("residual must have the shape of x")
+    x2 = x.reshape(-1, h)
+    m = x2.shape[0]
+    want_y = out or not quant
+    if inplace:
+        y = x if want_y else None
+        rsum = residual
+    else:
+        y = torch.empty_like(x) if want_y else None
+        rsum = torch.empty_like(x) if residual is not None else None
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device) if quant else None
+    s = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device) if quant else None
+    with _dev(x):
+        _lib.check(_lib.load().mp_add_rms_norm_quant(
+            x2.data_ptr(), _ptr(residual), weight.data_ptr(), float(eps), m, h, _DT[x.dtype], _ptr(rsum),
+            _ptr(y), _ptr(q), _ptr(s), _stream()), "mp_add_rms_norm_quant")
+    return y, q, s, rsum
+
+
 def w8_quantize_per_channel(w: torch.Tensor, rule: str = "export"):
     """Per-output-channel int8 weight quant.
 

@@ -5,20 +5,26 @@ MindPipe (``acceleration/runtime_patches/vllm_ascend.patch:3935-4033``): per-tok
 dynamic int8 quant (fp32 scale, the ``npu_dynamic_quant`` contract) then the int8
 GEMM with the per-token x per-channel epilogue (``npu_quant_matmul``).
 ``fused_experts_w8a8`` replaces the MoE expert chain of ``_run_expert_tile``
-(``vllm_ascend.patch:2356-2423``).  Layer attributes keep the reference's names
+(``vllm_ascend.patch:2356-2423``).  ``add_rms_norm_forward`` replaces the
+add-RMSNorm(-dynamic-quant) step in front of a W8A8 linear
+(``_addrmsnorm_forward_oot``, ``vllm_ascend.patch:740-792``), and
+``prepare_dense_mlp_w8a8`` / ``dense_mlp_w8a8`` the chunked dense-MLP chain
+(``vllm.patch:883-1037``, weight split ``vllm_ascend.patch:4149-4277``).  Layer attributes keep the reference's names
 (``weight``, ``weight_scale``, ``weight_offset``, ``weight_scale_fp32``,
 ``_ascend_quant_config``); the weight stays ``[N, K]`` (the kernel reads that layout
 directly, so no transpose or NZ cast is needed).
 """
 from __future__ import annotations
 
-from typing import Optional
+import os
+from typing import Optional, Tuple, Union
 
 import torch
 
 from . import ops
 
-__all__ = ["W8A8DynamicLinearMethod", "fused_experts_w8a8", "dynamic_quant"]
+__all__ = ["W8A8DynamicLinearMethod", "fused_experts_w8a8", "dynamic_quant", "add_rms_norm_forward",
+           "prepare_dense_mlp_w8a8", "dense_mlp_w8a8"]
 
 
 def dynamic_quant(x: torch.Tensor):
@@ -81,3 +87,147 @@ def fused_experts_w8a8(hidden_states: torch.Tensor, w1: torch.Tensor, w1_scale: 
     return ops.moe_w8a8_forward(hidden_states.contiguous(), topk_ids, topk_weights, w1,
                                 w1_scale.to(torch.float32).contiguous(), w2, w2_scale.to(torch.float32).contiguous(),
                                 out_dtype=output_dtype or hidden_states.dtype)
+
+
+# ---------------------------------------------------------------- add + RMSNorm (+ dynamic quant)
+def _env_int(name: str, default: int) -> int:
+    try:
+        return int(os.getenv(name, str(default)))
+    except ValueError:
+        return default
+
+
+def _quant_method_of(layer):
+    qm = getattr(layer, "quant_method", None)
+    return getattr(qm, "quant_method", qm)
+
+
+def _is_w8a8_dynamic_linear(layer) -> bool:
+    return isinstance(_quant_method_of(layer), W8A8DynamicLinearMethod)
+
+
+def _should_use_w8a8_dynamic_fusion(layer, x: torch.Tensor) -> bool:
+    """Token window of ``vllm_ascend.patch:720-738`` (same environment names and defaults,
+    ``:505-512``:
+    ``MINDPIPE_W8A8_DYNAMIC_RMSNORM_QUANT_MAX_TOKENS`` 256, ``..._MIN_TOKENS`` 0; a maximum
+    <= 0 removes the upper bound).  Here the fused and unfused paths give the same bits,
+    so the window only chooses the kernel count."""
+    if not _is_w8a8_dynamic_linear(layer):
+        return False
+    max_tokens = _env_int("MINDPIPE_W8A8_DYNAMIC_RMSNORM_QUANT_MAX_TOKENS", 256)
+    min_tokens = max(0, _env_int("MINDPIPE_W8A8_DYNAMIC_RMSNORM_QUANT_MIN_TOKENS", 0))
+    tokens = x.numel() // x.shape[-1]
+    if max_tokens <= 0:
+        return tokens >= min_tokens
+    return min_tokens <= tokens <= max_tokens
+
+
+def add_rms_norm_forward(norm, x: torch.Tensor, residual: Optional[torch.Tensor], layer=None):
+    """``_addrmsnorm_forward_oot(self, x, residual, layer)`` (``vllm_ascend.patch:740-792``).
+
+    ``norm`` carries ``weight`` and ``variance_epsilon`` (an RMSNorm module).  When the next
+    linear ``layer`` is a W8A8 dynamic linear inside the token window, returns
+    ``((int8 codes, fp32 scale), residual_sum)`` for its ``apply`` (the
+    ``npu_add_rms_norm_dynamic_quant`` branch); otherwise ``(normalised x, residual_sum)`` (the
+    ``npu_add_rms_norm`` branch).  With ``residual=None`` this is a plain RMSNorm and the
+    returned residual is ``x`` itself (the first layer of vLLM's decoder).
+    """
+    eps = float(getattr(norm, "variance_epsilon", getattr(norm, "eps", 1e-6)))
+    weight = norm.weight
+    if layer is not None and _should_use_w8a8_dynamic_fusion(layer, x):
+        _, q, s, rsum = ops.add_rms_norm_quant(x, residual, weight, eps, quant=True, out=False)
+        return (q, s), (rsum if residual is not None else x)
+    y, _, _, rsum = ops.add_rms_norm_quant(x, residual, weight, eps, quant=False)
+    return y, (rsum if residual is not None else x)
+
+
+# ---------------------------------------------------------------- dense MLP chain
+_OFFSETS = {}
+
+
+def _group_offsets(tokens: int, device) -> torch.Tensor:
+    """Cumulative group boundaries ``[0, T]`` of a dense call (one group of all tokens),
+    cached per device and T so that graph capture records no host copy."""
+    key = (str(device), tokens)
+    t = _OFFSETS.get(key)
+    if t is None:
+        t = torch.tensor([0, tokens], dtype=torch.int64, device=device)
+        _OFFSETS[key] = t
+    return t
+
+
+def prepare_dense_mlp_w8a8(gate_up, down, chunks: int = 1) -> None:
+    """Split a W8A8 ``gate_up`` / ``down`` pair into the chunk buffers of
+    ``_prepare_qwen2_gate_up_chunked_w8a8`` / ``_prepare_qwen2_down_chunked_w8a8``
+    (``vllm_ascend.patch:4149-4277``; same attribute names).  ``gate_up.weight`` is int8
+    ``[2I, H]`` (gate rows first), ``down.weight`` int8 ``[H, I]``, each with
+    ``weight_scale_fp32`` per output row (``process_weights_after_loading``).  Chunk ``c``
+    holds gate rows ``[c*cs, (c+1)*cs)`` and the matching up rows as ``[1, 2cs, H]`` (the
+    grouped kernel's ``[E, 2I, H]`` layout with one group); the down chunks are the matching
+    column slices ``[H, cs]`` with the down scale rounded to bf16 (``:4262-4264``; the
+    single-chunk path keeps the fp32 scale, ``vllm.patch:1003-1037``).  There is no
+    10240-column limit here, so ``chunks=1`` is the
+    fast choice; larger counts reproduce the reference's per-chunk requantisation.
+    """
+    w, sc = gate_up.weight.data, gate_up.weight_scale_fp32
+    inter = w.shape[0] // 2
+    if w.shape[0] % 2 or inter % chunks:
+        raise ValueError(f"gate_up rows {w.shape[0]} do not split into {chunks} chunks")
+    if down.weight.shape[1] != inter:
+        raise ValueError("down.weight must be [H, I]")
+    cs = inter // chunks
+    for idx in range(chunks):
+        rows = torch.cat([torch.arange(idx * cs, (idx + 1) * cs), torch.arange(inter + idx * cs, inter + (idx + 1) * cs)])
+        rows = rows.to(w.device)
+        setattr(gate_up, f"_mindpipe_chunked_gate_up_weight_{idx}", w.index_select(0, rows).unsqueeze(0).contiguous())
+        setattr(gate_up, f"_mindpipe_chunked_gate_up_scale_{idx}",
+                sc.index_select(0, rows).reshape(1, 2 * cs).to(torch.float32).contiguous())
+    dw = down.weight.data
+    down._mindpipe_chunked_down_weight = torch.stack([dw[:, i * cs:(i + 1) * cs] for i in range(chunks)]).contiguous()
+    down._mindpipe_chunked_down_scale_bf16 = down.weight_scale_fp32.to(torch.bfloat16).contiguous()
+    down._mindpipe_chunked_down_scale_fp32 = (down.weight_scale_fp32 if chunks == 1 else
+                                              down._mindpipe_chunked_down_scale_bf16).to(torch.float32).contiguous()
+    for layer, kind in ((gate_up, "gate_up"), (down, "down")):
+        layer._mindpipe_qwen2_mlp_chunked_kind = kind
+        layer._mindpipe_qwen2_mlp_chunk_count = chunks
+        layer._mindpipe_qwen2_mlp_chunk_size = cs
+
+
+def dense_mlp_w8a8(gate_up, down, x: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]) -> torch.Tensor:
+    """``_mindpipe_forward_chunked_mlp_w8a8`` (``vllm.patch:883-937``; one chunk
+    ``:1003-1037``) on the gfx950 kernels.
+
+    ``x`` is activations ``[T, H]`` (quantized here, fp32 per-token scale) or a pre-quantized
+    ``(int8 [T, H], scale)`` tuple (from ``add_rms_norm_forward``).  Each chunk runs the grouped
+    GEMM1 + SwiGLU + requant kernel with one group of all tokens, then the int8 down GEMM on the
+    chunk's columns; chunk outputs are summed in fp32 and rounded once to the output dtype
+    (``x.dtype``, or ``down.params_dtype`` / fp16 for a tuple input, as in
+    ``_mindpipe_chunked_mlp_output_dtype``).
+    """
+    chunks = int(getattr(gate_up, "_mindpipe_qwen2_mlp_chunk_count"))
+    cs = int(gate_up._mindpipe_qwen2_mlp_chunk_size)
+    if isinstance(x, tuple):
+        qx, sx = x
+        out_dtype = getattr(down, "params_dtype", torch.float16)
+        lead = qx.shape[:-1]
+        qx = qx.reshape(-1, qx.shape[-1]).contiguous()
+        sx = sx.flatten().to(torch.float32).contiguous()
+    else:
+        out_dtype = x.dtype
+        lead = x.shape[:-1]
+        qx, sx = dynamic_quant(x.reshape(-1, x.shape[-1]))
+    offsets = _group_offsets(qx.shape[0], qx.device)
+    w2 = down._mindpipe_chunked_down_weight
+    s2 = down._mindpipe_chunked_down_scale_fp32
+    out = None
+    for idx in range(chunks):
+        qh, sh = ops.moe_gmm1_swiglu_quant(qx, sx, getattr(gate_up, f"_mindpipe_chunked_gate_up_weight_{idx}"),
+                                           getattr(gate_up, f"_mindpipe_chunked_gate_up_scale_{idx}"), offsets, cs)
+        if chunks == 1:
+            out = ops.w8a8_gemm(qh, sh, w2[0], s2, None, out_dtype)
+            break
+        y = ops.w8a8_gemm(qh, sh, w2[idx], s2, None, torch.float32)
+        out = y if out is None else out + y
+    if chunks > 1:
+        out = out.to(out_dtype)
+    return out.reshape(*lead, out.shape[-1])

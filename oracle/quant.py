@@ -31,6 +31,9 @@ Pinning (how each function is checked; see ``tests/test_oracle.py``)
   row, |x - q*s| <= s/2, ties to even) and brute-force Python loops on small
   rows.
 * ``w8a8_linear_runtime``: exact int64 brute force on tiny inputs.
+* ``dense_mlp_runtime``: equals ``moe_runtime`` with one expert at one chunk.
+* ``add_rms_norm_quant``: closed forms (constant rows, +-a rows), scale
+  invariance, the residual identity and q == per-token quant of y.
 * MoE: a brute-force per-assignment loop on tiny E/T/H/I, routing invariants.
 Nothing here is "parity unpinned" except where a docstring says so.
 """
@@ -54,6 +57,8 @@ __all__ = [
     "quantize_activation_per_token_fake",
     "quantize_weight_per_channel_fake",
     "quantize_per_token_runtime",
+    "add_rms_norm_quant",
+    "dense_mlp_runtime",
     "quantize_weight_per_channel_export",
     "w8a8_linear_runtime",
     "w8a8_linear_fake",
@@ -313,6 +318,42 @@ def quantize_per_token_runtime(x, in_dtype="fp16"):
     return q, s
 
 
+def add_rms_norm_quant(x, residual, weight, eps, in_dtype="fp16", quant=True):
+    """Residual add + RMSNorm + per-token dynamic int8 quant: the chain the W8A8
+    runtime runs in front of qkv / gate_up (``vllm_ascend.patch:746-787``:
+    ``npu_add_rms_norm_dynamic_quant``, or ``npu_add_rms_norm`` then the linear's
+    ``npu_dynamic_quant``).  The Ascend ops are closed; the RMSNorm arithmetic
+    restated here is vLLM's native RMSNorm (third-party, not under the reference;
+    vLLM 0.11 is named by ``acceleration/README.md:10-11``):
+
+    * ``sum = fp32(x) + fp32(residual)``; ``residual_out = round(sum)``
+    * ``var = mean(sum**2)`` (fp32), ``rstd = 1 / sqrt(var + eps)``
+    * ``y = round(round(sum * rstd) * weight)`` (rounding to the input dtype twice:
+      ``x.to(orig_dtype)`` then ``* self.weight`` in that dtype)
+    * ``q, s = quantize_per_token_runtime(y)``
+
+    Pinned by closed forms (constant rows, +-a rows), RMSNorm scale invariance,
+    the residual identity ``f(x, r) == f(x + r, None)`` for exact sums, and the
+    identity ``q == quantize_per_token_runtime(y)``; the fp32 summation order of
+    ``mean`` is not fixed by any of them (a 1-ulp difference of ``y`` is allowed).
+    Returns ``(y, q, s, residual_out)`` (``q``/``s`` None unless ``quant``;
+    ``residual_out`` None without a residual).
+    """
+    xf = _in_f32(x, in_dtype)
+    if residual is not None:
+        xf = (xf + _in_f32(residual, in_dtype)).astype(np.float32)
+    rout = _to_out(xf, in_dtype) if residual is not None else None
+    var = (np.square(xf.astype(np.float64)).mean(axis=-1)).astype(np.float32)
+    rstd = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
+    yn = _in_f32(_to_out((xf * rstd[..., None]).astype(np.float32), in_dtype), in_dtype)
+    w = _in_f32(np.asarray(weight), in_dtype)
+    y = _to_out((yn * w).astype(np.float32), in_dtype)
+    if not quant:
+        return y, None, None, rout
+    q, sc = quantize_per_token_runtime(y, in_dtype)
+    return y, q, sc, rout
+
+
 def quantize_weight_per_channel_export(w, in_dtype="fp16"):
     """Real-export W8 quantizer ``quantize_weight_per_channel``
     (``scripts/repro/export_fp16_to_ascend_w8a8_dynamic_probe.py:175-195``; same as
@@ -453,6 +494,39 @@ def moe_runtime(x, topk_ids, topk_w, qw13, s13, qw2, s2, out_dtype="fp16", retur
     if return_intermediate:
         return res, qh_all
     return res
+
+
+def dense_mlp_runtime(x, qw13, s13, qw2, s2, chunks=1, out_dtype="fp16", qx=None, sx=None):
+    """Dense-MLP W8A8 chain of the reference's chunked Qwen2 MLP
+    (``vllm.patch:883-1037``; weight split ``vllm_ascend.patch:4149-4277``):
+    per-token quant of ``x`` (or a given ``(qx, sx)``), then for each of ``chunks``
+    slices of the intermediate dimension the grouped GEMM1 + SwiGLU + requant
+    (``npu_grouped_matmul_swiglu_quant`` with one group of all tokens) on the gate
+    rows ``[c*cs, (c+1)*cs)`` and the matching up rows, the down GEMM on the same
+    slice of the down weight's columns, and the fp32 sum over chunks
+    (``npu_quant_matmul_reduce_sum``, down scale rounded to bf16), rounded once.
+    With ``chunks == 1`` this is the single-chunk path (``npu_quant_matmul`` on the
+    requantized hidden state, fp32 down scale; ``vllm.patch:1003-1037``).
+    ``qw13 [2I, H]`` (gate rows first), ``s13 [2I]``, ``qw2 [H, I]``, ``s2 [H]``.
+    Pinned: ``chunks == 1`` equals ``moe_runtime`` with one expert, top-1, weight 1
+    (a separate code path); the integer products are exact."""
+    if qx is None:
+        qx, sx = quantize_per_token_runtime(x)
+    inter = qw2.shape[1]
+    cs = inter // chunks
+    # the chunked path's down scale is rounded to bf16 (vllm_ascend.patch:4262-4264)
+    s2c = _f(s2) if chunks == 1 else bf16_bits_to_f32(f32_to_bf16_bits(_f(s2)))
+    out = np.zeros((qx.shape[0], qw2.shape[0]), np.float32)
+    for c in range(chunks):
+        rows = np.r_[c * cs:(c + 1) * cs, inter + c * cs:inter + (c + 1) * cs]
+        acc = int_matmul_nt(qx, qw13[rows])
+        g = ((acc.astype(np.float32) * sx[:, None]).astype(np.float32) * _f(s13[rows])[None, :]).astype(np.float32)
+        h = (_silu(g[:, :cs]) * g[:, cs:]).astype(np.float32)
+        qh, sh = quantize_per_token_runtime(h, in_dtype="fp32")
+        acc2 = int_matmul_nt(qh, np.ascontiguousarray(qw2[:, c * cs:(c + 1) * cs]))
+        y = ((acc2.astype(np.float32) * sh[:, None]).astype(np.float32) * s2c[None, :]).astype(np.float32)
+        out = (out + y).astype(np.float32)
+    return _to_out(out, out_dtype)
 
 
 def moe_fake(x, topk_ids, topk_w, gate_up_proj, down_proj):

@@ -224,3 +224,65 @@ def test_export_then_load_round_trip(tmp_path):
     deq = (iw * np.repeat(art.scale.float().cpu().numpy(), 128, 1)).astype(np.float16)
     ref = O.w4a16_linear(x.cpu().numpy(), deq, m.proj.bias.detach().cpu().numpy())
     assert _rel(m2.proj(x).float().cpu().numpy(), ref.astype(np.float32)) <= 1e-3
+
+
+# ------------------------------------------------------------------ add-RMSNorm fusion, dense MLP chain
+def _w8_layer(n, k, seed):
+    from mindpipe_amd.runtime import W8A8DynamicLinearMethod
+    w = torch.randn(n, k, generator=torch.Generator().manual_seed(seed)) * 0.02
+    q, s32, s16, _ = O.quantize_weight_per_channel_export(w.half().numpy())
+
+    class Layer(nn.Module):
+        pass
+
+    layer = Layer()
+    layer.weight = nn.Parameter(torch.from_numpy(q).to(DEV), requires_grad=False)
+    layer.weight_scale = nn.Parameter(torch.from_numpy(s16).reshape(-1, 1).to(DEV), requires_grad=False)
+    layer.quant_method = W8A8DynamicLinearMethod()
+    layer.quant_method.process_weights_after_loading(layer)
+    return layer, q, s16
+
+
+def test_add_rms_norm_forward_fused_equals_unfused():
+    _say("add_rms_norm_forward")
+    from mindpipe_amd.runtime import add_rms_norm_forward
+    h, t = 512, 6
+    layer, q, s16 = _w8_layer(384, h, seed=4)
+    norm = nn.Module()
+    norm.weight = nn.Parameter((torch.rand(h, generator=torch.Generator().manual_seed(2)) + 0.5).half().to(DEV),
+                               requires_grad=False)
+    norm.variance_epsilon = 1e-6
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(t, h, generator=g).half().to(DEV)
+    res = torch.randn(t, h, generator=g).half().to(DEV)
+    fused, rsum = add_rms_norm_forward(norm, x, res, layer)        # (int8, scale) tuple for a W8A8 linear
+    assert isinstance(fused, tuple) and fused[0].dtype == torch.int8
+    plain, rsum2 = add_rms_norm_forward(norm, x, res, None)        # normalised fp16 activations
+    assert plain.dtype == torch.float16 and torch.equal(rsum, rsum2)
+    assert torch.equal(rsum, (x.float() + res.float()).half())
+    # the W8A8 linear gives the same bits from the fused tuple and from the unfused activations
+    y_f = layer.quant_method.apply(layer, fused)
+    y_u = layer.quant_method.apply(layer, plain)
+    assert torch.equal(y_f, y_u)
+    yr, qr, sr, _ = O.add_rms_norm_quant(x.cpu().numpy(), res.cpu().numpy(), norm.weight.cpu().numpy(), 1e-6)
+    assert np.abs(plain.cpu().numpy().view(np.int16).astype(int) - yr.view(np.int16).astype(int)).max() <= 2
+
+
+@pytest.mark.parametrize("chunks,tuple_in", [(1, False), (2, False), (4, True)])
+def test_dense_mlp_w8a8_matches_oracle(chunks, tuple_in):
+    _say("dense mlp", chunks, tuple_in)
+    from mindpipe_amd.runtime import dense_mlp_w8a8, dynamic_quant, prepare_dense_mlp_w8a8
+    h, inter, t = 512, 768, 20
+    gate_up, q13, s13 = _w8_layer(2 * inter, h, seed=5)
+    down, q2, s2 = _w8_layer(h, inter, seed=6)
+    prepare_dense_mlp_w8a8(gate_up, down, chunks)
+    x = torch.randn(t, h, generator=torch.Generator().manual_seed(7)).half()
+    xin = dynamic_quant(x.to(DEV)) if tuple_in else x.to(DEV)
+    y = dense_mlp_w8a8(gate_up, down, xin)
+    assert y.shape == (t, h) and y.dtype == torch.float16
+    ref = O.dense_mlp_runtime(x.numpy(), q13, s13.astype(np.float32), q2, s2.astype(np.float32), chunks=chunks)
+    yn = y.cpu().numpy()
+    err = _rel(yn, ref)
+    assert err <= 1e-3, err   # bar: rel. Frobenius error <= 1e-3
+    # bit-identical except where silu's exp puts a requant code on a rounding boundary
+    assert np.mean(yn.view(np.uint16) == ref.view(np.uint16)) >= 0.99

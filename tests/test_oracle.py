@@ -248,3 +248,64 @@ def test_moe_runtime_matches_bruteforce_and_fake_path():
     yf = O.moe_fake(x, ids, w, wgu, wdn)
     rel = np.linalg.norm(y.astype(np.float32) - yf.astype(np.float32)) / np.linalg.norm(yf.astype(np.float32))
     assert rel < 0.05
+
+
+def test_add_rms_norm_closed_forms_and_invariants():
+    h = 64
+    w1 = np.ones(h, np.float16)
+    # constant rows: rstd = 1/|c| (eps negligible) -> y = sign(c); the codes are +-127
+    x = np.stack([np.full(h, 3.0), np.full(h, -0.25), np.full(h, 1024.0)]).astype(np.float16)
+    y, q, s, r = O.add_rms_norm_quant(x, None, w1, 1e-12)
+    assert r is None
+    assert y.tolist() == np.sign(x.astype(np.float32)).astype(np.float16).tolist()
+    assert (np.abs(q) == 127).all() and np.allclose(s, 1.0 / 127.0)
+    # +-a rows: rms = a, so y = +-1 * weight (weight a power of two keeps it exact)
+    xa = np.tile(np.array([2.0, -2.0], np.float16), (2, h // 2))
+    wp = np.full(h, 0.5, np.float16)
+    y2, _, _, _ = O.add_rms_norm_quant(xa, None, wp, 0.0, quant=False)
+    assert y2.tolist() == (np.sign(xa.astype(np.float32)) * 0.5).astype(np.float16).tolist()
+    # a mean over h (not h - 1): one non-zero entry v in h gives y = sqrt(h) at that place
+    xo = np.zeros((1, h), np.float16)
+    xo[0, 5] = 0.75
+    y3, _, _, _ = O.add_rms_norm_quant(xo, None, w1, 0.0, quant=False)
+    assert float(y3[0, 5]) == 8.0 and float(np.abs(y3).sum()) == 8.0
+    # scale invariance: x and 4x normalise to the same y (eps 0)
+    g = np.random.default_rng(3)
+    xr = (g.standard_normal((5, h)) * 0.7).astype(np.float16)
+    wr = (g.standard_normal(h) * 0.5 + 1).astype(np.float16)
+    ya, _, _, _ = O.add_rms_norm_quant(xr, None, wr, 0.0, quant=False)
+    yb, _, _, _ = O.add_rms_norm_quant((xr.astype(np.float32) * 4).astype(np.float16), None, wr, 0.0, quant=False)
+    assert ya.tolist() == yb.tolist()
+    # residual identity: exact sums (multiples of 1/64 in a small range)
+    xi = (g.integers(-64, 64, (3, h)) / 64).astype(np.float16)
+    ri = (g.integers(-64, 64, (3, h)) / 64).astype(np.float16)
+    yc, qc, sc, rc = O.add_rms_norm_quant(xi, ri, wr, 1e-6)
+    yd, qd, sd, _ = O.add_rms_norm_quant((xi.astype(np.float32) + ri).astype(np.float16), None, wr, 1e-6)
+    assert rc.tolist() == (xi.astype(np.float32) + ri).astype(np.float16).tolist()
+    assert yc.tolist() == yd.tolist() and qc.tolist() == qd.tolist() and sc.tolist() == sd.tolist()
+    # q / s are the per-token runtime quant of y
+    q2, s2 = O.quantize_per_token_runtime(yc)
+    assert q2.tolist() == qc.tolist() and s2.tolist() == sc.tolist()
+
+
+def test_dense_mlp_single_chunk_equals_one_expert_moe():
+    g = np.random.default_rng(11)
+    t, h, inter = 6, 64, 32
+    x = (g.standard_normal((t, h))).astype(np.float16)
+    qw13 = g.integers(-127, 128, (2 * inter, h)).astype(np.int8)
+    qw2 = g.integers(-127, 128, (h, inter)).astype(np.int8)
+    s13 = (g.random(2 * inter) * 0.01 + 1e-3).astype(np.float32)
+    s2 = (g.random(h) * 0.01 + 1e-3).astype(np.float32)
+    y1 = O.dense_mlp_runtime(x, qw13, s13, qw2, s2, chunks=1)
+    ym = O.moe_runtime(x, np.zeros((t, 1), np.int32), np.ones((t, 1), np.float32), qw13[None], s13[None], qw2[None],
+                       s2[None])
+    assert y1.tobytes() == ym.tobytes()
+    # chunks split the intermediate dimension: every chunk alone is a one-chunk MLP on its slice
+    cs = inter // 2
+    parts = []
+    for c in range(2):
+        rows = np.r_[c * cs:(c + 1) * cs, inter + c * cs:inter + (c + 1) * cs]
+        parts.append(O.dense_mlp_runtime(x, qw13[rows], s13[rows], np.ascontiguousarray(qw2[:, c * cs:(c + 1) * cs]),
+                                         O.bf16_bits_to_f32(O.f32_to_bf16_bits(s2)), chunks=1, out_dtype="fp32"))
+    y2 = O.dense_mlp_runtime(x, qw13, s13, qw2, s2, chunks=2, out_dtype="fp32")
+    assert y2.tobytes() == (np.float32(0) + parts[0] + parts[1]).astype(np.float32).tobytes()
