@@ -234,11 +234,11 @@ def leg_decoder(cfg_name, batches, prompt, gen_tokens, prefill_batch=1):
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / gen_tokens
-        avg_len = prompt + gen_tokens / 2
-        step_bytes = wbytes + b * max_len * cfg.layers * kv_per_tok_layer  # masked attention reads the full cache
-        alg_bytes = wbytes + b * avg_len * cfg.layers * kv_per_tok_layer
+        avg_len = prompt + (gen_tokens + 1) / 2       # positions [0, pos] read by the attention kernel
+        kv_bytes = b * avg_len * cfg.layers * kv_per_tok_layer
+        alg_bytes = wbytes + kv_bytes
         out["decode"][str(b)] = {"ms_per_step": ms, "tok_s": b / (ms * 1e-3), "weight_bytes": wbytes,
-                                 "kv_bytes_per_step_read": step_bytes - wbytes,
+                                 "kv_bytes_per_step_read": kv_bytes,
                                  "roofline": _roof("hbm", alg_bytes / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s")}
         del graph, model
         torch.cuda.empty_cache()

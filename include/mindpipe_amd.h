@@ -180,6 +180,34 @@ int mp_moe_unpermute_combine(const float *y, const int32_t *row_of_slot, const f
                              int64_t t, int top_k, int64_t h, void *out, int out_dtype,
                              mp_stream_t stream);
 
+/* ---------------------------------------------------------------- decode-step harness kernels
+ * No counterpart in the reference (attention, RoPE and the MLP activation belong
+ * to vLLM's model code); they let the Llama-shaped measurement harness run one
+ * greedy decode step in ~10 launches per layer around the W4A16 GEMVs.  Head dim
+ * 128; KV cache per layer K, V [B, kvh, capacity, 128] fp16; *pos is the position
+ * of the new token (device memory, so launches are graph-capturable). */
+
+/* RoPE (interleaved pairs, fp16 rounding after every op) on the q and k heads of
+ * qkv [B, (nh + 2 kvh) * 128]; writes q_out [B, nh, 128] and the k, v rows of
+ * position *pos into the caches.  cos_t / sin_t: fp16 [capacity, 64].  A position
+ * outside [0, capacity) writes nothing. */
+int mp_decode_rope_append(const void *qkv, int64_t batch, int nh, int kvh, int head_dim, const void *cos_t,
+                          const void *sin_t, const int64_t *pos, int64_t capacity, void *q_out, void *k_cache,
+                          void *v_cache, mp_stream_t stream);
+
+/* Split-K decode attention (flash decoding) over positions [0, *pos] of one
+ * layer's cache: out [B, nh, 128] fp16 = softmax(q k^T * scale) v, fp32 inside;
+ * nh / kvh in {1, 2, 4, 8}.  splits workgroups per (row, kv head), each over
+ * ceil(capacity / splits) positions; workspace of
+ * mp_decode_attention_workspace_bytes(batch, nh, splits). */
+size_t mp_decode_attention_workspace_bytes(int64_t batch, int nh, int splits);
+int mp_decode_attention(const void *q, int64_t batch, int nh, int kvh, int head_dim, const void *k_cache,
+                        const void *v_cache, const int64_t *pos, int64_t capacity, int splits, float scale,
+                        void *out, void *workspace, size_t workspace_bytes, mp_stream_t stream);
+
+/* act [rows, I] = round(round(silu(gate)) * up) of gate_up [rows, 2I] (gate | up), fp16. */
+int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, mp_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

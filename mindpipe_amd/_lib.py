@@ -27,6 +27,11 @@ SIGNATURES = {
     "mp_w4a16_gemm": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp]),
     "mp_quant_per_token_i8": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _i32, _vp]),
     "mp_add_rms_norm_quant": (_i32, [_vp, _vp, _vp, C.c_float, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "mp_decode_rope_append": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "mp_decode_attention_workspace_bytes": (_sz, [_i64, _i32, _i32]),
+    "mp_decode_attention": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _i32, C.c_float, _vp, _vp, _sz,
+                                   _vp]),
+    "mp_silu_mul": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "mp_w8_quantize_per_channel": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "mp_w8a8_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp]),
     "mp_moe_route_workspace_bytes": (_sz, [_i64, _i64, _i32]),

@@ -5,10 +5,15 @@ workloads: Llama-2-7B (32 layers, hidden 4096, 32 heads, FFN 11008, vocab 32000)
 and Llama-3-70B (80 layers, hidden 8192, 64 q / 8 kv heads, FFN 28672, vocab 128256).
 Weights are random W4 g128 codes with fp16 scales / zeros (a random init of the
 quantized model; no checkpoint is loaded).  q/k/v and gate/up are fused into one
-W4A16 GEMM each (row concatenation of the packed weight is exact).  Attention,
-RMSNorm, RoPE and SwiGLU use PyTorch ops; the KV cache has a fixed capacity and
-attention is masked by the current length, so one decode step is shape-static and
-can be captured into a HIP graph.
+W4A16 GEMM each (row concatenation of the packed weight is exact).
+
+``decode_step`` runs one greedy step as ~10 launches per layer: fused residual-add
++ RMSNorm, the W4A16 GEMVs, RoPE + KV append, split-K decode attention, SiLU-mul.
+The KV cache has a fixed capacity ``[L, B, kvh, T, 128]`` and every kernel reads
+the current position from device memory, so a step is shape-static and can be
+captured into a HIP graph.  ``decode_step_torch`` is the same step in PyTorch ops
+(masked attention over the whole cache), kept as the numerical reference.  Prefill
+uses PyTorch attention (SDPA) around the same W4A16 linears.
 """
 from __future__ import annotations
 
@@ -86,9 +91,10 @@ class W4Decoder:
             })
         self.norm = torch.ones(h, device=device, dtype=torch.float16)
         self.lm_head = _W4(cfg.vocab, h, cfg.group, gen, device)
-        # KV cache: K stored [L, B, kvh, hd, T] (keys already transposed for q @ K), V [L, B, kvh, T, hd]
-        self.k_cache = torch.zeros(cfg.layers, max_batch, kvh, hd, max_len, device=device, dtype=torch.float16)
+        # KV cache [L, B, kvh, T, hd]: one 256-byte row per position
+        self.k_cache = torch.zeros(cfg.layers, max_batch, kvh, max_len, hd, device=device, dtype=torch.float16)
         self.v_cache = torch.zeros(cfg.layers, max_batch, kvh, max_len, hd, device=device, dtype=torch.float16)
+        self.attn_ws = {}
         inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, hd, 2, device=device).float() / hd))
         t = torch.arange(max_len, device=device).float()
         freqs = torch.outer(t, inv)
@@ -121,7 +127,7 @@ class W4Decoder:
             qkv = l["qkv"](hn.reshape(b * t, -1)).reshape(b, t, nh + 2 * kvh, hd).transpose(1, 2)
             q, k, v = qkv[:, :nh], qkv[:, nh:nh + kvh], qkv[:, nh + kvh:]
             q, k = self._rope(q, pos), self._rope(k, pos)
-            self.k_cache[li, :b, :, :, :t] = k.transpose(-1, -2)
+            self.k_cache[li, :b, :, :t] = k
             self.v_cache[li, :b, :, :t] = v
             kk = k.repeat_interleave(nh // kvh, dim=1) if kvh != nh else k
             vv = v.repeat_interleave(nh // kvh, dim=1) if kvh != nh else v
@@ -135,33 +141,78 @@ class W4Decoder:
         logits = self.lm_head(_rms(x[:, -1], self.norm, cfg.eps).contiguous())
         return logits.argmax(-1)
 
+    def attn_splits(self, b):
+        """Workgroups per (row, kv head) for the decode attention: ~1024 in all, and a score
+        buffer of at most 64 KB per workgroup."""
+        cfg = self.cfg
+        grp = cfg.heads // cfg.kv_heads
+        splits = max(1, min(64, 1024 // (b * cfg.kv_heads)))
+        while -(-self.max_len // splits) * grp * 4 > 64 * 1024:
+            splits += 1
+        return splits
+
+    def _attn_workspace(self, b):
+        splits = self.attn_splits(b)
+        key = (b, splits)
+        if key not in self.attn_ws:
+            self.attn_ws[key] = ops.decode_attention_workspace(b, self.cfg.heads, splits, self.k_cache.device)
+        return splits, self.attn_ws[key]
+
     @torch.no_grad()
-    def decode_step(self, tokens, cur_len):
-        """One greedy step for a batch.  tokens [B] int64 (the last token), cur_len [1]
-        int64 device tensor = position of that token; writes its K/V and returns the next ids."""
+    def decode_step(self, tokens, cur_len, return_logits=False):
+        """One greedy step for a batch on the fused kernels.  tokens [B] int64 (the last
+        token), cur_len [1] int64 device tensor = position of that token; writes its K/V
+        and returns the next ids (or the logits)."""
+        cfg = self.cfg
+        b = tokens.shape[0]
+        hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
+        splits, ws = self._attn_workspace(b)
+        scale = 1.0 / math.sqrt(hd)
+        x = self.embed[tokens]                                    # [B, H] residual stream
+        delta = None
+        for li, l in enumerate(self.layers):
+            if delta is None:
+                hn = ops.add_rms_norm_quant(x, None, l["ln1"], cfg.eps, quant=False)[0]
+            else:
+                hn, _, _, x = ops.add_rms_norm_quant(delta, x, l["ln1"], cfg.eps, quant=False)
+            qkv = l["qkv"](hn)
+            q = ops.decode_rope_append(qkv, nh, kvh, self.cos, self.sin, cur_len, self.k_cache[li, :b],
+                                       self.v_cache[li, :b])
+            att = ops.decode_attention(q, self.k_cache[li, :b], self.v_cache[li, :b], cur_len, splits, scale, ws)
+            hn, _, _, x = ops.add_rms_norm_quant(l["o"](att.reshape(b, nh * hd)), x, l["ln2"], cfg.eps, quant=False)
+            delta = l["down"](ops.silu_mul(l["gate_up"](hn)))
+        hn, _, _, x = ops.add_rms_norm_quant(delta, x, self.norm, cfg.eps, quant=False)
+        logits = self.lm_head(hn)
+        return logits if return_logits else logits.argmax(-1)
+
+    @torch.no_grad()
+    def decode_step_torch(self, tokens, cur_len, return_logits=False):
+        """The decode step in PyTorch ops (reference path): RMSNorm on the rounded residual,
+        fp32 attention over the whole cache masked by the current length."""
         cfg = self.cfg
         b = tokens.shape[0]
         hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
         grp = nh // kvh
         x = self.embed[tokens]                                    # [B, H]
         pos = cur_len.expand(b).unsqueeze(1)                      # [B, 1]
-        mask = (torch.arange(self.max_len, device=tokens.device) > cur_len).to(torch.float16) * -60000.0
+        mask = torch.where(torch.arange(self.max_len, device=tokens.device) > cur_len, float("-inf"), 0.0)
         scale = 1.0 / math.sqrt(hd)
         for li, l in enumerate(self.layers):
             hn = _rms(x, l["ln1"], cfg.eps)
             qkv = l["qkv"](hn).reshape(b, nh + 2 * kvh, 1, hd)
             q, k, v = qkv[:, :nh], qkv[:, nh:nh + kvh], qkv[:, nh + kvh:]
             q, k = self._rope(q, pos), self._rope(k, pos)
-            self.k_cache[li, :b].index_copy_(3, cur_len, k.transpose(-1, -2).contiguous())
+            self.k_cache[li, :b].index_copy_(2, cur_len, k.contiguous())
             self.v_cache[li, :b].index_copy_(2, cur_len, v.contiguous())
-            qg = q.reshape(b, kvh, grp, hd)                        # heads grouped by kv head
-            s = torch.matmul(qg, self.k_cache[li, :b]) * scale     # [B, kvh, grp, T]
-            p = torch.softmax((s + mask).float(), dim=-1).half()
-            att = torch.matmul(p, self.v_cache[li, :b])            # [B, kvh, grp, hd]
+            qg = q.reshape(b, kvh, grp, hd).float()                # heads grouped by kv head
+            kt = self.k_cache[li, :b].float().transpose(-1, -2).contiguous()
+            s = torch.matmul(qg, kt) * scale + mask                # [B, kvh, grp, T]
+            p = torch.softmax(s, dim=-1)
+            att = torch.matmul(p, self.v_cache[li, :b].float()).half()
             x = x + l["o"](att.reshape(b, nh * hd))
             hn = _rms(x, l["ln2"], cfg.eps)
             gu = l["gate_up"](hn)
             act = torch.nn.functional.silu(gu[:, :cfg.ffn]) * gu[:, cfg.ffn:]
             x = x + l["down"](act.contiguous())
         logits = self.lm_head(_rms(x, self.norm, cfg.eps).contiguous())
-        return logits.argmax(-1)
+        return logits if return_logits else logits.argmax(-1)

@@ -357,3 +357,52 @@ def moe_w8a8_forward(x, topk_ids, topk_w, w13, s13, w2, s2, out_dtype=None):
     y = moe_gmm2(q, s, w2, s2, offsets)
     return moe_unpermute_combine(y, row_of_slot, topk_w.to(torch.float32).contiguous(),
                                  out_dtype or x.dtype)
+
+
+# ---------------------------------------------------------------- decode-step harness kernels
+def decode_rope_append(qkv: torch.Tensor, nh: int, kvh: int, cos_t: torch.Tensor, sin_t: torch.Tensor,
+                       pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """RoPE on q/k of ``qkv [B, (nh+2kvh)*128]`` and append k/v at ``pos`` (int64 device scalar)
+    into ``k_cache``/``v_cache [B, kvh, T, 128]``; returns rotated ``q [B, nh, 128]``."""
+    b = qkv.shape[0]
+    cap = k_cache.shape[2]
+    if q_out is None:
+        q_out = torch.empty((b, nh, 128), dtype=torch.float16, device=qkv.device)
+    with _dev(qkv):
+        _lib.check(_lib.load().mp_decode_rope_append(
+            qkv.data_ptr(), b, nh, kvh, 128, cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(), cap,
+            q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), _stream()), "mp_decode_rope_append")
+    return q_out
+
+
+def decode_attention_workspace(batch: int, nh: int, splits: int, device) -> torch.Tensor:
+    nbytes = _lib.load().mp_decode_attention_workspace_bytes(batch, nh, splits)
+    return torch.empty((nbytes // 4,), dtype=torch.float32, device=device)
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor, splits: int,
+                     scale: float, workspace: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention of ``q [B, nh, 128]`` over cache positions ``[0, pos]``: ``[B, nh, 128]`` fp16."""
+    b, nh, hd = q.shape
+    kvh, cap = k_cache.shape[1], k_cache.shape[2]
+    if out is None:
+        out = torch.empty_like(q)
+    with _dev(q):
+        _lib.check(_lib.load().mp_decode_attention(
+            q.data_ptr(), b, nh, kvh, hd, k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr(), cap, splits,
+            float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * 4, _stream()),
+            "mp_decode_attention")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``round(round(silu(gate)) * up)`` of ``gate_up [B, 2I]`` (gate | up), fp16."""
+    _need(gate_up, "gate_up", torch.float16, 2)
+    rows, two_i = gate_up.shape
+    if out is None:
+        out = torch.empty((rows, two_i // 2), dtype=torch.float16, device=gate_up.device)
+    with _dev(gate_up):
+        _lib.check(_lib.load().mp_silu_mul(gate_up.data_ptr(), rows, two_i // 2, out.data_ptr(), _stream()),
+                   "mp_silu_mul")
+    return out
