@@ -377,14 +377,19 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
 // ------------------------------------------------------------------ large-M dense GEMM
 // 256 x 256 output tile per workgroup of 8 waves (2 along M x 4 along N), each
 // wave 128 x 64 = 4 x 2 MFMA i32_32x32x32_i8 tiles (128 accumulator registers,
-// so two waves fit per SIMD).  BK = 64, LDS double buffer (row pitch 80 B:
-// conflict-free ds_read_b128 fragments) and two register stages: K tile kt+2
-// is in flight while tile kt is multiplied and tile kt+1 is written to the
-// other LDS buffer; the LDS-only barrier leaves those loads outstanding.
+// so two waves fit per SIMD; the 32x32x32 form runs at twice the rate of
+// 16x16x64 on gfx950).  BK = 64, LDS double buffer and two register stages: K
+// tile kt+2 is in flight while tile kt is multiplied and tile kt+1 is written to
+// the other LDS buffer; the LDS-only barrier leaves those loads outstanding.
+// Within a step the LDS traffic is interleaved into the MFMA stream (see step()).
 // Tiles are assigned XCD-major: the workgroups the dispatcher places on one
 // XCD (id % 8) take a contiguous run of tiles, ordered in 4-row-tile bands, so
 // concurrent tiles share A and B rows in that XCD's L2.
-constexpr int kBigBM = 256, kBigBN = 256, kBigBK = 64, kBigLD = kBigBK + 16, kBigThreads = 512;
+// LDS tiles: 64-byte rows, the 16-byte chunk c of row r stored at slot
+// c ^ ((r >> 2) & 3).  Both access patterns are bank-conflict free: a store
+// covers 4 rows x 4 chunks per 16 lanes (rows 4q..4q+3 land on the four 16-bank
+// quarters), a fragment read 16 rows of one chunk (16 distinct 4-bank groups).
+constexpr int kBigBM = 256, kBigBN = 256, kBigBK = 64, kBigLD = kBigBK, kBigThreads = 512;
 
 __device__ __forceinline__ void big_tile_coords(int id, int tiles_m, int tiles_n, int &tm, int &tn) {
   const int total = tiles_m * tiles_n;
@@ -396,6 +401,110 @@ __device__ __forceinline__ void big_tile_coords(int id, int tiles_m, int tiles_n
   const int rows_in_band = (tiles_m - band * 4) < 4 ? (tiles_m - band * 4) : 4;
   tm = band * 4 + inb % rows_in_band;
   tn = inb / rows_in_band;
+}
+
+// Epilogue of the large-M kernels for one wave's TM x TN grid of 32x32 int32
+// accumulators: element r of tile (i, j) is row mbase + 32 i + 8 (r >> 2) + (r & 3)
+// (mbase includes 4 (lane >> 5)), column nbase + 32 j + lane % 32.
+// y = (acc * s_tok[m]) * s_ch[n] (+ bias[n]) in OUT_DT.  In a full-row tile the
+// lane's per-token scales come in runs of 4 rows and are read once as float4;
+// only the column guard (one per j) remains.  A partial tile clamps every row.
+template <int OUT_DT, int TM, int TN>
+__device__ __forceinline__ void big_epilogue(const mp_i8_args &p, const i16_t (&acc)[TM][TN], int64_t mbase,
+                                             int64_t nbase, bool full_rows, int lane) {
+  const bool has_bias = p.bias != nullptr;
+  float sbv[TN], bv[TN];
+  bool cval[TN];
+  int64_t colv[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t col = nbase + j * 32 + (lane & 31);
+    cval[j] = col < p.n;
+    colv[j] = col;
+    const int64_t colc = cval[j] ? col : p.n - 1;
+    sbv[j] = p.s_b[colc];
+    bv[j] = has_bias ? mp_load_as_f32(p.bias, colc, p.bias_dtype) : 0.f;
+  }
+  auto put = [&](int64_t m, int j, float v) {
+    if (OUT_DT == MP_F16) static_cast<uint16_t *>(p.y)[m * p.ldy + colv[j]] = mp_f2h(v);
+    else if (OUT_DT == MP_BF16) static_cast<uint16_t *>(p.y)[m * p.ldy + colv[j]] = mp_f2bf(v);
+    else static_cast<float *>(p.y)[m * p.ldy + colv[j]] = v;
+  };
+  const bool vec_sa = (reinterpret_cast<uintptr_t>(p.s_a) & 15) == 0;
+  // 16-bit outputs, even N / row stride: lanes (2c, 2c+1) swap halves so each stores
+  // two adjacent columns of two rows as 32-bit words (half the store instructions)
+  if (OUT_DT != MP_F32 && full_rows && vec_sa && (p.n & 1) == 0 && (p.ldy & 1) == 0 &&
+      (reinterpret_cast<uintptr_t>(p.y) & 3) == 0) {
+    const bool odd = lane & 1;
+    // perm(recv, mine): bytes 0-3 = mine, 4-7 = recv.  Even lane: [own | partner] of
+    // rows e0 / e1; odd lane: [partner | own] of rows e2 / e3 (columns 2c, 2c+1)
+    const uint32_t sel_lo = odd ? 0x01000504u : 0x05040100u;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float4 s4[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) s4[g] = *reinterpret_cast<const float4 *>(p.s_a + mbase + i * 32 + 8 * g);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if (!cval[j]) continue;  // the pair partner has the same guard (N even)
+        uint32_t *yw = reinterpret_cast<uint32_t *>(static_cast<uint16_t *>(p.y) + (colv[j] & ~int64_t(1)));
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float sv[4] = {s4[g].x, s4[g].y, s4[g].z, s4[g].w};
+          uint32_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][4 * g + e]), sv[e]), sbv[j]);
+            v = has_bias ? mp_add(v, bv[j]) : v;
+            h[e] = OUT_DT == MP_F16 ? mp_f2h(v) : mp_f2bf(v);
+          }
+          const uint32_t p01 = h[0] | (h[1] << 16), p23 = h[2] | (h[3] << 16);
+          // even lane keeps rows e0, e1 and takes the partner's; odd lane rows e2, e3
+          const uint32_t recv = __shfl_xor(odd ? p01 : p23, 1, 64);
+          const uint32_t mine = odd ? p23 : p01;
+          const uint32_t w0 = __builtin_amdgcn_perm(recv, mine, sel_lo);
+          const uint32_t w1 = __builtin_amdgcn_perm(recv, mine, sel_lo + 0x02020202u);
+          const int64_t m = mbase + i * 32 + 8 * g + (odd ? 2 : 0);
+          yw[(m * p.ldy) >> 1] = w0;
+          yw[((m + 1) * p.ldy) >> 1] = w1;
+        }
+      }
+    }
+    return;
+  }
+  if (full_rows && vec_sa) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float4 s4[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) s4[g] = *reinterpret_cast<const float4 *>(p.s_a + mbase + i * 32 + 8 * g);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if (!cval[j]) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float4 q = s4[r >> 2];
+          const float sa = (r & 3) == 0 ? q.x : ((r & 3) == 1 ? q.y : ((r & 3) == 2 ? q.z : q.w));
+          float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), sa), sbv[j]);
+          v = has_bias ? mp_add(v, bv[j]) : v;
+          put(mbase + i * 32 + 8 * (r >> 2) + (r & 3), j, v);
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = mbase + i * 32 + 8 * (r >> 2) + (r & 3);
+        const int64_t mc = m < p.rows ? m : p.rows - 1;
+        float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), p.s_a[mc]), sbv[j]);
+        v = has_bias ? mp_add(v, bv[j]) : v;
+        if (cval[j] && m < p.rows) put(m, j, v);
+      }
 }
 
 template <int OUT_DT>
@@ -418,6 +527,7 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
   // pass i of this thread covers tile row (tid / CPR + i * RPP), bytes (tid % CPR) * 16
   // of the K step; rows past the matrix are clamped (computed, never stored)
   const int rloc = tid / CPR, cloc = (tid % CPR) * 16;
+  const int cst = ((tid % CPR) ^ ((rloc >> 2) & 3)) * 16;  // swizzled slot (RPP % 16 == 0)
   int aoff[CA], boff[CB];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
@@ -444,10 +554,10 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
   auto store_tile = [&](const i4_t *r, int buf) {
 #pragma unroll
     for (int i = 0; i < CA; ++i)
-      *reinterpret_cast<i4_t *>(&sa[buf * BM * LD + (rloc + i * RPP) * LD + cloc]) = r[i];
+      *reinterpret_cast<i4_t *>(&sa[buf * BM * LD + (rloc + i * RPP) * LD + cst]) = r[i];
 #pragma unroll
     for (int i = 0; i < CB; ++i)
-      *reinterpret_cast<i4_t *>(&sb[buf * BN * LD + (rloc + i * RPP) * LD + cloc]) = r[CA + i];
+      *reinterpret_cast<i4_t *>(&sb[buf * BN * LD + (rloc + i * RPP) * LD + cst]) = r[CA + i];
   };
 
   i16_t acc[TM][TN];
@@ -457,25 +567,50 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-  const int arow = (wm * 128 + (lane & 31)) * LD + 16 * (lane >> 5);
-  const int brow = (wn * 64 + (lane & 31)) * LD + 16 * (lane >> 5);
-  auto compute = [&](int buf) {
+  const int rsw = 16 * ((lane >> 5) ^ ((lane >> 2) & 3));  // chunk (lane >> 5) of row lane & 31, swizzled
+  const int arow = (wm * 128 + (lane & 31)) * LD + rsw;
+  const int brow = (wn * 64 + (lane & 31)) * LD + rsw;
+  // One K step with the LDS traffic interleaved into the MFMA stream: the
+  // fragments of the second K32 half are read between the first half's MFMAs,
+  // the staged next tile is written to the other buffer between the second
+  // half's MFMAs, and the global loads of the tile after it go out first.
+  auto step = [&](int buf, const i4_t *st, int nbuf, i4_t *ld, int64_t kt_ld) {
     const int8_t *ca = sa + buf * BM * LD;
     const int8_t *cbp = sb + buf * BN * LD;
+    i4_t af[2][TM], bf[2][TN];
 #pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      i4_t af[TM], bf[TN];
+    for (int i = 0; i < TM; ++i) af[0][i] = *reinterpret_cast<const i4_t *>(ca + arow + i * 32 * LD);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i4_t *>(ca + arow + i * 32 * LD + ks * 32);
+    for (int j = 0; j < TN; ++j) bf[0][j] = *reinterpret_cast<const i4_t *>(cbp + brow + j * 32 * LD);
+    load_tile(ld, kt_ld);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const i4_t *>(cbp + brow + j * 32 * LD + ks * 32);
+    for (int i = 0; i < TM; ++i) af[1][i] = *reinterpret_cast<const i4_t *>(ca + (arow ^ 32) + i * 32 * LD);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+    for (int j = 0; j < TN; ++j) bf[1][j] = *reinterpret_cast<const i4_t *>(cbp + (brow ^ 32) + j * 32 * LD);
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);  // one K32 step of fragments live at a time
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0][i], bf[0][j], acc[i][j], 0, 0, 0);
+    store_tile(st, nbuf);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[1][i], bf[1][j], acc[i][j], 0, 0, 0);
+    // schedule: 6 reads, 4 global loads, then MFMA/read pairs, then MFMA/write pairs
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);
+    for (int r = 0; r < 6; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    for (int r = 0; r < 4; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
 
   // K is a multiple of 2 * BK (host check): the loop body is branch-free; the two
@@ -487,44 +622,117 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
   store_tile(ra, 0);
   mp_lds_barrier();
   for (int64_t kt = 0; kt < nkt; kt += 2) {
-    load_tile(ra, kt + 2 < nkt ? kt + 2 : nkt - 1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(0);
-    store_tile(rb, 1);
+    step(0, rb, 1, ra, kt + 2 < nkt ? kt + 2 : nkt - 1);
     mp_lds_barrier();
-    load_tile(rb, kt + 3 < nkt ? kt + 3 : nkt - 1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(1);
-    store_tile(ra, 0);
+    step(1, ra, 0, rb, kt + 3 < nkt ? kt + 3 : nkt - 1);
     mp_lds_barrier();
   }
 
-  // epilogue: (acc * s_tok) * s_ch (+ bias) -> OUT_DT; full tiles skip the row guard
-  const bool full_rows = m0 + BM <= p.rows;
-  const int64_t mbase = m0 + wm * 128 + 4 * (lane >> 5);
-  const bool has_bias = p.bias != nullptr;
+  // epilogue: (acc * s_tok) * s_ch (+ bias) -> OUT_DT
+  big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
+}
+
+// Large-M GEMM with direct global->LDS loads (global_load_lds_dwordx4): 256x256
+// tile, 8 waves of 128x64, 64-wide K steps, four LDS stages of 32 KB.  Tile kt+3
+// is loaded straight into stage (kt+3) % 4 while tile kt is computed, so three
+// tiles (96 KB per CU) are in flight without staging registers or LDS write
+// instructions.  Each load instruction fills 1 KB of LDS (16 rows x 64 B, lane l
+// at byte 16 l); a lane fetches the global chunk that the swizzled layout (chunk c
+// of row r at slot c ^ ((r >> 2) & 3)) puts at its slot.  One barrier per step:
+// after it every wave's loads of tile kt are complete and every read of stage
+// (kt+3) % 4 from step kt-1 is done.
+constexpr int kDmaStages = 4;
+
+template <int OUT_DT>
+__global__ __launch_bounds__(512) void i8_gemm_dma_kernel(mp_i8_args p, int tiles_m, int tiles_n) {
+  constexpr int BM = 256, BN = 256, BK = 64, LD = 64, TM = 4, TN = 2, S = kDmaStages;
+  constexpr int STAGE = (BM + BN) * LD;  // bytes per stage (A rows then B rows)
+  extern __shared__ __attribute__((aligned(16))) int8_t smem_dma[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  int tm, tn;
+  big_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const int64_t k = p.k;
+
+  // load instruction q (0..3) of this wave fills 16 rows: q < 2 -> A rows
+  // (2 wave + q) * 16, else B rows (2 wave + q - 2) * 16.  Lane l: row + l / 4,
+  // slot l % 4, global chunk slot ^ ((row >> 2) & 3).
+  const int8_t *gsrc[4];
+  int ldst[4];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
-    const bool cval = col < p.n;
-    const int64_t colc = cval ? col : p.n - 1;
-    const float sbv = p.s_b[colc];
-    const float bv = has_bias ? mp_load_as_f32(p.bias, colc, p.bias_dtype) : 0.f;
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = mbase + i * 32 + 8 * (r >> 2) + (r & 3);
-        const int64_t mc = (full_rows || m < p.rows) ? m : p.rows - 1;
-        float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), p.s_a[mc]), sbv);
-        v = has_bias ? mp_add(v, bv) : v;
-        if (cval && (full_rows || m < p.rows)) {
-          if (OUT_DT == MP_F16) static_cast<uint16_t *>(p.y)[m * p.ldy + col] = mp_f2h(v);
-          else if (OUT_DT == MP_BF16) static_cast<uint16_t *>(p.y)[m * p.ldy + col] = mp_f2bf(v);
-          else static_cast<float *>(p.y)[m * p.ldy + col] = v;
-        }
-      }
+  for (int q = 0; q < 4; ++q) {
+    const bool is_a = q < 2;
+    const int r0 = (2 * wave + (q & 1)) * 16;
+    const int r = r0 + lane / 4;
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    int64_t g = (is_a ? m0 : n0) + r;
+    const int64_t lim = is_a ? p.rows : p.n;
+    g = g < lim ? g : lim - 1;
+    gsrc[q] = (is_a ? p.a : p.b) + g * k + 16 * c;
+    ldst[q] = (is_a ? 0 : BM * LD) + r0 * LD;
   }
+  auto issue = [&](int64_t kt, int stage) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_global_load_lds(gsrc[q] + kt * BK, smem_dma + stage * STAGE + ldst[q], 16, 0, 0);
+  };
+
+  i16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  const int rsw = 16 * ((lane >> 5) ^ ((lane >> 2) & 3));
+  const int arow = (wm * 128 + (lane & 31)) * LD + rsw;
+  const int brow = BM * LD + (wn * 64 + (lane & 31)) * LD + rsw;
+  auto compute = [&](int stage) {
+    const int8_t *st = smem_dma + stage * STAGE;
+    i4_t af[2][TM], bf[2][TN];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[ks][i] = *reinterpret_cast<const i4_t *>(st + (arow ^ (ks * 32)) + i * 32 * LD);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(st + (brow ^ (ks * 32)) + j * 32 * LD);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+    for (int r = 0; r < 6; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);
+  };
+
+  const int64_t nkt = k / BK;
+  auto kc = [&](int64_t t) { return t < nkt ? t : nkt - 1; };
+  issue(0, 0);
+  issue(kc(1), 1);
+  issue(kc(2), 2);
+  // step kt: own loads of tile kt done (8 newer load instructions may remain), barrier,
+  // refill the stage read in step kt-1, compute
+  for (int64_t kt = 0; kt < nkt; kt += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      // own loads of tile kt landed (vmcnt) and own reads of the stage refilled next are
+      // done (lgkmcnt) before the barrier
+      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      issue(kc(kt + u + 3), (u + 3) % S);
+      compute(u);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS DMA outstanding at exit
+
+  big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
 }
 
 // Any-shape dense fallback: one thread per output.
@@ -543,6 +751,16 @@ __global__ void i8_simple_kernel(mp_i8_args p) {
 constexpr int kTBM = 128, kTBN = 128, kTBK = 64;
 
 }  // namespace
+
+// Large-M kernel variant: 4 (4 waves of 128x128) or 8 (8 waves of 128x64);
+// MP_W8_BIG_VARIANT overrides the default, for measurements.
+static int mp_big_variant() {
+  static int v = [] {
+    const char *e = getenv("MP_W8_BIG_VARIANT");
+    return e ? atoi(e) : 4;
+  }();
+  return v;
+}
 
 // Shared launcher (dense + grouped).
 int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
@@ -585,21 +803,39 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
   } else if (a.rows >= 1024 && a.k % (2 * kBigBK) == 0 && aligned && epilogue == MP_EPI_DENSE) {
     const int tiles_m = static_cast<int>(mp_cdiv(a.rows, kBigBM));
     const int tiles_n = static_cast<int>(mp_cdiv(a.n, kBigBN));
-    const size_t smem = static_cast<size_t>(2) * (kBigBM + kBigBN) * kBigLD;
-    const void *fn = a.out_dtype == MP_F16    ? reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F16>)
-                     : a.out_dtype == MP_BF16 ? reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_BF16>)
-                                              : reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F32>);
-    // > 64 KB of dynamic LDS must be allowed per kernel (idempotent, cheap)
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) != hipSuccess)
-      return MP_ERR_HIP;
     const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
-    const dim3 block(kBigThreads);
-    if (a.out_dtype == MP_F16)
-      hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F16>, grid, block, smem, stream, a, tiles_m, tiles_n);
-    else if (a.out_dtype == MP_BF16)
-      hipLaunchKernelGGL(i8_gemm_big_kernel<MP_BF16>, grid, block, smem, stream, a, tiles_m, tiles_n);
-    else
-      hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F32>, grid, block, smem, stream, a, tiles_m, tiles_n);
+    if (mp_big_variant() == 11 && a.k % (kDmaStages * kBigBK) == 0) {
+      const size_t smemd = static_cast<size_t>(kDmaStages) * (kBigBM + kBigBN) * kBigBK;
+      const void *fk[3] = {reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_F16>),
+                           reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_BF16>),
+                           reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_F32>)};
+      for (const void *fn : fk)
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smemd)) !=
+            hipSuccess)
+          return MP_ERR_HIP;
+      if (a.out_dtype == MP_F16)
+        hipLaunchKernelGGL(i8_gemm_dma_kernel<MP_F16>, grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
+      else if (a.out_dtype == MP_BF16)
+        hipLaunchKernelGGL(i8_gemm_dma_kernel<MP_BF16>, grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
+      else
+        hipLaunchKernelGGL(i8_gemm_dma_kernel<MP_F32>, grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
+    } else {
+      const size_t smem = static_cast<size_t>(2) * (kBigBM + kBigBN) * kBigLD;
+      const void *fk[3] = {reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F16>),
+                           reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_BF16>),
+                           reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F32>)};
+      // > 64 KB of dynamic LDS must be allowed per kernel (idempotent, cheap)
+      for (const void *fn : fk)
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) !=
+            hipSuccess)
+          return MP_ERR_HIP;
+      if (a.out_dtype == MP_F16)
+        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F16>, grid, dim3(kBigThreads), smem, stream, a, tiles_m, tiles_n);
+      else if (a.out_dtype == MP_BF16)
+        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_BF16>, grid, dim3(kBigThreads), smem, stream, a, tiles_m, tiles_n);
+      else
+        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F32>, grid, dim3(kBigThreads), smem, stream, a, tiles_m, tiles_n);
+    }
   } else if (a.k % kTBK == 0 && aligned) {
     const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));
     if (epilogue == MP_EPI_F32)

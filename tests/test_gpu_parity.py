@@ -208,11 +208,15 @@ def test_w8_quantize_export_and_fake_rules():
 
 # ------------------------------------------------------------------ W8A8 GEMM
 W8_CASES = [(1, 11008, 4096), (16, 11008, 4096), (5, 1000, 256), (17, 512, 1024), (64, 384, 512), (65, 256, 512),
-            (256, 1000, 1024), (300, 384, 4096), (7, 100, 48), (1100, 300, 256), (2048, 520, 320)]
+            (256, 1000, 1024), (300, 384, 4096), (7, 100, 48), (1100, 300, 256), (2048, 520, 320),
+            # large-M kernel: four register stages over 3 loop trips, two stages (K % 256 != 0)
+            (1024, 640, 768), (1300, 700, 384),
+            # large-M kernel with odd N: the unpaired store path
+            (1024, 333, 256)]
 
 
 @pytest.mark.parametrize("m,n,k", W8_CASES)
-@pytest.mark.parametrize("out", ["fp16", "bf16"])
+@pytest.mark.parametrize("out", ["fp16", "bf16", "fp32"])
 def test_w8a8_gemm_bitexact(m, n, k, out):
     _say("w8a8", m, n, k, out)
     rng = np.random.default_rng(m * 7 + n)
@@ -221,9 +225,12 @@ def test_w8a8_gemm_bitexact(m, n, k, out):
     sx = (rng.random(m) * 0.01).astype(np.float32)
     sw = (rng.random(n) * 0.001).astype(np.float32)
     bias = (rng.standard_normal(n) * 0.1).astype(np.float16)
-    odt = {"fp16": torch.float16, "bf16": torch.bfloat16}[out]
+    odt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[out]
     y = _ops().w8a8_gemm(_t(qx), _t(sx), _t(qw), _t(sw), _t(bias), odt)
     ref = O.w8a8_linear_runtime(qx, sx, qw, sw, bias, out_dtype=out)
+    if out == "fp32":
+        assert np.array_equal(_np(y).view(np.uint32), ref.view(np.uint32))   # bar: bit-exact
+        return
     got = _np(y.view(torch.int16)).view(np.uint16) if out == "bf16" else _np(y).view(np.uint16)
     assert np.array_equal(got, ref.view(np.uint16))   # bar: bit-exact
 
