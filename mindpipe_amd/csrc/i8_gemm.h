@@ -25,6 +25,7 @@ struct mp_i8_args {
   int64_t n;                 // output columns (SWIGLU: I)
   int64_t k;
   int64_t ldy;               // output row stride (elements)
+  int staged_epilogue;       // large-M kernel: 16-bit outputs through LDS, 16-byte stores
 };
 
 int mp_launch_i8_gemm(const mp_i8_args &args, int epilogue, hipStream_t stream);

@@ -507,6 +507,72 @@ __device__ __forceinline__ void big_epilogue(const mp_i8_args &p, const i16_t (&
       }
 }
 
+// LDS-staged epilogue of one wave's 128 x 64 tile for 16-bit outputs: in two
+// passes of 64 rows the wave writes its converted values into a private 8 KB LDS
+// region (row-major, 128-byte rows; lane pairs exchange halves so each writes
+// 32-bit words) and reads them back as 16-byte chunks, so a lane issues 16
+// global_store_dwordx4 instead of 64 narrow stores.  Needs a full-row,
+// full-column tile, a row stride that is a multiple of 8 elements, 16-byte
+// aligned y and s_tok; the caller checks.  Wave-private: only lgkmcnt waits.
+template <int OUT_DT>
+__device__ __forceinline__ void big_epilogue_staged(const mp_i8_args &p, const i16_t (&acc)[4][2], int64_t mbase_w,
+                                                    int64_t nbase_w, int lane, int8_t *stage) {
+  const bool has_bias = p.bias != nullptr;
+  const bool odd = lane & 1;
+  const uint32_t sel_lo = odd ? 0x01000504u : 0x05040100u;
+  float sbv[2], bv[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t col = nbase_w + j * 32 + (lane & 31);
+    sbv[j] = p.s_b[col];
+    bv[j] = has_bias ? mp_load_as_f32(p.bias, col, p.bias_dtype) : 0.f;
+  }
+  const int64_t row_l = 4 * (lane >> 5);  // row of element 0 within the 32-row tile
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = 2 * h + ii;
+      float4 s4[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        s4[g] = *reinterpret_cast<const float4 *>(p.s_a + mbase_w + row_l + i * 32 + 8 * g);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float sv[4] = {s4[g].x, s4[g].y, s4[g].z, s4[g].w};
+          uint32_t hv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][4 * g + e]), sv[e]), sbv[j]);
+            v = has_bias ? mp_add(v, bv[j]) : v;
+            hv[e] = OUT_DT == MP_F16 ? mp_f2h(v) : mp_f2bf(v);
+          }
+          const uint32_t p01 = hv[0] | (hv[1] << 16), p23 = hv[2] | (hv[3] << 16);
+          const uint32_t recv = __shfl_xor(odd ? p01 : p23, 1, 64);
+          const uint32_t mine = odd ? p23 : p01;
+          const uint32_t w0 = __builtin_amdgcn_perm(recv, mine, sel_lo);
+          const uint32_t w1 = __builtin_amdgcn_perm(recv, mine, sel_lo + 0x02020202u);
+          // local row within the 64-row pass, column pair (2c, 2c+1) of the 64 columns
+          const int r = ii * 32 + static_cast<int>(row_l) + 8 * g + (odd ? 2 : 0);
+          const int cb = (j * 32 + (lane & 31)) & ~1;
+          *reinterpret_cast<uint32_t *>(stage + r * 128 + cb * 2) = w0;
+          *reinterpret_cast<uint32_t *>(stage + (r + 1) * 128 + cb * 2) = w1;
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int c = q * 64 + lane;  // 16-byte chunk: row c / 8, columns 8 (c % 8) ..
+      const i4_t v = *reinterpret_cast<const i4_t *>(stage + c * 16);
+      const int64_t m = mbase_w + h * 64 + c / 8;
+      *reinterpret_cast<i4_t *>(static_cast<uint16_t *>(p.y) + m * p.ldy + nbase_w + 8 * (c % 8)) = v;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // region reused by the next pass
+  }
+}
+
 template <int OUT_DT>
 __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, int tiles_m, int tiles_n) {
   constexpr int BM = kBigBM, BN = kBigBN, BK = kBigBK, LD = kBigLD, NT = kBigThreads;
@@ -519,30 +585,56 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
   int8_t *sb = smem_big + 2 * BM * LD;  // [2][BN*LD]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
-  int tm, tn;
-  big_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const int64_t k = p.k;
+
+  // Tile schedule: the tiles of XCD x (workgroups id % 8 == x) form a contiguous
+  // run in band order (big_tile_coords); workgroup id takes run entries id / 8,
+  // id / 8 + stride, ...  With one workgroup per tile the stride ends the walk
+  // after the first tile; a persistent launch (gridDim a multiple of 8) walks the
+  // run, loading the next tile's first K steps before the current epilogue.
+  const int total = tiles_m * tiles_n;
+  const int per = total / 8, rem = total % 8;
+  const int xcd = blockIdx.x % 8;
+  const int run_start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
+  const int run_len = per + (xcd < rem ? 1 : 0);
+  const bool persist = static_cast<int>(gridDim.x) < total;
+  const int stride = persist ? static_cast<int>(gridDim.x) / 8 : run_len;
+  int t = blockIdx.x / 8;
+  if (t >= run_len) return;  // workgroup-uniform, before any barrier
+  auto coords = [&](int tt, int64_t &mm0, int64_t &nn0) {
+    const int g = run_start + tt;
+    const int band = g / (4 * tiles_n);
+    const int inb = g % (4 * tiles_n);
+    const int rows_in_band = (tiles_m - band * 4) < 4 ? (tiles_m - band * 4) : 4;
+    mm0 = static_cast<int64_t>(band * 4 + inb % rows_in_band) * BM;
+    nn0 = static_cast<int64_t>(inb / rows_in_band) * BN;
+  };
+  int64_t m0, n0;
+  coords(t, m0, n0);
 
   // pass i of this thread covers tile row (tid / CPR + i * RPP), bytes (tid % CPR) * 16
   // of the K step; rows past the matrix are clamped (computed, never stored)
   const int rloc = tid / CPR, cloc = (tid % CPR) * 16;
   const int cst = ((tid % CPR) ^ ((rloc >> 2) & 3)) * 16;  // swizzled slot (RPP % 16 == 0)
   int aoff[CA], boff[CB];
+  const int8_t *abase, *bbase;
+  auto set_tile = [&](int64_t mm0, int64_t nn0) {
 #pragma unroll
-  for (int i = 0; i < CA; ++i) {
-    int64_t r = m0 + rloc + i * RPP;
-    r = r < p.rows ? r : p.rows - 1;
-    aoff[i] = static_cast<int>(r - m0);
-  }
+    for (int i = 0; i < CA; ++i) {
+      int64_t r = mm0 + rloc + i * RPP;
+      r = r < p.rows ? r : p.rows - 1;
+      aoff[i] = static_cast<int>(r - mm0);
+    }
 #pragma unroll
-  for (int i = 0; i < CB; ++i) {
-    int64_t c = n0 + rloc + i * RPP;
-    c = c < p.n ? c : p.n - 1;
-    boff[i] = static_cast<int>(c - n0);
-  }
-  const int8_t *abase = p.a + m0 * k + cloc;
-  const int8_t *bbase = p.b + n0 * k + cloc;
+    for (int i = 0; i < CB; ++i) {
+      int64_t c = nn0 + rloc + i * RPP;
+      c = c < p.n ? c : p.n - 1;
+      boff[i] = static_cast<int>(c - nn0);
+    }
+    abase = p.a + mm0 * k + cloc;
+    bbase = p.b + nn0 * k + cloc;
+  };
+  set_tile(m0, n0);
   i4_t ra[CA + CB], rb[CA + CB];
   auto load_tile = [&](i4_t *r, int64_t kt) {
     const int64_t off = kt * BK;
@@ -570,47 +662,54 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
   const int rsw = 16 * ((lane >> 5) ^ ((lane >> 2) & 3));  // chunk (lane >> 5) of row lane & 31, swizzled
   const int arow = (wm * 128 + (lane & 31)) * LD + rsw;
   const int brow = (wn * 64 + (lane & 31)) * LD + rsw;
-  // One K step with the LDS traffic interleaved into the MFMA stream: the
-  // fragments of the second K32 half are read between the first half's MFMAs,
-  // the staged next tile is written to the other buffer between the second
-  // half's MFMAs, and the global loads of the tile after it go out first.
-  auto step = [&](int buf, const i4_t *st, int nbuf, i4_t *ld, int64_t kt_ld) {
+  // Software pipeline across the barrier.  Step s multiplies buffer b = s % 2:
+  //   first half : global loads of K tile s+2; K32 half 0 MFMAs (fragments read in
+  //                the previous step) interleaved with the reads of half 1's
+  //                fragments and the LDS writes of tile s+1 into buffer b^1;
+  //   barrier    : tile s+1 complete in b^1, every read of b's half 1 done;
+  //   second half: K32 half 1 MFMAs interleaved with the reads of half 0's
+  //                fragments of b^1 for step s+1.
+  // After the barrier the MFMAs start at once (their fragments are in registers);
+  // buffer b is rewritten only in step s+1's first half, after that barrier.
+  i4_t af[2][TM], bf[2][TN];
+  auto read_half = [&](int buf, int ks) {
     const int8_t *ca = sa + buf * BM * LD;
     const int8_t *cbp = sb + buf * BN * LD;
-    i4_t af[2][TM], bf[2][TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) af[0][i] = *reinterpret_cast<const i4_t *>(ca + arow + i * 32 * LD);
+    for (int i = 0; i < TM; ++i) af[ks][i] = *reinterpret_cast<const i4_t *>(ca + (arow ^ (ks * 32)) + i * 32 * LD);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bf[0][j] = *reinterpret_cast<const i4_t *>(cbp + brow + j * 32 * LD);
+    for (int j = 0; j < TN; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(cbp + (brow ^ (ks * 32)) + j * 32 * LD);
+  };
+  auto mfma_half = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
+  };
+  auto first_half = [&](int buf, const i4_t *st, int nbuf, i4_t *ld, int64_t kt_ld) {
     load_tile(ld, kt_ld);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) af[1][i] = *reinterpret_cast<const i4_t *>(ca + (arow ^ 32) + i * 32 * LD);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bf[1][j] = *reinterpret_cast<const i4_t *>(cbp + (brow ^ 32) + j * 32 * LD);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0][i], bf[0][j], acc[i][j], 0, 0, 0);
+    read_half(buf, 1);
+    mfma_half(0);
     store_tile(st, nbuf);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[1][i], bf[1][j], acc[i][j], 0, 0, 0);
-    // schedule: 6 reads, 4 global loads, then MFMA/read pairs, then MFMA/write pairs
-    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);
-    for (int r = 0; r < 6; ++r) {
+    __builtin_amdgcn_sched_group_barrier(0x020, CA + CB, 0);
+    for (int r = 0; r < TM + TN; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < TM * TN - (TM + TN); ++r) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  };
+  auto second_half = [&](int nbuf) {
+    read_half(nbuf, 0);
+    mfma_half(1);
+    for (int r = 0; r < TM + TN; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
   };
 
   // K is a multiple of 2 * BK (host check): the loop body is branch-free; the two
@@ -621,15 +720,54 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
   __builtin_amdgcn_sched_barrier(0);
   store_tile(ra, 0);
   mp_lds_barrier();
-  for (int64_t kt = 0; kt < nkt; kt += 2) {
-    step(0, rb, 1, ra, kt + 2 < nkt ? kt + 2 : nkt - 1);
+  read_half(0, 0);
+  while (true) {
+    for (int64_t kt = 0; kt < nkt; kt += 2) {
+      first_half(0, rb, 1, ra, kt + 2 < nkt ? kt + 2 : nkt - 1);
+      mp_lds_barrier();
+      second_half(1);
+      __builtin_amdgcn_sched_barrier(0);
+      first_half(1, ra, 0, rb, kt + 3 < nkt ? kt + 3 : nkt - 1);
+      mp_lds_barrier();
+      second_half(0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // next tile's first two K steps go out before this tile's epilogue (LDS is
+    // free: the last step's barrier has passed and the epilogue does not use it)
+    const int tn_next = t + stride;
+    const bool has_next = tn_next < run_len;
+    int64_t m1 = m0, n1 = n0;
+    if (has_next) {
+      coords(tn_next, m1, n1);
+      set_tile(m1, n1);
+      load_tile(ra, 0);
+      load_tile(rb, 1);
+    }
+    // epilogue: (acc * s_tok) * s_ch (+ bias) -> OUT_DT; 16-bit outputs of full tiles
+    // go through LDS (the K loop is done with it: the last barrier has passed; only
+    // the unused prefetch reads of buffer 0 may still be in flight in other waves)
+    const bool staged = p.staged_epilogue && OUT_DT != MP_F32 && m0 + BM <= p.rows && n0 + BN <= p.n && (p.ldy & 7) == 0 &&
+                        (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 &&
+                        (reinterpret_cast<uintptr_t>(p.s_a) & 15) == 0;
+    if (staged)
+      big_epilogue_staged<OUT_DT>(p, acc, m0 + wm * 128, n0 + wn * 64, lane, smem_big + wave * 8192);
+    else
+      big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
+    if (!has_next) break;
+    mp_lds_barrier();  // every wave's staging reads are done before buffer 0 is rewritten
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    store_tile(ra, 0);
     mp_lds_barrier();
-    step(1, ra, 0, rb, kt + 3 < nkt ? kt + 3 : nkt - 1);
-    mp_lds_barrier();
+    read_half(0, 0);
+    t = tn_next;
+    m0 = m1;
+    n0 = n1;
   }
-
-  // epilogue: (acc * s_tok) * s_ch (+ bias) -> OUT_DT
-  big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
 }
 
 // Large-M GEMM with direct global->LDS loads (global_load_lds_dwordx4): 256x256
@@ -752,12 +890,43 @@ constexpr int kTBM = 128, kTBN = 128, kTBK = 64;
 
 }  // namespace
 
-// Large-M kernel variant: 4 (4 waves of 128x128) or 8 (8 waves of 128x64);
-// MP_W8_BIG_VARIANT overrides the default, for measurements.
+// Large-M kernel: 8 = register-staged interleaved kernel (default), 11 = direct
+// global->LDS loads; MP_W8_BIG_VARIANT selects, for measurements.
 static int mp_big_variant() {
   static int v = [] {
     const char *e = getenv("MP_W8_BIG_VARIANT");
-    return e ? atoi(e) : 4;
+    return e ? atoi(e) : 8;
+  }();
+  return v;
+}
+
+// Compute units of the current device (cached per device id).
+static int mp_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
+// LDS-staged 16-byte-store epilogue (MP_W8_STAGED=0 turns it off, for measurements).
+static int mp_staged_epilogue() {
+  static int v = [] {
+    const char *e = getenv("MP_W8_STAGED");
+    return e ? atoi(e) : 1;
+  }();
+  return v;
+}
+
+// Persistent large-M launch (MP_W8_PERSIST=0 turns it off, for measurements).
+static int mp_persist() {
+  static int v = [] {
+    const char *e = getenv("MP_W8_PERSIST");
+    return e ? atoi(e) : 1;
   }();
   return v;
 }
@@ -820,6 +989,10 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
       else
         hipLaunchKernelGGL(i8_gemm_dma_kernel<MP_F32>, grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
     } else {
+      // persistent when the tiles exceed one workgroup per CU (MP_W8_PERSIST=0 disables)
+      const int cus = mp_cu_count();
+      const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+      const dim3 pgrid(static_cast<unsigned>(mp_persist() && tiles > cus && cus >= 8 ? (cus / 8) * 8 : tiles));
       const size_t smem = static_cast<size_t>(2) * (kBigBM + kBigBN) * kBigLD;
       const void *fk[3] = {reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F16>),
                            reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_BF16>),
@@ -829,12 +1002,14 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
         if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) !=
             hipSuccess)
           return MP_ERR_HIP;
+      mp_i8_args am = a;
+      am.staged_epilogue = mp_staged_epilogue();
       if (a.out_dtype == MP_F16)
-        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F16>, grid, dim3(kBigThreads), smem, stream, a, tiles_m, tiles_n);
+        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F16>, pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
       else if (a.out_dtype == MP_BF16)
-        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_BF16>, grid, dim3(kBigThreads), smem, stream, a, tiles_m, tiles_n);
+        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_BF16>, pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
       else
-        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F32>, grid, dim3(kBigThreads), smem, stream, a, tiles_m, tiles_n);
+        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F32>, pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
     }
   } else if (a.k % kTBK == 0 && aligned) {
     const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));
