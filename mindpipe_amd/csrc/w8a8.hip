@@ -507,6 +507,57 @@ __device__ __forceinline__ void big_epilogue(const mp_i8_args &p, const i16_t (&
       }
 }
 
+// Epilogues of the grouped (expert) launches of the large-M kernel, for one wave's
+// 4 x 2 accumulator tiles at rows mbase + 32 i + 8 (r >> 2) + (r & 3) (< row_end)
+// and columns nbase + lane % 32 (+ 32 j for F32).  Arithmetic as in
+// i8_tiled_kernel: F32 y = (acc * s_a) * s_b; SWIGLU g / u = (acc * s_a) * s_gate /
+// s_up, h = silu(g) * u to the fp32 workspace plus the row's abs-max over the
+// wave's 32 columns into amax_partial[m][4 * blockIdx.x + wave column].
+template <int EPI, int TM>
+__device__ __forceinline__ void grouped_epilogue(const mp_i8_args &p, const i16_t (&acc)[TM][2], int64_t mbase,
+                                                 int64_t row_end, int64_t nbase, const float *sbexp, int lane) {
+  float *yb = static_cast<float *>(p.y);
+  if (EPI == MP_EPI_SWIGLU) {
+    const int64_t col = nbase + (lane & 31);
+    const bool cval = col < p.n;
+    const int64_t colc = cval ? col : p.n - 1;
+    const float sg = sbexp[colc], su = sbexp[p.n + colc];
+    const int64_t pidx = static_cast<int64_t>(blockIdx.x) * 4 + (nbase % 128) / 32;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = mbase + i * 32 + 8 * (r >> 2) + (r & 3);
+        const bool mval = m < row_end;
+        const float sa_m = mval ? p.s_a[m] : 0.f;
+        const float g = mp_mul(mp_mul(static_cast<float>(acc[i][0][r]), sa_m), sg);
+        const float u = mp_mul(mp_mul(static_cast<float>(acc[i][1][r]), sa_m), su);
+        const float den = mp_add(1.0f, expf(-g));
+        const float h = mp_mul(__fdiv_rn(g, den), u);
+        if (mval && cval) yb[m * p.ldy + col] = h;
+        float a = (mval && cval) ? fabsf(h) : 0.f;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+        if ((lane & 31) == 0 && mval) p.amax_partial[m * p.n_partial + pidx] = a;
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = nbase + j * 32 + (lane & 31);
+      if (col >= p.n) continue;
+      const float sb = sbexp[col];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = mbase + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (m >= row_end) continue;
+          yb[m * p.ldy + col] = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), p.s_a[m]), sb);
+        }
+    }
+  }
+}
+
 // LDS-staged epilogue of one wave's 128 x 64 tile for 16-bit outputs: in two
 // passes of 64 rows the wave writes its converted values into a private 8 KB LDS
 // region (row-major, 128-byte rows; lane pairs exchange halves so each writes
@@ -573,10 +624,21 @@ __device__ __forceinline__ void big_epilogue_staged(const mp_i8_args &p, const i
   }
 }
 
-template <int OUT_DT>
-__global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, int tiles_m, int tiles_n) {
-  constexpr int BM = kBigBM, BN = kBigBN, BK = kBigBK, LD = kBigLD, NT = kBigThreads;
-  constexpr int TM = 4, TN = 2;                // 32x32 tiles per wave
+template <int OUT_DT, int EPI, int TMW = 4>
+__global__ __launch_bounds__(kBigThreads, TMW == 2 ? 4 : 2) void i8_gemm_big_kernel(mp_i8_args p, int tiles_m,
+                                                                                 int tiles_n) {
+  constexpr bool GROUPED = EPI != MP_EPI_DENSE;  // grouped expert GEMM: F32 (GEMM2) or SWIGLU (GEMM1)
+  constexpr bool SWI = EPI == MP_EPI_SWIGLU;
+  // B tile rows: dense / F32 = 256 output columns; SWIGLU = 128 gate rows then the 128
+  // matching up rows, so a wave's two 32-column fragments are gate j and up j
+  constexpr int OUTC = SWI ? kBigBN / 2 : kBigBN;  // output columns per tile
+  constexpr int WBN = SWI ? 32 : 64;               // wave column base step
+  constexpr int BJ = SWI ? kBigBN / 2 : 32;        // B rows between a wave's two fragments
+  // TMW = 4: 256-row tiles (waves of 128 x 64); TMW = 2: 128-row tiles (waves of 64 x 64, 48 KB of LDS
+  // and <= 128 registers, two workgroups per CU) for grouped launches whose experts hold ~128 rows
+  constexpr int BM = 64 * TMW, BN = kBigBN, BK = kBigBK, LD = kBigLD, NT = kBigThreads;
+  constexpr int TM = TMW, TN = 2;              // 32x32 tiles per wave
+  static_assert(TMW == 4 || EPI != MP_EPI_DENSE, "dense launches use 256-row tiles");
   constexpr int CPR = BK / 16;                 // 16-byte chunks per tile row
   constexpr int RPP = NT / CPR;                // tile rows covered per pass (128)
   constexpr int CA = BM / RPP, CB = BN / RPP;  // passes (2 each)
@@ -592,14 +654,43 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
   // id / 8 + stride, ...  With one workgroup per tile the stride ends the walk
   // after the first tile; a persistent launch (gridDim a multiple of 8) walks the
   // run, loading the next tile's first K steps before the current epilogue.
+  // Grouped launches (grid: weight slices x row slots) take one tile: the row slot
+  // walks group_offsets to the expert and its 256-row chunk.
   const int total = tiles_m * tiles_n;
   const int per = total / 8, rem = total % 8;
   const int xcd = blockIdx.x % 8;
   const int run_start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
-  const int run_len = per + (xcd < rem ? 1 : 0);
-  const bool persist = static_cast<int>(gridDim.x) < total;
-  const int stride = persist ? static_cast<int>(gridDim.x) / 8 : run_len;
+  int run_len = per + (xcd < rem ? 1 : 0);
+  const bool persist = !GROUPED && static_cast<int>(gridDim.x) < total;
+  int stride = persist ? static_cast<int>(gridDim.x) / 8 : run_len;
   int t = blockIdx.x / 8;
+  int64_t row_end = p.rows;
+  const int8_t *bexp = p.b;
+  const float *sbexp = p.s_b;
+  int64_t g_m0 = 0;
+  if (GROUPED) {
+    int64_t slot = blockIdx.y;
+    int e = 0;
+    bool found = false;
+    for (; e < p.n_experts; ++e) {
+      const int64_t lo = p.offsets[e], hi = p.offsets[e + 1];
+      const int64_t tiles_e = (hi - lo + BM - 1) / BM;
+      if (slot < tiles_e) {
+        g_m0 = lo + slot * BM;
+        row_end = hi < g_m0 + BM ? hi : g_m0 + BM;
+        found = true;
+        break;
+      }
+      slot -= tiles_e;
+    }
+    if (!found) return;  // workgroup-uniform, before any barrier
+    const int64_t nb_rows = SWI ? 2 * p.n : p.n;
+    bexp = p.b + static_cast<int64_t>(e) * nb_rows * k;
+    sbexp = p.s_b + static_cast<int64_t>(e) * nb_rows;
+    t = 0;
+    run_len = 1;
+    stride = 1;
+  }
   if (t >= run_len) return;  // workgroup-uniform, before any barrier
   auto coords = [&](int tt, int64_t &mm0, int64_t &nn0) {
     const int g = run_start + tt;
@@ -610,29 +701,41 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
     nn0 = static_cast<int64_t>(inb / rows_in_band) * BN;
   };
   int64_t m0, n0;
-  coords(t, m0, n0);
+  if (GROUPED) {
+    m0 = g_m0;
+    n0 = static_cast<int64_t>(blockIdx.x) * OUTC;
+  } else {
+    coords(t, m0, n0);
+  }
 
   // pass i of this thread covers tile row (tid / CPR + i * RPP), bytes (tid % CPR) * 16
   // of the K step; rows past the matrix are clamped (computed, never stored)
   const int rloc = tid / CPR, cloc = (tid % CPR) * 16;
   const int cst = ((tid % CPR) ^ ((rloc >> 2) & 3)) * 16;  // swizzled slot (RPP % 16 == 0)
+  // absolute A rows (clamped into the tile's valid rows) and B rows (clamped columns)
   int aoff[CA], boff[CB];
-  const int8_t *abase, *bbase;
+  const int8_t *abase = p.a + cloc, *bbase = bexp + cloc;
   auto set_tile = [&](int64_t mm0, int64_t nn0) {
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
       int64_t r = mm0 + rloc + i * RPP;
-      r = r < p.rows ? r : p.rows - 1;
-      aoff[i] = static_cast<int>(r - mm0);
+      r = r < row_end ? r : row_end - 1;
+      aoff[i] = static_cast<int>(r);
     }
 #pragma unroll
     for (int i = 0; i < CB; ++i) {
-      int64_t c = nn0 + rloc + i * RPP;
-      c = c < p.n ? c : p.n - 1;
-      boff[i] = static_cast<int>(c - nn0);
+      const int lr = rloc + i * RPP;
+      if (SWI) {
+        const int half = lr / (BN / 2);
+        int64_t c = nn0 + lr % (BN / 2);
+        c = c < p.n ? c : p.n - 1;
+        boff[i] = static_cast<int>(half * p.n + c);
+      } else {
+        int64_t c = nn0 + lr;
+        c = c < p.n ? c : p.n - 1;
+        boff[i] = static_cast<int>(c);
+      }
     }
-    abase = p.a + mm0 * k + cloc;
-    bbase = p.b + nn0 * k + cloc;
   };
   set_tile(m0, n0);
   i4_t ra[CA + CB], rb[CA + CB];
@@ -660,8 +763,8 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
   const int rsw = 16 * ((lane >> 5) ^ ((lane >> 2) & 3));  // chunk (lane >> 5) of row lane & 31, swizzled
-  const int arow = (wm * 128 + (lane & 31)) * LD + rsw;
-  const int brow = (wn * 64 + (lane & 31)) * LD + rsw;
+  const int arow = (wm * (32 * TM) + (lane & 31)) * LD + rsw;
+  const int brow = (wn * WBN + (lane & 31)) * LD + rsw;
   // Software pipeline across the barrier.  Step s multiplies buffer b = s % 2:
   //   first half : global loads of K tile s+2; K32 half 0 MFMAs (fragments read in
   //                the previous step) interleaved with the reads of half 1's
@@ -678,7 +781,7 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
 #pragma unroll
     for (int i = 0; i < TM; ++i) af[ks][i] = *reinterpret_cast<const i4_t *>(ca + (arow ^ (ks * 32)) + i * 32 * LD);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(cbp + (brow ^ (ks * 32)) + j * 32 * LD);
+    for (int j = 0; j < TN; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(cbp + (brow ^ (ks * 32)) + j * BJ * LD);
   };
   auto mfma_half = [&](int ks) {
 #pragma unroll
@@ -732,6 +835,10 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
       second_half(0);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (GROUPED) {
+      grouped_epilogue<EPI, TM>(p, acc, m0 + wm * (32 * TM) + 4 * (lane >> 5), row_end, n0 + wn * WBN, sbexp, lane);
+      break;
+    }
     // next tile's first two K steps go out before this tile's epilogue (LDS is
     // free: the last step's barrier has passed and the epilogue does not use it)
     const int tn_next = t + stride;
@@ -749,10 +856,12 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
     const bool staged = p.staged_epilogue && OUT_DT != MP_F32 && m0 + BM <= p.rows && n0 + BN <= p.n && (p.ldy & 7) == 0 &&
                         (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 &&
                         (reinterpret_cast<uintptr_t>(p.s_a) & 15) == 0;
-    if (staged)
-      big_epilogue_staged<OUT_DT>(p, acc, m0 + wm * 128, n0 + wn * 64, lane, smem_big + wave * 8192);
-    else
-      big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
+    if constexpr (TM == 4) {
+      if (staged)
+        big_epilogue_staged<OUT_DT>(p, acc, m0 + wm * 128, n0 + wn * 64, lane, smem_big + wave * 8192);
+      else
+        big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
+    }
     if (!has_next) break;
     mp_lds_barrier();  // every wave's staging reads are done before buffer 0 is rewritten
 #pragma unroll
@@ -781,17 +890,47 @@ __global__ __launch_bounds__(kBigThreads) void i8_gemm_big_kernel(mp_i8_args p, 
 // (kt+3) % 4 from step kt-1 is done.
 constexpr int kDmaStages = 4;
 
-template <int OUT_DT>
+template <int OUT_DT, int EPI>
 __global__ __launch_bounds__(512) void i8_gemm_dma_kernel(mp_i8_args p, int tiles_m, int tiles_n) {
   constexpr int BM = 256, BN = 256, BK = 64, LD = 64, TM = 4, TN = 2, S = kDmaStages;
   constexpr int STAGE = (BM + BN) * LD;  // bytes per stage (A rows then B rows)
+  // grouped expert launches (F32 / SWIGLU epilogue): B tile layout as in i8_gemm_big_kernel
+  constexpr bool GROUPED = EPI != MP_EPI_DENSE;
+  constexpr bool SWI = EPI == MP_EPI_SWIGLU;
+  constexpr int OUTC = SWI ? BN / 2 : BN, WBN = SWI ? 32 : 64, BJ = SWI ? BN / 2 : 32;
   extern __shared__ __attribute__((aligned(16))) int8_t smem_dma[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
-  int tm, tn;
-  big_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const int64_t k = p.k;
+  int64_t m0, n0, row_end = p.rows;
+  const int8_t *bexp = p.b;
+  const float *sbexp = p.s_b;
+  if (GROUPED) {
+    int64_t slot = blockIdx.y;
+    int e = 0;
+    bool found = false;
+    for (; e < p.n_experts; ++e) {
+      const int64_t lo = p.offsets[e], hi = p.offsets[e + 1];
+      const int64_t tiles_e = (hi - lo + BM - 1) / BM;
+      if (slot < tiles_e) {
+        m0 = lo + slot * BM;
+        row_end = hi < m0 + BM ? hi : m0 + BM;
+        found = true;
+        break;
+      }
+      slot -= tiles_e;
+    }
+    if (!found) return;  // workgroup-uniform, before any barrier or load
+    const int64_t nb_rows = SWI ? 2 * p.n : p.n;
+    bexp = p.b + static_cast<int64_t>(e) * nb_rows * k;
+    sbexp = p.s_b + static_cast<int64_t>(e) * nb_rows;
+    n0 = static_cast<int64_t>(blockIdx.x) * OUTC;
+  } else {
+    int tm, tn;
+    big_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    m0 = static_cast<int64_t>(tm) * BM;
+    n0 = static_cast<int64_t>(tn) * BN;
+  }
 
   // load instruction q (0..3) of this wave fills 16 rows: q < 2 -> A rows
   // (2 wave + q) * 16, else B rows (2 wave + q - 2) * 16.  Lane l: row + l / 4,
@@ -804,10 +943,19 @@ __global__ __launch_bounds__(512) void i8_gemm_dma_kernel(mp_i8_args p, int tile
     const int r0 = (2 * wave + (q & 1)) * 16;
     const int r = r0 + lane / 4;
     const int c = (lane & 3) ^ ((r >> 2) & 3);
-    int64_t g = (is_a ? m0 : n0) + r;
-    const int64_t lim = is_a ? p.rows : p.n;
-    g = g < lim ? g : lim - 1;
-    gsrc[q] = (is_a ? p.a : p.b) + g * k + 16 * c;
+    int64_t g;
+    if (is_a) {
+      g = m0 + r;
+      g = g < row_end ? g : row_end - 1;
+    } else if (SWI) {  // gate rows for r < 128, the matching up rows after
+      int64_t cc = n0 + r % (BN / 2);
+      cc = cc < p.n ? cc : p.n - 1;
+      g = (r / (BN / 2)) * p.n + cc;
+    } else {
+      g = n0 + r;
+      g = g < p.n ? g : p.n - 1;
+    }
+    gsrc[q] = (is_a ? p.a : bexp) + g * k + 16 * c;
     ldst[q] = (is_a ? 0 : BM * LD) + r0 * LD;
   }
   auto issue = [&](int64_t kt, int stage) {
@@ -825,7 +973,7 @@ __global__ __launch_bounds__(512) void i8_gemm_dma_kernel(mp_i8_args p, int tile
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
   const int rsw = 16 * ((lane >> 5) ^ ((lane >> 2) & 3));
   const int arow = (wm * 128 + (lane & 31)) * LD + rsw;
-  const int brow = BM * LD + (wn * 64 + (lane & 31)) * LD + rsw;
+  const int brow = BM * LD + (wn * WBN + (lane & 31)) * LD + rsw;
   auto compute = [&](int stage) {
     const int8_t *st = smem_dma + stage * STAGE;
     i4_t af[2][TM], bf[2][TN];
@@ -834,7 +982,7 @@ __global__ __launch_bounds__(512) void i8_gemm_dma_kernel(mp_i8_args p, int tile
 #pragma unroll
       for (int i = 0; i < TM; ++i) af[ks][i] = *reinterpret_cast<const i4_t *>(st + (arow ^ (ks * 32)) + i * 32 * LD);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(st + (brow ^ (ks * 32)) + j * 32 * LD);
+      for (int j = 0; j < TN; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(st + (brow ^ (ks * 32)) + j * BJ * LD);
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
@@ -870,7 +1018,10 @@ __global__ __launch_bounds__(512) void i8_gemm_dma_kernel(mp_i8_args p, int tile
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS DMA outstanding at exit
 
-  big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
+  if (GROUPED)
+    grouped_epilogue<EPI, TM>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), row_end, n0 + wn * WBN, sbexp, lane);
+  else
+    big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
 }
 
 // Any-shape dense fallback: one thread per output.
@@ -922,6 +1073,17 @@ static int mp_staged_epilogue() {
   return v;
 }
 
+// Grouped expert GEMMs on the large-M kernels: 1 = register-staged kernel with 128-row
+// tiles for SwiGLU outputs (default), 2 = the same for fp32 outputs too, 3 = direct-to-LDS
+// kernel with 256-row tiles, 0 = the tiled kernel (MP_W8_GROUPED_BIG, for measurements).
+static int mp_grouped_big() {
+  static int v = [] {
+    const char *e = getenv("MP_W8_GROUPED_BIG");
+    return e ? atoi(e) : 1;
+  }();
+  return v;
+}
+
 // Persistent large-M launch (MP_W8_PERSIST=0 turns it off, for measurements).
 static int mp_persist() {
   static int v = [] {
@@ -935,7 +1097,47 @@ static int mp_persist() {
 int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
   const bool aligned = mp_aligned(a.a, 16) && mp_aligned(a.b, 16);
   if (a.offsets) {
-    // grouped: tiled kernel only
+    // grouped: the large-M kernel (one 256-row chunk of one expert per workgroup, each
+    // weight slice streamed once per chunk) for fp32 / SwiGLU outputs, else the tiled kernel
+    // (fp32 outputs stay on the tiled kernel unless MP_W8_GROUPED_BIG >= 2: with N = hidden the
+    // 256-column tiles leave most CUs idle)
+    if (mp_grouped_big() && aligned && a.k % (2 * kBigBK) == 0 && a.k <= INT32_MAX &&
+        ((epilogue == MP_EPI_F32 && mp_grouped_big() >= 2) ||
+         (epilogue == MP_EPI_SWIGLU && a.n % (kBigBN / 2) == 0)) &&
+        a.n <= INT32_MAX / 2 && a.rows <= INT32_MAX) {
+      const bool swi = epilogue == MP_EPI_SWIGLU;
+      const int64_t n_tiles = mp_cdiv(a.n, swi ? kBigBN / 2 : kBigBN);
+      const int64_t m_slots = mp_cdiv(a.rows, kBigBM) + a.n_experts;
+      // the expert weights stream from HBM once: the direct-to-LDS kernel keeps three
+      // K tiles in flight per CU (K % 256), the register-staged one two
+      if (a.k % (kDmaStages * kBigBK) == 0 && mp_grouped_big() == 3) {
+        const size_t smemd = static_cast<size_t>(kDmaStages) * (kBigBM + kBigBN) * kBigBK;
+        const void *fd = swi ? reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_F32, MP_EPI_SWIGLU>)
+                             : reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_F32, MP_EPI_F32>);
+        if (hipFuncSetAttribute(fd, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smemd)) !=
+            hipSuccess)
+          return MP_ERR_HIP;
+        const dim3 gridd(static_cast<unsigned>(n_tiles), static_cast<unsigned>(m_slots));
+        if (swi)
+          hipLaunchKernelGGL((i8_gemm_dma_kernel<MP_F32, MP_EPI_SWIGLU>), gridd, dim3(512), smemd, stream, a, 1, 1);
+        else
+          hipLaunchKernelGGL((i8_gemm_dma_kernel<MP_F32, MP_EPI_F32>), gridd, dim3(512), smemd, stream, a, 1, 1);
+        MP_CHECK_LAUNCH();
+        return MP_OK;
+      }
+      // 128-row tiles: one tile per expert of up to 128 rows, 48 KB of LDS
+      const size_t smem = static_cast<size_t>(2) * (128 + kBigBN) * kBigLD;
+      const int64_t m_slots128 = mp_cdiv(a.rows, 128) + a.n_experts;
+      const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(m_slots128));
+      if (swi)
+        hipLaunchKernelGGL((i8_gemm_big_kernel<MP_F32, MP_EPI_SWIGLU, 2>), grid, dim3(kBigThreads), smem, stream, a, 1,
+                           1);
+      else
+        hipLaunchKernelGGL((i8_gemm_big_kernel<MP_F32, MP_EPI_F32, 2>), grid, dim3(kBigThreads), smem, stream, a, 1,
+                           1);
+      MP_CHECK_LAUNCH();
+      return MP_OK;
+    }
     if (a.k % kTBK != 0 || !aligned) return MP_ERR_SHAPE;
     const int64_t n_tiles =
         mp_cdiv(a.n, epilogue == MP_EPI_SWIGLU ? kTBN / 2 : kTBN);
@@ -975,28 +1177,28 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
     if (mp_big_variant() == 11 && a.k % (kDmaStages * kBigBK) == 0) {
       const size_t smemd = static_cast<size_t>(kDmaStages) * (kBigBM + kBigBN) * kBigBK;
-      const void *fk[3] = {reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_F16>),
-                           reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_BF16>),
-                           reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_F32>)};
+      const void *fk[3] = {reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_F16, MP_EPI_DENSE>),
+                           reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_BF16, MP_EPI_DENSE>),
+                           reinterpret_cast<const void *>(i8_gemm_dma_kernel<MP_F32, MP_EPI_DENSE>)};
       for (const void *fn : fk)
         if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smemd)) !=
             hipSuccess)
           return MP_ERR_HIP;
       if (a.out_dtype == MP_F16)
-        hipLaunchKernelGGL(i8_gemm_dma_kernel<MP_F16>, grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
+        hipLaunchKernelGGL((i8_gemm_dma_kernel<MP_F16, MP_EPI_DENSE>), grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
       else if (a.out_dtype == MP_BF16)
-        hipLaunchKernelGGL(i8_gemm_dma_kernel<MP_BF16>, grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
+        hipLaunchKernelGGL((i8_gemm_dma_kernel<MP_BF16, MP_EPI_DENSE>), grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
       else
-        hipLaunchKernelGGL(i8_gemm_dma_kernel<MP_F32>, grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
+        hipLaunchKernelGGL((i8_gemm_dma_kernel<MP_F32, MP_EPI_DENSE>), grid, dim3(512), smemd, stream, a, tiles_m, tiles_n);
     } else {
       // persistent when the tiles exceed one workgroup per CU (MP_W8_PERSIST=0 disables)
       const int cus = mp_cu_count();
       const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
       const dim3 pgrid(static_cast<unsigned>(mp_persist() && tiles > cus && cus >= 8 ? (cus / 8) * 8 : tiles));
       const size_t smem = static_cast<size_t>(2) * (kBigBM + kBigBN) * kBigLD;
-      const void *fk[3] = {reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F16>),
-                           reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_BF16>),
-                           reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F32>)};
+      const void *fk[3] = {reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F16, MP_EPI_DENSE>),
+                           reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_BF16, MP_EPI_DENSE>),
+                           reinterpret_cast<const void *>(i8_gemm_big_kernel<MP_F32, MP_EPI_DENSE>)};
       // > 64 KB of dynamic LDS must be allowed per kernel (idempotent, cheap)
       for (const void *fn : fk)
         if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) !=
@@ -1005,11 +1207,11 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
       mp_i8_args am = a;
       am.staged_epilogue = mp_staged_epilogue();
       if (a.out_dtype == MP_F16)
-        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F16>, pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
+        hipLaunchKernelGGL((i8_gemm_big_kernel<MP_F16, MP_EPI_DENSE>), pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
       else if (a.out_dtype == MP_BF16)
-        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_BF16>, pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
+        hipLaunchKernelGGL((i8_gemm_big_kernel<MP_BF16, MP_EPI_DENSE>), pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
       else
-        hipLaunchKernelGGL(i8_gemm_big_kernel<MP_F32>, pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
+        hipLaunchKernelGGL((i8_gemm_big_kernel<MP_F32, MP_EPI_DENSE>), pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
     }
   } else if (a.k % kTBK == 0 && aligned) {
     const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));

@@ -278,7 +278,10 @@ def _moe_case(t, h, inter, e, seed=0):
     return x, ids, tw, q13, s13, q2, s2
 
 
-@pytest.mark.parametrize("t,h,inter,e", [(64, 256, 512, 8), (200, 512, 384, 4), (3, 128, 128, 8)])
+# (t, h, inter, e): experts of up to ~300 rows (two 256-row chunks on the grouped large-M kernel),
+# an intermediate size that is not a multiple of 128 (tiled kernel), a nearly empty batch
+@pytest.mark.parametrize("t,h,inter,e", [(64, 256, 512, 8), (200, 512, 384, 4), (3, 128, 128, 8),
+                                         (600, 256, 256, 4), (64, 256, 320, 4)])
 def test_moe_chain_matches_oracle(t, h, inter, e):
     _say("moe", t, h, inter, e)
     x, ids, tw, q13, s13, q2, s2 = _moe_case(t, h, inter, e)
