@@ -198,12 +198,23 @@ int mp_decode_rope_append(const void *qkv, int64_t batch, int nh, int kvh, int h
 /* Split-K decode attention (flash decoding) over positions [0, *pos] of one
  * layer's cache: out [B, nh, 128] fp16 = softmax(q k^T * scale) v, fp32 inside;
  * nh / kvh in {1, 2, 4, 8}.  splits workgroups per (row, kv head), each over
- * ceil(capacity / splits) positions; workspace of
- * mp_decode_attention_workspace_bytes(batch, nh, splits). */
+ * ceil(capacity / splits) positions (splits <= 1024), then a merge launch when
+ * splits > 1.  workspace of mp_decode_attention_workspace_bytes(batch, nh,
+ * splits), 16-byte aligned; calls that share a workspace must not overlap. */
 size_t mp_decode_attention_workspace_bytes(int64_t batch, int nh, int splits);
 int mp_decode_attention(const void *q, int64_t batch, int nh, int kvh, int head_dim, const void *k_cache,
                         const void *v_cache, const int64_t *pos, int64_t capacity, int splits, float scale,
                         void *out, void *workspace, size_t workspace_bytes, mp_stream_t stream);
+
+/* mp_decode_rope_append followed by mp_decode_attention in one launch: the
+ * queries are rotated from qkv [B, (nh + 2 kvh) * 128] in registers and the
+ * workgroup whose split holds *pos appends the rotated key and the value before
+ * it scores.  A position outside [0, capacity) appends nothing and gives zeros.
+ * cos_t / sin_t fp16 [capacity, 64], 8-byte aligned; workspace as above. */
+int mp_decode_rope_attention(const void *qkv, int64_t batch, int nh, int kvh, int head_dim, const void *cos_t,
+                             const void *sin_t, const int64_t *pos, int64_t capacity, void *k_cache, void *v_cache,
+                             int splits, float scale, void *out, void *workspace, size_t workspace_bytes,
+                             mp_stream_t stream);
 
 /* act [rows, I] = round(round(silu(gate)) * up) of gate_up [rows, 2I] (gate | up), fp16. */
 int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, mp_stream_t stream);

@@ -31,6 +31,8 @@ SIGNATURES = {
     "mp_decode_attention_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "mp_decode_attention": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _i32, C.c_float, _vp, _vp, _sz,
                                    _vp]),
+    "mp_decode_rope_attention": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _vp, _i32, C.c_float,
+                                        _vp, _vp, _sz, _vp]),
     "mp_silu_mul": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "mp_w8_quantize_per_channel": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "mp_w8a8_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp]),

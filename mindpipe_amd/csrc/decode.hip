@@ -1,6 +1,7 @@
 // Decode-step kernels of the Llama-shaped measurement harness around the
 // quantized linears: RoPE + KV-cache append, split-K decode attention (flash
-// decoding) with its combine, and SiLU-multiply.  The reference has no
+// decoding) with its split merge (optionally with the RoPE and the append
+// fused into the attention launch), and SiLU-multiply.  The reference has no
 // counterpart (attention belongs to vLLM's backend); these exist so that one
 // greedy decode step runs as ~10 launches per layer and the W4A16 GEMVs, not
 // launch gaps, set the step time.
@@ -14,6 +15,7 @@
 namespace {
 
 constexpr int kHd = 128;
+constexpr int kMergeMaxSplits = 1024;  // splits per head the merge kernel takes
 
 // ---------------------------------------------------------------- RoPE + append
 // One wave per (row b, head); lane i owns the interleaved pair (2i, 2i+1).
@@ -52,44 +54,112 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
 }
 
 // ---------------------------------------------------------------- decode attention
+// Interleaved-pair RoPE of 8 consecutive dims (pairs 4 dl .. 4 dl + 3) at position
+// pos, rounding like PyTorch half ops (every product and the sum round to fp16).
+// cos_t / sin_t [T, 64] fp16; the rows are 8-byte aligned (host check).
+__device__ __forceinline__ void rope8(const uint4 xv, const uint16_t *__restrict__ cos_t,
+                                      const uint16_t *__restrict__ sin_t, int64_t pos, int dl, float (&o)[8]) {
+  // no contraction: the compiler narrows these to fp16 ops and would fuse a product
+  // into the subtraction (v_fma_f16), skipping the product's own rounding
+#pragma clang fp contract(off)
+  const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+  const uint2 cv = *reinterpret_cast<const uint2 *>(cos_t + pos * (kHd / 2) + dl * 4);
+  const uint2 sv = *reinterpret_cast<const uint2 *>(sin_t + pos * (kHd / 2) + dl * 4);
+  const uint32_t cw[2] = {cv.x, cv.y}, sw[2] = {sv.x, sv.y};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float x1 = mp_h2f(static_cast<uint16_t>(xw[j])), xb = mp_h2f(static_cast<uint16_t>(xw[j] >> 16));
+    const float c = mp_h2f(static_cast<uint16_t>(cw[j >> 1] >> (16 * (j & 1))));
+    const float s = mp_h2f(static_cast<uint16_t>(sw[j >> 1] >> (16 * (j & 1))));
+    o[2 * j] = mp_rh(mp_rh(x1 * c) - mp_rh(xb * s));
+    o[2 * j + 1] = mp_rh(mp_rh(x1 * s) + mp_rh(xb * c));
+  }
+}
+
 // Grid (splits, B * kvh), 256 threads.  A workgroup scores positions
 // [s*chunk, min((s+1)*chunk, len)) for the GRP query heads of one kv head:
 // 16 lanes per position (8 dims each, one 16-byte load), 4 positions per wave
 // per step, fp32 dot products reduced over the 16 lanes.  Scores go to LDS,
 // softmax statistics are taken over the workgroup, then P.V accumulates in
-// fp32 with the same lane layout.  Output: unnormalised partial o, running max
-// m and sum l per (row, head, split), merged by attn_combine_kernel.
-template <int GRP>
+// fp32 with the same lane layout; the first V step is loaded before the
+// softmax, so its latency overlaps it.
+//
+// ROPE: the queries come from the fused qkv row [B, (nh + 2 kvh) * 128] and are
+// rotated in registers; the workgroup whose split holds position pos (the last
+// used one) also rotates the new key and appends key and value to the cache
+// before it scores.  len = pos + 1; a position outside [0, cap) appends nothing
+// and yields zeros.  Otherwise q is [B, nh, 128] and len = clamp(pos + 1, 0, cap).
+//
+// With one split the workgroup normalises and stores the output; otherwise it
+// stores its unnormalised partial o, max m and sum l for attn_merge_kernel.
+template <int GRP, bool ROPE>
 __global__ __launch_bounds__(256) void decode_attn_kernel(
-    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k_cache, const uint16_t *__restrict__ v_cache,
-    const int64_t *__restrict__ pos_p, int kvh, int cap, int chunk, int splits, float scale,
-    float *__restrict__ part_o, float *__restrict__ part_ml) {
-  extern __shared__ float sm[];      // [GRP][chunk] scores, then [GRP][4][128] reduction
+    const uint16_t *__restrict__ qsrc, const uint16_t *__restrict__ cos_t, const uint16_t *__restrict__ sin_t,
+    uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache, const int64_t *__restrict__ pos_p, int kvh,
+    int cap, int chunk, int splits, float scale, float *__restrict__ part_o, float *__restrict__ part_ml,
+    uint16_t *__restrict__ out) {
+  extern __shared__ float sm[];  // [GRP][chunk] scores, then the [GRP][4][128] reduction
   __shared__ float red[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s = blockIdx.x;
-  const int bk = blockIdx.y;         // b * kvh + kh
-  const int64_t p1 = pos_p[0] + 1;   // valid positions [0, pos], clamped to the cache
-  const int len = static_cast<int>(p1 < 0 ? 0 : (p1 > cap ? cap : p1));
-  const int t0 = s * chunk;
-  if (t0 >= len) return;             // workgroup-uniform; the combine reads only used splits
-  const int t1 = min(t0 + chunk, len);
-  const int n = t1 - t0;
+  const int bk = blockIdx.y;  // b * kvh + kh
   const int nh = kvh * GRP;
   const int b = bk / kvh, kh = bk % kvh;
-  const int dl = lane & 15;          // 8-dim slice of this lane
-  const int pl = lane >> 4;          // position within the wave's group of 4
+  const int64_t pos = pos_p[0];
+  int len;
+  if (ROPE) {
+    len = (pos < 0 || pos >= cap) ? 0 : static_cast<int>(pos) + 1;
+  } else {
+    const int64_t p1 = pos + 1;
+    len = static_cast<int>(p1 < 0 ? 0 : (p1 > cap ? cap : p1));
+  }
+  const int t0 = s * chunk;
+  if (t0 >= len) {  // workgroup-uniform, before any barrier
+    if (len == 0 && s == 0 && splits == 1)  // (with splits the merge writes the zeros)
+      for (int i = tid; i < GRP * kHd; i += 256)
+        out[(static_cast<int64_t>(b) * nh + kh * GRP) * kHd + i] = 0;
+    return;
+  }
+  const int used = (len + chunk - 1) / chunk;  // <= splits: the host sizes chunk * splits >= cap
+  const int t1 = min(t0 + chunk, len);
+  const int n = t1 - t0;
+  const int dl = lane & 15;  // 8-dim slice of this lane
+  const int pl = lane >> 4;  // position within the wave's group of 4
   const uint16_t *kbase = k_cache + static_cast<int64_t>(bk) * cap * kHd + dl * 8;
   const uint16_t *vbase = v_cache + static_cast<int64_t>(bk) * cap * kHd + dl * 8;
 
   // query slices (fp32) of the GRP heads
   float qf[GRP][8];
+  if (ROPE) {
+    const uint16_t *row = qsrc + static_cast<int64_t>(b) * (nh + 2 * kvh) * kHd;
 #pragma unroll
-  for (int g = 0; g < GRP; ++g) {
-    const uint4 qv = *reinterpret_cast<const uint4 *>(q + (static_cast<int64_t>(b) * nh + kh * GRP + g) * kHd + dl * 8);
-    const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+    for (int g = 0; g < GRP; ++g)
+      rope8(*reinterpret_cast<const uint4 *>(row + (kh * GRP + g) * kHd + dl * 8), cos_t, sin_t, pos, dl, qf[g]);
+    if (s == used - 1 && tid < 32) {  // append: lanes 0-15 the rotated key, 16-31 the value
+      const int64_t crow = (static_cast<int64_t>(bk) * cap + pos) * kHd + dl * 8;
+      if (tid < 16) {
+        float kr[8];
+        rope8(*reinterpret_cast<const uint4 *>(row + (nh + kh) * kHd + dl * 8), cos_t, sin_t, pos, dl, kr);
+        uint32_t w[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[g][e] = mp_h2f(static_cast<uint16_t>(qw[e >> 1] >> (16 * (e & 1))));
+        for (int j = 0; j < 4; ++j)
+          w[j] = static_cast<uint32_t>(mp_f2h(kr[2 * j])) | (static_cast<uint32_t>(mp_f2h(kr[2 * j + 1])) << 16);
+        *reinterpret_cast<uint4 *>(k_cache + crow) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+        *reinterpret_cast<uint4 *>(v_cache + crow) =
+            *reinterpret_cast<const uint4 *>(row + (nh + kvh + kh) * kHd + dl * 8);
+      }
+    }
+    __syncthreads();  // the appended row is visible to this workgroup's cache loads
+  } else {
+#pragma unroll
+    for (int g = 0; g < GRP; ++g) {
+      const uint4 qv =
+          *reinterpret_cast<const uint4 *>(qsrc + (static_cast<int64_t>(b) * nh + kh * GRP + g) * kHd + dl * 8);
+      const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[g][e] = mp_h2f(static_cast<uint16_t>(qw[e >> 1] >> (16 * (e & 1))));
+    }
   }
 
   // ---- scores: steps of 16 positions per workgroup, 4 steps in flight
@@ -123,7 +193,15 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
       }
     }
   }
-  __syncthreads();
+  // first V step, in flight across the softmax (its barriers wait for LDS only)
+  uint4 vv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int t = u * 16 + wave * 4 + pl;
+    t = t < n ? t : n - 1;
+    vv[u] = *reinterpret_cast<const uint4 *>(vbase + static_cast<int64_t>(t0 + t) * kHd);
+  }
+  mp_lds_barrier();
 
   // ---- softmax statistics per head over the workgroup's positions
   float mx[GRP], sum[GRP];
@@ -133,9 +211,9 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
     for (int t = tid; t < n; t += 256) m = fmaxf(m, sc[g * chunk + t]);
     m = mp_wave_max(m);
     if (lane == 0) red[wave] = m;
-    __syncthreads();
+    mp_lds_barrier();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
+    mp_lds_barrier();
     float l = 0.f;
     for (int t = tid; t < n; t += 256) {
       const float p = expf(sc[g * chunk + t] - m);
@@ -145,9 +223,9 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
     if (lane == 0) red[wave] = l;
-    __syncthreads();
+    mp_lds_barrier();
     l = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
+    mp_lds_barrier();
     mx[g] = m;
     sum[g] = l;
   }
@@ -159,12 +237,13 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   for (int base = 0; base < n; base += 16 * U) {
-    uint4 vv[U];
+    if (base > 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int t = base + u * 16 + wave * 4 + pl;
-      t = t < n ? t : n - 1;
-      vv[u] = *reinterpret_cast<const uint4 *>(vbase + static_cast<int64_t>(t0 + t) * kHd);
+      for (int u = 0; u < U; ++u) {
+        int t = base + u * 16 + wave * 4 + pl;
+        t = t < n ? t : n - 1;
+        vv[u] = *reinterpret_cast<const uint4 *>(vbase + static_cast<int64_t>(t0 + t) * kHd);
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -189,48 +268,98 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
       acc[g][e] += __shfl_xor(acc[g][e], 16, 64);
       acc[g][e] += __shfl_xor(acc[g][e], 32, 64);
     }
-  __syncthreads();  // the score buffer is reused for the reduction
-  float *rw = sm;   // [GRP][4 waves][128]
+  mp_lds_barrier();  // the score buffer is reused for the reduction
+  float *rw = sm;    // [GRP][4 waves][128]
   if (pl == 0) {
 #pragma unroll
     for (int g = 0; g < GRP; ++g)
 #pragma unroll
       for (int e = 0; e < 8; ++e) rw[(g * 4 + wave) * kHd + dl * 8 + e] = acc[g][e];
   }
-  __syncthreads();
+  mp_lds_barrier();
+  const int64_t head0 = static_cast<int64_t>(b) * nh + kh * GRP;
+  if (splits == 1) {  // one split: normalise and store (what the merge computes for one split)
+    for (int i = tid; i < GRP * kHd; i += 256) {
+      const int g = i / kHd, d = i % kHd;
+      const float o = (rw[(g * 4 + 0) * kHd + d] + rw[(g * 4 + 1) * kHd + d]) +
+                      (rw[(g * 4 + 2) * kHd + d] + rw[(g * 4 + 3) * kHd + d]);
+      out[head0 * kHd + i] = mp_f2h(o / sum[g]);
+    }
+    return;
+  }
   for (int i = tid; i < GRP * kHd; i += 256) {
     const int g = i / kHd, d = i % kHd;
     const float o = (rw[(g * 4 + 0) * kHd + d] + rw[(g * 4 + 1) * kHd + d]) +
                     (rw[(g * 4 + 2) * kHd + d] + rw[(g * 4 + 3) * kHd + d]);
-    const int64_t head = static_cast<int64_t>(b) * nh + kh * GRP + g;
-    part_o[(head * splits + s) * kHd + d] = o;
+    part_o[((head0 + g) * splits + s) * kHd + d] = o;
     if (d == 0) {
-      part_ml[(head * splits + s) * 2 + 0] = mx[g];
-      part_ml[(head * splits + s) * 2 + 1] = sum[g];
+      part_ml[((head0 + g) * splits + s) * 2 + 0] = mx[g];
+      part_ml[((head0 + g) * splits + s) * 2 + 1] = sum[g];
     }
   }
 }
 
-// One 128-thread workgroup per (row, head): merge the used splits.
-__global__ __launch_bounds__(128) void attn_combine_kernel(const float *__restrict__ part_o,
-                                                           const float *__restrict__ part_ml,
-                                                           const int64_t *__restrict__ pos_p, int cap, int chunk,
-                                                           int splits, uint16_t *__restrict__ out) {
-  const int64_t head = blockIdx.x;
-  const int d = threadIdx.x;
-  const int64_t p1 = pos_p[0] + 1;
-  const int len = static_cast<int>(p1 < 0 ? 0 : (p1 > cap ? cap : p1));
-  int used = (len + chunk - 1) / chunk;
-  used = used < splits ? used : splits;
-  float m = -INFINITY;
-  for (int s = 0; s < used; ++s) m = fmaxf(m, part_ml[(head * splits + s) * 2]);
-  float num = 0.f, den = 0.f;
-  for (int s = 0; s < used; ++s) {
-    const float w = expf(part_ml[(head * splits + s) * 2] - m);
-    num = fmaf(w, part_o[(head * splits + s) * kHd + d], num);
-    den = fmaf(w, part_ml[(head * splits + s) * 2 + 1], den);
+// Merge of the used splits, one wave per (row, head), four heads per workgroup:
+// lanes take the splits' (m, l) pairs for the max and the weights
+// w_j = exp(m_j - max m), then each lane owns two dims and sums w_j o_j over the
+// splits with eight loads in flight.  Sums run in a fixed order, so the result
+// does not depend on timing.  An empty range (len 0) gives zeros.
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part_o,
+                                                         const float *__restrict__ part_ml,
+                                                         const int64_t *__restrict__ pos_p, int cap, int chunk,
+                                                         int splits, int rope, int64_t heads,
+                                                         uint16_t *__restrict__ out) {
+  __shared__ float wts[4][kMergeMaxSplits];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t head = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (head >= heads) return;  // wave-uniform; no barrier below
+  const int64_t pos = pos_p[0];
+  int len;
+  if (rope) {
+    len = (pos < 0 || pos >= cap) ? 0 : static_cast<int>(pos) + 1;
+  } else {
+    const int64_t p1 = pos + 1;
+    len = static_cast<int>(p1 < 0 ? 0 : (p1 > cap ? cap : p1));
   }
-  out[head * kHd + d] = mp_f2h(num / den);
+  const int used = (len + chunk - 1) / chunk;
+  uint32_t *o2 = reinterpret_cast<uint32_t *>(out + head * kHd) + lane;
+  if (used == 0) {
+    *o2 = 0u;
+    return;
+  }
+  const float *ml = part_ml + head * splits * 2;
+  float m = -INFINITY;
+  for (int j = lane; j < used; j += 64) m = fmaxf(m, ml[2 * j]);
+  m = mp_wave_max(m);
+  float den = 0.f;
+  for (int j = lane; j < used; j += 64) {
+    const float w = expf(ml[2 * j] - m);
+    wts[wave][j] = w;
+    den = fmaf(w, ml[2 * j + 1], den);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  const float2 *po = reinterpret_cast<const float2 *>(part_o + head * splits * kHd) + lane;
+  float n0 = 0.f, n1 = 0.f;
+  int j = 0;
+  for (; j + 8 <= used; j += 8) {
+    float2 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = po[(j + u) * (kHd / 2)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      n0 = fmaf(wts[wave][j + u], v[u].x, n0);
+      n1 = fmaf(wts[wave][j + u], v[u].y, n1);
+    }
+  }
+  for (; j < used; ++j) {
+    const float2 v = po[j * (kHd / 2)];
+    n0 = fmaf(wts[wave][j], v.x, n0);
+    n1 = fmaf(wts[wave][j], v.y, n1);
+  }
+  *o2 = static_cast<uint32_t>(mp_f2h(n0 / den)) | (static_cast<uint32_t>(mp_f2h(n1 / den)) << 16);
 }
 
 // ---------------------------------------------------------------- SiLU * up
@@ -267,58 +396,90 @@ extern "C" int mp_decode_rope_append(const void *qkv, int64_t batch, int nh, int
   return MP_OK;
 }
 
+// Workspace: partial o [B, nh, splits, 128] fp32 | partial (m, l) [B, nh, splits, 2] fp32.
 extern "C" size_t mp_decode_attention_workspace_bytes(int64_t batch, int nh, int splits) {
   if (batch <= 0 || nh <= 0 || splits <= 0) return 0;
   return static_cast<size_t>(batch) * nh * splits * (kHd + 2) * sizeof(float);
 }
 
-extern "C" int mp_decode_attention(const void *q, int64_t batch, int nh, int kvh, int head_dim, const void *k_cache,
-                                   const void *v_cache, const int64_t *pos, int64_t capacity, int splits, float scale,
-                                   void *out, void *workspace, size_t workspace_bytes, mp_stream_t stream) {
-  if (!q || !k_cache || !v_cache || !pos || !out || !workspace) return MP_ERR_ARG;
+namespace {
+
+// Shared launcher of the two attention entry points (ROPE: qsrc is the qkv row).
+int launch_decode_attention(bool rope, const void *qsrc, int64_t batch, int nh, int kvh, int head_dim,
+                            const void *cos_t, const void *sin_t, void *k_cache, void *v_cache, const int64_t *pos,
+                            int64_t capacity, int splits, float scale, void *out, void *workspace,
+                            size_t workspace_bytes, hipStream_t s) {
+  if (!qsrc || !k_cache || !v_cache || !pos || !out || !workspace) return MP_ERR_ARG;
+  if (rope && (!cos_t || !sin_t)) return MP_ERR_ARG;
   if (head_dim != kHd) return MP_ERR_SHAPE;
   if (batch <= 0 || nh <= 0 || kvh <= 0 || nh % kvh != 0 || capacity <= 0 || capacity > INT32_MAX) return MP_ERR_SHAPE;
   const int grp = nh / kvh;
   if (grp != 1 && grp != 2 && grp != 4 && grp != 8) return MP_ERR_SHAPE;
-  if (splits <= 0 || batch * kvh > 65535) return MP_ERR_SHAPE;
+  if (splits <= 0 || splits > kMergeMaxSplits || batch * kvh > 65535) return MP_ERR_SHAPE;
   const int chunk = static_cast<int>(mp_cdiv(capacity, splits));
   // scores [GRP][chunk] and the [GRP][4][128] reduction share the dynamic LDS
   const size_t lds = static_cast<size_t>(grp) * (chunk > 4 * kHd ? chunk : 4 * kHd) * sizeof(float);
   if (lds > 64 * 1024) return MP_ERR_SHAPE;
   if (workspace_bytes < mp_decode_attention_workspace_bytes(batch, nh, splits)) return MP_ERR_WORKSPACE;
-  if (!mp_aligned(q, 16) || !mp_aligned(k_cache, 16) || !mp_aligned(v_cache, 16) || !mp_aligned(workspace, 16))
+  if (!mp_aligned(qsrc, 16) || !mp_aligned(k_cache, 16) || !mp_aligned(v_cache, 16) || !mp_aligned(workspace, 16) ||
+      !mp_aligned(out, 4))
     return MP_ERR_ALIGN;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (rope && (!mp_aligned(cos_t, 8) || !mp_aligned(sin_t, 8))) return MP_ERR_ALIGN;
   float *part_o = static_cast<float *>(workspace);
   float *part_ml = part_o + static_cast<size_t>(batch) * nh * splits * kHd;
   const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(batch * kvh));
-  const auto *qp = static_cast<const uint16_t *>(q);
-  const auto *kp = static_cast<const uint16_t *>(k_cache);
-  const auto *vp = static_cast<const uint16_t *>(v_cache);
+  const auto *qp = static_cast<const uint16_t *>(qsrc);
+  const auto *cp = static_cast<const uint16_t *>(cos_t);
+  const auto *sp = static_cast<const uint16_t *>(sin_t);
+  auto *kp = static_cast<uint16_t *>(k_cache);
+  auto *vp = static_cast<uint16_t *>(v_cache);
+  auto *op = static_cast<uint16_t *>(out);
   const int cap = static_cast<int>(capacity);
-  switch (grp) {
-    case 1:
-      hipLaunchKernelGGL(decode_attn_kernel<1>, grid, dim3(256), lds, s, qp, kp, vp, pos, kvh, cap, chunk, splits,
-                         scale, part_o, part_ml);
-      break;
-    case 2:
-      hipLaunchKernelGGL(decode_attn_kernel<2>, grid, dim3(256), lds, s, qp, kp, vp, pos, kvh, cap, chunk, splits,
-                         scale, part_o, part_ml);
-      break;
-    case 4:
-      hipLaunchKernelGGL(decode_attn_kernel<4>, grid, dim3(256), lds, s, qp, kp, vp, pos, kvh, cap, chunk, splits,
-                         scale, part_o, part_ml);
-      break;
-    default:
-      hipLaunchKernelGGL(decode_attn_kernel<8>, grid, dim3(256), lds, s, qp, kp, vp, pos, kvh, cap, chunk, splits,
-                         scale, part_o, part_ml);
-      break;
+#define MP_ATTN_LAUNCH(G, R)                                                                                  \
+  hipLaunchKernelGGL((decode_attn_kernel<G, R>), grid, dim3(256), lds, s, qp, cp, sp, kp, vp, pos, kvh, cap, \
+                     chunk, splits, scale, part_o, part_ml, op)
+  if (rope) {
+    switch (grp) {
+      case 1: MP_ATTN_LAUNCH(1, true); break;
+      case 2: MP_ATTN_LAUNCH(2, true); break;
+      case 4: MP_ATTN_LAUNCH(4, true); break;
+      default: MP_ATTN_LAUNCH(8, true); break;
+    }
+  } else {
+    switch (grp) {
+      case 1: MP_ATTN_LAUNCH(1, false); break;
+      case 2: MP_ATTN_LAUNCH(2, false); break;
+      case 4: MP_ATTN_LAUNCH(4, false); break;
+      default: MP_ATTN_LAUNCH(8, false); break;
+    }
   }
+#undef MP_ATTN_LAUNCH
   MP_CHECK_LAUNCH();
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(batch * nh)), dim3(kHd), 0, s, part_o, part_ml,
-                     pos, cap, chunk, splits, static_cast<uint16_t *>(out));
-  MP_CHECK_LAUNCH();
+  if (splits > 1) {
+    const int64_t heads = batch * nh;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(static_cast<unsigned>(mp_cdiv(heads, 4))), dim3(256), 0, s, part_o,
+                       part_ml, pos, cap, chunk, splits, rope ? 1 : 0, heads, op);
+    MP_CHECK_LAUNCH();
+  }
   return MP_OK;
+}
+
+}  // namespace
+
+extern "C" int mp_decode_attention(const void *q, int64_t batch, int nh, int kvh, int head_dim, const void *k_cache,
+                                   const void *v_cache, const int64_t *pos, int64_t capacity, int splits, float scale,
+                                   void *out, void *workspace, size_t workspace_bytes, mp_stream_t stream) {
+  return launch_decode_attention(false, q, batch, nh, kvh, head_dim, nullptr, nullptr, const_cast<void *>(k_cache),
+                                 const_cast<void *>(v_cache), pos, capacity, splits, scale, out, workspace,
+                                 workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int mp_decode_rope_attention(const void *qkv, int64_t batch, int nh, int kvh, int head_dim,
+                                        const void *cos_t, const void *sin_t, const int64_t *pos, int64_t capacity,
+                                        void *k_cache, void *v_cache, int splits, float scale, void *out,
+                                        void *workspace, size_t workspace_bytes, mp_stream_t stream) {
+  return launch_decode_attention(true, qkv, batch, nh, kvh, head_dim, cos_t, sin_t, k_cache, v_cache, pos, capacity,
+                                 splits, scale, out, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, mp_stream_t stream) {

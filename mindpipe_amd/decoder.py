@@ -176,9 +176,8 @@ class W4Decoder:
             else:
                 hn, _, _, x = ops.add_rms_norm_quant(delta, x, l["ln1"], cfg.eps, quant=False)
             qkv = l["qkv"](hn)
-            q = ops.decode_rope_append(qkv, nh, kvh, self.cos, self.sin, cur_len, self.k_cache[li, :b],
-                                       self.v_cache[li, :b])
-            att = ops.decode_attention(q, self.k_cache[li, :b], self.v_cache[li, :b], cur_len, splits, scale, ws)
+            att = ops.decode_rope_attention(qkv, nh, kvh, self.cos, self.sin, cur_len, self.k_cache[li, :b],
+                                            self.v_cache[li, :b], splits, scale, ws)
             hn, _, _, x = ops.add_rms_norm_quant(l["o"](att.reshape(b, nh * hd)), x, l["ln2"], cfg.eps, quant=False)
             delta = l["down"](ops.silu_mul(l["gate_up"](hn)))
         hn, _, _, x = ops.add_rms_norm_quant(delta, x, self.norm, cfg.eps, quant=False)

@@ -377,6 +377,7 @@ def decode_rope_append(qkv: torch.Tensor, nh: int, kvh: int, cos_t: torch.Tensor
 
 
 def decode_attention_workspace(batch: int, nh: int, splits: int, device) -> torch.Tensor:
+    """Workspace of the decode attention: the splits' partial outputs and statistics."""
     nbytes = _lib.load().mp_decode_attention_workspace_bytes(batch, nh, splits)
     return torch.empty((nbytes // 4,), dtype=torch.float32, device=device)
 
@@ -393,6 +394,24 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
             q.data_ptr(), b, nh, kvh, hd, k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr(), cap, splits,
             float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * 4, _stream()),
             "mp_decode_attention")
+    return out
+
+
+def decode_rope_attention(qkv: torch.Tensor, nh: int, kvh: int, cos_t: torch.Tensor, sin_t: torch.Tensor,
+                          pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, splits: int, scale: float,
+                          workspace: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``decode_rope_append`` + ``decode_attention`` in one launch: RoPE on the q/k heads of
+    ``qkv [B, (nh+2kvh)*128]``, k/v appended at ``pos``, attention over ``[0, pos]``;
+    returns ``[B, nh, 128]`` fp16."""
+    b = qkv.shape[0]
+    cap = k_cache.shape[2]
+    if out is None:
+        out = torch.empty((b, nh, 128), dtype=torch.float16, device=qkv.device)
+    with _dev(qkv):
+        _lib.check(_lib.load().mp_decode_rope_attention(
+            qkv.data_ptr(), b, nh, kvh, 128, cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(), cap,
+            k_cache.data_ptr(), v_cache.data_ptr(), splits, float(scale), out.data_ptr(), workspace.data_ptr(),
+            workspace.numel() * 4, _stream()), "mp_decode_rope_attention")
     return out
 
 

@@ -1,5 +1,6 @@
 """GPU tests of the decode-step harness kernels (RoPE + KV append, split-K decode
-attention, SiLU-mul) and of one decoder step on them against the PyTorch step.
+attention with its in-launch split merge, the fused RoPE + append + attention
+launch, SiLU-mul) and of one decoder step on them against the PyTorch step.
 
 Bars: RoPE and the cache writes are bit-exact to the same fp16 op sequence in
 PyTorch; attention has relative Frobenius error <= 1e-3 against fp32 softmax
@@ -85,6 +86,70 @@ def test_decode_attention_matches_fp32(b, nh, kvh, cap, pos, splits):
     ref = torch.matmul(torch.softmax(s, -1), vc[:, :, :pos + 1].float()).reshape(b, nh, hd)
     err = _rel(out.float(), ref)
     assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("b,nh,kvh,cap,pos,splits", [(1, 4, 4, 300, 0, 8), (2, 8, 2, 300, 299, 1),
+                                                     (3, 8, 1, 257, 130, 5), (1, 32, 32, 2304, 2047, 32),
+                                                     (1, 64, 8, 4096, 4000, 100), (2, 16, 2, 640, 64, 10)])
+def test_decode_rope_attention_equals_two_launch_path(b, nh, kvh, cap, pos, splits):
+    """The fused RoPE + append + attention launch writes the same cache rows and the
+    same output bits as rope_append followed by attention (one kernel body)."""
+    _say("decode_rope_attention", b, nh, kvh, cap, pos, splits)
+    from mindpipe_amd import ops
+    hd = 128
+    g = torch.Generator(device=DEV).manual_seed(4)
+    qkv = torch.randn(b, (nh + 2 * kvh) * hd, device=DEV, generator=g).half()
+    cos, sin = _tables(cap)
+    kc = torch.randn(b, kvh, cap, hd, device=DEV, generator=g).half()
+    vc = torch.randn(b, kvh, cap, hd, device=DEV, generator=g).half()
+    k2, v2 = kc.clone(), vc.clone()
+    p = torch.tensor([pos], device=DEV, dtype=torch.int64)
+    scale = 1.0 / math.sqrt(hd)
+    ws = ops.decode_attention_workspace(b, nh, splits, DEV)
+    out = ops.decode_rope_attention(qkv, nh, kvh, cos, sin, p, kc, vc, splits, scale, ws)
+    q = ops.decode_rope_append(qkv, nh, kvh, cos, sin, p, k2, v2)
+    ref = ops.decode_attention(q, k2, v2, p, splits, scale, ws)
+    assert torch.equal(kc, k2) and torch.equal(vc, v2)
+    assert torch.equal(out, ref)
+    # a second call gives the same bits
+    out2 = ops.decode_rope_attention(qkv, nh, kvh, cos, sin, p, kc, vc, splits, scale, ws)
+    assert torch.equal(out2, out)
+    # and the fp32 attention over [0, pos] agrees
+    grp = nh // kvh
+    qf = q.float().reshape(b, kvh, grp, hd)
+    s = torch.matmul(qf, kc[:, :, :pos + 1].float().transpose(-1, -2).contiguous()) * scale
+    want = torch.matmul(torch.softmax(s, -1), vc[:, :, :pos + 1].float()).reshape(b, nh, hd)
+    assert _rel(out.float(), want) <= 1e-3
+
+
+def test_decode_attention_workspace_reuse_and_edges():
+    """One workspace across calls with different used-split counts; an empty range
+    gives zeros; a position outside the cache appends nothing and gives zeros in the
+    fused launch."""
+    _say("decode_attention workspace reuse")
+    from mindpipe_amd import ops
+    b, nh, kvh, cap, hd, splits = 2, 8, 2, 500, 128, 16
+    g = torch.Generator(device=DEV).manual_seed(5)
+    kc = torch.randn(b, kvh, cap, hd, device=DEV, generator=g).half()
+    vc = torch.randn(b, kvh, cap, hd, device=DEV, generator=g).half()
+    q = torch.randn(b, nh, hd, device=DEV, generator=g).half()
+    scale = 1.0 / math.sqrt(hd)
+    ws = ops.decode_attention_workspace(b, nh, splits, DEV)
+    grp = nh // kvh
+    for pos in [499, 3, 40, 0, 250, 31, 32, 499]:
+        out = ops.decode_attention(q, kc, vc, torch.tensor([pos], device=DEV), splits, scale, ws)
+        qf = q.float().reshape(b, kvh, grp, hd)
+        s = torch.matmul(qf, kc[:, :, :pos + 1].float().transpose(-1, -2).contiguous()) * scale
+        want = torch.matmul(torch.softmax(s, -1), vc[:, :, :pos + 1].float()).reshape(b, nh, hd)
+        assert _rel(out.float(), want) <= 1e-3, pos
+    out = ops.decode_attention(q, kc, vc, torch.tensor([-1], device=DEV), splits, scale, ws)
+    assert not out.any()
+    qkv = torch.randn(b, (nh + 2 * kvh) * hd, device=DEV, generator=g).half()
+    cos, sin = _tables(cap)
+    k0, v0 = kc.clone(), vc.clone()
+    out = ops.decode_rope_attention(qkv, nh, kvh, cos, sin, torch.tensor([cap], device=DEV), kc, vc, splits,
+                                    scale, ws)
+    assert not out.any() and torch.equal(kc, k0) and torch.equal(vc, v0)
 
 
 def test_silu_mul_within_one_ulp():
