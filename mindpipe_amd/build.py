@@ -33,9 +33,17 @@ FLAGS = [
 ]
 
 
+# Per-source extra flags.  w4a16.hip: MFMA results in ordinary VGPRs (its
+# kernels scale every MFMA result in VALU code; results in accumulation registers
+# would each need a copy first).
+FILE_FLAGS = {
+    "w4a16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")

@@ -91,5 +91,24 @@ __device__ __forceinline__ void mp_lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// ---- raw buffer loads
+// Buffer resource over [p, p + bytes) (gfx9 descriptor word 3: 32-bit data
+// format); a load at an offset past `bytes` returns zeros.  The per-lane part of
+// an address goes in voff, a wave-uniform part in soff (a scalar register: the
+// caller guarantees uniformity, readfirstlane only tells the compiler).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mp_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 mp_buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+  const u4v v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff),
+                                                      __builtin_amdgcn_readfirstlane(static_cast<int>(soff)), 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t mp_buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff),
+                                              __builtin_amdgcn_readfirstlane(static_cast<int>(soff)), 0);
+}
+
 // LDS budget (bytes) for an activation chunk staged by the decode kernels.
 constexpr int kMpXLdsBudget = 60 * 1024;

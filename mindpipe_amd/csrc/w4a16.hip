@@ -454,52 +454,68 @@ __global__ __launch_bounds__(512) void w4a16_decode_kernel(
 //
 // For small batches the activation bytes per weight byte grow with M, so the
 // activations are not staged per 16-column tile: each wave owns NT column
-// tiles (16 columns each) and a contiguous K range, loads its activation
-// fragments straight from L2 into registers (once per 128-column block, reused
-// by the NT tiles) and gets the per-row block sums from an MFMA against ones.
-// S waves of a workgroup split K; their partial sums meet in LDS.  Scales and
-// zeros come as 32-bit words holding two consecutive groups.
+// tiles (16 columns each) and a contiguous K range of whole 8-block steps, loads
+// its activation fragments straight from L2 into registers (once per 128-column
+// block, reused by the NT tiles) and gets the per-row block sums from an MFMA
+// against ones.  S waves of a workgroup split K; their partial sums meet in LDS.
+//
+// Load costs set the structure: a vector-memory instruction whose 64 lanes touch
+// 16 rows costs the CU several times the issue slots of one reading a contiguous
+// 1 KB, so the kernel keeps their number per weight byte low.  The scales and
+// zeros of a tile come as one 16-byte load per 8 blocks (8 groups), and NT tiles
+// share each activation load.  All loads are raw buffer loads: the per-lane part
+// of an address is fixed, the block offset is a wave-uniform scalar, and blocks
+// past the wave's range point beyond the buffer, where loads return zeros without
+// a memory access (no branches around loads: a join makes the compiler wait for
+// every outstanding load).  Each block pair's activation loads are issued before
+// the next pair's weight prefetch, so a compute step waits for its own data only.
+// Activation rows past M read row M-1: MFMA output rows depend only on their own
+// activation row, and those rows are never stored.
 template <int MT, int NT, int S, bool ZP>
 __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
-  constexpr int U = 2;  // blocks per prefetch buffer (even: one scale word per pair)
+  constexpr int U = 2;     // blocks per prefetch buffer
+  constexpr int STEP = 8;  // blocks per scale / zero vector
   __shared__ float red[S > 1 ? S : 1][MT * NT * 4][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kq = lane >> 4;
-  const int kw = k >> 3;
+  const uint32_t kw = static_cast<uint32_t>(k) >> 3;
   const int nblk = k >> 7;
   const int col0 = blockIdx.x * NT * 16;
-  // contiguous, even-aligned K block range of this wave
-  const int lo = ((nblk * wave) / S) & ~1;
-  const int hi = wave == S - 1 ? nblk : (((nblk * (wave + 1)) / S) & ~1);
-  const int nmine = hi - lo;
-  const int blast = nblk - 1;
+  // K range of this wave: whole steps; blocks at or past nblk are dead
+  const int nst = (nblk + STEP - 1) / STEP;
+  const int st_lo = (nst * wave) / S;
+  const int nsteps = (nst * (wave + 1)) / S - st_lo;
+  const int lo = st_lo * STEP;
   uint32_t magic_v = kMagic, mask_v = 0x000F000Fu;
   asm volatile("" : "+v"(magic_v), "+v"(mask_v));
   const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
-  const h8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
 
-  const uint32_t *wrow[NT];
-  const uint32_t *srow[NT];
-  const uint32_t *zrow[NT];
+  // buffer resources (the host checks that every size fits 32 bits)
+  const uint32_t wbytes = static_cast<uint32_t>(n_cols) * kw * 4u;
+  const uint32_t xbytes = static_cast<uint32_t>(m_rows) * static_cast<uint32_t>(k) * 2u;
+  const uint32_t sbytes = static_cast<uint32_t>(n_cols) * static_cast<uint32_t>(n_groups) * 2u;
+  const auto wr = mp_rsrc(wq, wbytes);
+  const auto xr = mp_rsrc(x, xbytes);
+  const auto sr = mp_rsrc(sc, sbytes);
+  const auto zrr = mp_rsrc(ZP ? zr : sc, sbytes);
+  uint32_t woff[NT], soff[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
     int n = col0 + j * 16 + (lane & 15);
     n = n < n_cols ? n : n_cols - 1;
-    wrow[j] = wq + static_cast<int64_t>(n) * kw + 4 * kq;
-    srow[j] = reinterpret_cast<const uint32_t *>(sc + static_cast<int64_t>(n) * n_groups);
-    zrow[j] = reinterpret_cast<const uint32_t *>(ZP ? zr + static_cast<int64_t>(n) * n_groups : sc);
+    woff[j] = (static_cast<uint32_t>(n) * kw + 4u * kq) * 4u;
+    soff[j] = static_cast<uint32_t>(n) * static_cast<uint32_t>(n_groups) * 2u;
   }
-  const uint16_t *xrow[MT];
-  bool xval[MT];
+  uint32_t xoff[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    const int m = t * 16 + (lane & 15);
-    xval[t] = m < m_rows;
-    xrow[t] = x + static_cast<int64_t>(xval[t] ? m : 0) * k + 32 * kq;
+    int m = t * 16 + (lane & 15);
+    m = m < m_rows ? m : m_rows - 1;
+    xoff[t] = (static_cast<uint32_t>(m) * static_cast<uint32_t>(k) + 32u * kq) * 2u;
   }
 
   f4_t acc[MT][NT];
@@ -508,32 +524,39 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[t][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
+  // block b (absolute) -> scalar byte offsets; dead blocks point past the buffers
+  auto woffs = [&](int b) { return b < nblk ? static_cast<uint32_t>(b) * 64u : wbytes; };
+  auto xoffs = [&](int b) { return b < nblk ? static_cast<uint32_t>(b) * 256u : xbytes; };
   uint4 wa[U][NT], wb[U][NT];
-  uint32_t sa[NT], za[NT], sb[NT], zb[NT];
-  auto issue = [&](uint4 (*w)[NT], uint32_t *s2, uint32_t *z2, int r0) {
+  auto issue_w = [&](uint4 (*w)[NT], int b0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int b = lo + r0 + u;
-      b = b < blast ? b : blast;
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int j = 0; j < NT; ++j) w[u][j] = *reinterpret_cast<const uint4 *>(wrow[j] + b * 16);
-    }
-    int b0 = lo + r0;
-    b0 = b0 < blast ? b0 : blast - 1;
+      for (int j = 0; j < NT; ++j) w[u][j] = mp_buf_load16(wr, woff[j], woffs(b0 + u));
+  };
+  uint4 xa[U][MT][4];
+  auto load_x = [&](int b0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xa[u][t][q] = mp_buf_load16(xr, xoff[t] + 16u * q, xoffs(b0 + u));
+  };
+  // scale / zero vectors (groups b0 .. b0+7 of each tile row; 4-byte aligned rows)
+  uint4 sv[NT], zv[NT];
+  auto load_sz = [&](int b0) {
+    const uint32_t so = b0 < nblk ? static_cast<uint32_t>(b0) * 2u : sbytes;
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      s2[j] = srow[j][b0 >> 1];
-      if (ZP) z2[j] = zrow[j][b0 >> 1];
+      sv[j] = mp_buf_load16(sr, soff[j], so);
+      if (ZP) zv[j] = mp_buf_load16(zrr, soff[j], so);
     }
   };
-  auto compute = [&](uint4 (*w)[NT], const uint32_t *s2, const uint32_t *z2, int r0) {
+  // pair p (0..3) of the current step
+  auto compute = [&](uint4 (*w)[NT], int p) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int r = r0 + u;
-      const bool live = r < nmine;
-      int b = lo + r;
-      b = b < blast ? b : blast;
-      // activation fragments of this block for every m tile, and their row sums
       h8_t af[MT][4];
       f4_t cs[MT];
 #pragma unroll
@@ -541,18 +564,17 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
         cs[t] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const uint4 d = *reinterpret_cast<const uint4 *>(xrow[t] + b * 128 + 8 * q);
-          h8_t a = perm_to_magic(d);
-          af[t][q] = xval[t] ? a : zero8;
+          af[t][q] = perm_to_magic(xa[u][t][q]);
           cs[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][q], ones, cs[t], 0, 0, 0);
         }
       }
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
+        const uint32_t sw = p == 0 ? sv[j].x : (p == 1 ? sv[j].y : (p == 2 ? sv[j].z : sv[j].w));
+        const uint32_t zw = p == 0 ? zv[j].x : (p == 1 ? zv[j].y : (p == 2 ? zv[j].z : zv[j].w));
+        const float su = mp_h2f(static_cast<uint16_t>(sw >> (16 * u)));
+        const float zu = 1024.0f + (ZP ? mp_h2f(static_cast<uint16_t>(zw >> (16 * u))) : 8.0f);
         const uint32_t wsel[4] = {w[u][j].x, w[u][j].y, w[u][j].z, w[u][j].w};
-        const int sh = ((b - (lo + r0)) & 1) * 16;
-        const float su = live ? mp_h2f(static_cast<uint16_t>(s2[j] >> sh)) : 0.0f;
-        const float zu = 1024.0f + (ZP ? mp_h2f(static_cast<uint16_t>(z2[j] >> sh)) : 8.0f);
         h8_t bq[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) bq[q] = dq_magic_fast(wsel[q], mask_v, magic_v);
@@ -568,16 +590,38 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     }
   };
 
-  const int ngrp = (nmine + U - 1) / U;
-  issue(wa, sa, za, 0);
-  for (int g = 0; g < ngrp; g += 2) {
-    if (g + 1 < ngrp) issue(wb, sb, zb, (g + 1) * U);
+  // Steps of 4 block pairs, fully unrolled inside: each prefetch is used in the
+  // basic block that issues it; scheduling barriers keep every group of loads
+  // where it is written.  Dead blocks (past nblk) read zeros: zero scale, no
+  // contribution.
+  issue_w(wa, lo);
+  for (int st = 0; st < nsteps; ++st) {
+    const int b = lo + st * STEP;
+    load_sz(b);
+    load_x(b);
     __builtin_amdgcn_sched_barrier(0);
-    compute(wa, sa, za, g * U);
-    if (g + 1 >= ngrp) break;
-    if (g + 2 < ngrp) issue(wa, sa, za, (g + 2) * U);
+    issue_w(wb, b + 2);
     __builtin_amdgcn_sched_barrier(0);
-    compute(wb, sb, zb, (g + 1) * U);
+    compute(wa, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_x(b + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_w(wa, b + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(wb, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_x(b + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_w(wb, b + 6);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(wa, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    load_x(b + 6);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_w(wa, st + 1 < nsteps ? b + STEP : nblk);  // the last prefetch reads nothing
+    __builtin_amdgcn_sched_barrier(0);
+    compute(wb, 3);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   if (S > 1) {
@@ -961,6 +1005,19 @@ static int mp_gemv_env(int which) {
   return v[which];
 }
 
+// Batched-kernel shape knobs (for measurements): MP_W4_BATCH_NT (column tiles per
+// wave), MP_W4_BATCH_S (waves splitting K), MP_W4_BATCH_WAVES (target wave count),
+// MP_W4_BATCH_ALWAYS=1 (batched kernel for every N).
+static int mp_batch_env(int which) {
+  static const int v[4] = {
+      getenv("MP_W4_BATCH_NT") ? atoi(getenv("MP_W4_BATCH_NT")) : 0,
+      getenv("MP_W4_BATCH_S") ? atoi(getenv("MP_W4_BATCH_S")) : 0,
+      getenv("MP_W4_BATCH_WAVES") ? atoi(getenv("MP_W4_BATCH_WAVES")) : 1024,
+      getenv("MP_W4_BATCH_ALWAYS") ? atoi(getenv("MP_W4_BATCH_ALWAYS")) : 0,
+  };
+  return v[which];
+}
+
 static int mp_batch_min_m() {
   static int v = [] {
     const char *e = getenv("MP_W4_BATCH_MIN_M");
@@ -1056,7 +1113,7 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
   const int n_groups_i = n_groups;
   const int batch_min_m = mp_batch_min_m();
   // batched kernel: small N (activation staging per 16-column tile would dominate) or M >= 32
-  const bool batch_shape = m >= 32 || n <= 16384;
+  const bool batch_shape = m >= 32 || n <= 16384 || mp_batch_env(3);
   if (m == 1 && mp_gemv_env(0) == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
     const int ki = static_cast<int>(k), ni = static_cast<int>(n);
     const int nch = (ki + 2047) / 2048;  // 2048-wide K chunks
@@ -1104,16 +1161,21 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
 #undef MP_W4_GEMV_C
 #undef MP_W4_GEMV
   } else if (m > batch_min_m && batch_shape && m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 &&
-      aligned) {
+      aligned && n * (k / 2) < (int64_t(1) << 32) && m * k * 2 < (int64_t(1) << 32)) {
     const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
     const int nblk = ki / 128;
     const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
     // column tiles per wave (activation reuse): 4 for 17..32 rows once N is large enough to fill the chip
-    const int nt = (mt == 2 && n >= 8192) ? 4 : 2;
-    const int smax = mt * nt >= 8 ? 8 : 16;            // LDS reduction buffer <= 64 KB
+    // column tiles per wave (measured on the 7B decode shapes, M = 8..64): one for N <= 4096
+    // (enough workgroups), four from N = 12288 (activation loads shared by more tiles)
+    int nt = n <= 4096 ? 1 : (n >= 12288 ? 4 : 2);
+    if (mp_batch_env(0) > 0) nt = mp_batch_env(0) >= 4 ? 4 : mp_batch_env(0);
+    const int smax = mt * nt >= 8 ? 4 : (mt * nt > 1 ? 8 : 16);  // register budget per wave count
     const int64_t groups = mp_cdiv(n, 16 * nt);
-    int split = 1;                                     // waves splitting K: ~2048 waves, >= 2 blocks each
-    while (split < smax && groups * split < 2048 && nblk / (split * 2) >= 2) split *= 2;
+    const int nsteps = (nblk + 7) / 8;                 // 8-block steps (one scale vector each)
+    int split = 1;                                     // waves splitting K: ~1024 waves, >= 1 step each
+    while (split < smax && groups * split < mp_batch_env(2) && nsteps / (split * 2) >= 1) split *= 2;
+    if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
     const dim3 grid(static_cast<unsigned>(groups));
 #define MP_W4_BATCH(MT_, NT_, S_)                                                                            \
   do {                                                                                                       \
@@ -1124,29 +1186,28 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
       hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, wp, \
                          ni, sp, zp, n_groups_i, bp, yp);                                                    \
   } while (0)
+#define MP_W4_BATCH_S(MT_, NT_)                    \
+  do {                                             \
+    if (split == 1) MP_W4_BATCH(MT_, NT_, 1);      \
+    else if (split == 2) MP_W4_BATCH(MT_, NT_, 2); \
+    else if (split == 4) MP_W4_BATCH(MT_, NT_, 4); \
+    else if (split == 8 || MT_ * NT_ > 1) MP_W4_BATCH(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : 8)); \
+    else MP_W4_BATCH(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : (MT_ * NT_ > 1 ? 8 : 16))); \
+  } while (0)
     if (mt == 1) {
-      if (split == 1) MP_W4_BATCH(1, 2, 1);
-      else if (split == 2) MP_W4_BATCH(1, 2, 2);
-      else if (split == 4) MP_W4_BATCH(1, 2, 4);
-      else if (split == 8) MP_W4_BATCH(1, 2, 8);
-      else MP_W4_BATCH(1, 2, 16);
-    } else if (mt == 2 && nt == 4) {
-      if (split == 1) MP_W4_BATCH(2, 4, 1);
-      else if (split == 2) MP_W4_BATCH(2, 4, 2);
-      else if (split == 4) MP_W4_BATCH(2, 4, 4);
-      else MP_W4_BATCH(2, 4, 8);
+      if (nt == 1) MP_W4_BATCH_S(1, 1);
+      else if (nt == 2) MP_W4_BATCH_S(1, 2);
+      else MP_W4_BATCH_S(1, 4);
     } else if (mt == 2) {
-      if (split == 1) MP_W4_BATCH(2, 2, 1);
-      else if (split == 2) MP_W4_BATCH(2, 2, 2);
-      else if (split == 4) MP_W4_BATCH(2, 2, 4);
-      else if (split == 8) MP_W4_BATCH(2, 2, 8);
-      else MP_W4_BATCH(2, 2, 16);
+      if (nt == 1) MP_W4_BATCH_S(2, 1);
+      else if (nt == 2) MP_W4_BATCH_S(2, 2);
+      else MP_W4_BATCH_S(2, 4);
     } else {
-      if (split == 1) MP_W4_BATCH(4, 2, 1);
-      else if (split == 2) MP_W4_BATCH(4, 2, 2);
-      else if (split == 4) MP_W4_BATCH(4, 2, 4);
-      else MP_W4_BATCH(4, 2, 8);
+      if (nt == 1) MP_W4_BATCH_S(4, 1);
+      else if (nt == 2) MP_W4_BATCH_S(4, 2);
+      else MP_W4_BATCH_S(4, 4);
     }
+#undef MP_W4_BATCH_S
 #undef MP_W4_BATCH
   } else if (m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
     const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
