@@ -452,35 +452,37 @@ __global__ __launch_bounds__(512) void w4a16_decode_kernel(
 
 // ------------------------------------------------------------------ batched decode (4 < M <= 64)
 //
-// For small batches the activation bytes per weight byte grow with M, so the
-// activations are not staged per 16-column tile: each wave owns NT column
-// tiles (16 columns each) and a contiguous K range of whole 8-block steps, loads
-// its activation fragments straight from L2 into registers (once per 128-column
-// block, reused by the NT tiles) and gets the per-row block sums from an MFMA
-// against ones.  S waves of a workgroup split K; their partial sums meet in LDS.
+// For small batches the activation bytes per weight byte grow with M: each wave
+// owns NT column tiles (16 columns each) and a contiguous K range of whole 8-block
+// steps, loads its activations once per 128-column block (reused by the NT tiles)
+// and gets the per-row block sums from an MFMA against ones.  S waves of a
+// workgroup split K; their partial sums meet in LDS.
 //
 // Load costs set the structure: a vector-memory instruction whose 64 lanes touch
 // 16 rows costs the CU several times the issue slots of one reading a contiguous
 // 1 KB, so the kernel keeps their number per weight byte low.  The scales and
-// zeros of a tile come as one 16-byte load per 8 blocks (8 groups), and NT tiles
-// share each activation load.  All loads are raw buffer loads: the per-lane part
-// of an address is fixed, the block offset is a wave-uniform scalar, and blocks
-// past the wave's range point beyond the buffer, where loads return zeros without
-// a memory access (no branches around loads: a join makes the compiler wait for
-// every outstanding load).  Each block pair's activation loads are issued before
-// the next pair's weight prefetch, so a compute step waits for its own data only.
-// Activation rows past M read row M-1: MFMA output rows depend only on their own
-// activation row, and those rows are never stored.
+// zeros of a tile come as one 16-byte load per 8 blocks (8 groups); activations
+// come as contiguous row pieces (4 rows x 256 bytes per load, zeros past M) and
+// reach the MFMA layout through the wave's LDS region.  All loads are raw buffer
+// loads: the per-lane part of an address is fixed, the block offset is a
+// wave-uniform scalar, and blocks past the wave's range point beyond the buffer,
+// where loads return zeros without a memory access (no branches around loads: a
+// join makes the compiler wait for every outstanding load).  Each block pair's
+// activation loads are issued before the next pair's weight prefetch, so a
+// compute step waits for its own data only.
 template <int MT, int NT, int S, bool ZP>
 __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
-  constexpr int U = 2;     // blocks per prefetch buffer
-  constexpr int STEP = 8;  // blocks per scale / zero vector
+  constexpr int U = 2;        // blocks per prefetch buffer
+  constexpr int STEP = 8;     // blocks per scale / zero vector
+  constexpr int XI = 4 * MT;  // activation loads per block (4 rows x 256 bytes each)
   __shared__ float red[S > 1 ? S : 1][MT * NT * 4][64];
+  __shared__ uint4 xst[S][16 * MT * 16];  // per wave: one block of 16 MT rows x 256 bytes
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint4 *xsw = xst[wave];
   const int kq = lane >> 4;
   const uint32_t kw = static_cast<uint32_t>(k) >> 3;
   const int nblk = k >> 7;
@@ -510,12 +512,13 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     woff[j] = (static_cast<uint32_t>(n) * kw + 4u * kq) * 4u;
     soff[j] = static_cast<uint32_t>(n) * static_cast<uint32_t>(n_groups) * 2u;
   }
-  uint32_t xoff[MT];
+  // activation load i, lane l: row 4 i + l / 16, 16-byte piece l % 16 of the block
+  // (rows past M point beyond the buffer: zeros, no memory access)
+  uint32_t xoff[XI];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    int m = t * 16 + (lane & 15);
-    m = m < m_rows ? m : m_rows - 1;
-    xoff[t] = (static_cast<uint32_t>(m) * static_cast<uint32_t>(k) + 32u * kq) * 2u;
+  for (int i = 0; i < XI; ++i) {
+    const int m = 4 * i + (lane >> 4);
+    xoff[i] = m < m_rows ? (static_cast<uint32_t>(m) * static_cast<uint32_t>(k) + 8u * (lane & 15)) * 2u : xbytes;
   }
 
   f4_t acc[MT][NT];
@@ -534,14 +537,12 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
 #pragma unroll
       for (int j = 0; j < NT; ++j) w[u][j] = mp_buf_load16(wr, woff[j], woffs(b0 + u));
   };
-  uint4 xa[U][MT][4];
+  uint4 xa[U][XI];
   auto load_x = [&](int b0) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) xa[u][t][q] = mp_buf_load16(xr, xoff[t] + 16u * q, xoffs(b0 + u));
+      for (int i = 0; i < XI; ++i) xa[u][i] = mp_buf_load16(xr, xoff[i], xoffs(b0 + u));
   };
   // scale / zero vectors (groups b0 .. b0+7 of each tile row; 4-byte aligned rows)
   uint4 sv[NT], zv[NT];
@@ -557,14 +558,25 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   auto compute = [&](uint4 (*w)[NT], int p) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      // transpose through the wave's LDS region into the MFMA layout (lane (m, kq), piece q
+      // = row m, K [32 kq + 8 q, +8)); piece c of row r sits at slot c ^ (r % 16), so
+      // the writes (16 pieces of one row) and the reads (16 rows, one piece) each
+      // cover all 16 bank groups.  One wave writes and reads the region and its LDS
+      // accesses execute in order: no barrier.
+#pragma unroll
+      for (int i = 0; i < XI; ++i) {
+        const int r = 4 * i + (lane >> 4);
+        xsw[r * 16 + ((lane & 15) ^ (r & 15))] = xa[u][i];
+      }
       h8_t af[MT][4];
       f4_t cs[MT];
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
         cs[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+        const int r = 16 * t + (lane & 15);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          af[t][q] = perm_to_magic(xa[u][t][q]);
+          af[t][q] = perm_to_magic(xsw[r * 16 + ((4 * kq + q) ^ (r & 15))]);
           cs[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][q], ones, cs[t], 0, 0, 0);
         }
       }
@@ -1007,13 +1019,13 @@ static int mp_gemv_env(int which) {
 
 // Batched-kernel shape knobs (for measurements): MP_W4_BATCH_NT (column tiles per
 // wave), MP_W4_BATCH_S (waves splitting K), MP_W4_BATCH_WAVES (target wave count),
-// MP_W4_BATCH_ALWAYS=1 (batched kernel for every N).
+// MP_W4_BATCH_ALWAYS=0 (LDS-staged decode kernel above N = 16384 for M < 32).
 static int mp_batch_env(int which) {
   static const int v[4] = {
       getenv("MP_W4_BATCH_NT") ? atoi(getenv("MP_W4_BATCH_NT")) : 0,
       getenv("MP_W4_BATCH_S") ? atoi(getenv("MP_W4_BATCH_S")) : 0,
       getenv("MP_W4_BATCH_WAVES") ? atoi(getenv("MP_W4_BATCH_WAVES")) : 1024,
-      getenv("MP_W4_BATCH_ALWAYS") ? atoi(getenv("MP_W4_BATCH_ALWAYS")) : 0,
+      getenv("MP_W4_BATCH_ALWAYS") ? atoi(getenv("MP_W4_BATCH_ALWAYS")) : 1,
   };
   return v[which];
 }
@@ -1112,7 +1124,8 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
                        (zeros == nullptr || mp_aligned(zeros, 4));
   const int n_groups_i = n_groups;
   const int batch_min_m = mp_batch_min_m();
-  // batched kernel: small N (activation staging per 16-column tile would dominate) or M >= 32
+  // batched kernel for every N (MP_W4_BATCH_ALWAYS=0: the LDS-staged kernel for
+  // N > 16384 below 32 rows, for measurements)
   const bool batch_shape = m >= 32 || n <= 16384 || mp_batch_env(3);
   if (m == 1 && mp_gemv_env(0) == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
     const int ki = static_cast<int>(k), ni = static_cast<int>(n);
