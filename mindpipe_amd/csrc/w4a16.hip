@@ -1142,7 +1142,7 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     } else if (nch % 2 == 0 && mp_cdiv(n, 4) < 2048) {
       sk = 2;
     }
-    if (mp_gemv_env(1) > 0) r = mp_gemv_env(1) >= 8 ? 8 : 4;
+    if (mp_gemv_env(1) > 0) r = mp_gemv_env(1) >= 8 ? 8 : (mp_gemv_env(1) >= 4 ? 4 : 2);
     if (mp_gemv_env(2) > 0) c = mp_gemv_env(2) >= 4 ? 4 : mp_gemv_env(2);
     if (mp_gemv_env(3) > 0) sk = mp_gemv_env(3) >= 4 ? 4 : mp_gemv_env(3);
     const int64_t groups = mp_cdiv(n, r);
@@ -1168,7 +1168,8 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     else if (sk == 2) MP_W4_GEMV_C(R_, 2); \
     else MP_W4_GEMV_C(R_, 4);          \
   } while (0)
-    if (r == 4) MP_W4_GEMV_S(4);
+    if (r == 2) MP_W4_GEMV_S(2);
+    else if (r == 4) MP_W4_GEMV_S(4);
     else MP_W4_GEMV_S(8);
 #undef MP_W4_GEMV_S
 #undef MP_W4_GEMV_C

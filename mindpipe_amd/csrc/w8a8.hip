@@ -62,8 +62,8 @@ __global__ __launch_bounds__(256) void rowquant_kernel(const void *__restrict__ 
 }
 
 // ------------------------------------------------------------------ decode GEMV (M <= 64)
-// One workgroup of NW waves per 16 output columns; waves take 64-byte K blocks
-// round-robin and are summed exactly (int32) through LDS.  The int8
+// One workgroup of NW waves per 16 output columns; each wave takes a contiguous
+// range of 64-byte K blocks, and the waves are summed exactly (int32) through LDS.  The int8
 // activations are staged once per workgroup into LDS (K chunks within the LDS
 // budget).  MFMA i32_16x16x64_i8: B = weight rows straight from HBM (16 B per
 // lane), A = activations from LDS (row m = lane%16, zero beyond M).  Weight
@@ -96,14 +96,18 @@ __global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb
 
   for (int c0 = 0; c0 < nblk; c0 += cb) {
     const int cbn = (nblk - c0) < cb ? (nblk - c0) : cb;
-    const int nmine = cbn > wave ? (cbn - wave + NW - 1) / NW : 0;
+    // contiguous block range per wave: consecutive loads of a wave read the two halves
+    // of each 128-byte weight line (round-robin blocks would leave every line half used)
+    const int per = (cbn + NW - 1) / NW;
+    const int jlo = wave * per;
+    const int nmine = cbn > jlo ? (cbn - jlo < per ? cbn - jlo : per) : 0;
     const int rmax = nmine > 0 ? nmine - 1 : 0;
     const int bmax = c0 + cbn - 1;
     auto issue = [&](i4_t *w, int r0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int r = (r0 + u) < rmax ? (r0 + u) : rmax;
-        int b = c0 + wave + NW * r;
+        int b = c0 + jlo + r;
         b = b < bmax ? b : bmax;
         w[u] = *reinterpret_cast<const i4_t *>(wrow + b * 64);
       }
@@ -113,7 +117,7 @@ __global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb
       for (int u = 0; u < U; ++u) {
         const int r = r0 + u;
         const bool live = r < nmine;
-        int jl = wave + NW * (r < rmax ? r : rmax);
+        int jl = jlo + (r < rmax ? r : rmax);
         jl = jl < cbn - 1 ? jl : cbn - 1;
         const i4_t wv = live ? w[u] : i4_t{0, 0, 0, 0};
 #pragma unroll
@@ -180,6 +184,91 @@ __global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb
       mp_store_from_f32(p.y, static_cast<int64_t>(m) * p.ldy + col, p.out_dtype, yv);
     }
   }
+}
+
+// ------------------------------------------------------------------ GEMV (M <= 2)
+// A wave owns R weight rows over all of K.  In chunk j lane l covers K bytes
+// [1024 j + 16 l, +16), so each weight load reads 1 KB of one row contiguously
+// (a load whose lanes touch 16 rows costs the CU several times the issue slots)
+// and the MR activation rows come the same way; v_dot4_i32_i8 multiplies
+// exactly.  C chunks are issued before any is used.  Lanes past K, and
+// activation rows past M, load beyond their buffer: zeros, no memory access.  A
+// wave butterfly sums the int32 partials exactly; the epilogue is the shared
+// (acc * s_tok) * s_ch (+ bias) of the other kernels, so the outputs are the same
+// bits.
+template <int R, int MR, int C>
+__global__ __launch_bounds__(256) void i8_gemv_kernel(mp_i8_args p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n_cols = static_cast<int>(p.n);
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  if (row0 >= n_cols) return;  // wave-uniform; no barrier in the kernel
+  const uint32_t k = static_cast<uint32_t>(p.k);
+  const int m_rows = static_cast<int>(p.rows);
+  const uint32_t wbytes = static_cast<uint32_t>(n_cols) * k;
+  const uint32_t xbytes = static_cast<uint32_t>(m_rows) * k;
+  const auto wr = mp_rsrc(p.b, wbytes);
+  const auto xr = mp_rsrc(p.a, xbytes);
+  uint32_t wbase[R], xbase[MR];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = row0 + r < n_cols ? row0 + r : n_cols - 1;
+    wbase[r] = static_cast<uint32_t>(n) * k;
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m) xbase[m] = m < m_rows ? static_cast<uint32_t>(m) * k : xbytes;
+  const int nch = static_cast<int>((k + 1023u) / 1024u);
+  int acc[MR][R];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0;
+  for (int j0 = 0; j0 < nch; j0 += C) {
+    i4_t w[C][R], xv[C][MR];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const uint32_t kx = static_cast<uint32_t>(j0 + c) * 1024u + 16u * lane;
+      const bool live = kx < k;  // chunks past nch give kx >= k too
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint4 v = mp_buf_load16(wr, live ? wbase[r] + kx : wbytes, 0);
+        w[c][r] = i4_t{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+      }
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const uint4 v = mp_buf_load16(xr, live ? xbase[m] + kx : xbytes, 0);
+        xv[c][m] = i4_t{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[m][r] = __builtin_amdgcn_sdot4(xv[c][m][e], w[c][r][e], acc[m][r], false);
+  }
+  // exact int32 sums over the 64 lanes
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) acc[m][r] += __shfl_xor(acc[m][r], o, 64);
+  // lane m * R + r stores output (m, row0 + r)
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int col = row0 + r;
+      if (lane == m * R + r && m < m_rows && col < n_cols) {
+        float yv = mp_mul(mp_mul(static_cast<float>(acc[m][r]), p.s_a[m]), p.s_b[col]);
+        if (p.bias) yv = mp_add(yv, mp_load_as_f32(p.bias, col, p.bias_dtype));
+        mp_store_from_f32(p.y, static_cast<int64_t>(m) * p.ldy + col, p.out_dtype, yv);
+      }
+    }
 }
 
 // ------------------------------------------------------------------ tiled GEMM
@@ -1084,6 +1173,16 @@ static int mp_grouped_big() {
   return v;
 }
 
+// Row-contiguous GEMV for M <= 2 (MP_W8_GEMV=0 routes those to the skinny MFMA
+// kernel, =2/3/5 sets 1/2/4 rows per wave; for measurements).
+static int mp_i8_gemv() {
+  static int v = [] {
+    const char *e = getenv("MP_W8_GEMV");
+    return e ? atoi(e) : 1;
+  }();
+  return v;
+}
+
 // Persistent large-M launch (MP_W8_PERSIST=0 turns it off, for measurements).
 static int mp_persist() {
   static int v = [] {
@@ -1153,7 +1252,27 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
     return MP_OK;
   }
   if (epilogue == MP_EPI_SWIGLU) return MP_ERR_ARG;
-  if (a.rows <= 64 && a.k % 64 == 0 && aligned && epilogue == MP_EPI_DENSE && a.k <= INT32_MAX &&
+  if (a.rows <= 2 && mp_i8_gemv() && a.k % 16 == 0 && aligned && epilogue == MP_EPI_DENSE &&
+      a.n * a.k < (int64_t(1) << 32) && a.rows * a.k < (int64_t(1) << 32)) {
+    // row-contiguous int8 GEMV: R rows per wave (1: measured best on the 7B shapes), 4 waves per
+    // workgroup
+    const int64_t nch = mp_cdiv(a.k, 1024);
+    const int rsel = mp_i8_gemv() >= 2 ? mp_i8_gemv() - 1 : 1;  // MP_W8_GEMV=2/3/5: 1/2/4 rows per wave
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, 4 * rsel)));
+#define MP_I8_GEMV(R_)                                                                              \
+  do {                                                                                              \
+    if (a.rows == 1) {                                                                              \
+      if (nch <= 4) hipLaunchKernelGGL((i8_gemv_kernel<R_, 1, 4>), grid, dim3(256), 0, stream, a); \
+      else hipLaunchKernelGGL((i8_gemv_kernel<R_, 1, 2>), grid, dim3(256), 0, stream, a);          \
+    } else {                                                                                        \
+      hipLaunchKernelGGL((i8_gemv_kernel<R_, 2, 2>), grid, dim3(256), 0, stream, a);               \
+    }                                                                                               \
+  } while (0)
+    if (rsel == 1) MP_I8_GEMV(1);
+    else if (rsel == 4) MP_I8_GEMV(4);
+    else MP_I8_GEMV(2);
+#undef MP_I8_GEMV
+  } else if (a.rows <= 64 && a.k % 64 == 0 && aligned && epilogue == MP_EPI_DENSE && a.k <= INT32_MAX &&
       a.n <= INT32_MAX) {
     const int mi = static_cast<int>(a.rows);
     const int mt = mi <= 16 ? 1 : (mi <= 32 ? 2 : 4);

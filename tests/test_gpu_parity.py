@@ -212,7 +212,9 @@ W8_CASES = [(1, 11008, 4096), (16, 11008, 4096), (5, 1000, 256), (17, 512, 1024)
             # large-M kernel: four register stages over 3 loop trips, two stages (K % 256 != 0)
             (1024, 640, 768), (1300, 700, 384),
             # large-M kernel with odd N: the unpaired store path
-            (1024, 333, 256)]
+            (1024, 333, 256),
+            # row-contiguous GEMV (M <= 2): K past the last 1 KB chunk, M = 2, tiny K, K = 11008
+            (2, 300, 1040), (1, 257, 4112), (2, 64, 16), (1, 100, 11008)]
 
 
 @pytest.mark.parametrize("m,n,k", W8_CASES)
