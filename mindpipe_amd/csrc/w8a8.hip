@@ -274,10 +274,12 @@ __global__ __launch_bounds__(256) void i8_gemv_kernel(mp_i8_args p) {
 // ------------------------------------------------------------------ tiled GEMM
 // BM x BN output tile per workgroup of 4 waves (2 x 2, each (BM/2) x (BN/2)
 // built from MFMA i32_32x32x32_i8 tiles), BK-byte K steps, LDS double buffer
-// with a 16-byte row pad (conflict-free ds_read_b128 for the MFMA fragments).
+// with a 16-byte row pad (conflict-free ds_read_b128 for the MFMA fragments),
+// D + 1 K tiles in flight in registers (a workgroup per CU or fewer: the loads'
+// latency must be covered by the workgroup's own MFMA time).
 // Grouped mode maps blockIdx.y to (expert, row tile) by walking the
 // cumulative row offsets; surplus tiles exit.
-template <int BM, int BN, int BK, int EPI>
+template <int BM, int BN, int BK, int EPI, int D = 0>
 __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
   constexpr int LD = BK + 16;
   constexpr int WM = BM / 2, WN = BN / 2;
@@ -347,25 +349,29 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
     bsrc[i] = bexp + wr * k + (c % CPR) * 16;
   }
 
-  i4_t areg[CA], breg[CB];
-  auto load_tile = [&](int64_t kt) {
+  // D + 1 register stages of tiles in flight.  Loads are unconditional (clamped to
+  // the last tile), so every wait is a partial vmcnt.
+  i4_t areg[D + 1][CA], breg[D + 1][CB];
+  const int64_t nkt = k / BK;
+  auto load_tile = [&](int set, int64_t kt) {
+    kt = kt < nkt ? kt : nkt - 1;
     const int64_t off = kt * BK;
 #pragma unroll
     for (int i = 0; i < CA; ++i)
-      areg[i] = aval[i] ? *reinterpret_cast<const i4_t *>(asrc[i] + off) : i4_t{0, 0, 0, 0};
+      areg[set][i] = aval[i] ? *reinterpret_cast<const i4_t *>(asrc[i] + off) : i4_t{0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < CB; ++i) breg[i] = *reinterpret_cast<const i4_t *>(bsrc[i] + off);
+    for (int i = 0; i < CB; ++i) breg[set][i] = *reinterpret_cast<const i4_t *>(bsrc[i] + off);
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int set, int buf) {
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
       const int c = tid + i * 256;
-      *reinterpret_cast<i4_t *>(&sa[buf][(c / CPR) * LD + (c % CPR) * 16]) = areg[i];
+      *reinterpret_cast<i4_t *>(&sa[buf][(c / CPR) * LD + (c % CPR) * 16]) = areg[set][i];
     }
 #pragma unroll
     for (int i = 0; i < CB; ++i) {
       const int c = tid + i * 256;
-      *reinterpret_cast<i4_t *>(&sb[buf][(c / CPR) * LD + (c % CPR) * 16]) = breg[i];
+      *reinterpret_cast<i4_t *>(&sb[buf][(c / CPR) * LD + (c % CPR) * 16]) = breg[set][i];
     }
   };
 
@@ -387,14 +393,7 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
                                           : (wn * WN + j * 32 + (lane & 31));
     brow_l[j] = lr * LD + 16 * (lane >> 5);
   }
-
-  const int64_t nkt = k / BK;
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int64_t kt = 0; kt < nkt; ++kt) {
-    const int cur = static_cast<int>(kt & 1);
-    if (kt + 1 < nkt) load_tile(kt + 1);
+  auto mma = [&](int cur) {
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
       i4_t af[TM], bf[TN];
@@ -408,8 +407,29 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nkt) store_tile(cur ^ 1);
-    __syncthreads();
+  };
+
+  // Register set s holds tile t with t % (D + 1) == s; at step kt tiles kt+1 .. kt+D+1
+  // are in flight.  Tile kt+1 goes to LDS after tile kt is multiplied, and its set is
+  // refilled with tile kt+D+2.
+  // (barriers wait for LDS traffic only: the prefetched global loads stay in flight)
+#pragma unroll
+  for (int d = 0; d <= D; ++d) load_tile(d, d);
+  store_tile(0, 0);
+  load_tile(0, D + 1);
+  mp_lds_barrier();
+  for (int64_t kt0 = 0; kt0 < nkt; kt0 += D + 1) {
+#pragma unroll
+    for (int d = 0; d <= D; ++d) {
+      const int64_t kt = kt0 + d;
+      const int nxt = (d + 1) % (D + 1);
+      if (kt < nkt) {  // workgroup-uniform
+        mma(static_cast<int>(kt & 1));
+        if (kt + 1 < nkt) store_tile(nxt, static_cast<int>((kt + 1) & 1));
+      }
+      load_tile(nxt, kt + D + 2);
+      mp_lds_barrier();
+    }
   }
 
   // ---------------------------------------------------------------- epilogues
@@ -1127,6 +1147,9 @@ __global__ void i8_simple_kernel(mp_i8_args p) {
 }
 
 constexpr int kTBM = 128, kTBN = 128, kTBK = 64;
+// 128-byte K steps: a 64-lane load covers 8 rows x 128 bytes (a 64-byte step makes it
+// 16 rows x 64 bytes, which costs the CU several times the load-issue slots)
+constexpr int kTBK2 = 128;
 
 }  // namespace
 
@@ -1181,6 +1204,27 @@ static int mp_i8_gemv() {
     return e ? atoi(e) : 1;
   }();
   return v;
+}
+
+// K step of the tiled kernel: 128 bytes when K allows (default), MP_W8_TILED_BK=64
+// forces 64 (for measurements).
+static int mp_tiled_bk() {
+  static int v = [] {
+    const char *e = getenv("MP_W8_TILED_BK");
+    return e ? atoi(e) : 128;
+  }();
+  return v;
+}
+
+// Tiled-kernel variant for a launch of `wgs` workgroups: 2 = 128-byte K steps with
+// four register stages (one workgroup per CU: the grid fits the CUs once), 1 =
+// 128-byte steps with one stage (two per CU), 0 = 64-byte steps (three per CU).
+static int mp_tiled_variant(int64_t k, int64_t wgs) {
+  if (k % kTBK2 != 0 || mp_tiled_bk() != 128) return 0;
+  const int64_t cus = mp_cu_count() > 0 ? mp_cu_count() : 256;
+  if (wgs <= cus) return 2;
+  if (wgs <= 2 * cus) return 1;
+  return 0;
 }
 
 // Persistent large-M launch (MP_W8_PERSIST=0 turns it off, for measurements).
@@ -1242,6 +1286,21 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
         mp_cdiv(a.n, epilogue == MP_EPI_SWIGLU ? kTBN / 2 : kTBN);
     const int64_t m_slots = mp_cdiv(a.rows, kTBM) + a.n_experts;
     const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(m_slots));
+    const int tv = mp_tiled_variant(a.k, n_tiles * m_slots);
+    if (tv > 0) {
+      if (epilogue == MP_EPI_SWIGLU) {
+        if (tv == 2) hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_SWIGLU, 3>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_SWIGLU, 0>), grid, dim3(256), 0, stream, a);
+      } else if (epilogue == MP_EPI_F32) {
+        if (tv == 2) hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_F32, 3>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_F32, 0>), grid, dim3(256), 0, stream, a);
+      } else {
+        if (tv == 2) hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_DENSE, 3>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_DENSE, 0>), grid, dim3(256), 0, stream, a);
+      }
+      MP_CHECK_LAUNCH();
+      return MP_OK;
+    }
     if (epilogue == MP_EPI_SWIGLU)
       hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_SWIGLU>), grid, dim3(256), 0, stream, a);
     else if (epilogue == MP_EPI_F32)
@@ -1331,6 +1390,16 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
         hipLaunchKernelGGL((i8_gemm_big_kernel<MP_BF16, MP_EPI_DENSE>), pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
       else
         hipLaunchKernelGGL((i8_gemm_big_kernel<MP_F32, MP_EPI_DENSE>), pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
+    }
+  } else if (aligned && mp_tiled_variant(a.k, mp_cdiv(a.n, kTBN) * mp_cdiv(a.rows, kTBM)) > 0) {
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));
+    const int tv = mp_tiled_variant(a.k, static_cast<int64_t>(grid.x) * grid.y);
+    if (epilogue == MP_EPI_F32) {
+      if (tv == 2) hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_F32, 3>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_F32, 0>), grid, dim3(256), 0, stream, a);
+    } else {
+      if (tv == 2) hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_DENSE, 3>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_DENSE, 0>), grid, dim3(256), 0, stream, a);
     }
   } else if (a.k % kTBK == 0 && aligned) {
     const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));
