@@ -99,6 +99,16 @@ int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t *w_packed, 
                   const void *scales, const void *zeros, int group_size, const void *bias, void *y,
                   int x_dtype, mp_stream_t stream);
 
+/* act[M, I] = silu(G) * U with [G | U] = X . dequant(W)^T (+ bias[2I]) for the fused
+ * gate/up weight W [2I, K] (gate rows first): the gate/up linear and the SiLU-mul
+ * of the SwiGLU MLP (act_fn(gate_up) in the HF / vLLM Llama MLP the W4A16 export
+ * serves) in one launch.  Every value is rounded as the two-step path rounds it
+ * (fp16 gate and up, then round(round(silu(g)) * u)).  M <= 64, group 128,
+ * K % 256 == 0; fp16. */
+int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n2,
+                         const void *scales, const void *zeros, int group_size, const void *bias, void *act,
+                         int x_dtype, mp_stream_t stream);
+
 /* ---------------------------------------------------------------- W8A8 (SmoothQuant) */
 
 /* Per-token dynamic symmetric int8 quant of x [M,K] (fp16/bf16/fp32).

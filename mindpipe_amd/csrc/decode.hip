@@ -369,10 +369,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= total) return;
   const int64_t b = i / inter, c = i % inter;
-  const float g = mp_h2f(gu[b * 2 * inter + c]);
-  const float u = mp_h2f(gu[b * 2 * inter + inter + c]);
-  const float sg = mp_rh(g / (1.0f + expf(-g)));
-  act[i] = mp_f2h(sg * u);
+  act[i] = mp_swiglu_h(mp_h2f(gu[b * 2 * inter + c]), mp_h2f(gu[b * 2 * inter + inter + c]));
 }
 
 }  // namespace

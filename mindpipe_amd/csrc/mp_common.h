@@ -59,6 +59,13 @@ __device__ __forceinline__ void mp_store_from_f32(void *p, int64_t i, int dtype,
   else static_cast<float *>(p)[i] = v;
 }
 
+// SwiGLU of fp16 values g, u (given as floats): round(round(silu(g)) * u), the
+// rounding of PyTorch's half ops (silu in fp32, rounded; the product rounded).
+__device__ __forceinline__ uint16_t mp_swiglu_h(float g, float u) {
+  const float sg = mp_rh(g / (1.0f + expf(-g)));
+  return mp_f2h(sg * u);
+}
+
 // ---- wave64 reductions (DPP-backed shuffles)
 __device__ __forceinline__ float mp_wave_max(float v) {
 #pragma unroll

@@ -470,7 +470,7 @@ __global__ __launch_bounds__(512) void w4a16_decode_kernel(
 // join makes the compiler wait for every outstanding load).  Each block pair's
 // activation loads are issued before the next pair's weight prefetch, so a
 // compute step waits for its own data only.
-template <int MT, int NT, int S, bool ZP>
+template <int MT, int NT, int S, bool ZP, bool SWI = false>
 __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
@@ -486,7 +486,12 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   const int kq = lane >> 4;
   const uint32_t kw = static_cast<uint32_t>(k) >> 3;
   const int nblk = k >> 7;
-  const int col0 = blockIdx.x * NT * 16;
+  // SWI: tiles j < NT/2 are gate columns, tile j + NT/2 the matching up columns (rows
+  // [I, 2I) of the weight, I = n_cols / 2); the output is act = silu(gate) * up, [M, I]
+  constexpr int NO = SWI ? NT / 2 : NT;  // output tiles per wave
+  static_assert(!SWI || NT % 2 == 0, "SwiGLU pairs tiles");
+  const int n_out = SWI ? n_cols / 2 : n_cols;
+  const int col0 = blockIdx.x * NO * 16;
   // K range of this wave: whole steps; blocks at or past nblk are dead
   const int nst = (nblk + STEP - 1) / STEP;
   const int st_lo = (nst * wave) / S;
@@ -507,8 +512,9 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   uint32_t woff[NT], soff[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
-    int n = col0 + j * 16 + (lane & 15);
-    n = n < n_cols ? n : n_cols - 1;
+    int n = col0 + (j % NO) * 16 + (lane & 15);
+    n = n < n_out ? n : n_out - 1;
+    if (SWI && j >= NO) n += n_out;
     woff[j] = (static_cast<uint32_t>(n) * kw + 4u * kq) * 4u;
     soff[j] = static_cast<uint32_t>(n) * static_cast<uint32_t>(n_groups) * 2u;
   }
@@ -636,6 +642,20 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  auto emit = [&](int m, int col, float v, float u) {
+    if (m < m_rows && col < n_out) {
+      if (SWI) {
+        if (bias) {
+          v += mp_h2f(bias[col]);
+          u += mp_h2f(bias[n_out + col]);
+        }
+        y[static_cast<int64_t>(m) * n_out + col] = mp_swiglu_h(mp_rh(v), mp_rh(u));
+      } else {
+        if (bias) v += mp_h2f(bias[col]);
+        y[static_cast<int64_t>(m) * n_out + col] = mp_f2h(v);
+      }
+    }
+  };
   if (S > 1) {
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -644,34 +664,26 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) red[wave][(t * NT + j) * 4 + i][lane] = acc[t][j][i];
     __syncthreads();
-    for (int o = threadIdx.x; o < MT * NT * 4 * 64; o += S * 64) {
+    for (int o = threadIdx.x; o < MT * NO * 4 * 64; o += S * 64) {
       const int slot = o >> 6, l = o & 63;
-      const int t = slot / (NT * 4), j = (slot / 4) % NT, i = slot % 4;
-      float v = 0.f;
+      const int t = slot / (NO * 4), j = (slot / 4) % NO, i = slot % 4;
+      const int sg = (t * NT + j) * 4 + i;  // gate (or plain) slot; its up slot is NO tiles on
+      float v = 0.f, u = 0.f;
 #pragma unroll
-      for (int w = 0; w < S; ++w) v += red[w][slot][l];
-      const int m = t * 16 + 4 * (l >> 4) + i;
-      const int col = col0 + j * 16 + (l & 15);
-      if (m < m_rows && col < n_cols) {
-        if (bias) v += mp_h2f(bias[col]);
-        y[static_cast<int64_t>(m) * n_cols + col] = mp_f2h(v);
+      for (int w = 0; w < S; ++w) {
+        v += red[w][sg][l];
+        if (SWI) u += red[w][sg + NO * 4][l];
       }
+      emit(t * 16 + 4 * (l >> 4) + i, col0 + j * 16 + (l & 15), v, u);
     }
   } else {
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
+      for (int j = 0; j < NO; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = t * 16 + 4 * kq + i;
-          const int col = col0 + j * 16 + (lane & 15);
-          if (m < m_rows && col < n_cols) {
-            float v = acc[t][j][i];
-            if (bias) v += mp_h2f(bias[col]);
-            y[static_cast<int64_t>(m) * n_cols + col] = mp_f2h(v);
-          }
-        }
+        for (int i = 0; i < 4; ++i)
+          emit(t * 16 + 4 * kq + i, col0 + j * 16 + (lane & 15), acc[t][j][i], SWI ? acc[t][j + NO][i] : 0.f);
   }
 }
 
@@ -848,7 +860,7 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ h2_t mp_as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 
-template <int R, int C, int S, bool ZP>
+template <int R, int C, int S, bool ZP, bool SWI = false>
 __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
     const uint16_t *__restrict__ x, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
@@ -856,23 +868,30 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
   constexpr int SZN = R * 16 > 64 ? R * 16 / 64 : 1;  // scale / zero loads per chunk
   constexpr int LPR = 64 / R;                         // lanes per row after the butterfly
   constexpr int GPW = 4 / S;                          // row groups per workgroup (S waves split K)
+  // SWI: rows [0, I) are gate rows and [I, 2I) the up rows (I = n_cols / 2); a wave owns
+  // R/2 gate rows and the matching R/2 up rows and writes act = silu(gate) * up
+  constexpr int RW = SWI ? R / 2 : R;                 // output rows per wave
   __shared__ float red[S > 1 ? 4 : 1][R];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sw = wave % S;
-  const int row0 = (blockIdx.x * GPW + wave / S) * R;
-  if (S == 1 && row0 >= n_cols) return;  // wave-uniform; with S == 1 there is no barrier
+  const int n_out = SWI ? n_cols / 2 : n_cols;
+  const int row0 = (blockIdx.x * GPW + wave / S) * RW;
+  if (S == 1 && row0 >= n_out) return;  // wave-uniform; with S == 1 there is no barrier
   const int kw = k >> 3;
   const int nch = (k + 2047) >> 11;
   uint32_t magic_v = kMagic, m0_v = 0x000F000Fu, m1_v = 0x00F000F0u;
   asm volatile("" : "+v"(magic_v), "+v"(m0_v), "+v"(m1_v));  // opaque: keep the constants in VGPRs
+  // weight row of the wave's row r (clamped into its half)
+  auto row_of = [&](int r) {
+    const int rr = SWI ? r % RW : r;
+    const int o = row0 + rr < n_out ? row0 + rr : n_out - 1;
+    return SWI && r >= RW ? n_out + o : o;
+  };
 
   const uint32_t *wrow[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int n = row0 + r < n_cols ? row0 + r : n_cols - 1;
-    wrow[r] = wq + static_cast<int64_t>(n) * kw;
-  }
+  for (int r = 0; r < R; ++r) wrow[r] = wq + static_cast<int64_t>(row_of(r)) * kw;
   // scale / zero entry e = lane + 64 i: row e / 16 of the wave, group 16 j + e % 16, read as the
   // 32-bit word holding groups (2 t, 2 t + 1) (n_groups even, 4-byte aligned rows)
   const uint32_t *srow[SZN];
@@ -882,7 +901,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
     const int e = lane + 64 * i;
     int r = e >> 4;
     r = r < R ? r : R - 1;
-    const int n = row0 + r < n_cols ? row0 + r : n_cols - 1;
+    const int n = row_of(r);
     srow[i] = reinterpret_cast<const uint32_t *>(sc + static_cast<int64_t>(n) * n_groups);
     zrow[i] = reinterpret_cast<const uint32_t *>(ZP ? zr + static_cast<int64_t>(n) * n_groups : sc);
   }
@@ -995,6 +1014,15 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
 #pragma unroll
     for (int t = 1; t < S; ++t) v += red[wave + t][lane / LPR];
   }
+  if (SWI) {
+    // lane r * LPR holds row r; gate row p pairs with up row p + RW (lane (p + RW) * LPR)
+    const int r = lane / LPR;
+    if (bias) v += mp_h2f(bias[row_of(r)]);
+    const float up = __shfl(v, (lane + RW * LPR) & 63, 64);
+    const int o = row0 + r;
+    if ((lane % LPR) == 0 && r < RW && o < n_out) y[o] = mp_swiglu_h(mp_rh(v), mp_rh(up));
+    return;
+  }
   const int row = row0 + lane / LPR;
   if ((lane % LPR) == 0 && row < n_cols) {
     if (bias) v += mp_h2f(bias[row]);
@@ -1099,6 +1127,102 @@ extern "C" int mp_unpack_int4(const int32_t *packed, int64_t n, int64_t k, int8_
   hipLaunchKernelGGL(unpack_int4_kernel, dim3(static_cast<unsigned>(mp_cdiv(n * k, 256))), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint32_t *>(packed), n,
                      k, mp_cdiv(k, 8), int_weight);
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n2,
+                                    const void *scales, const void *zeros, int group_size, const void *bias,
+                                    void *act, int x_dtype, mp_stream_t stream) {
+  if (x_dtype != MP_F16) return MP_ERR_DTYPE;
+  if (m < 0 || n2 <= 0 || (n2 & 1) || k <= 0 || group_size != 128 || k % 256 != 0) return MP_ERR_SHAPE;
+  if (m == 0) return MP_OK;
+  if (!x || !w_packed || !scales || !act) return MP_ERR_ARG;
+  if (m > 64 || n2 > INT32_MAX || k > INT32_MAX) return MP_ERR_SHAPE;
+  const int n_groups = static_cast<int>(k / group_size);
+  if (n_groups % 2 != 0) return MP_ERR_SHAPE;
+  if (!mp_aligned(x, 16) || !mp_aligned(w_packed, 16) || !mp_aligned(scales, 4) ||
+      (zeros != nullptr && !mp_aligned(zeros, 4)))
+    return MP_ERR_ALIGN;
+  if (n2 * (k / 2) >= (int64_t(1) << 32) || m * k * 2 >= (int64_t(1) << 32)) return MP_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const auto *xp = static_cast<const uint16_t *>(x);
+  const auto *wp = reinterpret_cast<const uint32_t *>(w_packed);
+  const auto *sp = static_cast<const uint16_t *>(scales);
+  const auto *zp = static_cast<const uint16_t *>(zeros);
+  const auto *bp = static_cast<const uint16_t *>(bias);
+  auto *yp = static_cast<uint16_t *>(act);
+  const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n2);
+  const int64_t half = n2 / 2;
+  if (m == 1) {
+    // two gate rows and the matching two up rows per wave; chunk / split choice as the GEMV
+    const int nch = (ki + 2047) / 2048;
+    int c = 1, sk = 1;
+    if (nch <= 2) c = nch;
+    else if (nch % 4 == 0) { c = 2; sk = 2; }
+    else if (nch % 2 == 0 && mp_cdiv(half, 2) < 2048) sk = 2;
+    const int64_t groups = mp_cdiv(half, 2);
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(groups, 4 / sk)));
+#define MP_W4_GEMV_SWI(C_, S_)                                                                               \
+  do {                                                                                                       \
+    if (zp)                                                                                                  \
+      hipLaunchKernelGGL((w4a16_gemv_kernel<4, C_, S_, true, true>), grid, dim3(256), 0, s, xp, ki, wp, ni, sp, \
+                         zp, n_groups, bp, yp);                                                              \
+    else                                                                                                     \
+      hipLaunchKernelGGL((w4a16_gemv_kernel<4, C_, S_, false, true>), grid, dim3(256), 0, s, xp, ki, wp, ni,   \
+                         sp, zp, n_groups, bp, yp);                                                          \
+  } while (0)
+    if (sk == 2) {
+      if (c == 2) MP_W4_GEMV_SWI(2, 2);
+      else MP_W4_GEMV_SWI(1, 2);
+    } else {
+      if (c == 2) MP_W4_GEMV_SWI(2, 1);
+      else MP_W4_GEMV_SWI(1, 1);
+    }
+#undef MP_W4_GEMV_SWI
+    MP_CHECK_LAUNCH();
+    return MP_OK;
+  }
+  // batched kernel: NT/2 gate tiles paired with NT/2 up tiles per wave
+  const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  int nt = half >= 8192 ? 4 : 2;
+  if (mp_batch_env(0) >= 2) nt = mp_batch_env(0) >= 4 ? 4 : 2;
+  const int smax = mt * nt >= 8 ? 4 : 8;
+  const int nblk = ki / 128;
+  const int nsteps = (nblk + 7) / 8;
+  const int64_t groups = mp_cdiv(half, 16 * (nt / 2));
+  int split = 1;
+  while (split < smax && groups * split < mp_batch_env(2) && nsteps / (split * 2) >= 1) split *= 2;
+  if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
+  const dim3 grid(static_cast<unsigned>(groups));
+#define MP_W4_BSWI(MT_, NT_, S_)                                                                              \
+  do {                                                                                                       \
+    if (zp)                                                                                                  \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki,  \
+                         wp, ni, sp, zp, n_groups, bp, yp);                                                  \
+    else                                                                                                     \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, \
+                         wp, ni, sp, zp, n_groups, bp, yp);                                                  \
+  } while (0)
+#define MP_W4_BSWI_S(MT_, NT_)                                                  \
+  do {                                                                          \
+    if (split == 1) MP_W4_BSWI(MT_, NT_, 1);                                    \
+    else if (split == 2) MP_W4_BSWI(MT_, NT_, 2);                               \
+    else if (split == 4) MP_W4_BSWI(MT_, NT_, 4);                               \
+    else MP_W4_BSWI(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : 8));                        \
+  } while (0)
+  if (mt == 1) {
+    if (nt == 2) MP_W4_BSWI_S(1, 2);
+    else MP_W4_BSWI_S(1, 4);
+  } else if (mt == 2) {
+    if (nt == 2) MP_W4_BSWI_S(2, 2);
+    else MP_W4_BSWI_S(2, 4);
+  } else {
+    if (nt == 2) MP_W4_BSWI_S(4, 2);
+    else MP_W4_BSWI_S(4, 4);
+  }
+#undef MP_W4_BSWI_S
+#undef MP_W4_BSWI
   MP_CHECK_LAUNCH();
   return MP_OK;
 }

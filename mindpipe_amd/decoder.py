@@ -64,6 +64,10 @@ class _W4:
     def __call__(self, x):
         return ops.w4a16_gemm(x, self.packed, self.scales, self.zeros, self.group, None)
 
+    def swiglu(self, x):
+        """silu(gate) * up of this fused gate/up linear in one launch."""
+        return ops.w4a16_gemm_swiglu(x, self.packed, self.scales, self.zeros, self.group, None)
+
     def nbytes(self):
         return self.packed.numel() * 4 + self.scales.numel() * 2 + self.zeros.numel() * 2
 
@@ -179,7 +183,7 @@ class W4Decoder:
             att = ops.decode_rope_attention(qkv, nh, kvh, self.cos, self.sin, cur_len, self.k_cache[li, :b],
                                             self.v_cache[li, :b], splits, scale, ws)
             hn, _, _, x = ops.add_rms_norm_quant(l["o"](att.reshape(b, nh * hd)), x, l["ln2"], cfg.eps, quant=False)
-            delta = l["down"](ops.silu_mul(l["gate_up"](hn)))
+            delta = l["down"](l["gate_up"].swiglu(hn))
         hn, _, _, x = ops.add_rms_norm_quant(delta, x, self.norm, cfg.eps, quant=False)
         logits = self.lm_head(hn)
         return logits if return_logits else logits.argmax(-1)

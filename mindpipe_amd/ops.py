@@ -360,6 +360,35 @@ def moe_w8a8_forward(x, topk_ids, topk_w, w13, s13, w2, s2, out_dtype=None):
 
 
 # ---------------------------------------------------------------- decode-step harness kernels
+def w4a16_gemm_swiglu(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor],
+                      group_size: int, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``silu(G) * U`` with ``[G | U] = X . dequant(W)^T (+ bias)`` for the fused gate/up weight
+    ``w_packed [2I, K/8]`` (gate rows first): ``[..., I]`` fp16, rounded as ``silu_mul`` of the
+    ``w4a16_gemm`` output.  One launch for M <= 64 (group 128, K % 256 == 0); otherwise the two
+    launches."""
+    k = x.shape[-1]
+    n2 = w_packed.shape[0]
+    x2 = x.reshape(-1, k)
+    m = x2.shape[0]
+    if m > 64 or group_size != 128 or k % 256 or n2 % 2:
+        return silu_mul(w4a16_gemm(x2, w_packed, scales, zeros, group_size, bias)).reshape(*x.shape[:-1], n2 // 2)
+    _need(x, "x", torch.float16)
+    _need(w_packed, "w_packed", torch.int32, 2)
+    _need(scales, "scales", torch.float16, 2)
+    if w_packed.shape[1] * 8 != k or scales.shape != (n2, k // group_size):
+        raise RuntimeError(f"w_packed {tuple(w_packed.shape)} / scales {tuple(scales.shape)} do not match K={k}")
+    if zeros is not None and zeros.shape != scales.shape:
+        raise RuntimeError("zeros must have the shape of scales")
+    if bias is not None and bias.shape != (n2,):
+        raise RuntimeError("bias must be [2I]")
+    act = torch.empty((m, n2 // 2), dtype=torch.float16, device=x.device)
+    with _dev(x):
+        _lib.check(_lib.load().mp_w4a16_gemm_swiglu(
+            x2.data_ptr(), m, k, w_packed.data_ptr(), n2, scales.data_ptr(), _ptr(zeros), group_size,
+            _ptr(bias), act.data_ptr(), MP_F16, _stream()), "mp_w4a16_gemm_swiglu")
+    return act.reshape(*x.shape[:-1], n2 // 2)
+
+
 def decode_rope_append(qkv: torch.Tensor, nh: int, kvh: int, cos_t: torch.Tensor, sin_t: torch.Tensor,
                        pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                        q_out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -134,6 +134,41 @@ def test_w4a16_gemm_matches_dequant_matmul(m, n, k, zp):
     assert err <= 1e-3, err   # bar: ||Y - Y_ref||_F / ||Y_ref||_F <= 1e-3
 
 
+@pytest.mark.parametrize("m,i,k", [(1, 2048, 4096), (1, 1001, 2304), (1, 300, 11008), (8, 2048, 4096), (16, 1000, 1024),
+                                   (24, 4096, 512), (40, 520, 2048), (64, 256, 1024)])
+@pytest.mark.parametrize("zp", [True, False])
+def test_w4a16_gemm_swiglu_matches_two_step(m, i, k, zp):
+    """Fused gate/up GEMM + SiLU-mul against silu_mul(w4a16_gemm) (bit-exact for the one-row
+    GEMV, whose per-row arithmetic is the same; <= 1 ulp for the batched kernel, whose K split
+    may differ) and against the oracle's dequant -> matmul -> SiLU-mul (rel. error <= 1e-3)."""
+    _say("w4a16 swiglu", m, i, k, zp)
+    ops = _ops()
+    n2 = 2 * i
+    w = _w(n2, k, seed=3)
+    x = _x(m, k, seed=4)
+    if zp:
+        rdeq, rs, rz, codes = O.pseudo_quantize_tensor(w, 4, True, 128)
+        packed = O.pack_uint4(codes)
+    else:
+        iw, rs, _ = O.gptq_rtn_quantize(w.astype(np.float32), 4, 128)
+        packed = O.pack_int4_signed(iw)
+        rz = None
+        rdeq = O.dequant_w4_fp16(packed, rs, None, k, 128)
+    bias = (np.random.default_rng(6).standard_normal(n2) * 0.1).astype(np.float16)
+    args = (_t(packed), _t(rs), None if rz is None else _t(rz), 128, _t(bias))
+    act = ops.w4a16_gemm_swiglu(_t(x), *args)
+    two = ops.silu_mul(ops.w4a16_gemm(_t(x), *args))
+    d = (act.view(torch.int16).int() - two.view(torch.int16).int()).abs()
+    if m == 1:
+        assert torch.equal(act, two)
+    else:
+        assert int(d.max()) <= 1 and float((d == 0).float().mean()) >= 0.99
+    gu = O.w4a16_linear(x, rdeq, bias).astype(np.float32)
+    g, u = gu[:, :i], gu[:, i:]
+    ref = (g / (1.0 + np.exp(-g))) * u
+    assert _rel(_np(act).astype(np.float32), ref) <= 1e-3   # bar: ||act - ref||_F / ||ref||_F <= 1e-3
+
+
 def test_w4a16_odd_shapes_use_exact_path():
     _say("w4a16 odd")
     # export KAT: K = 8, g = 4 (tests/test_vllm_real_quant_export.py:105-152)
