@@ -7,8 +7,9 @@ Weights are random W4 g128 codes with fp16 scales / zeros (a random init of the
 quantized model; no checkpoint is loaded).  q/k/v and gate/up are fused into one
 W4A16 GEMM each (row concatenation of the packed weight is exact).
 
-``decode_step`` runs one greedy step as ~10 launches per layer: fused residual-add
-+ RMSNorm, the W4A16 GEMVs, RoPE + KV append, split-K decode attention, SiLU-mul.
+``decode_step`` runs one greedy step as 7-8 launches per layer: fused residual-add
++ RMSNorm, the W4A16 GEMVs, split-K decode attention with RoPE and the KV append
+fused in (plus the split merge), and the gate/up GEMV with SiLU-mul in its epilogue.
 The KV cache has a fixed capacity ``[L, B, kvh, T, 128]`` and every kernel reads
 the current position from device memory, so a step is shape-static and can be
 captured into a HIP graph.  ``decode_step_torch`` is the same step in PyTorch ops
