@@ -112,6 +112,18 @@ __device__ __forceinline__ uint4 mp_buf_load16(__amdgpu_buffer_rsrc_t r, uint32_
                                                       __builtin_amdgcn_readfirstlane(static_cast<int>(soff)), 0);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ i4_t mp_buf_load16i(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(i4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                        r, static_cast<int>(voff), __builtin_amdgcn_readfirstlane(static_cast<int>(soff)), 0));
+}
+// Vector stores through a buffer descriptor: offsets at or past its size are dropped,
+// so guarded stores need no branch.
+__device__ __forceinline__ void mp_buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, static_cast<int>(voff), 0, 0);
+}
+__device__ __forceinline__ void mp_buf_store2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, static_cast<int>(voff), 0, 0);
+}
 __device__ __forceinline__ uint32_t mp_buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff),
                                               __builtin_amdgcn_readfirstlane(static_cast<int>(soff)), 0);

@@ -483,6 +483,377 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
   }
 }
 
+// ------------------------------------------------------------------ grouped (MoE) GEMM
+// Expert-grouped int8 GEMM for experts of up to a few hundred routed rows.  A work
+// item is rows [row_begin, row_end) of one expert, at most 256 of them, against 128
+// weight rows (fp32 / 16-bit outputs: 128 output columns; SwiGLU: 64 gate rows and
+// the 64 matching up rows), so a weight slice streams from HBM once per 256 rows of
+// its expert.  Items are numbered expert-major with the row chunk fastest; the
+// workgroups the dispatcher places on XCD x (id % 8) walk the x-th eighth of the
+// items, so the items an XCD runs together share their expert's activation rows (and
+// a slice's row chunks share its weights) in that XCD's L2.  The launch is
+// persistent (one workgroup per CU): the next item's first K tiles are loaded before
+// the current item's epilogue.
+// Eight waves: wave (wm, wn) loads and multiplies the 64-row slab wm and owns the 64
+// columns wn.  A slab past the expert's rows is inactive: its two waves load no A
+// rows and skip their MFMAs and epilogue (the K loop is instantiated for both cases;
+// every wave runs the same barriers).  128-byte K steps (a 64-lane load covers 8 rows
+// x 128 B), D + 1 register stages in flight, LDS double buffer of 144-byte rows.
+constexpr int kMoeBM = 256, kMoeBN = 128, kMoeBK = 128, kMoeLD = kMoeBK + 16, kMoeThreads = 512;
+constexpr int kMoeMaxExperts = 1024;
+// LDS: double-buffered A and B tiles; two buffers each of the item's per-token scales and
+// column scales; the group offsets
+constexpr size_t kMoeSmem = static_cast<size_t>(2) * (kMoeBM + kMoeBN) * kMoeLD +
+                            2 * (kMoeBM + kMoeBN) * sizeof(float) + (kMoeMaxExperts + 1) * sizeof(int64_t);
+
+__device__ __forceinline__ int moe_row_chunks(const int64_t *off, int e) {
+  const int64_t c = off[e + 1] - off[e];
+  return c > 0 ? static_cast<int>((c + kMoeBM - 1) / kMoeBM) : 0;
+}
+
+// Item g of the expert-major numbering: expert e, weight slice, 256-row chunk.
+// Every lane returns the same values (wave-level scan over the experts).
+__device__ __forceinline__ void moe_find_item(const int64_t *off, int ne, int n_slices, int g, int lane, int &e,
+                                              int &slice, int64_t &row_begin, int64_t &row_end) {
+  int found = -1, rem = 0, chunks = 1, base = 0;
+  for (int c0 = 0; c0 < ne && found < 0; c0 += 64) {
+    const int ch = c0 + lane < ne ? moe_row_chunks(off, c0 + lane) : 0;
+    const int it = ch * n_slices;
+    int incl = it;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o, 64);
+      incl += lane >= o ? t : 0;
+    }
+    const bool mine = it > 0 && g >= base + incl - it && g < base + incl;
+    const unsigned long long bal = __ballot(mine);
+    if (bal) {
+      const int src = __ffsll(static_cast<long long>(bal)) - 1;
+      found = c0 + src;
+      chunks = __shfl(ch, src, 64);
+      rem = g - base - (__shfl(incl, src, 64) - __shfl(it, src, 64));
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  e = __builtin_amdgcn_readfirstlane(found < 0 ? 0 : found);
+  chunks = __builtin_amdgcn_readfirstlane(chunks);
+  rem = __builtin_amdgcn_readfirstlane(rem);
+  slice = rem / chunks;
+  row_begin = off[e] + static_cast<int64_t>(rem % chunks) * kMoeBM;
+  row_end = off[e + 1] < row_begin + kMoeBM ? off[e + 1] : row_begin + kMoeBM;
+}
+
+// One step of the transposing max butterfly over 2B values per lane: lanes l and l ^ B
+// exchange half of their values; the lane with bit B set keeps the upper half.
+template <int B>
+__device__ __forceinline__ void moe_max_step(float (&v)[32], int lane) {
+  const bool hi = (lane & B) != 0;
+#pragma unroll
+  for (int j = 0; j < B; ++j) {
+    const float send = hi ? v[j] : v[j + B];
+    const float keep = hi ? v[j + B] : v[j];
+    v[j] = fmaxf(keep, __shfl_xor(send, B, 64));
+  }
+}
+
+template <int EPI, int D>
+__global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n_slices) {
+  constexpr int BM = kMoeBM, BN = kMoeBN, BK = kMoeBK, LD = kMoeLD, NT = kMoeThreads;
+  constexpr int CPR = BK / 16;          // 16-byte chunks per tile row
+  constexpr int CA = 4;                 // A loads per lane per K step (its wave's 32 rows)
+  constexpr int CB = BN * CPR / NT;     // B loads (2)
+  constexpr int TM = 2, TN = 2;         // 32x32 MFMA tiles per wave: 64 x 64
+  constexpr bool SWI = EPI == MP_EPI_SWIGLU;
+  extern __shared__ __attribute__((aligned(16))) int8_t smem_moe[];
+  int8_t *sa = smem_moe;                // [2][BM * LD]
+  int8_t *sb = smem_moe + 2 * BM * LD;  // [2][BN * LD]
+  float *ssa = reinterpret_cast<float *>(smem_moe + 2 * (BM + BN) * LD);  // [2][BM] per-token scales
+  float *ssc = ssa + 2 * BM;                                              // [2][BN] column scales
+  int64_t *soff = reinterpret_cast<int64_t *>(ssc + 2 * BN);             // [E + 1] group offsets
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- this workgroup's items (every wave derives the same ones).  The offsets are read
+  // from an LDS copy, so finding the next item never waits on the tile loads in flight.
+  const int ne = p.n_experts;
+  for (int i = tid; i <= ne; i += NT) soff[i] = p.offsets[i];
+  mp_lds_barrier();
+  const int64_t *off = soff;
+  int total = 0;
+  for (int c0 = 0; c0 < ne; c0 += 64) {
+    int it = c0 + lane < ne ? moe_row_chunks(off, c0 + lane) * n_slices : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) it += __shfl_xor(it, o, 64);
+    total += it;
+  }
+  // uniform to the compiler too: item state derived from it stays in scalar registers
+  // (a buffer descriptor it thinks divergent turns every load into a waterfall loop)
+  total = __builtin_amdgcn_readfirstlane(total);
+  const int share = (total + 7) / 8;
+  const int xcd = static_cast<int>(blockIdx.x) % 8, stride = static_cast<int>(gridDim.x) / 8;
+  int idx = static_cast<int>(blockIdx.x) / 8;
+  if (idx >= share || xcd * share + idx >= total) return;  // workgroup-uniform, before any barrier
+
+  const int64_t k = p.k;
+  const int64_t n_out = p.n;
+  const int64_t nb_rows = SWI ? 2 * n_out : n_out;  // weight rows per expert
+  const int64_t nkt = k / BK;
+
+  // A: lane's rows 64 wm + 32 wn + 8 i + lane / 8 (i < CA), chunk lane % 8, through a
+  // buffer descriptor that ends at row_end (rows past it read as zeros, no traffic)
+  const int arow0 = 64 * wm + 32 * wn + (lane >> 3);
+  const uint32_t aoff0 = static_cast<uint32_t>(arow0 * k + (lane & 7) * 16);
+  // B: chunk c = tid + i * NT of the 128 x 128 tile
+  int boff_row[CB];
+#pragma unroll
+  for (int i = 0; i < CB; ++i) boff_row[i] = (tid + i * NT) / CPR;
+  const int bchunk = (tid % CPR) * 16;
+
+  int e, slice;
+  int64_t row_begin, row_end;
+  __amdgpu_buffer_rsrc_t arsrc;
+  const int8_t *bsrc[CB];
+  bool act;
+  // next item's scale held by this thread: tid < BM per-token scale of row tid, BM <= tid <
+  // BM + BN the scale of weight row tid - BM of the tile
+  float scale_a = 0.f, scale_b = 0.f;
+  int par = 0;  // scale buffers of the current item
+  auto set_item = [&](int g) {
+    moe_find_item(off, ne, n_slices, g, lane, e, slice, row_begin, row_end);
+    arsrc = mp_rsrc(p.a + row_begin * k, static_cast<uint32_t>((row_end - row_begin) * k));
+    act = row_begin + 64 * wm < row_end;
+    const int8_t *bexp = p.b + static_cast<int64_t>(e) * nb_rows * k;
+    const int64_t col0 = static_cast<int64_t>(slice) * (SWI ? BN / 2 : BN);
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      const int lr = boff_row[i];
+      int64_t wr;
+      if (SWI) {
+        const int64_t oc = col0 + (lr % (BN / 2));
+        const int64_t occ = oc < n_out ? oc : n_out - 1;
+        wr = (lr < BN / 2) ? occ : n_out + occ;
+      } else {
+        const int64_t oc = col0 + lr;
+        wr = oc < n_out ? oc : n_out - 1;
+      }
+      bsrc[i] = bexp + wr * k + bchunk;
+    }
+  };
+  // Epilogue scales of the item, loaded ahead of the epilogue (whose stores may alias
+  // them), one per thread: per-token scales (zeros past row_end) and the scales of the
+  // tile's weight rows.  They go to the item's LDS scale buffers after the K loop's first
+  // barrier, so the epilogue waits on no global load.
+  auto load_scales = [&]() {
+    // both loads on every thread (one of them, or both, past its descriptor): no branch
+    const __amdgpu_buffer_rsrc_t srsrc = mp_rsrc(p.s_a + row_begin, static_cast<uint32_t>((row_end - row_begin) * 4));
+    scale_a = __uint_as_float(mp_buf_load4(srsrc, tid < BM ? static_cast<uint32_t>(tid * 4) : 0x80000000u, 0));
+    const __amdgpu_buffer_rsrc_t brsrc =
+        mp_rsrc(p.s_b + static_cast<int64_t>(e) * nb_rows, static_cast<uint32_t>(nb_rows * 4));
+    {
+      const int lr = (tid - BM) & (BN - 1);
+      const int64_t col0 = static_cast<int64_t>(slice) * (SWI ? BN / 2 : BN);
+      int64_t wr;
+      if (SWI) {
+        const int64_t oc = col0 + (lr % (BN / 2));
+        const int64_t occ = oc < n_out ? oc : n_out - 1;
+        wr = (lr < BN / 2) ? occ : n_out + occ;
+      } else {
+        const int64_t oc = col0 + lr;
+        wr = oc < n_out ? oc : n_out - 1;
+      }
+      const bool mine = tid >= BM && tid < BM + BN;
+      scale_b = __uint_as_float(mp_buf_load4(brsrc, mine ? static_cast<uint32_t>(wr * 4) : 0x80000000u, 0));
+    }
+  };
+
+  i4_t areg[D + 1][CA], breg[D + 1][CB];
+  // Every wave issues the same loads on every path (a uniform count keeps the compiler's
+  // load-wait accounting exact across items): idle slabs load A at offsets past the
+  // descriptor (zeros, no memory traffic) and skip the LDS stores and MFMAs.
+  auto load_tile = [&](int set, int64_t kt) {
+    kt = kt < 0 ? 0 : (kt < nkt ? kt : nkt - 1);  // every load stays inside the item's K range
+    const uint32_t koff = static_cast<uint32_t>(kt * BK);
+    const uint32_t ab = act ? aoff0 : 0x80000000u;
+#pragma unroll
+    for (int i = 0; i < CA; ++i) areg[set][i] = mp_buf_load16i(arsrc, ab + static_cast<uint32_t>(8 * i * k), koff);
+#pragma unroll
+    for (int i = 0; i < CB; ++i) breg[set][i] = *reinterpret_cast<const i4_t *>(bsrc[i] + kt * BK);
+  };
+  auto store_tile = [&](int set, int buf) {
+    if (act) {  // wave-uniform
+#pragma unroll
+      for (int i = 0; i < CA; ++i)
+        *reinterpret_cast<i4_t *>(sa + buf * BM * LD + (arow0 + 8 * i) * LD + (lane & 7) * 16) = areg[set][i];
+    }
+#pragma unroll
+    for (int i = 0; i < CB; ++i)
+      *reinterpret_cast<i4_t *>(sb + buf * BN * LD + boff_row[i] * LD + bchunk) = breg[set][i];
+  };
+
+  i16_t acc[TM][TN];
+  int arow_l[TM], brow_l[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) arow_l[i] = (wm * 64 + i * 32 + (lane & 31)) * LD + 16 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int lr = SWI ? (j * (BN / 2) + wn * 32 + (lane & 31)) : (wn * 64 + j * 32 + (lane & 31));
+    brow_l[j] = lr * LD + 16 * (lane >> 5);
+  }
+  auto mma = [&](int cur) {
+    const int8_t *ca = sa + cur * BM * LD;
+    const int8_t *cb = sb + cur * BN * LD;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      i4_t af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i4_t *>(ca + arow_l[i] + ks * 32);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const i4_t *>(cb + brow_l[j] + ks * 32);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  // Register set s holds tile t with t % (D + 1) == s; at step kt tiles kt+1 .. kt+D+1
+  // are in flight.  Tile kt+1 goes to LDS after tile kt is multiplied, and its set is
+  // refilled with tile kt+D+2 (loads past the last tile are clamped to it, never used).
+  // The item's tiles 0 .. D are loaded before the loop.
+  auto k_loop = [&]() {
+    store_tile(0, 0);
+    load_tile(0, D + 1);
+    mp_lds_barrier();
+    // scale buffers par were last read in the epilogue two items back: every wave has
+    // passed at least one barrier since (waves 0-3 and 4-5: wave-uniform branches)
+    if (tid < BM) ssa[par * BM + tid] = scale_a;
+    else if (tid < BM + BN) ssc[par * BN + tid - BM] = scale_b;
+    for (int64_t kt0 = 0; kt0 < nkt; kt0 += D + 1) {
+#pragma unroll
+      for (int d = 0; d <= D; ++d) {
+        const int64_t kt = kt0 + d;
+        const int nxt = (d + 1) % (D + 1);
+        if (kt < nkt) {  // workgroup-uniform
+          if (act) mma(static_cast<int>(kt & 1));
+          if (kt + 1 < nkt) store_tile(nxt, static_cast<int>((kt + 1) & 1));
+        }
+        load_tile(nxt, kt + D + 2);
+        mp_lds_barrier();
+      }
+    }
+  };
+  // tiles 0 .. D of the item (first_tile 0), or D + 1 copies of the current item's last
+  // tile when there is no next item (L2-resident; keeps the load count of every path equal)
+  auto prologue = [&](int64_t first_tile) {
+#pragma unroll
+    for (int d = 0; d <= D; ++d) load_tile(d, first_tile + d);
+  };
+
+  set_item(xcd * share + idx);
+  prologue(0);
+  load_scales();
+  while (true) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    k_loop();
+
+    // the current item's epilogue parameters, then the next item's first tiles (the
+    // loop's last barrier has passed: LDS is free, the register stages are consumed)
+    const bool cur_act = act;
+    const int cur_slice = slice;
+    const int64_t cur_begin = row_begin, cur_end = row_end;
+    idx += stride;
+    const bool has_next = idx < share && xcd * share + idx < total;  // workgroup-uniform
+    if (has_next) set_item(xcd * share + idx);
+    prologue(has_next ? 0 : nkt - 1);
+
+    if (cur_act) {
+      // element r of tile (i, j): local row 64 wm + 32 i + 8 (r >> 2) + 4 (lane >> 5) + (r & 3).
+      // Stores go through buffer descriptors over the item's rows: rows past cur_end and
+      // columns past n_out (offset kOob) are dropped without a branch.  (Guarding each
+      // store with a branch makes the compiler wait for every earlier store.)
+      constexpr uint32_t kOob = 0x80000000u;
+      const uint32_t nrows = static_cast<uint32_t>(cur_end - cur_begin);
+      const uint32_t ldy = static_cast<uint32_t>(p.ldy);
+      const int lm0 = wm * 64 + 4 * (lane >> 5);
+      // the lane's per-token scales: rows lm0 + 32 i + 8 q + (0..3)
+      float sa_r[TM][16];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f4_t s4 = *reinterpret_cast<const f4_t *>(ssa + par * BM + lm0 + 32 * i + 8 * q);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) sa_r[i][4 * q + c] = s4[c];
+        }
+      if (SWI) {
+        // h = silu((acc_g * s_tok) * s_g) * ((acc_u * s_tok) * s_u), and the abs-max of
+        // each row over the wave's 32 columns: the 32 row values of a lane are reduced
+        // across the 32 lanes of its half by a transposing butterfly (31 exchanges; after
+        // it lane l holds the maximum of row value l % 32)
+        const int64_t col = static_cast<int64_t>(cur_slice) * (BN / 2) + wn * 32 + (lane & 31);
+        const bool cval = col < n_out;
+        const float sg = ssc[par * BN + wn * 32 + (lane & 31)], su = ssc[par * BN + BN / 2 + wn * 32 + (lane & 31)];
+        const __amdgpu_buffer_rsrc_t hr = mp_rsrc(static_cast<float *>(p.y) + cur_begin * p.ldy, nrows * ldy * 4);
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int lm = lm0 + i * 32 + 8 * (r >> 2) + (r & 3);
+            const float gv = mp_mul(mp_mul(static_cast<float>(acc[i][0][r]), sa_r[i][r]), sg);
+            const float uv = mp_mul(mp_mul(static_cast<float>(acc[i][1][r]), sa_r[i][r]), su);
+            const float den = mp_add(1.0f, expf(-gv));
+            const float h = mp_mul(__fdiv_rn(gv, den), uv);
+            mp_buf_store4(hr, cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * 4 : kOob,
+                          __float_as_uint(h));
+            v[i * 16 + r] = (cval && static_cast<uint32_t>(lm) < nrows) ? fabsf(h) : 0.f;
+          }
+        moe_max_step<16>(v, lane);
+        moe_max_step<8>(v, lane);
+        moe_max_step<4>(v, lane);
+        moe_max_step<2>(v, lane);
+        moe_max_step<1>(v, lane);
+        const int jv = lane & 31;
+        const int lm = lm0 + (jv >> 4) * 32 + 8 * ((jv & 15) >> 2) + (jv & 3);
+        const uint32_t np = static_cast<uint32_t>(p.n_partial);
+        const __amdgpu_buffer_rsrc_t pr = mp_rsrc(p.amax_partial + cur_begin * p.n_partial, nrows * np * 4);
+        mp_buf_store4(pr, (static_cast<uint32_t>(lm) * np + static_cast<uint32_t>(cur_slice * 2 + wn)) * 4,
+                      __float_as_uint(v[0]));
+      } else {
+        const uint32_t esz = EPI == MP_EPI_F32 ? 4 : 2;
+        const bool bf = p.out_dtype == MP_BF16;
+        const __amdgpu_buffer_rsrc_t yr =
+            mp_rsrc(static_cast<char *>(p.y) + cur_begin * p.ldy * esz, nrows * ldy * esz);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int64_t col = static_cast<int64_t>(cur_slice) * BN + wn * 64 + j * 32 + (lane & 31);
+          const bool cval = col < n_out;
+          const float scj = ssc[par * BN + wn * 64 + j * 32 + (lane & 31)];
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int lm = lm0 + i * 32 + 8 * (r >> 2) + (r & 3);
+              const float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), sa_r[i][r]), scj);
+              const uint32_t off =
+                  cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * esz : kOob;
+              if (EPI == MP_EPI_F32) mp_buf_store4(yr, off, __float_as_uint(v));
+              else mp_buf_store2(yr, off, bf ? mp_f2bf(v) : mp_f2h(v));
+            }
+        }
+      }
+    }
+    load_scales();  // (the next item's, or again the current one's at the end)
+    if (!has_next) break;
+    par ^= 1;
+  }
+}
+
 // ------------------------------------------------------------------ large-M dense GEMM
 // 256 x 256 output tile per workgroup of 8 waves (2 along M x 4 along N), each
 // wave 128 x 64 = 4 x 2 MFMA i32_32x32x32_i8 tiles (128 accumulator registers,
@@ -1221,6 +1592,11 @@ static int mp_tiled_bk() {
 // 128-byte steps with one stage (two per CU), 0 = 64-byte steps (three per CU).
 static int mp_tiled_variant(int64_t k, int64_t wgs) {
   if (k % kTBK2 != 0 || mp_tiled_bk() != 128) return 0;
+  static const int forced = [] {  // MP_W8_TILED_VARIANT=0/1/2 forces a variant (for measurements)
+    const char *e = getenv("MP_W8_TILED_VARIANT");
+    return e ? atoi(e) : -1;
+  }();
+  if (forced >= 0 && forced <= 2) return forced;
   const int64_t cus = mp_cu_count() > 0 ? mp_cu_count() : 256;
   if (wgs <= cus) return 2;
   if (wgs <= 2 * cus) return 1;
@@ -1236,10 +1612,53 @@ static int mp_persist() {
   return v;
 }
 
+// Grouped GEMMs of experts averaging <= 256 rows on i8_moe_kernel: 1 = on (default, two
+// register stages in flight), 2 = three stages, 0 = off (MP_W8_MOE, for measurements).
+static int mp_moe_kernel() {
+  static int v = [] {
+    const char *e = getenv("MP_W8_MOE");
+    return e ? atoi(e) : 1;
+  }();
+  return v;
+}
+
+template <int EPI, int D>
+static int mp_launch_moe_d(const mp_i8_args &a, hipStream_t stream) {
+  const int64_t n_slices = mp_cdiv(a.n, EPI == MP_EPI_SWIGLU ? kMoeBN / 2 : kMoeBN);
+  const int64_t items_ub = n_slices * (mp_cdiv(a.rows, kMoeBM) + a.n_experts);
+  if (items_ub > INT32_MAX / 2) return MP_ERR_SHAPE;
+  // persistent: one workgroup per CU (whole multiples of 8), or fewer when the items are fewer
+  const int64_t cus = mp_cu_count() >= 8 ? mp_cu_count() / 8 * 8 : 256;
+  const int64_t wgs = mp_cdiv(items_ub, 8) * 8;
+  const dim3 grid(static_cast<unsigned>(wgs < cus ? wgs : cus));
+  // > 64 KB of dynamic LDS must be allowed per kernel (idempotent, cheap)
+  if (hipFuncSetAttribute(reinterpret_cast<const void *>(i8_moe_kernel<EPI, D>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMoeSmem)) != hipSuccess)
+    return MP_ERR_HIP;
+  hipLaunchKernelGGL((i8_moe_kernel<EPI, D>), grid, dim3(kMoeThreads), kMoeSmem, stream, a,
+                     static_cast<int>(n_slices));
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+template <int EPI>
+static int mp_launch_moe(const mp_i8_args &a, hipStream_t stream) {
+  if (mp_moe_kernel() == 2) return mp_launch_moe_d<EPI, 2>(a, stream);
+  return mp_launch_moe_d<EPI, 1>(a, stream);
+}
+
 // Shared launcher (dense + grouped).
 int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
   const bool aligned = mp_aligned(a.a, 16) && mp_aligned(a.b, 16);
   if (a.offsets) {
+    // experts of a few hundred rows (serving-size MoE): one workgroup per 256 rows of an
+    // expert and weight slice, so each slice streams once per expert
+    if (mp_moe_kernel() && aligned && a.k % kMoeBK == 0 && a.k <= (1 << 17) && a.n_experts <= kMoeMaxExperts &&
+        a.rows <= kMoeBM * static_cast<int64_t>(a.n_experts) && a.ldy <= (1 << 21) && a.n_partial <= (1 << 21)) {
+      if (epilogue == MP_EPI_SWIGLU) return mp_launch_moe<MP_EPI_SWIGLU>(a, stream);
+      if (epilogue == MP_EPI_F32) return mp_launch_moe<MP_EPI_F32>(a, stream);
+      return mp_launch_moe<MP_EPI_DENSE>(a, stream);
+    }
     // grouped: the large-M kernel (one 256-row chunk of one expert per workgroup, each
     // weight slice streamed once per chunk) for fp32 / SwiGLU outputs, else the tiled kernel
     // (fp32 outputs stay on the tiled kernel unless MP_W8_GROUPED_BIG >= 2: with N = hidden the

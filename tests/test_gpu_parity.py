@@ -351,6 +351,48 @@ def test_moe_chain_matches_oracle(t, h, inter, e):
     assert agree / total >= 0.999
 
 
+# Grouped GEMMs on crafted expert sizes (rows <= 256 per expert on average, the serving-size
+# kernel): empty experts, one-row experts, experts of several 256-row chunks, more than 64
+# experts, output widths that are not tile multiples.  (counts, k, n, inter)
+GROUPED_CASES = [([0, 300, 1, 0, 130, 64], 256, 320, 96), ([128] * 4, 512, 256, 128), ([0, 0, 700], 128, 128, 64),
+                 ([int(c) for c in np.random.default_rng(7).integers(0, 10, 70)], 256, 128, 64)]
+
+
+@pytest.mark.parametrize("counts,k,n,inter", GROUPED_CASES)
+def test_grouped_gemm_expert_sizes(counts, k, n, inter):
+    _say("grouped", len(counts), sum(counts), k, n, inter)
+    g = np.random.default_rng(sum(counts) + k)
+    e, rows = len(counts), sum(counts)
+    q = g.integers(-127, 128, (rows, k)).astype(np.int8)
+    s = (g.random(rows) * 0.01 + 1e-3).astype(np.float32)
+    w2 = g.integers(-127, 128, (e, n, k)).astype(np.int8)
+    s2 = (g.random((e, n)) * 1e-3).astype(np.float32)
+    w13 = g.integers(-127, 128, (e, 2 * inter, k)).astype(np.int8)
+    s13 = (g.random((e, 2 * inter)) * 1e-3).astype(np.float32)
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    ops = _ops()
+    y32 = _np(ops.moe_gmm2(_t(q), _t(s), _t(w2), _t(s2), _t(offs), torch.float32))
+    y16 = _np(ops.moe_gmm2(_t(q), _t(s), _t(w2), _t(s2), _t(offs), torch.float16))
+    qh, sh = ops.moe_gmm1_swiglu_quant(_t(q), _t(s), _t(w13), _t(s13), _t(offs), inter)
+    qh, sh = _np(qh), _np(sh)
+    agree = 0
+    for ex in range(e):
+        lo, hi = offs[ex], offs[ex + 1]
+        if lo == hi:
+            continue
+        ref = O.w8a8_linear_runtime(q[lo:hi], s[lo:hi], w2[ex], s2[ex], out_dtype="fp32")
+        assert np.array_equal(y32[lo:hi], ref), ex
+        assert np.array_equal(y16[lo:hi], O.w8a8_linear_runtime(q[lo:hi], s[lo:hi], w2[ex], s2[ex])), ex
+        acc = O.int_matmul_nt(q[lo:hi], w13[ex])
+        gu = ((acc.astype(np.float32) * s[lo:hi][:, None]).astype(np.float32) * s13[ex][None, :]).astype(np.float32)
+        hh = (O._silu(gu[:, :inter]) * gu[:, inter:]).astype(np.float32)
+        rq, rs = O.quantize_per_token_runtime(hh, in_dtype="fp32")
+        assert np.max(np.abs(qh[lo:hi].astype(int) - rq.astype(int))) <= 1, ex
+        assert np.allclose(sh[lo:hi], rs, rtol=1e-6, atol=0), ex
+        agree += np.sum(qh[lo:hi] == rq)
+    assert agree / max(1, rows * inter) >= 0.999
+
+
 # ------------------------------------------------------------------ fused add + RMSNorm + quant
 # (m, h, residual): vector kernel (H % 8 == 0, 1 / 2 / 8 loads per thread, partial last load),
 # three-pass kernel (H % 8 != 0)
