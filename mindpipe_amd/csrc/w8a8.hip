@@ -290,6 +290,11 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
   static_assert(EPI != MP_EPI_SWIGLU || TN == 2, "SwiGLU pairs gate/up in one wave");
   __shared__ __attribute__((aligned(16))) int8_t sa[2][BM * LD];
   __shared__ __attribute__((aligned(16))) int8_t sb[2][BN * LD];
+  // fp32 / 16-bit epilogues: per-token scales of the tile's rows, then the column scales
+  // and biases (fp32) of its columns, staged once so the epilogue reads no global memory
+  // (a global load there waits for every store issued before it)
+  __shared__ __attribute__((aligned(16))) float tscale[BM + 2 * BN];
+  static_assert(BM + BN == 256, "one epilogue scale per thread");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -347,6 +352,26 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
       wr = oc < n_out ? oc : n_out - 1;
     }
     bsrc[i] = bexp + wr * k + (c % CPR) * 16;
+  }
+
+  // Epilogue scales, loaded before the tiles (one load of each kind on every thread, past
+  // a descriptor or clamped where the thread owns none: the load count is the same on
+  // every path, so the waits below stay partial): thread t < BM the per-token scale of
+  // row row_begin + t (zero past row_end), t >= BM the scale and bias of column
+  // col0 + t - BM (clamped).
+  constexpr bool STAGED_SCALES = EPI != MP_EPI_SWIGLU;
+  float ts_a = 0.f, ts_b = 0.f, ts_bias = 0.f;
+  if constexpr (STAGED_SCALES) {
+    ts_a = __uint_as_float(mp_buf_load4(mp_rsrc(p.s_a + row_begin, static_cast<uint32_t>((row_end - row_begin) * 4)),
+                                        tid < BM ? static_cast<uint32_t>(tid) * 4 : 0x80000000u, 0));
+    int64_t c = col0 + ((tid - BM) & (BN - 1));
+    c = c < n_out ? c : n_out - 1;
+    ts_b = sbexp[c];
+    if (EPI == MP_EPI_DENSE) {
+      const bool hb = p.bias != nullptr;
+      const float bv = mp_load_as_f32(hb ? p.bias : static_cast<const void *>(sbexp), c, hb ? p.bias_dtype : MP_F32);
+      ts_bias = hb ? bv : 0.f;
+    }
   }
 
   // D + 1 register stages of tiles in flight.  Loads are unconditional (clamped to
@@ -418,6 +443,10 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
   store_tile(0, 0);
   load_tile(0, D + 1);
   mp_lds_barrier();
+  if constexpr (STAGED_SCALES) {  // read in the epilogue, after the K loop's barriers
+    tscale[tid] = tid < BM ? ts_a : ts_b;
+    if (tid >= BM) tscale[BN + tid] = ts_bias;  // waves 2-3: uniform
+  }
   for (int64_t kt0 = 0; kt0 < nkt; kt0 += D + 1) {
 #pragma unroll
     for (int d = 0; d <= D; ++d) {
@@ -459,24 +488,34 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
       }
     }
   } else {
+    // stores through a descriptor over the tile's rows: rows past row_end and columns past
+    // n_out (offset past the descriptor) are dropped without a branch (a branch per store
+    // makes the compiler wait for the stores before it)
+    const uint32_t esz = (EPI == MP_EPI_F32 || p.out_dtype == MP_F32) ? 4 : 2;
+    const bool bf = p.out_dtype == MP_BF16, hb = EPI == MP_EPI_DENSE && p.bias != nullptr;
+    const uint32_t ldy = static_cast<uint32_t>(p.ldy);
+    const __amdgpu_buffer_rsrc_t yr = mp_rsrc(static_cast<char *>(p.y) + row_begin * p.ldy * esz,
+                                              static_cast<uint32_t>(row_end - row_begin) * ldy * esz);
+    const int lm0 = wm * WM + 4 * (lane >> 5);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int64_t col = col0 + wn * WN + j * 32 + (lane & 31);
-      if (col >= n_out) continue;
-      const float sb = sbexp[col];
-      const float bv = (EPI == MP_EPI_DENSE && p.bias) ? mp_load_as_f32(p.bias, col, p.bias_dtype) : 0.f;
+      const int cl = wn * WN + j * 32 + (lane & 31);
+      const int64_t col = col0 + cl;
+      const bool cval = col < n_out;
+      const float sbv = tscale[BM + cl], bv = tscale[BM + BN + cl];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = row_begin + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (m >= row_end) continue;
-          float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), p.s_a[m]), sb);
-          if (EPI == MP_EPI_DENSE) {
-            if (p.bias) v = mp_add(v, bv);
-            mp_store_from_f32(p.y, m * p.ldy + col, p.out_dtype, v);
-          } else {
-            static_cast<float *>(p.y)[m * p.ldy + col] = v;
+        for (int q = 0; q < 4; ++q) {
+          const f4_t s4 = *reinterpret_cast<const f4_t *>(tscale + lm0 + i * 32 + 8 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int lm = lm0 + i * 32 + 8 * q + e;
+            float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][4 * q + e]), s4[e]), sbv);
+            if (hb) v = mp_add(v, bv);
+            const uint32_t off = cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * esz : 0x80000000u;
+            if (esz == 4) mp_buf_store4(yr, off, __float_as_uint(v));
+            else mp_buf_store2(yr, off, bf ? mp_f2bf(v) : mp_f2h(v));
           }
         }
     }
@@ -1649,7 +1688,8 @@ static int mp_launch_moe(const mp_i8_args &a, hipStream_t stream) {
 
 // Shared launcher (dense + grouped).
 int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
-  const bool aligned = mp_aligned(a.a, 16) && mp_aligned(a.b, 16);
+  // the tiled kernel addresses a tile's 128 output rows through one descriptor
+  const bool aligned = mp_aligned(a.a, 16) && mp_aligned(a.b, 16) && a.ldy < (int64_t(1) << 23);
   if (a.offsets) {
     // experts of a few hundred rows (serving-size MoE): one workgroup per 256 rows of an
     // expert and weight slice, so each slice streams once per expert
