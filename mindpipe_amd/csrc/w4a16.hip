@@ -642,16 +642,27 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  auto emit = [&](int m, int col, float v, float u) {
+  // biases of the lane's NO output columns (col0 + 16 j + lane % 16), read before any
+  // store: a load after a store waits for it
+  float bg[NO], bu[NO];
+#pragma unroll
+  for (int j = 0; j < NO; ++j) {
+    int col = col0 + j * 16 + (lane & 15);
+    col = col < n_out ? col : n_out - 1;
+    bg[j] = bias ? mp_h2f(bias[col]) : 0.f;
+    bu[j] = (SWI && bias) ? mp_h2f(bias[n_out + col]) : 0.f;
+  }
+  auto emit = [&](int m, int j, float v, float u) {
+    const int col = col0 + j * 16 + (lane & 15);
     if (m < m_rows && col < n_out) {
       if (SWI) {
         if (bias) {
-          v += mp_h2f(bias[col]);
-          u += mp_h2f(bias[n_out + col]);
+          v += bg[j];
+          u += bu[j];
         }
         y[static_cast<int64_t>(m) * n_out + col] = mp_swiglu_h(mp_rh(v), mp_rh(u));
       } else {
-        if (bias) v += mp_h2f(bias[col]);
+        if (bias) v += bg[j];
         y[static_cast<int64_t>(m) * n_out + col] = mp_f2h(v);
       }
     }
@@ -674,7 +685,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
         v += red[w][sg][l];
         if (SWI) u += red[w][sg + NO * 4][l];
       }
-      emit(t * 16 + 4 * (l >> 4) + i, col0 + j * 16 + (l & 15), v, u);
+      emit(t * 16 + 4 * (l >> 4) + i, j, v, u);  // l == lane: the stride is a multiple of 64
     }
   } else {
 #pragma unroll
@@ -683,7 +694,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
       for (int j = 0; j < NO; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          emit(t * 16 + 4 * kq + i, col0 + j * 16 + (lane & 15), acc[t][j][i], SWI ? acc[t][j + NO][i] : 0.f);
+          emit(t * 16 + 4 * kq + i, j, acc[t][j][i], SWI ? acc[t][j + NO][i] : 0.f);
   }
 }
 
