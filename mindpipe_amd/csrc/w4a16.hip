@@ -1041,8 +1041,6 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
   }
 }
 
-// Smallest M routed to the batched decode kernel is M > this value
-// (MP_W4_BATCH_MIN_M overrides it, for measurements).
 // Measurement knobs for the one-row GEMV shape choice: MP_W4_GEMV_R (rows per
 // wave), MP_W4_GEMV_C (chunks per iteration), MP_W4_GEMV_S (waves splitting K);
 // MP_W4_GEMV_OFF=1 routes one-row calls to the general decode kernel.
@@ -1069,10 +1067,13 @@ static int mp_batch_env(int which) {
   return v[which];
 }
 
+// The batched kernel takes M > this value (default 1: every 2 <= M <= 64, measured faster than
+// the LDS-staged kernel at 2..4 rows too, and the fused SwiGLU path then shares its sums);
+// MP_W4_BATCH_MIN_M overrides it, for measurements.
 static int mp_batch_min_m() {
   static int v = [] {
     const char *e = getenv("MP_W4_BATCH_MIN_M");
-    return e ? atoi(e) : 4;
+    return e ? atoi(e) : 1;
   }();
   return v;
 }
