@@ -703,15 +703,22 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
 // 128x128 output tile per workgroup of 4 waves (64x64 each, 2x2 MFMA
 // f32_32x32x16_f16 tiles), BK = 64.  Activations are staged to LDS as is; the
 // packed weights are dequantised by (u - z) * s in fp16 (the exact fp16 values
-// of the reference's pseudo-quantized weight) into LDS.  Double-buffered LDS.
+// of the reference's pseudo-quantized weight) into LDS.  Double-buffered LDS and
+// D + 1 register stages of K tiles in flight (the LDS-only barriers leave them
+// outstanding).  Every load is unconditional (rows past M read zeros through the
+// activation descriptor, K tiles past the end are clamped), so each wait is a
+// partial one; the epilogue stores through a descriptor without branches.
 constexpr int kPBM = 128, kPBN = 128, kPBK = 64, kPLD = kPBK + 8;  // row stride in halves
+constexpr int kPrefillStages = 4;  // register stages of K tiles
 
+template <int D>
 __global__ __launch_bounds__(256) void w4a16_prefill_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups, int gs,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
   __shared__ __attribute__((aligned(16))) uint16_t sa[2][kPBM * kPLD];
   __shared__ __attribute__((aligned(16))) uint16_t sb[2][kPBN * kPLD];
+  constexpr uint32_t kOob = 0x80000000u;  // past every descriptor (sizes < 2^31, host check)
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -720,42 +727,45 @@ __global__ __launch_bounds__(256) void w4a16_prefill_kernel(
 
   // A staging: 128 rows x 64 halves = 1024 chunks of 16 B, 4 per thread
   // B staging: 128 rows x 8 words = 256 chunks of 16 B (4 words), 1 per thread
+  const auto xr = mp_rsrc(x, static_cast<uint32_t>(m_rows) * static_cast<uint32_t>(k) * 2);
+  uint32_t aoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + i * 256;
+    const int m = m0 + (c >> 3);
+    aoff[i] = m < m_rows ? (static_cast<uint32_t>(m) * static_cast<uint32_t>(k) + (c & 7) * 8) * 2 : kOob;
+  }
   const int brow = tid >> 1, bhalf = tid & 1;  // each thread: 4 words = 32 columns
   const int bn = n0 + brow < n_cols ? n0 + brow : n_cols - 1;
   const uint32_t *bsrc = wq + static_cast<int64_t>(bn) * kw + 4 * bhalf;
+  const uint16_t *zsrc = zr ? zr : sc;  // (no zeros: the scale is read again and 8 used)
 
-  uint4 areg[4];
-  uint4 breg;
-  float bs = 0.f, bz = 0.f;
-
-  auto load_tile = [&](int kt) {
+  uint4 areg[D + 1][4];
+  uint4 breg[D + 1];
+  uint32_t sz[D + 1];  // scale bits | zero bits << 16 of the thread's 32 columns
+  const int nkt = k / kPBK;
+  auto load_tile = [&](int set, int kt) {
+    kt = kt < nkt ? kt : nkt - 1;
     const int kb = kt * kPBK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + i * 256;
-      const int r = c >> 3, cc = c & 7;
-      const int m = m0 + r;
-      if (m < m_rows)
-        areg[i] = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(m) * k + kb + cc * 8);
-      else
-        areg[i] = make_uint4(0, 0, 0, 0);
-    }
-    breg = *reinterpret_cast<const uint4 *>(bsrc + kb / 8);
-    const int gi = (kb + 32 * bhalf) / gs;
-    bs = mp_h2f(sc[static_cast<int64_t>(bn) * n_groups + gi]);
-    bz = zr ? mp_h2f(zr[static_cast<int64_t>(bn) * n_groups + gi]) : 8.0f;
+    for (int i = 0; i < 4; ++i)
+      areg[set][i] = __builtin_bit_cast(uint4, mp_buf_load16i(xr, aoff[i] + static_cast<uint32_t>(kb) * 2, 0));
+    breg[set] = *reinterpret_cast<const uint4 *>(bsrc + kb / 8);
+    const int64_t gi = static_cast<int64_t>(bn) * n_groups + (kb + 32 * bhalf) / gs;
+    sz[set] = static_cast<uint32_t>(sc[gi]) | (static_cast<uint32_t>(zsrc[gi]) << 16);
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int set, int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + i * 256;
       const int r = c >> 3, cc = c & 7;
-      *reinterpret_cast<uint4 *>(&sa[buf][r * kPLD + cc * 8]) = areg[i];
+      *reinterpret_cast<uint4 *>(&sa[buf][r * kPLD + cc * 8]) = areg[set][i];
     }
     // exact fp16 dequant: (1024+u) - (1024+z) is exact, times s rounds once
+    const float bz = zr ? mp_h2f(static_cast<uint16_t>(sz[set] >> 16)) : 8.0f;
     const __half2 off = __float2half2_rn(1024.0f + bz);
-    const __half2 s2 = __float2half2_rn(bs);
-    const uint32_t wsel[4] = {breg.x, breg.y, breg.z, breg.w};
+    const __half2 s2 = __float2half2_rn(mp_h2f(static_cast<uint16_t>(sz[set] & 0xFFFFu)));
+    const uint32_t wsel[4] = {breg[set].x, breg[set].y, breg[set].z, breg[set].w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t w = wsel[q];
@@ -778,14 +788,7 @@ __global__ __launch_bounds__(256) void w4a16_prefill_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  const int nkt = k / kPBK;
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nkt) load_tile(kt + 1);
+  auto mma = [&](int cur) {
 #pragma unroll
     for (int ks = 0; ks < kPBK / 16; ++ks) {
       h8_t af[2], bf[2];
@@ -805,25 +808,47 @@ __global__ __launch_bounds__(256) void w4a16_prefill_kernel(
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nkt) {
-      store_tile(cur ^ 1);
+  };
+
+  // Register set s holds tile t with t % (D + 1) == s; at step kt tiles kt+1 .. kt+D+1 are
+  // in flight.  Tile kt+1 goes to LDS after tile kt is multiplied, and its set is refilled
+  // with tile kt+D+2 (clamped past the end, never used).
+#pragma unroll
+  for (int d = 0; d <= D; ++d) load_tile(d, d);
+  store_tile(0, 0);
+  load_tile(0, D + 1);
+  mp_lds_barrier();
+  for (int kt0 = 0; kt0 < nkt; kt0 += D + 1) {
+#pragma unroll
+    for (int d = 0; d <= D; ++d) {
+      const int kt = kt0 + d;
+      const int nxt = (d + 1) % (D + 1);
+      if (kt < nkt) {  // workgroup-uniform
+        mma(kt & 1);
+        if (kt + 1 < nkt) store_tile(nxt, (kt + 1) & 1);
+      }
+      load_tile(nxt, kt + D + 2);
+      mp_lds_barrier();
     }
-    __syncthreads();
   }
 
+  // epilogue: biases first, then stores through a descriptor (rows past M and columns past
+  // N dropped without a branch)
+  const auto yr = mp_rsrc(y, static_cast<uint32_t>(m_rows) * static_cast<uint32_t>(n_cols) * 2);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+    const bool cval = col < n_cols;
+    const float bv = bias ? mp_h2f(bias[cval ? col : n_cols - 1]) : 0.f;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-      if (col >= n_cols) continue;
-      const float b = bias ? mp_h2f(bias[col]) : 0.f;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < m_rows) y[static_cast<int64_t>(m) * n_cols + col] = mp_f2h(acc[i][j][r] + b);
+        const uint32_t o = (cval && m < m_rows) ? (static_cast<uint32_t>(m) * static_cast<uint32_t>(n_cols) + col) * 2 : kOob;
+        mp_buf_store2(yr, o, mp_f2h(acc[i][j][r] + bv));
       }
-    }
+  }
 }
 
 // ------------------------------------------------------------------ any-shape fallback
@@ -1412,9 +1437,10 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     }
 #undef MP_W4_DEC_S
 #undef MP_W4_DEC
-  } else if (m > 64 && k % kPBK == 0 && group_size % 32 == 0 && aligned) {
+  } else if (m > 64 && k % kPBK == 0 && group_size % 32 == 0 && aligned && m * k * 2 < (int64_t(1) << 31) &&
+             m * n * 2 < (int64_t(1) << 31)) {
     const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, kPBM)));
-    hipLaunchKernelGGL(w4a16_prefill_kernel, grid, dim3(256), 0, s, xp, static_cast<int>(m),
+    hipLaunchKernelGGL(w4a16_prefill_kernel<kPrefillStages - 1>, grid, dim3(256), 0, s, xp, static_cast<int>(m),
                        static_cast<int>(k), wp, static_cast<int>(n), sp, zp, n_groups, group_size, bp, yp);
   } else {
     hipLaunchKernelGGL(w4a16_simple_kernel, dim3(static_cast<unsigned>(mp_cdiv(m * n, 256))), dim3(256), 0, s,
