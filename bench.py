@@ -168,9 +168,10 @@ def leg_moe(ops, steps, warmup, t=512, h=4096, inter=14336, e=8, top_k=2):
     ops_count = 2.0 * t * top_k * (2 * inter * h + h * inter)
     gbs = wbytes / (ms * 1e-3) / 1e9
     tops = ops_count / (ms * 1e-3) / 1e12
+    t1, t2 = _traffic("moe_gmm1_mixtral_t512"), _traffic("moe_gmm2_mixtral_t512")
     return {"tokens": t, "experts": e, "top_k": top_k, "hidden": h, "inter": inter, "ms_chain": ms,
             "weight_bytes": wbytes, "gb_s": gbs, "tops": tops,
-            "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s"),
+            "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", t1 + t2 if t1 and t2 else None),
             "roofline_mfma": _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS")}
 
 
@@ -297,6 +298,21 @@ def traffic_probe(ops):
     sw = torch.rand(11008, device="cuda")
     for _ in range(3):
         ops.w8a8_gemm(qx, st, qw, sw, None, torch.float16)
+    del qx, qw
+    # the Mixtral MoE leg's grouped GEMMs (routing of the bench leg: 512 tokens, top-2 of 8)
+    e, h, inter = 8, 4096, 14336
+    counts = [126, 117, 122, 140, 133, 124, 133, 129]
+    offs = torch.tensor([0] + [sum(counts[:i + 1]) for i in range(e)], dtype=torch.int64, device="cuda")
+    rows = sum(counts)
+    routed = torch.randint(-127, 128, (rows, h), dtype=torch.int8, device="cuda")
+    rs = torch.rand(rows, device="cuda") * 0.01
+    w13 = torch.randint(-127, 128, (e, 2 * inter, h), dtype=torch.int8, device="cuda")
+    s13 = torch.rand(e, 2 * inter, device="cuda") * 1e-3
+    w2 = torch.randint(-127, 128, (e, h, inter), dtype=torch.int8, device="cuda")
+    s2 = torch.rand(e, h, device="cuda") * 1e-3
+    for _ in range(3):
+        q, s = ops.moe_gmm1_swiglu_quant(routed, rs, w13, s13, offs, inter)
+        ops.moe_gmm2(q, s, w2, s2, offs)
     torch.cuda.synchronize()
     print("traffic probe done")
 
