@@ -11,53 +11,159 @@ constexpr int kMaxExperts = 1024;
 // Single-workgroup stable counting sort of the T*top_k assignments by expert.
 // Writes group_offsets [E+1] and row_of_slot [T*top_k].  Assignment a =
 // t*top_k + j keeps (t, j) order inside its expert, so the routed layout is
-// deterministic.  One wave does the placement; rank within a 64-assignment
-// batch comes from a ballot over lanes holding the same expert.
-__global__ __launch_bounds__(256) void moe_route_kernel(const int32_t *__restrict__ ids, int64_t n_assign,
-                                                       int n_experts, int64_t *__restrict__ offsets,
-                                                       int32_t *__restrict__ row_of_slot,
-                                                       int32_t *__restrict__ invalid) {
-  __shared__ int counts[kMaxExperts];
-  __shared__ int cursor[kMaxExperts];
-  for (int e = threadIdx.x; e < n_experts; e += blockDim.x) counts[e] = 0;
+// deterministic.  Wave w owns the w-th quarter of the assignments (whole batches
+// of 64): it counts its quarter per expert (LDS atomics; the ids are cached in LDS,
+// the first kRouteLds of them), the per-(wave, expert) bases follow from a prefix
+// over experts and waves, and each wave then places its quarter 64 at a time,
+// ranking a lane among the lower lanes of its expert with one ballot per distinct
+// expert of the batch.
+constexpr int kRouteLds = 16384;
+constexpr int kRouteWaves = 4;
+
+__global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(const int32_t *__restrict__ ids,
+                                                                    int64_t n_assign, int n_experts,
+                                                                    int64_t *__restrict__ offsets,
+                                                                    int32_t *__restrict__ row_of_slot,
+                                                                    int32_t *__restrict__ invalid) {
+  __shared__ int cnt[kRouteWaves][kMaxExperts];  // per-wave counts, then per-wave cursors
+  __shared__ int16_t sid[kRouteLds];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < kRouteWaves * n_experts; i += blockDim.x) cnt[i / n_experts][i % n_experts] = 0;
   __syncthreads();
-  for (int64_t a = threadIdx.x; a < n_assign; a += blockDim.x) {
+  const int64_t nb = (n_assign + 63) / 64;                         // batches of 64
+  const int64_t per = (nb + kRouteWaves - 1) / kRouteWaves;       // batches per wave
+  const int64_t lo = wave * per * 64, hi = (wave + 1) * per * 64 < n_assign ? (wave + 1) * per * 64 : n_assign;
+  for (int64_t a = lo + lane; a < hi; a += 64) {
     const int e = ids[a];
-    if (e >= 0 && e < n_experts) atomicAdd(&counts[e], 1);
+    const bool ok = e >= 0 && e < n_experts;
+    if (a < kRouteLds) sid[a] = static_cast<int16_t>(ok ? e : -1);
+    if (ok) atomicAdd(&cnt[wave][e], 1);
     else if (invalid) atomicAdd(invalid, 1);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
+    // offsets[e] = sum of earlier experts; the cursor of (wave w, expert e) starts after the
+    // earlier waves' rows of e
     int64_t run = 0;
     offsets[0] = 0;
     for (int e = 0; e < n_experts; ++e) {
-      cursor[e] = static_cast<int>(run);
-      run += counts[e];
+      for (int w = 0; w < kRouteWaves; ++w) {
+        const int c = cnt[w][e];
+        cnt[w][e] = static_cast<int>(run);
+        run += c;
+      }
       offsets[e + 1] = run;
     }
   }
   __syncthreads();
-  if (threadIdx.x >= 64) return;
-  const int lane = threadIdx.x;
-  for (int64_t base = 0; base < n_assign; base += 64) {
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  for (int64_t base = lo; base < hi; base += 64) {
     const int64_t a = base + lane;
-    const bool valid = a < n_assign;
-    const int e = valid ? ids[a] : -1;
-    const bool ok = valid && e >= 0 && e < n_experts;
-    // rank among lower lanes with the same expert
-    int rank = 0, total = 0;
-    for (int l = 0; l < 64; ++l) {
-      const int el = __shfl(e, l, 64);
-      const int same = (el == e) && ok;
-      rank += same && (l < lane);
-      total += same;
+    const bool valid = a < hi;
+    int e = -1;
+    if (valid) {
+      if (a < kRouteLds) {
+        e = sid[a];
+      } else {
+        const int v = ids[a];
+        e = (v >= 0 && v < n_experts) ? v : -1;
+      }
     }
-    const int pos = ok ? cursor[e] + rank : -1;
+    const bool ok = e >= 0;
+    int rank = 0, total = 0;
+    uint64_t pending = __ballot(ok);
+    while (pending) {  // one pass per distinct expert of the batch (wave-uniform)
+      const int leader = __ffsll(static_cast<long long>(pending)) - 1;
+      const int ee = __builtin_amdgcn_readlane(e, leader);
+      const uint64_t m = __ballot(ok && e == ee);
+      if (ok && e == ee) {
+        rank = __popcll(m & below);
+        total = __popcll(m);
+      }
+      pending &= ~m;
+    }
+    const int pos = ok ? cnt[wave][e] + rank : -1;
     if (valid) row_of_slot[a] = pos;
-    // the last lane of each expert in this batch advances the cursor
+    // the last lane of each expert in this batch advances the wave's cursor
     __builtin_amdgcn_wave_barrier();
-    if (ok && rank == total - 1) cursor[e] += total;
+    if (ok && rank == total - 1) cnt[wave][e] += total;
     __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// 16 bytes of a row as floats: 8 values of a 16-bit dtype or 4 of fp32
+template <int DT>
+struct Chunk16 {
+  static constexpr int N = DT == MP_F32 ? 4 : 8;
+};
+template <int DT>
+__device__ __forceinline__ void chunk_to_f32(const uint4 v, float (&f)[Chunk16<DT>::N]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  if constexpr (DT == MP_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(w[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = static_cast<uint16_t>(w[i] & 0xFFFFu), hi = static_cast<uint16_t>(w[i] >> 16);
+      f[2 * i] = DT == MP_F16 ? mp_h2f(lo) : mp_bf2f(lo);
+      f[2 * i + 1] = DT == MP_F16 ? mp_h2f(hi) : mp_bf2f(hi);
+    }
+  }
+}
+// per-token code of v with scale s (s == 0: 0), the runtime quantizer's expression
+__device__ __forceinline__ uint32_t moe_code(float v, float s) {
+  float q = (s == 0.f) ? 0.f : rintf(v / s);
+  q = fminf(fmaxf(q, -127.f), 127.f);
+  return static_cast<uint32_t>(static_cast<int>(q)) & 0xFFu;
+}
+__device__ __forceinline__ float moe_block_max(float amax, float *wmax) {
+  const int tid = threadIdx.x;
+  amax = mp_wave_max(amax);
+  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
+  __syncthreads();
+  return fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+}
+
+// Per-token quant of x[t] for routed row row_of_slot[a], 16-byte loads: the row is
+// read once for the abs-max and again (from L2) for the codes, stored 4 or 8 at a time.
+// Needs h a multiple of the values per 16 bytes and 16-byte aligned rows (host check).
+template <int DT>
+__global__ __launch_bounds__(256) void moe_permute_quant_vec_kernel(const void *__restrict__ x, int64_t h, int top_k,
+                                                                   const int32_t *__restrict__ row_of_slot,
+                                                                   int8_t *__restrict__ routed,
+                                                                   float *__restrict__ routed_scale) {
+  constexpr int N = Chunk16<DT>::N;
+  constexpr int ESZ = DT == MP_F32 ? 4 : 2;
+  __shared__ float wmax[4];
+  const int64_t a = blockIdx.x;
+  const int64_t t = a / top_k;
+  const int r = row_of_slot[a];
+  if (r < 0) return;  // workgroup-uniform
+  const int tid = threadIdx.x;
+  const int64_t nch = h / N;
+  const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const char *>(x) + t * h * ESZ);
+  float amax = 0.f;
+  for (int64_t c = tid; c < nch; c += 256) {
+    float f[N];
+    chunk_to_f32<DT>(src[c], f);
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  }
+  amax = moe_block_max(amax, wmax);
+  const float s = amax / 127.0f;
+  if (tid == 0) routed_scale[r] = s;
+  int8_t *dst = routed + static_cast<int64_t>(r) * h;
+  for (int64_t c = tid; c < nch; c += 256) {
+    float f[N];
+    chunk_to_f32<DT>(src[c], f);
+    uint32_t w[N / 4];
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i)
+      w[i] = moe_code(f[4 * i], s) | (moe_code(f[4 * i + 1], s) << 8) | (moe_code(f[4 * i + 2], s) << 16) |
+             (moe_code(f[4 * i + 3], s) << 24);
+    if constexpr (N == 8) *reinterpret_cast<uint2 *>(dst + c * 8) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t *>(dst + c * 4) = w[0];
   }
 }
 
@@ -113,6 +219,61 @@ __global__ __launch_bounds__(256) void moe_requant_kernel(const float *__restric
   }
 }
 
+// Requant with 16-byte loads of the fp32 SwiGLU rows (inter % 4 == 0): four codes per store.
+__global__ __launch_bounds__(256) void moe_requant_vec_kernel(const float *__restrict__ hbuf,
+                                                             const float *__restrict__ part, int n_partial,
+                                                             int64_t inter, int8_t *__restrict__ q,
+                                                             float *__restrict__ s_out) {
+  __shared__ float wmax[4];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  float amax = 0.f;
+  for (int i = tid; i < n_partial; i += 256) amax = fmaxf(amax, part[r * n_partial + i]);
+  amax = moe_block_max(amax, wmax);
+  const float s = amax / 127.0f;
+  if (tid == 0) s_out[r] = s;
+  const float4 *src = reinterpret_cast<const float4 *>(hbuf + r * inter);
+  uint32_t *dst = reinterpret_cast<uint32_t *>(q + r * inter);
+  for (int64_t c = tid; c < inter / 4; c += 256) {
+    const float4 v = src[c];
+    dst[c] = moe_code(v.x, s) | (moe_code(v.y, s) << 8) | (moe_code(v.z, s) << 16) | (moe_code(v.w, s) << 24);
+  }
+}
+
+// Weighted un-permute, four columns per thread (h % 4 == 0, 16-byte aligned y rows):
+// out[t, c] = sum_j w[t, j] * y[row_of_slot[t, j], c] in fp32 in slot order, one rounding.
+__global__ __launch_bounds__(256) void moe_combine_vec_kernel(const float *__restrict__ y,
+                                                             const int32_t *__restrict__ row_of_slot,
+                                                             const float *__restrict__ w, int64_t t_count,
+                                                             int top_k, int64_t h, void *__restrict__ out,
+                                                             int out_dtype) {
+  const int64_t q4 = h / 4;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= t_count * q4) return;
+  const int64_t t = tid / q4, c = (tid % q4) * 4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < top_k; ++j) {
+    const int r = row_of_slot[t * top_k + j];
+    if (r < 0) continue;
+    const float wj = w[t * top_k + j];
+    const float4 v = *reinterpret_cast<const float4 *>(y + static_cast<int64_t>(r) * h + c);
+    acc[0] = mp_add(acc[0], mp_mul(wj, v.x));
+    acc[1] = mp_add(acc[1], mp_mul(wj, v.y));
+    acc[2] = mp_add(acc[2], mp_mul(wj, v.z));
+    acc[3] = mp_add(acc[3], mp_mul(wj, v.w));
+  }
+  const int64_t o = t * h + c;
+  if (out_dtype == MP_F32) {
+    *reinterpret_cast<float4 *>(static_cast<float *>(out) + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  } else {
+    uint16_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = out_dtype == MP_F16 ? mp_f2h(acc[i]) : mp_f2bf(acc[i]);
+    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + o) =
+        make_uint2(b[0] | (static_cast<uint32_t>(b[1]) << 16), b[2] | (static_cast<uint32_t>(b[3]) << 16));
+  }
+}
+
 __global__ void moe_combine_kernel(const float *__restrict__ y, const int32_t *__restrict__ row_of_slot,
                                    const float *__restrict__ w, int64_t t_count, int top_k, int64_t h,
                                    void *__restrict__ out, int out_dtype) {
@@ -150,12 +311,26 @@ extern "C" int mp_moe_permute_quant(const void *x, int x_dtype, int64_t t, int64
   if (workspace && workspace_bytes < mp_moe_route_workspace_bytes(t, h, n_experts)) return MP_ERR_WORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t n_assign = t * top_k;
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 0, s, topk_ids, n_assign, n_experts, group_offsets,
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(64 * kRouteWaves), 0, s, topk_ids, n_assign, n_experts, group_offsets,
                      row_of_slot, static_cast<int32_t *>(workspace));
   MP_CHECK_LAUNCH();
   if (n_assign == 0) return MP_OK;
-  hipLaunchKernelGGL(moe_permute_quant_kernel, dim3(static_cast<unsigned>(n_assign)), dim3(256), 0, s, x, x_dtype, h,
-                     top_k, row_of_slot, routed, routed_scale);
+  const int per16 = x_dtype == MP_F32 ? 4 : 8;  // values per 16 bytes
+  if (h % per16 == 0 && mp_aligned(x, 16) && mp_aligned(routed, 8)) {
+    const dim3 g(static_cast<unsigned>(n_assign));
+    if (x_dtype == MP_F16)
+      hipLaunchKernelGGL(moe_permute_quant_vec_kernel<MP_F16>, g, dim3(256), 0, s, x, h, top_k, row_of_slot, routed,
+                         routed_scale);
+    else if (x_dtype == MP_BF16)
+      hipLaunchKernelGGL(moe_permute_quant_vec_kernel<MP_BF16>, g, dim3(256), 0, s, x, h, top_k, row_of_slot, routed,
+                         routed_scale);
+    else
+      hipLaunchKernelGGL(moe_permute_quant_vec_kernel<MP_F32>, g, dim3(256), 0, s, x, h, top_k, row_of_slot, routed,
+                         routed_scale);
+  } else {
+    hipLaunchKernelGGL(moe_permute_quant_kernel, dim3(static_cast<unsigned>(n_assign)), dim3(256), 0, s, x, x_dtype, h,
+                       top_k, row_of_slot, routed, routed_scale);
+  }
   MP_CHECK_LAUNCH();
   return MP_OK;
 }
@@ -199,8 +374,12 @@ extern "C" int mp_i8_gemm_swiglu_requant(const int8_t *routed, const float *rout
   a.ldy = inter;
   int rc = mp_launch_i8_gemm(a, MP_EPI_SWIGLU, s);
   if (rc != MP_OK) return rc;
-  hipLaunchKernelGGL(moe_requant_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, hbuf, part,
-                     a.n_partial, inter, q_out, s_out);
+  if (inter % 4 == 0 && mp_aligned(q_out, 4) && mp_aligned(hbuf, 16))
+    hipLaunchKernelGGL(moe_requant_vec_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, hbuf, part,
+                       a.n_partial, inter, q_out, s_out);
+  else
+    hipLaunchKernelGGL(moe_requant_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, hbuf, part,
+                       a.n_partial, inter, q_out, s_out);
   MP_CHECK_LAUNCH();
   return MP_OK;
 }
@@ -235,8 +414,12 @@ extern "C" int mp_moe_unpermute_combine(const float *y, const int32_t *row_of_sl
   if (out_dtype != MP_F32 && out_dtype != MP_F16 && out_dtype != MP_BF16) return MP_ERR_DTYPE;
   if (t < 0 || top_k <= 0 || h <= 0) return MP_ERR_SHAPE;
   if (t == 0) return MP_OK;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(static_cast<unsigned>(mp_cdiv(t * h, 256))), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), y, row_of_slot, topk_w, t, top_k, h, out, out_dtype);
+  if (h % 4 == 0 && mp_aligned(y, 16) && mp_aligned(out, out_dtype == MP_F32 ? 16 : 8))
+    hipLaunchKernelGGL(moe_combine_vec_kernel, dim3(static_cast<unsigned>(mp_cdiv(t * (h / 4), 256))), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), y, row_of_slot, topk_w, t, top_k, h, out, out_dtype);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(static_cast<unsigned>(mp_cdiv(t * h, 256))), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), y, row_of_slot, topk_w, t, top_k, h, out, out_dtype);
   MP_CHECK_LAUNCH();
   return MP_OK;
 }
