@@ -91,26 +91,6 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(const int32
   }
 }
 
-// 16 bytes of a row as floats: 8 values of a 16-bit dtype or 4 of fp32
-template <int DT>
-struct Chunk16 {
-  static constexpr int N = DT == MP_F32 ? 4 : 8;
-};
-template <int DT>
-__device__ __forceinline__ void chunk_to_f32(const uint4 v, float (&f)[Chunk16<DT>::N]) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  if constexpr (DT == MP_F32) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(w[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint16_t lo = static_cast<uint16_t>(w[i] & 0xFFFFu), hi = static_cast<uint16_t>(w[i] >> 16);
-      f[2 * i] = DT == MP_F16 ? mp_h2f(lo) : mp_bf2f(lo);
-      f[2 * i + 1] = DT == MP_F16 ? mp_h2f(hi) : mp_bf2f(hi);
-    }
-  }
-}
 // per-token code of v with scale s (s == 0: 0), the runtime quantizer's expression
 __device__ __forceinline__ uint32_t moe_code(float v, float s) {
   float q = (s == 0.f) ? 0.f : rintf(v / s);
@@ -133,7 +113,7 @@ __global__ __launch_bounds__(256) void moe_permute_quant_vec_kernel(const void *
                                                                    const int32_t *__restrict__ row_of_slot,
                                                                    int8_t *__restrict__ routed,
                                                                    float *__restrict__ routed_scale) {
-  constexpr int N = Chunk16<DT>::N;
+  constexpr int N = MpChunk16<DT>::N;
   constexpr int ESZ = DT == MP_F32 ? 4 : 2;
   __shared__ float wmax[4];
   const int64_t a = blockIdx.x;
@@ -146,7 +126,7 @@ __global__ __launch_bounds__(256) void moe_permute_quant_vec_kernel(const void *
   float amax = 0.f;
   for (int64_t c = tid; c < nch; c += 256) {
     float f[N];
-    chunk_to_f32<DT>(src[c], f);
+    mp_chunk_to_f32<DT>(src[c], f);
 #pragma unroll
     for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(f[i]));
   }
@@ -156,7 +136,7 @@ __global__ __launch_bounds__(256) void moe_permute_quant_vec_kernel(const void *
   int8_t *dst = routed + static_cast<int64_t>(r) * h;
   for (int64_t c = tid; c < nch; c += 256) {
     float f[N];
-    chunk_to_f32<DT>(src[c], f);
+    mp_chunk_to_f32<DT>(src[c], f);
     uint32_t w[N / 4];
 #pragma unroll
     for (int i = 0; i < N / 4; ++i)

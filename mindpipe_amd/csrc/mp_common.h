@@ -59,6 +59,26 @@ __device__ __forceinline__ void mp_store_from_f32(void *p, int64_t i, int dtype,
   else static_cast<float *>(p)[i] = v;
 }
 
+// 16 bytes of a row as floats: 8 values of a 16-bit dtype or 4 of fp32
+template <int DT>
+struct MpChunk16 {
+  static constexpr int N = DT == MP_F32 ? 4 : 8;
+};
+template <int DT>
+__device__ __forceinline__ void mp_chunk_to_f32(const uint4 v, float (&f)[MpChunk16<DT>::N]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  if constexpr (DT == MP_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(w[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = static_cast<uint16_t>(w[i] & 0xFFFFu), hi = static_cast<uint16_t>(w[i] >> 16);
+      f[2 * i] = DT == MP_F16 ? mp_h2f(lo) : mp_bf2f(lo);
+      f[2 * i + 1] = DT == MP_F16 ? mp_h2f(hi) : mp_bf2f(hi);
+    }
+  }
+}
 // SwiGLU of fp16 values g, u (given as floats): round(round(silu(g)) * u), the
 // rounding of PyTorch's half ops (silu in fp32, rounded; the product rounded).
 __device__ __forceinline__ uint16_t mp_swiglu_h(float g, float u) {

@@ -61,6 +61,78 @@ __global__ __launch_bounds__(256) void rowquant_kernel(const void *__restrict__ 
   }
 }
 
+// The same quantizer with 16-byte loads and 4- or 8-byte code stores (k a multiple of the
+// values per 16 bytes, 16-byte aligned rows); the per-element arithmetic is the same.
+template <int RULE, int DT>
+__global__ __launch_bounds__(256) void rowquant_vec_kernel(const void *__restrict__ x, int64_t k,
+                                                           int8_t *__restrict__ q, float *__restrict__ s_f32,
+                                                           uint16_t *__restrict__ s_src, int s_src_bf16,
+                                                           float min_scale, int32_t *__restrict__ bad) {
+  constexpr int N = MpChunk16<DT>::N, ESZ = DT == MP_F32 ? 4 : 2;
+  __shared__ float wmax[4];
+  __shared__ int wbad[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t nch = k / N;
+  const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const char *>(x) + row * k * ESZ);
+  float amax = 0.f;
+  int nonfinite = 0;
+  for (int64_t c = tid; c < nch; c += 256) {
+    float f[N];
+    mp_chunk_to_f32<DT>(src[c], f);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      nonfinite |= !isfinite(f[i]);
+      amax = fmaxf(amax, fabsf(f[i]));
+    }
+  }
+  amax = mp_wave_max(amax);
+  const int wb = __any(nonfinite);
+  if ((tid & 63) == 0) {
+    wmax[tid >> 6] = amax;
+    wbad[tid >> 6] = wb;
+  }
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const int row_bad = wbad[0] | wbad[1] | wbad[2] | wbad[3];
+  float s;
+  if (RULE == MP_SCALE_FP32) {
+    s = amax / 127.0f;
+    if (s < min_scale) s = min_scale;
+  } else {
+    float a = mp_rh(amax);
+    if (a < 1e-5f) a = mp_rh(1e-5f);
+    s = mp_rh(a / 127.0f);
+  }
+  if (tid == 0) {
+    if (s_f32) s_f32[row] = s;
+    if (s_src) s_src[row] = s_src_bf16 ? mp_f2bf(s) : mp_f2h(s);
+    if (bad && row_bad) atomicAdd(bad, 1);
+  }
+  int8_t *dst = q + row * k;
+  for (int64_t c = tid; c < nch; c += 256) {
+    float f[N];
+    mp_chunk_to_f32<DT>(src[c], f);
+    uint32_t w[N / 4];
+#pragma unroll
+    for (int g = 0; g < N / 4; ++g) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = f[4 * g + e];
+        float r;
+        if (RULE == MP_SCALE_FP32) r = (s == 0.f) ? 0.f : rintf(v / s);
+        else r = rintf(mp_rh(v / s));
+        r = fminf(fmaxf(r, -127.f), 127.f);
+        word |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xFFu) << (8 * e);
+      }
+      w[g] = word;
+    }
+    if constexpr (N == 8) *reinterpret_cast<uint2 *>(dst + c * 8) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t *>(dst + c * 4) = w[0];
+  }
+}
+
 // ------------------------------------------------------------------ decode GEMV (M <= 64)
 // One workgroup of NW waves per 16 output columns; each wave takes a contiguous
 // range of 64-byte K blocks, and the waves are summed exactly (int32) through LDS.  The int8
@@ -1877,6 +1949,28 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
 
 // ====================================================================== C ABI
 
+// Row quantizer launch: the 16-byte kernel when the rows allow it, else the scalar one.
+template <int RULE>
+static void mp_launch_rowquant(const void *x, int x_dtype, int64_t rows, int64_t k, int8_t *q, float *s_f32,
+                               uint16_t *s_src, int s_src_bf16, float min_scale, int32_t *bad, hipStream_t s) {
+  const int per16 = x_dtype == MP_F32 ? 4 : 8;
+  const dim3 g(static_cast<unsigned>(rows));
+  if (k % per16 == 0 && mp_aligned(x, 16) && mp_aligned(q, 8)) {
+    if (x_dtype == MP_F16)
+      hipLaunchKernelGGL((rowquant_vec_kernel<RULE, MP_F16>), g, dim3(256), 0, s, x, k, q, s_f32, s_src, s_src_bf16,
+                         min_scale, bad);
+    else if (x_dtype == MP_BF16)
+      hipLaunchKernelGGL((rowquant_vec_kernel<RULE, MP_BF16>), g, dim3(256), 0, s, x, k, q, s_f32, s_src, s_src_bf16,
+                         min_scale, bad);
+    else
+      hipLaunchKernelGGL((rowquant_vec_kernel<RULE, MP_F32>), g, dim3(256), 0, s, x, k, q, s_f32, s_src, s_src_bf16,
+                         min_scale, bad);
+  } else {
+    hipLaunchKernelGGL(rowquant_kernel<RULE>, g, dim3(256), 0, s, x, x_dtype, k, q, s_f32, s_src, s_src_bf16,
+                       min_scale, bad);
+  }
+}
+
 extern "C" int mp_quant_per_token_i8(const void *x, int64_t m, int64_t k, int x_dtype, int8_t *q,
                                      void *scale, int scale_rule, mp_stream_t stream) {
   if (!x || !q || !scale) return MP_ERR_ARG;
@@ -1886,12 +1980,10 @@ extern "C" int mp_quant_per_token_i8(const void *x, int64_t m, int64_t k, int x_
   if (m > INT32_MAX) return MP_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (scale_rule == MP_SCALE_FP32) {
-    hipLaunchKernelGGL(rowquant_kernel<MP_SCALE_FP32>, dim3(static_cast<unsigned>(m)), dim3(256), 0, s, x, x_dtype,
-                       k, q, static_cast<float *>(scale), nullptr, 0, 0.0f, nullptr);
+    mp_launch_rowquant<MP_SCALE_FP32>(x, x_dtype, m, k, q, static_cast<float *>(scale), nullptr, 0, 0.0f, nullptr, s);
   } else if (scale_rule == MP_SCALE_FP16) {
     if (x_dtype != MP_F16) return MP_ERR_DTYPE;
-    hipLaunchKernelGGL(rowquant_kernel<MP_SCALE_FP16>, dim3(static_cast<unsigned>(m)), dim3(256), 0, s, x, x_dtype,
-                       k, q, nullptr, static_cast<uint16_t *>(scale), 0, 0.0f, nullptr);
+    mp_launch_rowquant<MP_SCALE_FP16>(x, x_dtype, m, k, q, nullptr, static_cast<uint16_t *>(scale), 0, 0.0f, nullptr, s);
   } else {
     return MP_ERR_ARG;
   }
@@ -1909,13 +2001,12 @@ extern "C" int mp_w8_quantize_per_channel(const void *w, int64_t n, int64_t k, i
   if (n > INT32_MAX) return MP_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (scale_rule == MP_SCALE_FP32) {
-    hipLaunchKernelGGL(rowquant_kernel<MP_SCALE_FP32>, dim3(static_cast<unsigned>(n)), dim3(256), 0, s, w, w_dtype,
-                       k, q, scale_f32, static_cast<uint16_t *>(scale_src), w_dtype == MP_BF16 ? 1 : 0, 1e-8f,
-                       bad_count);
+    mp_launch_rowquant<MP_SCALE_FP32>(w, w_dtype, n, k, q, scale_f32, static_cast<uint16_t *>(scale_src),
+                                      w_dtype == MP_BF16 ? 1 : 0, 1e-8f, bad_count, s);
   } else if (scale_rule == MP_SCALE_FP16) {
     if (w_dtype != MP_F16) return MP_ERR_DTYPE;
-    hipLaunchKernelGGL(rowquant_kernel<MP_SCALE_FP16>, dim3(static_cast<unsigned>(n)), dim3(256), 0, s, w, w_dtype,
-                       k, q, scale_f32, static_cast<uint16_t *>(scale_src), 0, 0.0f, bad_count);
+    mp_launch_rowquant<MP_SCALE_FP16>(w, w_dtype, n, k, q, scale_f32, static_cast<uint16_t *>(scale_src), 0, 0.0f,
+                                      bad_count, s);
   } else {
     return MP_ERR_ARG;
   }

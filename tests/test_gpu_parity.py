@@ -194,14 +194,16 @@ def test_w4a16_empty_batch():
 
 
 # ------------------------------------------------------------------ W8 quantizers
+# k: 16-byte kernel (k a multiple of the values per 16 bytes), scalar kernel (4099), a short row
+@pytest.mark.parametrize("k", [4096, 4099, 24])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
-def test_per_token_quant_fp32_rule_bitexact(dtype):
-    _say("per_token fp32 rule", dtype)
+def test_per_token_quant_fp32_rule_bitexact(dtype, k):
+    _say("per_token fp32 rule", dtype, k)
     g = torch.Generator().manual_seed(0)
-    x = torch.randn(67, 4096, generator=g)
-    x[:, torch.randperm(4096, generator=g)[:41]] *= 20
+    x = torch.randn(67, k, generator=g)
+    x[:, torch.randperm(k, generator=g)[:41]] *= 20
     x[5] = 0.0
-    x[6] = (torch.arange(4096) - 2048) * 0.5
+    x[6] = (torch.arange(k) - k // 2) * 0.5
     tdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dtype]
     xt = x.to(tdt)
     q, s = _ops().quant_per_token_i8(xt.to(DEV))
