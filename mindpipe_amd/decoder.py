@@ -14,7 +14,7 @@ The KV cache has a fixed capacity ``[L, B, kvh, T, 128]`` and every kernel reads
 the current position from device memory, so a step is shape-static and can be
 captured into a HIP graph.  ``decode_step_torch`` is the same step in PyTorch ops
 (masked attention over the whole cache), kept as the numerical reference.  Prefill
-uses PyTorch attention (SDPA) around the same W4A16 linears.
+uses PyTorch attention (SDPA) around the same W4A16 linears and fused norm / SiLU-mul kernels.
 """
 from __future__ import annotations
 
@@ -120,8 +120,43 @@ class W4Decoder:
         return out
 
     @torch.no_grad()
-    def prefill(self, tokens):
-        """tokens [B, T] int64; fills the cache at positions [0, T); returns next-token ids [B]."""
+    def prefill(self, tokens, return_logits=False):
+        """tokens [B, T] int64; fills the cache at positions [0, T); returns next-token ids [B]
+        (or the last position's logits).  The residual adds, RMSNorms and SiLU-mul run on the
+        fused kernels (one launch each); attention is PyTorch SDPA."""
+        cfg = self.cfg
+        b, t = tokens.shape
+        hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
+        x = self.embed[tokens].reshape(b * t, -1)                  # [B*T, H] residual stream
+        pos = torch.arange(t, device=tokens.device)
+        delta = None
+        for li, l in enumerate(self.layers):
+            if delta is None:
+                hn = ops.add_rms_norm_quant(x, None, l["ln1"], cfg.eps, quant=False)[0]
+            else:
+                hn, _, _, x = ops.add_rms_norm_quant(delta, x, l["ln1"], cfg.eps, quant=False)
+            qkv = l["qkv"](hn).reshape(b, t, nh + 2 * kvh, hd).transpose(1, 2)
+            q, k, v = qkv[:, :nh], qkv[:, nh:nh + kvh], qkv[:, nh + kvh:]
+            q, k = self._rope(q, pos), self._rope(k, pos)
+            self.k_cache[li, :b, :, :t] = k
+            self.v_cache[li, :b, :, :t] = v
+            kk = k.repeat_interleave(nh // kvh, dim=1) if kvh != nh else k
+            vv = v.repeat_interleave(nh // kvh, dim=1) if kvh != nh else v
+            att = torch.nn.functional.scaled_dot_product_attention(q.contiguous(), kk.contiguous(), vv.contiguous(),
+                                                                   is_causal=True)
+            o = l["o"](att.transpose(1, 2).reshape(b * t, nh * hd))
+            hn, _, _, x = ops.add_rms_norm_quant(o, x, l["ln2"], cfg.eps, quant=False)
+            delta = l["down"](ops.silu_mul(l["gate_up"](hn)))
+        # the last position of each sequence only
+        d_last = delta.reshape(b, t, -1)[:, -1].contiguous()
+        x_last = x.reshape(b, t, -1)[:, -1].contiguous()
+        hn = ops.add_rms_norm_quant(d_last, x_last, self.norm, cfg.eps, quant=False)[0]
+        logits = self.lm_head(hn)
+        return logits if return_logits else logits.argmax(-1)
+
+    @torch.no_grad()
+    def prefill_torch(self, tokens, return_logits=False):
+        """The prefill in PyTorch ops around the same W4A16 linears (reference path)."""
         cfg = self.cfg
         b, t = tokens.shape
         hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
@@ -136,15 +171,15 @@ class W4Decoder:
             self.v_cache[li, :b, :, :t] = v
             kk = k.repeat_interleave(nh // kvh, dim=1) if kvh != nh else k
             vv = v.repeat_interleave(nh // kvh, dim=1) if kvh != nh else v
-            att = torch.nn.functional.scaled_dot_product_attention(q.contiguous(), kk.contiguous(), vv.contiguous(),
-                                                                   is_causal=True)
+            att = torch.nn.functional.scaled_dot_product_attention(q.float(), kk.float(), vv.float(),
+                                                                   is_causal=True).half()
             x = x + l["o"](att.transpose(1, 2).reshape(b * t, nh * hd)).reshape(b, t, -1)
             hn = _rms(x, l["ln2"], cfg.eps)
             gu = l["gate_up"](hn.reshape(b * t, -1))
             act = torch.nn.functional.silu(gu[:, :cfg.ffn]) * gu[:, cfg.ffn:]
             x = x + l["down"](act.contiguous()).reshape(b, t, -1)
         logits = self.lm_head(_rms(x[:, -1], self.norm, cfg.eps).contiguous())
-        return logits.argmax(-1)
+        return logits if return_logits else logits.argmax(-1)
 
     def attn_splits(self, b):
         """Workgroups per (row, kv head) for the decode attention: ~1024 in all, and a score

@@ -163,6 +163,21 @@ def test_silu_mul_within_one_ulp():
 
 
 @pytest.mark.parametrize("heads,kv_heads", [(2, 2), (4, 1)])
+def test_decoder_prefill_matches_torch_prefill(heads, kv_heads):
+    _say("decoder prefill", heads, kv_heads)
+    from mindpipe_amd.decoder import DecoderConfig, W4Decoder
+    cfg = DecoderConfig(layers=2, hidden=heads * 128, heads=heads, kv_heads=kv_heads, ffn=512, vocab=512)
+    model = W4Decoder(cfg, max_batch=2, max_len=96, device=DEV, seed=5)
+    toks = torch.randint(0, cfg.vocab, (2, 70), device=DEV, generator=torch.Generator(device=DEV).manual_seed(6))
+    lk = model.prefill(toks, return_logits=True)
+    kc, vc = model.k_cache.clone(), model.v_cache.clone()
+    lt = model.prefill_torch(toks, return_logits=True)
+    # fused kernels vs PyTorch ops (fp32 attention in the reference): same math, other roundings
+    assert _rel(lk.float(), lt.float()) <= 2e-2
+    assert _rel(kc.float(), model.k_cache.float()) <= 1e-2 and _rel(vc.float(), model.v_cache.float()) <= 1e-2
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(2, 2), (4, 1)])
 def test_decoder_kernel_step_matches_torch_step(heads, kv_heads):
     _say("decoder step", heads, kv_heads)
     from mindpipe_amd.decoder import DecoderConfig, W4Decoder
