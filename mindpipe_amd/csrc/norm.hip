@@ -42,19 +42,20 @@ __device__ __forceinline__ float nq_wave_sum(float v) {
   return v;
 }
 
-// workgroup sum / max of one value per thread, fixed order over the 4 waves
+// workgroup sum / max of one value per thread, fixed order over the 4 waves (LDS-only
+// barriers: the stores already issued need not complete first)
 __device__ __forceinline__ float nq_block_sum(float v, float *red) {
   v = nq_wave_sum(v);
-  __syncthreads();
+  mp_lds_barrier();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  mp_lds_barrier();
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 __device__ __forceinline__ float nq_block_max(float v, float *red) {
   v = mp_wave_max(v);
-  __syncthreads();
+  mp_lds_barrier();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  mp_lds_barrier();
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
@@ -74,6 +75,14 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
   const int64_t base = static_cast<int64_t>(blockIdx.x) * h;
   float v[V][8];
   float ss = 0.f;
+  // the norm weights are loaded with the row: a load after the residual stores would wait
+  // for them
+  uint4 wv[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = (tid + 256 * i) * 8;
+    wv[i] = *reinterpret_cast<const uint4 *>(w + (c < h ? c : 0));
+  }
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int c = (tid + 256 * i) * 8;
@@ -114,8 +123,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
   for (int i = 0; i < V; ++i) {
     const int c = (tid + 256 * i) * 8;
     const bool ok = c < h;
-    const uint4 wv = *reinterpret_cast<const uint4 *>(w + (ok ? c : 0));
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float we = nq_ld<BF16>(static_cast<uint16_t>(ww[e >> 1] >> (16 * (e & 1))));
