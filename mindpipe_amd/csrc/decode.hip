@@ -54,17 +54,14 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
 }
 
 // ---------------------------------------------------------------- decode attention
-// Interleaved-pair RoPE of 8 consecutive dims (pairs 4 dl .. 4 dl + 3) at position
-// pos, rounding like PyTorch half ops (every product and the sum round to fp16).
-// cos_t / sin_t [T, 64] fp16; the rows are 8-byte aligned (host check).
-__device__ __forceinline__ void rope8(const uint4 xv, const uint16_t *__restrict__ cos_t,
-                                      const uint16_t *__restrict__ sin_t, int64_t pos, int dl, float (&o)[8]) {
+// Interleaved-pair RoPE of 8 consecutive dims (pairs 4 dl .. 4 dl + 3) given the
+// four cos / sin values of those pairs, rounding like PyTorch half ops (every product
+// and the sum round to fp16).
+__device__ __forceinline__ void rope8(const uint4 xv, const uint2 cv, const uint2 sv, float (&o)[8]) {
   // no contraction: the compiler narrows these to fp16 ops and would fuse a product
   // into the subtraction (v_fma_f16), skipping the product's own rounding
 #pragma clang fp contract(off)
   const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-  const uint2 cv = *reinterpret_cast<const uint2 *>(cos_t + pos * (kHd / 2) + dl * 4);
-  const uint2 sv = *reinterpret_cast<const uint2 *>(sin_t + pos * (kHd / 2) + dl * 4);
   const uint32_t cw[2] = {cv.x, cv.y}, sw[2] = {sv.x, sv.y};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -76,28 +73,40 @@ __device__ __forceinline__ void rope8(const uint4 xv, const uint16_t *__restrict
   }
 }
 
+__device__ __forceinline__ void h8_to_f32(const uint4 v, float (&f)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = mp_h2f(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1))));
+}
+
 // Grid (splits, B * kvh), 256 threads.  A workgroup scores positions
 // [s*chunk, min((s+1)*chunk, len)) for the GRP query heads of one kv head:
 // 16 lanes per position (8 dims each, one 16-byte load), 4 positions per wave
-// per step, fp32 dot products reduced over the 16 lanes.  Scores go to LDS,
-// softmax statistics are taken over the workgroup, then P.V accumulates in
-// fp32 with the same lane layout; the first V step is loaded before the
-// softmax, so its latency overlaps it.
+// per step of 16, U steps per load round, fp32 dot products reduced over the 16
+// lanes.  Scores go to LDS, softmax statistics are taken over the workgroup,
+// then P.V accumulates in fp32 with the same lane layout.
+//
+// Memory round trips set the time of a short chunk, so the loads go out in this
+// order before any of them is waited for: the query slices (and, with ROPE, the
+// new key / value slices and their cos / sin), then the first K round, then the
+// first V round.  With U * 16 >= chunk the whole chunk is one round.
 //
 // ROPE: the queries come from the fused qkv row [B, (nh + 2 kvh) * 128] and are
-// rotated in registers; the workgroup whose split holds position pos (the last
-// used one) also rotates the new key and appends key and value to the cache
-// before it scores.  len = pos + 1; a position outside [0, cap) appends nothing
-// and yields zeros.  Otherwise q is [B, nh, 128] and len = clamp(pos + 1, 0, cap).
+// rotated in registers.  The workgroup whose split holds position pos (the last
+// used one) appends the rotated key and the value to the cache; its own use of
+// that position takes the rows from registers, so no load has to see the append.
+// len = pos + 1; a position outside [0, cap) appends nothing and yields zeros.
+// Otherwise q is [B, nh, 128] and len = clamp(pos + 1, 0, cap).
 //
 // With one split the workgroup normalises and stores the output; otherwise it
 // stores its unnormalised partial o, max m and sum l for attn_merge_kernel.
-template <int GRP, bool ROPE>
+template <int GRP, bool ROPE, int U>
 __global__ __launch_bounds__(256) void decode_attn_kernel(
     const uint16_t *__restrict__ qsrc, const uint16_t *__restrict__ cos_t, const uint16_t *__restrict__ sin_t,
     uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache, const int64_t *__restrict__ pos_p, int kvh,
     int cap, int chunk, int splits, float scale, float *__restrict__ part_o, float *__restrict__ part_ml,
     uint16_t *__restrict__ out) {
+  constexpr uint32_t kOob = 0x80000000u;  // past the cache descriptors (host: cap * 256 < 2^31)
   extern __shared__ float sm[];  // [GRP][chunk] scores, then the [GRP][4][128] reduction
   __shared__ float red[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -127,59 +136,74 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
   const int pl = lane >> 4;  // position within the wave's group of 4
   const uint16_t *kbase = k_cache + static_cast<int64_t>(bk) * cap * kHd + dl * 8;
   const uint16_t *vbase = v_cache + static_cast<int64_t>(bk) * cap * kHd + dl * 8;
+  // the appending workgroup: its last position (n - 1) is the new token's
+  const bool app = ROPE && s == used - 1;
+  auto tpos = [&](int base, int u) { return base + u * 16 + wave * 4 + pl; };  // unclamped
 
-  // query slices (fp32) of the GRP heads
-  float qf[GRP][8];
+  // ---- loads: query (+ new key / value) slices, then the first K and V rounds
+  uint4 qv[GRP], knv, vnv;
+  uint2 cv, sv;
   if (ROPE) {
-    const uint16_t *row = qsrc + static_cast<int64_t>(b) * (nh + 2 * kvh) * kHd;
+    const uint16_t *row = qsrc + static_cast<int64_t>(b) * (nh + 2 * kvh) * kHd + dl * 8;
 #pragma unroll
-    for (int g = 0; g < GRP; ++g)
-      rope8(*reinterpret_cast<const uint4 *>(row + (kh * GRP + g) * kHd + dl * 8), cos_t, sin_t, pos, dl, qf[g]);
-    if (s == used - 1 && tid < 32) {  // append: lanes 0-15 the rotated key, 16-31 the value
-      const int64_t crow = (static_cast<int64_t>(bk) * cap + pos) * kHd + dl * 8;
-      if (tid < 16) {
-        float kr[8];
-        rope8(*reinterpret_cast<const uint4 *>(row + (nh + kh) * kHd + dl * 8), cos_t, sin_t, pos, dl, kr);
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          w[j] = static_cast<uint32_t>(mp_f2h(kr[2 * j])) | (static_cast<uint32_t>(mp_f2h(kr[2 * j + 1])) << 16);
-        *reinterpret_cast<uint4 *>(k_cache + crow) = make_uint4(w[0], w[1], w[2], w[3]);
-      } else {
-        *reinterpret_cast<uint4 *>(v_cache + crow) =
-            *reinterpret_cast<const uint4 *>(row + (nh + kvh + kh) * kHd + dl * 8);
-      }
-    }
-    __syncthreads();  // the appended row is visible to this workgroup's cache loads
+    for (int g = 0; g < GRP; ++g) qv[g] = *reinterpret_cast<const uint4 *>(row + (kh * GRP + g) * kHd);
+    knv = *reinterpret_cast<const uint4 *>(row + (nh + kh) * kHd);
+    vnv = *reinterpret_cast<const uint4 *>(row + (nh + kvh + kh) * kHd);
+    cv = *reinterpret_cast<const uint2 *>(cos_t + pos * (kHd / 2) + dl * 4);
+    sv = *reinterpret_cast<const uint2 *>(sin_t + pos * (kHd / 2) + dl * 4);
   } else {
 #pragma unroll
-    for (int g = 0; g < GRP; ++g) {
-      const uint4 qv =
-          *reinterpret_cast<const uint4 *>(qsrc + (static_cast<int64_t>(b) * nh + kh * GRP + g) * kHd + dl * 8);
-      const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[g][e] = mp_h2f(static_cast<uint16_t>(qw[e >> 1] >> (16 * (e & 1))));
-    }
+    for (int g = 0; g < GRP; ++g)
+      qv[g] = *reinterpret_cast<const uint4 *>(qsrc + (static_cast<int64_t>(b) * nh + kh * GRP + g) * kHd + dl * 8);
   }
-
-  // ---- scores: steps of 16 positions per workgroup, 4 steps in flight
-  float *sc = sm;
-  constexpr int U = 4;
-  for (int base = 0; base < n; base += 16 * U) {
-    uint4 kv[U];
+  auto load_round = [&](uint4 (&r)[U], const uint16_t *base_p, int base) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      int t = base + u * 16 + wave * 4 + pl;
-      t = t < n ? t : n - 1;
-      kv[u] = *reinterpret_cast<const uint4 *>(kbase + static_cast<int64_t>(t0 + t) * kHd);
+      const int t = min(tpos(base, u), n - 1);
+      r[u] = *reinterpret_cast<const uint4 *>(base_p + static_cast<int64_t>(t0 + t) * kHd);
     }
+  };
+  uint4 kv[U], vv[U];
+  load_round(kv, kbase, 0);
+  load_round(vv, vbase, 0);
+
+  // ---- queries to fp32; with ROPE rotate, and append the new row (lanes 0-15 the key,
+  // 16-31 the value of the appending workgroup; every other store is dropped)
+  float qf[GRP][8];
+  uint4 knew = make_uint4(0, 0, 0, 0);
+  if (ROPE) {
+#pragma unroll
+    for (int g = 0; g < GRP; ++g) rope8(qv[g], cv, sv, qf[g]);
+    float kr[8];
+    rope8(knv, cv, sv, kr);
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = static_cast<uint32_t>(mp_f2h(kr[2 * j])) | (static_cast<uint32_t>(mp_f2h(kr[2 * j + 1])) << 16);
+    knew = make_uint4(w[0], w[1], w[2], w[3]);
+    const uint32_t cbytes = static_cast<uint32_t>(cap) * kHd * 2;
+    const uint32_t roff = (static_cast<uint32_t>(pos) * kHd + dl * 8) * 2;
+    mp_buf_store16(mp_rsrc(k_cache + static_cast<int64_t>(bk) * cap * kHd, cbytes), app && tid < 16 ? roff : kOob,
+                   knew);
+    mp_buf_store16(mp_rsrc(v_cache + static_cast<int64_t>(bk) * cap * kHd, cbytes),
+                   app && tid >= 16 && tid < 32 ? roff : kOob, vnv);
+  } else {
+#pragma unroll
+    for (int g = 0; g < GRP; ++g) h8_to_f32(qv[g], qf[g]);
+  }
+  // the row a lane uses for (clamped) position t: the new token's from registers
+  auto pick = [&](const uint4 cached, const uint4 fresh, int t) {
+    return (app && min(t, n - 1) == n - 1) ? fresh : cached;
+  };
+
+  // ---- scores
+  float *sc = sm;
+  auto score_round = [&](const uint4 (&r)[U], int base) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int t = base + u * 16 + wave * 4 + pl;
-      const uint32_t kw[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
+      const int t = tpos(base, u);
       float kf[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kf[e] = mp_h2f(static_cast<uint16_t>(kw[e >> 1] >> (16 * (e & 1))));
+      h8_to_f32(ROPE ? pick(r[u], knew, t) : r[u], kf);
 #pragma unroll
       for (int g = 0; g < GRP; ++g) {
         float d = 0.f;
@@ -192,14 +216,12 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
         if (dl == 0 && t < n) sc[g * chunk + t] = d * scale;
       }
     }
-  }
-  // first V step, in flight across the softmax (its barriers wait for LDS only)
-  uint4 vv[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    int t = u * 16 + wave * 4 + pl;
-    t = t < n ? t : n - 1;
-    vv[u] = *reinterpret_cast<const uint4 *>(vbase + static_cast<int64_t>(t0 + t) * kHd);
+  };
+  score_round(kv, 0);
+  for (int base = 16 * U; base < n; base += 16 * U) {
+    uint4 k2[U];
+    load_round(k2, kbase, base);
+    score_round(k2, base);
   }
   mp_lds_barrier();
 
@@ -236,22 +258,12 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
   for (int g = 0; g < GRP; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-  for (int base = 0; base < n; base += 16 * U) {
-    if (base > 0) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        int t = base + u * 16 + wave * 4 + pl;
-        t = t < n ? t : n - 1;
-        vv[u] = *reinterpret_cast<const uint4 *>(vbase + static_cast<int64_t>(t0 + t) * kHd);
-      }
-    }
+  auto pv_round = [&](const uint4 (&r)[U], int base) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int t = base + u * 16 + wave * 4 + pl;
-      const uint32_t vw[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
+      const int t = tpos(base, u);
       float vf[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vf[e] = mp_h2f(static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1))));
+      h8_to_f32(ROPE ? pick(r[u], vnv, t) : r[u], vf);
 #pragma unroll
       for (int g = 0; g < GRP; ++g) {
         const float p = t < n ? sc[g * chunk + t] : 0.f;
@@ -259,6 +271,12 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
         for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
       }
     }
+  };
+  pv_round(vv, 0);
+  for (int base = 16 * U; base < n; base += 16 * U) {
+    uint4 v2[U];
+    load_round(v2, vbase, base);
+    pv_round(v2, base);
   }
   // reduce over the 4 positions of a wave (lanes l, l^16, l^32, l^48), then over the waves
 #pragma unroll
@@ -302,8 +320,11 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
 // Merge of the used splits, one wave per (row, head), four heads per workgroup:
 // lanes take the splits' (m, l) pairs for the max and the weights
 // w_j = exp(m_j - max m), then each lane owns two dims and sums w_j o_j over the
-// splits with eight loads in flight.  Sums run in a fixed order, so the result
-// does not depend on timing.  An empty range (len 0) gives zeros.
+// splits.  The partial outputs of the first kMergeRound splits are loaded right
+// after the (m, l) pairs, before the weights are computed, so one memory round trip
+// covers them.  Sums run in a fixed order (ascending j), so the result does not
+// depend on timing.  An empty range (len 0) gives zeros.
+constexpr int kMergeRound = 32;
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part_o,
                                                          const float *__restrict__ part_ml,
                                                          const int64_t *__restrict__ pos_p, int cap, int chunk,
@@ -328,11 +349,22 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     return;
   }
   const float *ml = part_ml + head * splits * 2;
-  float m = -INFINITY;
-  for (int j = lane; j < used; j += 64) m = fmaxf(m, ml[2 * j]);
+  const float2 *po = reinterpret_cast<const float2 *>(part_o + head * splits * kHd) + lane;
+  // (m, l) of split lane (clamped into the used ones), then the first round of partials
+  const float2 ml0 = reinterpret_cast<const float2 *>(ml)[min(lane, used - 1)];
+  float2 v[kMergeRound];
+#pragma unroll
+  for (int u = 0; u < kMergeRound; ++u) v[u] = po[min(u, used - 1) * (kHd / 2)];
+  float m = lane < used ? ml0.x : -INFINITY;
+  for (int j = lane + 64; j < used; j += 64) m = fmaxf(m, ml[2 * j]);
   m = mp_wave_max(m);
   float den = 0.f;
-  for (int j = lane; j < used; j += 64) {
+  if (lane < used) {
+    const float w = expf(ml0.x - m);
+    wts[wave][lane] = w;
+    den = w * ml0.y;  // fmaf(w, l, 0)
+  }
+  for (int j = lane + 64; j < used; j += 64) {
     const float w = expf(ml[2 * j] - m);
     wts[wave][j] = w;
     den = fmaf(w, ml[2 * j + 1], den);
@@ -341,23 +373,28 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
   for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  const float2 *po = reinterpret_cast<const float2 *>(part_o + head * splits * kHd) + lane;
   float n0 = 0.f, n1 = 0.f;
-  int j = 0;
-  for (; j + 8 <= used; j += 8) {
-    float2 v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = po[(j + u) * (kHd / 2)];
+  for (int u = 0; u < kMergeRound; ++u)
+    if (u < used) {
+      n0 = fmaf(wts[wave][u], v[u].x, n0);
+      n1 = fmaf(wts[wave][u], v[u].y, n1);
+    }
+  int j = kMergeRound;
+  for (; j + 8 <= used; j += 8) {
+    float2 w8[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) w8[u] = po[(j + u) * (kHd / 2)];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      n0 = fmaf(wts[wave][j + u], v[u].x, n0);
-      n1 = fmaf(wts[wave][j + u], v[u].y, n1);
+      n0 = fmaf(wts[wave][j + u], w8[u].x, n0);
+      n1 = fmaf(wts[wave][j + u], w8[u].y, n1);
     }
   }
   for (; j < used; ++j) {
-    const float2 v = po[j * (kHd / 2)];
-    n0 = fmaf(wts[wave][j], v.x, n0);
-    n1 = fmaf(wts[wave][j], v.y, n1);
+    const float2 w1 = po[j * (kHd / 2)];
+    n0 = fmaf(wts[wave][j], w1.x, n0);
+    n1 = fmaf(wts[wave][j], w1.y, n1);
   }
   *o2 = static_cast<uint32_t>(mp_f2h(n0 / den)) | (static_cast<uint32_t>(mp_f2h(n1 / den)) << 16);
 }
@@ -409,6 +446,8 @@ int launch_decode_attention(bool rope, const void *qsrc, int64_t batch, int nh, 
   if (!qsrc || !k_cache || !v_cache || !pos || !out || !workspace) return MP_ERR_ARG;
   if (rope && (!cos_t || !sin_t)) return MP_ERR_ARG;
   if (head_dim != kHd) return MP_ERR_SHAPE;
+  // the fused append stores through a descriptor over one (row, kv head) cache slice
+  if (rope && capacity * kHd * 2 >= (int64_t(1) << 31)) return MP_ERR_SHAPE;
   if (batch <= 0 || nh <= 0 || kvh <= 0 || nh % kvh != 0 || capacity <= 0 || capacity > INT32_MAX) return MP_ERR_SHAPE;
   const int grp = nh / kvh;
   if (grp != 1 && grp != 2 && grp != 4 && grp != 8) return MP_ERR_SHAPE;
@@ -432,9 +471,17 @@ int launch_decode_attention(bool rope, const void *qsrc, int64_t batch, int nh, 
   auto *vp = static_cast<uint16_t *>(v_cache);
   auto *op = static_cast<uint16_t *>(out);
   const int cap = static_cast<int>(capacity);
-#define MP_ATTN_LAUNCH(G, R)                                                                                  \
-  hipLaunchKernelGGL((decode_attn_kernel<G, R>), grid, dim3(256), lds, s, qp, cp, sp, kp, vp, pos, kvh, cap, \
-                     chunk, splits, scale, part_o, part_ml, op)
+  // one load round covers a chunk of up to 80 positions (five steps of 16)
+  const bool u5 = chunk <= 80;
+#define MP_ATTN_LAUNCH(G, R)                                                                                   \
+  do {                                                                                                         \
+    if (u5)                                                                                                    \
+      hipLaunchKernelGGL((decode_attn_kernel<G, R, 5>), grid, dim3(256), lds, s, qp, cp, sp, kp, vp, pos, kvh, \
+                         cap, chunk, splits, scale, part_o, part_ml, op);                                      \
+    else                                                                                                       \
+      hipLaunchKernelGGL((decode_attn_kernel<G, R, 4>), grid, dim3(256), lds, s, qp, cp, sp, kp, vp, pos, kvh, \
+                         cap, chunk, splits, scale, part_o, part_ml, op);                                      \
+  } while (0)
   if (rope) {
     switch (grp) {
       case 1: MP_ATTN_LAUNCH(1, true); break;

@@ -138,6 +138,11 @@ __device__ __forceinline__ i4_t mp_buf_load16i(__amdgpu_buffer_rsrc_t r, uint32_
 }
 // Vector stores through a buffer descriptor: offsets at or past its size are dropped,
 // so guarded stores need no branch.
+__device__ __forceinline__ void mp_buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint4 v) {
+  typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+  const u4v w = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, static_cast<int>(voff), 0, 0);
+}
 __device__ __forceinline__ void mp_buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t v) {
   __builtin_amdgcn_raw_buffer_store_b32(v, r, static_cast<int>(voff), 0, 0);
 }
