@@ -109,6 +109,18 @@ int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const int32_t *w_p
                          const void *scales, const void *zeros, int group_size, const void *bias, void *act,
                          int x_dtype, mp_stream_t stream);
 
+/* One activation row x [K] (fp16): y = RMSNorm(x + residual) * norm_weight . dequant(W)^T
+ * (+ bias), or with swiglu != 0 the SiLU-up product of the fused gate/up weight [N = 2I, K]
+ * (y [I]); residual_out = round(x + residual) (optional; residual may be NULL).  No
+ * counterpart in the reference: the fusion of mp_add_rms_norm_quant (quant off) with
+ * mp_w4a16_gemm / mp_w4a16_gemm_swiglu at M = 1 for a decode step, bit-identical to
+ * that two-launch chain.  K in {2048, 4096, 8192}, group 128; residual_out must not
+ * overlap x or residual. */
+int mp_w4a16_gemv_rmsnorm(const void *x, const void *residual, const void *norm_weight, float eps,
+                          void *residual_out, int64_t k, const int32_t *w_packed, int64_t n, const void *scales,
+                          const void *zeros, int group_size, const void *bias, int swiglu, void *y, int x_dtype,
+                          mp_stream_t stream);
+
 /* ---------------------------------------------------------------- W8A8 (SmoothQuant) */
 
 /* Per-token dynamic symmetric int8 quant of x [M,K] (fp16/bf16/fp32).

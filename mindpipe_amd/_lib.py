@@ -26,6 +26,8 @@ SIGNATURES = {
     "mp_unpack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "mp_w4a16_gemm": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp]),
     "mp_w4a16_gemm_swiglu": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp]),
+    "mp_w4a16_gemv_rmsnorm": (_i32, [_vp, _vp, _vp, C.c_float, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _i32,
+                                     _vp, _i32, _vp]),
     "mp_quant_per_token_i8": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _i32, _vp]),
     "mp_add_rms_norm_quant": (_i32, [_vp, _vp, _vp, C.c_float, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp]),
     "mp_decode_rope_append": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),

@@ -896,11 +896,25 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ h2_t mp_as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 
-template <int R, int C, int S, bool ZP, bool SWI = false>
+// NRM: the activation row is h = RMSNorm(x + residual) * w, computed by every
+// workgroup in its prologue into LDS (the arithmetic of add_rmsnorm_quant_kernel
+// with fp16 rows: fp32 sum, residual_out = round(sum), r = 1 / sqrt(mean(sum^2) +
+// eps), h = round(round(sum * r) * w)); workgroup 0 writes residual_out.  One K
+// iteration per wave (k = 2048 C S): the row's loads go out first, then the
+// weights, so the norm runs while the weights stream in.
+struct MpRowNorm {
+  const uint16_t *x;    // row to normalise
+  const uint16_t *res;  // residual added to it (nullable)
+  const uint16_t *w;    // norm weight [k]
+  uint16_t *res_out;    // round(x + res) (nullable)
+  float eps;
+};
+
+template <int R, int C, int S, bool ZP, bool SWI = false, bool NRM = false>
 __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
     const uint16_t *__restrict__ x, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
-    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, const MpRowNorm nrm) {
   constexpr int SZN = R * 16 > 64 ? R * 16 / 64 : 1;  // scale / zero loads per chunk
   constexpr int LPR = 64 / R;                         // lanes per row after the butterfly
   constexpr int GPW = 4 / S;                          // row groups per workgroup (S waves split K)
@@ -913,7 +927,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
   const int sw = wave % S;
   const int n_out = SWI ? n_cols / 2 : n_cols;
   const int row0 = (blockIdx.x * GPW + wave / S) * RW;
-  if (S == 1 && row0 >= n_out) return;  // wave-uniform; with S == 1 there is no barrier
+  if (!NRM && S == 1 && row0 >= n_out) return;  // wave-uniform; with S == 1 there is no barrier
   const int kw = k >> 3;
   const int nch = (k + 2047) >> 11;
   uint32_t magic_v = kMagic, m0_v = 0x000F000Fu, m1_v = 0x00F000F0u;
@@ -959,6 +973,17 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
     for (int q = 0; q < 4; ++q) st.xv[q] = *reinterpret_cast<const uint4 *>(x + kp + 8 * q);
     int t = 8 * j + gpair;
     t = t < (n_groups >> 1) ? t : (n_groups >> 1) - 1;
+#pragma unroll
+    for (int i = 0; i < SZN; ++i) {
+      st.s[i] = srow[i][t];
+      st.z[i] = ZP ? zrow[i][t] : 0x48004800u;  // fp16 8.0
+    }
+  };
+  auto issue_w = [&](Stage &st, int j) {  // issue() without the activation loads
+    const int kp = j * 2048 + 32 * lane;
+#pragma unroll
+    for (int r = 0; r < R; ++r) st.w[r] = *reinterpret_cast<const uint4 *>(wrow[r] + (kp >> 3));
+    const int t = 8 * j + gpair;
 #pragma unroll
     for (int i = 0; i < SZN; ++i) {
       st.s[i] = srow[i][t];
@@ -1018,14 +1043,96 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
   // crosses an iteration, so every wait is a partial vmcnt and latency is
   // hidden by the other waves of the CU.
   Stage st[C];
-  for (int j = sw * C; j < nch; j += S * C) {
+  if constexpr (NRM) {
+    constexpr int NV = C * S;          // 2048-element slices of the row: k == 2048 NV (host check)
+    constexpr uint32_t kOob = 0x80000000u;
+    __shared__ uint4 xs[NV * 256];     // the normalised row, fp16
+    __shared__ float nred[4];
+    const int tid = threadIdx.x;
+    const uint32_t rb = static_cast<uint32_t>(k) * 2;
+    const auto xr = mp_rsrc(nrm.x, rb);
+    const auto rr = mp_rsrc(nrm.res ? nrm.res : nrm.x, nrm.res ? rb : 0);  // null: zeros, unused
+    const auto wr = mp_rsrc(nrm.w, rb);
+    // row loads first: their wait below leaves the weight loads in flight
+    uint4 pw[NV], pa[NV], pr[NV];
 #pragma unroll
-    for (int c = 0; c < C; ++c) issue(st[c], j + c < nch ? j + c : nch - 1);
+    for (int i = 0; i < NV; ++i) pw[i] = mp_buf_load16(wr, (tid + 256 * i) * 16, 0);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      pa[i] = mp_buf_load16(xr, (tid + 256 * i) * 16, 0);
+      pr[i] = mp_buf_load16(rr, (tid + 256 * i) * 16, 0);
+    }
+    const int j = sw * C;
+#pragma unroll
+    for (int c = 0; c < C; ++c) issue_w(st[c], j + c);
     __builtin_amdgcn_sched_barrier(0);
+    const bool has_res = nrm.res != nullptr;
+    float v[NV][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t aw[4] = {pa[i].x, pa[i].y, pa[i].z, pa[i].w}, bw[4] = {pr[i].x, pr[i].y, pr[i].z, pr[i].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float f = mp_h2f(static_cast<uint16_t>(aw[e >> 1] >> (16 * (e & 1))));
+        const float fb = mp_h2f(static_cast<uint16_t>(bw[e >> 1] >> (16 * (e & 1))));
+        f = has_res ? mp_add(f, fb) : f;
+        v[i][e] = f;
+        ss = mp_add(ss, mp_mul(f, f));
+      }
+    }
+    // residual_out from workgroup 0 (the other workgroups' stores are dropped)
+    const auto ro = mp_rsrc(nrm.res_out ? nrm.res_out : nrm.x, nrm.res_out ? rb : 0);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = static_cast<uint32_t>(mp_f2h(v[i][2 * e])) | (static_cast<uint32_t>(mp_f2h(v[i][2 * e + 1])) << 16);
+      mp_buf_store16(ro, blockIdx.x == 0 ? (tid + 256 * i) * 16 : kOob, make_uint4(o[0], o[1], o[2], o[3]));
+    }
+    // workgroup sum in the fixed order of the norm kernel: wave butterfly, then the 4 waves
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) nred[wave] = ss;
+    mp_lds_barrier();
+    const float var = ((nred[0] + nred[1]) + (nred[2] + nred[3])) / static_cast<float>(k);
+    const float rs = 1.0f / sqrtf(var + nrm.eps);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t ww[4] = {pw[i].x, pw[i].y, pw[i].z, pw[i].w};
+      uint32_t o[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float we = mp_h2f(static_cast<uint16_t>(ww[e >> 1] >> (16 * (e & 1))));
+        const float yn = mp_rh(mp_mul(v[i][e], rs));
+        o[e >> 1] |= static_cast<uint32_t>(mp_f2h(mp_mul(yn, we))) << (16 * (e & 1));
+      }
+      xs[tid + 256 * i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    mp_lds_barrier();
+    if (S == 1 && row0 >= n_out) return;  // wave-uniform, after the last barrier of S == 1
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int kp = (j + c) * 2048 + 32 * lane;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) st[c].xv[q] = xs[(kp >> 3) + q];
+    }
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       compute(st[c], j + c);
-      __builtin_amdgcn_sched_barrier(0);  // chunk c + 1's waits stay after chunk c's math
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    for (int j = sw * C; j < nch; j += S * C) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) issue(st[c], j + c < nch ? j + c : nch - 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        compute(st[c], j + c);
+        __builtin_amdgcn_sched_barrier(0);  // chunk c + 1's waits stay after chunk c's math
+      }
     }
   }
 
@@ -1168,6 +1275,65 @@ extern "C" int mp_unpack_int4(const int32_t *packed, int64_t n, int64_t k, int8_
   return MP_OK;
 }
 
+// One activation row through the norm-fused GEMV (see MpRowNorm): the fused
+// add-RMSNorm and the M = 1 GEMV (or gate/up GEMV with SiLU-up) in one launch, the
+// same bits as mp_add_rms_norm_quant (quant off) followed by mp_w4a16_gemm /
+// mp_w4a16_gemm_swiglu.  K in {2048, 4096, 8192}: the K split the GEMV uses at
+// that K, one iteration per wave.
+extern "C" int mp_w4a16_gemv_rmsnorm(const void *x, const void *residual, const void *norm_weight, float eps,
+                                     void *residual_out, int64_t k, const int32_t *w_packed, int64_t n,
+                                     const void *scales, const void *zeros, int group_size, const void *bias,
+                                     int swiglu, void *y, int x_dtype, mp_stream_t stream) {
+  if (x_dtype != MP_F16) return MP_ERR_DTYPE;
+  if (!x || !norm_weight || !w_packed || !scales || !y) return MP_ERR_ARG;
+  if (group_size != 128 || (k != 2048 && k != 4096 && k != 8192) || n <= 0 || n > INT32_MAX ||
+      (swiglu && (n & 1)))
+    return MP_ERR_SHAPE;
+  if (!mp_aligned(x, 16) || !mp_aligned(norm_weight, 16) || (residual && !mp_aligned(residual, 16)) ||
+      (residual_out && !mp_aligned(residual_out, 16)) || !mp_aligned(w_packed, 16) || !mp_aligned(scales, 4) ||
+      (zeros && !mp_aligned(zeros, 4)))
+    return MP_ERR_ALIGN;
+  // workgroup 0 writes residual_out while the others read x and residual: no overlap
+  auto overlaps = [&](const void *a, const void *b) {
+    const auto pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return a && b && pa < pb + static_cast<uintptr_t>(k) * 2 && pb < pa + static_cast<uintptr_t>(k) * 2;
+  };
+  if (overlaps(residual_out, x) || overlaps(residual_out, residual)) return MP_ERR_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const MpRowNorm nrm{static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(residual),
+                      static_cast<const uint16_t *>(norm_weight), static_cast<uint16_t *>(residual_out), eps};
+  const auto *wp = reinterpret_cast<const uint32_t *>(w_packed);
+  const auto *sp = static_cast<const uint16_t *>(scales);
+  const auto *zp = static_cast<const uint16_t *>(zeros);
+  const auto *bp = static_cast<const uint16_t *>(bias);
+  auto *yp = static_cast<uint16_t *>(y);
+  const int ki = static_cast<int>(k), ni = static_cast<int>(n), n_groups = ki / 128;
+  const int sk = k == 8192 ? 2 : 1;  // the GEMV's choice at these K (chunks C = K / 2048 / S)
+  const int64_t groups = swiglu ? mp_cdiv(n / 2, 2) : mp_cdiv(n, 4);
+  const dim3 grid(static_cast<unsigned>(mp_cdiv(groups, 4 / sk)));
+#define MP_W4_GEMV_NRM(C_, S_, SWI_)                                                                          \
+  do {                                                                                                        \
+    if (zp)                                                                                                   \
+      hipLaunchKernelGGL((w4a16_gemv_kernel<4, C_, S_, true, SWI_, true>), grid, dim3(256), 0, s, nrm.x, ki, wp, \
+                         ni, sp, zp, n_groups, bp, yp, nrm);                                                  \
+    else                                                                                                      \
+      hipLaunchKernelGGL((w4a16_gemv_kernel<4, C_, S_, false, SWI_, true>), grid, dim3(256), 0, s, nrm.x, ki,   \
+                         wp, ni, sp, zp, n_groups, bp, yp, nrm);                                              \
+  } while (0)
+  if (swiglu) {
+    if (k == 2048) MP_W4_GEMV_NRM(1, 1, true);
+    else if (k == 4096) MP_W4_GEMV_NRM(2, 1, true);
+    else MP_W4_GEMV_NRM(2, 2, true);
+  } else {
+    if (k == 2048) MP_W4_GEMV_NRM(1, 1, false);
+    else if (k == 4096) MP_W4_GEMV_NRM(2, 1, false);
+    else MP_W4_GEMV_NRM(2, 2, false);
+  }
+#undef MP_W4_GEMV_NRM
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
 extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n2,
                                     const void *scales, const void *zeros, int group_size, const void *bias,
                                     void *act, int x_dtype, mp_stream_t stream) {
@@ -1204,10 +1370,10 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
   do {                                                                                                       \
     if (zp)                                                                                                  \
       hipLaunchKernelGGL((w4a16_gemv_kernel<4, C_, S_, true, true>), grid, dim3(256), 0, s, xp, ki, wp, ni, sp, \
-                         zp, n_groups, bp, yp);                                                              \
+                         zp, n_groups, bp, yp, MpRowNorm{});                                                 \
     else                                                                                                     \
       hipLaunchKernelGGL((w4a16_gemv_kernel<4, C_, S_, false, true>), grid, dim3(256), 0, s, xp, ki, wp, ni,   \
-                         sp, zp, n_groups, bp, yp);                                                          \
+                         sp, zp, n_groups, bp, yp, MpRowNorm{});                                             \
   } while (0)
     if (sk == 2) {
       if (c == 2) MP_W4_GEMV_SWI(2, 2);
@@ -1312,10 +1478,10 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
   do {                                                                                                       \
     if (zp)                                                                                                  \
       hipLaunchKernelGGL((w4a16_gemv_kernel<R_, C_, S_, true>), grid, dim3(256), 0, s, xp, ki, wp, ni, sp,  \
-                         zp, n_groups_i, bp, yp);                                                            \
+                         zp, n_groups_i, bp, yp, MpRowNorm{});                                               \
     else                                                                                                     \
       hipLaunchKernelGGL((w4a16_gemv_kernel<R_, C_, S_, false>), grid, dim3(256), 0, s, xp, ki, wp, ni, sp, \
-                         zp, n_groups_i, bp, yp);                                                            \
+                         zp, n_groups_i, bp, yp, MpRowNorm{});                                               \
   } while (0)
 #define MP_W4_GEMV_C(R_, S_)           \
   do {                                 \

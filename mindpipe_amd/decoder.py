@@ -81,6 +81,7 @@ def _rms(x, w, eps):
 class W4Decoder:
     def __init__(self, cfg: DecoderConfig, max_batch: int, max_len: int, device="cuda", seed: int = 1):
         self.cfg, self.max_batch, self.max_len = cfg, max_batch, max_len
+        self.fuse_norm = True  # one-row decode steps: add-RMSNorm inside the next GEMV
         gen = torch.Generator(device=device).manual_seed(seed)
         h, hd, kvh = cfg.hidden, cfg.head_dim, cfg.kv_heads
         self.embed = (torch.randn(cfg.vocab, h, generator=gen, device=device) * 0.02).half()
@@ -209,19 +210,30 @@ class W4Decoder:
         splits, ws = self._attn_workspace(b)
         scale = 1.0 / math.sqrt(hd)
         x = self.embed[tokens]                                    # [B, H] residual stream
+        # one row with a supported width: each add-RMSNorm runs inside the next GEMV
+        fused = self.fuse_norm and b == 1 and cfg.hidden in (2048, 4096, 8192) and cfg.group == 128
+
+        def norm_linear(delta, x, w, lin, swiglu=False):
+            """(lin(RMSNorm(delta + x) * w), delta + x); delta None: no residual add."""
+            if fused:
+                src, res = (x, None) if delta is None else (delta, x)
+                y, rsum = ops.w4a16_gemv_add_rms_norm(src, res, w, cfg.eps, lin.packed, lin.scales, lin.zeros,
+                                                      lin.group, None, swiglu)
+                return y, (x if rsum is None else rsum)
+            if delta is None:
+                hn = ops.add_rms_norm_quant(x, None, w, cfg.eps, quant=False)[0]
+            else:
+                hn, _, _, x = ops.add_rms_norm_quant(delta, x, w, cfg.eps, quant=False)
+            return (lin.swiglu(hn) if swiglu else lin(hn)), x
+
         delta = None
         for li, l in enumerate(self.layers):
-            if delta is None:
-                hn = ops.add_rms_norm_quant(x, None, l["ln1"], cfg.eps, quant=False)[0]
-            else:
-                hn, _, _, x = ops.add_rms_norm_quant(delta, x, l["ln1"], cfg.eps, quant=False)
-            qkv = l["qkv"](hn)
+            qkv, x = norm_linear(delta, x, l["ln1"], l["qkv"])
             att = ops.decode_rope_attention(qkv, nh, kvh, self.cos, self.sin, cur_len, self.k_cache[li, :b],
                                             self.v_cache[li, :b], splits, scale, ws)
-            hn, _, _, x = ops.add_rms_norm_quant(l["o"](att.reshape(b, nh * hd)), x, l["ln2"], cfg.eps, quant=False)
-            delta = l["down"](l["gate_up"].swiglu(hn))
-        hn, _, _, x = ops.add_rms_norm_quant(delta, x, self.norm, cfg.eps, quant=False)
-        logits = self.lm_head(hn)
+            act, x = norm_linear(l["o"](att.reshape(b, nh * hd)), x, l["ln2"], l["gate_up"], swiglu=True)
+            delta = l["down"](act)
+        logits, x = norm_linear(delta, x, self.norm, self.lm_head)
         return logits if return_logits else logits.argmax(-1)
 
     @torch.no_grad()

@@ -389,6 +389,42 @@ def w4a16_gemm_swiglu(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Ten
     return act.reshape(*x.shape[:-1], n2 // 2)
 
 
+def w4a16_gemv_add_rms_norm(x: torch.Tensor, residual: Optional[torch.Tensor], norm_weight: torch.Tensor,
+                            eps: float, w_packed: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor],
+                            group_size: int, bias: Optional[torch.Tensor] = None, swiglu: bool = False):
+    """One fp16 row ``x [1, K]``: ``(y, residual_sum)`` with ``residual_sum = x + residual``
+    (``None`` without a residual) and ``y`` the W4A16 linear (``swiglu``: the SiLU-up product
+    of the fused gate/up weight) of ``RMSNorm(x + residual) * norm_weight``, in one launch.
+    The same bits as ``add_rms_norm_quant(..., quant=False)`` followed by ``w4a16_gemm`` /
+    ``w4a16_gemm_swiglu``.  K in {2048, 4096, 8192}, group 128."""
+    _need(x, "x", torch.float16)
+    _need(norm_weight, "norm_weight", torch.float16, 1)
+    _need(w_packed, "w_packed", torch.int32, 2)
+    _need(scales, "scales", torch.float16, 2)
+    k = x.shape[-1]
+    if x.numel() != k:
+        raise RuntimeError(f"x must hold one row, got {tuple(x.shape)}")
+    n = w_packed.shape[0]
+    if w_packed.shape[1] * 8 != k or norm_weight.shape[0] != k:
+        raise RuntimeError(f"w_packed {tuple(w_packed.shape)} / norm_weight do not match K={k}")
+    if scales.shape != (n, k // group_size) or (zeros is not None and zeros.shape != scales.shape):
+        raise RuntimeError(f"scales / zeros do not match N={n}, K={k}, g={group_size}")
+    if residual is not None:
+        _need(residual, "residual", torch.float16)
+        if residual.shape != x.shape:
+            raise RuntimeError("residual must have the shape of x")
+    if bias is not None and bias.shape != (n,):
+        raise RuntimeError("bias must be [N]")
+    y = torch.empty((*x.shape[:-1], n // 2 if swiglu else n), dtype=torch.float16, device=x.device)
+    rsum = torch.empty_like(x) if residual is not None else None
+    with _dev(x):
+        _lib.check(_lib.load().mp_w4a16_gemv_rmsnorm(
+            x.data_ptr(), _ptr(residual), norm_weight.data_ptr(), float(eps), _ptr(rsum), k, w_packed.data_ptr(),
+            n, scales.data_ptr(), _ptr(zeros), group_size, _ptr(bias), 1 if swiglu else 0, y.data_ptr(), MP_F16,
+            _stream()), "mp_w4a16_gemv_rmsnorm")
+    return y, rsum
+
+
 def decode_rope_append(qkv: torch.Tensor, nh: int, kvh: int, cos_t: torch.Tensor, sin_t: torch.Tensor,
                        pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                        q_out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -192,3 +192,70 @@ def test_decoder_kernel_step_matches_torch_step(heads, kv_heads):
     lt = model.decode_step_torch(tok, cur, return_logits=True)
     err = _rel(lk.float(), lt.float())
     assert err <= 2e-2, err
+
+
+@pytest.mark.parametrize("k,n,swiglu,res,bias,zp", [(4096, 12288, False, True, False, True),
+                                                    (4096, 2 * 1000, True, True, False, True),
+                                                    (2048, 300, False, False, True, False),
+                                                    (8192, 1100, False, True, True, True),
+                                                    (8192, 2 * 700, True, False, False, True),
+                                                    (2048, 2 * 64, True, True, True, False)])
+def test_gemv_add_rms_norm_equals_two_launch_chain(k, n, swiglu, res, bias, zp):
+    """The norm-fused one-row GEMV gives the bits of add_rms_norm_quant (quant off)
+    followed by w4a16_gemm / w4a16_gemm_swiglu, and the same residual sum."""
+    _say("gemv_add_rms_norm", k, n, swiglu, res, bias, zp)
+    from mindpipe_amd import ops
+    g = torch.Generator(device=DEV).manual_seed(k + n)
+    x = torch.randn(1, k, device=DEV, generator=g).half()
+    r = torch.randn(1, k, device=DEV, generator=g).half() if res else None
+    w = (1.0 + 0.1 * torch.randn(k, device=DEV, generator=g)).half()
+    packed = torch.randint(-2**31, 2**31 - 1, (n, k // 8), device=DEV, dtype=torch.int32, generator=g)
+    sc = (torch.rand(n, k // 128, device=DEV, generator=g) * 0.002 + 0.001).half()
+    zr = torch.randint(0, 16, (n, k // 128), device=DEV, generator=g).half() if zp else None
+    b = torch.randn(n, device=DEV, generator=g).half() if bias else None
+    y, rsum = ops.w4a16_gemv_add_rms_norm(x, r, w, 1e-5, packed, sc, zr, 128, b, swiglu)
+    hn, _, _, rs2 = ops.add_rms_norm_quant(x, r, w, 1e-5, quant=False)
+    want = (ops.w4a16_gemm_swiglu(hn, packed, sc, zr, 128, b) if swiglu
+            else ops.w4a16_gemm(hn, packed, sc, zr, 128, b))
+    assert torch.equal(y, want)
+    assert (rsum is None) == (r is None) and (rsum is None or torch.equal(rsum, rs2))
+    # a second call (other workgroup timing) gives the same bits
+    y2, _ = ops.w4a16_gemv_add_rms_norm(x, r, w, 1e-5, packed, sc, zr, 128, b, swiglu)
+    assert torch.equal(y2, y)
+
+
+def test_gemv_add_rms_norm_rejects_unsupported():
+    from mindpipe_amd import ops
+    x = torch.randn(1, 1024, device=DEV).half()
+    w = torch.ones(1024, device=DEV).half()
+    packed = torch.zeros(64, 128, device=DEV, dtype=torch.int32)
+    sc = torch.ones(64, 8, device=DEV).half()
+    with pytest.raises(RuntimeError):
+        ops.w4a16_gemv_add_rms_norm(x, None, w, 1e-5, packed, sc, None, 128)  # K = 1024
+    with pytest.raises(RuntimeError):  # more than one row
+        ops.w4a16_gemv_add_rms_norm(torch.randn(2, 2048, device=DEV).half(), None, torch.ones(2048, device=DEV).half(),
+                                    1e-5, torch.zeros(64, 256, device=DEV, dtype=torch.int32),
+                                    torch.ones(64, 16, device=DEV).half(), None, 128)
+
+
+def test_decoder_one_row_step_fused_norm():
+    """B = 1 decode step with every add-RMSNorm inside the next GEMV: the same logits bits
+    as the two-launch chain, and within 2e-2 of the PyTorch step."""
+    _say("decoder fused-norm step")
+    from mindpipe_amd.decoder import DecoderConfig, W4Decoder
+    cfg = DecoderConfig(layers=2, hidden=2048, heads=16, kv_heads=4, ffn=1024, vocab=512)
+    model = W4Decoder(cfg, max_batch=1, max_len=96, device=DEV, seed=7)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    toks = torch.randint(0, cfg.vocab, (1, 40), device=DEV, generator=g)
+    model.prefill(toks)
+    kc, vc = model.k_cache.clone(), model.v_cache.clone()
+    tok = torch.randint(0, cfg.vocab, (1,), device=DEV, generator=g)
+    cur = torch.tensor([40], device=DEV, dtype=torch.int64)
+    lf = model.decode_step(tok, cur, return_logits=True)
+    model.k_cache.copy_(kc); model.v_cache.copy_(vc)
+    model.fuse_norm = False
+    lu = model.decode_step(tok, cur, return_logits=True)
+    assert torch.equal(lf, lu)
+    model.k_cache.copy_(kc); model.v_cache.copy_(vc)
+    lt = model.decode_step_torch(tok, cur, return_logits=True)
+    assert _rel(lf.float(), lt.float()) <= 2e-2
