@@ -3,7 +3,7 @@
 // decoding) with its split merge (optionally with the RoPE and the append
 // fused into the attention launch), and SiLU-multiply.  The reference has no
 // counterpart (attention belongs to vLLM's backend); these exist so that one
-// greedy decode step runs as ~10 launches per layer and the W4A16 GEMVs, not
+// greedy decode step runs as 6-8 launches per layer and the W4A16 GEMVs, not
 // launch gaps, set the step time.
 //
 // Shapes: head dim 128; q/k/v heads packed as one qkv row [B, (nh + 2 kvh) * 128]

@@ -10,6 +10,8 @@ W4A16 GEMM each (row concatenation of the packed weight is exact).
 ``decode_step`` runs one greedy step as 7-8 launches per layer: fused residual-add
 + RMSNorm, the W4A16 GEMVs, split-K decode attention with RoPE and the KV append
 fused in (plus the split merge), and the gate/up GEMV with SiLU-mul in its epilogue.
+With one row (and hidden 2048 / 4096 / 8192) each add-RMSNorm runs in the prologue
+of the GEMV that consumes it: 6 launches per layer.
 The KV cache has a fixed capacity ``[L, B, kvh, T, 128]`` and every kernel reads
 the current position from device memory, so a step is shape-static and can be
 captured into a HIP graph.  ``decode_step_torch`` is the same step in PyTorch ops
