@@ -5,7 +5,9 @@ Prints ONE JSON line.  ``value`` is the headline W4A16 g128 GEMV at M=1
 with the weights rotated over >= 64 distinct copies (>= 571 MB) so the 256 MB
 Infinity Cache cannot serve them; inputs are resident in HBM before timing.
 The other legs of the metric (W8A8 int8 GEMM TOPS at M=4096, the W8A8 sweep,
-W4A16 M=16, the Mixtral-shaped MoE chain) are reported under ``legs``, each
+W4A16 M=16, the Mixtral-shaped MoE chain, the Llama-2-7B-shaped decode at
+B = 1 / 8 / 32 with its 2048-token prefill, and the Llama-3-70B-shaped decode at
+B = 1 / 16 / 64 over a 4096-token context) are reported under ``legs``, each
 with its own roofline fraction.  Timing uses HIP events recorded on the stream
 the kernels are launched on (torch's current stream), bracketed by
 ``torch.cuda.synchronize()``.
@@ -322,7 +324,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--legs", default="w4,w8,moe,dec7b")
+    ap.add_argument("--legs", default="w4,w8,moe,dec7b,dec70b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the kernel mix profiled for HBM traffic (profiles/traffic.json) and exit")
@@ -392,6 +394,8 @@ def main():
         "cpu_baseline": cpu,
         "int8_tops_m4096": round(w8["tops"], 2) if w8 else None,
         "decode_7b_tok_s": {k: round(v["tok_s"], 1) for k, v in dec["decode"].items()} if dec else None,
+        "decode_70b_tok_s": ({k: round(v["tok_s"], 1) for k, v in out_legs["llama3_70b_w4a16"]["decode"].items()}
+                             if "llama3_70b_w4a16" in out_legs else None),
         "legs": out_legs,
         "device": dev.name,
     }

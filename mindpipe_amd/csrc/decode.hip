@@ -73,6 +73,22 @@ __device__ __forceinline__ void rope8(const uint4 xv, const uint2 cv, const uint
   }
 }
 
+// Sum over each row of 16 lanes with DPP adds (full-rate VALU; __shfl_xor lowers to
+// ds_bpermute chains): pairs (quad_perm 1,0,3,2), quads (2,3,0,1), then half-rows
+// (row_half_mirror) and rows (row_mirror).  Every lane of the row gets the same value:
+// each stage adds two equal partial sums in either order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_sum16(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  return v;
+}
+
 __device__ __forceinline__ void h8_to_f32(const uint4 v, float (&f)[8]) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -209,10 +225,7 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
         float d = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) d = fmaf(qf[g][e], kf[e], d);
-        d += __shfl_xor(d, 1, 64);
-        d += __shfl_xor(d, 2, 64);
-        d += __shfl_xor(d, 4, 64);
-        d += __shfl_xor(d, 8, 64);
+        d = dpp_sum16(d);
         if (dl == 0 && t < n) sc[g * chunk + t] = d * scale;
       }
     }
