@@ -89,6 +89,8 @@ __device__ __forceinline__ float dpp_sum16(float v) {
   return v;
 }
 
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ void h8_to_f32(const uint4 v, float (&f)[8]) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -157,21 +159,6 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
   auto tpos = [&](int base, int u) { return base + u * 16 + wave * 4 + pl; };  // unclamped
 
   // ---- loads: query (+ new key / value) slices, then the first K and V rounds
-  uint4 qv[GRP], knv, vnv;
-  uint2 cv, sv;
-  if (ROPE) {
-    const uint16_t *row = qsrc + static_cast<int64_t>(b) * (nh + 2 * kvh) * kHd + dl * 8;
-#pragma unroll
-    for (int g = 0; g < GRP; ++g) qv[g] = *reinterpret_cast<const uint4 *>(row + (kh * GRP + g) * kHd);
-    knv = *reinterpret_cast<const uint4 *>(row + (nh + kh) * kHd);
-    vnv = *reinterpret_cast<const uint4 *>(row + (nh + kvh + kh) * kHd);
-    cv = *reinterpret_cast<const uint2 *>(cos_t + pos * (kHd / 2) + dl * 4);
-    sv = *reinterpret_cast<const uint2 *>(sin_t + pos * (kHd / 2) + dl * 4);
-  } else {
-#pragma unroll
-    for (int g = 0; g < GRP; ++g)
-      qv[g] = *reinterpret_cast<const uint4 *>(qsrc + (static_cast<int64_t>(b) * nh + kh * GRP + g) * kHd + dl * 8);
-  }
   auto load_round = [&](uint4 (&r)[U], const uint16_t *base_p, int base) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -179,62 +166,191 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
       r[u] = *reinterpret_cast<const uint4 *>(base_p + static_cast<int64_t>(t0 + t) * kHd);
     }
   };
-  uint4 kv[U], vv[U];
-  load_round(kv, kbase, 0);
-  load_round(vv, vbase, 0);
-
-  // ---- queries to fp32; with ROPE rotate, and append the new row (lanes 0-15 the key,
-  // 16-31 the value of the appending workgroup; every other store is dropped)
-  float qf[GRP][8];
-  uint4 knew = make_uint4(0, 0, 0, 0);
-  if (ROPE) {
-#pragma unroll
-    for (int g = 0; g < GRP; ++g) rope8(qv[g], cv, sv, qf[g]);
-    float kr[8];
-    rope8(knv, cv, sv, kr);
-    uint32_t w[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      w[j] = static_cast<uint32_t>(mp_f2h(kr[2 * j])) | (static_cast<uint32_t>(mp_f2h(kr[2 * j + 1])) << 16);
-    knew = make_uint4(w[0], w[1], w[2], w[3]);
-    const uint32_t cbytes = static_cast<uint32_t>(cap) * kHd * 2;
-    const uint32_t roff = (static_cast<uint32_t>(pos) * kHd + dl * 8) * 2;
-    mp_buf_store16(mp_rsrc(k_cache + static_cast<int64_t>(bk) * cap * kHd, cbytes), app && tid < 16 ? roff : kOob,
-                   knew);
-    mp_buf_store16(mp_rsrc(v_cache + static_cast<int64_t>(bk) * cap * kHd, cbytes),
-                   app && tid >= 16 && tid < 32 ? roff : kOob, vnv);
-  } else {
-#pragma unroll
-    for (int g = 0; g < GRP; ++g) h8_to_f32(qv[g], qf[g]);
-  }
   // the row a lane uses for (clamped) position t: the new token's from registers
   auto pick = [&](const uint4 cached, const uint4 fresh, int t) {
     return (app && min(t, n - 1) == n - 1) ? fresh : cached;
   };
-
-  // ---- scores
+  const uint32_t cbytes = static_cast<uint32_t>(cap) * kHd * 2;
+  const auto krs = mp_rsrc(k_cache + static_cast<int64_t>(bk) * cap * kHd, cbytes);
+  const auto vrs = mp_rsrc(v_cache + static_cast<int64_t>(bk) * cap * kHd, cbytes);
+  const uint16_t *qkv_row = qsrc + static_cast<int64_t>(b) * (nh + 2 * kvh) * kHd;  // ROPE
   float *sc = sm;
-  auto score_round = [&](const uint4 (&r)[U], int base) {
+  uint4 vv[U], vnv = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (GRP >= 4) {
+    // ---- scores on MFMA (f32_16x16x16_f16): D[t][g] = K[t] . Q[g] for 16 positions of the
+    // wave x 16 head slots (GRP used).  Lane l: position / head slot tl = l % 16 and the dims
+    // [32 q4, +32), q4 = l / 16; MFMA j takes dims 32 q4 + 4 j + [0, 4) of both operands (one
+    // permutation of the reduction index).  D: lane l holds positions 4 q4 + i of head tl.
+    const int q4 = lane >> 4, tl = lane & 15;
+    const int gq = tl < GRP ? tl : GRP - 1;
+    uint4 q32[4], k32[4];
+    uint2 c32[4], s32[4];
+    if (ROPE) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = tpos(base, u);
-      float kf[8];
-      h8_to_f32(ROPE ? pick(r[u], knew, t) : r[u], kf);
-#pragma unroll
-      for (int g = 0; g < GRP; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qf[g][e], kf[e], d);
-        d = dpp_sum16(d);
-        if (dl == 0 && t < n) sc[g * chunk + t] = d * scale;
+      for (int c = 0; c < 4; ++c) {
+        q32[c] = *reinterpret_cast<const uint4 *>(qkv_row + (kh * GRP + gq) * kHd + q4 * 32 + c * 8);
+        k32[c] = *reinterpret_cast<const uint4 *>(qkv_row + (nh + kh) * kHd + q4 * 32 + c * 8);
+        c32[c] = *reinterpret_cast<const uint2 *>(cos_t + pos * (kHd / 2) + (4 * q4 + c) * 4);
+        s32[c] = *reinterpret_cast<const uint2 *>(sin_t + pos * (kHd / 2) + (4 * q4 + c) * 4);
       }
+      vnv = *reinterpret_cast<const uint4 *>(qkv_row + (nh + kvh + kh) * kHd + dl * 8);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        q32[c] = *reinterpret_cast<const uint4 *>(qsrc + (static_cast<int64_t>(b) * nh + kh * GRP + gq) * kHd +
+                                                  q4 * 32 + c * 8);
     }
-  };
-  score_round(kv, 0);
-  for (int base = 16 * U; base < n; base += 16 * U) {
-    uint4 k2[U];
-    load_round(k2, kbase, base);
-    score_round(k2, base);
+    const uint16_t *kb32 = k_cache + static_cast<int64_t>(bk) * cap * kHd + q4 * 32;
+    auto load_k = [&](uint4 (&r)[4], int base) {
+      const int t = min(base + 16 * wave + tl, n - 1);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r[c] = *reinterpret_cast<const uint4 *>(kb32 + static_cast<int64_t>(t0 + t) * kHd + c * 8);
+    };
+    uint4 kc[4];
+    load_k(kc, 0);
+    load_round(vv, vbase, 0);
+    __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the rotation waits
+
+    // operands: rotated (ROPE) queries of head slot tl, zero for the unused slots
+    h4_t qb[8];
+    uint4 knew32[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (ROPE) {
+        float f[8], kr[8];
+        rope8(q32[c], c32[c], s32[c], f);
+        rope8(k32[c], c32[c], s32[c], kr);
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          w[j] = static_cast<uint32_t>(mp_f2h(kr[2 * j])) | (static_cast<uint32_t>(mp_f2h(kr[2 * j + 1])) << 16);
+        knew32[c] = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qb[2 * c][e] = static_cast<_Float16>(f[e]);
+          qb[2 * c + 1][e] = static_cast<_Float16>(f[4 + e]);
+        }
+      } else {
+        knew32[c] = make_uint4(0u, 0u, 0u, 0u);
+        qb[2 * c] = __builtin_bit_cast(h4_t, make_uint2(q32[c].x, q32[c].y));
+        qb[2 * c + 1] = __builtin_bit_cast(h4_t, make_uint2(q32[c].z, q32[c].w));
+      }
+      const h4_t zero = {0, 0, 0, 0};
+      qb[2 * c] = tl < GRP ? qb[2 * c] : zero;
+      qb[2 * c + 1] = tl < GRP ? qb[2 * c + 1] : zero;
+    }
+    if (ROPE) {  // append: the key from wave 0's lanes with tl == 0, the value from lanes 16-31
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        mp_buf_store16(krs, app && tid < 64 && tl == 0 ? (static_cast<uint32_t>(pos) * kHd + q4 * 32 + c * 8) * 2 : kOob,
+                       knew32[c]);
+      mp_buf_store16(vrs, app && tid >= 16 && tid < 32 ? (static_cast<uint32_t>(pos) * kHd + dl * 8) * 2 : kOob,
+                     vnv);
+    }
+    // the appending workgroup's last position is scored from the new key after the loop
+    auto score_step = [&](const uint4 (&r)[4], int base) {
+      f4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint4 w = r[j >> 1];
+        const h4_t a = __builtin_bit_cast(h4_t, (j & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y));
+        d = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qb[j], d, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = base + 16 * wave + 4 * q4 + i;
+        if (tl < GRP && t < n && !(app && t == n - 1)) sc[tl * chunk + t] = d[i] * scale;
+      }
+    };
+    // two register sets in turn (n >= 1: at least one step); the prefetch past the end
+    // re-reads the last row
+    uint4 kd[4];
+    int base = 0;
+    while (true) {
+      load_k(kd, base + 64);
+      score_step(kc, base);
+      base += 64;
+      if (base >= n) break;
+      load_k(kc, base + 64);
+      score_step(kd, base);
+      base += 64;
+      if (base >= n) break;
+    }
+    if (app) {  // workgroup-uniform: every row of A is the new key, so D row 0 is its score
+      f4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint4 w = knew32[j >> 1];
+        const h4_t a = __builtin_bit_cast(h4_t, (j & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y));
+        d = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qb[j], d, 0, 0, 0);
+      }
+      if (wave == 0 && q4 == 0 && tl < GRP) sc[tl * chunk + n - 1] = d[0] * scale;
+    }
+  } else {
+    uint4 qv[GRP], knv;
+    uint2 cv, sv;
+    if (ROPE) {
+      const uint16_t *row = qkv_row + dl * 8;
+#pragma unroll
+      for (int g = 0; g < GRP; ++g) qv[g] = *reinterpret_cast<const uint4 *>(row + (kh * GRP + g) * kHd);
+      knv = *reinterpret_cast<const uint4 *>(row + (nh + kh) * kHd);
+      vnv = *reinterpret_cast<const uint4 *>(row + (nh + kvh + kh) * kHd);
+      cv = *reinterpret_cast<const uint2 *>(cos_t + pos * (kHd / 2) + dl * 4);
+      sv = *reinterpret_cast<const uint2 *>(sin_t + pos * (kHd / 2) + dl * 4);
+    } else {
+#pragma unroll
+      for (int g = 0; g < GRP; ++g)
+        qv[g] = *reinterpret_cast<const uint4 *>(qsrc + (static_cast<int64_t>(b) * nh + kh * GRP + g) * kHd + dl * 8);
+    }
+    uint4 kv[U];
+    load_round(kv, kbase, 0);
+    load_round(vv, vbase, 0);
+
+    // queries to fp32; with ROPE rotate, and append the new row (lanes 0-15 the key,
+    // 16-31 the value of the appending workgroup; every other store is dropped)
+    float qf[GRP][8];
+    uint4 knew = make_uint4(0, 0, 0, 0);
+    if (ROPE) {
+#pragma unroll
+      for (int g = 0; g < GRP; ++g) rope8(qv[g], cv, sv, qf[g]);
+      float kr[8];
+      rope8(knv, cv, sv, kr);
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = static_cast<uint32_t>(mp_f2h(kr[2 * j])) | (static_cast<uint32_t>(mp_f2h(kr[2 * j + 1])) << 16);
+      knew = make_uint4(w[0], w[1], w[2], w[3]);
+      const uint32_t roff = (static_cast<uint32_t>(pos) * kHd + dl * 8) * 2;
+      mp_buf_store16(krs, app && tid < 16 ? roff : kOob, knew);
+      mp_buf_store16(vrs, app && tid >= 16 && tid < 32 ? roff : kOob, vnv);
+    } else {
+#pragma unroll
+      for (int g = 0; g < GRP; ++g) h8_to_f32(qv[g], qf[g]);
+    }
+
+    // ---- scores on the VALU: 16 lanes per position, DPP sums
+    auto score_round = [&](const uint4 (&r)[U], int base) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int t = tpos(base, u);
+        float kf[8];
+        h8_to_f32(ROPE ? pick(r[u], knew, t) : r[u], kf);
+#pragma unroll
+        for (int g = 0; g < GRP; ++g) {
+          float d = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) d = fmaf(qf[g][e], kf[e], d);
+          d = dpp_sum16(d);
+          if (dl == 0 && t < n) sc[g * chunk + t] = d * scale;
+        }
+      }
+    };
+    score_round(kv, 0);
+    for (int base = 16 * U; base < n; base += 16 * U) {
+      uint4 k2[U];
+      load_round(k2, kbase, base);
+      score_round(k2, base);
+    }
   }
   mp_lds_barrier();
 
