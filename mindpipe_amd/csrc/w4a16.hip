@@ -474,7 +474,7 @@ template <int MT, int NT, int S, bool ZP, bool SWI = false>
 __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
-    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, int halves) {
   constexpr int U = 2;        // blocks per prefetch buffer
   constexpr int STEP = 8;     // blocks per scale / zero vector
   constexpr int XI = 4 * MT;  // activation loads per block (4 rows x 256 bytes each)
@@ -491,7 +491,19 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   constexpr int NO = SWI ? NT / 2 : NT;  // output tiles per wave
   static_assert(!SWI || NT % 2 == 0, "SwiGLU pairs tiles");
   const int n_out = SWI ? n_cols / 2 : n_cols;
-  const int col0 = blockIdx.x * NO * 16;
+  // halves == 2 (33..64 rows on the 32-row tiling): the two workgroups of a column group take
+  // rows [0, 32) and [32, M).  They sit 8 apart in dispatch order, so on one XCD at nearly the
+  // same time, and the second read of the weight slab comes from that XCD's L2.
+  int bx = blockIdx.x;
+  if (halves == 2) {
+    const int half = (bx >> 3) & 1;
+    bx = (bx >> 4) * 8 + (bx & 7);
+    x += static_cast<int64_t>(half) * 32 * k;
+    y += static_cast<int64_t>(half) * 32 * n_out;
+    m_rows = half ? m_rows - 32 : 32;
+  }
+  const int col0 = bx * NO * 16;
+  if (col0 >= n_out) return;  // padding workgroups of the halves grid; uniform, before any barrier
   // K range of this wave: whole steps; blocks at or past nblk are dead
   const int nst = (nblk + STEP - 1) / STEP;
   const int st_lo = (nst * wave) / S;
@@ -1199,6 +1211,12 @@ static int mp_batch_env(int which) {
   return v[which];
 }
 
+// 33..64 rows run as two 32-row halves of one grid (MP_W4_BATCH_HALVES=0: the 64-row tiling).
+static bool mp_batch_halves() {
+  static const bool v = !(getenv("MP_W4_BATCH_HALVES") && atoi(getenv("MP_W4_BATCH_HALVES")) == 0);
+  return v;
+}
+
 // The batched kernel takes M > this value (default 1: every 2 <= M <= 64, measured faster than
 // the LDS-staged kernel at 2..4 rows too, and the fused SwiGLU path then shares its sums);
 // MP_W4_BATCH_MIN_M overrides it, for measurements.
@@ -1387,26 +1405,29 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
     return MP_OK;
   }
   // batched kernel: NT/2 gate tiles paired with NT/2 up tiles per wave
-  const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-  int nt = half >= 8192 ? 4 : 2;
+  const bool halves = m > 32 && mp_batch_halves();
+  const int mt = m <= 16 ? 1 : (m <= 32 || halves ? 2 : 4);
+  int nt = half >= 8192 && mt < 4 ? 4 : 2;  // 64-row tiling: 2 (registers)
   if (mp_batch_env(0) >= 2) nt = mp_batch_env(0) >= 4 ? 4 : 2;
   const int smax = mt * nt >= 8 ? 4 : 8;
   const int nblk = ki / 128;
   const int nsteps = (nblk + 7) / 8;
   const int64_t groups = mp_cdiv(half, 16 * (nt / 2));
+  const int64_t wgs = halves ? 2 * groups : groups;
   int split = 1;
-  while (split < smax && groups * split < (mp_batch_env(2) > 0 ? mp_batch_env(2) : 1024) && nsteps / (split * 2) >= 1)
+  while (split < smax && wgs * split < (mp_batch_env(2) > 0 ? mp_batch_env(2) : 1024) && nsteps / (split * 2) >= 1)
     split *= 2;
   if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
-  const dim3 grid(static_cast<unsigned>(groups));
+  const dim3 grid(static_cast<unsigned>(halves ? mp_cdiv(groups, 8) * 16 : groups));
+  const int hv = halves ? 2 : 1;
 #define MP_W4_BSWI(MT_, NT_, S_)                                                                              \
   do {                                                                                                       \
     if (zp)                                                                                                  \
       hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki,  \
-                         wp, ni, sp, zp, n_groups, bp, yp);                                                  \
+                         wp, ni, sp, zp, n_groups, bp, yp, hv);                                              \
     else                                                                                                     \
       hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, \
-                         wp, ni, sp, zp, n_groups, bp, yp);                                                  \
+                         wp, ni, sp, zp, n_groups, bp, yp, hv);                                              \
   } while (0)
 #define MP_W4_BSWI_S(MT_, NT_)                                                  \
   do {                                                                          \
@@ -1506,11 +1527,12 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
       aligned && n * (k / 2) < (int64_t(1) << 32) && m * k * 2 < (int64_t(1) << 32)) {
     const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
     const int nblk = ki / 128;
-    const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-    // column tiles per wave (activation reuse): 4 for 17..32 rows once N is large enough to fill the chip
+    const bool halves = m > 32 && mp_batch_halves();
+    const int mt = m <= 16 ? 1 : (m <= 32 || halves ? 2 : 4);
     // column tiles per wave (measured on the 7B decode shapes, M = 8..64): one for N <= 4096
-    // (enough workgroups), four from N = 12288 (activation loads shared by more tiles)
-    int nt = n <= 4096 ? 1 : (n >= 12288 ? 4 : 2);
+    // (enough workgroups), four from N = 12288 (activation loads shared by more tiles); the
+    // 64-row tiling takes at most 2 (registers)
+    int nt = n <= 4096 ? 1 : (n >= 12288 && mt < 4 ? 4 : 2);
     if (mp_batch_env(0) > 0) nt = mp_batch_env(0) >= 4 ? 4 : mp_batch_env(0);
     const int smax = mt * nt >= 8 ? 4 : (mt * nt > 1 ? 8 : 16);  // register budget per wave count
     const int64_t groups = mp_cdiv(n, 16 * nt);
@@ -1518,18 +1540,20 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     // waves splitting K, >= 1 step each, up to ~1024 waves (~2048 for one-tile waves of <= 16 rows,
     // measured on the 7B down projection at M = 8: 11.6 -> 10.2 us)
     const int64_t target = mp_batch_env(2) > 0 ? mp_batch_env(2) : (mt == 1 && nt == 1 ? 2048 : 1024);
+    const int64_t wgs = halves ? 2 * groups : groups;
     int split = 1;
-    while (split < smax && groups * split < target && nsteps / (split * 2) >= 1) split *= 2;
+    while (split < smax && wgs * split < target && nsteps / (split * 2) >= 1) split *= 2;
     if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
-    const dim3 grid(static_cast<unsigned>(groups));
+    const dim3 grid(static_cast<unsigned>(halves ? mp_cdiv(groups, 8) * 16 : groups));
+    const int hv = halves ? 2 : 1;
 #define MP_W4_BATCH(MT_, NT_, S_)                                                                            \
   do {                                                                                                       \
     if (zp)                                                                                                  \
       hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, wp, \
-                         ni, sp, zp, n_groups_i, bp, yp);                                                    \
+                         ni, sp, zp, n_groups_i, bp, yp, hv);                                                \
     else                                                                                                     \
       hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, wp, \
-                         ni, sp, zp, n_groups_i, bp, yp);                                                    \
+                         ni, sp, zp, n_groups_i, bp, yp, hv);                                                \
   } while (0)
 #define MP_W4_BATCH_S(MT_, NT_)                    \
   do {                                             \

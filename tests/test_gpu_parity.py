@@ -112,7 +112,9 @@ W4_CASES = [(1, 4096, 4096), (16, 4096, 4096), (3, 512, 1024), (17, 256, 2048), 
             # one-row GEMV: partial 2048-wide K chunk, N not a multiple of the rows per wave, odd chunk count
             (1, 37, 768), (1, 301, 2304), (1, 1001, 11008), (1, 64, 6144),
             # 2..8 rows (four-row MFMA kernel): half-filled last K chunk, N not a multiple of 16, split-K waves
-            (2, 4096, 4096), (4, 1000, 2304), (5, 4096, 11008), (8, 12288, 4096), (7, 300, 1280), (6, 72, 512)]
+            (2, 4096, 4096), (4, 1000, 2304), (5, 4096, 11008), (8, 12288, 4096), (7, 300, 1280), (6, 72, 512),
+            # 33..64 rows as two 32-row halves of one grid: padding workgroups, 4 / 2 / 1 column tiles
+            (48, 12288, 4096), (64, 8192, 2048), (37, 1000, 1024), (57, 4096, 1280)]
 
 
 @pytest.mark.parametrize("m,n,k", W4_CASES)
@@ -138,7 +140,7 @@ def test_w4a16_gemm_matches_dequant_matmul(m, n, k, zp):
 
 @pytest.mark.parametrize("m,i,k", [(1, 2048, 4096), (1, 1001, 2304), (1, 300, 11008), (8, 2048, 4096), (16, 1000, 1024),
                                    (24, 4096, 512), (40, 520, 2048), (64, 256, 1024), (3, 1001, 2304),
-                                   (6, 300, 11008)])
+                                   (6, 300, 11008), (64, 8192, 2048), (45, 1000, 1024)])
 @pytest.mark.parametrize("zp", [True, False])
 def test_w4a16_gemm_swiglu_matches_two_step(m, i, k, zp):
     """Fused gate/up GEMM + SiLU-mul against silu_mul(w4a16_gemm) (bit-exact for the one-row
