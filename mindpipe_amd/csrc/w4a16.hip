@@ -474,7 +474,7 @@ template <int MT, int NT, int S, bool ZP, bool SWI = false>
 __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
-    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, int halves) {
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, int parts) {
   constexpr int U = 2;        // blocks per prefetch buffer
   constexpr int STEP = 8;     // blocks per scale / zero vector
   constexpr int XI = 4 * MT;  // activation loads per block (4 rows x 256 bytes each)
@@ -491,19 +491,19 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   constexpr int NO = SWI ? NT / 2 : NT;  // output tiles per wave
   static_assert(!SWI || NT % 2 == 0, "SwiGLU pairs tiles");
   const int n_out = SWI ? n_cols / 2 : n_cols;
-  // halves == 2 (33..64 rows on the 32-row tiling): the two workgroups of a column group take
-  // rows [0, 32) and [32, M).  They sit 8 apart in dispatch order, so on one XCD at nearly the
-  // same time, and the second read of the weight slab comes from that XCD's L2.
+  // parts > 1 (more rows than the 16 MT-row tiling): the parts workgroups of a column group take
+  // rows [16 MT p, 16 MT (p + 1)).  They sit 8 apart in dispatch order, so on one XCD at nearly
+  // the same time, and the later reads of the weight slab come from that XCD's L2.
   int bx = blockIdx.x;
-  if (halves == 2) {
-    const int half = (bx >> 3) & 1;
-    bx = (bx >> 4) * 8 + (bx & 7);
-    x += static_cast<int64_t>(half) * 32 * k;
-    y += static_cast<int64_t>(half) * 32 * n_out;
-    m_rows = half ? m_rows - 32 : 32;
+  if (parts > 1) {
+    const int part = (bx >> 3) % parts;
+    bx = (bx / (8 * parts)) * 8 + (bx & 7);
+    x += static_cast<int64_t>(part) * 16 * MT * k;
+    y += static_cast<int64_t>(part) * 16 * MT * n_out;
+    m_rows = min(16 * MT, m_rows - part * 16 * MT);
   }
   const int col0 = bx * NO * 16;
-  if (col0 >= n_out) return;  // padding workgroups of the halves grid; uniform, before any barrier
+  if (col0 >= n_out || m_rows <= 0) return;  // padding workgroups of a parts grid; uniform, before any barrier
   // K range of this wave: whole steps; blocks at or past nblk are dead
   const int nst = (nblk + STEP - 1) / STEP;
   const int st_lo = (nst * wave) / S;
@@ -1211,10 +1211,13 @@ static int mp_batch_env(int which) {
   return v[which];
 }
 
-// 33..64 rows run as two 32-row halves of one grid (MP_W4_BATCH_HALVES=0: the 64-row tiling).
-static bool mp_batch_halves() {
-  static const bool v = !(getenv("MP_W4_BATCH_HALVES") && atoi(getenv("MP_W4_BATCH_HALVES")) == 0);
-  return v;
+// Row tiling of the batched kernel: MT 16-row tiles per wave, and parts = ceil(M / 16 MT)
+// workgroups per column group when M exceeds them.  Default: MT = 1 up to 16 rows, 2 above
+// (33..64 rows in two parts).  MP_W4_BATCH_PART_MT=1 / 2 / 4 fixes MT (for measurements).
+static int mp_batch_part_mt(int64_t m) {
+  static const int v = getenv("MP_W4_BATCH_PART_MT") ? atoi(getenv("MP_W4_BATCH_PART_MT")) : 0;
+  if (v == 1 || v == 2 || v == 4) return v;
+  return m <= 16 ? 1 : 2;
 }
 
 // The batched kernel takes M > this value (default 1: every 2 <= M <= 64, measured faster than
@@ -1405,21 +1408,21 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
     return MP_OK;
   }
   // batched kernel: NT/2 gate tiles paired with NT/2 up tiles per wave
-  const bool halves = m > 32 && mp_batch_halves();
-  const int mt = m <= 16 ? 1 : (m <= 32 || halves ? 2 : 4);
+  const int mt = mp_batch_part_mt(m);
+  const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
   int nt = half >= 8192 && mt < 4 ? 4 : 2;  // 64-row tiling: 2 (registers)
   if (mp_batch_env(0) >= 2) nt = mp_batch_env(0) >= 4 ? 4 : 2;
   const int smax = mt * nt >= 8 ? 4 : 8;
   const int nblk = ki / 128;
   const int nsteps = (nblk + 7) / 8;
   const int64_t groups = mp_cdiv(half, 16 * (nt / 2));
-  const int64_t wgs = halves ? 2 * groups : groups;
+  const int64_t wgs = groups * parts;
   int split = 1;
   while (split < smax && wgs * split < (mp_batch_env(2) > 0 ? mp_batch_env(2) : 1024) && nsteps / (split * 2) >= 1)
     split *= 2;
   if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
-  const dim3 grid(static_cast<unsigned>(halves ? mp_cdiv(groups, 8) * 16 : groups));
-  const int hv = halves ? 2 : 1;
+  const dim3 grid(static_cast<unsigned>(parts > 1 ? mp_cdiv(groups, 8) * 8 * parts : groups));
+  const int hv = parts;
 #define MP_W4_BSWI(MT_, NT_, S_)                                                                              \
   do {                                                                                                       \
     if (zp)                                                                                                  \
@@ -1527,8 +1530,8 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
       aligned && n * (k / 2) < (int64_t(1) << 32) && m * k * 2 < (int64_t(1) << 32)) {
     const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
     const int nblk = ki / 128;
-    const bool halves = m > 32 && mp_batch_halves();
-    const int mt = m <= 16 ? 1 : (m <= 32 || halves ? 2 : 4);
+    const int mt = mp_batch_part_mt(m);
+    const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
     // column tiles per wave (measured on the 7B decode shapes, M = 8..64): one for N <= 4096
     // (enough workgroups), four from N = 12288 (activation loads shared by more tiles); the
     // 64-row tiling takes at most 2 (registers)
@@ -1540,12 +1543,12 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     // waves splitting K, >= 1 step each, up to ~1024 waves (~2048 for one-tile waves of <= 16 rows,
     // measured on the 7B down projection at M = 8: 11.6 -> 10.2 us)
     const int64_t target = mp_batch_env(2) > 0 ? mp_batch_env(2) : (mt == 1 && nt == 1 ? 2048 : 1024);
-    const int64_t wgs = halves ? 2 * groups : groups;
+    const int64_t wgs = groups * parts;
     int split = 1;
     while (split < smax && wgs * split < target && nsteps / (split * 2) >= 1) split *= 2;
     if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
-    const dim3 grid(static_cast<unsigned>(halves ? mp_cdiv(groups, 8) * 16 : groups));
-    const int hv = halves ? 2 : 1;
+    const dim3 grid(static_cast<unsigned>(parts > 1 ? mp_cdiv(groups, 8) * 8 * parts : groups));
+    const int hv = parts;
 #define MP_W4_BATCH(MT_, NT_, S_)                                                                            \
   do {                                                                                                       \
     if (zp)                                                                                                  \
