@@ -81,6 +81,26 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_add(float x) {
   return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float x) {
+  return fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF,
+                                                                        false)));
+}
+// wave-wide max / sum: the 16-lane DPP stages, then the four rows (lanes l ^ 16, l ^ 32)
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = dpp_max<0xB1>(v);
+  v = dpp_max<0x4E>(v);
+  v = dpp_max<0x141>(v);
+  v = dpp_max<0x140>(v);
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float dpp_sum16(float v);
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = dpp_sum16(v);
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
+}
 __device__ __forceinline__ float dpp_sum16(float v) {
   v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
   v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
@@ -356,6 +376,34 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
 
   // ---- softmax statistics per head over the workgroup's positions
   float mx[GRP], sum[GRP];
+  if constexpr (GRP >= 4) {
+    // one wave per head (heads wave, wave + 4, ...): the statistics need a single barrier
+    __shared__ float hstat[GRP][2];
+#pragma unroll
+    for (int hh = 0; hh < GRP / 4; ++hh) {
+      const int g = wave + 4 * hh;
+      float m = -INFINITY;
+      for (int t = lane; t < n; t += 64) m = fmaxf(m, sc[g * chunk + t]);
+      m = wave_max_dpp(m);
+      float l = 0.f;
+      for (int t = lane; t < n; t += 64) {
+        const float p = expf(sc[g * chunk + t] - m);
+        sc[g * chunk + t] = p;
+        l += p;
+      }
+      l = wave_sum_dpp(l);
+      if (lane == 0) {
+        hstat[g][0] = m;
+        hstat[g][1] = l;
+      }
+    }
+    mp_lds_barrier();
+#pragma unroll
+    for (int g = 0; g < GRP; ++g) {
+      mx[g] = hstat[g][0];
+      sum[g] = hstat[g][1];
+    }
+  } else {
 #pragma unroll
   for (int g = 0; g < GRP; ++g) {
     float m = -INFINITY;
@@ -379,6 +427,7 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
     mp_lds_barrier();
     mx[g] = m;
     sum[g] = l;
+  }
   }
 
   // ---- P.V
