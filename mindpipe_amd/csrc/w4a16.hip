@@ -713,7 +713,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
 // ------------------------------------------------------------------ prefill GEMM (M > 64)
 //
 // 128x128 output tile per workgroup of 4 waves (64x64 each, 2x2 MFMA
-// f32_32x32x16_f16 tiles), BK = 64.  Activations are staged to LDS as is; the
+// f32_32x32x16_f16 tiles), BK = 64; from M = 256 a 256x128 tile of 8 waves.  Activations are staged to LDS as is; the
 // packed weights are dequantised by (u - z) * s in fp16 (the exact fp16 values
 // of the reference's pseudo-quantized weight) into LDS.  Double-buffered LDS and
 // D + 1 register stages of K tiles in flight (the LDS-only barriers leave them
@@ -723,18 +723,23 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
 constexpr int kPBM = 128, kPBN = 128, kPBK = 64, kPLD = kPBK + 8;  // row stride in halves
 constexpr int kPrefillStages = 4;  // register stages of K tiles
 
-template <int D>
-__global__ __launch_bounds__(256) void w4a16_prefill_kernel(
+// NTH = 512: a 256 x 128 tile of 8 waves (4 x 2 of 64 x 64): the weight tile is dequantised
+// once per 256 rows, each thread two of its words.
+template <int D, int NTH = 256>
+__global__ __launch_bounds__(NTH) void w4a16_prefill_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups, int gs,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
-  __shared__ __attribute__((aligned(16))) uint16_t sa[2][kPBM * kPLD];
+  constexpr int BM = NTH / 2;         // 64 rows per wave pair
+  constexpr int BW = 1024 / NTH;      // weight words per thread per K tile (a row holds 8)
+  constexpr int TPR = 8 / BW;         // threads per weight row
+  __shared__ __attribute__((aligned(16))) uint16_t sa[2][BM * kPLD];
   __shared__ __attribute__((aligned(16))) uint16_t sb[2][kPBN * kPLD];
   constexpr uint32_t kOob = 0x80000000u;  // past every descriptor (sizes < 2^31, host check)
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * kPBM, n0 = blockIdx.x * kPBN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kPBN;
   const int kw = k >> 3;
 
   // A staging: 128 rows x 64 halves = 1024 chunks of 16 B, 4 per thread
@@ -743,17 +748,17 @@ __global__ __launch_bounds__(256) void w4a16_prefill_kernel(
   uint32_t aoff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int c = tid + i * 256;
+    const int c = tid + i * NTH;
     const int m = m0 + (c >> 3);
     aoff[i] = m < m_rows ? (static_cast<uint32_t>(m) * static_cast<uint32_t>(k) + (c & 7) * 8) * 2 : kOob;
   }
-  const int brow = tid >> 1, bhalf = tid & 1;  // each thread: 4 words = 32 columns
+  const int brow = tid / TPR, bhalf = tid % TPR;  // each thread: BW words = 8 BW columns
   const int bn = n0 + brow < n_cols ? n0 + brow : n_cols - 1;
-  const uint32_t *bsrc = wq + static_cast<int64_t>(bn) * kw + 4 * bhalf;
+  const uint32_t *bsrc = wq + static_cast<int64_t>(bn) * kw + BW * bhalf;
   const uint16_t *zsrc = zr ? zr : sc;  // (no zeros: the scale is read again and 8 used)
 
   uint4 areg[D + 1][4];
-  uint4 breg[D + 1];
+  uint32_t breg[D + 1][BW];
   uint32_t sz[D + 1];  // scale bits | zero bits << 16 of the thread's 32 columns
   const int nkt = k / kPBK;
   auto load_tile = [&](int set, int kt) {
@@ -762,14 +767,20 @@ __global__ __launch_bounds__(256) void w4a16_prefill_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       areg[set][i] = __builtin_bit_cast(uint4, mp_buf_load16i(xr, aoff[i] + static_cast<uint32_t>(kb) * 2, 0));
-    breg[set] = *reinterpret_cast<const uint4 *>(bsrc + kb / 8);
-    const int64_t gi = static_cast<int64_t>(bn) * n_groups + (kb + 32 * bhalf) / gs;
+    if constexpr (BW == 4) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(bsrc + kb / 8);
+      breg[set][0] = v.x; breg[set][1] = v.y; breg[set][2] = v.z; breg[set][3] = v.w;
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2 *>(bsrc + kb / 8);
+      breg[set][0] = v.x; breg[set][1] = v.y;
+    }
+    const int64_t gi = static_cast<int64_t>(bn) * n_groups + (kb + 8 * BW * bhalf) / gs;
     sz[set] = static_cast<uint32_t>(sc[gi]) | (static_cast<uint32_t>(zsrc[gi]) << 16);
   };
   auto store_tile = [&](int set, int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = tid + i * 256;
+      const int c = tid + i * NTH;
       const int r = c >> 3, cc = c & 7;
       *reinterpret_cast<uint4 *>(&sa[buf][r * kPLD + cc * 8]) = areg[set][i];
     }
@@ -777,10 +788,9 @@ __global__ __launch_bounds__(256) void w4a16_prefill_kernel(
     const float bz = zr ? mp_h2f(static_cast<uint16_t>(sz[set] >> 16)) : 8.0f;
     const __half2 off = __float2half2_rn(1024.0f + bz);
     const __half2 s2 = __float2half2_rn(mp_h2f(static_cast<uint16_t>(sz[set] & 0xFFFFu)));
-    const uint32_t wsel[4] = {breg[set].x, breg[set].y, breg[set].z, breg[set].w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t w = wsel[q];
+    for (int q = 0; q < BW; ++q) {
+      const uint32_t w = breg[set][q];
       uint32_t t[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -789,7 +799,7 @@ __global__ __launch_bounds__(256) void w4a16_prefill_kernel(
         t[j] = __builtin_bit_cast(uint32_t, h);
       }
       const uint4 nat = magic_to_natural(t[0], t[1], t[2], t[3]);
-      *reinterpret_cast<uint4 *>(&sb[buf][brow * kPLD + bhalf * 32 + q * 8]) = nat;
+      *reinterpret_cast<uint4 *>(&sb[buf][brow * kPLD + bhalf * 8 * BW + q * 8]) = nat;
     }
   };
 
@@ -1231,6 +1241,14 @@ static int mp_batch_min_m() {
   return v;
 }
 
+// Prefill GEMM workgroup: 256 x 128 tiles of 8 waves from M = 256 (measured 8-13% faster than
+// 128 x 128 tiles of 4 waves on the 7B linears at M = 2048); MP_W4_PREFILL_THREADS=256 selects the
+// smaller tile (for measurements).
+static int mp_prefill_threads() {
+  static const int v = getenv("MP_W4_PREFILL_THREADS") ? atoi(getenv("MP_W4_PREFILL_THREADS")) : 512;
+  return v;
+}
+
 // ====================================================================== C ABI
 
 extern "C" int mp_w4_quantize_awq(const void *w, int64_t n, int64_t k, int group_size, int zero_point,
@@ -1636,9 +1654,16 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
 #undef MP_W4_DEC
   } else if (m > 64 && k % kPBK == 0 && group_size % 32 == 0 && aligned && m * k * 2 < (int64_t(1) << 31) &&
              m * n * 2 < (int64_t(1) << 31)) {
-    const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, kPBM)));
-    hipLaunchKernelGGL(w4a16_prefill_kernel<kPrefillStages - 1>, grid, dim3(256), 0, s, xp, static_cast<int>(m),
-                       static_cast<int>(k), wp, static_cast<int>(n), sp, zp, n_groups, group_size, bp, yp);
+    if (mp_prefill_threads() == 512 && m >= 256) {
+      const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, 256)));
+      hipLaunchKernelGGL((w4a16_prefill_kernel<kPrefillStages - 1, 512>), grid, dim3(512), 0, s, xp,
+                         static_cast<int>(m), static_cast<int>(k), wp, static_cast<int>(n), sp, zp, n_groups,
+                         group_size, bp, yp);
+    } else {
+      const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, kPBM)));
+      hipLaunchKernelGGL(w4a16_prefill_kernel<kPrefillStages - 1>, grid, dim3(256), 0, s, xp, static_cast<int>(m),
+                         static_cast<int>(k), wp, static_cast<int>(n), sp, zp, n_groups, group_size, bp, yp);
+    }
   } else {
     hipLaunchKernelGGL(w4a16_simple_kernel, dim3(static_cast<unsigned>(mp_cdiv(m * n, 256))), dim3(256), 0, s,
                        xp, m, k, wp, n, mp_cdiv(k, 8), sp, zp, n_groups, group_size, bp, yp);
