@@ -1656,9 +1656,15 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
              m * n * 2 < (int64_t(1) << 31)) {
     if (mp_prefill_threads() == 512 && m >= 256) {
       const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, 256)));
-      hipLaunchKernelGGL((w4a16_prefill_kernel<kPrefillStages - 1, 512>), grid, dim3(512), 0, s, xp,
-                         static_cast<int>(m), static_cast<int>(k), wp, static_cast<int>(n), sp, zp, n_groups,
-                         group_size, bp, yp);
+#define MP_W4_PF512(D_)                                                                                      \
+  hipLaunchKernelGGL((w4a16_prefill_kernel<D_, 512>), grid, dim3(512), 0, s, xp, static_cast<int>(m),         \
+                     static_cast<int>(k), wp, static_cast<int>(n), sp, zp, n_groups, group_size, bp, yp)
+      const int st = getenv("MP_W4_PREFILL_STAGES") ? atoi(getenv("MP_W4_PREFILL_STAGES")) : kPrefillStages;
+      if (st == 2) MP_W4_PF512(1);
+      else if (st == 3) MP_W4_PF512(2);
+      else if (st == 5) MP_W4_PF512(4);
+      else MP_W4_PF512(kPrefillStages - 1);
+#undef MP_W4_PF512
     } else {
       const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, kPBM)));
       hipLaunchKernelGGL(w4a16_prefill_kernel<kPrefillStages - 1>, grid, dim3(256), 0, s, xp, static_cast<int>(m),
