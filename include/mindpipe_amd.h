@@ -238,6 +238,11 @@ int mp_decode_rope_attention(const void *qkv, int64_t batch, int nh, int kvh, in
                              int splits, float scale, void *out, void *workspace, size_t workspace_bytes,
                              mp_stream_t stream);
 
+/* idx [rows] int64 = the first index of the maximum of each row of x [rows, n] fp16 (a NaN
+ * counts as the maximum): the greedy sampling step of the decode harness, torch.argmax's
+ * rules.  No counterpart in the reference. */
+int mp_argmax_rows(const void *x, int64_t rows, int64_t n, int64_t *idx, mp_stream_t stream);
+
 /* act [rows, I] = round(round(silu(gate)) * up) of gate_up [rows, 2I] (gate | up), fp16. */
 int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, mp_stream_t stream);
 

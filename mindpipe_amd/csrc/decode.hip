@@ -10,6 +10,8 @@
 // (the fused qkv W4A16 output); KV cache per layer K, V [B, kvh, T, 128] fp16
 // (one 256-byte row per position).  The current position is read from device
 // memory, so every launch has a fixed shape and a step can be graph-captured.
+#include <climits>
+
 #include "mp_common.h"
 
 namespace {
@@ -577,6 +579,56 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
   *o2 = static_cast<uint32_t>(mp_f2h(n0 / den)) | (static_cast<uint32_t>(mp_f2h(n1 / den)) << 16);
 }
 
+// ---------------------------------------------------------------- row argmax
+// Greedy sampling of the decode step: idx[r] = the first index of the maximum of row r
+// of x [rows, n] fp16 (torch.argmax's rules: the lowest index among equal maxima, and a
+// NaN counts as the maximum).  One 1024-thread workgroup per row: each thread keeps the
+// best (value, index) of a strided slice, then wave and workgroup reductions.
+__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const uint16_t *__restrict__ x, int n,
+                                                          int64_t *__restrict__ idx) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const uint16_t *row = x + static_cast<int64_t>(blockIdx.x) * n;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float bv = -INFINITY;
+  int bi = INT_MAX;
+  for (int i = threadIdx.x; i < n; i += 1024) {
+    const float v = mp_h2f(row[i]);
+    if (am_better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  auto reduce = [&](int width) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      if (o >= width) continue;
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (am_better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+  };
+  reduce(64);
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  bv = lane < 16 ? sv[lane] : -INFINITY;
+  bi = lane < 16 ? si[lane] : INT_MAX;
+  reduce(16);
+  if (lane == 0) idx[blockIdx.x] = bi;
+}
+
 // ---------------------------------------------------------------- SiLU * up
 // gu [B, 2I] (gate | up) -> act [B, I] = round(round(silu(gate)) * up).
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ gu, int inter, int64_t total,
@@ -702,6 +754,16 @@ extern "C" int mp_decode_rope_attention(const void *qkv, int64_t batch, int nh, 
                                         void *workspace, size_t workspace_bytes, mp_stream_t stream) {
   return launch_decode_attention(true, qkv, batch, nh, kvh, head_dim, cos_t, sin_t, k_cache, v_cache, pos, capacity,
                                  splits, scale, out, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int mp_argmax_rows(const void *x, int64_t rows, int64_t n, int64_t *idx, mp_stream_t stream) {
+  if (!x || !idx) return MP_ERR_ARG;
+  if (rows < 0 || rows > UINT32_MAX || n <= 0 || n > INT32_MAX - 1024) return MP_ERR_SHAPE;
+  if (rows == 0) return MP_OK;
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(1024), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t *>(x), static_cast<int>(n), idx);
+  MP_CHECK_LAUNCH();
+  return MP_OK;
 }
 
 extern "C" int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, mp_stream_t stream) {

@@ -236,7 +236,7 @@ class W4Decoder:
             act, x = norm_linear(l["o"](att.reshape(b, nh * hd)), x, l["ln2"], l["gate_up"], swiglu=True)
             delta = l["down"](act)
         logits, x = norm_linear(delta, x, self.norm, self.lm_head)
-        return logits if return_logits else logits.argmax(-1)
+        return logits if return_logits else ops.argmax_rows(logits)
 
     @torch.no_grad()
     def decode_step_torch(self, tokens, cur_len, return_logits=False):

@@ -480,6 +480,17 @@ def decode_rope_attention(qkv: torch.Tensor, nh: int, kvh: int, cos_t: torch.Ten
     return out
 
 
+def argmax_rows(x: torch.Tensor) -> torch.Tensor:
+    """``x.argmax(-1)`` of fp16 ``x [rows, n]`` (first index of the maximum; NaN counts as the
+    maximum), int64 ``[rows]``: the decode step's greedy sampling in one launch."""
+    _need(x, "x", torch.float16, 2)
+    rows, n = x.shape
+    out = torch.empty(rows, dtype=torch.int64, device=x.device)
+    with _dev(x):
+        _lib.check(_lib.load().mp_argmax_rows(x.data_ptr(), rows, n, out.data_ptr(), _stream()), "mp_argmax_rows")
+    return out
+
+
 def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``round(round(silu(gate)) * up)`` of ``gate_up [B, 2I]`` (gate | up), fp16."""
     _need(gate_up, "gate_up", torch.float16, 2)

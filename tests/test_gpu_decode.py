@@ -259,3 +259,19 @@ def test_decoder_one_row_step_fused_norm():
     model.k_cache.copy_(kc); model.v_cache.copy_(vc)
     lt = model.decode_step_torch(tok, cur, return_logits=True)
     assert _rel(lf.float(), lt.float()) <= 2e-2
+
+
+@pytest.mark.parametrize("rows,n", [(1, 32000), (8, 128256), (3, 1), (5, 1500)])
+def test_argmax_rows_matches_torch(rows, n):
+    """Row argmax equals torch.argmax, including ties (first index), all -inf rows and NaN."""
+    _say("argmax_rows", rows, n)
+    from mindpipe_amd import ops
+    g = torch.Generator(device=DEV).manual_seed(rows * 7 + n)
+    x = torch.randn(rows, n, device=DEV, generator=g).half()
+    if n > 100:
+        x[0, 17] = 30.0
+        x[0, n - 5] = 30.0                      # tie: the lower index wins
+    if rows > 2:
+        x[1] = float("-inf")                     # all equal: index 0
+        x[2, n // 2] = float("nan")              # NaN counts as the maximum
+    assert torch.equal(ops.argmax_rows(x), torch.argmax(x, dim=-1))
