@@ -1428,7 +1428,9 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
   // batched kernel: NT/2 gate tiles paired with NT/2 up tiles per wave
   const int mt = mp_batch_part_mt(m);
   const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
-  int nt = half >= 8192 && mt < 4 ? 4 : 2;  // 64-row tiling: 2 (registers)
+  // column tiles per wave: 4 for 17..32 rows from I = 8192, else 2 (<= 16 rows: measured on the
+  // 7B gate/up at M = 8, 17.4 -> 16.3 us; the 64-row tiling: registers)
+  int nt = half >= 8192 && mt == 2 ? 4 : 2;
   if (mp_batch_env(0) >= 2) nt = mp_batch_env(0) >= 4 ? 4 : 2;
   const int smax = mt * nt >= 8 ? 4 : 8;
   const int nblk = ki / 128;
