@@ -470,7 +470,7 @@ __global__ __launch_bounds__(512) void w4a16_decode_kernel(
 // join makes the compiler wait for every outstanding load).  Each block pair's
 // activation loads are issued before the next pair's weight prefetch, so a
 // compute step waits for its own data only.
-template <int MT, int NT, int S, bool ZP, bool SWI = false>
+template <int MT, int NT, int S, bool ZP, bool SWI = false, bool XDB_ON = true>
 __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
@@ -478,6 +478,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   constexpr int U = 2;        // blocks per prefetch buffer
   constexpr int STEP = 8;     // blocks per scale / zero vector
   constexpr int XI = 4 * MT;  // activation loads per block (4 rows x 256 bytes each)
+  constexpr bool XDB = MT == 1 && XDB_ON;  // double-buffered activations (registers allow it at 16 rows)
   __shared__ float red[S > 1 ? S : 1][MT * NT * 4][64];
   __shared__ uint4 xst[S][16 * MT * 16];  // per wave: one block of 16 MT rows x 256 bytes
   const int lane = threadIdx.x & 63;
@@ -556,12 +557,14 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
       for (int j = 0; j < NT; ++j) w[u][j] = mp_buf_load16(wr, woff[j], woffs(b0 + u));
   };
   uint4 xa[U][XI];
-  auto load_x = [&](int b0) {
+  uint4 xb[XDB ? U : 1][XDB ? XI : 1];  // second activation buffer (XDB)
+  auto load_x_to = [&](uint4 (*xbuf)[XI], int b0) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int i = 0; i < XI; ++i) xa[u][i] = mp_buf_load16(xr, xoff[i], xoffs(b0 + u));
+      for (int i = 0; i < XI; ++i) xbuf[u][i] = mp_buf_load16(xr, xoff[i], xoffs(b0 + u));
   };
+  auto load_x = [&](int b0) { load_x_to(xa, b0); };
   // scale / zero vectors (groups b0 .. b0+7 of each tile row; 4-byte aligned rows)
   uint4 sv[NT], zv[NT];
   auto load_sz = [&](int b0) {
@@ -572,8 +575,8 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
       if (ZP) zv[j] = mp_buf_load16(zrr, soff[j], so);
     }
   };
-  // pair p (0..3) of the current step
-  auto compute = [&](uint4 (*w)[NT], int p) {
+  // a block pair: weights w, activations xbuf, scale / zero words sw / zw of each tile
+  auto compute_x = [&](uint4 (*w)[NT], uint4 (*xbuf)[XI], const uint32_t (&swd)[NT], const uint32_t (&zwd)[NT]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       // transpose through the wave's LDS region into the MFMA layout (lane (m, kq), piece q
@@ -584,7 +587,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
 #pragma unroll
       for (int i = 0; i < XI; ++i) {
         const int r = 4 * i + (lane >> 4);
-        xsw[r * 16 + ((lane & 15) ^ (r & 15))] = xa[u][i];
+        xsw[r * 16 + ((lane & 15) ^ (r & 15))] = xbuf[u][i];
       }
       h8_t af[MT][4];
       f4_t cs[MT];
@@ -600,8 +603,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
       }
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
-        const uint32_t sw = p == 0 ? sv[j].x : (p == 1 ? sv[j].y : (p == 2 ? sv[j].z : sv[j].w));
-        const uint32_t zw = p == 0 ? zv[j].x : (p == 1 ? zv[j].y : (p == 2 ? zv[j].z : zv[j].w));
+        const uint32_t sw = swd[j], zw = zwd[j];
         const float su = mp_h2f(static_cast<uint16_t>(sw >> (16 * u)));
         const float zu = 1024.0f + (ZP ? mp_h2f(static_cast<uint16_t>(zw >> (16 * u))) : 8.0f);
         const uint32_t wsel[4] = {w[u][j].x, w[u][j].y, w[u][j].z, w[u][j].w};
@@ -619,11 +621,62 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
       }
     }
   };
+  // the scale / zero words of pair p (0..3) of the current step
+  auto words = [&](int p, uint32_t (&swd)[NT], uint32_t (&zwd)[NT]) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      swd[j] = p == 0 ? sv[j].x : (p == 1 ? sv[j].y : (p == 2 ? sv[j].z : sv[j].w));
+      zwd[j] = p == 0 ? zv[j].x : (p == 1 ? zv[j].y : (p == 2 ? zv[j].z : zv[j].w));
+    }
+  };
+  auto compute = [&](uint4 (*w)[NT], int p) {
+    uint32_t swd[NT], zwd[NT];
+    words(p, swd, zwd);
+    compute_x(w, xa, swd, zwd);
+  };
 
   // Steps of 4 block pairs, fully unrolled inside: each prefetch is used in the
   // basic block that issues it; scheduling barriers keep every group of loads
   // where it is written.  Dead blocks (past nblk) read zeros: zero scale, no
   // contribution.
+  if constexpr (XDB) {
+    // activations one pair ahead in two buffers, the next step's scales during the
+    // current step's last pair (its words copied out first): a pair waits only for loads
+    // issued a pair or more before it
+    issue_w(wa, lo);
+    load_x_to(xa, lo);
+    load_sz(lo);
+    for (int st = 0; st < nsteps; ++st) {
+      const int b = lo + st * STEP;
+      uint32_t swd[NT], zwd[NT];
+      load_x_to(xb, b + 2);
+      issue_w(wb, b + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      words(0, swd, zwd);
+      compute_x(wa, xa, swd, zwd);
+      __builtin_amdgcn_sched_barrier(0);
+      load_x_to(xa, b + 4);
+      issue_w(wa, b + 4);
+      __builtin_amdgcn_sched_barrier(0);
+      words(1, swd, zwd);
+      compute_x(wb, xb, swd, zwd);
+      __builtin_amdgcn_sched_barrier(0);
+      load_x_to(xb, b + 6);
+      issue_w(wb, b + 6);
+      __builtin_amdgcn_sched_barrier(0);
+      words(2, swd, zwd);
+      compute_x(wa, xa, swd, zwd);
+      __builtin_amdgcn_sched_barrier(0);
+      words(3, swd, zwd);
+      const int nb = st + 1 < nsteps ? b + STEP : nblk;  // past the range: reads nothing
+      load_x_to(xa, nb);
+      issue_w(wa, nb);
+      load_sz(nb);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_x(wb, xb, swd, zwd);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
   issue_w(wa, lo);
   for (int st = 0; st < nsteps; ++st) {
     const int b = lo + st * STEP;
@@ -652,6 +705,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     __builtin_amdgcn_sched_barrier(0);
     compute(wb, 3);
     __builtin_amdgcn_sched_barrier(0);
+  }
   }
 
   // biases of the lane's NO output columns (col0 + 16 j + lane % 16), read before any
@@ -1221,6 +1275,12 @@ static int mp_batch_env(int which) {
   return v[which];
 }
 
+// Double-buffered activations at <= 16 rows (MP_W4_BATCH_XDB=0 turns them off, for measurements).
+static bool mp_batch_xdb() {
+  static const bool v = !(getenv("MP_W4_BATCH_XDB") && atoi(getenv("MP_W4_BATCH_XDB")) == 0);
+  return v;
+}
+
 // Row tiling of the batched kernel: MT 16-row tiles per wave, and parts = ceil(M / 16 MT)
 // workgroups per column group when M exceeds them.  Default: MT = 1 up to 16 rows, 2 above
 // (33..64 rows in two parts).  MP_W4_BATCH_PART_MT=1 / 2 / 4 fixes MT (for measurements).
@@ -1428,6 +1488,7 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
   // batched kernel: NT/2 gate tiles paired with NT/2 up tiles per wave
   const int mt = mp_batch_part_mt(m);
   const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
+  const bool xdb = mp_batch_xdb();
   // column tiles per wave: 4 for 17..32 rows from I = 8192, else 2 (<= 16 rows: measured on the
   // 7B gate/up at M = 8, 17.4 -> 16.3 us; the 64-row tiling: registers)
   int nt = half >= 8192 && mt == 2 ? 4 : 2;
@@ -1445,12 +1506,18 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
   const int hv = parts;
 #define MP_W4_BSWI(MT_, NT_, S_)                                                                              \
   do {                                                                                                       \
-    if (zp)                                                                                                  \
+    if (zp && (xdb || MT_ != 1))                                                                             \
       hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki,  \
                          wp, ni, sp, zp, n_groups, bp, yp, hv);                                              \
-    else                                                                                                     \
+    else if (xdb || MT_ != 1)                                                                                \
       hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, \
                          wp, ni, sp, zp, n_groups, bp, yp, hv);                                              \
+    else if (zp)                                                                                             \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, true, false>), grid, dim3(S_ * 64), 0, s, xp, mi, \
+                         ki, wp, ni, sp, zp, n_groups, bp, yp, hv);                                          \
+    else                                                                                                     \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, true, false>), grid, dim3(S_ * 64), 0, s, xp,   \
+                         mi, ki, wp, ni, sp, zp, n_groups, bp, yp, hv);                                      \
   } while (0)
 #define MP_W4_BSWI_S(MT_, NT_)                                                  \
   do {                                                                          \
@@ -1552,6 +1619,7 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     const int nblk = ki / 128;
     const int mt = mp_batch_part_mt(m);
     const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
+    const bool xdb = mp_batch_xdb();
     // column tiles per wave (measured on the 7B decode shapes, M = 8..64): one for N <= 4096
     // (enough workgroups), four from N = 12288 (activation loads shared by more tiles); the
     // 64-row tiling takes at most 2 (registers)
@@ -1571,12 +1639,18 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     const int hv = parts;
 #define MP_W4_BATCH(MT_, NT_, S_)                                                                            \
   do {                                                                                                       \
-    if (zp)                                                                                                  \
+    if (zp && (xdb || MT_ != 1))                                                                             \
       hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, wp, \
                          ni, sp, zp, n_groups_i, bp, yp, hv);                                                \
-    else                                                                                                     \
+    else if (xdb || MT_ != 1)                                                                                \
       hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, wp, \
                          ni, sp, zp, n_groups_i, bp, yp, hv);                                                \
+    else if (zp)                                                                                             \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, false, false>), grid, dim3(S_ * 64), 0, s, xp,  \
+                         mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                    \
+    else                                                                                                     \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, false, false>), grid, dim3(S_ * 64), 0, s, xp, \
+                         mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                    \
   } while (0)
 #define MP_W4_BATCH_S(MT_, NT_)                    \
   do {                                             \
