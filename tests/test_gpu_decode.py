@@ -90,7 +90,10 @@ def test_decode_attention_matches_fp32(b, nh, kvh, cap, pos, splits):
 
 @pytest.mark.parametrize("b,nh,kvh,cap,pos,splits", [(1, 4, 4, 300, 0, 8), (2, 8, 2, 300, 299, 1),
                                                      (3, 8, 1, 257, 130, 5), (1, 32, 32, 2304, 2047, 32),
-                                                     (1, 64, 8, 4096, 4000, 100), (2, 16, 2, 640, 64, 10)])
+                                                     (1, 64, 8, 4096, 4000, 100), (2, 16, 2, 640, 64, 10),
+                                                     # head groups on MFMA: two 64-position steps, the
+                                                     # appended row in the second
+                                                     (1, 32, 4, 1024, 1000, 8), (2, 32, 8, 512, 383, 4)])
 def test_decode_rope_attention_equals_two_launch_path(b, nh, kvh, cap, pos, splits):
     """The fused RoPE + append + attention launch writes the same cache rows and the
     same output bits as rope_append followed by attention (one kernel body)."""
