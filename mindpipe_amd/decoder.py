@@ -10,8 +10,8 @@ W4A16 GEMM each (row concatenation of the packed weight is exact).
 ``decode_step`` runs one greedy step as 7-8 launches per layer: fused residual-add
 + RMSNorm, the W4A16 GEMVs, split-K decode attention with RoPE and the KV append
 fused in (plus the split merge), and the gate/up GEMV with SiLU-mul in its epilogue.
-With one row (and hidden 2048 / 4096 / 8192) each add-RMSNorm runs in the prologue
-of the GEMV that consumes it: 6 launches per layer.
+With one row (and hidden 2048 / 4096) each add-RMSNorm runs in the prologue of the
+GEMV that consumes it: 6 launches per layer.
 The KV cache has a fixed capacity ``[L, B, kvh, T, 128]`` and every kernel reads
 the current position from device memory, so a step is shape-static and can be
 captured into a HIP graph.  ``decode_step_torch`` is the same step in PyTorch ops
@@ -212,8 +212,9 @@ class W4Decoder:
         splits, ws = self._attn_workspace(b)
         scale = 1.0 / math.sqrt(hd)
         x = self.embed[tokens]                                    # [B, H] residual stream
-        # one row with a supported width: each add-RMSNorm runs inside the next GEMV
-        fused = self.fuse_norm and b == 1 and cfg.hidden in (2048, 4096, 8192) and cfg.group == 128
+        # one row of width <= 4096: each add-RMSNorm runs inside the next GEMV (at 8192 every
+        # workgroup's 48 KB prologue costs more than the launch it saves: 70B 9.37 -> 9.80 ms/step)
+        fused = self.fuse_norm and b == 1 and cfg.hidden in (2048, 4096) and cfg.group == 128
 
         def norm_linear(delta, x, w, lin, swiglu=False):
             """(lin(RMSNorm(delta + x) * w), delta + x); delta None: no residual add."""
