@@ -1714,6 +1714,11 @@ static int mp_tiled_variant(int64_t k, int64_t wgs) {
   return 0;
 }
 
+static bool mp_skinny_one_chunk() {
+  static const bool v = !(getenv("MP_W8_SKINNY_ONE_CHUNK") && atoi(getenv("MP_W8_SKINNY_ONE_CHUNK")) == 0);
+  return v;
+}
+
 // Persistent large-M launch (MP_W8_PERSIST=0 turns it off, for measurements).
 static int mp_persist() {
   static int v = [] {
@@ -1870,6 +1875,9 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
     const int nblk = static_cast<int>(a.k / 64);
     int cb = (kMpXLdsBudget / mi - 16) / 64;
     cb = cb < 1 ? 1 : (cb > nblk ? nblk : cb);
+    // the whole K in one chunk when it fits 76 KB (two workgroups per CU still fit): no second
+    // activation round trip and weight-pipeline restart (MP_W8_SKINNY_ONE_CHUNK=0: off)
+    if (mp_skinny_one_chunk() && static_cast<int64_t>(mi) * (nblk * 64 + 16) + 16 <= 76 * 1024) cb = nblk;
     size_t smem = static_cast<size_t>(mi) * (cb * 64 + 16) + 16;
     const size_t red = static_cast<size_t>(nw) * mt * 1024;
     smem = smem > red ? smem : red;
