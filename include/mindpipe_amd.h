@@ -42,15 +42,20 @@ enum mp_status {
   MP_ERR_WORKSPACE = 6 /* workspace smaller than mp_*_workspace_bytes */
 };
 
-enum mp_dtype { MP_F16 = 0, MP_BF16 = 1, MP_F32 = 2 };
+/* MP_I8: int8 codes with an fp32 per-row scale (pre-quantized input; mp_moe_permute_quant only). */
+enum mp_dtype { MP_F16 = 0, MP_BF16 = 1, MP_F32 = 2, MP_I8 = 3 };
 
 /* Scale rule of the int8 quantizers.
  * MP_SCALE_FP32 : s = fp32(absmax)/127, q = rint(x/s)   (runtime npu_dynamic_quant
  *                 contract, vllm_ascend.patch:1741, and the W8 export rule with
  *                 its 1e-8 clamp).
- * MP_SCALE_FP16 : fp16 arithmetic of quantize_*_absmax (fake_quant.py:10-31):
- *                 s = h(h(max(absmax,1e-5))/127), q = rint(h(x/s)).          */
-enum mp_scale_rule { MP_SCALE_FP32 = 0, MP_SCALE_FP16 = 1 };
+ * MP_SCALE_FAKE : the arithmetic of quantize_*_absmax (fake_quant.py:10-31) in the
+ *                 input dtype r (fp16 or bf16): s = r(r(max(absmax,1e-5))/127),
+ *                 q = rint(r(x/s)).  In fp16 |q| <= 127.  In bf16 q can reach
+ *                 +-128: a row whose codes reach +128 but not -128 is stored as
+ *                 (-q, -s) (same products q*s), a row reaching both clamps +128 to
+ *                 127.  MP_SCALE_FP16 is the older name of this rule.           */
+enum mp_scale_rule { MP_SCALE_FP32 = 0, MP_SCALE_FAKE = 1, MP_SCALE_FP16 = 1 };
 
 const char *mp_strerror(int status);
 int mp_abi_version(void);
@@ -58,14 +63,14 @@ int mp_abi_version(void);
 /* ---------------------------------------------------------------- W4 (AWQ / GPTQ) */
 
 /* AWQ pseudo_quantize_tensor(w, n_bit=4, zero_point, q_group_size=g,
- * get_scale_zp=True) in fp16 arithmetic; replaces
+ * get_scale_zp=True) in the arithmetic of w's dtype (fp16 or bf16); replaces
  * algorithm/quantization/ptq/awq/source/awq/quantize/quantizer.py:63-105.
- * w fp16 [N,K].  Effective group = g if g > 0 and K % g == 0, else K (per row,
+ * w [N,K].  Effective group = g if g > 0 and K % g == 0, else K (per row,
  * quantizer.py:67-68).  Outputs: packed int32 [N, ceil(K/8)] (u = q when
- * zero_point, u = q + 8 when symmetric), scales fp16 [N, K/g_eff], zeros fp16
- * [N, K/g_eff] (zero_point only; pass NULL when symmetric), w_deq fp16 [N,K]
- * (optional, NULL to skip) = the tensor the reference returns. */
-int mp_w4_quantize_awq(const void *w, int64_t n, int64_t k, int group_size, int zero_point,
+ * zero_point, u = q + 8 when symmetric), scales [N, K/g_eff], zeros
+ * [N, K/g_eff] (zero_point only; pass NULL when symmetric), w_deq [N,K]
+ * (optional, NULL to skip) = the tensor the reference returns; all in w_dtype. */
+int mp_w4_quantize_awq(const void *w, int w_dtype, int64_t n, int64_t k, int group_size, int zero_point,
                        int32_t *packed, void *scales, void *zeros, void *w_deq, mp_stream_t stream);
 
 /* GPTQ symmetric round-to-nearest group quantizer in fp32: Quantizer.find_params
@@ -92,9 +97,10 @@ int mp_unpack_int4(const int32_t *packed, int64_t n, int64_t k, int8_t *int_weig
  * from zeros (or 8 when zeros == NULL).  Replaces the fp16 F.linear on AWQ
  * pseudo-quantized weights (quantizer.py:108-130 + the HF forward) and the
  * vLLM compressed-tensors WNA16 kernel the export targets
- * (scripts/repro/evaluate_vllm_real_int4_ppl.py:48-76).  x, bias, y fp16
- * (x_dtype MP_F16); K % 8 == 0, K % g == 0.  M <= 64 runs the streaming
- * (decode) kernel, larger M the tiled (prefill) kernel. */
+ * (scripts/repro/evaluate_vllm_real_int4_ppl.py:48-76).  x, scales, zeros, bias, y
+ * in x_dtype; K % 8 == 0, K % g == 0.  fp16: M <= 64 runs the streaming (decode)
+ * kernels, larger M the tiled (prefill) kernel.  bf16: the dequantising MFMA GEMM,
+ * each weight rounded to bf16 as the reference's pseudo-quantized weight is. */
 int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n,
                   const void *scales, const void *zeros, int group_size, const void *bias, void *y,
                   int x_dtype, mp_stream_t stream);
@@ -126,8 +132,9 @@ int mp_w4a16_gemv_rmsnorm(const void *x, const void *residual, const void *norm_
 /* Per-token dynamic symmetric int8 quant of x [M,K] (fp16/bf16/fp32).
  * MP_SCALE_FP32: replaces torch_npu.npu_dynamic_quant (vllm_ascend.patch:3950),
  *   scale fp32 [M].
- * MP_SCALE_FP16: codes of quantize_activation_per_token_absmax
- *   (fake_quant.py:22-31), scale fp16 [M] (x must be fp16). */
+ * MP_SCALE_FAKE: codes of quantize_activation_per_token_absmax
+ *   (fake_quant.py:22-31), scale [M] in x's dtype (x fp16 or bf16; signed as the
+ *   rule above stores the row). */
 int mp_quant_per_token_i8(const void *x, int64_t m, int64_t k, int x_dtype, int8_t *q, void *scale,
                           int scale_rule, mp_stream_t stream);
 
@@ -147,8 +154,9 @@ int mp_add_rms_norm_quant(const void *x, const void *residual, const void *weigh
  * MP_SCALE_FP32: quantize_weight_per_channel
  *   (scripts/repro/export_fp16_to_ascend_w8a8_dynamic_probe.py:175-195),
  *   scale_f32 [N] and scale_src [N] in the source dtype (optional).
- * MP_SCALE_FP16: quantize_weight_per_channel_absmax (fake_quant.py:10-19),
- *   scale_f32 [N] holds the fp16 scale value exactly; scale_src fp16 [N].
+ * MP_SCALE_FAKE: quantize_weight_per_channel_absmax (fake_quant.py:10-19) in the
+ *   weight dtype, scale_f32 [N] holds the (signed) scale value exactly; scale_src [N]
+ *   in the weight dtype.
  * Rows holding a non-finite value are counted into *bad_count (optional). */
 int mp_w8_quantize_per_channel(const void *w, int64_t n, int64_t k, int w_dtype, int8_t *q,
                                float *scale_f32, void *scale_src, int scale_rule, int32_t *bad_count,
@@ -161,6 +169,17 @@ int mp_w8a8_gemm(const int8_t *qx, const float *s_tok, const int8_t *w, const fl
                  const void *bias, int bias_dtype, void *y, int out_dtype, int64_t m, int64_t n,
                  int64_t k, mp_stream_t stream);
 
+/* y[M,N] = F.linear(r(qx * s_tok), r(w * s_ch), bias) in act_dtype (fp16 / bf16): the
+ * fake path of SmoothQuantLinear.forward (fake_quant.py:85-88) on the fake rule's codes
+ * (MP_SCALE_FAKE of mp_quant_per_token_i8 / mp_w8_quantize_per_channel), each operand
+ * element rounded to act_dtype as the reference's fake-quant tensors are, fp32
+ * accumulation, bias added in fp32, one rounding.  The int8 GEMM above multiplies the
+ * unrounded q * s; in bf16 (8 significant bits) that differs from the fake path by ~3e-3,
+ * so the bf16 fake-rule linear runs here.  bias in act_dtype or NULL. */
+int mp_w8a8_gemm_fake(const int8_t *qx, const float *s_tok, const int8_t *w, const float *s_ch,
+                      const void *bias, int act_dtype, void *y, int64_t m, int64_t n, int64_t k,
+                      mp_stream_t stream);
+
 /* ---------------------------------------------------------------- W8A8 MoE */
 
 /* Routing + per-token quant (replaces npu_moe_init_routing_quant,
@@ -168,12 +187,16 @@ int mp_w8a8_gemm(const int8_t *qx, const float *s_tok, const int8_t *w, const fl
  * Outputs: routed int8 [T*top_k, H] (token copies sorted by expert, stable in
  * (token, slot) order), routed_scale fp32 [T*top_k], row_of_slot int32
  * [T*top_k] (row in routed for assignment t*top_k+j), group_offsets int64
- * [E+1] (cumulative endpoints, offsets[0] = 0).  workspace >=
- * mp_moe_route_workspace_bytes(T, H, E). */
+ * [E+1] (cumulative endpoints, offsets[0] = 0).  scale_rule MP_SCALE_FP32 is the
+ * runtime rule; MP_SCALE_FAKE the act_quant of SmoothQuantPackedMoeExperts.forward
+ * (fake_quant.py:183) in x's dtype (fp16 / bf16).  x_dtype MP_I8: x is already
+ * quantized (int8 [T, H] with fp32 scales x_scale [T], the pertoken_scale input of
+ * the runtime's fused_experts, vllm_ascend.patch:4447-4468) and is routed only;
+ * x_scale is ignored otherwise.  workspace >= mp_moe_route_workspace_bytes(T, H, E). */
 size_t mp_moe_route_workspace_bytes(int64_t t, int64_t h, int n_experts);
-int mp_moe_permute_quant(const void *x, int x_dtype, int64_t t, int64_t h, const int32_t *topk_ids,
-                         int top_k, int n_experts, int8_t *routed, float *routed_scale,
-                         int32_t *row_of_slot, int64_t *group_offsets, void *workspace,
+int mp_moe_permute_quant(const void *x, int x_dtype, const float *x_scale, int64_t t, int64_t h,
+                         const int32_t *topk_ids, int top_k, int n_experts, int scale_rule, int8_t *routed,
+                         float *routed_scale, int32_t *row_of_slot, int64_t *group_offsets, void *workspace,
                          size_t workspace_bytes, mp_stream_t stream);
 
 /* GMM1 + SwiGLU + per-row requant (replaces npu_grouped_matmul_swiglu_quant,
@@ -181,25 +204,39 @@ int mp_moe_permute_quant(const void *x, int x_dtype, int64_t t, int64_t h, const
  * acceleration/custom_ops/qwen2_5_vl/aclnn_grouped_swiglu_out_bridge.cpp:157-273).
  * For routed row r of expert e: g = (Qx_r . W13_e^T) * sx_r * s13_e (fp32),
  * h = silu(g[:I]) * g[I:], then h -> int8 q_out [R, I] + fp32 s_out [R].
+ * scale_rule MP_SCALE_FP32: h in fp32, the runtime requant.  MP_SCALE_FAKE: the
+ * arithmetic of SmoothQuantPackedMoeExperts.forward (fake_quant.py:184-186) in
+ * act_dtype (fp16 / bf16): gate and up = F.linear of the fake-quant tensors
+ * (sum_k r(qx_k * sx) * r(w_k * s13), fp32 accumulation, rounded), silu(gate)
+ * rounded, the product rounded, then the fake per-token rule.
  * No limit on I (the CANN op rejects 2I > 10240, moe_mlp.py patch). */
 size_t mp_moe_gmm1_workspace_bytes(int64_t rows, int64_t inter);
 int mp_i8_gemm_swiglu_requant(const int8_t *routed, const float *routed_scale, const int8_t *w13,
                               const float *s13, const int64_t *group_offsets, int n_experts,
-                              int64_t rows, int64_t h, int64_t inter, int8_t *q_out, float *s_out,
-                              void *workspace, size_t workspace_bytes, mp_stream_t stream);
+                              int64_t rows, int64_t h, int64_t inter, int scale_rule, int act_dtype,
+                              int8_t *q_out, float *s_out, void *workspace, size_t workspace_bytes,
+                              mp_stream_t stream);
 
 /* GMM2: Y_r = (Qh_r . W2_e^T) * sh_r * s2_e -> out_dtype [R, N] (fp32 for the
  * combine).  Replaces npu_grouped_matmul with per_token_scale
- * (vllm_ascend.patch:2401-2412). */
+ * (vllm_ascend.patch:2401-2412).  scale_rule MP_SCALE_FAKE: the reference's F.linear on
+ * the fake-quant tensors instead, sum_k r(qh_k * sh) * r(w_k * s2) with r the rounding to
+ * act_dtype (fp16 / bf16), fp32 accumulation (fake_quant.py:187).  K % 64 == 0 for the
+ * runtime rule. */
 int mp_w8a8_grouped_gemm(const int8_t *q, const float *s, const int8_t *w, const float *s_w,
                          const int64_t *group_offsets, int n_experts, int64_t rows, int64_t n,
-                         int64_t k, void *y, int out_dtype, mp_stream_t stream);
+                         int64_t k, int scale_rule, int act_dtype, void *y, int out_dtype,
+                         mp_stream_t stream);
 
-/* out[t] = sum_j topk_w[t,j] * y[row_of_slot[t*top_k+j]] in fp32, rounded once
- * (replaces npu_moe_token_unpermute, vllm_ascend.patch:2415-2419).  y fp32
- * [R, H]; topk_w fp32 [T, top_k]; out fp16/bf16/fp32 [T, H]. */
+/* scale_rule MP_SCALE_FP32: out[t] = sum_j topk_w[t,j] * y[row_of_slot[t*top_k+j]]
+ * in fp32 in slot order, rounded once (replaces npu_moe_token_unpermute,
+ * vllm_ascend.patch:2415-2419).  MP_SCALE_FAKE: the index_add_ of
+ * SmoothQuantPackedMoeExperts.forward (fake_quant.py:187-189) in out_dtype r
+ * (fp16 / bf16): over the token's assignments in ascending expert order,
+ * out = r(out + r(r(y) * topk_w)).  y fp32 [R, H]; topk_w fp32 [T, top_k];
+ * out fp16/bf16/fp32 [T, H]; top_k <= 64. */
 int mp_moe_unpermute_combine(const float *y, const int32_t *row_of_slot, const float *topk_w,
-                             int64_t t, int top_k, int64_t h, void *out, int out_dtype,
+                             int64_t t, int top_k, int64_t h, int scale_rule, void *out, int out_dtype,
                              mp_stream_t stream);
 
 /* ---------------------------------------------------------------- decode-step harness kernels

@@ -11,8 +11,10 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("MINDPIPE_AMD_LIB", Path(__file__).resolve().parent / "libmindpipe_amd.so"))
 
-MP_F16, MP_BF16, MP_F32 = 0, 1, 2
-MP_SCALE_FP32, MP_SCALE_FP16 = 0, 1
+MP_F16, MP_BF16, MP_F32, MP_I8 = 0, 1, 2, 3
+MP_SCALE_FP32, MP_SCALE_FAKE = 0, 1
+MP_SCALE_FP16 = MP_SCALE_FAKE  # older name of the fake rule
+ABI_VERSION = 2
 
 _vp, _i64, _i32, _sz = C.c_void_p, C.c_int64, C.c_int, C.c_size_t
 
@@ -20,7 +22,7 @@ _vp, _i64, _i32, _sz = C.c_void_p, C.c_int64, C.c_int, C.c_size_t
 SIGNATURES = {
     "mp_strerror": (C.c_char_p, [_i32]),
     "mp_abi_version": (_i32, []),
-    "mp_w4_quantize_awq": (_i32, [_vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "mp_w4_quantize_awq": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "mp_w4_quantize_gptq_rtn": (_i32, [_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _vp]),
     "mp_pack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "mp_unpack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp]),
@@ -41,11 +43,14 @@ SIGNATURES = {
     "mp_w8_quantize_per_channel": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "mp_w8a8_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp]),
     "mp_moe_route_workspace_bytes": (_sz, [_i64, _i64, _i32]),
-    "mp_moe_permute_quant": (_i32, [_vp, _i32, _i64, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mp_moe_permute_quant": (_i32, [_vp, _i32, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _sz,
+                                    _vp]),
     "mp_moe_gmm1_workspace_bytes": (_sz, [_i64, _i64]),
-    "mp_i8_gemm_swiglu_requant": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
-    "mp_w8a8_grouped_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp]),
-    "mp_moe_unpermute_combine": (_i32, [_vp, _vp, _vp, _i64, _i32, _i64, _vp, _i32, _vp]),
+    "mp_i8_gemm_swiglu_requant": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp,
+                                         _sz, _vp]),
+    "mp_w8a8_grouped_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp]),
+    "mp_w8a8_gemm_fake": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
+    "mp_moe_unpermute_combine": (_i32, [_vp, _vp, _vp, _i64, _i32, _i64, _i32, _vp, _i32, _vp]),
 }
 
 _LIB = None
@@ -65,7 +70,7 @@ def load() -> C.CDLL:
         fn = getattr(lib, name)  # AttributeError if the symbol is missing
         fn.restype = res
         fn.argtypes = args
-    if lib.mp_abi_version() != 1:
+    if lib.mp_abi_version() != ABI_VERSION:
         raise ImportError("mindpipe_amd: ABI version mismatch")
     _LIB = lib
     return lib

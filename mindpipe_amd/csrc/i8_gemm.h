@@ -26,6 +26,7 @@ struct mp_i8_args {
   int64_t k;
   int64_t ldy;               // output row stride (elements)
   int staged_epilogue;       // large-M kernel: 16-bit outputs through LDS, 16-byte stores
+  int epi_round;             // SWIGLU: mp_round_mode of g, u, silu(g) and h (kRoundNone: fp32)
 };
 
 int mp_launch_i8_gemm(const mp_i8_args &args, int epilogue, hipStream_t stream);

@@ -2,7 +2,7 @@
 // with the per-token int8 quant, GMM1 + SwiGLU + requant, GMM2, and the
 // weighted un-permute.  The two grouped GEMMs use the tiled int8 MFMA kernel
 // of w8a8.hip with a grouped row schedule.
-#include "i8_gemm.h"
+#include "dq_gemm.h"
 
 namespace {
 
@@ -91,31 +91,20 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(const int32
   }
 }
 
-// per-token code of v with scale s (s == 0: 0), the runtime quantizer's expression
-__device__ __forceinline__ uint32_t moe_code(float v, float s) {
-  float q = (s == 0.f) ? 0.f : rintf(v / s);
-  q = fminf(fmaxf(q, -127.f), 127.f);
-  return static_cast<uint32_t>(static_cast<int>(q)) & 0xFFu;
-}
-__device__ __forceinline__ float moe_block_max(float amax, float *wmax) {
-  const int tid = threadIdx.x;
-  amax = mp_wave_max(amax);
-  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
-  __syncthreads();
-  return fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-}
-
 // Per-token quant of x[t] for routed row row_of_slot[a], 16-byte loads: the row is
-// read once for the abs-max and again (from L2) for the codes, stored 4 or 8 at a time.
+// read once for its statistics and again (from L2) for the codes, stored 4 or 8 at a time.
 // Needs h a multiple of the values per 16 bytes and 16-byte aligned rows (host check).
-template <int DT>
+// RULE: MP_SCALE_FP32 (runtime) or MP_SCALE_FAKE in DT's rounding (signed stored scale).
+template <int DT, int RULE>
 __global__ __launch_bounds__(256) void moe_permute_quant_vec_kernel(const void *__restrict__ x, int64_t h, int top_k,
                                                                    const int32_t *__restrict__ row_of_slot,
                                                                    int8_t *__restrict__ routed,
                                                                    float *__restrict__ routed_scale) {
   constexpr int N = MpChunk16<DT>::N;
   constexpr int ESZ = DT == MP_F32 ? 4 : 2;
-  __shared__ float wmax[4];
+  constexpr int MODE = DT == MP_F16 ? kRoundF16 : (DT == MP_BF16 ? kRoundBF16 : kRoundNone);
+  __shared__ float red[3][4];
+  __shared__ int wbad[4];
   const int64_t a = blockIdx.x;
   const int64_t t = a / top_k;
   const int r = row_of_slot[a];
@@ -123,16 +112,23 @@ __global__ __launch_bounds__(256) void moe_permute_quant_vec_kernel(const void *
   const int tid = threadIdx.x;
   const int64_t nch = h / N;
   const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const char *>(x) + t * h * ESZ);
-  float amax = 0.f;
+  mp_rowstat st{0.f, -INFINITY, INFINITY, 0};
   for (int64_t c = tid; c < nch; c += 256) {
     float f[N];
     mp_chunk_to_f32<DT>(src[c], f);
 #pragma unroll
-    for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(f[i]));
+    for (int i = 0; i < N; ++i) {
+      st.amax = fmaxf(st.amax, fabsf(f[i]));
+      if (RULE != MP_SCALE_FP32) {
+        st.vmax = fmaxf(st.vmax, f[i]);
+        st.vmin = fminf(st.vmin, f[i]);
+      }
+    }
   }
-  amax = moe_block_max(amax, wmax);
-  const float s = amax / 127.0f;
-  if (tid == 0) routed_scale[r] = s;
+  st = mp_block_rowstat(st, red, wbad);
+  float s, sg;
+  mp_row_scale<RULE>(st, MODE, 0.0f, s, sg);
+  if (tid == 0) routed_scale[r] = sg * s;
   int8_t *dst = routed + static_cast<int64_t>(r) * h;
   for (int64_t c = tid; c < nch; c += 256) {
     float f[N];
@@ -140,8 +136,9 @@ __global__ __launch_bounds__(256) void moe_permute_quant_vec_kernel(const void *
     uint32_t w[N / 4];
 #pragma unroll
     for (int i = 0; i < N / 4; ++i)
-      w[i] = moe_code(f[4 * i], s) | (moe_code(f[4 * i + 1], s) << 8) | (moe_code(f[4 * i + 2], s) << 16) |
-             (moe_code(f[4 * i + 3], s) << 24);
+      w[i] = mp_row_code<RULE>(f[4 * i], s, sg, MODE) | (mp_row_code<RULE>(f[4 * i + 1], s, sg, MODE) << 8) |
+             (mp_row_code<RULE>(f[4 * i + 2], s, sg, MODE) << 16) |
+             (mp_row_code<RULE>(f[4 * i + 3], s, sg, MODE) << 24);
     if constexpr (N == 8) *reinterpret_cast<uint2 *>(dst + c * 8) = make_uint2(w[0], w[1]);
     else *reinterpret_cast<uint32_t *>(dst + c * 4) = w[0];
   }
@@ -149,124 +146,175 @@ __global__ __launch_bounds__(256) void moe_permute_quant_vec_kernel(const void *
 
 // Per-token quant of x[t] written to every routed row that copies it.  One
 // workgroup per assignment; the activation row is re-read from L2 per copy.
+template <int RULE>
 __global__ __launch_bounds__(256) void moe_permute_quant_kernel(const void *__restrict__ x, int x_dtype,
                                                                int64_t h, int top_k,
                                                                const int32_t *__restrict__ row_of_slot,
                                                                int8_t *__restrict__ routed,
                                                                float *__restrict__ routed_scale) {
-  __shared__ float wmax[4];
+  __shared__ float red[3][4];
+  __shared__ int wbad[4];
   const int64_t a = blockIdx.x;
   const int64_t t = a / top_k;
   const int r = row_of_slot[a];
   if (r < 0) return;
   const int tid = threadIdx.x;
-  float amax = 0.f;
-  for (int64_t c = tid; c < h; c += 256) amax = fmaxf(amax, fabsf(mp_load_as_f32(x, t * h + c, x_dtype)));
-  amax = mp_wave_max(amax);
-  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  const float s = amax / 127.0f;
-  if (tid == 0) routed_scale[r] = s;
+  const int mode = mp_round_mode_of(x_dtype);
+  mp_rowstat st{0.f, -INFINITY, INFINITY, 0};
   for (int64_t c = tid; c < h; c += 256) {
     const float v = mp_load_as_f32(x, t * h + c, x_dtype);
-    float q = (s == 0.f) ? 0.f : rintf(v / s);
-    q = fminf(fmaxf(q, -127.f), 127.f);
-    routed[static_cast<int64_t>(r) * h + c] = static_cast<int8_t>(static_cast<int>(q));
+    st.amax = fmaxf(st.amax, fabsf(v));
+    st.vmax = fmaxf(st.vmax, v);
+    st.vmin = fminf(st.vmin, v);
+  }
+  st = mp_block_rowstat(st, red, wbad);
+  float s, sg;
+  mp_row_scale<RULE>(st, mode, 0.0f, s, sg);
+  if (tid == 0) routed_scale[r] = sg * s;
+  for (int64_t c = tid; c < h; c += 256)
+    routed[static_cast<int64_t>(r) * h + c] =
+        static_cast<int8_t>(mp_row_code<RULE>(mp_load_as_f32(x, t * h + c, x_dtype), s, sg, mode));
+}
+
+// Routing of pre-quantized input (int8 rows x_q [T, H] with fp32 scales): routed row
+// row_of_slot[a] copies token a / top_k, 16 bytes per thread-step when the rows allow it.
+template <bool VEC>
+__global__ __launch_bounds__(256) void moe_permute_rows_kernel(const int8_t *__restrict__ xq, const float *__restrict__ xs,
+                                                              int64_t h, int top_k,
+                                                              const int32_t *__restrict__ row_of_slot,
+                                                              int8_t *__restrict__ routed,
+                                                              float *__restrict__ routed_scale) {
+  const int64_t a = blockIdx.x;
+  const int64_t t = a / top_k;
+  const int r = row_of_slot[a];
+  if (r < 0) return;
+  if (threadIdx.x == 0) routed_scale[r] = xs[t];
+  if constexpr (VEC) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(xq + t * h);
+    uint4 *dst = reinterpret_cast<uint4 *>(routed + static_cast<int64_t>(r) * h);
+    for (int64_t c = threadIdx.x; c < h / 16; c += 256) dst[c] = src[c];
+  } else {
+    for (int64_t c = threadIdx.x; c < h; c += 256) routed[static_cast<int64_t>(r) * h + c] = xq[t * h + c];
   }
 }
 
-// Requant of the SwiGLU output: per routed row, abs-max over the GMM1
-// workgroups' partial maxima, then q = rint(h / (amax / 127)).
+// Requant of the SwiGLU output: per routed row, the abs-max over the GMM1 workgroups'
+// partial maxima, then the codes of the row quantizer.  The fake rule in bf16 also needs the
+// row's largest and smallest value (mp_fake_row_sign), which the partials do not carry: that
+// case reads the row once more for them (SIGNED).  VEC: 16-byte loads of the fp32 row
+// (inter % 4 == 0), four codes per store.
+template <int RULE, bool SIGNED, bool VEC>
 __global__ __launch_bounds__(256) void moe_requant_kernel(const float *__restrict__ hbuf, const float *__restrict__ part,
-                                                         int n_partial, int64_t inter, int8_t *__restrict__ q,
+                                                         int n_partial, int64_t inter, int mode, int8_t *__restrict__ q,
                                                          float *__restrict__ s_out) {
-  __shared__ float wmax[4];
+  __shared__ float red[3][4];
+  __shared__ int wbad[4];
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
-  float amax = 0.f;
-  for (int i = tid; i < n_partial; i += 256) amax = fmaxf(amax, part[r * n_partial + i]);
-  amax = mp_wave_max(amax);
-  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  const float s = amax / 127.0f;
-  if (tid == 0) s_out[r] = s;
-  for (int64_t c = tid; c < inter; c += 256) {
-    float v = (s == 0.f) ? 0.f : rintf(hbuf[r * inter + c] / s);
-    v = fminf(fmaxf(v, -127.f), 127.f);
-    q[r * inter + c] = static_cast<int8_t>(static_cast<int>(v));
+  const float *row = hbuf + r * inter;
+  mp_rowstat st{0.f, -INFINITY, INFINITY, 0};
+  if (SIGNED) {
+    for (int64_t c = tid; c < inter; c += 256) {
+      const float v = row[c];
+      st.amax = fmaxf(st.amax, fabsf(v));
+      st.vmax = fmaxf(st.vmax, v);
+      st.vmin = fminf(st.vmin, v);
+    }
+  } else {
+    for (int i = tid; i < n_partial; i += 256) st.amax = fmaxf(st.amax, part[r * n_partial + i]);
+  }
+  st = mp_block_rowstat(st, red, wbad);
+  float s, sg;
+  mp_row_scale<RULE>(st, mode, 0.0f, s, sg);
+  if (tid == 0) s_out[r] = sg * s;
+  if (VEC) {
+    const float4 *src = reinterpret_cast<const float4 *>(row);
+    uint32_t *dst = reinterpret_cast<uint32_t *>(q + r * inter);
+    for (int64_t c = tid; c < inter / 4; c += 256) {
+      const float4 v = src[c];
+      dst[c] = mp_row_code<RULE>(v.x, s, sg, mode) | (mp_row_code<RULE>(v.y, s, sg, mode) << 8) |
+               (mp_row_code<RULE>(v.z, s, sg, mode) << 16) | (mp_row_code<RULE>(v.w, s, sg, mode) << 24);
+    }
+  } else {
+    for (int64_t c = tid; c < inter; c += 256) q[r * inter + c] = static_cast<int8_t>(mp_row_code<RULE>(row[c], s, sg, mode));
   }
 }
 
-// Requant with 16-byte loads of the fp32 SwiGLU rows (inter % 4 == 0): four codes per store.
-__global__ __launch_bounds__(256) void moe_requant_vec_kernel(const float *__restrict__ hbuf,
-                                                             const float *__restrict__ part, int n_partial,
-                                                             int64_t inter, int8_t *__restrict__ q,
-                                                             float *__restrict__ s_out) {
-  __shared__ float wmax[4];
-  const int64_t r = blockIdx.x;
-  const int tid = threadIdx.x;
-  float amax = 0.f;
-  for (int i = tid; i < n_partial; i += 256) amax = fmaxf(amax, part[r * n_partial + i]);
-  amax = moe_block_max(amax, wmax);
-  const float s = amax / 127.0f;
-  if (tid == 0) s_out[r] = s;
-  const float4 *src = reinterpret_cast<const float4 *>(hbuf + r * inter);
-  uint32_t *dst = reinterpret_cast<uint32_t *>(q + r * inter);
-  for (int64_t c = tid; c < inter / 4; c += 256) {
-    const float4 v = src[c];
-    dst[c] = moe_code(v.x, s) | (moe_code(v.y, s) << 8) | (moe_code(v.z, s) << 16) | (moe_code(v.w, s) << 24);
-  }
-}
-
-// Weighted un-permute, four columns per thread (h % 4 == 0, 16-byte aligned y rows):
-// out[t, c] = sum_j w[t, j] * y[row_of_slot[t, j], c] in fp32 in slot order, one rounding.
-__global__ __launch_bounds__(256) void moe_combine_vec_kernel(const float *__restrict__ y,
-                                                             const int32_t *__restrict__ row_of_slot,
-                                                             const float *__restrict__ w, int64_t t_count,
-                                                             int top_k, int64_t h, void *__restrict__ out,
-                                                             int out_dtype) {
-  const int64_t q4 = h / 4;
+// Weighted un-permute of a token's assignments, four columns per thread (VEC: h % 4 == 0,
+// 16-byte aligned y rows) or one.
+//   FAKE = false: out[t, c] = sum_j w[t, j] * y[row_of_slot[t, j], c] in fp32 in slot order,
+//                 one rounding to out_dtype.
+//   FAKE = true : the reference's index_add_ in out_dtype r: over the assignments in
+//                 ascending expert order (= ascending routed row), out = r(out + r(r(y) * w)).
+template <bool FAKE, bool VEC>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float *__restrict__ y,
+                                                         const int32_t *__restrict__ row_of_slot,
+                                                         const float *__restrict__ w, int64_t t_count, int top_k,
+                                                         int64_t h, void *__restrict__ out, int out_dtype) {
+  constexpr int NC = VEC ? 4 : 1;
+  const int64_t per_row = h / NC;
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (tid >= t_count * q4) return;
-  const int64_t t = tid / q4, c = (tid % q4) * 4;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (tid >= t_count * per_row) return;
+  const int64_t t = tid / per_row, c = (tid % per_row) * NC;
+  const int mode = mp_round_mode_of(out_dtype);
+  float acc[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) acc[i] = 0.f;
+  int prev = -1;  // FAKE: rows are taken in ascending order, the smallest above prev each time
   for (int j = 0; j < top_k; ++j) {
-    const int r = row_of_slot[t * top_k + j];
-    if (r < 0) continue;
-    const float wj = w[t * top_k + j];
-    const float4 v = *reinterpret_cast<const float4 *>(y + static_cast<int64_t>(r) * h + c);
-    acc[0] = mp_add(acc[0], mp_mul(wj, v.x));
-    acc[1] = mp_add(acc[1], mp_mul(wj, v.y));
-    acc[2] = mp_add(acc[2], mp_mul(wj, v.z));
-    acc[3] = mp_add(acc[3], mp_mul(wj, v.w));
+    int r, slot;
+    if (FAKE) {
+      r = INT32_MAX;
+      slot = -1;
+      for (int jj = 0; jj < top_k; ++jj) {
+        const int rr = row_of_slot[t * top_k + jj];
+        if (rr > prev && rr < r) {
+          r = rr;
+          slot = jj;
+        }
+      }
+      if (slot < 0) break;
+      prev = r;
+    } else {
+      r = row_of_slot[t * top_k + j];
+      slot = j;
+      if (r < 0) continue;
+    }
+    const float wj = w[t * top_k + slot];
+    float v[NC];
+    if constexpr (VEC) {
+      const float4 y4 = *reinterpret_cast<const float4 *>(y + static_cast<int64_t>(r) * h + c);
+      v[0] = y4.x;
+      v[1] = y4.y;
+      v[2] = y4.z;
+      v[3] = y4.w;
+    } else {
+      v[0] = y[static_cast<int64_t>(r) * h + c];
+    }
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      if (FAKE)
+        acc[i] = mp_round_mode_apply(
+            mp_add(acc[i], mp_round_mode_apply(mp_mul(mp_round_mode_apply(v[i], mode), wj), mode)), mode);
+      else
+        acc[i] = mp_add(acc[i], mp_mul(wj, v[i]));
+    }
   }
   const int64_t o = t * h + c;
-  if (out_dtype == MP_F32) {
-    *reinterpret_cast<float4 *>(static_cast<float *>(out) + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  } else {
-    uint16_t b[4];
+  if constexpr (VEC) {
+    if (out_dtype == MP_F32) {
+      *reinterpret_cast<float4 *>(static_cast<float *>(out) + o) =
+          make_float4(acc[0], acc[1], acc[2], acc[3]);
+    } else {
+      uint16_t b[NC];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) b[i] = out_dtype == MP_F16 ? mp_f2h(acc[i]) : mp_f2bf(acc[i]);
-    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + o) =
-        make_uint2(b[0] | (static_cast<uint32_t>(b[1]) << 16), b[2] | (static_cast<uint32_t>(b[3]) << 16));
+      for (int i = 0; i < NC; ++i) b[i] = out_dtype == MP_F16 ? mp_f2h(acc[i]) : mp_f2bf(acc[i]);
+      *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + o) =
+          make_uint2(b[0] | (static_cast<uint32_t>(b[1]) << 16), b[2] | (static_cast<uint32_t>(b[3]) << 16));
+    }
+  } else {
+    mp_store_from_f32(out, o, out_dtype, acc[0]);
   }
-}
-
-__global__ void moe_combine_kernel(const float *__restrict__ y, const int32_t *__restrict__ row_of_slot,
-                                   const float *__restrict__ w, int64_t t_count, int top_k, int64_t h,
-                                   void *__restrict__ out, int out_dtype) {
-  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (tid >= t_count * h) return;
-  const int64_t t = tid / h, c = tid % h;
-  float acc = 0.f;
-  for (int j = 0; j < top_k; ++j) {
-    const int r = row_of_slot[t * top_k + j];
-    if (r < 0) continue;
-    acc = mp_add(acc, mp_mul(w[t * top_k + j], y[static_cast<int64_t>(r) * h + c]));
-  }
-  mp_store_from_f32(out, tid, out_dtype, acc);
 }
 
 }  // namespace
@@ -280,12 +328,15 @@ extern "C" size_t mp_moe_route_workspace_bytes(int64_t t, int64_t h, int n_exper
   return 256;  // invalid-id counter (kept for future multi-workgroup routing)
 }
 
-extern "C" int mp_moe_permute_quant(const void *x, int x_dtype, int64_t t, int64_t h, const int32_t *topk_ids,
-                                    int top_k, int n_experts, int8_t *routed, float *routed_scale,
-                                    int32_t *row_of_slot, int64_t *group_offsets, void *workspace,
+extern "C" int mp_moe_permute_quant(const void *x, int x_dtype, const float *x_scale, int64_t t, int64_t h,
+                                    const int32_t *topk_ids, int top_k, int n_experts, int scale_rule, int8_t *routed,
+                                    float *routed_scale, int32_t *row_of_slot, int64_t *group_offsets, void *workspace,
                                     size_t workspace_bytes, mp_stream_t stream) {
   if (!x || !topk_ids || !routed || !routed_scale || !row_of_slot || !group_offsets) return MP_ERR_ARG;
-  if (x_dtype != MP_F16 && x_dtype != MP_BF16 && x_dtype != MP_F32) return MP_ERR_DTYPE;
+  if (x_dtype != MP_F16 && x_dtype != MP_BF16 && x_dtype != MP_F32 && x_dtype != MP_I8) return MP_ERR_DTYPE;
+  if (x_dtype == MP_I8 && !x_scale) return MP_ERR_ARG;
+  if (scale_rule != MP_SCALE_FP32 && scale_rule != MP_SCALE_FAKE) return MP_ERR_ARG;
+  if (scale_rule == MP_SCALE_FAKE && x_dtype == MP_F32) return MP_ERR_DTYPE;
   if (t < 0 || h <= 0 || top_k <= 0 || n_experts <= 0 || n_experts > kMaxExperts) return MP_ERR_SHAPE;
   if (t * top_k > INT32_MAX) return MP_ERR_SHAPE;
   if (workspace && workspace_bytes < mp_moe_route_workspace_bytes(t, h, n_experts)) return MP_ERR_WORKSPACE;
@@ -295,21 +346,40 @@ extern "C" int mp_moe_permute_quant(const void *x, int x_dtype, int64_t t, int64
                      row_of_slot, static_cast<int32_t *>(workspace));
   MP_CHECK_LAUNCH();
   if (n_assign == 0) return MP_OK;
-  const int per16 = x_dtype == MP_F32 ? 4 : 8;  // values per 16 bytes
-  if (h % per16 == 0 && mp_aligned(x, 16) && mp_aligned(routed, 8)) {
-    const dim3 g(static_cast<unsigned>(n_assign));
-    if (x_dtype == MP_F16)
-      hipLaunchKernelGGL(moe_permute_quant_vec_kernel<MP_F16>, g, dim3(256), 0, s, x, h, top_k, row_of_slot, routed,
-                         routed_scale);
-    else if (x_dtype == MP_BF16)
-      hipLaunchKernelGGL(moe_permute_quant_vec_kernel<MP_BF16>, g, dim3(256), 0, s, x, h, top_k, row_of_slot, routed,
+  const dim3 g(static_cast<unsigned>(n_assign));
+  if (x_dtype == MP_I8) {  // pre-quantized rows: routing only
+    const int8_t *xq = static_cast<const int8_t *>(x);
+    if (h % 16 == 0 && mp_aligned(x, 16) && mp_aligned(routed, 16))
+      hipLaunchKernelGGL(moe_permute_rows_kernel<true>, g, dim3(256), 0, s, xq, x_scale, h, top_k, row_of_slot, routed,
                          routed_scale);
     else
-      hipLaunchKernelGGL(moe_permute_quant_vec_kernel<MP_F32>, g, dim3(256), 0, s, x, h, top_k, row_of_slot, routed,
-                         routed_scale);
+      hipLaunchKernelGGL(moe_permute_rows_kernel<false>, g, dim3(256), 0, s, xq, x_scale, h, top_k, row_of_slot,
+                         routed, routed_scale);
+    MP_CHECK_LAUNCH();
+    return MP_OK;
+  }
+  const int per16 = x_dtype == MP_F32 ? 4 : 8;  // values per 16 bytes
+  const bool fake = scale_rule == MP_SCALE_FAKE;
+  if (h % per16 == 0 && mp_aligned(x, 16) && mp_aligned(routed, 8)) {
+#define MP_PQ_VEC(DT_, RULE_) \
+  hipLaunchKernelGGL((moe_permute_quant_vec_kernel<DT_, RULE_>), g, dim3(256), 0, s, x, h, top_k, row_of_slot, routed, \
+                     routed_scale)
+    if (x_dtype == MP_F16) {
+      if (fake) MP_PQ_VEC(MP_F16, MP_SCALE_FAKE);
+      else MP_PQ_VEC(MP_F16, MP_SCALE_FP32);
+    } else if (x_dtype == MP_BF16) {
+      if (fake) MP_PQ_VEC(MP_BF16, MP_SCALE_FAKE);
+      else MP_PQ_VEC(MP_BF16, MP_SCALE_FP32);
+    } else {
+      MP_PQ_VEC(MP_F32, MP_SCALE_FP32);
+    }
+#undef MP_PQ_VEC
+  } else if (fake) {
+    hipLaunchKernelGGL(moe_permute_quant_kernel<MP_SCALE_FAKE>, g, dim3(256), 0, s, x, x_dtype, h, top_k, row_of_slot,
+                       routed, routed_scale);
   } else {
-    hipLaunchKernelGGL(moe_permute_quant_kernel, dim3(static_cast<unsigned>(n_assign)), dim3(256), 0, s, x, x_dtype, h,
-                       top_k, row_of_slot, routed, routed_scale);
+    hipLaunchKernelGGL(moe_permute_quant_kernel<MP_SCALE_FP32>, g, dim3(256), 0, s, x, x_dtype, h, top_k, row_of_slot,
+                       routed, routed_scale);
   }
   MP_CHECK_LAUNCH();
   return MP_OK;
@@ -325,10 +395,13 @@ extern "C" size_t mp_moe_gmm1_workspace_bytes(int64_t rows, int64_t inter) {
 
 extern "C" int mp_i8_gemm_swiglu_requant(const int8_t *routed, const float *routed_scale, const int8_t *w13,
                                          const float *s13, const int64_t *group_offsets, int n_experts,
-                                         int64_t rows, int64_t h, int64_t inter, int8_t *q_out, float *s_out,
-                                         void *workspace, size_t workspace_bytes, mp_stream_t stream) {
+                                         int64_t rows, int64_t h, int64_t inter, int scale_rule, int act_dtype,
+                                         int8_t *q_out, float *s_out, void *workspace, size_t workspace_bytes,
+                                         mp_stream_t stream) {
   if (!routed || !routed_scale || !w13 || !s13 || !group_offsets || !q_out || !s_out || !workspace)
     return MP_ERR_ARG;
+  if (scale_rule != MP_SCALE_FP32 && scale_rule != MP_SCALE_FAKE) return MP_ERR_ARG;
+  if (scale_rule == MP_SCALE_FAKE && act_dtype != MP_F16 && act_dtype != MP_BF16) return MP_ERR_DTYPE;
   if (rows < 0 || h <= 0 || inter <= 0 || n_experts <= 0 || n_experts > kMaxExperts) return MP_ERR_SHAPE;
   if (h % 64 != 0 || h > (1 << 17)) return MP_ERR_SHAPE;
   if (workspace_bytes < mp_moe_gmm1_workspace_bytes(rows, inter)) return MP_ERR_WORKSPACE;
@@ -337,39 +410,102 @@ extern "C" int mp_i8_gemm_swiglu_requant(const int8_t *routed, const float *rout
   float *hbuf = static_cast<float *>(workspace);
   const size_t hbytes = static_cast<size_t>(rows) * static_cast<size_t>(inter) * sizeof(float);
   float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + ((hbytes + 255) & ~static_cast<size_t>(255)));
-  mp_i8_args a{};
-  a.a = routed;
-  a.s_a = routed_scale;
-  a.b = w13;
-  a.s_b = s13;
-  a.y = hbuf;
-  a.out_dtype = MP_F32;
-  a.amax_partial = part;
-  a.n_partial = static_cast<int>(gmm1_partials(inter));
-  a.offsets = group_offsets;
-  a.n_experts = n_experts;
-  a.rows = rows;
-  a.n = inter;
-  a.k = h;
-  a.ldy = inter;
-  int rc = mp_launch_i8_gemm(a, MP_EPI_SWIGLU, s);
+  const int mode = scale_rule == MP_SCALE_FAKE ? mp_round_mode_of(act_dtype) : kRoundNone;
+  const int n_partial = static_cast<int>(gmm1_partials(inter));
+  int rc;
+  if (scale_rule == MP_SCALE_FAKE) {
+    // the reference's F.linear on the fake-quant tensors: fp16 / bf16 MFMA on r(q * s) values
+    // (the int8 product of the unrounded q * s moves gate / up by an ulp often enough to flip
+    // requant codes: ~4e-3 of output error at Mixtral-like shapes)
+    mp_dq_args d{};
+    d.dt = act_dtype;
+    d.a = routed;
+    d.a_fmt = MP_DQ_I8ROW;
+    d.a_scale = routed_scale;
+    d.b = w13;
+    d.b_fmt = MP_DQ_I8ROW;
+    d.b_scale = s13;
+    d.y = hbuf;
+    d.out_dtype = MP_F32;
+    d.ldy = inter;
+    d.amax_partial = part;
+    d.n_partial = n_partial;
+    d.offsets = group_offsets;
+    d.n_experts = n_experts;
+    d.rows = rows;
+    d.n = inter;
+    d.k = h;
+    rc = mp_launch_dq_gemm(d, MP_EPI_SWIGLU, s);
+  } else {
+    mp_i8_args a{};
+    a.a = routed;
+    a.s_a = routed_scale;
+    a.b = w13;
+    a.s_b = s13;
+    a.y = hbuf;
+    a.out_dtype = MP_F32;
+    a.amax_partial = part;
+    a.n_partial = n_partial;
+    a.offsets = group_offsets;
+    a.n_experts = n_experts;
+    a.rows = rows;
+    a.n = inter;
+    a.k = h;
+    a.ldy = inter;
+    a.epi_round = mode;
+    rc = mp_launch_i8_gemm(a, MP_EPI_SWIGLU, s);
+  }
   if (rc != MP_OK) return rc;
-  if (inter % 4 == 0 && mp_aligned(q_out, 4) && mp_aligned(hbuf, 16))
-    hipLaunchKernelGGL(moe_requant_vec_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, hbuf, part,
-                       a.n_partial, inter, q_out, s_out);
-  else
-    hipLaunchKernelGGL(moe_requant_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, hbuf, part,
-                       a.n_partial, inter, q_out, s_out);
+  const bool vec = inter % 4 == 0 && mp_aligned(q_out, 4) && mp_aligned(hbuf, 16);
+  const dim3 g(static_cast<unsigned>(rows));
+#define MP_RQ(RULE_, SIGNED_, VEC_)                                                                              \
+  hipLaunchKernelGGL((moe_requant_kernel<RULE_, SIGNED_, VEC_>), g, dim3(256), 0, s, hbuf, part, n_partial, inter, \
+                     mode, q_out, s_out)
+  if (scale_rule == MP_SCALE_FP32) {
+    if (vec) MP_RQ(MP_SCALE_FP32, false, true);
+    else MP_RQ(MP_SCALE_FP32, false, false);
+  } else if (mode == kRoundBF16) {  // the bf16 codes reach +-128: the row's sign needs its extremes
+    if (vec) MP_RQ(MP_SCALE_FAKE, true, true);
+    else MP_RQ(MP_SCALE_FAKE, true, false);
+  } else {
+    if (vec) MP_RQ(MP_SCALE_FAKE, false, true);
+    else MP_RQ(MP_SCALE_FAKE, false, false);
+  }
+#undef MP_RQ
   MP_CHECK_LAUNCH();
   return MP_OK;
 }
 
 extern "C" int mp_w8a8_grouped_gemm(const int8_t *q, const float *s, const int8_t *w, const float *s_w,
                                     const int64_t *group_offsets, int n_experts, int64_t rows, int64_t n,
-                                    int64_t k, void *y, int out_dtype, mp_stream_t stream) {
+                                    int64_t k, int scale_rule, int act_dtype, void *y, int out_dtype,
+                                    mp_stream_t stream) {
   if (!q || !s || !w || !s_w || !group_offsets || !y) return MP_ERR_ARG;
   if (out_dtype != MP_F32 && out_dtype != MP_F16 && out_dtype != MP_BF16) return MP_ERR_DTYPE;
+  if (scale_rule != MP_SCALE_FP32 && scale_rule != MP_SCALE_FAKE) return MP_ERR_ARG;
   if (rows < 0 || n <= 0 || k <= 0 || n_experts <= 0 || n_experts > kMaxExperts) return MP_ERR_SHAPE;
+  if (scale_rule == MP_SCALE_FAKE) {
+    if (act_dtype != MP_F16 && act_dtype != MP_BF16) return MP_ERR_DTYPE;
+    if (k > (1 << 20)) return MP_ERR_SHAPE;
+    if (rows == 0) return MP_OK;
+    mp_dq_args d{};
+    d.dt = act_dtype;
+    d.a = q;
+    d.a_fmt = MP_DQ_I8ROW;
+    d.a_scale = s;
+    d.b = w;
+    d.b_fmt = MP_DQ_I8ROW;
+    d.b_scale = s_w;
+    d.y = y;
+    d.out_dtype = out_dtype;
+    d.ldy = n;
+    d.offsets = group_offsets;
+    d.n_experts = n_experts;
+    d.rows = rows;
+    d.n = n;
+    d.k = k;
+    return mp_launch_dq_gemm(d, out_dtype == MP_F32 ? MP_EPI_F32 : MP_EPI_DENSE, reinterpret_cast<hipStream_t>(stream));
+  }
   if (k % 64 != 0 || k > (1 << 17)) return MP_ERR_SHAPE;
   if (rows == 0) return MP_OK;
   mp_i8_args a{};
@@ -389,17 +525,28 @@ extern "C" int mp_w8a8_grouped_gemm(const int8_t *q, const float *s, const int8_
 }
 
 extern "C" int mp_moe_unpermute_combine(const float *y, const int32_t *row_of_slot, const float *topk_w, int64_t t,
-                                        int top_k, int64_t h, void *out, int out_dtype, mp_stream_t stream) {
+                                        int top_k, int64_t h, int scale_rule, void *out, int out_dtype,
+                                        mp_stream_t stream) {
   if (!y || !row_of_slot || !topk_w || !out) return MP_ERR_ARG;
   if (out_dtype != MP_F32 && out_dtype != MP_F16 && out_dtype != MP_BF16) return MP_ERR_DTYPE;
-  if (t < 0 || top_k <= 0 || h <= 0) return MP_ERR_SHAPE;
+  if (scale_rule != MP_SCALE_FP32 && scale_rule != MP_SCALE_FAKE) return MP_ERR_ARG;
+  if (scale_rule == MP_SCALE_FAKE && out_dtype == MP_F32) return MP_ERR_DTYPE;
+  if (t < 0 || top_k <= 0 || top_k > 64 || h <= 0) return MP_ERR_SHAPE;
   if (t == 0) return MP_OK;
-  if (h % 4 == 0 && mp_aligned(y, 16) && mp_aligned(out, out_dtype == MP_F32 ? 16 : 8))
-    hipLaunchKernelGGL(moe_combine_vec_kernel, dim3(static_cast<unsigned>(mp_cdiv(t * (h / 4), 256))), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(stream), y, row_of_slot, topk_w, t, top_k, h, out, out_dtype);
-  else
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(static_cast<unsigned>(mp_cdiv(t * h, 256))), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(stream), y, row_of_slot, topk_w, t, top_k, h, out, out_dtype);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = h % 4 == 0 && mp_aligned(y, 16) && mp_aligned(out, out_dtype == MP_F32 ? 16 : 8);
+  const dim3 g(static_cast<unsigned>(mp_cdiv(vec ? t * (h / 4) : t * h, 256)));
+#define MP_CB(FAKE_, VEC_) \
+  hipLaunchKernelGGL((moe_combine_kernel<FAKE_, VEC_>), g, dim3(256), 0, st, y, row_of_slot, topk_w, t, top_k, h, out, \
+                     out_dtype)
+  if (scale_rule == MP_SCALE_FAKE) {
+    if (vec) MP_CB(true, true);
+    else MP_CB(true, false);
+  } else {
+    if (vec) MP_CB(false, true);
+    else MP_CB(false, false);
+  }
+#undef MP_CB
   MP_CHECK_LAUNCH();
   return MP_OK;
 }
@@ -418,4 +565,4 @@ extern "C" const char *mp_strerror(int status) {
   }
 }
 
-extern "C" int mp_abi_version(void) { return 1; }
+extern "C" int mp_abi_version(void) { return 2; }

@@ -47,6 +47,48 @@ __device__ __forceinline__ uint16_t mp_f2bf(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// fp32 -> bf16 -> fp32: the value PyTorch keeps after a bfloat16 op.
+__device__ __forceinline__ float mp_rbf(float f) { return mp_bf2f(mp_f2bf(f)); }
+
+// Rounding of a value to the dtype of the op that produced it (the reference's fake-quant
+// path runs every op in the activation dtype).  kRoundNone keeps fp32.
+enum mp_round_mode { kRoundNone = 0, kRoundF16 = 1, kRoundBF16 = 2 };
+__device__ __forceinline__ float mp_round_mode_apply(float v, int mode) {
+  const float h = mp_rh(v), b = mp_rbf(v);
+  return mode == kRoundF16 ? h : (mode == kRoundBF16 ? b : v);
+}
+__host__ __device__ inline int mp_round_mode_of(int dtype) {
+  return dtype == MP_F16 ? kRoundF16 : (dtype == MP_BF16 ? kRoundBF16 : kRoundNone);
+}
+
+// The fake per-token / per-channel int8 rule (quantize_*_absmax of the reference's
+// fake_quant.py:10-31) in the input dtype: s = r(r(max(amax, 1e-5)) / 127), code =
+// rint(r(v / s)), every op rounded once (r = mp_round_mode_apply).  In fp16 the codes stay
+// within +-127; in bf16 (8-bit significand) r(v / s) can reach +-127.5 and the code +-128.
+// int8 holds -128 but not +128, so a row is stored as (q, s) when no code is +128, as
+// (-q, -s) when some code is +128 and none is -128 (the products q * s are the same bits),
+// and with +128 clamped to 127 when both occur (the one case that departs from the reference
+// values; it needs two entries of opposite sign within 0.4% of the row maximum).
+__device__ __forceinline__ float mp_fake_scale(float amax, int mode) {
+  float a = mp_round_mode_apply(amax, mode);
+  if (a < 1e-5f) a = mp_round_mode_apply(1e-5f, mode);
+  return mp_round_mode_apply(a / 127.0f, mode);
+}
+__device__ __forceinline__ float mp_fake_code(float v, float s, int mode) {
+  return rintf(mp_round_mode_apply(v / s, mode));
+}
+// Sign of the stored row (+1 or -1) from the row's largest and smallest values.
+__device__ __forceinline__ float mp_fake_row_sign(float vmax, float vmin, float s, int mode) {
+  const bool pos128 = mp_fake_code(vmax, s, mode) >= 128.f;
+  const bool neg128 = mp_fake_code(vmin, s, mode) <= -128.f;
+  return (pos128 && !neg128) ? -1.f : 1.f;
+}
+// Stored int8 code of v for a row of sign sg (-1: negated row).
+__device__ __forceinline__ int mp_fake_store(float v, float s, float sg, int mode) {
+  const float q = sg * mp_fake_code(v, s, mode);
+  return static_cast<int>(fminf(fmaxf(q, -128.f), 127.f));
+}
+
 __device__ __forceinline__ float mp_load_as_f32(const void *p, int64_t i, int dtype) {
   if (dtype == MP_F16) return mp_h2f(static_cast<const uint16_t *>(p)[i]);
   if (dtype == MP_BF16) return mp_bf2f(static_cast<const uint16_t *>(p)[i]);
@@ -86,6 +128,20 @@ __device__ __forceinline__ uint16_t mp_swiglu_h(float g, float u) {
   return mp_f2h(sg * u);
 }
 
+// SwiGLU of the grouped GEMM1 epilogue, h = silu(g) * u for the fp32 products g, u.  mode
+// kRoundNone keeps fp32 (the runtime rule); kRoundF16 / kRoundBF16 round as the reference's
+// fake path (fake_quant.py:184-185): gate and up as F.linear's output, silu(gate), and the
+// product, each once.  mode is uniform, so the branch costs the runtime path nothing.
+__device__ __forceinline__ float mp_swiglu_epi(float g, float u, int mode) {
+#pragma clang fp contract(off)
+  if (mode != kRoundNone) {
+    const float gr = mp_round_mode_apply(g, mode), ur = mp_round_mode_apply(u, mode);
+    const float sg = mp_round_mode_apply(__fdiv_rn(gr, 1.0f + expf(-gr)), mode);
+    return mp_round_mode_apply(sg * ur, mode);
+  }
+  return __fdiv_rn(g, 1.0f + expf(-g)) * u;
+}
+
 // ---- wave64 reductions (DPP-backed shuffles)
 __device__ __forceinline__ float mp_wave_max(float v) {
 #pragma unroll
@@ -96,6 +152,55 @@ __device__ __forceinline__ float mp_wave_min(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
   return v;
+}
+
+// ---- per-row statistics of the int8 row quantizers (256-thread workgroups)
+struct mp_rowstat {
+  float amax, vmax, vmin;
+  int bad;
+};
+__device__ __forceinline__ mp_rowstat mp_block_rowstat(mp_rowstat st, float (*red)[4], int *wbad) {
+  const int tid = threadIdx.x;
+  st.amax = mp_wave_max(st.amax);
+  st.vmax = mp_wave_max(st.vmax);
+  st.vmin = mp_wave_min(st.vmin);
+  const int wb = __any(st.bad);
+  if ((tid & 63) == 0) {
+    red[0][tid >> 6] = st.amax;
+    red[1][tid >> 6] = st.vmax;
+    red[2][tid >> 6] = st.vmin;
+    wbad[tid >> 6] = wb;
+  }
+  __syncthreads();
+  mp_rowstat o;
+  o.amax = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  o.vmax = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+  o.vmin = fminf(fminf(red[2][0], red[2][1]), fminf(red[2][2], red[2][3]));
+  o.bad = wbad[0] | wbad[1] | wbad[2] | wbad[3];
+  return o;
+}
+
+// Scale of a row and the sign of its stored codes.
+template <int RULE>
+__device__ __forceinline__ void mp_row_scale(const mp_rowstat &st, int mode, float min_scale, float &s, float &sg) {
+  if (RULE == MP_SCALE_FP32) {
+    s = st.amax / 127.0f;
+    if (s < min_scale) s = min_scale;
+    sg = 1.f;
+  } else {
+    s = mp_fake_scale(st.amax, mode);
+    sg = mp_fake_row_sign(st.vmax, st.vmin, s, mode);
+  }
+}
+
+template <int RULE>
+__device__ __forceinline__ uint32_t mp_row_code(float v, float s, float sg, int mode) {
+  if (RULE == MP_SCALE_FP32) {
+    float r = (s == 0.f) ? 0.f : rintf(v / s);
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    return static_cast<uint32_t>(static_cast<int>(r)) & 0xFFu;
+  }
+  return static_cast<uint32_t>(mp_fake_store(v, s, sg, mode)) & 0xFFu;
 }
 
 // Uniform-order float multiply/add that the compiler may not contract into an

@@ -5,7 +5,7 @@
 // packed int32 [N, ceil(K/8)], column k in nibble k%8 of word k/8, plus fp16
 // scales [N, K/g] and fp16 zeros [N, K/g] (AWQ) or an implicit zero point 8
 // (GPTQ symmetric export, stored nibble = int + 8).
-#include "mp_common.h"
+#include "dq_gemm.h"
 
 namespace {
 
@@ -52,9 +52,17 @@ __device__ __forceinline__ uint4 magic_to_natural(uint32_t t0, uint32_t t1, uint
 
 // ------------------------------------------------------------------ quantizers
 
-// One wave per quantization group (row segment of g elements).  fp16
-// arithmetic restated as fp32 op + one rounding, as PyTorch does for half
+// One wave per quantization group (row segment of g elements).  The weight dtype's
+// arithmetic (fp16 or bf16) restated as fp32 op + one rounding, as PyTorch does for half
 // tensors; quantizer.py:63-105.
+template <int DT>
+__device__ __forceinline__ float awq_ld(uint16_t b) { return DT == MP_F16 ? mp_h2f(b) : mp_bf2f(b); }
+template <int DT>
+__device__ __forceinline__ float awq_r(float v) { return DT == MP_F16 ? mp_rh(v) : mp_rbf(v); }
+template <int DT>
+__device__ __forceinline__ uint16_t awq_st(float v) { return DT == MP_F16 ? mp_f2h(v) : mp_f2bf(v); }
+
+template <int DT>
 __global__ __launch_bounds__(256) void awq_quantize_kernel(
     const uint16_t *__restrict__ w, int64_t n_rows, int64_t k, int gs, int n_groups, int zero_point,
     uint32_t *__restrict__ packed, int64_t kw, uint16_t *__restrict__ scales,
@@ -69,7 +77,7 @@ __global__ __launch_bounds__(256) void awq_quantize_kernel(
 
   float mx = -INFINITY, mn = INFINITY;
   for (int i = lane; i < gs; i += 64) {
-    const float v = mp_h2f(src[i]);
+    const float v = awq_ld<DT>(src[i]);
     mx = fmaxf(mx, zero_point ? v : fabsf(v));
     mn = fminf(mn, v);
   }
@@ -78,25 +86,25 @@ __global__ __launch_bounds__(256) void awq_quantize_kernel(
 
   float s, z, qmin, qmax;
   if (zero_point) {
-    float d = mp_rh(mx - mn);
-    if (d < 1e-5f) d = mp_rh(1e-5f);
-    s = mp_rh(d / 15.0f);
-    z = -rintf(mp_rh(mn / s));
+    float d = awq_r<DT>(mx - mn);
+    if (d < 1e-5f) d = awq_r<DT>(1e-5f);
+    s = awq_r<DT>(d / 15.0f);
+    z = -rintf(awq_r<DT>(mn / s));
     if (z < 0.0f) z = 0.0f;   // keeps -0.0 like torch.clamp_
     if (z > 15.0f) z = 15.0f;
     qmin = 0.0f;
     qmax = 15.0f;
   } else {
     float a = mx;
-    if (a < 1e-5f) a = mp_rh(1e-5f);
-    s = mp_rh(a / 7.0f);
+    if (a < 1e-5f) a = awq_r<DT>(1e-5f);
+    s = awq_r<DT>(a / 7.0f);
     z = 0.0f;
     qmin = -8.0f;
     qmax = 7.0f;
   }
   if (lane == 0) {
-    scales[row * n_groups + gi] = mp_f2h(s);
-    if (zero_point) zeros[row * n_groups + gi] = mp_f2h(z);
+    scales[row * n_groups + gi] = awq_st<DT>(s);
+    if (zero_point) zeros[row * n_groups + gi] = awq_st<DT>(z);
   }
   // pass 2: one packed word (8 consecutive columns) per lane iteration
   const int nwords = (gs + 7) / 8;
@@ -106,13 +114,13 @@ __global__ __launch_bounds__(256) void awq_quantize_kernel(
     for (int j = 0; j < 8; ++j) {
       const int idx = 8 * c + j;
       if (idx >= gs) break;
-      const float v = mp_h2f(src[idx]);
-      const float t = rintf(mp_rh(v / s));
-      float q = mp_rh(t + z);
+      const float v = awq_ld<DT>(src[idx]);
+      const float t = rintf(awq_r<DT>(v / s));
+      float q = awq_r<DT>(t + z);
       if (q < qmin) q = qmin;
       if (q > qmax) q = qmax;
-      const float deq = mp_rh(mp_rh(q - z) * s);
-      if (wdeq) wdeq[row * k + e0 + idx] = mp_f2h(deq);
+      const float deq = awq_r<DT>(awq_r<DT>(q - z) * s);
+      if (wdeq) wdeq[row * k + e0 + idx] = awq_st<DT>(deq);
       const uint32_t u = static_cast<uint32_t>(static_cast<int>(q) + (zero_point ? 0 : 8));
       word |= u << (4 * j);
     }
@@ -1311,10 +1319,11 @@ static int mp_prefill_threads() {
 
 // ====================================================================== C ABI
 
-extern "C" int mp_w4_quantize_awq(const void *w, int64_t n, int64_t k, int group_size, int zero_point,
+extern "C" int mp_w4_quantize_awq(const void *w, int w_dtype, int64_t n, int64_t k, int group_size, int zero_point,
                                   int32_t *packed, void *scales, void *zeros, void *w_deq,
                                   mp_stream_t stream) {
   if (!w || !packed || !scales || (zero_point && !zeros)) return MP_ERR_ARG;
+  if (w_dtype != MP_F16 && w_dtype != MP_BF16) return MP_ERR_DTYPE;
   if (n <= 0 || k <= 0) return MP_ERR_SHAPE;
   const int64_t gs = (group_size > 0 && k % group_size == 0) ? group_size : k;
   if (gs % 8 != 0 && gs != k) return MP_ERR_SHAPE;
@@ -1322,11 +1331,15 @@ extern "C" int mp_w4_quantize_awq(const void *w, int64_t n, int64_t k, int group
   const int64_t n_groups = k / gs;
   const int64_t total = n * n_groups;
   const int64_t kw = mp_cdiv(k, 8);
-  hipLaunchKernelGGL(awq_quantize_kernel, dim3(static_cast<unsigned>(mp_cdiv(total, 4))), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t *>(w), n, k,
-                     static_cast<int>(gs), static_cast<int>(n_groups), zero_point,
-                     reinterpret_cast<uint32_t *>(packed), kw, static_cast<uint16_t *>(scales),
-                     static_cast<uint16_t *>(zeros), static_cast<uint16_t *>(w_deq));
+#define MP_AWQ(DT_)                                                                                          \
+  hipLaunchKernelGGL(awq_quantize_kernel<DT_>, dim3(static_cast<unsigned>(mp_cdiv(total, 4))), dim3(256), 0,  \
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t *>(w), n, k,         \
+                     static_cast<int>(gs), static_cast<int>(n_groups), zero_point,                          \
+                     reinterpret_cast<uint32_t *>(packed), kw, static_cast<uint16_t *>(scales),             \
+                     static_cast<uint16_t *>(zeros), static_cast<uint16_t *>(w_deq))
+  if (w_dtype == MP_F16) MP_AWQ(MP_F16);
+  else MP_AWQ(MP_BF16);
+#undef MP_AWQ
   MP_CHECK_LAUNCH();
   return MP_OK;
 }
@@ -1545,13 +1558,36 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
 extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n,
                              const void *scales, const void *zeros, int group_size, const void *bias,
                              void *y, int x_dtype, mp_stream_t stream) {
-  if (x_dtype != MP_F16) return MP_ERR_DTYPE;
+  if (x_dtype != MP_F16 && x_dtype != MP_BF16) return MP_ERR_DTYPE;
   if (m < 0 || n <= 0 || k <= 0 || group_size <= 0 || k % group_size != 0 || k % 8 != 0)
     return MP_ERR_SHAPE;
   if (m == 0) return MP_OK;
   if (!x || !w_packed || !scales || !y) return MP_ERR_ARG;
   if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return MP_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (x_dtype == MP_BF16) {
+    // bf16: every dequantised weight rounded to bf16 as the reference's pseudo-quantized
+    // weight is (bf16 keeps 8 significant bits: factoring the group scale out of the sum, as
+    // the fp16 streaming kernels do, would miss the reference by ~1e-3)
+    mp_dq_args a{};
+    a.dt = MP_BF16;
+    a.a = x;
+    a.a_fmt = MP_DQ_DT;
+    a.b = w_packed;
+    a.b_fmt = MP_DQ_U4GRP;
+    a.b_gscale = static_cast<const uint16_t *>(scales);
+    a.b_gzero = static_cast<const uint16_t *>(zeros);
+    a.group = group_size;
+    a.bias = bias;
+    a.bias_dtype = MP_BF16;
+    a.y = y;
+    a.out_dtype = MP_BF16;
+    a.ldy = n;
+    a.rows = m;
+    a.n = n;
+    a.k = k;
+    return mp_launch_dq_gemm(a, MP_EPI_DENSE, s);
+  }
   const int n_groups = static_cast<int>(k / group_size);
   const auto *xp = static_cast<const uint16_t *>(x);
   const auto *wp = reinterpret_cast<const uint32_t *>(w_packed);

@@ -1,63 +1,44 @@
 // W8A8 for gfx950: per-token / per-channel int8 quantizers and the int8 MFMA
 // GEMM with the per-token x per-channel scale epilogue (dense and grouped).
-#include "i8_gemm.h"
+#include "dq_gemm.h"
 
 namespace {
 
 // ------------------------------------------------------------------ row quantizer
-// One 256-thread workgroup per row.  Pass 1: abs-max; pass 2: codes (the row
-// is re-read from L2).  RULE selects the scale arithmetic (see mp_scale_rule).
+// One 256-thread workgroup per row.  Pass 1: abs-max (and, for the fake rule, the largest
+// and smallest value: the sign rule of mp_fake_row_sign); pass 2: codes (the row is re-read
+// from L2).  RULE selects the scale arithmetic (see mp_scale_rule): MP_SCALE_FP32, or
+// MP_SCALE_FAKE in the input dtype (fp16 / bf16) with the stored scale signed like the row.
 template <int RULE>
 __global__ __launch_bounds__(256) void rowquant_kernel(const void *__restrict__ x, int x_dtype, int64_t k,
                                                        int8_t *__restrict__ q, float *__restrict__ s_f32,
                                                        uint16_t *__restrict__ s_src, int s_src_bf16,
                                                        float min_scale, int32_t *__restrict__ bad) {
-  __shared__ float wmax[4];
+  __shared__ float red[3][4];
   __shared__ int wbad[4];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t base = row * k;
-  float amax = 0.f;
-  int nonfinite = 0;
+  const int mode = mp_round_mode_of(x_dtype);
+  mp_rowstat st{0.f, -INFINITY, INFINITY, 0};
   for (int64_t c = tid; c < k; c += 256) {
     const float v = mp_load_as_f32(x, base + c, x_dtype);
-    nonfinite |= !isfinite(v);
-    amax = fmaxf(amax, fabsf(v));
+    st.bad |= !isfinite(v);
+    st.amax = fmaxf(st.amax, fabsf(v));
+    st.vmax = fmaxf(st.vmax, v);
+    st.vmin = fminf(st.vmin, v);
   }
-  amax = mp_wave_max(amax);
-  const int wb = __any(nonfinite);
-  if ((tid & 63) == 0) {
-    wmax[tid >> 6] = amax;
-    wbad[tid >> 6] = wb;
-  }
-  __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  const int row_bad = wbad[0] | wbad[1] | wbad[2] | wbad[3];
-
-  float s;
-  if (RULE == MP_SCALE_FP32) {
-    s = amax / 127.0f;
-    if (s < min_scale) s = min_scale;
-  } else {
-    float a = mp_rh(amax);
-    if (a < 1e-5f) a = mp_rh(1e-5f);
-    s = mp_rh(a / 127.0f);
-  }
+  st = mp_block_rowstat(st, red, wbad);
+  float s, sg;
+  mp_row_scale<RULE>(st, mode, min_scale, s, sg);
   if (tid == 0) {
-    if (s_f32) s_f32[row] = s;
-    if (s_src) s_src[row] = s_src_bf16 ? mp_f2bf(s) : mp_f2h(s);
-    if (bad && row_bad) atomicAdd(bad, 1);
+    if (s_f32) s_f32[row] = sg * s;
+    if (s_src) s_src[row] = s_src_bf16 ? mp_f2bf(sg * s) : mp_f2h(sg * s);
+    if (bad && st.bad) atomicAdd(bad, 1);
   }
   for (int64_t c = tid; c < k; c += 256) {
     const float v = mp_load_as_f32(x, base + c, x_dtype);
-    float r;
-    if (RULE == MP_SCALE_FP32) {
-      r = (s == 0.f) ? 0.f : rintf(v / s);
-    } else {
-      r = rintf(mp_rh(v / s));
-    }
-    r = fminf(fmaxf(r, -127.f), 127.f);
-    q[base + c] = static_cast<int8_t>(static_cast<int>(r));
+    q[base + c] = static_cast<int8_t>(mp_row_code<RULE>(v, s, sg, mode));
   }
 }
 
@@ -69,45 +50,34 @@ __global__ __launch_bounds__(256) void rowquant_vec_kernel(const void *__restric
                                                            uint16_t *__restrict__ s_src, int s_src_bf16,
                                                            float min_scale, int32_t *__restrict__ bad) {
   constexpr int N = MpChunk16<DT>::N, ESZ = DT == MP_F32 ? 4 : 2;
-  __shared__ float wmax[4];
+  __shared__ float red[3][4];
   __shared__ int wbad[4];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t nch = k / N;
+  const int mode = DT == MP_F16 ? kRoundF16 : (DT == MP_BF16 ? kRoundBF16 : kRoundNone);
   const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const char *>(x) + row * k * ESZ);
-  float amax = 0.f;
-  int nonfinite = 0;
+  mp_rowstat st{0.f, -INFINITY, INFINITY, 0};
   for (int64_t c = tid; c < nch; c += 256) {
     float f[N];
     mp_chunk_to_f32<DT>(src[c], f);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      nonfinite |= !isfinite(f[i]);
-      amax = fmaxf(amax, fabsf(f[i]));
+      st.bad |= !isfinite(f[i]);
+      st.amax = fmaxf(st.amax, fabsf(f[i]));
+      if (RULE != MP_SCALE_FP32) {
+        st.vmax = fmaxf(st.vmax, f[i]);
+        st.vmin = fminf(st.vmin, f[i]);
+      }
     }
   }
-  amax = mp_wave_max(amax);
-  const int wb = __any(nonfinite);
-  if ((tid & 63) == 0) {
-    wmax[tid >> 6] = amax;
-    wbad[tid >> 6] = wb;
-  }
-  __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  const int row_bad = wbad[0] | wbad[1] | wbad[2] | wbad[3];
-  float s;
-  if (RULE == MP_SCALE_FP32) {
-    s = amax / 127.0f;
-    if (s < min_scale) s = min_scale;
-  } else {
-    float a = mp_rh(amax);
-    if (a < 1e-5f) a = mp_rh(1e-5f);
-    s = mp_rh(a / 127.0f);
-  }
+  st = mp_block_rowstat(st, red, wbad);
+  float s, sg;
+  mp_row_scale<RULE>(st, mode, min_scale, s, sg);
   if (tid == 0) {
-    if (s_f32) s_f32[row] = s;
-    if (s_src) s_src[row] = s_src_bf16 ? mp_f2bf(s) : mp_f2h(s);
-    if (bad && row_bad) atomicAdd(bad, 1);
+    if (s_f32) s_f32[row] = sg * s;
+    if (s_src) s_src[row] = s_src_bf16 ? mp_f2bf(sg * s) : mp_f2h(sg * s);
+    if (bad && st.bad) atomicAdd(bad, 1);
   }
   int8_t *dst = q + row * k;
   for (int64_t c = tid; c < nch; c += 256) {
@@ -118,14 +88,7 @@ __global__ __launch_bounds__(256) void rowquant_vec_kernel(const void *__restric
     for (int g = 0; g < N / 4; ++g) {
       uint32_t word = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float v = f[4 * g + e];
-        float r;
-        if (RULE == MP_SCALE_FP32) r = (s == 0.f) ? 0.f : rintf(v / s);
-        else r = rintf(mp_rh(v / s));
-        r = fminf(fmaxf(r, -127.f), 127.f);
-        word |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xFFu) << (8 * e);
-      }
+      for (int e = 0; e < 4; ++e) word |= mp_row_code<RULE>(f[4 * g + e], s, sg, mode) << (8 * e);
       w[g] = word;
     }
     if constexpr (N == 8) *reinterpret_cast<uint2 *>(dst + c * 8) = make_uint2(w[0], w[1]);
@@ -134,6 +97,10 @@ __global__ __launch_bounds__(256) void rowquant_vec_kernel(const void *__restric
 }
 
 // ------------------------------------------------------------------ decode GEMV (M <= 64)
+// 16-byte activation pieces a thread of an NT-thread skinny workgroup stages per K chunk; a chunk
+// holds at most skinny_pmax(NT) * NT pieces (the launcher sizes chunks to that).
+constexpr int skinny_pmax(int nt) { return kMpXLdsBudget / 16 / nt + 1; }
+
 // One workgroup of NW waves per 16 output columns; each wave takes a contiguous
 // range of 64-byte K blocks, and the waves are summed exactly (int32) through LDS.  The int8
 // activations are staged once per workgroup into LDS (K chunks within the LDS
@@ -202,8 +169,8 @@ __global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb
         }
       }
     };
-    constexpr int PMAX = kMpXLdsBudget / 16 / NT + 1;
-    const int pieces = m_rows * cbn * 4;
+    constexpr int PMAX = skinny_pmax(NT);
+    const int pieces = m_rows * cbn * 4;  // <= PMAX * NT: the launcher's chunk rule
     i4_t xv[PMAX];
 #pragma unroll
     for (int i = 0; i < PMAX; ++i) {
@@ -549,8 +516,7 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
         const float sa_m = mval ? p.s_a[m] : 0.f;
         const float g = mp_mul(mp_mul(static_cast<float>(acc[i][0][r]), sa_m), sg);
         const float u = mp_mul(mp_mul(static_cast<float>(acc[i][1][r]), sa_m), su);
-        const float den = mp_add(1.0f, expf(-g));
-        const float h = mp_mul(__fdiv_rn(g, den), u);
+        const float h = mp_swiglu_epi(g, u, p.epi_round);
         if (mval && cval) hbuf[m * p.ldy + col] = h;
         float a = (mval && cval) ? fabsf(h) : 0.f;
 #pragma unroll
@@ -918,8 +884,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
             const int lm = lm0 + i * 32 + 8 * (r >> 2) + (r & 3);
             const float gv = mp_mul(mp_mul(static_cast<float>(acc[i][0][r]), sa_r[i][r]), sg);
             const float uv = mp_mul(mp_mul(static_cast<float>(acc[i][1][r]), sa_r[i][r]), su);
-            const float den = mp_add(1.0f, expf(-gv));
-            const float h = mp_mul(__fdiv_rn(gv, den), uv);
+            const float h = mp_swiglu_epi(gv, uv, p.epi_round);
             mp_buf_store4(hr, cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * 4 : kOob,
                           __float_as_uint(h));
             v[i * 16 + r] = (cval && static_cast<uint32_t>(lm) < nrows) ? fabsf(h) : 0.f;
@@ -1123,8 +1088,7 @@ __device__ __forceinline__ void grouped_epilogue(const mp_i8_args &p, const i16_
         const float sa_m = mval ? p.s_a[m] : 0.f;
         const float g = mp_mul(mp_mul(static_cast<float>(acc[i][0][r]), sa_m), sg);
         const float u = mp_mul(mp_mul(static_cast<float>(acc[i][1][r]), sa_m), su);
-        const float den = mp_add(1.0f, expf(-g));
-        const float h = mp_mul(__fdiv_rn(g, den), u);
+        const float h = mp_swiglu_epi(g, u, p.epi_round);
         if (mval && cval) yb[m * p.ldy + col] = h;
         float a = (mval && cval) ? fabsf(h) : 0.f;
 #pragma unroll
@@ -1875,9 +1839,14 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
     const int nblk = static_cast<int>(a.k / 64);
     int cb = (kMpXLdsBudget / mi - 16) / 64;
     cb = cb < 1 ? 1 : (cb > nblk ? nblk : cb);
-    // the whole K in one chunk when it fits 76 KB (two workgroups per CU still fit): no second
+    // the whole K in one chunk when it fits 76 KB (two workgroups per CU still fit) and the
+    // workgroup's staging registers (skinny_pmax pieces per thread) hold it: no second
     // activation round trip and weight-pipeline restart (MP_W8_SKINNY_ONE_CHUNK=0: off)
-    if (mp_skinny_one_chunk() && static_cast<int64_t>(mi) * (nblk * 64 + 16) + 16 <= 76 * 1024) cb = nblk;
+    const int64_t stage_cap = static_cast<int64_t>(nw) * 64 * skinny_pmax(nw * 64);
+    if (mp_skinny_one_chunk() && static_cast<int64_t>(mi) * (nblk * 64 + 16) + 16 <= 76 * 1024 &&
+        static_cast<int64_t>(mi) * nblk * 4 <= stage_cap)
+      cb = nblk;
+    if (static_cast<int64_t>(mi) * cb * 4 > stage_cap) return MP_ERR_SHAPE;  // cannot happen with the rule above
     size_t smem = static_cast<size_t>(mi) * (cb * 64 + 16) + 16;
     const size_t red = static_cast<size_t>(nw) * mt * 1024;
     smem = smem > red ? smem : red;
@@ -1989,9 +1958,10 @@ extern "C" int mp_quant_per_token_i8(const void *x, int64_t m, int64_t k, int x_
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (scale_rule == MP_SCALE_FP32) {
     mp_launch_rowquant<MP_SCALE_FP32>(x, x_dtype, m, k, q, static_cast<float *>(scale), nullptr, 0, 0.0f, nullptr, s);
-  } else if (scale_rule == MP_SCALE_FP16) {
-    if (x_dtype != MP_F16) return MP_ERR_DTYPE;
-    mp_launch_rowquant<MP_SCALE_FP16>(x, x_dtype, m, k, q, nullptr, static_cast<uint16_t *>(scale), 0, 0.0f, nullptr, s);
+  } else if (scale_rule == MP_SCALE_FAKE) {
+    if (x_dtype != MP_F16 && x_dtype != MP_BF16) return MP_ERR_DTYPE;
+    mp_launch_rowquant<MP_SCALE_FAKE>(x, x_dtype, m, k, q, nullptr, static_cast<uint16_t *>(scale),
+                                      x_dtype == MP_BF16 ? 1 : 0, 0.0f, nullptr, s);
   } else {
     return MP_ERR_ARG;
   }
@@ -2011,10 +1981,9 @@ extern "C" int mp_w8_quantize_per_channel(const void *w, int64_t n, int64_t k, i
   if (scale_rule == MP_SCALE_FP32) {
     mp_launch_rowquant<MP_SCALE_FP32>(w, w_dtype, n, k, q, scale_f32, static_cast<uint16_t *>(scale_src),
                                       w_dtype == MP_BF16 ? 1 : 0, 1e-8f, bad_count, s);
-  } else if (scale_rule == MP_SCALE_FP16) {
-    if (w_dtype != MP_F16) return MP_ERR_DTYPE;
-    mp_launch_rowquant<MP_SCALE_FP16>(w, w_dtype, n, k, q, scale_f32, static_cast<uint16_t *>(scale_src), 0, 0.0f,
-                                      bad_count, s);
+  } else if (scale_rule == MP_SCALE_FAKE) {
+    mp_launch_rowquant<MP_SCALE_FAKE>(w, w_dtype, n, k, q, scale_f32, static_cast<uint16_t *>(scale_src),
+                                      w_dtype == MP_BF16 ? 1 : 0, 0.0f, bad_count, s);
   } else {
     return MP_ERR_ARG;
   }
@@ -2045,4 +2014,30 @@ extern "C" int mp_w8a8_gemm(const int8_t *qx, const float *s_tok, const int8_t *
   a.k = k;
   a.ldy = n;
   return mp_launch_i8_gemm(a, MP_EPI_DENSE, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int mp_w8a8_gemm_fake(const int8_t *qx, const float *s_tok, const int8_t *w, const float *s_ch,
+                                 const void *bias, int act_dtype, void *y, int64_t m, int64_t n, int64_t k,
+                                 mp_stream_t stream) {
+  if (!qx || !s_tok || !w || !s_ch || !y) return MP_ERR_ARG;
+  if (act_dtype != MP_F16 && act_dtype != MP_BF16) return MP_ERR_DTYPE;
+  if (m < 0 || n <= 0 || k <= 0) return MP_ERR_SHAPE;
+  if (m == 0) return MP_OK;
+  mp_dq_args d{};
+  d.dt = act_dtype;
+  d.a = qx;
+  d.a_fmt = MP_DQ_I8ROW;
+  d.a_scale = s_tok;
+  d.b = w;
+  d.b_fmt = MP_DQ_I8ROW;
+  d.b_scale = s_ch;
+  d.bias = bias;
+  d.bias_dtype = act_dtype;
+  d.y = y;
+  d.out_dtype = act_dtype;
+  d.ldy = n;
+  d.rows = m;
+  d.n = n;
+  d.k = k;
+  return mp_launch_dq_gemm(d, MP_EPI_DENSE, reinterpret_cast<hipStream_t>(stream));
 }

@@ -16,7 +16,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from ._lib import MP_BF16, MP_F16, MP_F32, MP_SCALE_FP16, MP_SCALE_FP32
+from ._lib import MP_BF16, MP_F16, MP_F32, MP_I8, MP_SCALE_FAKE, MP_SCALE_FP32
 
 _DT = {torch.float16: MP_F16, torch.bfloat16: MP_BF16, torch.float32: MP_F32}
 
@@ -49,17 +49,18 @@ def _dev(t: torch.Tensor):
 # ---------------------------------------------------------------- W4
 def w4_quantize_awq(w: torch.Tensor, group_size: int = 128, zero_point: bool = True,
                     return_deq: bool = True):
-    """AWQ ``pseudo_quantize_tensor`` on the GPU: returns ``(packed, scales, zeros, w_deq)``."""
-    _need(w, "w", torch.float16, 2)
+    """AWQ ``pseudo_quantize_tensor`` on the GPU, in the arithmetic of ``w``'s dtype (fp16 or
+    bf16): returns ``(packed, scales, zeros, w_deq)`` with scales / zeros / w_deq in that dtype."""
+    _need(w, "w", (torch.float16, torch.bfloat16), 2)
     n, k = w.shape
     g = group_size if (group_size > 0 and k % group_size == 0) else k
     packed = torch.empty((n, (k + 7) // 8), dtype=torch.int32, device=w.device)
-    scales = torch.empty((n, k // g), dtype=torch.float16, device=w.device)
+    scales = torch.empty((n, k // g), dtype=w.dtype, device=w.device)
     zeros = torch.empty_like(scales) if zero_point else None
     deq = torch.empty_like(w) if return_deq else None
     with _dev(w):
         _lib.check(_lib.load().mp_w4_quantize_awq(
-            w.data_ptr(), n, k, group_size, int(zero_point), packed.data_ptr(), scales.data_ptr(),
+            w.data_ptr(), _DT[w.dtype], n, k, group_size, int(zero_point), packed.data_ptr(), scales.data_ptr(),
             _ptr(zeros), _ptr(deq), _stream()), "mp_w4_quantize_awq")
     return packed, scales, zeros, deq
 
@@ -111,10 +112,11 @@ def unpack_int4(packed: torch.Tensor, k: int) -> torch.Tensor:
 @torch.library.custom_op("mindpipe_amd::w4a16_gemm", mutates_args=())
 def w4a16_gemm(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor],
                group_size: int, bias: Optional[torch.Tensor]) -> torch.Tensor:
-    """``Y = X . dequant(W)^T (+ bias)``; ``x`` fp16 ``[..., K]``; ``w_packed`` int32 ``[N, K/8]``."""
-    _need(x, "x", torch.float16)
+    """``Y = X . dequant(W)^T (+ bias)``; ``x`` fp16 or bf16 ``[..., K]`` (scales, zeros, bias and
+    the output in the same dtype); ``w_packed`` int32 ``[N, K/8]``."""
+    _need(x, "x", (torch.float16, torch.bfloat16))
     _need(w_packed, "w_packed", torch.int32, 2)
-    _need(scales, "scales", torch.float16, 2)
+    _need(scales, "scales", x.dtype, 2)
     k = x.shape[-1]
     n = w_packed.shape[0]
     if w_packed.shape[1] * 8 != k:
@@ -122,20 +124,20 @@ def w4a16_gemm(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Tensor, ze
     if k % group_size or scales.shape != (n, k // group_size):
         raise RuntimeError(f"scales {tuple(scales.shape)} do not match N={n}, K={k}, g={group_size}")
     if zeros is not None:
-        _need(zeros, "zeros", torch.float16, 2)
+        _need(zeros, "zeros", x.dtype, 2)
         if zeros.shape != scales.shape:
             raise RuntimeError("zeros must have the shape of scales")
     if bias is not None:
-        _need(bias, "bias", torch.float16, 1)
+        _need(bias, "bias", x.dtype, 1)
         if bias.shape[0] != n:
             raise RuntimeError("bias must be [N]")
     x2 = x.reshape(-1, k)
     m = x2.shape[0]
-    y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    y = torch.empty((m, n), dtype=x.dtype, device=x.device)
     with _dev(x):
         _lib.check(_lib.load().mp_w4a16_gemm(
             x2.data_ptr(), m, k, w_packed.data_ptr(), n, scales.data_ptr(), _ptr(zeros), group_size,
-            _ptr(bias), y.data_ptr(), MP_F16, _stream()), "mp_w4a16_gemm")
+            _ptr(bias), y.data_ptr(), _DT[x.dtype], _stream()), "mp_w4a16_gemm")
     return y.reshape(*x.shape[:-1], n)
 
 
@@ -146,34 +148,36 @@ def _(x, w_packed, scales, zeros, group_size, bias):
 
 # ---------------------------------------------------------------- W8A8
 @torch.library.custom_op("mindpipe_amd::quant_per_token_i8", mutates_args=())
-def quant_per_token_i8(x: torch.Tensor, fp16_scale: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+def quant_per_token_i8(x: torch.Tensor, fake_rule: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """Per-token dynamic int8 quant: ``(q int8 [..., K], scale [...])``.
 
-    ``fp16_scale=False``: fp32 scale ``absmax/127`` (``npu_dynamic_quant`` contract).
-    ``fp16_scale=True``: fp16 scale and codes of ``quantize_activation_per_token_absmax``.
+    ``fake_rule=False``: fp32 scale ``absmax/127`` (``npu_dynamic_quant`` contract).
+    ``fake_rule=True``: codes and scale (in ``x``'s dtype, fp16 or bf16) of
+    ``quantize_activation_per_token_absmax``; ``q * scale`` is the reference's fake value
+    (a bf16 row whose codes reach +128 is stored negated with a negated scale).
     """
     _need(x, "x", (torch.float16, torch.bfloat16, torch.float32))
     k = x.shape[-1]
     x2 = x.reshape(-1, k)
     m = x2.shape[0]
     q = torch.empty((m, k), dtype=torch.int8, device=x.device)
-    if fp16_scale:
-        if x.dtype != torch.float16:
-            raise RuntimeError("the fp16 scale rule takes fp16 activations")
-        s = torch.empty((m,), dtype=torch.float16, device=x.device)
+    if fake_rule:
+        if x.dtype not in (torch.float16, torch.bfloat16):
+            raise RuntimeError("the fake rule takes fp16 or bf16 activations")
+        s = torch.empty((m,), dtype=x.dtype, device=x.device)
     else:
         s = torch.empty((m,), dtype=torch.float32, device=x.device)
     with _dev(x):
         _lib.check(_lib.load().mp_quant_per_token_i8(
             x2.data_ptr(), m, k, _DT[x.dtype], q.data_ptr(), s.data_ptr(),
-            MP_SCALE_FP16 if fp16_scale else MP_SCALE_FP32, _stream()), "mp_quant_per_token_i8")
+            MP_SCALE_FAKE if fake_rule else MP_SCALE_FP32, _stream()), "mp_quant_per_token_i8")
     return q.reshape(x.shape), s.reshape(x.shape[:-1])
 
 
 @quant_per_token_i8.register_fake
-def _(x, fp16_scale=False):
+def _(x, fake_rule=False):
     return (torch.empty_like(x, dtype=torch.int8),
-            x.new_empty(x.shape[:-1], dtype=torch.float16 if fp16_scale else torch.float32))
+            x.new_empty(x.shape[:-1], dtype=x.dtype if fake_rule else torch.float32))
 
 
 def add_rms_norm_quant(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor, eps: float,
@@ -218,7 +222,8 @@ def w8_quantize_per_channel(w: torch.Tensor, rule: str = "export"):
     """Per-output-channel int8 weight quant.
 
     ``rule="export"``: fp32 rule of the Ascend W8A8 export (clamp 1e-8).
-    ``rule="fake"``: fp16 rule of ``quantize_weight_per_channel_absmax``.
+    ``rule="fake"``: the rule of ``quantize_weight_per_channel_absmax`` in ``w``'s dtype
+    (fp16 / bf16; a bf16 row whose codes reach +128 is stored negated with a negated scale).
     Returns ``(q int8 [N,K], scale_f32 [N], scale_src [N] in w.dtype)``.
     """
     _need(w, "w", (torch.float16, torch.bfloat16), 2)
@@ -227,7 +232,7 @@ def w8_quantize_per_channel(w: torch.Tensor, rule: str = "export"):
     s32 = torch.empty((n,), dtype=torch.float32, device=w.device)
     ssrc = torch.empty((n,), dtype=w.dtype, device=w.device)
     bad = torch.zeros(1, dtype=torch.int32, device=w.device)
-    r = MP_SCALE_FP32 if rule == "export" else MP_SCALE_FP16
+    r = MP_SCALE_FP32 if rule == "export" else MP_SCALE_FAKE
     if rule not in ("export", "fake"):
         raise ValueError(f"unknown rule {rule!r}")
     with _dev(w):
@@ -271,11 +276,68 @@ def _(qx, s_tok, w, s_ch, bias, out_dtype):
     return qx.new_empty((*qx.shape[:-1], w.shape[0]), dtype=out_dtype)
 
 
+@torch.library.custom_op("mindpipe_amd::w8a8_gemm_fake", mutates_args=())
+def w8a8_gemm_fake(qx: torch.Tensor, s_tok: torch.Tensor, w: torch.Tensor, s_ch: torch.Tensor,
+                   bias: Optional[torch.Tensor], act_dtype: torch.dtype) -> torch.Tensor:
+    """``F.linear(r(qx * s_tok), r(w * s_ch), bias)`` in ``act_dtype`` (fp16 / bf16): the fake
+    path of ``SmoothQuantLinear.forward`` (``fake_quant.py:85-88``) on the fake rule's codes,
+    every operand element rounded as the reference's fake-quant tensors are."""
+    _need(qx, "qx", torch.int8)
+    _need(w, "w", torch.int8, 2)
+    _need(s_tok, "s_tok", torch.float32)
+    _need(s_ch, "s_ch", torch.float32, 1)
+    if act_dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError("the fake path runs in fp16 or bf16")
+    k = qx.shape[-1]
+    n = w.shape[0]
+    if w.shape[1] != k:
+        raise RuntimeError(f"weight {tuple(w.shape)} does not match K={k}")
+    q2 = qx.reshape(-1, k)
+    m = q2.shape[0]
+    if s_tok.numel() != m or s_ch.numel() != n:
+        raise RuntimeError("scale sizes do not match M / N")
+    if bias is not None:
+        _need(bias, "bias", act_dtype, 1)
+    y = torch.empty((m, n), dtype=act_dtype, device=qx.device)
+    with _dev(qx):
+        _lib.check(_lib.load().mp_w8a8_gemm_fake(
+            q2.data_ptr(), s_tok.data_ptr(), w.data_ptr(), s_ch.data_ptr(), _ptr(bias), _DT[act_dtype],
+            y.data_ptr(), m, n, k, _stream()), "mp_w8a8_gemm_fake")
+    return y.reshape(*qx.shape[:-1], n)
+
+
+@w8a8_gemm_fake.register_fake
+def _(qx, s_tok, w, s_ch, bias, act_dtype):
+    return qx.new_empty((*qx.shape[:-1], w.shape[0]), dtype=act_dtype)
+
+
 # ---------------------------------------------------------------- MoE
-def moe_permute_quant(x: torch.Tensor, topk_ids: torch.Tensor, n_experts: int):
+_RULES = {"runtime": MP_SCALE_FP32, "fake": MP_SCALE_FAKE}
+
+
+def _rule(rule: str) -> int:
+    if rule not in _RULES:
+        raise ValueError(f"unknown scale rule {rule!r} (expected 'runtime' or 'fake')")
+    return _RULES[rule]
+
+
+def moe_permute_quant(x: torch.Tensor, topk_ids: torch.Tensor, n_experts: int, rule: str = "runtime",
+                      x_scale: Optional[torch.Tensor] = None):
     """Routing + per-token quant: ``(routed int8 [T*k,H], routed_scale f32, row_of_slot int32 [T*k],
-    group_offsets int64 [E+1])``.  Rows of ``routed`` past ``group_offsets[-1]`` are unused."""
-    _need(x, "x", (torch.float16, torch.bfloat16, torch.float32), 2)
+    group_offsets int64 [E+1])``.  Rows of ``routed`` past ``group_offsets[-1]`` are unused.
+
+    ``rule="runtime"``: fp32 scale ``absmax/127``; ``rule="fake"``: the reference module's
+    ``act_quant`` in ``x``'s dtype (fp16 / bf16).  With ``x_scale`` (fp32 ``[T]``), ``x`` is
+    already int8 (the runtime's ``pertoken_scale`` input) and is routed without re-quantizing."""
+    if x_scale is not None:
+        _need(x, "x", torch.int8, 2)
+        _need(x_scale, "x_scale", torch.float32)
+        if x_scale.numel() != x.shape[0]:
+            raise RuntimeError("x_scale must hold one scale per token")
+        x_dt = MP_I8
+    else:
+        _need(x, "x", (torch.float16, torch.bfloat16, torch.float32), 2)
+        x_dt = _DT[x.dtype]
     _need(topk_ids, "topk_ids", torch.int32, 2)
     t, h = x.shape
     top_k = topk_ids.shape[1]
@@ -291,15 +353,23 @@ def moe_permute_quant(x: torch.Tensor, topk_ids: torch.Tensor, n_experts: int):
     ws = torch.zeros((wsb,), dtype=torch.uint8, device=x.device)
     with _dev(x):
         _lib.check(lib.mp_moe_permute_quant(
-            x.data_ptr(), _DT[x.dtype], t, h, topk_ids.data_ptr(), top_k, n_experts, routed.data_ptr(),
-            rscale.data_ptr(), row_of_slot.data_ptr(), offsets.data_ptr(), ws.data_ptr(), wsb, _stream()),
-            "mp_moe_permute_quant")
+            x.data_ptr(), x_dt, _ptr(x_scale), t, h, topk_ids.data_ptr(), top_k, n_experts, _rule(rule),
+            routed.data_ptr(), rscale.data_ptr(), row_of_slot.data_ptr(), offsets.data_ptr(), ws.data_ptr(), wsb,
+            _stream()), "mp_moe_permute_quant")
     return routed, rscale, row_of_slot, offsets
 
 
-def moe_gmm1_swiglu_quant(routed, rscale, w13, s13, offsets, inter: int):
-    """GMM1 + SwiGLU + requant over expert groups: ``(q int8 [R, I], s f32 [R])``."""
+@torch.library.custom_op("mindpipe_amd::i8_gemm_swiglu_requant", mutates_args=())
+def moe_gmm1_swiglu_quant(routed: torch.Tensor, rscale: torch.Tensor, w13: torch.Tensor, s13: torch.Tensor,
+                          offsets: torch.Tensor, inter: int, rule: str = "runtime",
+                          act_dtype: torch.dtype = torch.float16) -> Tuple[torch.Tensor, torch.Tensor]:
+    """GMM1 + SwiGLU + requant over expert groups: ``(q int8 [R, I], s f32 [R])``.  The
+    counterpart of the reference bridge op ``mindpipe_qwen2_grouped_swiglu_loop_out``
+    (``aclnn_grouped_swiglu_out_bridge.cpp:157-273``) with no 10240-column limit.
+    ``rule="fake"`` rounds gate, up, silu(gate) and h in ``act_dtype`` and requantizes with the
+    fake rule (the reference module's forward); ``"runtime"`` keeps fp32."""
     _need(routed, "routed", torch.int8, 2)
+    _need(rscale, "routed_scale", torch.float32, 1)
     _need(w13, "w13", torch.int8, 3)
     _need(s13, "s13", torch.float32, 2)
     _need(offsets, "group_offsets", torch.int64, 1)
@@ -307,6 +377,8 @@ def moe_gmm1_swiglu_quant(routed, rscale, w13, s13, offsets, inter: int):
     e = w13.shape[0]
     if w13.shape[1] != 2 * inter or w13.shape[2] != h or s13.shape != (e, 2 * inter):
         raise RuntimeError("w13 must be [E, 2I, H] with s13 [E, 2I]")
+    if offsets.numel() != e + 1 or rscale.numel() != rows:
+        raise RuntimeError("group_offsets must be [E+1] and routed_scale [R]")
     lib = _lib.load()
     q = torch.empty((rows, inter), dtype=torch.int8, device=routed.device)
     s = torch.empty((rows,), dtype=torch.float32, device=routed.device)
@@ -315,48 +387,96 @@ def moe_gmm1_swiglu_quant(routed, rscale, w13, s13, offsets, inter: int):
     with _dev(routed):
         _lib.check(lib.mp_i8_gemm_swiglu_requant(
             routed.data_ptr(), rscale.data_ptr(), w13.data_ptr(), s13.data_ptr(), offsets.data_ptr(), e, rows, h,
-            inter, q.data_ptr(), s.data_ptr(), ws.data_ptr(), wsb, _stream()), "mp_i8_gemm_swiglu_requant")
+            inter, _rule(rule), _DT[act_dtype], q.data_ptr(), s.data_ptr(), ws.data_ptr(), wsb, _stream()),
+            "mp_i8_gemm_swiglu_requant")
     return q, s
 
 
-def moe_gmm2(q, s, w2, s2, offsets, out_dtype=torch.float32):
+@moe_gmm1_swiglu_quant.register_fake
+def _(routed, rscale, w13, s13, offsets, inter, rule="runtime", act_dtype=torch.float16):
+    return (routed.new_empty((routed.shape[0], inter), dtype=torch.int8),
+            routed.new_empty((routed.shape[0],), dtype=torch.float32))
+
+
+def moe_gmm2(q, s, w2, s2, offsets, out_dtype=torch.float32, rule: str = "runtime",
+             act_dtype: torch.dtype = torch.float16):
+    """Grouped GEMM2 ``[R, N]``: the int8 product with the per-token x per-row epilogue
+    (``rule="runtime"``), or ``F.linear`` of the fake-quant tensors in ``act_dtype``
+    (``rule="fake"``)."""
     _need(q, "q", torch.int8, 2)
+    _need(s, "s", torch.float32, 1)
     _need(w2, "w2", torch.int8, 3)
     _need(s2, "s2", torch.float32, 2)
+    _need(offsets, "group_offsets", torch.int64, 1)
     rows, k = q.shape
     e, n, k2 = w2.shape
-    if k2 != k or s2.shape != (e, n):
-        raise RuntimeError("w2 must be [E, H, I] with s2 [E, H]")
+    if k2 != k or s2.shape != (e, n) or offsets.numel() != e + 1 or s.numel() != rows:
+        raise RuntimeError("w2 must be [E, H, I] with s2 [E, H], group_offsets [E+1], s [R]")
     y = torch.empty((rows, n), dtype=out_dtype, device=q.device)
     with _dev(q):
         _lib.check(_lib.load().mp_w8a8_grouped_gemm(
             q.data_ptr(), s.data_ptr(), w2.data_ptr(), s2.data_ptr(), offsets.data_ptr(), e, rows, n, k,
-            y.data_ptr(), _DT[out_dtype], _stream()), "mp_w8a8_grouped_gemm")
+            _rule(rule), _DT[act_dtype], y.data_ptr(), _DT[out_dtype], _stream()), "mp_w8a8_grouped_gemm")
     return y
 
 
-def moe_unpermute_combine(y, row_of_slot, topk_w, out_dtype=torch.float16):
+def moe_unpermute_combine(y, row_of_slot, topk_w, out_dtype=torch.float16, rule: str = "runtime"):
+    """``rule="runtime"``: fp32 weighted sum in slot order, one rounding; ``rule="fake"``: the
+    reference's ``index_add_`` in ``out_dtype`` over ascending experts."""
     _need(y, "y", torch.float32, 2)
+    _need(row_of_slot, "row_of_slot", torch.int32, 1)
     _need(topk_w, "topk_weights", torch.float32, 2)
     t, top_k = topk_w.shape
     h = y.shape[1]
+    if row_of_slot.numel() != t * top_k:
+        raise RuntimeError("row_of_slot must hold T * top_k entries")
     out = torch.empty((t, h), dtype=out_dtype, device=y.device)
     with _dev(y):
         _lib.check(_lib.load().mp_moe_unpermute_combine(
-            y.data_ptr(), row_of_slot.data_ptr(), topk_w.data_ptr(), t, top_k, h, out.data_ptr(), _DT[out_dtype],
-            _stream()), "mp_moe_unpermute_combine")
+            y.data_ptr(), row_of_slot.data_ptr(), topk_w.data_ptr(), t, top_k, h, _rule(rule), out.data_ptr(),
+            _DT[out_dtype], _stream()), "mp_moe_unpermute_combine")
     return out
 
 
-def moe_w8a8_forward(x, topk_ids, topk_w, w13, s13, w2, s2, out_dtype=None):
-    """Whole W8A8 MoE chain (routing quant -> GMM1+SwiGLU+requant -> GMM2 -> combine)."""
+@torch.library.custom_op("mindpipe_amd::moe_w8a8_forward", mutates_args=())
+def moe_w8a8_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, w13: torch.Tensor,
+                     s13: torch.Tensor, w2: torch.Tensor, s2: torch.Tensor, out_dtype: Optional[torch.dtype] = None,
+                     rule: str = "runtime", x_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Whole W8A8 MoE chain (routing quant -> GMM1+SwiGLU+requant -> GMM2 -> combine) on the
+    kernel layout ``w13 [E, 2I, H]``, ``w2 [E, H, I]`` with fp32 per-row scales.
+
+    ``rule="fake"`` reproduces ``SmoothQuantPackedMoeExperts.forward`` (``fake_quant.py:166-191``)
+    in ``x``'s dtype; ``rule="runtime"`` is the fp32-scale chain of ``_run_expert_tile``
+    (``vllm_ascend.patch:2356-2423``).  ``x_scale`` marks ``x`` as pre-quantized int8."""
     e = w13.shape[0]
     inter = w2.shape[2]
-    routed, rscale, row_of_slot, offsets = moe_permute_quant(x, topk_ids.to(torch.int32).contiguous(), e)
-    q, s = moe_gmm1_swiglu_quant(routed, rscale, w13, s13, offsets, inter)
-    y = moe_gmm2(q, s, w2, s2, offsets)
-    return moe_unpermute_combine(y, row_of_slot, topk_w.to(torch.float32).contiguous(),
-                                 out_dtype or x.dtype)
+    if out_dtype is None:
+        out_dtype = x.dtype if x_scale is None else torch.float16
+    act_dtype = x.dtype if x_scale is None else out_dtype
+    if rule == "fake" and act_dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError("the fake rule runs in fp16 or bf16")
+    routed, rscale, row_of_slot, offsets = moe_permute_quant(x, topk_ids.to(torch.int32).contiguous(), e, rule,
+                                                             x_scale)
+    q, s = moe_gmm1_swiglu_quant(routed, rscale, w13, s13, offsets, inter, rule, act_dtype)
+    y = moe_gmm2(q, s, w2, s2, offsets, torch.float32, rule, act_dtype)
+    return moe_unpermute_combine(y, row_of_slot, topk_w.to(torch.float32).contiguous(), out_dtype, rule)
+
+
+@moe_w8a8_forward.register_fake
+def _(x, topk_ids, topk_w, w13, s13, w2, s2, out_dtype=None, rule="runtime", x_scale=None):
+    if out_dtype is None:
+        out_dtype = x.dtype if x_scale is None else torch.float16
+    return x.new_empty((x.shape[0], w2.shape[1]), dtype=out_dtype)
+
+
+def group_offsets_from_list(group_list: torch.Tensor, group_list_type: int) -> torch.Tensor:
+    """``group_offsets [E+1]`` (leading 0) from the runtime's ``group_list [E]``: cumulative
+    endpoints (type 0) or raw counts (type 1) (``vllm_ascend.patch:2015-2031``)."""
+    if group_list_type not in (0, 1):
+        raise ValueError(f"group_list_type must be 0 (cumulative) or 1 (counts), got {group_list_type}")
+    gl = group_list.to(torch.int64).reshape(-1)
+    ends = gl if group_list_type == 0 else torch.cumsum(gl, 0)
+    return torch.cat([ends.new_zeros(1), ends]).contiguous()
 
 
 # ---------------------------------------------------------------- decode-step harness kernels

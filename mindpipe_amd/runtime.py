@@ -23,8 +23,8 @@ import torch
 
 from . import ops
 
-__all__ = ["W8A8DynamicLinearMethod", "fused_experts_w8a8", "dynamic_quant", "add_rms_norm_forward",
-           "prepare_dense_mlp_w8a8", "dense_mlp_w8a8"]
+__all__ = ["W8A8DynamicLinearMethod", "fused_experts_w8a8", "grouped_apply_mlp_w8a8", "dynamic_quant",
+           "add_rms_norm_forward", "prepare_dense_mlp_w8a8", "dense_mlp_w8a8"]
 
 
 def dynamic_quant(x: torch.Tensor):
@@ -78,15 +78,91 @@ class W8A8DynamicLinearMethod:
         return (output, dynamic_scale) if config.get("return_scale", False) else output
 
 
+_KERNEL_LAYOUT_CACHE = {}
+
+
+def _kernel_layout(w: torch.Tensor, cache_key: str) -> torch.Tensor:
+    """``[E, A, B]`` runtime weight -> contiguous ``[E, B, A]`` kernel layout, cached per source
+    tensor (version-checked), so a layer's transposed weights are materialised once."""
+    key = (cache_key, w.data_ptr(), tuple(w.shape), w._version)
+    t = _KERNEL_LAYOUT_CACHE.get(key)
+    if t is None:
+        t = w.transpose(1, 2).contiguous()
+        if len(_KERNEL_LAYOUT_CACHE) >= 64:
+            _KERNEL_LAYOUT_CACHE.clear()
+        _KERNEL_LAYOUT_CACHE[key] = t
+    return t
+
+
+def _expert_weights(w1, w1_scale, w2, w2_scale, layout):
+    """Weights and fp32 per-row scales in the kernel layout ``w13 [E, 2I, H]`` / ``w2 [E, H, I]``.
+    ``layout="runtime"``: the loaded runtime layout ``w13 [E, H, 2I]`` / ``w2 [E, I, H]``
+    (``vllm_ascend.patch:2278-2291``); scales ``[E, 2I]`` / ``[E, H]`` (or ``[E, N, 1]``) in any
+    float dtype."""
+    if layout == "runtime":
+        w1 = _kernel_layout(w1, "w13")
+        w2 = _kernel_layout(w2, "w2")
+    elif layout != "kernel":
+        raise ValueError(f"layout must be 'kernel' or 'runtime', got {layout!r}")
+    e = w1.shape[0]
+    s1 = w1_scale.reshape(e, -1).to(torch.float32).contiguous()
+    s2 = w2_scale.reshape(e, -1).to(torch.float32).contiguous()
+    return w1, s1, w2, s2
+
+
 def fused_experts_w8a8(hidden_states: torch.Tensor, w1: torch.Tensor, w1_scale: torch.Tensor, w2: torch.Tensor,
                        w2_scale: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
-                       output_dtype: Optional[torch.dtype] = None, **_unused) -> torch.Tensor:
-    """W8A8 MoE experts: routing quant -> grouped GEMM1 + SwiGLU + requant -> grouped GEMM2
-    -> weighted un-permute.  ``w1`` int8 ``[E, 2I, H]`` (gate rows first), ``w2`` int8
-    ``[E, H, I]``, per-row scales ``[E, 2I]`` / ``[E, H]`` (any float dtype)."""
-    return ops.moe_w8a8_forward(hidden_states.contiguous(), topk_ids, topk_weights, w1,
-                                w1_scale.to(torch.float32).contiguous(), w2, w2_scale.to(torch.float32).contiguous(),
-                                out_dtype=output_dtype or hidden_states.dtype)
+                       row_idx: Optional[torch.Tensor] = None, use_int8_w8a8: bool = True,
+                       pertoken_scale: Optional[torch.Tensor] = None, expert_map: Optional[torch.Tensor] = None,
+                       output_dtype: Optional[torch.dtype] = None, layout: str = "kernel",
+                       **_unused) -> torch.Tensor:
+    """The runtime's ``fused_experts(hidden_states, w1, w1_scale, w2, w2_scale, topk_weights,
+    topk_ids, row_idx, use_int8_w8a8=True, pertoken_scale, expert_map, ..., output_dtype)``
+    (``vllm_ascend.patch:4447-4468``) on the gfx950 chain: routing quant -> grouped GEMM1 +
+    SwiGLU + requant -> grouped GEMM2 -> weighted un-permute.
+
+    * ``layout="kernel"``: ``w1`` int8 ``[E, 2I, H]`` (gate rows first), ``w2`` int8 ``[E, H, I]``;
+      ``layout="runtime"``: the loaded runtime layout ``[E, H, 2I]`` / ``[E, I, H]`` (transposed
+      once per weight tensor and cached).
+    * ``pertoken_scale``: ``hidden_states`` is already int8 with these fp32 per-token scales
+      (routed without re-quantizing); ``output_dtype`` then defaults to fp16.
+    * ``expert_map`` (expert parallelism: global -> local id, -1 = not on this rank): ids are
+      mapped and assignments to other ranks contribute nothing.
+    * ``row_idx`` is accepted for signature compatibility; the routing kernel builds its own.
+    """
+    if not use_int8_w8a8:
+        raise NotImplementedError("fused_experts_w8a8 is the int8 W8A8 path")
+    w1, s1, w2, s2 = _expert_weights(w1, w1_scale, w2, w2_scale, layout)
+    ids = topk_ids.to(torch.int32)
+    if expert_map is not None:
+        ids = expert_map.to(device=ids.device, dtype=torch.int32)[ids.long()]
+    if pertoken_scale is not None:
+        return ops.moe_w8a8_forward(hidden_states.contiguous(), ids.contiguous(), topk_weights, w1, s1, w2, s2,
+                                    out_dtype=output_dtype or torch.float16, rule="runtime",
+                                    x_scale=pertoken_scale.reshape(-1).to(torch.float32).contiguous())
+    return ops.moe_w8a8_forward(hidden_states.contiguous(), ids.contiguous(), topk_weights, w1, s1, w2, s2,
+                                out_dtype=output_dtype or hidden_states.dtype, rule="runtime")
+
+
+def grouped_apply_mlp_w8a8(hidden_states: torch.Tensor, w1: torch.Tensor, w1_scale: torch.Tensor, w2: torch.Tensor,
+                           w2_scale: torch.Tensor, group_list: torch.Tensor, group_list_type: int = 0,
+                           dynamic_scale: Optional[torch.Tensor] = None, output_dtype: Optional[torch.dtype] = None,
+                           layout: str = "kernel") -> torch.Tensor:
+    """The runtime's ``quant_apply_mlp`` on already-permuted rows (``vllm_ascend.patch:2895-2964``):
+    ``hidden_states [R, H]`` grouped by expert with ``group_list`` cumulative endpoints
+    (``group_list_type=0``) or raw counts (``1``) (``:2015-2031``); quantized here unless
+    ``dynamic_scale`` marks it as int8 codes.  GEMM1 + SwiGLU + requant, then GEMM2 with the
+    per-token scale, output ``output_dtype`` (default fp16; the reference's default is the down
+    scale's dtype).  There is no 10240-column limit (``_can_use_fused_swiglu_quant``)."""
+    w1, s1, w2, s2 = _expert_weights(w1, w1_scale, w2, w2_scale, layout)
+    offsets = ops.group_offsets_from_list(group_list.to(hidden_states.device), group_list_type)
+    if dynamic_scale is None:
+        qx, sx = dynamic_quant(hidden_states)
+    else:
+        qx, sx = hidden_states.contiguous(), dynamic_scale.reshape(-1).to(torch.float32).contiguous()
+    inter = w2.shape[2]
+    qh, sh = ops.moe_gmm1_swiglu_quant(qx, sx, w1, s1, offsets, inter)
+    return ops.moe_gmm2(qh, sh, w2, s2, offsets, output_dtype or torch.float16)
 
 
 # ---------------------------------------------------------------- add + RMSNorm (+ dynamic quant)

@@ -10,10 +10,12 @@ codes with per-row scales and ``forward`` runs the per-token int8 quantizer and 
 int8 MFMA GEMM (or the MoE chain) instead of fake-quant ``F.linear``.
 
 Scale rule (``scale_rule``):
-  * ``"fake"`` (default for the modules): the fp16 arithmetic of the reference's
-    ``quantize_*_absmax`` -- the int8 codes are bit-identical to the codes the
+  * ``"fake"`` (default for the modules): the arithmetic of the reference's
+    ``quantize_*_absmax`` in the module dtype (fp16 or bf16) -- ``q * s`` is the value the
     reference's fake quantizer rounds to, and outputs match its ``F.linear`` on the
-    fake-quant tensors to fp16 rounding.
+    fake-quant tensors to the output rounding.  The packed MoE experts additionally round
+    gate, up, ``silu(gate)``, ``h``, the down output, the router-weighted rows and every
+    ``index_add_`` step as the reference forward does.
   * ``"export"``: the fp32 rule of the Ascend W8A8 export / runtime
     (``npu_dynamic_quant`` contract), the one ``runtime.W8A8DynamicLinearMethod`` uses.
 """
@@ -35,6 +37,8 @@ __all__ = [
     "SmoothQuantPackedMoeExperts",
     "quantize_llama_like",
     "quantize_model",
+    "text_backbone",
+    "SUPPORTED_MODEL_TYPES",
     "compute_smooth_scales",
     "smooth_ln_fcs_llama_like",
 ]
@@ -45,13 +49,16 @@ def _require_gpu(t: torch.Tensor, what: str) -> None:
         raise RuntimeError(f"{what}: mindpipe_amd runs on the GPU only (tensor is on {t.device})")
 
 
+_FAKE_DTYPES = (torch.float16, torch.bfloat16)
+
+
 @torch.no_grad()
 def quantize_weight_per_channel_absmax(weight: torch.Tensor, n_bits: int = 8) -> torch.Tensor:
-    """Fake-quantized weight (``q * s`` in fp16), as ``fake_quant.py:10-19`` returns it.
+    """Fake-quantized weight (``q * s`` in the weight dtype), as ``fake_quant.py:10-19`` returns it.
 
-    The codes come from the GPU quantizer (fp16 rule); the returned tensor holds the
-    same values as the reference's (the sign of an exact zero is not carried by int8
-    codes).  ``n_bits >= 16`` returns a copy, like the reference.
+    The codes come from the GPU quantizer (fake rule in the weight's dtype, fp16 or bf16);
+    the returned tensor holds the same values as the reference's (the sign of an exact zero
+    is not carried by int8 codes).  ``n_bits >= 16`` returns a copy, like the reference.
     """
     if int(n_bits) >= 16:
         return weight.detach().clone()
@@ -60,15 +67,15 @@ def quantize_weight_per_channel_absmax(weight: torch.Tensor, n_bits: int = 8) ->
     _require_gpu(weight, "quantize_weight_per_channel_absmax")
     shape = weight.shape
     w2 = weight.detach().reshape(-1, shape[-1]).contiguous()
-    if w2.dtype != torch.float16:
-        raise NotImplementedError("the fp16 fake-quant rule takes fp16 weights")
+    if w2.dtype not in _FAKE_DTYPES:
+        raise NotImplementedError("the fake-quant rule takes fp16 or bf16 weights")
     q, s32, _ = ops.w8_quantize_per_channel(w2, "fake")
     return (q.float() * s32[:, None]).to(weight.dtype).reshape(shape)
 
 
 @torch.no_grad()
 def quantize_activation_per_token_absmax(tensor: torch.Tensor, n_bits: int = 8) -> torch.Tensor:
-    """Fake-quantized activation (``q * s`` in fp16), as ``fake_quant.py:22-31`` returns it."""
+    """Fake-quantized activation (``q * s`` in the input dtype), as ``fake_quant.py:22-31`` returns it."""
     if int(n_bits) >= 16:
         return tensor
     if int(n_bits) != 8:
@@ -138,11 +145,18 @@ class SmoothQuantLinear(nn.Module):
             return self.output_quant(F.linear(self.act_quant(x), self.weight, self.bias))
         if self.activation_bits >= 16:
             raise NotImplementedError("W8A16 is not a path of this build (weights int8 need int8 activations)")
-        fp16_rule = self.scale_rule == "fake"
-        if fp16_rule and x.dtype != torch.float16:
-            raise NotImplementedError("the fp16 scale rule takes fp16 activations")
-        q, s = ops.quant_per_token_i8(x.contiguous(), fp16_rule)
-        y = ops.w8a8_gemm(q, s.float().contiguous(), self.weight, self.weight_scale, self.bias, x.dtype)
+        fake = self.scale_rule == "fake"
+        if fake and x.dtype not in _FAKE_DTYPES:
+            raise NotImplementedError("the fake scale rule takes fp16 or bf16 activations")
+        q, s = ops.quant_per_token_i8(x.contiguous(), fake)
+        if fake and x.dtype == torch.bfloat16:
+            # bf16 keeps 8 significant bits: the reference multiplies the bf16-rounded fake values
+            # r(q * s), which the int8 product of q * s misses by ~3e-3; the dequantising GEMM
+            # rounds each element as the reference does
+            bias = None if self.bias is None else self.bias.to(torch.bfloat16)
+            y = ops.w8a8_gemm_fake(q, s.float().contiguous(), self.weight, self.weight_scale, bias, x.dtype)
+        else:
+            y = ops.w8a8_gemm(q, s.float().contiguous(), self.weight, self.weight_scale, self.bias, x.dtype)
         return self.output_quant(y)
 
     @staticmethod
@@ -182,10 +196,12 @@ class SmoothQuantPackedMoeExperts(nn.Module):
     """Packed W8A8 experts: ``gate_up_proj`` int8 ``[E,2I,H]``, ``down_proj`` int8 ``[E,H,I]``
     with per-row fp32 scales; ``forward(hidden_states, top_k_index, top_k_weights)`` as
     ``fake_quant.py:166-191``.  The chain runs as routing+quant -> grouped GEMM1 +
-    SwiGLU + requant -> grouped GEMM2 -> weighted un-permute (the runtime contract of
-    ``vllm_ascend.patch:2356-2423``); ``act_fn`` must be SiLU (the fused SwiGLU)."""
+    SwiGLU + requant -> grouped GEMM2 -> un-permute (one launch each).  With
+    ``scale_rule="fake"`` (default) every step rounds as the reference module does, in the
+    weight dtype (fp16 / bf16); ``"export"`` is the fp32-scale runtime chain of
+    ``vllm_ascend.patch:2356-2423``.  ``act_fn`` must be SiLU (the fused SwiGLU)."""
 
-    def __init__(self, gate_up_proj, down_proj, act_fn, *, weight_bits=8, activation_bits=8, scale_rule="export"):
+    def __init__(self, gate_up_proj, down_proj, act_fn, *, weight_bits=8, activation_bits=8, scale_rule="fake"):
         super().__init__()
         self.num_experts = int(gate_up_proj.shape[0])
         self.hidden_dim = int(gate_up_proj.shape[2])
@@ -196,9 +212,13 @@ class SmoothQuantPackedMoeExperts(nn.Module):
             raise NotImplementedError("the packed MoE path is W8A8")
         if not _is_silu(act_fn):
             raise NotImplementedError(f"the fused expert kernel computes SiLU(gate) * up; got {act_fn!r}")
+        if scale_rule not in ("fake", "export"):
+            raise ValueError(f"Invalid scale_rule: {scale_rule}")
+        if scale_rule == "fake" and gate_up_proj.dtype not in _FAKE_DTYPES:
+            raise NotImplementedError("the fake scale rule takes fp16 or bf16 expert weights")
         self.act_fn = act_fn
+        self.scale_rule = scale_rule
         _require_gpu(gate_up_proj, "SmoothQuantPackedMoeExperts")
-        e, two_i, h = gate_up_proj.shape
         q13, s13 = self._quant3d(gate_up_proj, scale_rule)
         q2, s2 = self._quant3d(down_proj, scale_rule)
         self.register_buffer("gate_up_proj", q13)
@@ -214,18 +234,24 @@ class SmoothQuantPackedMoeExperts(nn.Module):
         return q.reshape(e, n, k), s32.reshape(e, n)
 
     @staticmethod
-    def from_float(module, weight_bits=8, activation_bits=8, scale_rule="export"):
+    def from_float(module, weight_bits=8, activation_bits=8, scale_rule="fake"):
         return SmoothQuantPackedMoeExperts(module.gate_up_proj.detach(), module.down_proj.detach(), module.act_fn,
                                            weight_bits=weight_bits, activation_bits=activation_bits,
                                            scale_rule=scale_rule)
+
+    def dequantized_weights(self):
+        """The fake-quant ``(gate_up_proj, down_proj)`` the reference module holds (``q * s``)."""
+        return ((self.gate_up_proj.float() * self.gate_up_scale[..., None]).to(self.dtype),
+                (self.down_proj.float() * self.down_scale[..., None]).to(self.dtype))
 
     @torch.no_grad()
     def forward(self, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
                 top_k_weights: torch.Tensor) -> torch.Tensor:
         _require_gpu(hidden_states, "SmoothQuantPackedMoeExperts")
+        rule = "fake" if self.scale_rule == "fake" else "runtime"
         return ops.moe_w8a8_forward(hidden_states.contiguous(), top_k_index, top_k_weights, self.gate_up_proj,
                                     self.gate_up_scale, self.down_proj, self.down_scale,
-                                    out_dtype=hidden_states.dtype)
+                                    out_dtype=hidden_states.dtype, rule=rule)
 
     def __repr__(self):
         return (f"SmoothQuantPackedMoeExperts(num_experts={self.num_experts}, "
@@ -233,69 +259,121 @@ class SmoothQuantPackedMoeExperts(nn.Module):
                 f"weight_bits={self.weight_bits}, activation_bits={self.activation_bits})")
 
 
-_SUPPORTED = {"llama", "qwen2", "qwen3", "qwen3_moe", "mixtral", "mistral", "minicpm"}
+# model types quantize_llama_like accepts (fake_quant.py:227-239)
+SUPPORTED_MODEL_TYPES = frozenset({"llama", "qwen2", "qwen2_5_vl", "qwen3", "qwen3_moe", "qwen3_vl", "qwen3_5",
+                                   "qwen3_5_moe", "qwen3_5_moe_text", "minicpm", "minicpmv"})
+# accepted only with ``allow_extension_models=True``: the HF Mixtral / Mistral decoders
+# (packed ``mlp.experts`` like qwen3_moe, or a dense MLP), which the reference router rejects
+# but its serving runtime routes (``packed_modules_model_mapping``, vllm_ascend.patch:3473-3484)
+EXTENSION_MODEL_TYPES = frozenset({"mixtral", "mistral"})
 
 
-def _text_layers(model):
-    inner = getattr(model, "model", model)
-    if hasattr(inner, "language_model"):
-        inner = inner.language_model
-    layers = getattr(inner, "layers", None)
-    if layers is None:
-        raise ValueError("model has no decoder layers (expected model.model.layers)")
-    prefix = "model" if hasattr(model, "model") else ""
-    return layers, prefix
+def text_backbone(model):
+    """``(root, prefix)`` of the decoder stack, resolved in the order of the reference's
+    ``get_text_backbone`` (``algorithm/common/modeling.py``): a text-model adapter, ``llm.model``
+    (MiniCPM-V), ``model.language_model`` (Qwen2.5-VL / Qwen3-VL; or its ``.model`` for
+    LLaVA-style wrappers), ``language_model``, ``model``, ``model.decoder``, ``transformer``
+    (``h``)."""
+    tm = getattr(model, "text_model", None)
+    if tm is not None:
+        if hasattr(getattr(tm, "model", None), "layers"):
+            return tm.model, "text_model.model"
+        if hasattr(tm, "layers"):
+            return tm, "text_model"
+    llm = getattr(model, "llm", None)
+    if llm is not None and hasattr(getattr(llm, "model", None), "layers"):
+        return llm.model, "llm.model"
+    inner = getattr(model, "model", None)
+    lm = getattr(inner, "language_model", None) if inner is not None else None
+    if lm is not None:
+        if hasattr(lm, "layers"):
+            return lm, "model.language_model"
+        if hasattr(getattr(lm, "model", None), "layers"):
+            return lm.model, "model.language_model.model"
+    if hasattr(getattr(model, "language_model", None), "layers"):
+        return model.language_model, "language_model"
+    if inner is not None and hasattr(inner, "layers"):
+        return inner, "model"
+    if inner is not None and hasattr(getattr(inner, "decoder", None), "layers"):
+        return inner.decoder, "model.decoder"
+    if hasattr(getattr(model, "transformer", None), "h"):
+        return model.transformer, "transformer"
+    raise NotImplementedError(f"Unsupported model backbone: {type(model)}")
 
 
-def _swap(parent, name, qualified, names, **kw):
-    setattr(parent, name, SmoothQuantLinear.from_float(getattr(parent, name), **kw))
-    names.append(qualified)
+def _layers_of(root):
+    return root.layers if hasattr(root, "layers") else root.h
 
 
 def quantize_llama_like(model, weight_bits=8, activation_bits=8, act_quant="per_token", quantize_bmm_input=True,
-                        scale_rule="fake") -> List[str]:
-    """Module-swap router (``fake_quant.py:226-438``): q/k/v (with output quant when
-    ``quantize_bmm_input``), o, gate/up/down; packed experts become
-    ``SmoothQuantPackedMoeExperts``.  Returns the qualified names, in the reference's order."""
+                        scale_rule="fake", *, allow_extension_models=False) -> List[str]:
+    """Module-swap router (``fake_quant.py:226-438``): per decoder layer, q/k/v (output quant
+    when ``quantize_bmm_input``) and o; for Qwen3.5 linear-attention layers ``in_proj_qkv /
+    in_proj_z / in_proj_a / in_proj_b`` (output quant) and ``out_proj``; the Qwen3.5-MoE
+    ``shared_expert`` gate/up/down and ``shared_expert_gate``; packed experts become
+    ``SmoothQuantPackedMoeExperts`` (per-expert ``nn.ModuleList`` experts of qwen3_moe swap
+    their linears); every other model's MLP gate/up/down.  Returns the qualified names in
+    the reference's order."""
     model_type = getattr(getattr(model, "config", None), "model_type", None)
-    if model_type not in _SUPPORTED:
+    allowed = SUPPORTED_MODEL_TYPES | (EXTENSION_MODEL_TYPES if allow_extension_models else frozenset())
+    if model_type not in allowed:
         raise ValueError(f"Unsupported model type: {model_type!r}")
-    layers, prefix = _text_layers(model)
+    root, prefix = text_backbone(model)
     names: List[str] = []
-    kw = dict(weight_bits=weight_bits, activation_bits=activation_bits, act_quant=act_quant,
-              scale_rule=scale_rule)
-    for li, layer in enumerate(layers):
-        lp = f"{prefix}.layers.{li}" if prefix else f"layers.{li}"
-        attn = layer.self_attn
+    kw = dict(weight_bits=weight_bits, activation_bits=activation_bits, act_quant=act_quant, scale_rule=scale_rule)
+
+    def swap(parent, attr, qualified, qout=False):
+        setattr(parent, attr, SmoothQuantLinear.from_float(getattr(parent, attr), quantize_output=qout, **kw))
+        names.append(qualified)
+
+    def attention(layer, lp):
+        if model_type in ("qwen3_5", "qwen3_5_moe", "qwen3_5_moe_text") and \
+                getattr(layer, "layer_type", None) == "linear_attention":
+            la = layer.linear_attn
+            for p in ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b"):
+                swap(la, p, f"{lp}.linear_attn.{p}", quantize_bmm_input)
+            swap(la, "out_proj", f"{lp}.linear_attn.out_proj")
+            return
         for p in ("q_proj", "k_proj", "v_proj"):
-            _swap(attn, p, f"{lp}.self_attn.{p}", names, quantize_output=quantize_bmm_input, **kw)
-        _swap(attn, "o_proj", f"{lp}.self_attn.o_proj", names, **kw)
-        mlp = getattr(layer, "mlp", None) or getattr(layer, "block_sparse_moe", None)
-        experts = getattr(mlp, "experts", None)
-        if experts is not None:
-            mlp_name = "mlp" if hasattr(layer, "mlp") else "block_sparse_moe"
-            if isinstance(experts, nn.ModuleList):
-                for ei, ex in enumerate(experts):
+            swap(layer.self_attn, p, f"{lp}.self_attn.{p}", quantize_bmm_input)
+        swap(layer.self_attn, "o_proj", f"{lp}.self_attn.o_proj")
+
+    def packed_experts(mlp, lp):
+        mlp.experts = SmoothQuantPackedMoeExperts.from_float(mlp.experts, weight_bits=weight_bits,
+                                                             activation_bits=activation_bits, scale_rule=scale_rule)
+        names.append(f"{lp}.mlp.experts.gate_up_proj")
+        names.append(f"{lp}.mlp.experts.down_proj")
+
+    for li, layer in enumerate(_layers_of(root)):
+        lp = f"{prefix}.layers.{li}"
+        attention(layer, lp)
+        mlp = layer.mlp
+        if model_type in ("qwen3_5_moe", "qwen3_5_moe_text"):
+            for p in ("gate_proj", "up_proj", "down_proj"):
+                swap(mlp.shared_expert, p, f"{lp}.mlp.shared_expert.{p}")
+            swap(mlp, "shared_expert_gate", f"{lp}.mlp.shared_expert_gate")
+            packed_experts(mlp, lp)
+        elif model_type in ("qwen3_moe", "mixtral") and hasattr(mlp, "experts"):
+            if isinstance(mlp.experts, nn.ModuleList):
+                for ei, ex in enumerate(mlp.experts):
                     for p in ("gate_proj", "up_proj", "down_proj"):
-                        _swap(ex, p, f"{lp}.{mlp_name}.experts.{ei}.{p}", names, **kw)
+                        swap(ex, p, f"{lp}.mlp.experts.{ei}.{p}")
             else:
-                mlp.experts = SmoothQuantPackedMoeExperts.from_float(experts, weight_bits=weight_bits,
-                                                                     activation_bits=activation_bits)
-                names.append(f"{lp}.{mlp_name}.experts.gate_up_proj")
-                names.append(f"{lp}.{mlp_name}.experts.down_proj")
+                packed_experts(mlp, lp)
         else:
             for p in ("gate_proj", "up_proj", "down_proj"):
-                _swap(mlp, p, f"{lp}.mlp.{p}", names, **kw)
+                swap(mlp, p, f"{lp}.mlp.{p}")
     return names
 
 
 def quantize_model(model, weight_bits=8, activation_bits=8, weight_quant="per_channel", act_quant="per_token",
-                   quantize_bmm_input=True, scale_rule="fake") -> List[str]:
+                   quantize_bmm_input=True, scale_rule="fake", *, allow_extension_models=False) -> List[str]:
     """``fake_quant.py:441-457``."""
     if weight_quant != "per_channel":
         raise ValueError(f"Invalid weight_quant: {weight_quant}")
     return quantize_llama_like(model, weight_bits=weight_bits, activation_bits=activation_bits,
-                               act_quant=act_quant, quantize_bmm_input=quantize_bmm_input, scale_rule=scale_rule)
+                               act_quant=act_quant, quantize_bmm_input=quantize_bmm_input, scale_rule=scale_rule,
+                               allow_extension_models=allow_extension_models)
 
 
 @torch.no_grad()

@@ -63,9 +63,10 @@ class RealQuantLinearArtifact:
 def pseudo_quantize_tensor(w, n_bit=8, zero_point=True, q_group_size=-1, inplace=False, get_scale_zp=False):
     """AWQ pseudo-quantization on the GPU, same signature and results as the reference.
 
-    Only ``n_bit=4`` is a kernel of this build.  Returns the fp16 dequantized weight
-    (bit-identical to the reference's), plus ``scales``/``zeros`` ``[N, K/g]`` when
-    ``get_scale_zp`` (zero_point only, as in the reference).
+    Only ``n_bit=4`` is a kernel of this build; fp16 and bf16 weights are quantized in their
+    own arithmetic.  Returns the dequantized weight (bit-identical to the reference's), plus
+    ``scales``/``zeros`` ``[N, K/g]`` when ``get_scale_zp`` (zero_point only, as in the
+    reference).
     """
     if n_bit != 4:
         raise NotImplementedError("mindpipe_amd implements the 4-bit AWQ quantizer")
@@ -74,8 +75,8 @@ def pseudo_quantize_tensor(w, n_bit=8, zero_point=True, q_group_size=-1, inplace
     src = _gpu(w.detach())
     shape = src.shape
     w2 = src.reshape(-1, shape[-1]).contiguous()
-    if w2.dtype != torch.float16:
-        raise NotImplementedError("the AWQ quantizer takes fp16 weights (fp16 arithmetic of the reference)")
+    if w2.dtype not in (torch.float16, torch.bfloat16):
+        raise NotImplementedError("the AWQ quantizer takes fp16 or bf16 weights (the reference's arithmetic)")
     packed, s, z, deq = ops.w4_quantize_awq(w2, q_group_size, zero_point, return_deq=True)
     deq = deq.reshape(shape).to(w.device)
     if inplace:
@@ -111,20 +112,24 @@ def unpack_int4(packed: torch.Tensor, columns: int) -> torch.Tensor:
 
 
 class W4A16Linear(nn.Module):
-    """Real int4 linear: ``weight_packed`` int32 ``[N, K/8]``, ``weight_scale`` fp16 ``[N, K/g]``,
-    ``weight_zero_point`` fp16 ``[N, K/g]`` (AWQ asymmetric) or ``None`` (symmetric,
-    zero point 8), ``weight_shape`` int64 ``[2]``, ``bias``; ``forward`` runs the W4A16 kernel."""
+    """Real int4 linear: ``weight_packed`` int32 ``[N, K/8]``, ``weight_scale`` ``[N, K/g]``,
+    ``weight_zero_point`` ``[N, K/g]`` (AWQ asymmetric) or ``None`` (symmetric, zero point 8),
+    ``weight_shape`` int64 ``[2]``, ``bias``; scales, zeros and bias in the module dtype (fp16
+    or bf16, the dtype of the activations); ``forward`` runs the W4A16 kernel."""
 
     def __init__(self, in_features: int, out_features: int, group_size: int = 128, bias: bool = True,
                  zero_point: bool = True, dtype=torch.float16, device=None):
         super().__init__()
         if in_features % 8 or in_features % group_size:
             raise ValueError("in_features must be a multiple of 8 and of group_size")
+        if dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError("W4A16Linear computes in fp16 or bf16")
         self.in_features, self.out_features, self.group_size = in_features, out_features, group_size
+        self.dtype = dtype
         g = in_features // group_size
         self.register_buffer("weight_packed", torch.zeros((out_features, in_features // 8), dtype=torch.int32, device=device))
-        self.register_buffer("weight_scale", torch.ones((out_features, g), dtype=torch.float16, device=device))
-        self.register_buffer("weight_zero_point", torch.full((out_features, g), 8.0, dtype=torch.float16, device=device)
+        self.register_buffer("weight_scale", torch.ones((out_features, g), dtype=dtype, device=device))
+        self.register_buffer("weight_zero_point", torch.full((out_features, g), 8.0, dtype=dtype, device=device)
                              if zero_point else None)
         self.register_buffer("weight_shape", torch.tensor([out_features, in_features], dtype=torch.int64))
         self.register_buffer("bias", torch.zeros(out_features, dtype=dtype, device=device) if bias else None)
@@ -132,9 +137,12 @@ class W4A16Linear(nn.Module):
     @classmethod
     @torch.no_grad()
     def from_float(cls, linear: nn.Linear, group_size: int = 128, zero_point: bool = True) -> "W4A16Linear":
-        w = _gpu(linear.weight.detach()).to(torch.float16).contiguous()
+        """AWQ codes of ``linear.weight`` in its own dtype (bf16 stays bf16, anything else is
+        quantized in fp16)."""
+        dt = linear.weight.dtype if linear.weight.dtype in (torch.float16, torch.bfloat16) else torch.float16
+        w = _gpu(linear.weight.detach()).to(dt).contiguous()
         n, k = w.shape
-        mod = cls(k, n, group_size, linear.bias is not None, zero_point, device=w.device)
+        mod = cls(k, n, group_size, linear.bias is not None, zero_point, dtype=dt, device=w.device)
         packed, s, z, _ = ops.w4_quantize_awq(w, group_size, zero_point, return_deq=False)
         if s.shape[1] != k // group_size:
             raise ValueError("group_size must divide in_features")
@@ -143,7 +151,7 @@ class W4A16Linear(nn.Module):
         if zero_point:
             mod.weight_zero_point.copy_(z)
         if linear.bias is not None:
-            mod.bias.copy_(linear.bias.detach().to(torch.float16))
+            mod.bias.copy_(linear.bias.detach().to(dt))
         return mod
 
     @classmethod
@@ -158,17 +166,20 @@ class W4A16Linear(nn.Module):
         return mod
 
     def dequantized_weight(self) -> torch.Tensor:
-        """``(u - z) * s`` in fp16 (the reference's pseudo-quantized weight for AWQ codes)."""
+        """``(u - z) * s`` in the module dtype (the reference's pseudo-quantized weight for AWQ
+        codes)."""
         u = ops.unpack_int4(self.weight_packed, self.in_features).to(torch.int16) + 8
         s = self.weight_scale.repeat_interleave(self.group_size, dim=1)
         z = (self.weight_zero_point.repeat_interleave(self.group_size, dim=1) if self.weight_zero_point is not None
              else torch.full_like(s, 8.0))
-        return ((u.half() - z) * s).half()
+        return ((u.to(s.dtype) - z) * s).to(s.dtype)
 
     @torch.no_grad()
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not x.is_cuda:
             raise RuntimeError("W4A16Linear runs on the GPU only")
+        if x.dtype != self.weight_scale.dtype:
+            raise RuntimeError(f"W4A16Linear holds {self.weight_scale.dtype} scales; got {x.dtype} activations")
         return ops.w4a16_gemm(x.contiguous(), self.weight_packed, self.weight_scale, self.weight_zero_point,
                               self.group_size, self.bias)
 

@@ -20,10 +20,19 @@ Pinning (how each function is checked; see ``tests/test_oracle.py``)
   answers (pack KAT, export KAT) plus a brute-force bit loop.
 * ``quantize_weight_per_channel_export``: the reference's tiny-Qwen2 export
   fixture values (including the 63.5 / -63.5 ties).
-* ``pseudo_quantize_tensor``: invariants fixed by the definition (codes in
-  [0,15], group min/max map to codes 0/15 up to one rounding step, dequant
-  reconstruction error <= s/2 inside the representable range), a hand-computed
-  case, and a float64 brute force of the same rounding sequence.
+* ``pseudo_quantize_tensor``: the reference's own outputs (fp16: asym, per-row
+  fallback, sym; bf16: asym with a constant group, sym), invariants fixed by the
+  definition (codes in [0,15], group min/max map to codes 0/15 up to one
+  rounding step), a hand-computed case, and a float64 brute force.
+* ``quantize_activation_per_token_fake`` / ``quantize_weight_per_channel_fake``:
+  the reference's own outputs in fp16 and bf16.
+* ``w8a8_linear_fake``: the reference ``SmoothQuantLinear`` forward (fp16, bf16,
+  with and without the output fake-quant), bit-exact.
+* ``compute_smooth_scales``: the reference ``_compute_smooth_scales`` (fp16,
+  bf16, with a clamped column), bit-exact, plus a closed form.
+* ``moe_fake``: the reference ``SmoothQuantPackedMoeExperts`` forward (fp16,
+  bf16, with an all-zero token and a one-token expert), bit-exact, and a planted
+  mistake (gate/up swapped) that lands far from it.
 * ``gptq_rtn_quantize``: the reference's GPTQ reconstruction invariant
   (int in [-8,7], int*scale reproduces the fake-quant weight) and hand cases
   (all-positive rows keep xmin = 0).
@@ -93,6 +102,22 @@ def bf16_bits_to_f32(bits) -> np.ndarray:
     return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def _round_to(x, dt: str) -> np.ndarray:
+    """float32 values rounded once to ``dt`` ("fp16" / "bf16"), returned as float32
+    (the value PyTorch keeps after one op in that dtype)."""
+    x = np.asarray(x, dtype=np.float32)
+    if dt == "fp16":
+        return x.astype(np.float16).astype(np.float32)
+    if dt == "bf16":
+        return bf16_bits_to_f32(f32_to_bf16_bits(x))
+    raise ValueError(dt)
+
+
+def _bits_out(x32: np.ndarray, dt: str) -> np.ndarray:
+    """float32 values that are exact in ``dt`` -> an fp16 array or bf16 uint16 bits."""
+    return np.asarray(x32, np.float32).astype(np.float16) if dt == "fp16" else f32_to_bf16_bits(x32)
+
+
 def _to_out(y_f32: np.ndarray, out_dtype: str) -> np.ndarray:
     if out_dtype == "fp16":
         return y_f32.astype(np.float16)
@@ -110,51 +135,60 @@ def _in_f32(x: np.ndarray, in_dtype: str) -> np.ndarray:
 
 
 # ---------------------------------------------------------------- W4 (AWQ / GPTQ)
-def pseudo_quantize_tensor(w, n_bit=4, zero_point=True, q_group_size=128):
-    """AWQ pseudo-quantization in fp16 arithmetic.
+def pseudo_quantize_tensor(w, n_bit=4, zero_point=True, q_group_size=128, dtype="fp16"):
+    """AWQ pseudo-quantization in the arithmetic of the weight dtype (fp16 or bf16).
 
     Follows ``algorithm/quantization/ptq/awq/source/awq/quantize/quantizer.py:63-105``:
     reshape to ``[-1, g]`` (per-row when g does not divide K, ``:67-68``),
     ``s = (max-min).clamp(1e-5) / (2^n-1)``, ``z = clamp(-round(min/s), 0, 2^n-1)``,
-    ``q = clamp(round(w/s) + z, 0, 2^n-1)``, ``w_deq = (q - z) * s``.
-    ``zero_point=False`` is the symmetric branch (``:79-85``): ``s = max|w|.clamp(1e-5)/(2^(n-1)-1)``,
-    codes in ``[-2^(n-1), 2^(n-1)-1]``.
+    ``q = clamp(round(w/s) + z, 0, 2^n-1)``, ``w_deq = (q - z) * s``, each op rounded
+    once to the weight dtype.  ``zero_point=False`` is the symmetric branch
+    (``:79-85``): ``s = max|w|.clamp(1e-5)/(2^(n-1)-1)``, codes in
+    ``[-2^(n-1), 2^(n-1)-1]``.
 
-    Returns ``(w_deq fp16 [N,K], scales fp16 [N,K/g], zeros fp16 [N,K/g] or None,
-    codes uint8/int8 [N,K])``; the first three are what ``get_scale_zp=True`` returns.
+    ``dtype="fp16"``: ``w`` is a float16 array and the float outputs are float16.
+    ``dtype="bf16"``: ``w`` holds bfloat16 bit patterns (uint16) and so do the outputs.
+
+    Returns ``(w_deq [N,K], scales [N,K/g], zeros [N,K/g] or None, codes uint8/int8 [N,K])``;
+    the first three are what ``get_scale_zp=True`` returns.
     """
-    w = np.asarray(w, dtype=np.float16)
-    if w.ndim != 2:
+    if dtype == "fp16":
+        wf = _f(np.asarray(w, dtype=np.float16))
+    else:
+        wf = bf16_bits_to_f32(w)
+    if wf.ndim != 2:
         raise ValueError("expected a 2-D weight")
-    n_rows, k = w.shape
+    R = lambda v: _round_to(v, dtype)  # noqa: E731
+    n_rows, k = wf.shape
     g = q_group_size
     if g > 0 and k % g != 0:
         g = -1
-    wg = w.reshape(-1, g) if g > 0 else w
+    wg = wf.reshape(-1, g) if g > 0 else wf
+    eps = R(np.float32(1e-5))
     with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
         if zero_point:
             max_val = wg.max(axis=1, keepdims=True)
             min_val = wg.min(axis=1, keepdims=True)
             max_int, min_int = 2**n_bit - 1, 0
-            d = _h(_f(max_val) - _f(min_val))
-            d = np.where(_f(d) < np.float32(1e-5), np.float16(1e-5), d)
-            scales = _h(_f(d) / np.float32(max_int))
-            zeros = np.clip(-np.rint(_h(_f(min_val) / _f(scales))), min_int, max_int).astype(np.float16)
+            d = R(max_val - min_val)
+            d = np.where(d < np.float32(1e-5), eps, d)
+            scales = R(d / np.float32(max_int))
+            zeros = np.clip(-np.rint(R(min_val / scales)), min_int, max_int).astype(np.float32)
         else:
             max_val = np.abs(wg).max(axis=1, keepdims=True)
-            max_val = np.where(_f(max_val) < np.float32(1e-5), np.float16(1e-5), max_val)
+            max_val = np.where(max_val < np.float32(1e-5), eps, max_val)
             max_int, min_int = 2 ** (n_bit - 1) - 1, -(2 ** (n_bit - 1))
-            scales = _h(_f(max_val) / np.float32(max_int))
+            scales = R(max_val / np.float32(max_int))
             zeros = np.zeros_like(scales)
-        t = np.rint(_h(_f(wg) / _f(scales)))
-        q = np.clip(_h(_f(t) + _f(zeros)), min_int, max_int).astype(np.float16)
-        deq = _h(_f(_h(_f(q) - _f(zeros))) * _f(scales))
-    deq = deq.reshape(n_rows, k)
-    scales = scales.reshape(n_rows, -1)
+        t = np.rint(R(wg / scales))
+        q = np.clip(R(t + zeros), min_int, max_int)
+        deq = R(R(q - zeros) * scales)
+    deq = _bits_out(deq.reshape(n_rows, k), dtype)
+    scales_o = _bits_out(scales.reshape(n_rows, -1), dtype)
     codes = q.reshape(n_rows, k).astype(np.int16)
     if zero_point:
-        return deq, scales, zeros.reshape(n_rows, -1), codes.astype(np.uint8)
-    return deq, scales, None, codes.astype(np.int8)
+        return deq, scales_o, _bits_out(zeros.reshape(n_rows, -1), dtype), codes.astype(np.uint8)
+    return deq, scales_o, None, codes.astype(np.int8)
 
 
 def gptq_rtn_quantize(w, bits=4, groupsize=128):
@@ -266,36 +300,42 @@ def dequant_w4_export_fp32(packed, scale, weight_shape):
     return iw * np.repeat(_f(scale), g, axis=1)[:, :cols]
 
 
-def w4a16_linear(x, w_deq, bias=None):
-    """``F.linear(x, w_deq, bias)`` on fp16 operands: fp32 accumulation, one fp16 rounding."""
-    y = _f(x) @ _f(w_deq).T
+def w4a16_linear(x, w_deq, bias=None, dtype="fp16"):
+    """``F.linear(x, w_deq, bias)`` on fp16 (or bf16 bit-pattern) operands: fp32 accumulation,
+    one rounding to the dtype."""
+    y = _in_f32(x, dtype) @ _in_f32(w_deq, dtype).T
     if bias is not None:
-        y = y + _f(bias)
-    return y.astype(np.float16)
+        y = y + _in_f32(bias, dtype)
+    return _to_out(y.astype(np.float32), dtype)
 
 
 # ---------------------------------------------------------------- W8A8 (SmoothQuant)
-def quantize_activation_per_token_fake(x, n_bits=8):
-    """``quantize_activation_per_token_absmax`` in fp16
-    (``algorithm/quantization/ptq/smoothquant/source/smoothquant/fake_quant.py:22-31``).
+def quantize_activation_per_token_fake(x, n_bits=8, dtype="fp16"):
+    """``quantize_activation_per_token_absmax`` in the arithmetic of ``x``'s dtype
+    (``algorithm/quantization/ptq/smoothquant/source/smoothquant/fake_quant.py:22-31``):
+    ``s = (max|x|).clamp(1e-5) / 127``, ``fake = round(x / s) * s``, each op rounded once.
 
-    Returns ``(codes int8, scale fp16 [M], fake fp16)`` where ``fake = q * s``.
+    ``dtype="fp16"``: float16 arrays in and out.  ``dtype="bf16"``: bfloat16 bit patterns
+    (uint16) in and out.  Returns ``(codes int16, scale [M], fake)``: the integer codes
+    ``round(x / s)``, in [-127, 127] for fp16 and [-128, 128] for bf16 (``r(x / s)`` can reach
+    127.5 when the bf16 scale rounds down).
     """
-    x = np.asarray(x, dtype=np.float16)
+    xf = _f(np.asarray(x, dtype=np.float16)) if dtype == "fp16" else bf16_bits_to_f32(x)
+    R = lambda v: _round_to(v, dtype)  # noqa: E731
     q_max = np.float32(2 ** (n_bits - 1) - 1)
     with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
-        s = np.abs(x).max(axis=-1, keepdims=True)
-        s = np.where(_f(s) < np.float32(1e-5), np.float16(1e-5), s)
-        s = _h(_f(s) / q_max)
-        q = np.rint(_h(_f(x) / _f(s)))
-        fake = _h(_f(q) * _f(s))
-    return q.astype(np.int8), s[..., 0], fake
+        s = np.abs(xf).max(axis=-1, keepdims=True)
+        s = np.where(s < np.float32(1e-5), R(np.float32(1e-5)), s)
+        s = R(s / q_max)
+        q = np.rint(R(xf / s))
+        fake = R(q * s)
+    return q.astype(np.int16), _bits_out(s[..., 0], dtype), _bits_out(fake, dtype)
 
 
-def quantize_weight_per_channel_fake(w, n_bits=8):
-    """``quantize_weight_per_channel_absmax`` in fp16 (``fake_quant.py:10-19``).
-    Same arithmetic as the activation quantizer along the last dim."""
-    return quantize_activation_per_token_fake(w, n_bits)
+def quantize_weight_per_channel_fake(w, n_bits=8, dtype="fp16"):
+    """``quantize_weight_per_channel_absmax`` (``fake_quant.py:10-19``): the same
+    arithmetic as the activation quantizer along the last dim."""
+    return quantize_activation_per_token_fake(w, n_bits, dtype)
 
 
 def quantize_per_token_runtime(x, in_dtype="fp16"):
@@ -382,7 +422,12 @@ def int_matmul_nt(a, b) -> np.ndarray:
     b = np.asarray(b)
     if a.shape[-1] > (1 << 20):
         raise ValueError("K too large for the exact float64 path")
-    return np.rint(a.astype(np.float64) @ b.astype(np.float64).T).astype(np.int64)
+    af = a.astype(np.float64)
+    out = np.empty((a.shape[0], b.shape[0]), np.int64)
+    step = max(1, (64 << 20) // max(1, 8 * b.shape[1]))  # ~64 MB of float64 weight rows at a time
+    for r0 in range(0, b.shape[0], step):
+        out[:, r0:r0 + step] = np.rint(af @ b[r0:r0 + step].astype(np.float64).T).astype(np.int64)
+    return out
 
 
 def w8a8_linear_runtime(qx, s_tok, qw, s_ch, bias=None, out_dtype="fp16", bias_dtype="fp16"):
@@ -402,33 +447,38 @@ def w8a8_linear_runtime(qx, s_tok, qw, s_ch, bias=None, out_dtype="fp16", bias_d
     return _to_out(y, out_dtype)
 
 
-def w8a8_linear_fake(x, w, bias=None):
-    """``SmoothQuantLinear.forward`` fake path (``fake_quant.py:85-88``) on fp16 inputs:
-    ``F.linear(fq_token(x), fq_channel(w), b)``; ``w`` is the float weight before
-    ``from_float`` (which applies ``quantize_weight_per_channel_absmax``, ``:110``)."""
-    _, _, xq = quantize_activation_per_token_fake(x)
-    _, _, wq = quantize_weight_per_channel_fake(w)
-    y = _f(xq) @ _f(wq).T
+def w8a8_linear_fake(x, w, bias=None, dtype="fp16"):
+    """``SmoothQuantLinear.forward`` fake path (``fake_quant.py:85-88``):
+    ``F.linear(fq_token(x), fq_channel(w), b)`` with fp32 accumulation and one rounding to
+    ``dtype``; ``w`` is the float weight before ``from_float`` (which applies
+    ``quantize_weight_per_channel_absmax``, ``:110``).  fp16 arrays, or bf16 bit patterns
+    for ``dtype="bf16"``."""
+    _, _, xq = quantize_activation_per_token_fake(x, 8, dtype)
+    _, _, wq = quantize_weight_per_channel_fake(w, 8, dtype)
+    y = _in_f32(xq, dtype) @ _in_f32(wq, dtype).T
     if bias is not None:
-        y = y + _f(bias)
-    return y.astype(np.float16)
+        y = y + _in_f32(bias, dtype)
+    return _to_out(y.astype(np.float32), dtype)
 
 
-def compute_smooth_scales(act_max, weights, alpha=0.5):
-    """``_compute_smooth_scales`` (``smoothquant/smooth.py:7-25``) for fp16 weights:
+def compute_smooth_scales(act_max, weights, alpha=0.5, dtype="fp16"):
+    """``_compute_smooth_scales`` (``smoothquant/smooth.py:7-25``):
     ``s_j = (a_j^alpha / w_j^(1-alpha)).clamp(1e-5)`` in the weight dtype, where
-    ``a_j`` is the calibration abs-max cast to fp16 and ``w_j = max_n |W_nj|``
-    (max over every fc sharing the norm, clamped at 1e-5)."""
-    a = np.asarray(act_max, dtype=np.float32).astype(np.float16)
+    ``a_j`` is the calibration abs-max (fp32) cast to that dtype and
+    ``w_j = max_n |W_nj|`` (max over every fc sharing the norm, clamped at 1e-5).
+    fp16 arrays, or bf16 bit patterns (weights and result) for ``dtype="bf16"``."""
+    R = lambda v: _round_to(v, dtype)  # noqa: E731
+    a = R(np.asarray(act_max, dtype=np.float32))
     if not isinstance(weights, (list, tuple)):
         weights = [weights]
-    wmax = np.max(np.stack([np.abs(np.asarray(w, np.float16)).max(axis=0) for w in weights]), axis=0)
-    wmax = np.where(_f(wmax) < np.float32(1e-5), np.float16(1e-5), wmax)
+    wmax = np.max(np.stack([np.abs(_in_f32(np.asarray(w), dtype)).max(axis=0) for w in weights]), axis=0)
+    wmax = np.where(wmax < np.float32(1e-5), R(np.float32(1e-5)), wmax)
     with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
-        num = _h(np.power(_f(a), np.float32(alpha)))
-        den = _h(np.power(_f(wmax), np.float32(1 - alpha)))
-        s = _h(_f(num) / _f(den))
-    return np.where(_f(s) < np.float32(1e-5), np.float16(1e-5), s)
+        num = R(np.power(a, np.float32(alpha)))
+        den = R(np.power(wmax, np.float32(1 - alpha)))
+        sc = R(num / den)
+    sc = np.where(sc < np.float32(1e-5), R(np.float32(1e-5)), sc)
+    return _bits_out(sc, dtype)
 
 
 # ---------------------------------------------------------------- MoE
@@ -529,29 +579,35 @@ def dense_mlp_runtime(x, qw13, s13, qw2, s2, chunks=1, out_dtype="fp16", qx=None
     return _to_out(out, out_dtype)
 
 
-def moe_fake(x, topk_ids, topk_w, gate_up_proj, down_proj):
-    """``SmoothQuantPackedMoeExperts.forward`` fake path (``fake_quant.py:166-191``)
-    on fp16 weights ``gate_up_proj [E,2I,H]`` / ``down_proj [E,H,I]`` with SiLU.
-    fp16 rounding after every op, router weights fp32, ``index_add_`` into fp16
-    in ascending expert order."""
-    x = np.asarray(x, np.float16)
+def moe_fake(x, topk_ids, topk_w, gate_up_proj, down_proj, dtype="fp16"):
+    """``SmoothQuantPackedMoeExperts`` construction + ``forward`` fake path
+    (``fake_quant.py:124-191``) with SiLU: per-channel fake-quant weights
+    ``gate_up_proj [E,2I,H]`` / ``down_proj [E,H,I]``; for each hit expert in ascending
+    order, per-token fake quant of its tokens, ``F.linear`` (fp32 accumulation, one
+    rounding), ``chunk(2)``, ``silu(gate) * up`` (two roundings), per-token fake quant,
+    ``F.linear``, times the fp32 router weight (rounded once), ``index_add_`` (one
+    rounding per add).  Every rounding is to ``dtype``; fp16 arrays, or bf16 bit
+    patterns for ``dtype="bf16"`` (router weights fp32 in both cases)."""
+    R = lambda v: _round_to(v, dtype)  # noqa: E731
+    F32 = lambda a: _in_f32(np.asarray(a), dtype)  # noqa: E731
+    xf = F32(x)
     n_exp = gate_up_proj.shape[0]
-    wq13 = [quantize_weight_per_channel_fake(gate_up_proj[e])[2] for e in range(n_exp)]
-    wq2 = [quantize_weight_per_channel_fake(down_proj[e])[2] for e in range(n_exp)]
-    out = np.zeros_like(x)
+    wq13 = [F32(quantize_weight_per_channel_fake(gate_up_proj[e], 8, dtype)[2]) for e in range(n_exp)]
+    wq2 = [F32(quantize_weight_per_channel_fake(down_proj[e], 8, dtype)[2]) for e in range(n_exp)]
+    out = np.zeros_like(xf)
     inter = down_proj.shape[2]
     for e in range(n_exp):
         top_k_pos, token_idx = np.nonzero((topk_ids == e).T)
         if token_idx.size == 0:
             continue
-        cur = quantize_activation_per_token_fake(x[token_idx])[2]
-        gu = _h(_f(cur) @ _f(wq13[e]).T)
+        cur = F32(quantize_activation_per_token_fake(_bits_out(xf[token_idx], dtype), 8, dtype)[2])
+        gu = R(cur @ wq13[e].T)
         gate, up = gu[:, :inter], gu[:, inter:]
-        act = _h(_silu(_f(gate)))
-        hcur = _h(_f(act) * _f(up))
-        hcur = quantize_activation_per_token_fake(hcur)[2]
-        y = _h(_f(hcur) @ _f(wq2[e]).T)
-        y = (_f(y) * _f(topk_w[token_idx, top_k_pos])[:, None]).astype(np.float32).astype(np.float16)
+        act = R(_silu(gate))
+        hcur = R(act * up)
+        hcur = F32(quantize_activation_per_token_fake(_bits_out(hcur, dtype), 8, dtype)[2])
+        y = R(hcur @ wq2[e].T)
+        y = R(y * _f(topk_w[token_idx, top_k_pos])[:, None])
         for r, t in enumerate(token_idx):
-            out[t] = _h(_f(out[t]) + _f(y[r]))
-    return out
+            out[t] = R(out[t] + y[r])
+    return _bits_out(out, dtype)

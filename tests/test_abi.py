@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), name
     assert set(_declared()) == set(_lib.SIGNATURES)
-    assert lib.mp_abi_version() == 1
+    assert lib.mp_abi_version() == _lib.ABI_VERSION
     assert lib.mp_strerror(1).decode().startswith("mindpipe_amd")
 
 
@@ -41,4 +41,5 @@ def test_host_validation_without_gpu():
     assert lib.mp_w8a8_gemm(1, 1, 1, 1, None, 0, 1, 9, 1, 16, 64, None) == 2      # bad out dtype
     assert lib.mp_w8a8_gemm(1, 1, 1, 1, None, 0, 1, 0, 1, 16, 1 << 18, None) == 1  # K too large for int32
     assert lib.mp_quant_per_token_i8(1, 4, 64, 7, 1, 1, 0, None) == 2
-    assert lib.mp_i8_gemm_swiglu_requant(1, 1, 1, 1, 1, 8, 16, 64, 128, 1, 1, 1, 0, None) == 6
+    assert lib.mp_i8_gemm_swiglu_requant(1, 1, 1, 1, 1, 8, 16, 64, 128, 0, 0, 1, 1, 1, 0, None) == 6
+    assert lib.mp_moe_unpermute_combine(1, 1, 1, 4, 2, 64, 1, 1, 2, None) == 2   # fake rule needs fp16/bf16 out

@@ -14,6 +14,7 @@ from oracle import quant as O
 
 pytestmark = pytest.mark.gpu
 GOLD = np.load(Path(__file__).parent / "golden" / "reference_vectors.npz")
+EXT = np.load(Path(__file__).parent / "golden" / "reference_ext_vectors.npz")
 DEV = "cuda:0"
 
 
@@ -108,6 +109,10 @@ def test_quantize_model_tiny_llama_names_and_forward():
 
 
 def test_quantize_model_tiny_mixtral_packed_experts():
+    """Mixtral is outside the reference's allow-list: rejected by default, accepted as an
+    extension (packed experts like qwen3_moe).  The packed experts follow the reference
+    module's fake-quant forward (oracle.moe_fake) by default and the fp32 runtime chain
+    (oracle.moe_runtime) with scale_rule="export"."""
     _say("quantize_model mixtral")
     from transformers import MixtralConfig, MixtralForCausalLM
     from mindpipe_amd.smoothquant import SmoothQuantPackedMoeExperts, quantize_model
@@ -115,29 +120,127 @@ def test_quantize_model_tiny_mixtral_packed_experts():
     cfg = MixtralConfig(hidden_size=256, intermediate_size=384, num_hidden_layers=1, num_attention_heads=4,
                         num_key_value_heads=2, vocab_size=512, num_local_experts=4, num_experts_per_tok=2)
     model = MixtralForCausalLM(cfg).half().to(DEV).eval()
+    with pytest.raises(ValueError, match="Unsupported model type"):
+        quantize_model(model)
     experts = model.model.layers[0].mlp.experts
     gu = experts.gate_up_proj.detach().clone()
     dn = experts.down_proj.detach().clone()
-    names = quantize_model(model)
+    names = quantize_model(model, allow_extension_models=True)
     assert names[-2:] == ["model.layers.0.mlp.experts.gate_up_proj", "model.layers.0.mlp.experts.down_proj"]
     mod = model.model.layers[0].mlp.experts
     assert isinstance(mod, SmoothQuantPackedMoeExperts)
     assert repr(mod) == ("SmoothQuantPackedMoeExperts(num_experts=4, hidden_dim=256, intermediate_dim=384, "
                          "weight_bits=8, activation_bits=8)")
-    # expert chain vs the oracle on the same codes / routing
     t = 40
     x = torch.randn(t, 256, generator=torch.Generator().manual_seed(1)).half()
     ids, tw = O.mixtral_router(np.random.default_rng(2).standard_normal((t, 4)).astype(np.float32), 2)
     y = mod(x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(tw).to(DEV)).float().cpu().numpy()
-    q13 = np.stack([O.quantize_weight_per_channel_export(gu[e].cpu().numpy())[0] for e in range(4)])
-    s13 = np.stack([O.quantize_weight_per_channel_export(gu[e].cpu().numpy())[1] for e in range(4)])
-    q2 = np.stack([O.quantize_weight_per_channel_export(dn[e].cpu().numpy())[0] for e in range(4)])
-    s2 = np.stack([O.quantize_weight_per_channel_export(dn[e].cpu().numpy())[1] for e in range(4)])
-    assert np.array_equal(mod.gate_up_proj.cpu().numpy(), q13)
-    ref = O.moe_runtime(x.numpy(), ids, tw, q13, s13, q2, s2)
+    gun, dnn = gu.cpu().numpy(), dn.cpu().numpy()
+    gq, dq = mod.dequantized_weights()   # values (int8 codes carry no sign of zero)
+    assert np.array_equal(gq.float().cpu().numpy(),
+                          np.stack([O.quantize_weight_per_channel_fake(gun[e])[2] for e in range(4)]).astype(np.float32))
+    ref = O.moe_fake(x.numpy(), ids, tw, gun, dnn)
     assert _rel(y, ref.astype(np.float32)) <= 1e-3
+    # the runtime rule: export-rule codes and the fp32 chain
+    modr = SmoothQuantPackedMoeExperts(gu, dn, torch.nn.SiLU(), scale_rule="export")
+    yr = modr(x.to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(tw).to(DEV)).float().cpu().numpy()
+    q13 = np.stack([O.quantize_weight_per_channel_export(gun[e])[0] for e in range(4)])
+    s13 = np.stack([O.quantize_weight_per_channel_export(gun[e])[1] for e in range(4)])
+    q2 = np.stack([O.quantize_weight_per_channel_export(dnn[e])[0] for e in range(4)])
+    s2 = np.stack([O.quantize_weight_per_channel_export(dnn[e])[1] for e in range(4)])
+    assert np.array_equal(modr.gate_up_proj.cpu().numpy(), q13)
+    assert _rel(yr, O.moe_runtime(x.numpy(), ids, tw, q13, s13, q2, s2).astype(np.float32)) <= 1e-3
     with torch.no_grad():
         model(torch.randint(0, 512, (1, 9), device=DEV))
+
+
+@pytest.mark.parametrize("tag,dt", [("f16", "fp16"), ("bf16", "bf16")])
+def test_smoothquant_linear_matches_reference_outputs(tag, dt):
+    """SmoothQuantLinear.from_float + forward in fp16 and bf16 against the outputs the
+    reference module wrote (fake_quant.py:85-113): rel. Frobenius error <= 1e-3; with the
+    output fake-quant, the module's output is the fake rule applied to its own linear output."""
+    _say("SmoothQuantLinear fixture", dt)
+    from mindpipe_amd.smoothquant import SmoothQuantLinear
+    tdt = torch.float16 if dt == "fp16" else torch.bfloat16
+
+    def cv(a):
+        t = torch.from_numpy(np.ascontiguousarray(a))
+        return (t if dt == "fp16" else t.view(torch.bfloat16)).to(DEV)
+
+    def f32(t):
+        return t.float().cpu().numpy()
+
+    w, b, x = cv(EXT[f"sql_{tag}_w"]), cv(EXT[f"sql_{tag}_b"]), cv(EXT[f"sql_{tag}_x"])
+    lin = nn.Linear(w.shape[1], w.shape[0], bias=True).to(device=DEV, dtype=tdt)
+    with torch.no_grad():
+        lin.weight.copy_(w)
+        lin.bias.copy_(b)
+    ref = cv(EXT[f"sql_{tag}_y"])
+    mod = SmoothQuantLinear.from_float(lin)
+    y = mod(x)
+    assert y.dtype == tdt
+    assert _rel(f32(y), f32(ref)) <= 1e-3     # bar: rel. Frobenius error <= 1e-3
+    modq = SmoothQuantLinear.from_float(lin, quantize_output=True)
+    yq = modq(x)
+    from mindpipe_amd.smoothquant import quantize_activation_per_token_absmax
+    assert torch.equal(yq, quantize_activation_per_token_absmax(y))
+    assert _rel(f32(yq), f32(cv(EXT[f"sql_{tag}_yq"]))) <= 1e-2   # re-quantized: a code step is 1/127
+
+
+def test_runtime_fused_experts_contract():
+    """fused_experts_w8a8 on the runtime's loaded layout (w13 [E,H,2I], w2 [E,I,H], bf16 scales),
+    a pre-quantized input with pertoken_scale, and an expert_map; grouped_apply_mlp_w8a8 with
+    group_list types 0 and 1 (vllm_ascend.patch:2015-2031, 2278-2291, 4447-4468)."""
+    _say("runtime fused_experts")
+    from mindpipe_amd.runtime import dynamic_quant, fused_experts_w8a8, grouped_apply_mlp_w8a8
+    from mindpipe_amd import ops
+    rng = np.random.default_rng(8)
+    t, h, inter, e = 64, 256, 192, 4
+    x = rng.standard_normal((t, h)).astype(np.float16)
+    ids, tw = O.mixtral_router(rng.standard_normal((t, e)).astype(np.float32), 2)
+    gu = (rng.standard_normal((e, 2 * inter, h)) * 0.02).astype(np.float16)
+    dn = (rng.standard_normal((e, h, inter)) * 0.02).astype(np.float16)
+    q13 = np.stack([O.quantize_weight_per_channel_export(gu[i])[0] for i in range(e)])
+    s13 = np.stack([O.quantize_weight_per_channel_export(gu[i])[1] for i in range(e)])
+    q2 = np.stack([O.quantize_weight_per_channel_export(dn[i])[0] for i in range(e)])
+    s2 = np.stack([O.quantize_weight_per_channel_export(dn[i])[1] for i in range(e)])
+    # runtime layout with bf16 scales: the oracle sees the bf16-rounded scales
+    s13b = O.bf16_bits_to_f32(O.f32_to_bf16_bits(s13))
+    s2b = O.bf16_bits_to_f32(O.f32_to_bf16_bits(s2))
+    w13_rt = torch.from_numpy(np.ascontiguousarray(q13.transpose(0, 2, 1))).to(DEV)
+    w2_rt = torch.from_numpy(np.ascontiguousarray(q2.transpose(0, 2, 1))).to(DEV)
+    sc13 = torch.from_numpy(s13).to(DEV).bfloat16()
+    sc2 = torch.from_numpy(s2).to(DEV).bfloat16()
+    xt, idt, twt = torch.from_numpy(x).to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(tw).to(DEV)
+    y = fused_experts_w8a8(xt, w13_rt, sc13, w2_rt, sc2, twt, idt, layout="runtime")
+    ref = O.moe_runtime(x, ids, tw, q13, s13b, q2, s2b)
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), ref.view(np.uint16)) or \
+        _rel(y.float().cpu().numpy(), ref.astype(np.float32)) <= 1e-3
+    # pre-quantized input: the same bits as quantizing inside
+    qx, sx = dynamic_quant(xt)
+    y2 = fused_experts_w8a8(qx, w13_rt, sc13, w2_rt, sc2, twt, idt, pertoken_scale=sx, layout="runtime",
+                            output_dtype=torch.float16)
+    assert torch.equal(y, y2)
+    # expert_map: experts 2, 3 live elsewhere (-1); their assignments contribute nothing
+    emap = torch.tensor([0, 1, -1, -1], dtype=torch.int32, device=DEV)
+    y3 = fused_experts_w8a8(xt, w13_rt[:2], sc13[:2], w2_rt[:2], sc2[:2], twt, idt, expert_map=emap,
+                            layout="runtime")
+    tw_loc = np.where(ids < 2, tw, 0).astype(np.float32)
+    ref3 = O.moe_runtime(x, np.where(ids < 2, ids, 0).astype(np.int32), tw_loc, q13, s13b, q2, s2b)
+    assert _rel(y3.float().cpu().numpy(), ref3.astype(np.float32)) <= 1e-3
+    # grouped MLP over pre-permuted rows, group_list as cumulative endpoints (0) or counts (1)
+    routed, rscale, row_of_slot, offs = ops.moe_permute_quant(xt, idt, e)
+    counts = torch.diff(offs)
+    outs = [grouped_apply_mlp_w8a8(routed, w13_rt, sc13, w2_rt, sc2, gl, glt, dynamic_scale=rscale,
+                                   output_dtype=torch.float32, layout="runtime")
+            for gl, glt in ((offs[1:], 0), (counts, 1))]
+    assert torch.equal(outs[0], outs[1])
+    yk = ops.moe_gmm2(*ops.moe_gmm1_swiglu_quant(routed, rscale, torch.from_numpy(q13).to(DEV),
+                                                 torch.from_numpy(s13b).to(DEV), offs, inter),
+                      torch.from_numpy(q2).to(DEV), torch.from_numpy(s2b).to(DEV), offs)
+    assert torch.equal(outs[0], yk)
+    with pytest.raises(ValueError):
+        grouped_apply_mlp_w8a8(routed, w13_rt, sc13, w2_rt, sc2, counts, 2, dynamic_scale=rscale, layout="runtime")
 
 
 def test_runtime_apply_contract():

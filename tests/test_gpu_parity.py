@@ -16,6 +16,7 @@ from oracle import quant as O
 
 pytestmark = pytest.mark.gpu
 GOLD = np.load(Path(__file__).parent / "golden" / "reference_vectors.npz")
+EXT = np.load(Path(__file__).parent / "golden" / "reference_ext_vectors.npz")
 DEV = "cuda:0"
 
 
@@ -176,6 +177,50 @@ def test_w4a16_gemm_swiglu_matches_two_step(m, i, k, zp):
     assert _rel(_np(act).astype(np.float32), ref) <= 1e-3   # bar: ||act - ref||_F / ||ref||_F <= 1e-3
 
 
+def test_awq_quantize_bf16_matches_reference():
+    """AWQ pseudo_quantize_tensor in bf16 arithmetic (asym with a constant group; sym): the
+    dequantized weight, scales and zeros bit-exact to the reference's bf16 outputs."""
+    _say("awq bf16")
+    w = EXT["awqb_w"].view(np.uint16)
+    wt = torch.from_numpy(EXT["awqb_w"]).view(torch.bfloat16).to(DEV)
+    packed, s, z, deq = _ops().w4_quantize_awq(wt, 128, True)
+    bits = lambda t: _np(t.view(torch.int16)).view(np.uint16)  # noqa: E731
+    assert np.array_equal(bits(deq), EXT["awqb_deq"].view(np.uint16))
+    assert np.array_equal(bits(s), EXT["awqb_s"].view(np.uint16))
+    assert np.array_equal(bits(z), EXT["awqb_z"].view(np.uint16))
+    _, _, _, codes = O.pseudo_quantize_tensor(w, 4, True, 128, dtype="bf16")
+    assert np.array_equal(_np(packed), O.pack_uint4(codes))
+    _, _, _, deq_s = _ops().w4_quantize_awq(wt, 128, False)
+    assert np.array_equal(bits(deq_s), EXT["awqb_sym_deq"].view(np.uint16))
+
+
+# bf16: (m, n, k) through the dequantising MFMA GEMM -- tiled (K % 64 == 0) incl. ragged M / N and
+# the 7B / 70B shapes (sampled rows not needed: the oracle handles them), and the any-K kernel
+W4_BF16_CASES = [(1, 4096, 4096), (16, 4096, 4096), (3, 1000, 1024), (64, 384, 512), (200, 320, 1024),
+                 (300, 12288, 4096), (5, 256, 8192), (2, 100, 96)]
+
+
+@pytest.mark.parametrize("m,n,k", W4_BF16_CASES)
+@pytest.mark.parametrize("zp", [True, False])
+def test_w4a16_gemm_bf16_matches_dequant_matmul(m, n, k, zp):
+    """bf16 W4A16 against F.linear(x, pseudo_quantize_tensor(w)) in bf16 (fp32 accumulation, one
+    rounding): rel. Frobenius error <= 1e-3."""
+    _say("w4a16 bf16", m, n, k, zp)
+    g = 128 if k % 128 == 0 else 32
+    rng = np.random.default_rng(m + n + k)
+    w = O.f32_to_bf16_bits((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = O.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    bias = O.f32_to_bf16_bits((rng.standard_normal(n) * 0.1).astype(np.float32))
+    rdeq, rs, rz, codes = O.pseudo_quantize_tensor(w, 4, zp, g, dtype="bf16")
+    packed = O.pack_uint4(codes) if zp else O.pack_int4_signed(codes)
+    ref = O.bf16_bits_to_f32(O.w4a16_linear(x, rdeq, bias, dtype="bf16"))
+    tb = lambda a: _t(a.view(np.int16), torch.bfloat16)  # noqa: E731
+    y = _ops().w4a16_gemm(tb(x), _t(packed), tb(rs), None if rz is None else tb(rz), g, tb(bias))
+    assert y.dtype == torch.bfloat16
+    err = _rel(_np(y.float()), ref)
+    assert err <= 1e-3, err   # bar: ||Y - Y_ref||_F / ||Y_ref||_F <= 1e-3
+
+
 def test_w4a16_odd_shapes_use_exact_path():
     _say("w4a16 odd")
     # export KAT: K = 8, g = 4 (tests/test_vllm_real_quant_export.py:105-152)
@@ -229,6 +274,66 @@ def test_per_token_quant_fp16_rule_matches_reference():
     assert np.array_equal(fake, GOLD["sq_x_fq"])
 
 
+def _fake_values(q, s, dt):
+    """Values ``q * s`` of stored codes rounded to the rule's dtype, as float32 (int8 codes carry
+    no sign of zero, so values are compared, -0.0 == 0.0)."""
+    v = q.float() * s.float().unsqueeze(-1)
+    return _np((v.bfloat16() if dt == "bf16" else v.half()).float())
+
+
+def _both_128_rows(codes):
+    """Rows whose fake-rule codes reach both +128 and -128 (stored with +128 clamped to 127)."""
+    c = codes.astype(np.int32)
+    return (c >= 128).any(-1) & (c <= -128).any(-1)
+
+
+@pytest.mark.parametrize("which", ["act", "weight"])
+def test_fake_rule_bf16_matches_reference(which):
+    """bf16 fake rule (quantize_*_absmax in bf16): q * s equals the reference's fake values on
+    every row (rows reaching +128 are stored negated); the codes are the oracle's codes up to
+    that sign, within [-128, 127]."""
+    _say("fake rule bf16", which)
+    ops = _ops()
+    xb = EXT["sqb_x" if which == "act" else "sqb_w"]
+    ref = EXT["sqb_x_fq" if which == "act" else "sqb_w_fq"].view(np.uint16)
+    xt = torch.from_numpy(xb).view(torch.bfloat16).to(DEV)
+    if which == "act":
+        q, s = ops.quant_per_token_i8(xt, True)
+        assert s.dtype == torch.bfloat16
+    else:
+        q, s32, s = ops.w8_quantize_per_channel(xt, "fake")
+        assert torch.equal(s32, s.float())
+    codes, _, _ = O.quantize_activation_per_token_fake(xb.view(np.uint16), 8, "bf16")
+    assert not _both_128_rows(codes).any()
+    assert np.array_equal(_fake_values(q, s, "bf16"), O.bf16_bits_to_f32(ref))
+    sign = np.where(_np(s.float()) < 0, -1, 1)[:, None]
+    assert np.array_equal(_np(q).astype(np.int32) * sign, codes.astype(np.int32))
+
+
+def test_fake_rule_bf16_random_rows_and_ties():
+    """bf16 fake rule on 2000 random rows with outliers plus +-a rows (every code +-128):
+    bit-exact fake values except on rows reaching both +-128, where only the +128 entries move
+    by one code."""
+    _say("fake rule bf16 random")
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2000, 1024, generator=g)
+    x[:, torch.randperm(1024, generator=g)[:10]] *= 20
+    x[0] = torch.tensor([3.0, -3.0]).repeat(512)
+    x[1] = 1.0
+    xb = x.bfloat16()
+    bits = xb.view(torch.int16).numpy().view(np.uint16)
+    codes, _, fake = O.quantize_activation_per_token_fake(bits, 8, "bf16")
+    q, s = _ops().quant_per_token_i8(xb.to(DEV), True)
+    got = _fake_values(q, s, "bf16")
+    both = _both_128_rows(codes)
+    assert np.array_equal(got[~both], O.bf16_bits_to_f32(fake)[~both])
+    qn = _np(q).astype(np.int32)
+    assert qn.min() >= -128 and qn.max() <= 127
+    for r in np.nonzero(both)[0]:
+        d = codes[r].astype(np.int32) - qn[r]
+        assert set(np.unique(d)) <= {0, 1} and np.all((d == 0) | (codes[r] == 128))
+
+
 def test_w8_quantize_export_and_fake_rules():
     _say("w8 quantize")
     ops = _ops()
@@ -258,7 +363,12 @@ W8_CASES = [(1, 11008, 4096), (16, 11008, 4096), (5, 1000, 256), (17, 512, 1024)
             # large-M kernel with odd N: the unpaired store path
             (1024, 333, 256),
             # row-contiguous GEMV (M <= 2): K past the last 1 KB chunk, M = 2, tiny K, K = 11008
-            (2, 300, 1040), (1, 257, 4112), (2, 64, 16), (1, 100, 11008)]
+            (2, 300, 1040), (1, 257, 4112), (2, 64, 16), (1, 100, 11008),
+            # skinny kernel where the whole K fits the 76 KB LDS budget but not the staging
+            # registers (more than 4096 sixteen-byte pieces): K split into chunks
+            (17, 512, 4096), (18, 300, 4096), (7, 256, 11008), (5, 256, 14336), (33, 256, 2048),
+            # C2 sweep at M = 256 (tiled kernel) on the full N x K
+            (256, 11008, 4096)]
 
 
 @pytest.mark.parametrize("m,n,k", W8_CASES)
@@ -358,6 +468,104 @@ def test_moe_chain_matches_oracle(t, h, inter, e):
         total += rq.size
         assert np.max(np.abs(qh[rows].astype(int) - rq.astype(int))) <= 1
     assert agree / total >= 0.999
+
+
+def _moe_module(gu, dn, dt, rule="fake"):
+    from mindpipe_amd.smoothquant import SmoothQuantPackedMoeExperts
+    tdt = torch.float16 if dt == "fp16" else torch.bfloat16
+    cv = (lambda a: torch.from_numpy(np.ascontiguousarray(a))) if dt == "fp16" else \
+        (lambda a: torch.from_numpy(np.ascontiguousarray(a)).view(torch.bfloat16))
+    return SmoothQuantPackedMoeExperts(cv(gu).to(DEV), cv(dn).to(DEV), torch.nn.SiLU(), scale_rule=rule), cv, tdt
+
+
+@pytest.mark.parametrize("tag,dt", [("f16", "fp16"), ("bf16", "bf16")])
+def test_moe_fake_rule_matches_reference_module(tag, dt):
+    """SmoothQuantPackedMoeExperts (default fake rule) against the output the reference module
+    wrote for the same weights, tokens and routing (fake_quant.py:124-191): rel. Frobenius
+    error <= 1e-3 (fp32 sums in a different order, silu's exp), most elements bit-identical."""
+    _say("moe fake vs reference", dt)
+    mod, cv, tdt = _moe_module(EXT[f"moe_{tag}_gu"], EXT[f"moe_{tag}_dn"], dt)
+    x = cv(EXT[f"moe_{tag}_x"]).to(DEV)
+    ids = torch.from_numpy(EXT[f"moe_{tag}_ids"]).long().to(DEV)
+    w = torch.from_numpy(EXT[f"moe_{tag}_w"]).to(DEV)
+    y = mod(x, ids, w)
+    assert y.dtype == tdt and y.shape == x.shape
+    ref = EXT[f"moe_{tag}_y"]
+    yv = _np(y.float())
+    rv = ref.astype(np.float32) if dt == "fp16" else O.bf16_bits_to_f32(ref.view(np.uint16))
+    err = _rel(yv, rv)
+    assert err <= 1e-3, err   # bar: rel. Frobenius error <= 1e-3 against the reference module
+    same = np.mean(_np(y.view(torch.int16)).view(np.uint16) == ref.view(np.uint16))
+    assert same >= 0.9, same
+    assert not yv[0].any()    # token 0 is all zeros in the fixture
+
+
+@pytest.mark.parametrize("dt", ["fp16", "bf16"])
+def test_moe_fake_rule_matches_oracle_larger(dt):
+    """Fake-rule chain at T = 300, H = 1024, I = 768, E = 8 (experts over 64 rows, tiled and
+    grouped kernels) against oracle.moe_fake: rel. Frobenius error <= 1e-3."""
+    _say("moe fake larger", dt)
+    t, h, inter, e = 300, 1024, 768, 8
+    rng = np.random.default_rng(21)
+    xf = rng.standard_normal((t, h)).astype(np.float32)
+    xf[:, rng.choice(h, 10, replace=False)] *= 20
+    ids, tw = O.mixtral_router(rng.standard_normal((t, e)).astype(np.float32), 2)
+    guf = (rng.standard_normal((e, 2 * inter, h)) * 0.02).astype(np.float32)
+    dnf = (rng.standard_normal((e, h, inter)) * 0.02).astype(np.float32)
+    conv = (lambda a: a.astype(np.float16)) if dt == "fp16" else O.f32_to_bf16_bits
+    x, gu, dn = conv(xf), conv(guf), conv(dnf)
+    mod, cv, _ = _moe_module(gu, dn, dt)
+    y = mod(cv(x).to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(tw).to(DEV))
+    ref = O.moe_fake(x, ids, tw, gu, dn, dt)
+    rv = ref.astype(np.float32) if dt == "fp16" else O.bf16_bits_to_f32(ref)
+    err = _rel(_np(y.float()), rv)
+    assert err <= 1e-3, err   # bar: rel. Frobenius error <= 1e-3
+
+
+def test_moe_prequantized_input_equals_quantizing_first():
+    """Routing pre-quantized rows (the runtime's pertoken_scale input) gives the bits of routing
+    and quantizing the float rows in one step."""
+    _say("moe prequant")
+    x, ids, tw, q13, s13, q2, s2 = _moe_case(96, 256, 256, 4, seed=3)
+    ops = _ops()
+    qx, sx = ops.quant_per_token_i8(_t(x))
+    a = ops.moe_permute_quant(_t(x), _t(ids), 4)
+    b = ops.moe_permute_quant(qx, _t(ids), 4, x_scale=sx)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    y1 = ops.moe_w8a8_forward(_t(x), _t(ids), _t(tw), _t(q13), _t(s13), _t(q2), _t(s2))
+    y2 = ops.moe_w8a8_forward(qx, _t(ids), _t(tw), _t(q13), _t(s13), _t(q2), _t(s2), out_dtype=torch.float16,
+                              x_scale=sx)
+    assert torch.equal(y1, y2)
+
+
+def test_moe_mixtral_full_shape_sampled_tokens():
+    """The Mixtral-shaped layer the bench measures (T = 512, H = 4096, I = 14336, E = 8, top-2;
+    GEMM1 over 2I = 28672 > 10240 columns), runtime rule, checked on 34 sampled tokens against
+    oracle.moe_runtime (per-token quantization makes every token independent): rel. Frobenius
+    error <= 1e-3 and the routing offsets exact."""
+    t, h, inter, e = 512, 4096, 14336, 8
+    _say("moe mixtral full shape", t, h, inter, e)
+    ops = _ops()
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    rng = np.random.default_rng(12)
+    x = torch.randn(t, h, generator=gen, device=DEV).half()
+    ids, tw = O.mixtral_router(rng.standard_normal((t, e)).astype(np.float32), 2)
+    q13, s13, _ = ops.w8_quantize_per_channel(
+        (torch.randn(e * 2 * inter, h, generator=gen, device=DEV) * 0.02).half(), "export")
+    q2, s2, _ = ops.w8_quantize_per_channel((torch.randn(e * h, inter, generator=gen, device=DEV) * 0.02).half(),
+                                            "export")
+    q13, s13 = q13.reshape(e, 2 * inter, h), s13.reshape(e, 2 * inter)
+    q2, s2 = q2.reshape(e, h, inter), s2.reshape(e, h)
+    y = ops.moe_w8a8_forward(x, _t(ids), _t(tw), q13, s13, q2, s2)
+    torch.cuda.synchronize()
+    _, _, _, offs = ops.moe_permute_quant(x, _t(ids), e)
+    counts = np.bincount(ids.reshape(-1), minlength=e)
+    assert np.array_equal(_np(offs), np.concatenate([[0], np.cumsum(counts)]))
+    toks = np.unique(np.concatenate([rng.choice(t, 32, replace=False), [0, t - 1]]))
+    ref = O.moe_runtime(_np(x)[toks], ids[toks], tw[toks], _np(q13), _np(s13), _np(q2), _np(s2))
+    err = _rel(_np(y)[toks], ref)
+    assert err <= 1e-3, err   # bar: rel. Frobenius error <= 1e-3
 
 
 # Grouped GEMMs on crafted expert sizes (rows <= 256 per expert on average, the serving-size

@@ -3,8 +3,10 @@
 Sources of truth used here (never the oracle's own formula retyped):
 * known answers held in the reference's tests (pack KAT, export KAT, tiny
   Qwen2 W8A8 export values), restated as literal data;
-* ``tests/golden/reference_vectors.npz``, written by running the reference's
-  own quantizers (``tests/golden/make_reference_vectors.py``);
+* ``tests/golden/reference_vectors.npz`` and ``reference_ext_vectors.npz``,
+  written by running the reference's own quantizers, ``SmoothQuantLinear``,
+  ``SmoothQuantPackedMoeExperts`` and ``_compute_smooth_scales``
+  (``tests/golden/make_reference_vectors.py``);
 * brute-force loops and closed-form invariants.
 """
 import json
@@ -16,6 +18,7 @@ import pytest
 from oracle import quant as O
 
 GOLD = np.load(Path(__file__).parent / "golden" / "reference_vectors.npz")
+EXT = np.load(Path(__file__).parent / "golden" / "reference_ext_vectors.npz")
 KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
 
 
@@ -244,10 +247,82 @@ def test_moe_runtime_matches_bruteforce_and_fake_path():
     y = O.moe_runtime(x, ids, w, q13, s13, q2, s2)
     yb = _moe_bruteforce(x, ids, w, q13, s13, q2, s2)
     assert np.array_equal(y.view(np.uint16), yb.view(np.uint16))
-    # the fake-quant reference path lands close (different scale dtypes / fp16 steps)
-    yf = O.moe_fake(x, ids, w, wgu, wdn)
-    rel = np.linalg.norm(y.astype(np.float32) - yf.astype(np.float32)) / np.linalg.norm(yf.astype(np.float32))
-    assert rel < 0.05
+
+
+def _u16(a):
+    return np.ascontiguousarray(a).view(np.uint16)
+
+
+def _cv(dt):
+    return (lambda a: a) if dt == "fp16" else (lambda a: np.ascontiguousarray(a).view(np.uint16))
+
+
+@pytest.mark.parametrize("tag,dt", [("f16", "fp16"), ("bf16", "bf16")])
+def test_moe_fake_matches_reference_module_forward(tag, dt):
+    """``SmoothQuantPackedMoeExperts(gate_up, down, SiLU)(x, ids, w)`` as the reference computes it
+    (fake_quant.py:124-191; vectors written by the reference module): bit-exact, fp16 and bf16,
+    including an all-zero token and an expert hit by one token."""
+    cv = _cv(dt)
+    y = O.moe_fake(cv(EXT[f"moe_{tag}_x"]), EXT[f"moe_{tag}_ids"], EXT[f"moe_{tag}_w"], cv(EXT[f"moe_{tag}_gu"]),
+                   cv(EXT[f"moe_{tag}_dn"]), dt)
+    assert np.array_equal(_u16(y), _u16(EXT[f"moe_{tag}_y"]))
+
+
+def test_moe_fake_differs_from_runtime_rule_by_rounding_only():
+    """The fake rule (fp16 scales and fp16 roundings) and the runtime rule (fp32 scales, fp32
+    SwiGLU) describe the same layer: within a few 1e-3 of each other on the reference's case,
+    and a planted mistake (gate/up swapped) is far from both."""
+    x, ids, w = EXT["moe_f16_x"], EXT["moe_f16_ids"], EXT["moe_f16_w"]
+    gu, dn = EXT["moe_f16_gu"], EXT["moe_f16_dn"]
+    e = gu.shape[0]
+    q13 = np.stack([O.quantize_weight_per_channel_export(gu[i])[0] for i in range(e)])
+    s13 = np.stack([O.quantize_weight_per_channel_export(gu[i])[1] for i in range(e)])
+    q2 = np.stack([O.quantize_weight_per_channel_export(dn[i])[0] for i in range(e)])
+    s2 = np.stack([O.quantize_weight_per_channel_export(dn[i])[1] for i in range(e)])
+    yr = O.moe_runtime(x, ids, w, q13, s13, q2, s2).astype(np.float64)
+    yf = EXT["moe_f16_y"].astype(np.float64)
+    assert np.linalg.norm(yr - yf) / np.linalg.norm(yf) < 2e-2
+    inter = dn.shape[2]
+    swapped = np.concatenate([gu[:, inter:], gu[:, :inter]], axis=1)
+    ys = O.moe_fake(x, ids, w, swapped, dn).astype(np.float64)
+    assert np.linalg.norm(ys - yf) / np.linalg.norm(yf) > 0.3
+
+
+def test_bf16_awq_and_fake_quant_match_reference():
+    """bf16 arithmetic of pseudo_quantize_tensor (asym with a constant group, and sym) and of
+    the per-token / per-channel fake quantizers: bit-exact to the reference's outputs."""
+    w = _u16(EXT["awqb_w"])
+    d, s, z, c = O.pseudo_quantize_tensor(w, 4, True, 128, dtype="bf16")
+    assert np.array_equal(d, _u16(EXT["awqb_deq"]))
+    assert np.array_equal(s, _u16(EXT["awqb_s"])) and np.array_equal(z, _u16(EXT["awqb_z"]))
+    assert c.min() >= 0 and c.max() <= 15
+    d2, _, _, _ = O.pseudo_quantize_tensor(w, 4, False, 128, dtype="bf16")
+    assert np.array_equal(d2, _u16(EXT["awqb_sym_deq"]))
+    _, _, fx = O.quantize_activation_per_token_fake(_u16(EXT["sqb_x"]), 8, "bf16")
+    assert np.array_equal(fx, _u16(EXT["sqb_x_fq"]))
+    _, _, fw = O.quantize_weight_per_channel_fake(_u16(EXT["sqb_w"]), 8, "bf16")
+    assert np.array_equal(fw, _u16(EXT["sqb_w_fq"]))
+
+
+@pytest.mark.parametrize("tag,dt", [("f16", "fp16"), ("bf16", "bf16")])
+def test_smoothquant_linear_fake_forward_matches_reference(tag, dt):
+    """SmoothQuantLinear.from_float + forward (fake_quant.py:85-113), with and without the
+    output fake-quant: bit-exact in fp16 and bf16."""
+    cv = _cv(dt)
+    y = O.w8a8_linear_fake(cv(EXT[f"sql_{tag}_x"]), cv(EXT[f"sql_{tag}_w"]), cv(EXT[f"sql_{tag}_b"]), dt)
+    assert np.array_equal(_u16(y), _u16(EXT[f"sql_{tag}_y"]))
+    yq = O.quantize_activation_per_token_fake(y, 8, dt)[2]
+    assert np.array_equal(_u16(yq), _u16(EXT[f"sql_{tag}_yq"]))
+
+
+@pytest.mark.parametrize("tag,dt", [("f16", "fp16"), ("bf16", "bf16")])
+def test_smooth_scales_match_reference(tag, dt):
+    """_compute_smooth_scales (smooth.py:7-25) over two fcs sharing a norm, with a clamped
+    weight column and activation outliers: bit-exact."""
+    cv = _cv(dt)
+    s = O.compute_smooth_scales(EXT[f"smooth_{tag}_a"], [cv(EXT[f"smooth_{tag}_w0"]), cv(EXT[f"smooth_{tag}_w1"])],
+                                0.5, dt)
+    assert np.array_equal(_u16(s), _u16(EXT[f"smooth_{tag}_s"]))
 
 
 def test_add_rms_norm_closed_forms_and_invariants():
