@@ -217,6 +217,18 @@ int mp_i8_gemm_swiglu_requant(const int8_t *routed, const float *routed_scale, c
                               int8_t *q_out, float *s_out, void *workspace, size_t workspace_bytes,
                               mp_stream_t stream);
 
+/* mp_i8_gemm_swiglu_requant without a workspace argument: no counterpart in the reference.
+ * For callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the scratch lives in a library-owned 64 MiB device array
+ * per GPU, held until the process ends; the call allocates nothing.  Shapes whose
+ * mp_moe_gmm1_workspace_bytes(rows, inter) exceeds 64 MiB return MP_ERR_WORKSPACE.  Every
+ * call on one GPU uses that GPU's array: calls that overlap on one GPU (other streams or
+ * threads) race.  Run with the stream's device current (the array is found per device). */
+int mp_i8_gemm_swiglu_requant_noalloc(const int8_t *routed, const float *routed_scale, const int8_t *w13,
+                                      const float *s13, const int64_t *group_offsets, int n_experts,
+                                      int64_t rows, int64_t h, int64_t inter, int scale_rule, int act_dtype,
+                                      int8_t *q_out, float *s_out, mp_stream_t stream);
+
 /* GMM2: Y_r = (Qh_r . W2_e^T) * sh_r * s2_e -> out_dtype [R, N] (fp32 for the
  * combine).  Replaces npu_grouped_matmul with per_token_scale
  * (vllm_ascend.patch:2401-2412).  scale_rule MP_SCALE_FAKE: the reference's F.linear on

@@ -48,6 +48,8 @@ SIGNATURES = {
     "mp_moe_gmm1_workspace_bytes": (_sz, [_i64, _i64]),
     "mp_i8_gemm_swiglu_requant": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp,
                                          _sz, _vp]),
+    "mp_i8_gemm_swiglu_requant_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp,
+                                                 _vp, _vp]),
     "mp_w8a8_grouped_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp]),
     "mp_w8a8_gemm_fake": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
     "mp_moe_unpermute_combine": (_i32, [_vp, _vp, _vp, _i64, _i32, _i64, _i32, _vp, _i32, _vp]),

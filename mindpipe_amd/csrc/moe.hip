@@ -4,6 +4,8 @@
 // of w8a8.hip with a grouped row schedule.
 #include "dq_gemm.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kMaxExperts = 1024;
@@ -549,6 +551,47 @@ extern "C" int mp_moe_unpermute_combine(const float *y, const int32_t *row_of_sl
 #undef MP_CB
   MP_CHECK_LAUNCH();
   return MP_OK;
+}
+
+// ---------------------------------------------------------------- allocation-free GMM1
+// mp_i8_gemm_swiglu_requant with its scratch (the fp32 SwiGLU rows and the per-row abs-max
+// partials) in a library-owned device array instead of a caller workspace, for callers that
+// cannot allocate.  Each GPU holds its own copy of `scratch` (64 MiB, until the process ends);
+// host code never passes the array's name to a kernel (that is a host-side stand-in): the
+// device address comes from hipGetSymbolAddress, once per device, on the first call with that
+// device current.  Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+// race.  Nothing in it has to start at zero -- the requant reads only rows and partials the
+// GEMM epilogue wrote in the same call.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+constexpr int kNoAllocMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kNoAllocMaxDevices] = {};
+
+static int mp_scratch_address(void **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices) return MP_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return MP_ERR_HIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MP_OK;
+}
+
+extern "C" int mp_i8_gemm_swiglu_requant_noalloc(const int8_t *routed, const float *routed_scale, const int8_t *w13,
+                                                 const float *s13, const int64_t *group_offsets, int n_experts,
+                                                 int64_t rows, int64_t h, int64_t inter, int scale_rule,
+                                                 int act_dtype, int8_t *q_out, float *s_out, mp_stream_t stream) {
+  if (rows < 0 || inter <= 0) return MP_ERR_SHAPE;
+  if (mp_moe_gmm1_workspace_bytes(rows, inter) > kNoAllocScratchBytes) return MP_ERR_WORKSPACE;
+  void *ws = nullptr;
+  const int rc = mp_scratch_address(&ws);
+  if (rc != MP_OK) return rc;
+  return mp_i8_gemm_swiglu_requant(routed, routed_scale, w13, s13, group_offsets, n_experts, rows, h, inter,
+                                   scale_rule, act_dtype, q_out, s_out, ws, kNoAllocScratchBytes, stream);
 }
 
 // ---------------------------------------------------------------- misc
