@@ -1,20 +1,25 @@
 """Benchmark of the quantized-linear forward path on one MI355X.
 
-Prints ONE JSON line.  ``value`` is the headline W4A16 g128 GEMV at M=1
-(K=N=4096, the BASELINE metric's first figure) in TB/s of algorithmic bytes,
-with the weights rotated over >= 64 distinct copies (>= 571 MB) so the 256 MB
-Infinity Cache cannot serve them; inputs are resident in HBM before timing.
-The other legs of the metric (W8A8 int8 GEMM TOPS at M=4096, the W8A8 sweep,
-W4A16 M=16, the Mixtral-shaped MoE chain, the Llama-2-7B-shaped decode at
-B = 1 / 8 / 32 with its 2048-token prefill, and the Llama-3-70B-shaped decode at
-B = 1 / 16 / 64 over a 4096-token context) are reported under ``legs``, each
-with its own roofline fraction.  Timing uses HIP events recorded on the stream
-the kernels are launched on (torch's current stream), bracketed by
-``torch.cuda.synchronize()``.
+Prints ONE JSON line.  ``value`` is the headline W4A16 g128 GEMV at M=1 (K=N=4096, the
+BASELINE metric's first figure) in TB/s of algorithmic bytes.  A step is one pass over 64
+distinct W4A16 linears of that shape (64 rotated weight copies, 571 MB, so the 256 MB Infinity
+Cache cannot serve them): one HIP graph of 64 GEMV launches, replayed ``--steps`` times after
+``--warmup`` untimed replays; inputs are resident in HBM before timing.  The other legs of the
+metric (W8A8 int8 GEMM TOPS at M=4096, the W8A8 sweep, W4A16 M=16 and the 70B GEMV shapes, the
+Mixtral-shaped MoE chain, the Llama-2-7B-shaped decode at B = 1 / 8 / 32 with its 2048-token
+prefill, and the Llama-3-70B-shaped decode at B = 1 / 16 / 64 over a 4096-token context) are
+reported under ``legs``, each with its roofline fraction and its CPU baseline.  Timing uses HIP
+events recorded on the stream the kernels are launched on (torch's current stream), bracketed
+by ``torch.cuda.synchronize()``.
 
-``cpu_baseline``: the oracle's restatement of the reference CPU fake-quant
-forward (``F.linear`` on AWQ pseudo-quantized fp16 weights) timed on this
-host's cores for a bounded sample.
+``cpu_baseline``: the reference's CPU fake-quant forward restated with torch CPU ops
+(``oracle/cpu_baseline.py``), timed on this host's cores on the same workload (bounded samples
+stated in each ``sample``).
+
+``--profile NAME`` runs one kernel mix for rocprofv3 (the commands in ``profiles/``):
+``w4gemv`` (the headline loop), ``readfloor`` (one-launch reads of 8.9 MB, rotated),
+``w4shapes`` (M=16 and the 70B GEMV shapes), ``w8big`` (the M=4096 int8 GEMM), and
+``--traffic-probe`` the kernel mix of ``profiles/traffic.json``.
 """
 from __future__ import annotations
 
@@ -38,19 +43,17 @@ def _log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def _time_launches(fn, n_launch, warmup, per_graph=None):
-    """Average time per launch (ms) of back-to-back launches, HIP events recorded on the
-    current stream.  The launches are captured into a HIP graph (``per_graph`` launches,
-    cycling through the rotated inputs) and the graph is replayed, so host-side Python
-    dispatch does not separate the kernels."""
-    per_graph = per_graph or min(n_launch, 64)
+def _time_graph(fn, per_graph, steps, warmup):
+    """Milliseconds per step: a step is one replay of a HIP graph holding ``per_graph`` launches
+    ``fn(0) .. fn(per_graph - 1)`` (each on its own rotated input); ``warmup`` untimed replays,
+    then exactly ``steps`` timed replays between HIP events on the current stream."""
     for i in range(per_graph):
         fn(i)
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        for i in range(2):
+        for i in range(min(2, per_graph)):
             fn(i)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
@@ -58,19 +61,18 @@ def _time_launches(fn, n_launch, warmup, per_graph=None):
     with torch.cuda.graph(graph):
         for i in range(per_graph):
             fn(i)
-    replays = max(1, -(-n_launch // per_graph))
-    for _ in range(max(1, warmup // per_graph)):
+    for _ in range(max(1, warmup)):
         graph.replay()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(st)
-    for _ in range(replays):
+    for _ in range(steps):
         graph.replay()
     e1.record(st)
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / (replays * per_graph)
+    ms = e0.elapsed_time(e1) / steps
     del graph
     return ms
 
@@ -89,26 +91,30 @@ def _roof(bound, achieved, peak, unit, traffic=None):
             "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
-def leg_w4a16(ops, m, n, k, steps, warmup, copies=64, g=128):
+def _w4_copies(ops, n, k, copies, g=128):
     gen = torch.Generator(device="cuda").manual_seed(1)
     w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).half()
     packed, s, z, _ = ops.w4_quantize_awq(w, g, True, return_deq=False)
     del w
-    pk = [packed.clone() for _ in range(copies)]
-    sc = [s.clone() for _ in range(copies)]
-    zr = [z.clone() for _ in range(copies)]
+    return [packed.clone() for _ in range(copies)], [s.clone() for _ in range(copies)], \
+        [z.clone() for _ in range(copies)]
+
+
+def leg_w4a16(ops, m, n, k, steps, warmup, copies=64, g=128):
+    """W4A16 at M x K x N: one step = ``copies`` launches, each on its own weight copy."""
+    pk, sc, zr = _w4_copies(ops, n, k, copies, g)
     gx = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(m, k, generator=gx, device="cuda").half()
     y = ops.w4a16_gemm(x, pk[0], sc[0], zr[0], g, None)
-    ms = _time_launches(lambda i: ops.w4a16_gemm(x, pk[i % copies], sc[i % copies], zr[i % copies], g, None),
-                        steps, warmup)
+    ms_step = _time_graph(lambda i: ops.w4a16_gemm(x, pk[i], sc[i], zr[i], g, None), copies, steps, warmup)
+    ms = ms_step / copies
     nbytes = n * k // 2 + 2 * n * (k // g) * 2 + m * k * 2 + m * n * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
     del pk, sc, zr
     torch.cuda.empty_cache()
-    return {"m": m, "n": n, "k": k, "group": g, "ms_per_call": ms, "bytes_per_call": nbytes,
-            "tb_s": gbs / 1000.0, "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s"),
-            "weight_copies": copies}, y
+    return {"m": m, "n": n, "k": k, "group": g, "ms_per_call": ms, "ms_per_step": ms_step,
+            "bytes_per_call": nbytes, "tb_s": gbs / 1000.0, "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s"),
+            "weight_copies": copies, "working_set_bytes": copies * (n * k // 2 + 2 * n * (k // g) * 2)}, y
 
 
 def leg_w8a8(ops, m, n, k, steps, warmup):
@@ -116,23 +122,25 @@ def leg_w8a8(ops, m, n, k, steps, warmup):
     w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).half()
     qw, sw, _ = ops.w8_quantize_per_channel(w, "export")
     del w
-    copies = max(1, min(16, int(600e6 // (n * k))))  # rotate weights past the Infinity Cache when HBM-bound
-    qws = [qw.clone() for _ in range(copies)] if m <= 256 else [qw]
+    # HBM-bound shapes rotate distinct weight copies past the Infinity Cache (>= 600 MB); the
+    # MFMA-bound M = 4096 GEMM runs 4 launches per step on one copy
+    copies = max(1, min(16, int(600e6 // (n * k)))) if m <= 256 else 4
+    qws = [qw.clone() for _ in range(copies)] if m <= 256 else [qw] * copies
     gx = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(m, k, generator=gx, device="cuda")
     idx = torch.randperm(k, generator=torch.Generator().manual_seed(2))[: max(1, round(k * 0.01))]
     x[:, idx.cuda()] *= 20
     x = x.half()
     q, st = ops.quant_per_token_i8(x)
-    nc = len(qws)
-    ms = _time_launches(lambda i: ops.w8a8_gemm(q, st, qws[i % nc], sw, None, torch.float16), steps, warmup)
-    ms_q = _time_launches(lambda i: ops.quant_per_token_i8(x), steps, warmup)
+    ms = _time_graph(lambda i: ops.w8a8_gemm(q, st, qws[i], sw, None, torch.float16), copies, steps, warmup) / copies
+    ms_q = _time_graph(lambda i: ops.quant_per_token_i8(x), 4, steps, warmup) / 4
     ops_count = 2.0 * m * n * k
     nbytes = n * k + m * k + m * n * 2 + 4 * n + 4 * m
     tops = ops_count / (ms * 1e-3) / 1e12
     gbs = nbytes / (ms * 1e-3) / 1e9
     out = {"m": m, "n": n, "k": k, "ms_gemm": ms, "ms_quant": ms_q, "ms_e2e": ms + ms_q, "tops": tops,
-           "tops_e2e": ops_count / ((ms + ms_q) * 1e-3) / 1e12, "gb_s": gbs, "weight_copies": nc}
+           "tops_e2e": ops_count / ((ms + ms_q) * 1e-3) / 1e12, "gb_s": gbs,
+           "weight_copies": len({id(t) for t in qws})}
     if m >= 1024:
         out["roofline"] = _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS",
                                 _traffic(f"w8a8_gemm_m{m}_k{k}_n{n}"))
@@ -165,7 +173,7 @@ def leg_moe(ops, steps, warmup, t=512, h=4096, inter=14336, e=8, top_k=2):
     tw, ids = torch.topk(p, top_k, dim=-1)
     tw = (tw / tw.sum(-1, keepdim=True)).float().cuda()
     ids = ids.to(torch.int32).cuda()
-    ms = _time_launches(lambda i: ops.moe_w8a8_forward(x, ids, tw, q13, s13, q2, s2), steps, warmup)
+    ms = _time_graph(lambda i: ops.moe_w8a8_forward(x, ids, tw, q13, s13, q2, s2), 1, steps, warmup)
     wbytes = e * (2 * inter * h + h * inter)
     ops_count = 2.0 * t * top_k * (2 * inter * h + h * inter)
     gbs = wbytes / (ms * 1e-3) / 1e9
@@ -248,33 +256,70 @@ def leg_decoder(cfg_name, batches, prompt, gen_tokens, prefill_batch=1):
     return out
 
 
-def cpu_baseline_w4a16(m=1, n=4096, k=4096, g=128, budget_s=12.0):
-    """Oracle restatement of the reference CPU path: AWQ pseudo-quantized fp16 weight, then
-    F.linear (fp32 accumulate).  Timed per call on the host, bounded sample."""
+def cpu_baselines(legs):
+    """The reference's CPU path (oracle/cpu_baseline.py) on each leg's workload."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import quant as O
-    gen = torch.Generator().manual_seed(1)
-    w = (torch.randn(n, k, generator=gen) * 0.02).half().numpy()
-    x = torch.randn(m, k, generator=torch.Generator().manual_seed(0)).half().numpy()
-    t0 = time.perf_counter()
-    deq, _, _, _ = O.pseudo_quantize_tensor(w, 4, True, g)
-    t_deq = time.perf_counter() - t0
-    O.w4a16_linear(x, deq)
-    n_calls, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and n_calls < 2000:
-        O.w4a16_linear(x, deq)
-        n_calls += 1
-    per = (time.perf_counter() - t0) / n_calls
-    nbytes = n * k // 2 + 2 * n * (k // g) * 2 + m * k * 2 + m * n * 2
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count()
-    return {"value": round(nbytes / per / 1e12, 6), "unit": "TB/s", "cores": cores, "kind": "port",
-            "sample": f"{n_calls} calls of oracle w4a16_linear (numpy fp32 BLAS on fp16 AWQ-dequantized "
-                      f"weights) at M={m}, K=N={k}, g={g}; {per * 1e3:.3f} ms/call; AWQ dequant "
-                      f"{t_deq:.2f} s once (excluded)",
-            "ms_per_call": per * 1e3}
+    from oracle import cpu_baseline as CB
+    info = CB.host_info()
+    out = {}
+    _log("cpu baseline: W4A16 M=1")
+    out["head"] = CB.w4a16_linear(m=1)
+    if "w4" in legs:
+        _log("cpu baseline: W4A16 M=16")
+        out["w4a16_m16_k4096_n4096"] = CB.w4a16_linear(m=16)
+    if "w8" in legs:
+        _log("cpu baseline: W8A8 M=16 / 4096")
+        out["w8a8_m16_k4096_n11008"] = CB.w8a8_fake_linear(m=16)
+        out["w8a8_m4096_k4096_n11008"] = CB.w8a8_fake_linear(m=4096)
+    if "moe" in legs:
+        _log("cpu baseline: MoE")
+        out["moe_w8a8_mixtral_t512"] = CB.moe_fake()
+    if "dec7b" in legs:
+        _log("cpu baseline: 7B layer")
+        out["llama2_7b_w4a16"] = CB.decoder_layer_decode(4096, 11008, 32, 32, 32)
+    if "dec70b" in legs:
+        _log("cpu baseline: 70B layer")
+        out["llama3_70b_w4a16"] = CB.decoder_layer_decode(8192, 28672, 64, 8, 80)
+    for v in out.values():
+        v.update({"cores": info["threads"], "nproc": info["nproc"], "cpu_model": info["cpu_model"],
+                  "kind": "port"})
+    return out
+
+
+def profile_mix(ops, name, steps):
+    """Kernel mixes that the rocprofv3 summaries in profiles/ were taken from."""
+    if name == "w4gemv":
+        pk, sc, zr = _w4_copies(ops, 4096, 4096, 64)
+        x = torch.randn(1, 4096, device="cuda").half()
+        ms = _time_graph(lambda i: ops.w4a16_gemm(x, pk[i], sc[i], zr[i], 128, None), 64, steps, 5)
+        print(f"w4gemv: {ms / 64 * 1e3:.3f} us per launch")
+    elif name == "readfloor":
+        # a one-launch read of the headline GEMV's 8.9 MB (int32 sum over 64 rotated buffers):
+        # launch + latency + transfer with no dequant or dot work
+        bufs = [torch.ones(8929280 // 4, dtype=torch.int32, device="cuda") for _ in range(64)]
+        outs = [torch.empty((), dtype=torch.int64, device="cuda") for _ in range(64)]
+        ms = _time_graph(lambda i: torch.sum(bufs[i], dim=0, out=outs[i]), 64, steps, 5)
+        print(f"readfloor: {ms / 64 * 1e3:.3f} us per 8.9 MB read launch")
+    elif name == "w4shapes":
+        for m, n, k, c in ((16, 4096, 4096, 64), (1, 28672, 8192, 8), (1, 8192, 28672, 8), (16, 28672, 8192, 8),
+                           (64, 28672, 8192, 8)):
+            pk, sc, zr = _w4_copies(ops, n, k, c)
+            x = torch.randn(m, k, device="cuda").half()
+            ms = _time_graph(lambda i: ops.w4a16_gemm(x, pk[i], sc[i], zr[i], 128, None), c, steps, 3)
+            print(f"w4 m={m} n={n} k={k}: {ms / c * 1e3:.3f} us per launch")
+            del pk, sc, zr
+            torch.cuda.empty_cache()
+    elif name == "w8big":
+        gen = torch.Generator(device="cuda").manual_seed(1)
+        qx = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device="cuda", generator=gen)
+        qw = torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device="cuda", generator=gen)
+        st = torch.rand(4096, device="cuda") * 0.01
+        sw = torch.rand(11008, device="cuda") * 0.001
+        ms = _time_graph(lambda i: ops.w8a8_gemm(qx, st, qw, sw, None, torch.float16), 4, steps, 3) / 4
+        print(f"w8big: {ms * 1e3:.1f} us per launch, {2 * 4096 * 11008 * 4096 / (ms * 1e-3) / 1e12:.1f} TOPS")
+    else:
+        raise SystemExit(f"unknown profile mix {name!r}")
+    torch.cuda.synchronize()
 
 
 def traffic_probe(ops):
@@ -322,12 +367,13 @@ def traffic_probe(ops):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--legs", default="w4,w8,moe,dec7b,dec70b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the kernel mix profiled for HBM traffic (profiles/traffic.json) and exit")
+    ap.add_argument("--profile", default=None, help="run one kernel mix for rocprofv3 and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -337,6 +383,9 @@ def main():
 
     if args.traffic_probe:
         traffic_probe(ops)
+        return
+    if args.profile:
+        profile_mix(ops, args.profile, args.steps)
         return
     legs = set(args.legs.split(","))
     steps, warmup = args.steps, args.warmup
@@ -350,17 +399,20 @@ def main():
     if "w4" in legs:
         _log("leg w4a16 M=16")
         out_legs["w4a16_m16_k4096_n4096"], _ = leg_w4a16(ops, 16, 4096, 4096, steps, warmup)
+        out_legs["w4a16_m16_k4096_n4096"]["roofline"]["traffic"] = _traffic("w4a16_m16_k4096_n4096")
         _log("leg w4a16 70B shapes")
-        out_legs["w4a16_m1_k8192_n28672"], _ = leg_w4a16(ops, 1, 28672, 8192, max(20, steps // 4), warmup // 2, copies=8)
-        out_legs["w4a16_m1_k28672_n8192"], _ = leg_w4a16(ops, 1, 8192, 28672, max(20, steps // 4), warmup // 2, copies=8)
+        small = max(2, steps // 4)
+        for m, n, k in ((1, 28672, 8192), (1, 8192, 28672)):
+            key = f"w4a16_m{m}_k{k}_n{n}"
+            out_legs[key], _ = leg_w4a16(ops, m, n, k, small, max(1, warmup // 2), copies=8)
+            out_legs[key]["roofline"]["traffic"] = _traffic(key)
     if "w8" in legs:
         for m in (4096, 256, 16, 1):
             _log(f"leg w8a8 M={m}")
-            out_legs[f"w8a8_m{m}_k4096_n11008"] = leg_w8a8(ops, m, 11008, 4096,
-                                                            max(10, steps // (10 if m >= 4096 else 2)), warmup // 2)
+            out_legs[f"w8a8_m{m}_k4096_n11008"] = leg_w8a8(ops, m, 11008, 4096, steps, max(1, warmup // 2))
     if "moe" in legs:
         _log("leg moe")
-        out_legs["moe_w8a8_mixtral_t512"] = leg_moe(ops, max(5, steps // 20), max(2, warmup // 4))
+        out_legs["moe_w8a8_mixtral_t512"] = leg_moe(ops, max(3, steps // 2), max(1, warmup // 4))
     dec = None
     if "dec7b" in legs:
         _log("leg llama-2-7b-shaped W4A16 decode")
@@ -372,8 +424,11 @@ def main():
                                                    prefill_batch=0)
     cpu = None
     if not args.no_cpu_baseline:
-        _log("cpu baseline")
-        cpu = cpu_baseline_w4a16()
+        cpus = cpu_baselines(legs)
+        cpu = cpus.pop("head")
+        for key, v in cpus.items():
+            if key in out_legs:
+                out_legs[key]["cpu_baseline"] = v
     w8 = out_legs.get("w8a8_m4096_k4096_n11008")
     res = {
         "metric": METRIC,
@@ -382,14 +437,16 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": round(head["ms_per_call"], 6),
+        "ms_per_step": round(head["ms_per_step"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u4xf16->f32",
+        "dtype": "u4*f16->f16",
         "data": "synthetic",
-        "config": {"workload": "W4A16 g128 asym GEMV, M=1, K=N=4096, fp16 activations, 64 rotated weight copies",
-                   "m": 1, "k": 4096, "n": 4096, "group_size": 128},
+        "config": {"workload": "W4A16 g128 asym GEMV, M=1, K=N=4096, fp16 activations; a step is one pass over "
+                               "64 distinct linears (64 rotated weight copies, one launch each)",
+                   "m": 1, "k": 4096, "n": 4096, "group_size": 128, "launches_per_step": 64,
+                   "working_set_bytes": head["working_set_bytes"], "us_per_launch": round(head["ms_per_call"] * 1e3, 3)},
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "int8_tops_m4096": round(w8["tops"], 2) if w8 else None,

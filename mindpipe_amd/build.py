@@ -55,13 +55,26 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
+def _stale(src: Path) -> bool:
+    """An object is stale when it is missing or older than its source or any shared header."""
+    obj = BUILD_DIR / (src.stem + ".o")
+    if not obj.exists():
+        return True
+    deps = [src, *CSRC.glob("*.h"), PKG.parent / "include" / "mindpipe_amd.h", Path(__file__)]
+    return any(d.stat().st_mtime > obj.stat().st_mtime for d in deps if d.exists())
+
+
+def build(verbose: bool = True, incremental: bool = False) -> Path:
+    """Compile every ``csrc/*.hip`` and link the library.  ``incremental=True`` (a development
+    aid) recompiles only sources whose object is stale."""
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     BUILD_DIR.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+    todo = [s for s in srcs if _stale(s)] if incremental else srcs
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(8, len(todo)))) as ex:
+        list(ex.map(_compile, todo))
+    objs = [BUILD_DIR / (s.stem + ".o") for s in srcs]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -74,4 +87,4 @@ def build(verbose: bool = True) -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv[1:])
