@@ -42,9 +42,19 @@ FILE_FLAGS = {
 }
 
 
+# ``--knobs`` (or MINDPIPE_AMD_KNOBS=1) builds a measurement library whose kernel choice follows
+# the MP_W4_* / MP_W8_* environment variables; the default library ignores them.
+KNOB_FLAGS = ["-DMP_MEASUREMENT_KNOBS"]
+
+
+def _knobs() -> bool:
+    return "--knobs" in sys.argv[1:] or os.environ.get("MINDPIPE_AMD_KNOBS") == "1"
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *(KNOB_FLAGS if _knobs() else []), *FILE_FLAGS.get(src.name, []), "-c", str(src),
+           "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")

@@ -27,6 +27,18 @@ static inline bool mp_aligned(const void *p, size_t a) {
 
 static inline int64_t mp_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Measurement knobs: the environment variables that steer a kernel choice (MP_W4_*, MP_W8_*) are
+// read only by a library compiled with -DMP_MEASUREMENT_KNOBS (python -m mindpipe_amd.build
+// --knobs).  The default build ignores the environment, so every call takes the tested default.
+static inline const char *mp_knob(const char *name) {
+#ifdef MP_MEASUREMENT_KNOBS
+  return getenv(name);
+#else
+  (void)name;
+  return nullptr;
+#endif
+}
+
 // ---- scalar conversions (round to nearest even everywhere)
 __device__ __forceinline__ float mp_h2f(uint16_t b) {
   return __half2float(__ushort_as_half(b));

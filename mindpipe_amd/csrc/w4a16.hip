@@ -1257,17 +1257,146 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(
   }
 }
 
+// One-row GEMV on the matrix cores: y[n] = sum_k x[k] * s(n, g) * (u(n, k) - z(n, g)) (+ bias),
+// the product of ``VllmPackedInt4Linear``'s dequantised weight with one token row
+// (reference: scripts/repro/dequant_vllm_int4.py:21-47 dequantisation, then F.linear).
+// A workgroup of W waves owns 16 output rows; wave w takes the 512-wide K slices w, w + W, ...
+// (NSL of them, K = 512 W NSL).  Lane l: output row n = l & 15, lane group g = l >> 4.
+//  * Weights: per slice, four 16-byte loads per lane (row n, K offset 32 (4 i + g) of the slice,
+//    i = the slice's 128-wide group); every load of every slice is issued before any arithmetic.
+//  * Activations: one 16-byte load per lane per slice (K 8 l .. 8 l + 7 of the slice), permuted
+//    into the nibble order of the dequantised words and staged in a wave-private LDS block (no
+//    workgroup barrier before the MFMAs).
+//  * Dequantisation: (w & 0x000F000F) | 0x64006400 is the fp16 pair 1024 + u, and the 0x00F000F0
+//    mask gives 1024 + 16 u; subtracting 1024 + z (resp. 1024 + 16 z) in fp16 is exact, so the
+//    MFMA (16x16x32 f16, the row broadcast over the 16 A rows) sums exact products x (u - z) into
+//    fp32 and the group scale multiplies each group's sum.
+//  * The W waves' partial rows meet in LDS; wave 0 adds them in wave order and stores.
+template <int W, int NSL, bool ZP>
+__global__ __launch_bounds__(W * 64) void w4a16_gemv_mfma_kernel(
+    const uint16_t *__restrict__ x, int k, const uint32_t *__restrict__ wq, int n_rows,
+    const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
+  constexpr int KS = 512, NG = KS / 128;
+  __shared__ uint4 xs[W][NSL][64];  // per slice: 32 blocks of 16 K, each (even 16 B, odd 16 B)
+  __shared__ float red[W][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int row = blockIdx.x * 16 + n;
+  const int rowc = row < n_rows ? row : n_rows - 1;
+  const int kw = k >> 3;
+  // scale / zero words of the slice's four groups first, then the activations, then the weights
+  uint2 sv[NSL], zv[NSL];
+#pragma unroll
+  for (int sl = 0; sl < NSL; ++sl) {
+    const int64_t e = static_cast<int64_t>(rowc) * n_groups + (wave + W * sl) * NG;
+    sv[sl] = *reinterpret_cast<const uint2 *>(sc + e);
+    zv[sl] = ZP ? *reinterpret_cast<const uint2 *>(zr + e) : make_uint2(0x48004800u, 0x48004800u);  // fp16 8
+  }
+  uint4 xv[NSL];
+#pragma unroll
+  for (int sl = 0; sl < NSL; ++sl) xv[sl] = *reinterpret_cast<const uint4 *>(x + (wave + W * sl) * KS + 8 * lane);
+  uint4 wv[NSL][NG];
+#pragma unroll
+  for (int sl = 0; sl < NSL; ++sl) {
+    const uint32_t *wr = wq + static_cast<int64_t>(rowc) * kw + (wave + W * sl) * (KS / 8);
+#pragma unroll
+    for (int i = 0; i < NG; ++i) wv[sl][i] = *reinterpret_cast<const uint4 *>(wr + 4 * (4 * i + g));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // lane l holds K 8 l .. 8 l + 7 = half (l & 1) of block l >> 1: even positions (0 4 2 6) and
+  // odd ones (1 5 3 7) of that half, in the order the dequantised words hold the nibbles
+#pragma unroll
+  for (int sl = 0; sl < NSL; ++sl) {
+    const uint4 d = xv[sl];
+    uint2 ev, od;
+    ev.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);  // x0 x4
+    ev.y = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);  // x2 x6
+    od.x = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);  // x1 x5
+    od.y = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);  // x3 x7
+    uint2 *blk = reinterpret_cast<uint2 *>(&xs[wave][sl][2 * (lane >> 1)]);
+    blk[lane & 1] = ev;
+    blk[2 + (lane & 1)] = od;
+  }
+#pragma unroll
+  for (int sl = 0; sl < NSL; ++sl)  // keep the scale / zero loads ahead of the weights
+    asm volatile("" : "+v"(sv[sl].x), "+v"(sv[sl].y), "+v"(zv[sl].x), "+v"(zv[sl].y));
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes land before its reads
+  __builtin_amdgcn_wave_barrier();
+  uint32_t magic_v = kMagic, m0_v = 0x000F000Fu, m1_v = 0x00F000F0u;
+  asm volatile("" : "+v"(magic_v), "+v"(m0_v), "+v"(m1_v));  // opaque: keep the constants in VGPRs
+  float total = 0.f;
+#pragma unroll
+  for (int sl = 0; sl < NSL; ++sl) {
+    const uint32_t sw[2] = {sv[sl].x, sv[sl].y}, zw[2] = {zv[sl].x, zv[sl].y};
+    f4_t accr[NG], accx[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const uint32_t zh = (zw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+      const h2_t z2 = mp_as_h2(zh | (zh << 16));
+      const h2_t ze = z2 + mp_as_h2(kMagic);                        // 1024 + z
+      const h2_t zo = z2 * mp_as_h2(0x4C004C00u) + mp_as_h2(kMagic);  // 1024 + 16 z
+      const uint32_t w4[4] = {wv[sl][i].x, wv[sl][i].y, wv[sl][i].z, wv[sl][i].w};
+      accr[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+      accx[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t wa = w4[2 * t], wb = w4[2 * t + 1];
+        const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
+        h2_t br[4], bx[4];
+        br[0] = mp_as_h2((wa & m0_v) | magic_v) - ze;
+        br[1] = mp_as_h2((wa8 & m0_v) | magic_v) - ze;
+        br[2] = mp_as_h2((wb & m0_v) | magic_v) - ze;
+        br[3] = mp_as_h2((wb8 & m0_v) | magic_v) - ze;
+        bx[0] = mp_as_h2((wa & m1_v) | magic_v) - zo;
+        bx[1] = mp_as_h2((wa8 & m1_v) | magic_v) - zo;
+        bx[2] = mp_as_h2((wb & m1_v) | magic_v) - zo;
+        bx[3] = mp_as_h2((wb8 & m1_v) | magic_v) - zo;
+        const int b = 2 * (4 * i + g) + t;  // 16-K block of the slice
+        const uint4 ae = xs[wave][sl][2 * b], ao = xs[wave][sl][2 * b + 1];
+        accr[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, ae), __builtin_bit_cast(h8_t, br),
+                                                         accr[i], 0, 0, 0);
+        accx[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, ao), __builtin_bit_cast(h8_t, bx),
+                                                         accx[i], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+      total = fmaf(mp_h2f(static_cast<uint16_t>(sw[i >> 1] >> (16 * (i & 1)))), fmaf(accx[i][0], 0.0625f, accr[i][0]),
+                   total);
+  }
+  if (W > 1) {
+    if (g == 0) red[wave][n] = total;
+    mp_lds_barrier();
+    if (wave != 0) return;
+    total = red[0][n];
+#pragma unroll
+    for (int w = 1; w < W; ++w) total += red[w][n];
+  }
+  if (g == 0 && row < n_rows) {
+    if (bias) total += mp_h2f(bias[row]);
+    y[row] = mp_f2h(total);
+  }
+}
+
 // Measurement knobs for the one-row GEMV shape choice: MP_W4_GEMV_R (rows per
 // wave), MP_W4_GEMV_C (chunks per iteration), MP_W4_GEMV_S (waves splitting K);
 // MP_W4_GEMV_OFF=1 routes one-row calls to the general decode kernel.
 static int mp_gemv_env(int which) {
   static const int v[4] = {
-      getenv("MP_W4_GEMV_OFF") ? atoi(getenv("MP_W4_GEMV_OFF")) : 0,
-      getenv("MP_W4_GEMV_R") ? atoi(getenv("MP_W4_GEMV_R")) : 0,
-      getenv("MP_W4_GEMV_C") ? atoi(getenv("MP_W4_GEMV_C")) : 0,
-      getenv("MP_W4_GEMV_S") ? atoi(getenv("MP_W4_GEMV_S")) : 0,
+      mp_knob("MP_W4_GEMV_OFF") ? atoi(mp_knob("MP_W4_GEMV_OFF")) : 0,
+      mp_knob("MP_W4_GEMV_R") ? atoi(mp_knob("MP_W4_GEMV_R")) : 0,
+      mp_knob("MP_W4_GEMV_C") ? atoi(mp_knob("MP_W4_GEMV_C")) : 0,
+      mp_knob("MP_W4_GEMV_S") ? atoi(mp_knob("MP_W4_GEMV_S")) : 0,
   };
   return v[which];
+}
+
+// MP_W4_GEMV_MFMA=0 routes the one-row shapes the matrix-core GEMV takes to the VALU GEMV (for
+// measurements).
+static bool mp_gemv_mfma() {
+  static const bool v = !(mp_knob("MP_W4_GEMV_MFMA") && atoi(mp_knob("MP_W4_GEMV_MFMA")) == 0);
+  return v;
 }
 
 // Batched-kernel shape knobs (for measurements): MP_W4_BATCH_NT (column tiles per
@@ -1275,17 +1404,17 @@ static int mp_gemv_env(int which) {
 // MP_W4_BATCH_ALWAYS=0 (LDS-staged decode kernel above N = 16384 for M < 32).
 static int mp_batch_env(int which) {
   static const int v[4] = {
-      getenv("MP_W4_BATCH_NT") ? atoi(getenv("MP_W4_BATCH_NT")) : 0,
-      getenv("MP_W4_BATCH_S") ? atoi(getenv("MP_W4_BATCH_S")) : 0,
-      getenv("MP_W4_BATCH_WAVES") ? atoi(getenv("MP_W4_BATCH_WAVES")) : 0,  // 0: the shape's default
-      getenv("MP_W4_BATCH_ALWAYS") ? atoi(getenv("MP_W4_BATCH_ALWAYS")) : 1,
+      mp_knob("MP_W4_BATCH_NT") ? atoi(mp_knob("MP_W4_BATCH_NT")) : 0,
+      mp_knob("MP_W4_BATCH_S") ? atoi(mp_knob("MP_W4_BATCH_S")) : 0,
+      mp_knob("MP_W4_BATCH_WAVES") ? atoi(mp_knob("MP_W4_BATCH_WAVES")) : 0,  // 0: the shape's default
+      mp_knob("MP_W4_BATCH_ALWAYS") ? atoi(mp_knob("MP_W4_BATCH_ALWAYS")) : 1,
   };
   return v[which];
 }
 
 // Double-buffered activations at <= 16 rows (MP_W4_BATCH_XDB=0 turns them off, for measurements).
 static bool mp_batch_xdb() {
-  static const bool v = !(getenv("MP_W4_BATCH_XDB") && atoi(getenv("MP_W4_BATCH_XDB")) == 0);
+  static const bool v = !(mp_knob("MP_W4_BATCH_XDB") && atoi(mp_knob("MP_W4_BATCH_XDB")) == 0);
   return v;
 }
 
@@ -1293,7 +1422,7 @@ static bool mp_batch_xdb() {
 // workgroups per column group when M exceeds them.  Default: MT = 1 up to 16 rows, 2 above
 // (33..64 rows in two parts).  MP_W4_BATCH_PART_MT=1 / 2 / 4 fixes MT (for measurements).
 static int mp_batch_part_mt(int64_t m) {
-  static const int v = getenv("MP_W4_BATCH_PART_MT") ? atoi(getenv("MP_W4_BATCH_PART_MT")) : 0;
+  static const int v = mp_knob("MP_W4_BATCH_PART_MT") ? atoi(mp_knob("MP_W4_BATCH_PART_MT")) : 0;
   if (v == 1 || v == 2 || v == 4) return v;
   return m <= 16 ? 1 : 2;
 }
@@ -1303,7 +1432,7 @@ static int mp_batch_part_mt(int64_t m) {
 // MP_W4_BATCH_MIN_M overrides it, for measurements.
 static int mp_batch_min_m() {
   static int v = [] {
-    const char *e = getenv("MP_W4_BATCH_MIN_M");
+    const char *e = mp_knob("MP_W4_BATCH_MIN_M");
     return e ? atoi(e) : 1;
   }();
   return v;
@@ -1313,7 +1442,7 @@ static int mp_batch_min_m() {
 // 128 x 128 tiles of 4 waves on the 7B linears at M = 2048); MP_W4_PREFILL_THREADS=256 selects the
 // smaller tile (for measurements).
 static int mp_prefill_threads() {
-  static const int v = getenv("MP_W4_PREFILL_THREADS") ? atoi(getenv("MP_W4_PREFILL_THREADS")) : 512;
+  static const int v = mp_knob("MP_W4_PREFILL_THREADS") ? atoi(mp_knob("MP_W4_PREFILL_THREADS")) : 512;
   return v;
 }
 
@@ -1602,7 +1731,30 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
   // batched kernel for every N (MP_W4_BATCH_ALWAYS=0: the LDS-staged kernel for
   // N > 16384 below 32 rows, for measurements)
   const bool batch_shape = m >= 32 || n <= 16384 || mp_batch_env(3);
-  if (m == 1 && mp_gemv_env(0) == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
+  // matrix-core GEMV at K = 2048 and 4096 (W = 4, 8 waves of 512-wide slices); measured against the
+  // VALU GEMV on the 7B / 70B layer shapes: 4.24 vs 4.74 us at N = K = 4096, 11.3 vs 11.6 us at
+  // N = 22016, 2.98 vs 3.24 us at N = K = 2048, but 26.5 vs 24.9 us at K = 8192, N = 28672 (with
+  // 8 or 16 waves), where the VALU GEMV's contiguous 2048-wide row chunks stream faster
+  const int mfma_slices = (k == 2048 || k == 4096) ? static_cast<int>(k / 512) : 0;
+  const bool mfma_gemv = m == 1 && mp_gemv_env(0) == 0 && mp_gemv_mfma() && group_size == 128 &&
+                         mfma_slices != 0 && mp_aligned(x, 16) &&
+                         mp_aligned(w_packed, 16) && mp_aligned(scales, 8) && (zeros == nullptr || mp_aligned(zeros, 8));
+  if (mfma_gemv) {
+    const int ki = static_cast<int>(k), ni = static_cast<int>(n);
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(n, 16)));
+#define MP_W4_GEMV_MFMA(W_, NSL_)                                                                          \
+  do {                                                                                                     \
+    if (zp)                                                                                                \
+      hipLaunchKernelGGL((w4a16_gemv_mfma_kernel<W_, NSL_, true>), grid, dim3(W_ * 64), 0, s, xp, ki, wp, ni, \
+                         sp, zp, n_groups_i, bp, yp);                                                       \
+    else                                                                                                   \
+      hipLaunchKernelGGL((w4a16_gemv_mfma_kernel<W_, NSL_, false>), grid, dim3(W_ * 64), 0, s, xp, ki, wp,   \
+                         ni, sp, zp, n_groups_i, bp, yp);                                                   \
+  } while (0)
+    if (mfma_slices == 4) MP_W4_GEMV_MFMA(4, 1);
+    else MP_W4_GEMV_MFMA(8, 1);
+#undef MP_W4_GEMV_MFMA
+  } else if (m == 1 && mp_gemv_env(0) == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
     const int ki = static_cast<int>(k), ni = static_cast<int>(n);
     const int nch = (ki + 2047) / 2048;  // 2048-wide K chunks
     // measured on the 7B / 70B layer shapes: all chunks up front for short K, two waves
@@ -1771,7 +1923,7 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
 #define MP_W4_PF512(D_)                                                                                      \
   hipLaunchKernelGGL((w4a16_prefill_kernel<D_, 512>), grid, dim3(512), 0, s, xp, static_cast<int>(m),         \
                      static_cast<int>(k), wp, static_cast<int>(n), sp, zp, n_groups, group_size, bp, yp)
-      const int st = getenv("MP_W4_PREFILL_STAGES") ? atoi(getenv("MP_W4_PREFILL_STAGES")) : kPrefillStages;
+      const int st = mp_knob("MP_W4_PREFILL_STAGES") ? atoi(mp_knob("MP_W4_PREFILL_STAGES")) : kPrefillStages;
       if (st == 2) MP_W4_PF512(1);
       else if (st == 3) MP_W4_PF512(2);
       else if (st == 5) MP_W4_PF512(4);

@@ -1603,7 +1603,7 @@ constexpr int kTBK2 = 128;
 // global->LDS loads; MP_W8_BIG_VARIANT selects, for measurements.
 static int mp_big_variant() {
   static int v = [] {
-    const char *e = getenv("MP_W8_BIG_VARIANT");
+    const char *e = mp_knob("MP_W8_BIG_VARIANT");
     return e ? atoi(e) : 8;
   }();
   return v;
@@ -1625,7 +1625,7 @@ static int mp_cu_count() {
 // LDS-staged 16-byte-store epilogue (MP_W8_STAGED=0 turns it off, for measurements).
 static int mp_staged_epilogue() {
   static int v = [] {
-    const char *e = getenv("MP_W8_STAGED");
+    const char *e = mp_knob("MP_W8_STAGED");
     return e ? atoi(e) : 1;
   }();
   return v;
@@ -1636,7 +1636,7 @@ static int mp_staged_epilogue() {
 // kernel with 256-row tiles, 0 = the tiled kernel (MP_W8_GROUPED_BIG, for measurements).
 static int mp_grouped_big() {
   static int v = [] {
-    const char *e = getenv("MP_W8_GROUPED_BIG");
+    const char *e = mp_knob("MP_W8_GROUPED_BIG");
     return e ? atoi(e) : 1;
   }();
   return v;
@@ -1646,7 +1646,7 @@ static int mp_grouped_big() {
 // kernel, =2/3/5 sets 1/2/4 rows per wave; for measurements).
 static int mp_i8_gemv() {
   static int v = [] {
-    const char *e = getenv("MP_W8_GEMV");
+    const char *e = mp_knob("MP_W8_GEMV");
     return e ? atoi(e) : 1;
   }();
   return v;
@@ -1656,7 +1656,7 @@ static int mp_i8_gemv() {
 // forces 64 (for measurements).
 static int mp_tiled_bk() {
   static int v = [] {
-    const char *e = getenv("MP_W8_TILED_BK");
+    const char *e = mp_knob("MP_W8_TILED_BK");
     return e ? atoi(e) : 128;
   }();
   return v;
@@ -1668,7 +1668,7 @@ static int mp_tiled_bk() {
 static int mp_tiled_variant(int64_t k, int64_t wgs) {
   if (k % kTBK2 != 0 || mp_tiled_bk() != 128) return 0;
   static const int forced = [] {  // MP_W8_TILED_VARIANT=0/1/2 forces a variant (for measurements)
-    const char *e = getenv("MP_W8_TILED_VARIANT");
+    const char *e = mp_knob("MP_W8_TILED_VARIANT");
     return e ? atoi(e) : -1;
   }();
   if (forced >= 0 && forced <= 2) return forced;
@@ -1679,14 +1679,14 @@ static int mp_tiled_variant(int64_t k, int64_t wgs) {
 }
 
 static bool mp_skinny_one_chunk() {
-  static const bool v = !(getenv("MP_W8_SKINNY_ONE_CHUNK") && atoi(getenv("MP_W8_SKINNY_ONE_CHUNK")) == 0);
+  static const bool v = !(mp_knob("MP_W8_SKINNY_ONE_CHUNK") && atoi(mp_knob("MP_W8_SKINNY_ONE_CHUNK")) == 0);
   return v;
 }
 
 // Persistent large-M launch (MP_W8_PERSIST=0 turns it off, for measurements).
 static int mp_persist() {
   static int v = [] {
-    const char *e = getenv("MP_W8_PERSIST");
+    const char *e = mp_knob("MP_W8_PERSIST");
     return e ? atoi(e) : 1;
   }();
   return v;
@@ -1696,7 +1696,7 @@ static int mp_persist() {
 // register stages in flight), 2 = three stages, 0 = off (MP_W8_MOE, for measurements).
 static int mp_moe_kernel() {
   static int v = [] {
-    const char *e = getenv("MP_W8_MOE");
+    const char *e = mp_knob("MP_W8_MOE");
     return e ? atoi(e) : 1;
   }();
   return v;

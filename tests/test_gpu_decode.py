@@ -204,8 +204,10 @@ def test_decoder_kernel_step_matches_torch_step(heads, kv_heads):
                                                     (8192, 2 * 700, True, False, False, True),
                                                     (2048, 2 * 64, True, True, True, False)])
 def test_gemv_add_rms_norm_equals_two_launch_chain(k, n, swiglu, res, bias, zp):
-    """The norm-fused one-row GEMV gives the bits of add_rms_norm_quant (quant off)
-    followed by w4a16_gemm / w4a16_gemm_swiglu, and the same residual sum."""
+    """The norm-fused one-row GEMV against add_rms_norm_quant (quant off) followed by w4a16_gemm /
+    w4a16_gemm_swiglu: the same residual sum bits, and the same output bits where the second step runs
+    the same VALU GEMV arithmetic (the fused gate/up, K = 8192); where w4a16_gemm takes the
+    matrix-core GEMV (one row, K = 2048 / 4096: another summation order) rel. error <= 1e-3."""
     _say("gemv_add_rms_norm", k, n, swiglu, res, bias, zp)
     from mindpipe_amd import ops
     g = torch.Generator(device=DEV).manual_seed(k + n)
@@ -220,7 +222,10 @@ def test_gemv_add_rms_norm_equals_two_launch_chain(k, n, swiglu, res, bias, zp):
     hn, _, _, rs2 = ops.add_rms_norm_quant(x, r, w, 1e-5, quant=False)
     want = (ops.w4a16_gemm_swiglu(hn, packed, sc, zr, 128, b) if swiglu
             else ops.w4a16_gemm(hn, packed, sc, zr, 128, b))
-    assert torch.equal(y, want)
+    if swiglu or k not in (2048, 4096):
+        assert torch.equal(y, want)
+    else:
+        assert _rel(y.float(), want.float()) <= 1e-3
     assert (rsum is None) == (r is None) and (rsum is None or torch.equal(rsum, rs2))
     # a second call (other workgroup timing) gives the same bits
     y2, _ = ops.w4a16_gemv_add_rms_norm(x, r, w, 1e-5, packed, sc, zr, 128, b, swiglu)
@@ -242,8 +247,9 @@ def test_gemv_add_rms_norm_rejects_unsupported():
 
 
 def test_decoder_one_row_step_fused_norm():
-    """B = 1 decode step with every add-RMSNorm inside the next GEMV: the same logits bits
-    as the two-launch chain, and within 2e-2 of the PyTorch step."""
+    """B = 1 decode step with every add-RMSNorm inside the next GEMV: within 1e-3 of the two-launch
+    chain (whose q/k/v GEMV at K = 2048 runs the matrix-core GEMV, another summation order than the
+    norm-fused VALU GEMV), and within 2e-2 of the PyTorch step."""
     _say("decoder fused-norm step")
     from mindpipe_amd.decoder import DecoderConfig, W4Decoder
     cfg = DecoderConfig(layers=2, hidden=2048, heads=16, kv_heads=4, ffn=1024, vocab=512)
@@ -258,7 +264,7 @@ def test_decoder_one_row_step_fused_norm():
     model.k_cache.copy_(kc); model.v_cache.copy_(vc)
     model.fuse_norm = False
     lu = model.decode_step(tok, cur, return_logits=True)
-    assert torch.equal(lf, lu)
+    assert _rel(lf.float(), lu.float()) <= 1e-3
     model.k_cache.copy_(kc); model.v_cache.copy_(vc)
     lt = model.decode_step_torch(tok, cur, return_logits=True)
     assert _rel(lf.float(), lt.float()) <= 2e-2

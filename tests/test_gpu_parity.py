@@ -112,6 +112,8 @@ W4_CASES = [(1, 4096, 4096), (16, 4096, 4096), (3, 512, 1024), (17, 256, 2048), 
             (24, 8192, 1024), (32, 1024, 2048), (40, 400, 1024), (12, 20480, 512),
             # one-row GEMV: partial 2048-wide K chunk, N not a multiple of the rows per wave, odd chunk count
             (1, 37, 768), (1, 301, 2304), (1, 1001, 11008), (1, 64, 6144),
+            # one-row matrix-core GEMV (K = 2048, 4096): N not a multiple of its 16-row tiles
+            (1, 2048, 2048), (1, 1000, 4096), (1, 24, 2048), (1, 4097, 4096), (1, 8, 2048),
             # 2..8 rows (four-row MFMA kernel): half-filled last K chunk, N not a multiple of 16, split-K waves
             (2, 4096, 4096), (4, 1000, 2304), (5, 4096, 11008), (8, 12288, 4096), (7, 300, 1280), (6, 72, 512),
             # 33..64 rows as two 32-row halves of one grid: padding workgroups, 4 / 2 / 1 column tiles
@@ -146,9 +148,10 @@ def test_w4a16_gemm_matches_dequant_matmul(m, n, k, zp):
                                    (6, 300, 11008), (64, 8192, 2048), (45, 1000, 1024)])
 @pytest.mark.parametrize("zp", [True, False])
 def test_w4a16_gemm_swiglu_matches_two_step(m, i, k, zp):
-    """Fused gate/up GEMM + SiLU-mul against silu_mul(w4a16_gemm) (bit-exact for the one-row
-    GEMV, whose per-row arithmetic is the same; <= 1 ulp for the batched kernel, whose K split
-    may differ) and against the oracle's dequant -> matmul -> SiLU-mul (rel. error <= 1e-3)."""
+    """Fused gate/up GEMM + SiLU-mul against silu_mul(w4a16_gemm) (bit-exact where both run the
+    one-row VALU GEMV, whose per-row arithmetic is the same; <= 1 ulp for the batched kernel, whose K
+    split may differ; rel. <= 1e-3 where w4a16_gemm takes the one-row matrix-core GEMV, K = 2048 /
+    4096) and against the oracle's dequant -> matmul -> SiLU-mul (rel. error <= 1e-3)."""
     _say("w4a16 swiglu", m, i, k, zp)
     ops = _ops()
     n2 = 2 * i
@@ -167,7 +170,9 @@ def test_w4a16_gemm_swiglu_matches_two_step(m, i, k, zp):
     act = ops.w4a16_gemm_swiglu(_t(x), *args)
     two = ops.silu_mul(ops.w4a16_gemm(_t(x), *args))
     d = (act.view(torch.int16).int() - two.view(torch.int16).int()).abs()
-    if m == 1:
+    if m == 1 and k in (2048, 4096):
+        assert _rel(_np(act), _np(two)) <= 1e-3
+    elif m == 1:
         assert torch.equal(act, two)
     else:
         assert int(d.max()) <= 1 and float((d == 0).float().mean()) >= 0.99
