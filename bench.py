@@ -294,11 +294,11 @@ def profile_mix(ops, name, steps):
         ms = _time_graph(lambda i: ops.w4a16_gemm(x, pk[i], sc[i], zr[i], 128, None), 64, steps, 5)
         print(f"w4gemv: {ms / 64 * 1e3:.3f} us per launch")
     elif name == "readfloor":
-        # a one-launch read of the headline GEMV's 8.9 MB (int32 sum over 64 rotated buffers):
+        # the library's read probe over the headline GEMV's 8,929,280 bytes (64 rotated buffers):
         # launch + latency + transfer with no dequant or dot work
         bufs = [torch.ones(8929280 // 4, dtype=torch.int32, device="cuda") for _ in range(64)]
-        outs = [torch.empty((), dtype=torch.int64, device="cuda") for _ in range(64)]
-        ms = _time_graph(lambda i: torch.sum(bufs[i], dim=0, out=outs[i]), 64, steps, 5)
+        sinks = [ops.probe_read(b) for b in bufs]
+        ms = _time_graph(lambda i: ops.probe_read(bufs[i], sinks[i]), 64, steps, 5)
         print(f"readfloor: {ms / 64 * 1e3:.3f} us per 8.9 MB read launch")
     elif name == "w4shapes":
         for m, n, k, c in ((16, 4096, 4096, 64), (1, 28672, 8192, 8), (1, 8192, 28672, 8), (16, 28672, 8192, 8),
@@ -309,6 +309,20 @@ def profile_mix(ops, name, steps):
             print(f"w4 m={m} n={n} k={k}: {ms / c * 1e3:.3f} us per launch")
             del pk, sc, zr
             torch.cuda.empty_cache()
+    elif name == "w4batch8":
+        # the 7B gate/up (fused SiLU-up, N = 2 x 11008, K = 4096) and down (N = 4096, K = 11008)
+        # linears at M = 1 (one-row GEMV) and M = 8 (batched kernel), 4 eager launches each
+        for n, k, swiglu in ((2 * 11008, 4096, True), (4096, 11008, False)):
+            pk, sc, zr = _w4_copies(ops, n, k, 1)
+            for m in (1, 8):
+                x = torch.randn(m, k, device="cuda").half()
+                for _ in range(4):
+                    if swiglu:
+                        ops.w4a16_gemm_swiglu(x, pk[0], sc[0], zr[0], 128, None)
+                    else:
+                        ops.w4a16_gemm(x, pk[0], sc[0], zr[0], 128, None)
+            del pk, sc, zr
+        print("w4batch8 done")
     elif name == "w8big":
         gen = torch.Generator(device="cuda").manual_seed(1)
         qx = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device="cuda", generator=gen)
@@ -339,6 +353,17 @@ def traffic_probe(ops):
     x = torch.randn(1, 4096, device="cuda").half()
     for i in range(128):
         ops.w4a16_gemm(x, pk[i % 64], sc[i % 64], zr[i % 64], 128, None)
+    x16 = torch.randn(16, 4096, device="cuda").half()
+    for i in range(64):
+        ops.w4a16_gemm(x16, pk[i], sc[i], zr[i], 128, None)
+    del pk, sc, zr
+    # the 70B decode GEMVs (M = 1): K = 8192, N = 28672 and K = 28672, N = 8192, 4 rotated copies each
+    for n, k in ((28672, 8192), (8192, 28672)):
+        pk, sc, zr = _w4_copies(ops, n, k, 4)
+        xk = torch.randn(1, k, device="cuda").half()
+        for i in range(8):
+            ops.w4a16_gemm(xk, pk[i % 4], sc[i % 4], zr[i % 4], 128, None)
+        del pk, sc, zr
     qx = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device="cuda")
     qw = torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device="cuda")
     st = torch.rand(4096, device="cuda")

@@ -295,6 +295,13 @@ int mp_argmax_rows(const void *x, int64_t rows, int64_t n, int64_t *idx, mp_stre
 /* act [rows, I] = round(round(silu(gate)) * up) of gate_up [rows, 2I] (gate | up), fp16. */
 int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, mp_stream_t stream);
 
+/* Measurement probe (no counterpart in the reference): one launch that reads `bytes` (a multiple
+ * of 16, 16-byte aligned buf) with the one-row GEMVs' launch shape and no other work, so its
+ * duration is the read floor the kernels' roofline fractions are read against.  sink: uint32
+ * [mp_probe_read_sink_words(bytes)], written at most once per workgroup. */
+size_t mp_probe_read_sink_words(int64_t bytes);
+int mp_probe_read(const void *buf, int64_t bytes, uint32_t *sink, mp_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

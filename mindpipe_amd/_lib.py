@@ -40,6 +40,8 @@ SIGNATURES = {
                                         _vp, _vp, _sz, _vp]),
     "mp_silu_mul": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "mp_argmax_rows": (_i32, [_vp, _i64, _i64, _vp, _vp]),
+    "mp_probe_read_sink_words": (C.c_size_t, [_i64]),
+    "mp_probe_read": (_i32, [_vp, _i64, _vp, _vp]),
     "mp_w8_quantize_per_channel": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "mp_w8a8_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp]),
     "mp_moe_route_workspace_bytes": (_sz, [_i64, _i64, _i32]),

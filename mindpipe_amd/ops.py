@@ -621,3 +621,17 @@ def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch
         _lib.check(_lib.load().mp_silu_mul(gate_up.data_ptr(), rows, two_i // 2, out.data_ptr(), _stream()),
                    "mp_silu_mul")
     return out
+
+
+def probe_read(buf: torch.Tensor, sink: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One launch reading all of ``buf`` with the one-row GEMVs' launch shape and no other work (the
+    read floor of a one-launch kernel; a measurement probe).  Returns the sink it may write."""
+    if not buf.is_cuda or not buf.is_contiguous():
+        raise RuntimeError("buf must be a contiguous device tensor")
+    nbytes = buf.numel() * buf.element_size()
+    lib = _lib.load()
+    if sink is None:
+        sink = torch.zeros(max(1, int(lib.mp_probe_read_sink_words(nbytes))), dtype=torch.int32, device=buf.device)
+    with _dev(buf):
+        _lib.check(lib.mp_probe_read(buf.data_ptr(), nbytes, sink.data_ptr(), _stream()), "mp_probe_read")
+    return sink

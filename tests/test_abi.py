@@ -32,14 +32,18 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_host_validation_without_gpu():
-    """Argument checks run on the host before any launch (no GPU needed)."""
+    """Argument checks run on the host before any launch (no GPU needed).  Every pointer argument is
+    a real (host) buffer that no check reaches through: the calls are rejected before a launch."""
+    import ctypes
     from mindpipe_amd import _lib
     if not _lib.LIB_PATH.exists():
         pytest.skip("library not built")
     lib = _lib.load()
+    buf = ctypes.create_string_buffer(4096)
+    p = ctypes.addressof(buf)
     assert lib.mp_w4a16_gemm(None, 1, 128, None, 16, None, None, 128, None, None, 0, None) == 5
-    assert lib.mp_w8a8_gemm(1, 1, 1, 1, None, 0, 1, 9, 1, 16, 64, None) == 2      # bad out dtype
-    assert lib.mp_w8a8_gemm(1, 1, 1, 1, None, 0, 1, 0, 1, 16, 1 << 18, None) == 1  # K too large for int32
-    assert lib.mp_quant_per_token_i8(1, 4, 64, 7, 1, 1, 0, None) == 2
-    assert lib.mp_i8_gemm_swiglu_requant(1, 1, 1, 1, 1, 8, 16, 64, 128, 0, 0, 1, 1, 1, 0, None) == 6
-    assert lib.mp_moe_unpermute_combine(1, 1, 1, 4, 2, 64, 1, 1, 2, None) == 2   # fake rule needs fp16/bf16 out
+    assert lib.mp_w8a8_gemm(p, p, p, p, None, 0, p, 9, 1, 16, 64, None) == 2      # bad out dtype
+    assert lib.mp_w8a8_gemm(p, p, p, p, None, 0, p, 0, 1, 16, 1 << 18, None) == 1  # K too large for int32
+    assert lib.mp_quant_per_token_i8(p, 4, 64, 7, p, p, 0, None) == 2
+    assert lib.mp_i8_gemm_swiglu_requant(p, p, p, p, p, 8, 16, 64, 128, 0, 0, p, p, p, 0, None) == 6
+    assert lib.mp_moe_unpermute_combine(p, p, p, 4, 2, 64, 1, p, 2, None) == 2   # fake rule needs fp16/bf16 out
