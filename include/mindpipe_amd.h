@@ -295,6 +295,28 @@ int mp_argmax_rows(const void *x, int64_t rows, int64_t n, int64_t *idx, mp_stre
 /* act [rows, I] = round(round(silu(gate)) * up) of gate_up [rows, 2I] (gate | up), fp16. */
 int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, mp_stream_t stream);
 
+/* ---- SmoothQuant smoothing (offline) ----
+ * colmax [k] fp32 = max(colmax, max over rows |x[r, :]|) for x [rows, k] row-major (fp16 / bf16 /
+ * fp32, 16-byte aligned): the per-input-channel abs-max statistic of get_act_scales
+ * (smoothquant/calibration.py:27-58) over a calibration batch, and the weight statistic
+ * w_j = max_n |W_nj| of _compute_smooth_scales (smooth.py:16-20) over every fc sharing a norm.
+ * accumulate = 0 starts from zeros; 1 keeps the running maxima (several fcs / batches).  Exact. */
+int mp_colmax_abs(const void *x, int dtype, int64_t rows, int64_t k, int accumulate, float *colmax,
+                  mp_stream_t stream);
+
+/* scales [k] in dtype = (a^alpha / w^(1-alpha)).clamp(1e-5) of _compute_smooth_scales
+ * (smooth.py:7-25): a = act_max cast to dtype, w = w_colmax clamped at 1e-5, every op rounded to
+ * dtype, with the fp32 powers correctly rounded (square roots at alpha = 0.5, as torch's pow).  alpha
+ * is a double, as the Python scalar is: the exponents are (float)alpha and (float)(1 - alpha), the
+ * values torch applies. */
+int mp_smooth_scales(const float *act_max, const float *w_colmax, int64_t k, double alpha, int dtype, void *scales,
+                     mp_stream_t stream);
+
+/* In place w[r, j] = w[r, j] * scales[j] (divide = 0: fc.weight.mul_(s.view(1, -1))) or
+ * w[r, j] / scales[j] (divide = 1: ln.weight.div_(s), rows = 1), rounded to dtype
+ * (smooth_ln_fcs_llama_like, smooth.py:91-101). */
+int mp_scale_columns(void *w, int dtype, int64_t rows, int64_t k, const void *scales, int divide, mp_stream_t stream);
+
 /* Measurement probe (no counterpart in the reference): one launch that reads `bytes` (a multiple
  * of 16, 16-byte aligned buf) with the one-row GEMVs' launch shape and no other work, so its
  * duration is the read floor the kernels' roofline fractions are read against.  sink: uint32

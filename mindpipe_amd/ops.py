@@ -623,6 +623,65 @@ def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch
     return out
 
 
+# ------------------------------------------------------------------ SmoothQuant smoothing
+_DT3 = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def colmax_abs(x: torch.Tensor, colmax: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Per-column ``max |x|`` over the rows of ``x [..., K]`` (fp16 / bf16 / fp32) into the fp32
+    vector ``colmax [K]``: a new one, or the given one updated in place with the running maximum."""
+    if x.dtype not in _DT3:
+        raise RuntimeError(f"colmax_abs takes fp16, bf16 or fp32, got {x.dtype}")
+    if not x.is_cuda:
+        raise RuntimeError("colmax_abs runs on the GPU only")
+    k = x.shape[-1]
+    x2 = x.reshape(-1, k)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    acc = colmax is not None
+    if colmax is None:
+        colmax = torch.empty(k, dtype=torch.float32, device=x.device)
+    _need(colmax, "colmax", torch.float32, 1)
+    if colmax.numel() != k:
+        raise ValueError("colmax must have one entry per column")
+    with _dev(x):
+        _lib.check(_lib.load().mp_colmax_abs(x2.data_ptr(), _DT3[x.dtype], x2.shape[0], k, int(acc),
+                                             colmax.data_ptr(), _stream()), "mp_colmax_abs")
+    return colmax
+
+
+def smooth_scales(act_max: torch.Tensor, w_colmax: torch.Tensor, alpha: float, dtype: torch.dtype) -> torch.Tensor:
+    """``(a^alpha / w^(1-alpha)).clamp(1e-5)`` in ``dtype`` from the fp32 statistics (GPU vectors)."""
+    _need(act_max, "act_max", torch.float32, 1)
+    _need(w_colmax, "w_colmax", torch.float32, 1)
+    if act_max.numel() != w_colmax.numel():
+        raise ValueError("act_max and w_colmax differ in length")
+    if dtype not in _DT3:
+        raise RuntimeError(f"smoothing scales in fp16, bf16 or fp32, got {dtype}")
+    out = torch.empty(act_max.numel(), dtype=dtype, device=act_max.device)
+    with _dev(act_max):
+        _lib.check(_lib.load().mp_smooth_scales(act_max.data_ptr(), w_colmax.data_ptr(), act_max.numel(),
+                                                float(alpha), _DT3[dtype], out.data_ptr(), _stream()),
+                   "mp_smooth_scales")
+    return out
+
+
+def scale_columns_(w: torch.Tensor, scales: torch.Tensor, divide: bool = False) -> torch.Tensor:
+    """In place ``w *= scales`` (or ``/=``) along the last dimension, rounded to ``w``'s dtype."""
+    if w.dtype not in _DT3 or scales.dtype != w.dtype:
+        raise RuntimeError("scale_columns_ needs w and scales of one dtype among fp16, bf16, fp32")
+    if not w.is_cuda or not w.is_contiguous():
+        raise RuntimeError("scale_columns_ takes a contiguous GPU tensor")
+    k = w.shape[-1]
+    sc = scales.contiguous()
+    if sc.numel() != k:
+        raise ValueError("one scale per column")
+    with _dev(w):
+        _lib.check(_lib.load().mp_scale_columns(w.data_ptr(), _DT3[w.dtype], w.numel() // k, k, sc.data_ptr(),
+                                                int(divide), _stream()), "mp_scale_columns")
+    return w
+
+
 def probe_read(buf: torch.Tensor, sink: Optional[torch.Tensor] = None) -> torch.Tensor:
     """One launch reading all of ``buf`` with the one-row GEMVs' launch shape and no other work (the
     read floor of a one-launch kernel; a measurement probe).  Returns the sink it may write."""

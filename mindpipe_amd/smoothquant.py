@@ -41,6 +41,11 @@ __all__ = [
     "SUPPORTED_MODEL_TYPES",
     "compute_smooth_scales",
     "smooth_ln_fcs_llama_like",
+    "smooth_ln_fcs_qwen3_5",
+    "smooth_qwen3_moe_ffn",
+    "smooth_qwen3_5_moe_ffn",
+    "smooth_lm",
+    "get_act_scales",
 ]
 
 
@@ -376,26 +381,189 @@ def quantize_model(model, weight_bits=8, activation_bits=8, weight_quant="per_ch
                                allow_extension_models=allow_extension_models)
 
 
+# ------------------------------------------------------------------ smoothing (smooth.py, calibration.py)
+def _colmax_of(tensors, k: int) -> torch.Tensor:
+    cm = None
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError("SmoothQuant smoothing runs on the GPU only; move the model to the GPU first")
+        cm = ops.colmax_abs(t.detach().reshape(-1, k), cm)
+    return cm
+
+
+def _scales_for(weights, act_scales: torch.Tensor, alpha: float, like: torch.Tensor) -> torch.Tensor:
+    k = act_scales.numel()
+    cm = _colmax_of(weights, k)
+    a = act_scales.detach().to(device=like.device, dtype=torch.float32).reshape(-1).contiguous()
+    return ops.smooth_scales(a, cm, alpha, like.dtype)
+
+
 @torch.no_grad()
 def compute_smooth_scales(fcs, act_scales: torch.Tensor, alpha: float = 0.5) -> torch.Tensor:
-    """``_compute_smooth_scales`` (``smooth.py:7-25``): ``(a^alpha / w^(1-alpha)).clamp(1e-5)``
-    in the weight dtype, ``w_j = max_n |W_nj|`` over every fc sharing the norm."""
+    """``_compute_smooth_scales`` (``smooth.py:7-25``) on the GPU: ``(a^alpha / w^(1-alpha)).clamp(1e-5)``
+    in the weight dtype, ``a`` the activation statistic cast to that dtype and ``w_j = max_n |W_nj|``
+    over every fc sharing the norm (clamped at 1e-5).  Same checks as the reference (``AssertionError``
+    on a non-Linear or a width mismatch)."""
     if not isinstance(fcs, (list, tuple)):
         fcs = [fcs]
-    dtype, device = fcs[0].weight.dtype, fcs[0].weight.device
-    a = act_scales.to(device=device, dtype=dtype)
-    wmax = torch.cat([fc.weight.abs().max(dim=0, keepdim=True)[0] for fc in fcs], dim=0)
-    wmax = wmax.max(dim=0)[0].clamp(min=1e-5)
-    return (a.pow(alpha) / wmax.pow(1 - alpha)).clamp(min=1e-5).to(device=device, dtype=dtype)
+    for fc in fcs:
+        assert isinstance(fc, nn.Linear)
+        assert fc.in_features == act_scales.numel()
+    return _scales_for([fc.weight for fc in fcs], act_scales, alpha, fcs[0].weight)
+
+
+def _norm_weight(ln):
+    if not hasattr(ln, "weight") or ln.weight is None:
+        raise TypeError(f"SmoothQuant requires a norm module with a learnable weight; got {type(ln)}")
+    return ln.weight
 
 
 @torch.no_grad()
 def smooth_ln_fcs_llama_like(ln, fcs, act_scales, alpha=0.5):
-    """``smooth.py:91-101``: ``ln.weight /= s``, every fc weight ``*= s`` (column-wise)."""
+    """``smooth.py:91-101``: ``ln.weight /= s`` and every fc weight ``*= s`` along its input columns,
+    each product / quotient rounded to the weight dtype (the in-place half ops of the reference)."""
+    w = _norm_weight(ln)
+    assert w.numel() == act_scales.numel()
     if not isinstance(fcs, (list, tuple)):
         fcs = [fcs]
     s = compute_smooth_scales(fcs, act_scales, alpha)
-    ln.weight.div_(s)
+    ops.scale_columns_(w.data, s.to(w.dtype), divide=True)
     for fc in fcs:
-        fc.weight.mul_(s.view(1, -1))
-    return s
+        ops.scale_columns_(fc.weight.data, s)
+
+
+def _qwen3_5_norm_update(ln, s):
+    """Qwen3.5 norms scale by ``1 + weight``: ``weight = (1 + weight) / s - 1`` in float64, cast back
+    (``smooth.py:104-117``)."""
+    w = ln.weight.data
+    ln.weight.data = ((1.0 + w.to(torch.float64)) / s.to(torch.float64) - 1.0).to(w.dtype)
+
+
+@torch.no_grad()
+def smooth_ln_fcs_qwen3_5(ln, fcs, act_scales, alpha=0.5):
+    """``smooth.py:104-117``: the Qwen3.5 ``(1 + w)`` norm update, fc weights ``*= s``."""
+    assert _norm_weight(ln).numel() == act_scales.numel()
+    s = compute_smooth_scales(fcs, act_scales, alpha)
+    _qwen3_5_norm_update(ln, s)
+    for fc in fcs:
+        ops.scale_columns_(fc.weight.data, s)
+
+
+def _experts_packed(experts) -> bool:
+    return not isinstance(experts, nn.ModuleList)
+
+
+@torch.no_grad()
+def smooth_qwen3_moe_ffn(ln, mlp, act_scales, alpha=0.5):
+    """``smooth.py:147-168``: one scale over the router and every expert's gate/up (per-expert
+    linears or the packed ``gate_up_proj [E, 2I, H]``); ``ln /= s``, all of them ``*= s``."""
+    assert _norm_weight(ln).numel() == act_scales.numel()
+    k = act_scales.numel()
+    ws = [mlp.gate.weight]
+    if _experts_packed(mlp.experts):
+        ws.append(mlp.experts.gate_up_proj)
+    else:
+        for ex in mlp.experts:
+            ws += [ex.gate_proj.weight, ex.up_proj.weight]
+    for w in ws:
+        assert w.shape[-1] == k
+    s = _scales_for(ws, act_scales, alpha, mlp.gate.weight)
+    ops.scale_columns_(ln.weight.data, s.to(ln.weight.dtype), divide=True)
+    for w in ws:
+        ops.scale_columns_(w.data, s.to(w.dtype))
+
+
+@torch.no_grad()
+def smooth_qwen3_5_moe_ffn(ln, mlp, act_scales, alpha=0.5):
+    """``smooth.py:120-144``: one scale over the shared expert's gate/up, ``shared_expert_gate``, the
+    router and the packed experts' ``gate_up_proj``; the Qwen3.5 norm update; all of them ``*= s``."""
+    assert _norm_weight(ln).numel() == act_scales.numel()
+    k = act_scales.numel()
+    ws = [mlp.shared_expert.gate_proj.weight, mlp.shared_expert.up_proj.weight, mlp.shared_expert_gate.weight,
+          mlp.gate.weight, mlp.experts.gate_up_proj]
+    for w in ws:
+        assert w.shape[-1] == k
+    s = _scales_for(ws, act_scales, alpha, mlp.shared_expert.gate_proj.weight)
+    _qwen3_5_norm_update(ln, s)
+    for w in ws:
+        ops.scale_columns_(w.data, s.to(w.dtype))
+
+
+SMOOTH_MODEL_TYPES = SUPPORTED_MODEL_TYPES
+
+
+@torch.no_grad()
+def smooth_lm(model, scales, alpha=0.5):
+    """``smooth_lm`` (``smooth.py:171-245``): per decoder layer, smooth the attention input norm into
+    q/k/v (Qwen3.5 linear-attention layers: ``in_proj_qkv/z/a/b``) and the MLP input norm into
+    gate/up (or the MoE router and experts), keyed by the qualified names of ``get_act_scales``."""
+    model_type = getattr(getattr(model, "config", None), "model_type", None)
+    if model_type not in SMOOTH_MODEL_TYPES:
+        raise NotImplementedError(f"Unsupported SmoothQuant model type: {model_type!r}")
+    root, prefix = text_backbone(model)
+    qwen35 = model_type in ("qwen3_5", "qwen3_5_moe", "qwen3_5_moe_text")
+    for li, layer in enumerate(_layers_of(root)):
+        lp = f"{prefix}.layers.{li}"
+        if qwen35:
+            if getattr(layer, "layer_type", None) == "linear_attention":
+                la = layer.linear_attn
+                fcs = [la.in_proj_qkv, la.in_proj_z, la.in_proj_a, la.in_proj_b]
+                key = lp + ".linear_attn.in_proj_qkv"
+            else:
+                fcs = [layer.self_attn.q_proj, layer.self_attn.k_proj, layer.self_attn.v_proj]
+                key = lp + ".self_attn.q_proj"
+            smooth_ln_fcs_qwen3_5(layer.input_layernorm, fcs, scales[key], alpha)
+            if model_type == "qwen3_5":
+                smooth_ln_fcs_qwen3_5(layer.post_attention_layernorm, [layer.mlp.gate_proj, layer.mlp.up_proj],
+                                      scales[lp + ".mlp.gate_proj"], alpha)
+            else:
+                smooth_qwen3_5_moe_ffn(layer.post_attention_layernorm, layer.mlp,
+                                       scales[lp + ".mlp.shared_expert.gate_proj"], alpha)
+            continue
+        qkv = [layer.self_attn.q_proj, layer.self_attn.k_proj, layer.self_attn.v_proj]
+        smooth_ln_fcs_llama_like(layer.input_layernorm, qkv, scales[lp + ".self_attn.q_proj"], alpha)
+        if model_type == "qwen3_moe" and hasattr(layer.mlp, "experts"):
+            smooth_qwen3_moe_ffn(layer.post_attention_layernorm, layer.mlp, scales[lp + ".mlp.gate"], alpha)
+        else:
+            smooth_ln_fcs_llama_like(layer.post_attention_layernorm, [layer.mlp.gate_proj, layer.mlp.up_proj],
+                                     scales[lp + ".mlp.gate_proj"], alpha)
+
+
+_MASKED_CALIBRATION = {"qwen2_5_vl", "qwen3_vl", "qwen3_moe", "qwen3_5", "qwen3_5_moe", "qwen3_5_moe_text"}
+
+
+@torch.no_grad()
+def get_act_scales(model, calibration_batches, device=None):
+    """``get_act_scales`` (``calibration.py:27-58``): the per-input-channel ``max |x|`` of every
+    ``nn.Linear``'s input over all calibration tokens, keyed by qualified name, fp32 on the host.
+
+    The statistics are kept on the GPU and updated by the column abs-max kernel after each linear's
+    forward; ``calibration_batches`` yields ``(token_ids, labels)`` pairs.  The forward passes
+    ``use_cache=False`` (and an all-ones attention mask for the model types the reference gives one).
+    ``device`` is accepted for the reference's signature: the tokens go to the embedding's device."""
+    del device
+    model.eval()
+    root, prefix = text_backbone(model)
+    emb = getattr(getattr(root, "embed_tokens", None), "weight", None)
+    in_dev = emb.device if emb is not None else next(model.parameters()).device
+    stats = {}
+
+    def hook(_m, inputs, _out, name):
+        x = inputs[0] if isinstance(inputs, tuple) else inputs
+        stats[name] = ops.colmax_abs(x.detach(), stats.get(name))
+
+    handles = []
+    for n, m in root.named_modules():
+        if isinstance(m, nn.Linear):
+            q = f"{prefix}.{n}" if n else prefix
+            handles.append(m.register_forward_hook(partial(hook, name=q)))
+    mtype = getattr(getattr(model, "config", None), "model_type", None)
+    try:
+        for ids, _labels in calibration_batches:
+            ids = ids.to(in_dev)
+            kw = {"attention_mask": torch.ones_like(ids, dtype=torch.long)} if mtype in _MASKED_CALIBRATION else {}
+            model(input_ids=ids, use_cache=False, **kw)
+    finally:
+        for h in handles:
+            h.remove()
+    return {k: v.cpu() for k, v in stats.items()}

@@ -32,8 +32,11 @@ __all__ = [
     "W4A16Linear",
     "VllmPackedInt4Linear",
     "build_compression_config",
+    "get_blocks",
+    "get_named_linears",
+    "pseudo_quantize_model_weight",
     "quantize_model_w4a16",
-    "export_vllm_w4a16",
+    "export_vllm_gptq_w4a16",
     "load_vllm_w4a16",
 ]
 
@@ -225,55 +228,207 @@ def _set_module(model: nn.Module, name: str, new: nn.Module) -> None:
     setattr(parent, child, new)
 
 
+def _is_qwen3_5(model) -> bool:
+    return str(getattr(getattr(model, "config", None), "model_type", None)) in {"qwen3_5", "qwen3_5_text"}
+
+
+def get_blocks(model: nn.Module):
+    """The decoder blocks whose linears the AWQ router rewrites (``get_blocks``,
+    ``awq/source/awq/quantize/pre_quant.py:47-76``): the language model's ``layers`` for HF decoders
+    and VL wrappers, ``decoder.layers`` (OPT), ``transformer.h`` (BLOOM / Falcon / BigCode),
+    ``transformer.blocks`` (MPT), ``gpt_neox.layers``, ``llm.model.layers`` (LLaVA-Llama)."""
+    inner = getattr(model, "model", None)
+    if inner is not None and hasattr(inner, "language_model"):
+        return inner.language_model.layers
+    lm = getattr(model, "language_model", None)
+    if lm is not None and hasattr(lm, "layers"):
+        return lm.layers
+    cls = model.__class__.__name__
+    if cls == "InternVL3":
+        return model.language_model.model.layers
+    if inner is not None and hasattr(inner, "layers"):
+        return inner.layers
+    if inner is not None and hasattr(inner, "decoder") and hasattr(inner.decoder, "layers"):
+        return inner.decoder.layers
+    low = str(model.__class__).lower()
+    tr = getattr(model, "transformer", None)
+    if tr is not None:
+        if "mpt" in low and hasattr(tr, "blocks"):
+            return tr.blocks
+        if hasattr(tr, "h"):
+            return tr.h
+    if "neox" in low:
+        return model.gpt_neox.layers
+    if cls == "LlavaLlamaModel":
+        return model.llm.model.layers
+    raise NotImplementedError(type(model))
+
+
+def get_named_linears(module: nn.Module, model: Optional[nn.Module] = None,
+                      qwen3_5_quantize_linear_attn: bool = True) -> Dict[str, nn.Linear]:
+    """Every ``nn.Linear`` of a block by qualified name (``pre_quant.py:34-44``).  In a Qwen3.5 model
+    a full-attention block keeps only its ``mlp.*`` linears, and so does a linear-attention block when
+    ``qwen3_5_quantize_linear_attn`` is off."""
+    found = {name: m for name, m in module.named_modules() if isinstance(m, nn.Linear)}
+    if model is not None and _is_qwen3_5(model):
+        kind = getattr(module, "layer_type", None)
+        if kind == "full_attention" or (kind == "linear_attention" and not qwen3_5_quantize_linear_attn):
+            found = {name: m for name, m in found.items() if name.startswith("mlp.")}
+    return found
+
+
+@torch.no_grad()
+def pseudo_quantize_model_weight(model: nn.Module, w_bit: int, q_config: dict,
+                                 qwen3_5_quantize_linear_attn: bool = True, device=None) -> None:
+    """The AWQ router (``quantizer.py:108-130``): every block linear's weight is replaced in place by
+    its pseudo-quantized value, computed by the GPU quantizer in the weight's dtype.  ``q_config``
+    holds ``zero_point`` and ``q_group_size``; ``device`` is accepted for the reference's signature
+    (each weight is quantized where it lives, staged through the GPU when it lives on the host)."""
+    del device
+    for layer in get_blocks(model):
+        for _, lin in get_named_linears(layer, model=model,
+                                        qwen3_5_quantize_linear_attn=qwen3_5_quantize_linear_attn).items():
+            lin.weight.data = pseudo_quantize_tensor(lin.weight.data, n_bit=w_bit, **q_config)
+
+
 @torch.no_grad()
 def quantize_model_w4a16(model: nn.Module, group_size: int = 128, zero_point: bool = True,
-                         skip: Iterable[str] = ("lm_head",)) -> List[str]:
-    """Swap every ``nn.Linear`` (except names containing a ``skip`` entry) for a
-    ``W4A16Linear`` holding the AWQ codes ``pseudo_quantize_model_weight`` would round to
-    (``quantizer.py:108-130``); returns the swapped names."""
+                         qwen3_5_quantize_linear_attn: bool = True) -> List[str]:
+    """Real-int4 counterpart of ``pseudo_quantize_model_weight``: the same block linears
+    (``get_blocks`` / ``get_named_linears``) become ``W4A16Linear`` modules holding the AWQ codes the
+    router would round the weights to.  Returns the qualified names of the swapped linears."""
+    blocks = get_blocks(model)
+    prefix = {id(m): n for n, m in model.named_modules()}
     names = []
-    for name, lin in _named_linears(model).items():
-        if any(s in name for s in skip):
-            continue
-        _set_module(model, name, W4A16Linear.from_float(lin, group_size, zero_point))
-        names.append(name)
+    for layer in blocks:
+        lp = prefix[id(layer)]
+        for name, lin in get_named_linears(layer, model=model,
+                                           qwen3_5_quantize_linear_attn=qwen3_5_quantize_linear_attn).items():
+            _set_module(layer, name, W4A16Linear.from_float(lin, group_size, zero_point))
+            names.append(f"{lp}.{name}" if lp else name)
     return names
 
 
+# Files a vLLM export directory takes over from the source checkpoint (tokenizer, chat template,
+# generation and processor configs, remote-code modules) and the weight files it never copies: the
+# on-disk format of ``exporters/vllm.py:18-54``.
+_INFERENCE_FILES = ("tokenizer.json", "tokenizer_config.json", "special_tokens_map.json", "added_tokens.json",
+                    "vocab.*", "merges.txt", "*.model", "spiece.model", "sentencepiece.bpe.model",
+                    "chat_template*.jinja", "generation_config*.json", "preprocessor_config.json",
+                    "processor_config.json", "image_processor_config.json", "video_processor_config.json",
+                    "feature_extractor_config.json", "configuration.json", "configuration*.py", "modeling*.py",
+                    "processing*.py", "tokenization*.py", "image_processing*.py", "video_processing*.py")
+_WEIGHT_FILES = ("*.safetensors", "*.bin", "*.pt", "*.pth", "*.ckpt", "*.gguf", "*.onnx",
+                 "model.safetensors.index.json", "pytorch_model.bin.index.json")
+
+
+def _glob_any(name: str, patterns) -> bool:
+    return any(Path(name).match(p) for p in patterns)
+
+
+def _copy_inference_files(tokenizer_bundle, out: Path) -> List[str]:
+    src = getattr(tokenizer_bundle, "source_path", None)
+    if not src or not Path(src).is_dir():
+        return []
+    copied = []
+    for f in sorted(Path(src).iterdir()):
+        if not f.is_file() or f.name == "config.json" or _glob_any(f.name, _WEIGHT_FILES):
+            continue
+        if not _glob_any(f.name, _INFERENCE_FILES):
+            continue
+        dst = out / f.name
+        if f.resolve() == dst.resolve():
+            continue
+        import shutil
+        shutil.copy2(f, dst)
+        copied.append(f.name)
+    return copied
+
+
+def _write_compression_config(out: Path, group_size: int, ignored: List[str]) -> None:
+    """``config.json`` of the export: the source ``quantization_config`` dropped, ``rope_theta`` and
+    ``rope_parameters`` made to carry each other (whichever one the model config has), and the
+    compressed-tensors ``compression_config`` added (``vllm.py:168-190``)."""
+    path = out / "config.json"
+    cfg = json.loads(path.read_text(encoding="utf-8"))
+    cfg.pop("quantization_config", None)
+    rope = cfg.get("rope_parameters")
+    if isinstance(rope, dict):
+        if rope.get("rope_theta") is not None and cfg.get("rope_theta") is None:
+            cfg["rope_theta"] = rope["rope_theta"]
+    elif cfg.get("rope_theta") is not None:
+        cfg["rope_parameters"] = {"rope_theta": cfg["rope_theta"], "rope_type": "default"}
+    cfg["compression_config"] = build_compression_config(group_size=group_size, ignored_layers=ignored)
+    path.write_text(json.dumps(cfg, ensure_ascii=False, indent=2), encoding="utf-8")
+
+
 @torch.no_grad()
-def export_vllm_w4a16(model: nn.Module, artifacts: Dict[str, RealQuantLinearArtifact], export_dir,
-                      group_size: int) -> dict:
-    """Write a compressed-tensors ``pack-quantized`` checkpoint (``exporters/vllm.py:224-327``):
-    quantized linears become ``<name>.weight_packed / weight_scale / weight_shape (+ bias)``,
-    other tensors are kept; ``config.json`` gets the ``compression_config``."""
-    from safetensors.torch import save_file
+def export_vllm_gptq_w4a16(*, model: nn.Module, tokenizer_bundle, artifacts: Dict[str, RealQuantLinearArtifact],
+                           export_dir, group_size: int) -> dict:
+    """Export GPTQ W4A16 artifacts as a vLLM compressed-tensors ``pack-quantized`` checkpoint
+    (``exporters/vllm.py:224-327``), same keyword-only signature, checks, files and summary:
+
+    * each artifact must name an ``nn.Linear`` of the model, be symmetric 4-bit with the export's
+      ``group_size``, match the weight shape, and have ``scale [N, K/g]`` with ``K % g == 0``;
+    * the linears are swapped for ``VllmPackedInt4Linear`` (codes packed by the GPU packer) for
+      ``model.save_pretrained(..., safe_serialization=True)`` and swapped back afterwards, also on
+      error; ``tokenizer_bundle.save_pretrained`` writes the tokenizer, the source checkpoint's
+      inference files are copied, and ``config.json`` gets the ``compression_config``;
+    * unquantized linears are listed in ``ignore``.
+    """
+    if not artifacts:
+        raise ValueError("No real-quant Linear artifacts were provided for vLLM export.")
     out = Path(export_dir)
     out.mkdir(parents=True, exist_ok=True)
-    tensors = {}
-    lin = _named_linears(model)
-    for k_, v in model.state_dict().items():
-        mod_name = k_.rsplit(".", 1)[0]
-        if mod_name in artifacts:
-            continue
-        tensors[k_] = v.detach().cpu().contiguous()
-    for name, art in artifacts.items():
-        if art.int_weight.shape[1] % art.group_size:
-            raise ValueError(f"{name}: in_features must be a multiple of group_size")
-        tensors[f"{name}.weight_packed"] = pack_int4_for_vllm(art.int_weight).cpu()
-        tensors[f"{name}.weight_scale"] = art.scale.detach().cpu().to(torch.float16).contiguous()
-        tensors[f"{name}.weight_shape"] = torch.tensor(list(art.original_shape), dtype=torch.int64)
-        b = getattr(lin.get(name), "bias", None)
-        if b is not None:
-            tensors[f"{name}.bias"] = b.detach().cpu().contiguous()
-    save_file(tensors, str(out / "model.safetensors"))
-    ignored = sorted(n for n in lin if n not in artifacts)
-    cfg_path = out / "config.json"
-    cfg = json.loads(cfg_path.read_text()) if cfg_path.exists() else {}
-    cfg.pop("quantization_config", None)
-    cfg["compression_config"] = build_compression_config(group_size=group_size, ignored_layers=ignored)
-    cfg_path.write_text(json.dumps(cfg, indent=2))
-    return {"backend": "vllm", "quantized_linear_count": len(artifacts), "ignored_layers": ignored,
-            "export_dir": str(out)}
+    modules = dict(model.named_modules())
+    ignored = sorted(n for n, m in modules.items() if isinstance(m, nn.Linear) and n not in artifacts)
+    g = int(group_size)
+    swapped = []
+    copied: List[str] = []
+    try:
+        for name, art in artifacts.items():
+            mod = modules.get(name)
+            if mod is None:
+                raise KeyError(f"Cannot find quantized module {name!r} in model.")
+            if not isinstance(mod, nn.Linear):
+                raise TypeError(f"Module {name!r} is {type(mod)!r}, expected nn.Linear.")
+            if art.bits != 4 or not art.symmetric:
+                raise ValueError(f"Only symmetric W4 artifacts are supported, got {art!r}.")
+            if int(art.group_size) != g:
+                raise ValueError(f"Artifact {name!r} group_size={art.group_size}, expected {g}.")
+            shape = tuple(mod.weight.shape)
+            if tuple(art.original_shape) != shape:
+                raise ValueError(f"Artifact {name!r} original_shape={art.original_shape}, "
+                                 f"but module weight shape is {shape}.")
+            if tuple(art.int_weight.shape) != shape:
+                raise ValueError(f"Artifact {name!r} int_weight shape={tuple(art.int_weight.shape)}, expected {shape}.")
+            if mod.in_features % g:
+                raise ValueError("vLLM compressed-tensors W4A16 requires in_features divisible by group_size; "
+                                 f"{name!r} has in_features={mod.in_features}, group_size={g}.")
+            if tuple(art.scale.shape) != (mod.out_features, mod.in_features // g):
+                raise ValueError(f"Artifact {name!r} scale shape={tuple(art.scale.shape)}, "
+                                 f"expected {(mod.out_features, mod.in_features // g)}.")
+            packed = pack_int4_for_vllm(art.int_weight).cpu()
+            bias = mod.bias.data.detach().cpu() if mod.bias is not None else None
+            new = VllmPackedInt4Linear(packed_weight=packed, scale=art.scale.detach().cpu(), bias=bias,
+                                       in_features=mod.in_features, out_features=mod.out_features)
+            parent_name, _, child = name.rpartition(".")
+            parent = model.get_submodule(parent_name) if parent_name else model
+            swapped.append((parent, child, mod))
+            _set_module(model, name, new)
+        model.save_pretrained(out, safe_serialization=True)
+        tokenizer_bundle.save_pretrained(str(out))
+        copied = _copy_inference_files(tokenizer_bundle, out)
+        _write_compression_config(out, g, ignored)
+    finally:
+        for parent, child, orig in reversed(swapped):
+            if child in parent._modules:
+                parent._modules[child] = orig
+            else:
+                setattr(parent, child, orig)
+    return {"backend": "vllm", "format": "compressed-tensors", "precision": "W4A16", "path": str(out),
+            "quantized_linear_count": len(artifacts), "ignored_linear_count": len(ignored),
+            "ignored_layers": ignored, "copied_inference_files": copied}
 
 
 @torch.no_grad()

@@ -473,9 +473,14 @@ def compute_smooth_scales(act_max, weights, alpha=0.5, dtype="fp16"):
         weights = [weights]
     wmax = np.max(np.stack([np.abs(_in_f32(np.asarray(w), dtype)).max(axis=0) for w in weights]), axis=0)
     wmax = np.where(wmax < np.float32(1e-5), R(np.float32(1e-5)), wmax)
+    # the fp32 powers taken correctly rounded (float64 power, rounded to float32): torch's x.pow(0.5) is
+    # a square root, which is; other exponents go through the platform's powf, faithful to an ulp but
+    # not correctly rounded (numpy's float32 power differs from the correctly rounded value in about
+    # 20% of entries here), so the correctly rounded value is the one definition every platform nears
+    e1, e2 = np.float64(np.float32(alpha)), np.float64(np.float32(1 - alpha))
     with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
-        num = R(np.power(a, np.float32(alpha)))
-        den = R(np.power(wmax, np.float32(1 - alpha)))
+        num = R(np.power(a.astype(np.float64), e1).astype(np.float32))
+        den = R(np.power(wmax.astype(np.float64), e2).astype(np.float32))
         sc = R(num / den)
     sc = np.where(sc < np.float32(1e-5), R(np.float32(1e-5)), sc)
     return _bits_out(sc, dtype)

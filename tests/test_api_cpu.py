@@ -58,13 +58,34 @@ def test_w4_module_buffers_and_shapes():
         W4.pseudo_quantize_tensor(torch.zeros(4, 128, dtype=torch.float16), n_bit=8)
 
 
-def test_smooth_scales_closed_form_cpu():
-    fc = nn.Linear(3, 2, bias=False)
-    with torch.no_grad():
-        fc.weight.copy_(torch.tensor([[1.0, -0.25, 0.0], [0.5, 0.0625, 0.0]]))
-    fc = fc.half()
-    s = SQ.compute_smooth_scales(fc, torch.tensor([4.0, 9.0, 0.0]), 0.5)
-    assert s.dtype == torch.float16 and s.tolist()[:2] == [2.0, 6.0]
-    ln = nn.LayerNorm(3).half()
-    SQ.smooth_ln_fcs_llama_like(ln, [fc], torch.tensor([4.0, 9.0, 0.0]), 0.5)
-    assert fc.weight[0, 0].item() == 2.0
+def test_smoothing_refuses_cpu_weights():
+    """Smoothing runs on the GPU kernels only: CPU weights raise instead of falling back."""
+    fc = nn.Linear(3, 2, bias=False).half()
+    with pytest.raises(RuntimeError):
+        SQ.compute_smooth_scales(fc, torch.tensor([4.0, 9.0, 0.0]), 0.5)
+    with pytest.raises(AssertionError):  # the reference's width check comes first
+        SQ.compute_smooth_scales(fc, torch.tensor([4.0, 9.0]), 0.5)
+
+def test_method_adapters_validate_like_the_reference():
+    """apply_fake_quantization's argument checks (smoothquant/method.py:85-108): unsupported model type,
+    non-W8A8 bits, quantized Q/K/V caches, missing calibration data; AWQ's search is refused."""
+    from types import SimpleNamespace
+    from mindpipe_amd.methods import AWQMethod, BaseQuantizationMethod, METHODS, SmoothQuantMethod
+    assert issubclass(SmoothQuantMethod, BaseQuantizationMethod) and set(METHODS) == {"smoothquant", "awq"}
+
+    class M(nn.Module):
+        def __init__(self, t):
+            super().__init__()
+            self.config = SimpleNamespace(model_type=t)
+
+    ok = dict(weight_bits=8, activation_bits=8, query_bits=16, key_bits=16, value_bits=16, smoothquant_alpha=0.85)
+    with pytest.raises(NotImplementedError):
+        SmoothQuantMethod().apply_fake_quantization(M("gpt2"), None, SimpleNamespace(**ok))
+    with pytest.raises(ValueError):
+        SmoothQuantMethod().apply_fake_quantization(M("llama"), None, SimpleNamespace(**{**ok, "weight_bits": 4}))
+    with pytest.raises(ValueError):
+        SmoothQuantMethod().apply_fake_quantization(M("llama"), None, SimpleNamespace(**{**ok, "key_bits": 8}))
+    with pytest.raises(ValueError):  # no calibration_batches / act scales
+        SmoothQuantMethod().apply_fake_quantization(M("llama"), None, SimpleNamespace(**ok))
+    with pytest.raises(NotImplementedError):
+        AWQMethod().apply_fake_quantization(M("llama"), None, SimpleNamespace(awq_search=True))

@@ -300,25 +300,112 @@ def test_w4_module_paths():
         assert np.array_equal(mod.dequantized_weight().cpu().numpy().view(np.uint16), rdeq.view(np.uint16)) or not zp
 
 
+class _Bundle:
+    """Tokenizer bundle of the export contract: ``save_pretrained`` and an optional ``source_path``."""
+
+    def __init__(self, source_path=None):
+        self.source_path = source_path
+
+    def save_pretrained(self, output_dir):
+        Path(output_dir, "tokenizer_config.json").write_text("{}", encoding="utf-8")
+
+
+class _TinyExport(nn.Module):
+    """A model with the ``save_pretrained(dir, safe_serialization=True)`` contract of HF models."""
+
+    def __init__(self, k=256, n=64, config=None):
+        super().__init__()
+        self.proj = nn.Linear(k, n, bias=True)
+        self.ignored = nn.Linear(k, n, bias=False)
+        self.config_dict = config or {"model_type": "tiny"}
+
+    def save_pretrained(self, output_dir, *, safe_serialization):
+        from safetensors.torch import save_file
+        assert safe_serialization is True
+        out = Path(output_dir)
+        out.mkdir(parents=True, exist_ok=True)
+        save_file({k: v.detach().cpu().contiguous() for k, v in self.state_dict().items()}, str(out / "model.safetensors"))
+        (out / "config.json").write_text(json.dumps(self.config_dict), encoding="utf-8")
+
+
+def test_export_vllm_gptq_w4a16_reference_kat(tmp_path):
+    """The reference's export case (tests/test_vllm_real_quant_export.py:105-152): K = 8, g = 4, the
+    signed codes packed to [[1609139984], [-1340634641]], scale (2, 2), ignore == ["ignored"], the
+    model's own module restored afterwards, and the rope_theta -> rope_parameters fix-up."""
+    _say("export kat")
+    from safetensors import safe_open
+    from mindpipe_amd.w4a16 import RealQuantLinearArtifact, export_vllm_gptq_w4a16, unpack_int4
+    model = _TinyExport(8, 2, {"model_type": "tiny", "rope_theta": 10000.0})
+    orig = model.proj
+    iw = torch.tensor([[-8, -7, -1, 0, 1, 6, 7, -3], [7, 6, 1, 0, -1, -7, -8, 3]], dtype=torch.int8)
+    art = RealQuantLinearArtifact(name="proj", bits=4, group_size=4, symmetric=True, original_shape=(2, 8),
+                                  int_weight=iw, scale=torch.tensor([[0.1, 0.2], [0.3, 0.4]], dtype=torch.float16))
+    summary = export_vllm_gptq_w4a16(model=model, tokenizer_bundle=_Bundle(), artifacts={"proj": art},
+                                     export_dir=tmp_path, group_size=4)
+    assert model.proj is orig
+    assert summary["backend"] == "vllm" and summary["format"] == "compressed-tensors"
+    assert summary["quantized_linear_count"] == 1 and summary["ignored_layers"] == ["ignored"]
+    with safe_open(str(tmp_path / "model.safetensors"), framework="pt", device="cpu") as f:
+        assert f.get_tensor("proj.weight_packed").tolist() == [[1609139984], [-1340634641]]
+        assert torch.equal(unpack_int4(f.get_tensor("proj.weight_packed"), 8), iw)
+        assert tuple(f.get_tensor("proj.weight_scale").shape) == (2, 2)
+        assert f.get_tensor("proj.weight_shape").tolist() == [2, 8]
+    cfg = json.loads((tmp_path / "config.json").read_text())
+    assert cfg["compression_config"]["format"] == "pack-quantized"
+    assert cfg["compression_config"]["config_groups"]["group_0"]["weights"]["group_size"] == 4
+    assert cfg["compression_config"]["ignore"] == ["ignored"]
+    assert cfg["rope_parameters"] == {"rope_theta": 10000.0, "rope_type": "default"}
+    assert (tmp_path / "tokenizer_config.json").exists()
+
+
+def test_export_vllm_gptq_w4a16_checks_and_inference_files(tmp_path):
+    """Argument checks of the export (each raises before anything is written or swapped) and the copy
+    of the source checkpoint's inference files (weights and config.json never copied)."""
+    _say("export checks")
+    from mindpipe_amd.w4a16 import RealQuantLinearArtifact, export_vllm_gptq_w4a16
+    iw = torch.zeros(2, 8, dtype=torch.int8)
+    sc = torch.ones(2, 2, dtype=torch.float16)
+    good = dict(name="proj", bits=4, group_size=4, symmetric=True, original_shape=(2, 8), int_weight=iw, scale=sc)
+    model = _TinyExport(8, 2)
+    orig = model.proj
+    cases = [({}, ValueError), ({"missing": RealQuantLinearArtifact(**good)}, KeyError),
+             ({"proj": RealQuantLinearArtifact(**{**good, "symmetric": False})}, ValueError),
+             ({"proj": RealQuantLinearArtifact(**{**good, "group_size": 2})}, ValueError),
+             ({"proj": RealQuantLinearArtifact(**{**good, "original_shape": (2, 16)})}, ValueError),
+             ({"proj": RealQuantLinearArtifact(**{**good, "scale": torch.ones(2, 3, dtype=torch.float16)})}, ValueError)]
+    for arts, exc in cases:
+        with pytest.raises(exc):
+            export_vllm_gptq_w4a16(model=model, tokenizer_bundle=_Bundle(), artifacts=arts, export_dir=tmp_path / "x",
+                                   group_size=4)
+        assert model.proj is orig
+    src = tmp_path / "src"
+    src.mkdir()
+    for name in ("tokenizer.json", "generation_config.json", "chat_template.jinja", "model.safetensors",
+                 "config.json", "notes.txt", "modeling_tiny.py"):
+        (src / name).write_text("{}")
+    out = tmp_path / "out"
+    summary = export_vllm_gptq_w4a16(model=_TinyExport(8, 2, {"model_type": "tiny",
+                                                             "rope_parameters": {"rope_theta": 5e5, "rope_type": "llama3"}}),
+                                     tokenizer_bundle=_Bundle(str(src)), artifacts={"proj": RealQuantLinearArtifact(**good)},
+                                     export_dir=out, group_size=4)
+    assert summary["copied_inference_files"] == ["chat_template.jinja", "generation_config.json", "modeling_tiny.py",
+                                                 "tokenizer.json"]
+    cfg = json.loads((out / "config.json").read_text())
+    assert cfg["rope_theta"] == 5e5 and cfg["rope_parameters"]["rope_type"] == "llama3"
+
+
 def test_export_then_load_round_trip(tmp_path):
     _say("export/load")
-    from mindpipe_amd.w4a16 import VllmPackedInt4Linear, export_vllm_w4a16, gptq_rtn_quantize, load_vllm_w4a16
-
-    class Tiny(nn.Module):
-        def __init__(self):
-            super().__init__()
-            self.proj = nn.Linear(256, 64, bias=True)
-            self.ignored = nn.Linear(256, 64, bias=False)
-
+    from mindpipe_amd.w4a16 import VllmPackedInt4Linear, export_vllm_gptq_w4a16, gptq_rtn_quantize, load_vllm_w4a16
     torch.manual_seed(0)
-    m = Tiny().half().to(DEV)
+    m = _TinyExport().half().to(DEV)
     art = gptq_rtn_quantize("proj", m.proj.weight.float(), 4, 128)
-    (tmp_path / "config.json").write_text(json.dumps({"model_type": "tiny"}))
-    summary = export_vllm_w4a16(m, {"proj": art}, tmp_path, 128)
+    summary = export_vllm_gptq_w4a16(model=m, tokenizer_bundle=_Bundle(), artifacts={"proj": art}, export_dir=tmp_path,
+                                     group_size=128)
     assert summary["ignored_layers"] == ["ignored"] and summary["quantized_linear_count"] == 1
     cfg = json.loads((tmp_path / "config.json").read_text())["compression_config"]
     assert cfg["format"] == "pack-quantized" and cfg["config_groups"]["group_0"]["weights"]["group_size"] == 128
-    m2 = Tiny().half().to(DEV)
+    m2 = _TinyExport().half().to(DEV)
     names = load_vllm_w4a16(m2, tmp_path)
     assert names == ["proj"] and isinstance(m2.proj, VllmPackedInt4Linear)
     assert torch.equal(m2.ignored.weight, m.ignored.weight)
@@ -327,6 +414,54 @@ def test_export_then_load_round_trip(tmp_path):
     deq = (iw * np.repeat(art.scale.float().cpu().numpy(), 128, 1)).astype(np.float16)
     ref = O.w4a16_linear(x.cpu().numpy(), deq, m.proj.bias.detach().cpu().numpy())
     assert _rel(m2.proj(x).float().cpu().numpy(), ref.astype(np.float32)) <= 1e-3
+
+
+def _tiny_llama(seed=0, dtype=torch.float16):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    torch.manual_seed(seed)
+    cfg = LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+                      num_key_value_heads=2, vocab_size=512)
+    return LlamaForCausalLM(cfg).to(dtype).to(DEV).eval()
+
+
+@pytest.mark.parametrize("zero_point", [True, False])
+def test_pseudo_quantize_model_weight_router(zero_point):
+    """The AWQ router rewrites exactly the block linears (q/k/v/o/gate/up/down of every layer, not the
+    embeddings or lm_head), each bit-identical to the oracle's pseudo_quantize_tensor of its weight."""
+    _say("pseudo_quantize_model_weight", zero_point)
+    from mindpipe_amd.w4a16 import get_blocks, pseudo_quantize_model_weight
+    model = _tiny_llama()
+    before = {n: p.detach().clone() for n, p in model.named_parameters()}
+    pseudo_quantize_model_weight(model, w_bit=4, q_config={"zero_point": zero_point, "q_group_size": 128})
+    assert len(get_blocks(model)) == 2
+    changed = sorted(n for n, p in model.named_parameters() if not torch.equal(p, before[n]))
+    exp = sorted(f"model.layers.{i}.{p}.weight" for i in range(2)
+                 for p in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                           "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"))
+    assert changed == exp
+    for n in exp:
+        ref = O.pseudo_quantize_tensor(before[n].cpu().numpy(), 4, zero_point, 128)[0]
+        got = dict(model.named_parameters())[n].detach().cpu().numpy()
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)), n
+
+
+def test_quantize_model_w4a16_swaps_block_linears():
+    """Real-int4 swap of the router's linears: the same names, W4A16Linear modules, and logits within
+    1e-3 of the pseudo-quantized model's (the same codes; fp32 accumulation in both)."""
+    _say("quantize_model_w4a16")
+    from mindpipe_amd.w4a16 import W4A16Linear, pseudo_quantize_model_weight, quantize_model_w4a16
+    ids = torch.randint(0, 512, (2, 16), device=DEV, generator=torch.Generator(device=DEV).manual_seed(1))
+    ref_model = _tiny_llama()
+    pseudo_quantize_model_weight(ref_model, 4, {"zero_point": True, "q_group_size": 128})
+    model = _tiny_llama()
+    names = quantize_model_w4a16(model, 128, True)
+    assert len(names) == 14 and names[0] == "model.layers.0.self_attn.q_proj"
+    assert all(isinstance(model.get_submodule(n), W4A16Linear) for n in names)
+    assert isinstance(model.lm_head, nn.Linear)
+    with torch.no_grad():
+        a = model(ids).logits.float()
+        b = ref_model(ids).logits.float()
+    assert _rel(a.cpu().numpy(), b.cpu().numpy()) <= 1e-3
 
 
 # ------------------------------------------------------------------ add-RMSNorm fusion, dense MLP chain
@@ -389,3 +524,50 @@ def test_dense_mlp_w8a8_matches_oracle(chunks, tuple_in):
     assert err <= 1e-3, err   # bar: rel. Frobenius error <= 1e-3
     # bit-identical except where silu's exp puts a requant code on a rounding boundary
     assert np.mean(yn.view(np.uint16) == ref.view(np.uint16)) >= 0.99
+
+
+# ------------------------------------------------------------------ method adapters (base.py:20-21)
+def test_smoothquant_method_adapter_on_tiny_llama(tmp_path):
+    """apply_fake_quantization: statistics from calibration batches, smoothing, int8 swap; the
+    artifact dict of the reference; logits close to the fp16 model's; statistics saved and reused."""
+    _say("SmoothQuantMethod")
+    from types import SimpleNamespace
+    from mindpipe_amd.methods import SmoothQuantMethod
+    from mindpipe_amd.smoothquant import SmoothQuantLinear
+    model = _tiny_llama()
+    g = torch.Generator().manual_seed(5)
+    batches = [(torch.randint(0, 512, (2, 32), generator=g), None) for _ in range(2)]
+    ids = batches[0][0].to(DEV)
+    with torch.no_grad():
+        ref = model(ids).logits.float()
+    args = SimpleNamespace(weight_bits=8, activation_bits=8, query_bits=16, key_bits=16, value_bits=16,
+                           smoothquant_alpha=0.85, calibration_batches=batches, smoothquant_save_act_scales=True,
+                           model_path=str(tmp_path / "tiny"), output_root=str(tmp_path / "runs"), sequence_length=32)
+    art = SmoothQuantMethod().apply_fake_quantization(model, None, args)
+    assert art["quantized_linear_count"] == 14 and art["smoothquant_config"]["alpha"] == 0.85
+    assert art["smoothquant_config"]["model_type"] == "llama" and Path(art["act_scales_path"]).exists()
+    assert isinstance(model.model.layers[1].mlp.down_proj, SmoothQuantLinear)
+    with torch.no_grad():
+        out = model(ids).logits.float()
+    cos = torch.nn.functional.cosine_similarity(out.flatten(), ref.flatten(), dim=0).item()
+    assert cos > 0.99, cos
+    # reuse of the saved statistics on a fresh model gives the same quantized weights
+    model2 = _tiny_llama()
+    args2 = SimpleNamespace(**{**vars(args), "calibration_batches": None,
+                               "smoothquant_act_scales_from": art["act_scales_path"]})
+    SmoothQuantMethod().apply_fake_quantization(model2, None, args2)
+    assert torch.equal(model2.model.layers[0].self_attn.q_proj.weight, model.model.layers[0].self_attn.q_proj.weight)
+
+
+def test_awq_method_adapter_equals_router():
+    _say("AWQMethod")
+    from types import SimpleNamespace
+    from mindpipe_amd.methods import AWQMethod
+    from mindpipe_amd.w4a16 import pseudo_quantize_model_weight
+    a, b = _tiny_llama(), _tiny_llama()
+    args = SimpleNamespace(weight_bits=4, activation_bits=16, weight_symmetric=False, weight_group_size=128)
+    art = AWQMethod().apply_fake_quantization(a, None, args)
+    assert art["quantization_config"] == {"zero_point": True, "q_group_size": 128}
+    pseudo_quantize_model_weight(b, 4, {"zero_point": True, "q_group_size": 128})
+    for (n, p), (_, q) in zip(a.named_parameters(), b.named_parameters()):
+        assert torch.equal(p, q), n
