@@ -11,7 +11,7 @@ capture see shapes without running kernels (the pattern of the reference's
 """
 from __future__ import annotations
 
-from typing import Optional, Tuple
+from typing import List, Optional, Tuple
 
 import torch
 
@@ -216,6 +216,50 @@ def add_rms_norm_quant(x: torch.Tensor, residual: Optional[torch.Tensor], weight
             x2.data_ptr(), _ptr(residual), weight.data_ptr(), float(eps), m, h, _DT[x.dtype], _ptr(rsum),
             _ptr(y), _ptr(q), _ptr(s), _stream()), "mp_add_rms_norm_quant")
     return y, q, s, rsum
+
+
+# Functional custom ops over the fused norm (fixed output schemas, fake implementations), the form
+# torch.compile and graph capture take: the registration pattern of the reference's
+# torch.ops.vllm.* ops (vllm.patch:171-228,291-306).
+@torch.library.custom_op("mindpipe_amd::add_rms_norm_dynamic_quant", mutates_args=())
+def add_rms_norm_dynamic_quant(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                               eps: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``(int8 codes, fp32 per-token scale, x + residual)`` of RMSNorm(x + residual) * weight
+    (``npu_add_rms_norm_dynamic_quant``, ``vllm_ascend.patch:740-792``)."""
+    _, q, sc, rsum = add_rms_norm_quant(x, residual, weight, eps, quant=True, out=False)
+    return q, sc, rsum
+
+
+@add_rms_norm_dynamic_quant.register_fake
+def _(x, residual, weight, eps):
+    return (torch.empty(x.shape, dtype=torch.int8, device=x.device),
+            torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device), torch.empty_like(x))
+
+
+@torch.library.custom_op("mindpipe_amd::rms_norm_dynamic_quant", mutates_args=())
+def rms_norm_dynamic_quant(x: torch.Tensor, weight: torch.Tensor, eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``(int8 codes, fp32 per-token scale)`` of RMSNorm(x) * weight (the first layer, no residual)."""
+    _, q, sc, _ = add_rms_norm_quant(x, None, weight, eps, quant=True, out=False)
+    return q, sc
+
+
+@rms_norm_dynamic_quant.register_fake
+def _(x, weight, eps):
+    return (torch.empty(x.shape, dtype=torch.int8, device=x.device),
+            torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device))
+
+
+@torch.library.custom_op("mindpipe_amd::add_rms_norm", mutates_args=())
+def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                 eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``(RMSNorm(x + residual) * weight, x + residual)`` in x's dtype (``npu_add_rms_norm``)."""
+    y, _, _, rsum = add_rms_norm_quant(x, residual, weight, eps, quant=False)
+    return y, rsum
+
+
+@add_rms_norm.register_fake
+def _(x, residual, weight, eps):
+    return torch.empty_like(x), torch.empty_like(x)
 
 
 def w8_quantize_per_channel(w: torch.Tensor, rule: str = "export"):
@@ -467,6 +511,33 @@ def _(x, topk_ids, topk_w, w13, s13, w2, s2, out_dtype=None, rule="runtime", x_s
     if out_dtype is None:
         out_dtype = x.dtype if x_scale is None else torch.float16
     return x.new_empty((x.shape[0], w2.shape[1]), dtype=out_dtype)
+
+
+@torch.library.custom_op("mindpipe_amd::dense_mlp_w8a8", mutates_args=())
+def dense_mlp_w8a8(qx: torch.Tensor, sx: torch.Tensor, offsets: torch.Tensor, w13_chunks: List[torch.Tensor],
+                   s13_chunks: List[torch.Tensor], w2_chunks: torch.Tensor, s2: torch.Tensor, chunk_size: int,
+                   out_dtype: torch.dtype) -> torch.Tensor:
+    """The chunked W8A8 MLP chain (``vllm.patch:883-937``; one chunk ``:1003-1037``): per chunk, GEMM1
+    + SwiGLU + requant over one group of all T tokens (``offsets = [0, T]``), then the int8 down GEMM
+    on the chunk's columns; one chunk writes ``out_dtype`` directly, several are summed in fp32 and
+    rounded once.  ``w13_chunks[c] [1, 2cs, H]`` / ``s13_chunks[c] [1, 2cs]`` fp32, ``w2_chunks
+    [chunks, H, cs]``, ``s2 [H]`` fp32."""
+    chunks = len(w13_chunks)
+    if chunks == 0 or len(s13_chunks) != chunks or w2_chunks.shape[0] != chunks:
+        raise ValueError("dense_mlp_w8a8: chunk lists disagree")
+    out = None
+    for c in range(chunks):
+        qh, sh = moe_gmm1_swiglu_quant(qx, sx, w13_chunks[c], s13_chunks[c], offsets, chunk_size)
+        if chunks == 1:
+            return w8a8_gemm(qh, sh, w2_chunks[0], s2, None, out_dtype)
+        y = w8a8_gemm(qh, sh, w2_chunks[c], s2, None, torch.float32)
+        out = y if out is None else out + y
+    return out.to(out_dtype)
+
+
+@dense_mlp_w8a8.register_fake
+def _(qx, sx, offsets, w13_chunks, s13_chunks, w2_chunks, s2, chunk_size, out_dtype):
+    return torch.empty((qx.shape[0], w2_chunks.shape[1]), dtype=out_dtype, device=qx.device)
 
 
 def group_offsets_from_list(group_list: torch.Tensor, group_list_type: int) -> torch.Tensor:

@@ -210,11 +210,18 @@ def add_rms_norm_forward(norm, x: torch.Tensor, residual: Optional[torch.Tensor]
     """
     eps = float(getattr(norm, "variance_epsilon", getattr(norm, "eps", 1e-6)))
     weight = norm.weight
+    mp = torch.ops.mindpipe_amd
     if layer is not None and _should_use_w8a8_dynamic_fusion(layer, x):
-        _, q, s, rsum = ops.add_rms_norm_quant(x, residual, weight, eps, quant=True, out=False)
-        return (q, s), (rsum if residual is not None else x)
-    y, _, _, rsum = ops.add_rms_norm_quant(x, residual, weight, eps, quant=False)
-    return y, (rsum if residual is not None else x)
+        if residual is None:
+            q, s = mp.rms_norm_dynamic_quant(x, weight, eps)
+            return (q, s), x
+        q, s, rsum = mp.add_rms_norm_dynamic_quant(x, residual, weight, eps)
+        return (q, s), rsum
+    if residual is None:
+        y, _, _, _ = ops.add_rms_norm_quant(x, None, weight, eps, quant=False)
+        return y, x
+    y, rsum = mp.add_rms_norm(x, residual, weight, eps)
+    return y, rsum
 
 
 # ---------------------------------------------------------------- dense MLP chain
@@ -293,17 +300,8 @@ def dense_mlp_w8a8(gate_up, down, x: Union[torch.Tensor, Tuple[torch.Tensor, tor
         lead = x.shape[:-1]
         qx, sx = dynamic_quant(x.reshape(-1, x.shape[-1]))
     offsets = _group_offsets(qx.shape[0], qx.device)
-    w2 = down._mindpipe_chunked_down_weight
-    s2 = down._mindpipe_chunked_down_scale_fp32
-    out = None
-    for idx in range(chunks):
-        qh, sh = ops.moe_gmm1_swiglu_quant(qx, sx, getattr(gate_up, f"_mindpipe_chunked_gate_up_weight_{idx}"),
-                                           getattr(gate_up, f"_mindpipe_chunked_gate_up_scale_{idx}"), offsets, cs)
-        if chunks == 1:
-            out = ops.w8a8_gemm(qh, sh, w2[0], s2, None, out_dtype)
-            break
-        y = ops.w8a8_gemm(qh, sh, w2[idx], s2, None, torch.float32)
-        out = y if out is None else out + y
-    if chunks > 1:
-        out = out.to(out_dtype)
+    w13 = [getattr(gate_up, f"_mindpipe_chunked_gate_up_weight_{i}") for i in range(chunks)]
+    s13 = [getattr(gate_up, f"_mindpipe_chunked_gate_up_scale_{i}") for i in range(chunks)]
+    out = torch.ops.mindpipe_amd.dense_mlp_w8a8(qx, sx, offsets, w13, s13, down._mindpipe_chunked_down_weight,
+                                                down._mindpipe_chunked_down_scale_fp32, cs, out_dtype)
     return out.reshape(*lead, out.shape[-1])
