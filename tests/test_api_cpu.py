@@ -89,3 +89,15 @@ def test_method_adapters_validate_like_the_reference():
         SmoothQuantMethod().apply_fake_quantization(M("llama"), None, SimpleNamespace(**ok))
     with pytest.raises(NotImplementedError):
         AWQMethod().apply_fake_quantization(M("llama"), None, SimpleNamespace(awq_search=True))
+
+
+@pytest.mark.parametrize("model_type", ["qwen2_vl", "qwen3", "qwen3_moe"])
+def test_ascend_export_rejects_non_dense_qwen2(tmp_path, model_type):
+    """read_config of the W8A8_DYNAMIC export (export_fp16_to_ascend_w8a8_dynamic_probe.py:75-101):
+    only dense Qwen2 / Qwen2.5 checkpoints."""
+    import json
+    from mindpipe_amd.ascend_w8a8 import read_config
+    (tmp_path / "config.json").write_text(json.dumps({"architectures": ["Qwen2ForCausalLM"], "model_type": model_type,
+                                                      "num_hidden_layers": 1}))
+    with pytest.raises(ValueError, match="Expected dense Qwen2/Qwen2.5"):
+        read_config(tmp_path)
