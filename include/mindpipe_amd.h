@@ -180,6 +180,22 @@ int mp_w8a8_gemm_fake(const int8_t *qx, const float *s_tok, const int8_t *w, con
                       const void *bias, int act_dtype, void *y, int64_t m, int64_t n, int64_t k,
                       mp_stream_t stream);
 
+/* Output-quant W8A8 linear: y[M,N] = mp_w8a8_gemm's output (out_dtype fp16 / bf16, bias in
+ * bias_dtype or NULL) together with its per-token int8 codes q_out[M,N] and scale s_out[M]:
+ * the q/k/v output quant of SmoothQuantLinear(quantize_output=True) (fake_quant.py:77-82),
+ * returned as (int8, scale) in the return_scale form (vllm_ascend.patch:4019-4020).
+ * scale_rule MP_SCALE_FP32: s = max|y|/127 in fp32, q = rint(y / s) (quantize_per_token_i8's
+ * runtime rule on y); MP_SCALE_FAKE: quantize_activation_per_token_absmax in out_dtype.  The
+ * GEMM epilogue rounds y and writes each row's partial abs-max per 64 columns; a second launch
+ * reduces them and writes the codes.  K % 128 == 0, K <= 2^17, M <= 262144, N <= 2^20;
+ * qx, w 16-byte aligned; workspace of mp_w8a8_gemm_quant_out_workspace_bytes(M, N), 16-byte
+ * aligned.  Calls that share a workspace must not overlap. */
+size_t mp_w8a8_gemm_quant_out_workspace_bytes(int64_t m, int64_t n);
+int mp_w8a8_gemm_quant_out(const int8_t *qx, const float *s_tok, const int8_t *w, const float *s_ch,
+                           const void *bias, int bias_dtype, int64_t m, int64_t n, int64_t k, int out_dtype,
+                           int scale_rule, void *y, int8_t *q_out, float *s_out, void *workspace,
+                           size_t workspace_bytes, mp_stream_t stream);
+
 /* ---------------------------------------------------------------- W8A8 MoE */
 
 /* Routing + per-token quant (replaces npu_moe_init_routing_quant,

@@ -5,7 +5,9 @@
 enum mp_i8_epilogue {
   MP_EPI_DENSE = 0,  // y = ((acc * s_tok) * s_ch) (+ bias) -> out dtype
   MP_EPI_F32 = 1,    // y = (acc * s_tok) * s_ch -> fp32 (grouped GEMM2)
-  MP_EPI_SWIGLU = 2  // h = silu(g) * u -> fp32 workspace + per-row partial absmax
+  MP_EPI_SWIGLU = 2, // h = silu(g) * u -> fp32 workspace + per-row partial absmax
+  MP_EPI_AMAX = 3    // y = ((acc * s_tok) * s_ch) (+ bias) -> 16-bit out dtype + per-row partial absmax
+                     // of the rounded outputs (the output-quant GEMM; i8_moe_kernel only)
 };
 
 struct mp_i8_args {
@@ -27,6 +29,8 @@ struct mp_i8_args {
   int64_t ldy;               // output row stride (elements)
   int staged_epilogue;       // large-M kernel: 16-bit outputs through LDS, 16-byte stores
   int epi_round;             // SWIGLU: mp_round_mode of g, u, silu(g) and h (kRoundNone: fp32)
+  int shared_b;              // grouped launches: every group multiplies the same b / s_b (a dense
+                             // GEMM run as 256-row groups); 0: group e uses expert e's rows
 };
 
 int mp_launch_i8_gemm(const mp_i8_args &args, int epilogue, hipStream_t stream);

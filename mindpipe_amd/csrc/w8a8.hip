@@ -699,7 +699,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
     moe_find_item(off, ne, n_slices, g, lane, e, slice, row_begin, row_end);
     arsrc = mp_rsrc(p.a + row_begin * k, static_cast<uint32_t>((row_end - row_begin) * k));
     act = row_begin + 64 * wm < row_end;
-    const int8_t *bexp = p.b + static_cast<int64_t>(e) * nb_rows * k;
+    const int8_t *bexp = p.b + (p.shared_b ? 0 : static_cast<int64_t>(e) * nb_rows * k);
     const int64_t col0 = static_cast<int64_t>(slice) * (SWI ? BN / 2 : BN);
 #pragma unroll
     for (int i = 0; i < CB; ++i) {
@@ -725,7 +725,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
     const __amdgpu_buffer_rsrc_t srsrc = mp_rsrc(p.s_a + row_begin, static_cast<uint32_t>((row_end - row_begin) * 4));
     scale_a = __uint_as_float(mp_buf_load4(srsrc, tid < BM ? static_cast<uint32_t>(tid * 4) : 0x80000000u, 0));
     const __amdgpu_buffer_rsrc_t brsrc =
-        mp_rsrc(p.s_b + static_cast<int64_t>(e) * nb_rows, static_cast<uint32_t>(nb_rows * 4));
+        mp_rsrc(p.s_b + (p.shared_b ? 0 : static_cast<int64_t>(e) * nb_rows), static_cast<uint32_t>(nb_rows * 4));
     {
       const int lr = (tid - BM) & (BN - 1);
       const int64_t col0 = static_cast<int64_t>(slice) * (SWI ? BN / 2 : BN);
@@ -889,6 +889,49 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
                           __float_as_uint(h));
             v[i * 16 + r] = (cval && static_cast<uint32_t>(lm) < nrows) ? fabsf(h) : 0.f;
           }
+        moe_max_step<16>(v, lane);
+        moe_max_step<8>(v, lane);
+        moe_max_step<4>(v, lane);
+        moe_max_step<2>(v, lane);
+        moe_max_step<1>(v, lane);
+        const int jv = lane & 31;
+        const int lm = lm0 + (jv >> 4) * 32 + 8 * ((jv & 15) >> 2) + (jv & 3);
+        const uint32_t np = static_cast<uint32_t>(p.n_partial);
+        const __amdgpu_buffer_rsrc_t pr = mp_rsrc(p.amax_partial + cur_begin * p.n_partial, nrows * np * 4);
+        mp_buf_store4(pr, (static_cast<uint32_t>(lm) * np + static_cast<uint32_t>(cur_slice * 2 + wn)) * 4,
+                      __float_as_uint(v[0]));
+      } else if (EPI == MP_EPI_AMAX) {
+        // y = (acc * s_tok) * s_ch (+ bias), rounded to the 16-bit output and stored (the
+        // arithmetic and order of the dense epilogues), and the abs-max of each row's rounded
+        // values over the wave's 64 columns, reduced as in the SwiGLU epilogue, into
+        // amax_partial[row][2 * slice + wave column]
+        const bool bf = p.out_dtype == MP_BF16, hb = p.bias != nullptr;
+        const __amdgpu_buffer_rsrc_t yr =
+            mp_rsrc(static_cast<char *>(p.y) + cur_begin * p.ldy * 2, nrows * ldy * 2);
+        float v[32];
+#pragma unroll
+        for (int t = 0; t < 32; ++t) v[t] = 0.f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int64_t col = static_cast<int64_t>(cur_slice) * BN + wn * 64 + j * 32 + (lane & 31);
+          const bool cval = col < n_out;
+          const float scj = ssc[par * BN + wn * 64 + j * 32 + (lane & 31)];
+          const float bj = hb ? mp_load_as_f32(p.bias, cval ? col : n_out - 1, p.bias_dtype) : 0.f;
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int lm = lm0 + i * 32 + 8 * (r >> 2) + (r & 3);
+              float yv = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), sa_r[i][r]), scj);
+              yv = hb ? mp_add(yv, bj) : yv;
+              const uint16_t hv = bf ? mp_f2bf(yv) : mp_f2h(yv);
+              const uint32_t off =
+                  cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * 2 : kOob;
+              mp_buf_store2(yr, off, hv);
+              const float rv = bf ? mp_bf2f(hv) : mp_h2f(hv);
+              v[i * 16 + r] = fmaxf(v[i * 16 + r], (cval && static_cast<uint32_t>(lm) < nrows) ? fabsf(rv) : 0.f);
+            }
+        }
         moe_max_step<16>(v, lane);
         moe_max_step<8>(v, lane);
         moe_max_step<4>(v, lane);
@@ -2040,4 +2083,141 @@ extern "C" int mp_w8a8_gemm_fake(const int8_t *qx, const float *s_tok, const int
   d.n = n;
   d.k = k;
   return mp_launch_dq_gemm(d, MP_EPI_DENSE, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------ output-quant W8A8 GEMM
+// y = W8A8 GEMM output (16-bit), then its per-token int8 codes and scale -- the q/k/v output
+// quant of SmoothQuantLinear(quantize_output=True) (fake_quant.py:77-82) returned as
+// (int8, scale) (the return_scale form of vllm_ascend.patch:4019-4020).  The GEMM runs on
+// i8_moe_kernel with every 256-row group multiplying the same weight (shared_b) and the AMAX
+// epilogue: each wave stores its 64 columns of y and the abs-max of each row's rounded values
+// over them.  The second launch reduces a row's partial maxima (2 per 128 columns, not the row),
+// derives the scale and writes the codes from the 16-bit y.
+
+__global__ void iota_groups_kernel(int64_t *__restrict__ off, int64_t groups, int64_t rows) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i <= groups) off[i] = i * kMoeBM < rows ? i * kMoeBM : rows;
+}
+
+// One workgroup per row: scale from the partial maxima (SIGNED: the bf16 fake rule's row sign
+// also needs the row's extremes, read from y), codes of the row's 16-bit values.  VEC: four
+// values per 8-byte load, four codes per store (n % 4 == 0, aligned rows).
+template <int RULE, bool SIGNED, bool VEC, int DT>
+__global__ __launch_bounds__(256) void rows_requant16_kernel(const uint16_t *__restrict__ y, const float *__restrict__ part,
+                                                             int n_partial, int64_t n, int mode, int8_t *__restrict__ q,
+                                                             float *__restrict__ s_out) {
+  __shared__ float red[3][4];
+  __shared__ int wbad[4];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t *row = y + r * n;
+  auto val = [&](uint16_t b) { return DT == MP_BF16 ? mp_bf2f(b) : mp_h2f(b); };
+  mp_rowstat st{0.f, -INFINITY, INFINITY, 0};
+  if (SIGNED) {
+    for (int64_t c = tid; c < n; c += 256) {
+      const float v = val(row[c]);
+      st.amax = fmaxf(st.amax, fabsf(v));
+      st.vmax = fmaxf(st.vmax, v);
+      st.vmin = fminf(st.vmin, v);
+    }
+  } else {
+    for (int i = tid; i < n_partial; i += 256) st.amax = fmaxf(st.amax, part[r * n_partial + i]);
+  }
+  st = mp_block_rowstat(st, red, wbad);
+  float s, sg;
+  mp_row_scale<RULE>(st, mode, 0.0f, s, sg);
+  if (tid == 0) s_out[r] = sg * s;
+  if (VEC) {
+    const uint2 *src = reinterpret_cast<const uint2 *>(row);
+    uint32_t *dst = reinterpret_cast<uint32_t *>(q + r * n);
+    for (int64_t c = tid; c < n / 4; c += 256) {
+      const uint2 w = src[c];
+      const float v0 = val(static_cast<uint16_t>(w.x & 0xFFFFu)), v1 = val(static_cast<uint16_t>(w.x >> 16));
+      const float v2 = val(static_cast<uint16_t>(w.y & 0xFFFFu)), v3 = val(static_cast<uint16_t>(w.y >> 16));
+      dst[c] = mp_row_code<RULE>(v0, s, sg, mode) | (mp_row_code<RULE>(v1, s, sg, mode) << 8) |
+               (mp_row_code<RULE>(v2, s, sg, mode) << 16) | (mp_row_code<RULE>(v3, s, sg, mode) << 24);
+    }
+  } else {
+    for (int64_t c = tid; c < n; c += 256)
+      q[r * n + c] = static_cast<int8_t>(mp_row_code<RULE>(val(row[c]), s, sg, mode));
+  }
+}
+
+static int64_t mp_qout_groups(int64_t m) { return mp_cdiv(m, kMoeBM); }
+static int64_t mp_qout_partials(int64_t n) { return 2 * mp_cdiv(n, kMoeBN); }
+
+extern "C" size_t mp_w8a8_gemm_quant_out_workspace_bytes(int64_t m, int64_t n) {
+  if (m <= 0 || n <= 0) return 0;
+  const int64_t off_bytes = mp_cdiv((mp_qout_groups(m) + 1) * 8, 256) * 256;
+  return static_cast<size_t>(off_bytes + m * mp_qout_partials(n) * 4);
+}
+
+extern "C" int mp_w8a8_gemm_quant_out(const int8_t *qx, const float *s_tok, const int8_t *w, const float *s_ch,
+                                      const void *bias, int bias_dtype, int64_t m, int64_t n, int64_t k, int out_dtype,
+                                      int scale_rule, void *y, int8_t *q_out, float *s_out, void *workspace,
+                                      size_t workspace_bytes, mp_stream_t stream) {
+  if (!qx || !s_tok || !w || !s_ch || !y || !q_out || !s_out) return MP_ERR_ARG;
+  if (out_dtype != MP_F16 && out_dtype != MP_BF16) return MP_ERR_DTYPE;
+  if (bias && bias_dtype != MP_F16 && bias_dtype != MP_BF16 && bias_dtype != MP_F32) return MP_ERR_DTYPE;
+  if (scale_rule != MP_SCALE_FP32 && scale_rule != MP_SCALE_FAKE) return MP_ERR_ARG;
+  if (m < 0 || n <= 0 || k <= 0) return MP_ERR_SHAPE;
+  if (k % kMoeBK != 0 || k > (1 << 17)) return MP_ERR_SHAPE;
+  if (n > (1 << 20) || mp_qout_groups(m) > kMoeMaxExperts) return MP_ERR_SHAPE;
+  if (m == 0) return MP_OK;
+  if (!mp_aligned(qx, 16) || !mp_aligned(w, 16) || !mp_aligned(y, 4)) return MP_ERR_ALIGN;
+  if (!workspace || workspace_bytes < mp_w8a8_gemm_quant_out_workspace_bytes(m, n)) return MP_ERR_WORKSPACE;
+  if (!mp_aligned(workspace, 16)) return MP_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t groups = mp_qout_groups(m);
+  auto *off = static_cast<int64_t *>(workspace);
+  float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + mp_cdiv((groups + 1) * 8, 256) * 256);
+  hipLaunchKernelGGL(iota_groups_kernel, dim3(static_cast<unsigned>(mp_cdiv(groups + 1, 256))), dim3(256), 0, s, off,
+                     groups, m);
+  MP_CHECK_LAUNCH();
+  mp_i8_args a{};
+  a.a = qx;
+  a.s_a = s_tok;
+  a.b = w;
+  a.s_b = s_ch;
+  a.bias = bias;
+  a.bias_dtype = bias_dtype;
+  a.y = y;
+  a.out_dtype = out_dtype;
+  a.amax_partial = part;
+  a.n_partial = static_cast<int>(mp_qout_partials(n));
+  a.offsets = off;
+  a.n_experts = static_cast<int>(groups);
+  a.rows = m;
+  a.n = n;
+  a.k = k;
+  a.ldy = n;
+  a.shared_b = 1;
+  const int rc = mp_launch_moe<MP_EPI_AMAX>(a, s);
+  if (rc != MP_OK) return rc;
+  const int mode = mp_round_mode_of(out_dtype);
+  const bool vec = n % 4 == 0 && mp_aligned(y, 8) && mp_aligned(q_out, 4);
+  const auto *yh = static_cast<const uint16_t *>(y);
+  const dim3 g(static_cast<unsigned>(m));
+#define MP_RQ16(RULE_, SIGNED_, VEC_)                                                                          \
+  do {                                                                                                         \
+    if (out_dtype == MP_BF16)                                                                                  \
+      hipLaunchKernelGGL((rows_requant16_kernel<RULE_, SIGNED_, VEC_, MP_BF16>), g, dim3(256), 0, s, yh, part, \
+                         a.n_partial, n, mode, q_out, s_out);                                                  \
+    else                                                                                                       \
+      hipLaunchKernelGGL((rows_requant16_kernel<RULE_, SIGNED_, VEC_, MP_F16>), g, dim3(256), 0, s, yh, part,  \
+                         a.n_partial, n, mode, q_out, s_out);                                                  \
+  } while (0)
+  if (scale_rule == MP_SCALE_FP32) {
+    if (vec) MP_RQ16(MP_SCALE_FP32, false, true);
+    else MP_RQ16(MP_SCALE_FP32, false, false);
+  } else if (mode == kRoundBF16) {  // the bf16 fake codes reach +-128: the row sign needs its extremes
+    if (vec) MP_RQ16(MP_SCALE_FAKE, true, true);
+    else MP_RQ16(MP_SCALE_FAKE, true, false);
+  } else {
+    if (vec) MP_RQ16(MP_SCALE_FAKE, false, true);
+    else MP_RQ16(MP_SCALE_FAKE, false, false);
+  }
+#undef MP_RQ16
+  MP_CHECK_LAUNCH();
+  return MP_OK;
 }

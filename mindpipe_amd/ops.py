@@ -359,6 +359,49 @@ def _(qx, s_tok, w, s_ch, bias, act_dtype):
 _RULES = {"runtime": MP_SCALE_FP32, "fake": MP_SCALE_FAKE}
 
 
+@torch.library.custom_op("mindpipe_amd::w8a8_gemm_quant_out", mutates_args=())
+def w8a8_gemm_quant_out(qx: torch.Tensor, s_tok: torch.Tensor, w: torch.Tensor, s_ch: torch.Tensor,
+                        bias: Optional[torch.Tensor], out_dtype: torch.dtype,
+                        fake_rule: bool = False) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``(y, q, s)``: the W8A8 linear's output ``y [M, N]`` in ``out_dtype`` (fp16 / bf16) and its
+    per-token int8 codes and scale, from the GEMM epilogue's row abs-max (``quantize_output``,
+    ``fake_quant.py:77-82``).  ``fake_rule``: the reference's fake rule in ``out_dtype`` (else the
+    fp32 runtime rule)."""
+    _need(qx, "qx", torch.int8, 2)
+    _need(w, "w", torch.int8, 2)
+    _need(s_tok, "s_tok", torch.float32, 1)
+    _need(s_ch, "s_ch", torch.float32, 1)
+    if out_dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError(f"w8a8_gemm_quant_out writes fp16 or bf16, got {out_dtype}")
+    m, k = qx.shape
+    n = w.shape[0]
+    if w.shape[1] != k or s_tok.numel() != m or s_ch.numel() != n:
+        raise RuntimeError("w8a8_gemm_quant_out: operand shapes disagree")
+    if bias is not None:
+        _need(bias, "bias", (torch.float16, torch.bfloat16, torch.float32), 1)
+    y = torch.empty((m, n), dtype=out_dtype, device=qx.device)
+    q = torch.empty((m, n), dtype=torch.int8, device=qx.device)
+    sc = torch.empty((m,), dtype=torch.float32, device=qx.device)
+    lib = _lib.load()
+    ws = torch.empty(max(16, int(lib.mp_w8a8_gemm_quant_out_workspace_bytes(m, n))), dtype=torch.uint8,
+                     device=qx.device)
+    with _dev(qx):
+        _lib.check(lib.mp_w8a8_gemm_quant_out(
+            qx.data_ptr(), s_tok.data_ptr(), w.data_ptr(), s_ch.data_ptr(), _ptr(bias),
+            _DT[bias.dtype] if bias is not None else 0, m, n, k, _DT[out_dtype],
+            MP_SCALE_FAKE if fake_rule else MP_SCALE_FP32, y.data_ptr(), q.data_ptr(), sc.data_ptr(), ws.data_ptr(),
+            ws.numel(), _stream()), "mp_w8a8_gemm_quant_out")
+    return y, q, sc
+
+
+@w8a8_gemm_quant_out.register_fake
+def _(qx, s_tok, w, s_ch, bias, out_dtype, fake_rule=False):
+    m, n = qx.shape[0], w.shape[0]
+    return (torch.empty((m, n), dtype=out_dtype, device=qx.device),
+            torch.empty((m, n), dtype=torch.int8, device=qx.device),
+            torch.empty((m,), dtype=torch.float32, device=qx.device))
+
+
 def _rule(rule: str) -> int:
     if rule not in _RULES:
         raise ValueError(f"unknown scale rule {rule!r} (expected 'runtime' or 'fake')")

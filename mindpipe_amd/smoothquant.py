@@ -148,21 +148,57 @@ class SmoothQuantLinear(nn.Module):
         _require_gpu(x, "SmoothQuantLinear")
         if self.weight_bits >= 16:
             return self.output_quant(F.linear(self.act_quant(x), self.weight, self.bias))
+        fake, q, s = self._input_codes(x)
+        if self._fused_output_quant(x, fake):
+            qo, so = self._output_codes(q, s, x.dtype)
+            return (qo.float() * so.unsqueeze(-1)).to(x.dtype)
+        return self.output_quant(self._linear(x, fake, q, s))
+
+    def _input_codes(self, x):
         if self.activation_bits >= 16:
             raise NotImplementedError("W8A16 is not a path of this build (weights int8 need int8 activations)")
         fake = self.scale_rule == "fake"
         if fake and x.dtype not in _FAKE_DTYPES:
             raise NotImplementedError("the fake scale rule takes fp16 or bf16 activations")
         q, s = ops.quant_per_token_i8(x.contiguous(), fake)
+        return fake, q, s
+
+    def _linear(self, x, fake, q, s):
+        """The linear's output before any output quant."""
         if fake and x.dtype == torch.bfloat16:
             # bf16 keeps 8 significant bits: the reference multiplies the bf16-rounded fake values
             # r(q * s), which the int8 product of q * s misses by ~3e-3; the dequantising GEMM
             # rounds each element as the reference does
             bias = None if self.bias is None else self.bias.to(torch.bfloat16)
-            y = ops.w8a8_gemm_fake(q, s.float().contiguous(), self.weight, self.weight_scale, bias, x.dtype)
-        else:
-            y = ops.w8a8_gemm(q, s.float().contiguous(), self.weight, self.weight_scale, self.bias, x.dtype)
-        return self.output_quant(y)
+            return ops.w8a8_gemm_fake(q, s.float().contiguous(), self.weight, self.weight_scale, bias, x.dtype)
+        return ops.w8a8_gemm(q, s.float().contiguous(), self.weight, self.weight_scale, self.bias, x.dtype)
+
+    def _fused_output_quant(self, x, fake: bool) -> bool:
+        """The output quant runs in the GEMM epilogue (``w8a8_gemm_quant_out``) for 8-bit outputs of
+        the int8 GEMM (not the bf16 fake-rule linear, which rounds its operands) when K % 128 == 0."""
+        return (self.output_quant_name != "none" and self.activation_bits == 8 and self.in_features % 128 == 0
+                and not (fake and x.dtype == torch.bfloat16))
+
+    def _output_codes(self, q, s, dtype):
+        lead = q.shape[:-1]
+        bias = None if self.bias is None else self.bias.to(dtype)
+        _, qo, so = ops.w8a8_gemm_quant_out(q.reshape(-1, self.in_features).contiguous(),
+                                            s.reshape(-1).float().contiguous(), self.weight, self.weight_scale, bias,
+                                            dtype, True)
+        return qo.reshape(*lead, self.out_features), so.reshape(lead)
+
+    @torch.no_grad()
+    def quantized_output(self, x):
+        """``(int8 codes, scale)`` of the fake-quantized output (``quantize_output=True``): the codes
+        and per-token scale of the reference's output fake quant (``fake_quant.py:77-82``), from the
+        GEMM epilogue, for consumers that take quantized q/k/v (the ``return_scale`` form)."""
+        _require_gpu(x, "SmoothQuantLinear")
+        if self.output_quant_name == "none" or self.weight_bits >= 16:
+            raise RuntimeError("quantized_output needs an int8 linear with quantize_output=True")
+        fake, q, s = self._input_codes(x)
+        if self._fused_output_quant(x, fake):
+            return self._output_codes(q, s, x.dtype)
+        return ops.quant_per_token_i8(self._linear(x, fake, q, s).contiguous(), True)
 
     @staticmethod
     def from_float(module, weight_bits=8, activation_bits=8, act_quant="per_token", quantize_output=False,

@@ -58,14 +58,15 @@ def _cases():
         "w8a8_gemm_fake": (mp.w8a8_gemm_fake.default, (qx, sx.half().float(), w8, s8.half().float(), None,
                                                        torch.float16)),
         "w4a16_gemm": (mp.w4a16_gemm.default, (x, pk, gs, gz, 128, None)),
+        "w8a8_gemm_quant_out": (mp.w8a8_gemm_quant_out.default, (qx, sx, w8, s8, None, torch.float16, False)),
         "i8_gemm_swiglu_requant": (mp.i8_gemm_swiglu_requant.default, (qx, sx, w13, s13, offs, i)),
         "moe_w8a8_forward": (mp.moe_w8a8_forward.default, (x, ids, tw, mw13, ms13, mw2, ms2)),
     }
 
 
 NAMES = ["add_rms_norm_dynamic_quant", "rms_norm_dynamic_quant", "add_rms_norm", "dense_mlp_w8a8",
-         "quant_per_token_i8", "w8a8_gemm", "w8a8_gemm_fake", "w4a16_gemm", "i8_gemm_swiglu_requant",
-         "moe_w8a8_forward"]
+         "quant_per_token_i8", "w8a8_gemm", "w8a8_gemm_fake", "w8a8_gemm_quant_out", "w4a16_gemm",
+         "i8_gemm_swiglu_requant", "moe_w8a8_forward"]
 
 
 @pytest.mark.parametrize("name", NAMES)
