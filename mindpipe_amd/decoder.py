@@ -74,6 +74,24 @@ class _W4:
     def nbytes(self):
         return self.packed.numel() * 4 + self.scales.numel() * 2 + self.zeros.numel() * 2
 
+    def dequantized(self):
+        """The pseudo-quantized fp16 weight ``(u - z) * s`` (each op rounded to fp16, as the reference's
+        dequantised tensor), unpacked with torch bit operations: the reference path shares no kernel
+        with the W4A16 GEMMs it checks.  Cached."""
+        w = getattr(self, "_deq", None)
+        if w is None:
+            shifts = torch.arange(0, 32, 4, device=self.packed.device, dtype=torch.int32)
+            u = ((self.packed.unsqueeze(-1) >> shifts) & 0xF).reshape(self.n, self.k).to(torch.float16)
+            s = self.scales.repeat_interleave(self.group, dim=1)
+            z = self.zeros.repeat_interleave(self.group, dim=1)
+            w = (u - z) * s
+            self._deq = w
+        return w
+
+    def reference(self, x):
+        """``F.linear`` on the pseudo-quantized weight with fp32 accumulation, one rounding to fp16."""
+        return (x.float() @ self.dequantized().float().t()).half()
+
 
 def _rms(x, w, eps):
     xf = x.float()
@@ -159,7 +177,8 @@ class W4Decoder:
 
     @torch.no_grad()
     def prefill_torch(self, tokens, return_logits=False):
-        """The prefill in PyTorch ops around the same W4A16 linears (reference path)."""
+        """The prefill in PyTorch ops (reference path): every linear is F.linear on the
+        pseudo-quantized fp16 weight (fp32 accumulation), attention in fp32."""
         cfg = self.cfg
         b, t = tokens.shape
         hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
@@ -167,7 +186,7 @@ class W4Decoder:
         pos = torch.arange(t, device=tokens.device)
         for li, l in enumerate(self.layers):
             hn = _rms(x, l["ln1"], cfg.eps)
-            qkv = l["qkv"](hn.reshape(b * t, -1)).reshape(b, t, nh + 2 * kvh, hd).transpose(1, 2)
+            qkv = l["qkv"].reference(hn.reshape(b * t, -1)).reshape(b, t, nh + 2 * kvh, hd).transpose(1, 2)
             q, k, v = qkv[:, :nh], qkv[:, nh:nh + kvh], qkv[:, nh + kvh:]
             q, k = self._rope(q, pos), self._rope(k, pos)
             self.k_cache[li, :b, :, :t] = k
@@ -176,12 +195,12 @@ class W4Decoder:
             vv = v.repeat_interleave(nh // kvh, dim=1) if kvh != nh else v
             att = torch.nn.functional.scaled_dot_product_attention(q.float(), kk.float(), vv.float(),
                                                                    is_causal=True).half()
-            x = x + l["o"](att.transpose(1, 2).reshape(b * t, nh * hd)).reshape(b, t, -1)
+            x = x + l["o"].reference(att.transpose(1, 2).reshape(b * t, nh * hd)).reshape(b, t, -1)
             hn = _rms(x, l["ln2"], cfg.eps)
-            gu = l["gate_up"](hn.reshape(b * t, -1))
+            gu = l["gate_up"].reference(hn.reshape(b * t, -1))
             act = torch.nn.functional.silu(gu[:, :cfg.ffn]) * gu[:, cfg.ffn:]
-            x = x + l["down"](act.contiguous()).reshape(b, t, -1)
-        logits = self.lm_head(_rms(x[:, -1], self.norm, cfg.eps).contiguous())
+            x = x + l["down"].reference(act.contiguous()).reshape(b, t, -1)
+        logits = self.lm_head.reference(_rms(x[:, -1], self.norm, cfg.eps).contiguous())
         return logits if return_logits else logits.argmax(-1)
 
     def attn_splits(self, b):
@@ -247,8 +266,9 @@ class W4Decoder:
 
     @torch.no_grad()
     def decode_step_torch(self, tokens, cur_len, return_logits=False):
-        """The decode step in PyTorch ops (reference path): RMSNorm on the rounded residual,
-        fp32 attention over the whole cache masked by the current length."""
+        """The decode step in PyTorch ops (reference path): RMSNorm on the rounded residual, every
+        linear F.linear on the pseudo-quantized fp16 weight (fp32 accumulation), fp32 attention over the
+        whole cache masked by the current length."""
         cfg = self.cfg
         b = tokens.shape[0]
         hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
@@ -259,7 +279,7 @@ class W4Decoder:
         scale = 1.0 / math.sqrt(hd)
         for li, l in enumerate(self.layers):
             hn = _rms(x, l["ln1"], cfg.eps)
-            qkv = l["qkv"](hn).reshape(b, nh + 2 * kvh, 1, hd)
+            qkv = l["qkv"].reference(hn).reshape(b, nh + 2 * kvh, 1, hd)
             q, k, v = qkv[:, :nh], qkv[:, nh:nh + kvh], qkv[:, nh + kvh:]
             q, k = self._rope(q, pos), self._rope(k, pos)
             self.k_cache[li, :b].index_copy_(2, cur_len, k.contiguous())
@@ -269,10 +289,10 @@ class W4Decoder:
             s = torch.matmul(qg, kt) * scale + mask                # [B, kvh, grp, T]
             p = torch.softmax(s, dim=-1)
             att = torch.matmul(p, self.v_cache[li, :b].float()).half()
-            x = x + l["o"](att.reshape(b, nh * hd))
+            x = x + l["o"].reference(att.reshape(b, nh * hd))
             hn = _rms(x, l["ln2"], cfg.eps)
-            gu = l["gate_up"](hn)
+            gu = l["gate_up"].reference(hn)
             act = torch.nn.functional.silu(gu[:, :cfg.ffn]) * gu[:, cfg.ffn:]
-            x = x + l["down"](act.contiguous())
-        logits = self.lm_head(_rms(x, self.norm, cfg.eps).contiguous())
+            x = x + l["down"].reference(act.contiguous())
+        logits = self.lm_head.reference(_rms(x, self.norm, cfg.eps).contiguous())
         return logits if return_logits else logits.argmax(-1)

@@ -659,12 +659,50 @@ def w4a16_gemv_add_rms_norm(x: torch.Tensor, residual: Optional[torch.Tensor], n
     return y, rsum
 
 
+def _decode_checks(b: int, nh: int, kvh: int, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
+                   qkv: Optional[torch.Tensor] = None, q: Optional[torch.Tensor] = None,
+                   cos_t: Optional[torch.Tensor] = None, sin_t: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None) -> None:
+    """Shapes the decode kernels assume (the C ABI sees pointers only, so a wrong extent would become
+    an out-of-bounds access instead of an error): head dim 128, caches ``[B, kvh, T, 128]`` fp16,
+    RoPE tables ``[>= T, 64]`` fp16, ``pos`` one int64, outputs ``[B, nh, 128]`` fp16."""
+    if nh <= 0 or kvh <= 0 or nh % kvh:
+        raise RuntimeError(f"heads {nh} must be a positive multiple of kv heads {kvh}")
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, torch.float16, 4)
+        if c.shape[0] != b or c.shape[1] != kvh or c.shape[3] != 128:
+            raise RuntimeError(f"{name} must be [{b}, {kvh}, T, 128], got {tuple(c.shape)}")
+    if v_cache.shape != k_cache.shape:
+        raise RuntimeError("k_cache and v_cache must have one shape")
+    _need(pos, "pos", torch.int64)
+    if pos.numel() != 1:
+        raise RuntimeError("pos must hold one position")
+    if qkv is not None:
+        _need(qkv, "qkv", torch.float16, 2)
+        if qkv.shape != (b, (nh + 2 * kvh) * 128):
+            raise RuntimeError(f"qkv must be [{b}, {(nh + 2 * kvh) * 128}], got {tuple(qkv.shape)}")
+    if q is not None:
+        _need(q, "q", torch.float16, 3)
+        if q.shape != (b, nh, 128):
+            raise RuntimeError(f"q must be [{b}, {nh}, 128], got {tuple(q.shape)}")
+    for name, t in (("cos_t", cos_t), ("sin_t", sin_t)):
+        if t is not None:
+            _need(t, name, torch.float16, 2)
+            if t.shape[0] < k_cache.shape[2] or t.shape[1] != 64:
+                raise RuntimeError(f"{name} must be [>= {k_cache.shape[2]}, 64], got {tuple(t.shape)}")
+    if out is not None:
+        _need(out, "out", torch.float16, 3)
+        if out.shape != (b, nh, 128):
+            raise RuntimeError(f"out must be [{b}, {nh}, 128], got {tuple(out.shape)}")
+
+
 def decode_rope_append(qkv: torch.Tensor, nh: int, kvh: int, cos_t: torch.Tensor, sin_t: torch.Tensor,
                        pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                        q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """RoPE on q/k of ``qkv [B, (nh+2kvh)*128]`` and append k/v at ``pos`` (int64 device scalar)
     into ``k_cache``/``v_cache [B, kvh, T, 128]``; returns rotated ``q [B, nh, 128]``."""
     b = qkv.shape[0]
+    _decode_checks(b, nh, kvh, k_cache, v_cache, pos, qkv=qkv, cos_t=cos_t, sin_t=sin_t, out=q_out)
     cap = k_cache.shape[2]
     if q_out is None:
         q_out = torch.empty((b, nh, 128), dtype=torch.float16, device=qkv.device)
@@ -684,7 +722,10 @@ def decode_attention_workspace(batch: int, nh: int, splits: int, device) -> torc
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor, splits: int,
                      scale: float, workspace: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Attention of ``q [B, nh, 128]`` over cache positions ``[0, pos]``: ``[B, nh, 128]`` fp16."""
+    _need(q, "q", torch.float16, 3)
     b, nh, hd = q.shape
+    _need(workspace, "workspace", torch.float32, 1)
+    _decode_checks(b, nh, k_cache.shape[1] if k_cache.dim() == 4 else 1, k_cache, v_cache, pos, q=q, out=out)
     kvh, cap = k_cache.shape[1], k_cache.shape[2]
     if out is None:
         out = torch.empty_like(q)
@@ -703,6 +744,8 @@ def decode_rope_attention(qkv: torch.Tensor, nh: int, kvh: int, cos_t: torch.Ten
     ``qkv [B, (nh+2kvh)*128]``, k/v appended at ``pos``, attention over ``[0, pos]``;
     returns ``[B, nh, 128]`` fp16."""
     b = qkv.shape[0]
+    _need(workspace, "workspace", torch.float32, 1)
+    _decode_checks(b, nh, kvh, k_cache, v_cache, pos, qkv=qkv, cos_t=cos_t, sin_t=sin_t, out=out)
     cap = k_cache.shape[2]
     if out is None:
         out = torch.empty((b, nh, 128), dtype=torch.float16, device=qkv.device)

@@ -6,7 +6,10 @@ Bars: RoPE and the cache writes are bit-exact to the same fp16 op sequence in
 PyTorch; attention has relative Frobenius error <= 1e-3 against fp32 softmax
 attention; SiLU-mul is within one fp16 ulp (exp is not correctly rounded on
 either side); decoder logits within 2e-2 relative of the PyTorch step (the
-RMSNorm statistics differ by design: fp32 sum vs the rounded residual)."""
+RMSNorm statistics differ by design: fp32 sum vs the rounded residual).  The PyTorch
+step shares no kernel with the HIP step: its linears are F.linear on the
+pseudo-quantized fp16 weights unpacked with torch bit operations, its norms, RoPE and
+attention are torch ops."""
 import math
 
 import numpy as np
@@ -284,3 +287,36 @@ def test_argmax_rows_matches_torch(rows, n):
         x[1] = float("-inf")                     # all equal: index 0
         x[2, n // 2] = float("nan")              # NaN counts as the maximum
     assert torch.equal(ops.argmax_rows(x), torch.argmax(x, dim=-1))
+
+
+def test_decode_ops_reject_wrong_extents():
+    """The decode ops check every extent the kernels assume before launching (the C ABI sees only
+    pointers): qkv width, cache shapes, RoPE table rows, pos, output and workspace."""
+    _say("decode op checks")
+    from mindpipe_amd import ops
+    b, nh, kvh, cap = 2, 4, 2, 64
+    qkv = torch.zeros(b, (nh + 2 * kvh) * 128, device=DEV).half()
+    kc = torch.zeros(b, kvh, cap, 128, device=DEV).half()
+    vc = torch.zeros_like(kc)
+    cos = torch.zeros(cap, 64, device=DEV).half()
+    sin = torch.zeros_like(cos)
+    pos = torch.tensor([3], device=DEV, dtype=torch.int64)
+    ws = ops.decode_attention_workspace(b, nh, 1, DEV)
+    ops.decode_rope_attention(qkv, nh, kvh, cos, sin, pos, kc, vc, 1, 0.1, ws)   # the valid call
+    bad = [
+        lambda: ops.decode_rope_attention(qkv[:, :-128].contiguous(), nh, kvh, cos, sin, pos, kc, vc, 1, 0.1, ws),
+        lambda: ops.decode_rope_attention(qkv, nh, kvh, cos[:cap - 1].contiguous(), sin, pos, kc, vc, 1, 0.1, ws),
+        lambda: ops.decode_rope_attention(qkv, nh, kvh, cos, sin, pos, kc[:1].contiguous(), vc, 1, 0.1, ws),
+        lambda: ops.decode_rope_attention(qkv, nh, kvh, cos, sin, pos.int(), kc, vc, 1, 0.1, ws),
+        lambda: ops.decode_rope_attention(qkv, nh, kvh, cos, sin, torch.tensor([1, 2], device=DEV), kc, vc, 1, 0.1, ws),
+        lambda: ops.decode_rope_append(qkv, nh, 3, cos, sin, pos, kc, vc),
+        lambda: ops.decode_attention(torch.zeros(b, nh, 64, device=DEV).half(), kc, vc, pos, 1, 0.1, ws),
+        lambda: ops.decode_attention(torch.zeros(b, nh, 128, device=DEV).half(), kc, vc[..., :64].contiguous(), pos,
+                                     1, 0.1, ws),
+        lambda: ops.decode_rope_attention(qkv, nh, kvh, cos, sin, pos, kc, vc, 1, 0.1, ws,
+                                          out=torch.empty(b, nh + 1, 128, device=DEV).half()),
+    ]
+    for i, f in enumerate(bad):
+        with pytest.raises(RuntimeError):
+            f()
+        torch.cuda.synchronize()
