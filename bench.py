@@ -323,6 +323,25 @@ def profile_mix(ops, name, steps):
                         ops.w4a16_gemm(x, pk[0], sc[0], zr[0], 128, None)
             del pk, sc, zr
         print("w4batch8 done")
+    elif name == "dec7b":
+        # the Llama-2-7B decode step at B = 1 and B = 8 with a 2048-token context (random KV values),
+        # 4 eager steps each: the kernels of the bench's decode leg, one launch at a time
+        from mindpipe_amd.decoder import DecoderConfig, W4Decoder
+        cfg = DecoderConfig.llama2_7b()
+        for b in (1, 8):
+            model = W4Decoder(cfg, max_batch=b, max_len=2048 + 8)
+            g = torch.Generator(device="cuda").manual_seed(5)
+            model.k_cache.normal_(0, 1, generator=g)
+            model.v_cache.normal_(0, 1, generator=g)
+            tok = torch.randint(0, cfg.vocab, (b,), device="cuda", generator=g)
+            cur = torch.tensor([2048], device="cuda", dtype=torch.int64)
+            for _ in range(4):
+                tok = model.decode_step(tok, cur)
+                cur.add_(1)
+            torch.cuda.synchronize()
+            del model
+            torch.cuda.empty_cache()
+        print("dec7b done")
     elif name == "w8big":
         gen = torch.Generator(device="cuda").manual_seed(1)
         qx = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device="cuda", generator=gen)
