@@ -1379,6 +1379,174 @@ __global__ __launch_bounds__(W * 64) void w4a16_gemv_mfma_kernel(
   }
 }
 
+typedef __bf16 bf8w_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf2w_t __attribute__((ext_vector_type(2)));
+
+// The eight weights of one packed word (K positions 0..7, natural order) as bf16 pairs, each
+// R_bf16((u - z) s): the reference's bf16 pseudo-quantized weight, (q - z) exact and one rounding of
+// the product (awq/quantize/quantizer.py:95-105 in bf16 arithmetic).  (w & 0x000F000F) | 0x64006400
+// is the fp16 pair (1024 + u0, 1024 + u4) and the 0x00F000F0 mask gives (1024 + 16 u1, 1024 + 16 u5).
+// Each v_fma_mix computes (1024 + u) s - (1024 + z) s, resp. (1024 + 16 u) (s / 16) - (64 + z) s,
+// in one fp32 rounding that is exact: both subtracted products are exact in fp32 (at most 19
+// significant bits) and so is the difference (u - z) s (at most 12).  v_cvt_pk_bf16_f32 then rounds
+// to nearest even once.
+__device__ __forceinline__ uint4 w4_bf16x8(uint32_t w, float s, float s16, float nce, float nco, uint32_t m0,
+                                           uint32_t m1, uint32_t magic) {
+  const uint32_t w8 = w >> 8;
+  const h2_t e0 = mp_as_h2((w & m0) | magic), o0 = mp_as_h2((w & m1) | magic);
+  const h2_t e1 = mp_as_h2((w8 & m0) | magic), o1 = mp_as_h2((w8 & m1) | magic);
+  const bf2w_t p0 = {static_cast<__bf16>(fmaf(static_cast<float>(e0[0]), s, nce)),
+                     static_cast<__bf16>(fmaf(static_cast<float>(o0[0]), s16, nco))};
+  const bf2w_t p1 = {static_cast<__bf16>(fmaf(static_cast<float>(e1[0]), s, nce)),
+                     static_cast<__bf16>(fmaf(static_cast<float>(o1[0]), s16, nco))};
+  const bf2w_t p2 = {static_cast<__bf16>(fmaf(static_cast<float>(e0[1]), s, nce)),
+                     static_cast<__bf16>(fmaf(static_cast<float>(o0[1]), s16, nco))};
+  const bf2w_t p3 = {static_cast<__bf16>(fmaf(static_cast<float>(e1[1]), s, nce)),
+                     static_cast<__bf16>(fmaf(static_cast<float>(o1[1]), s16, nco))};
+  return make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                    __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
+}
+
+// bf16 W4A16 for 1 to 16 activation rows on the matrix cores (group size 128):
+// y[m][n] = sum_k x[m][k] R_bf16((u(n, k) - z(n, g)) s(n, g)) (+ bias[n]), F.linear on the
+// reference's bf16 pseudo-quantized weight (fp32 accumulation, one rounding of the output).
+// A workgroup of W waves owns 16 output rows; wave w takes the contiguous 128-wide K groups
+// [w gpw, (w + 1) gpw) and streams them in rounds of two groups, the next round's weight loads in
+// flight while the current one is dequantised (register ping-pong).  Lane l: output row
+// n = l & 15 (MFMA B column), token l & 15 (A row), lane group g = l >> 4.
+//  * Scale / zero: before the first round the wave copies the (s, z) pairs of its 16 rows x gpw
+//    groups into LDS with coalesced loads (consecutive lanes, consecutive groups of a row); the
+//    rounds read one 32-bit pair per group.  Per-group 16-bit loads scattered over 16 rows cost
+//    more than the weight stream itself.
+//  * Weights: per group one 16-byte load per lane, words 4 g .. 4 g + 3 of row n's group (K 32 g ..
+//    32 g + 31 of the group); word j, dequantised by w4_bf16x8, is the B operand of MFMA j.
+//  * Activations: the A operand of MFMA j is x[token][32 g + 8 j .. + 7] of the group, in natural
+//    order.  One row (ONE): the wave's slice of x is copied into LDS before the first round and
+//    every A row reads it back; several rows: each lane loads its token's row with the weights
+//    (lanes past M repeat row M - 1, whose outputs are dropped).
+//  * D: lane (n, g) holds tokens 4 g .. 4 g + 3 of output row n; the W partials meet in LDS and
+//    wave 0 adds them in wave order.
+// Dynamic LDS: W x 16 x (gpw + 1) pair words (row stride padded by one word), then, for ONE,
+// W x gpw x 256 bytes of activations.
+template <int W, bool ONE, bool ZP>
+__global__ __launch_bounds__(W * 64) void w4a16_bf16_small_kernel(
+    const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_rows,
+    const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups, int gpw,
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ y) {
+  constexpr int U = 2;
+  extern __shared__ uint4 bf_lds[];
+  __shared__ f4_t red[W][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int row0 = blockIdx.x * 16;
+  const int row = row0 + n;
+  const int rowc = row < n_rows ? row : n_rows - 1;
+  const int tok = ONE ? 0 : (n < m_rows ? n : m_rows - 1);
+  const int gb = wave * gpw;
+  const int ge = gb + gpw < n_groups ? gb + gpw : n_groups;
+  const int cnt = ge > gb ? ge - gb : 0;  // groups of this wave (wave-uniform)
+  const int nr = (cnt + U - 1) / U;       // rounds
+  const int szst = gpw + 1;
+  uint32_t *szw = reinterpret_cast<uint32_t *>(bf_lds) + wave * 16 * szst;
+  uint4 *xw = bf_lds + (W * 16 * szst + 3) / 4 + static_cast<int64_t>(wave) * gpw * 16;
+  const uint32_t *wr = wq + static_cast<int64_t>(rowc) * (k >> 3) + 4 * g;
+  const uint16_t *xr = x + static_cast<int64_t>(tok) * k + 32 * g;
+  uint32_t magic_v = kMagic, m0_v = 0x000F000Fu, m1_v = 0x00F000F0u;
+  asm volatile("" : "+v"(magic_v), "+v"(m0_v), "+v"(m1_v));  // opaque: keep the constants in VGPRs
+  f4_t acc = {0.f, 0.f, 0.f, 0.f};
+  struct Round {
+    uint4 w[U];
+    uint4 xv[ONE ? 1 : U][ONE ? 1 : 4];
+  };
+  // loads of round r (group indices past the wave's range repeat its last group, never used)
+  auto load = [&](Round &b, int r) {
+    if constexpr (!ONE) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int gi = gb + r * U + u < ge ? gb + r * U + u : ge - 1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          b.xv[u][j] = *reinterpret_cast<const uint4 *>(xr + static_cast<int64_t>(gi) * 128 + 8 * j);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int gi = gb + r * U + u < ge ? gb + r * U + u : ge - 1;
+      b.w[u] = *reinterpret_cast<const uint4 *>(wr + static_cast<int64_t>(gi) * 16);
+    }
+  };
+  auto compute = [&](Round &b, int r) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int gl = r * U + u;
+      if (gl < cnt) {  // wave-uniform
+        const uint32_t szv = szw[n * szst + gl];
+        const float s = __uint_as_float(szv << 16), z = __uint_as_float(szv & 0xFFFF0000u);
+        const float s16 = s * 0.0625f, nce = -((1024.f + z) * s), nco = -((64.f + z) * s);
+        const uint32_t w4[4] = {b.w[u].x, b.w[u].y, b.w[u].z, b.w[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 bw = w4_bf16x8(w4[j], s, s16, nce, nco, m0_v, m1_v, magic_v);
+          const uint4 a = ONE ? xw[gl * 16 + 4 * g + j] : b.xv[ONE ? 0 : u][j];
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8w_t, a), __builtin_bit_cast(bf8w_t, bw),
+                                                        acc, 0, 0, 0);
+        }
+      }
+    }
+  };
+  if (nr > 0) {
+    // (s, z) pairs of the 16 rows x cnt groups, element e = row r * cnt + group c
+    for (int e = lane; e < 16 * cnt; e += 64) {
+      const int r = e / cnt, c = e - r * cnt;
+      const int rr = row0 + r < n_rows ? row0 + r : n_rows - 1;
+      const int64_t gi = static_cast<int64_t>(rr) * n_groups + gb + c;
+      szw[r * szst + c] = static_cast<uint32_t>(sc[gi]) | (static_cast<uint32_t>(ZP ? zr[gi] : 0x4100u) << 16);
+    }
+    Round A, B;
+    load(A, 0);
+    if constexpr (ONE) {  // the wave's activation slice: lane group g copies groups g, g + 4, ...
+      for (int c = g; c < cnt; c += 4)
+        xw[c * 16 + n] = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(gb + c) * 128 + 8 * n);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes land before its reads
+    __builtin_amdgcn_wave_barrier();
+    int r = 0;
+    for (; r + 2 < nr; r += 2) {
+      load(B, r + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(A, r);
+      __builtin_amdgcn_sched_barrier(0);
+      load(A, r + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(B, r + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (r + 1 < nr) {
+      load(B, r + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(A, r);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(B, r + 1);
+    } else {
+      compute(A, r);
+    }
+  }
+  if (W > 1) {
+    red[wave][lane] = acc;
+    mp_lds_barrier();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 1; w < W; ++w) acc += red[w][lane];
+  }
+  if (row >= n_rows) return;
+  const float bv = bias ? mp_bf2f(bias[row]) : 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 4 * g + i;
+    if (t < (ONE ? 1 : m_rows)) y[static_cast<int64_t>(t) * n_rows + row] = mp_f2bf(acc[i] + bv);
+  }
+}
+
 // Measurement knobs for the one-row GEMV shape choice: MP_W4_GEMV_R (rows per
 // wave), MP_W4_GEMV_C (chunks per iteration), MP_W4_GEMV_S (waves splitting K);
 // MP_W4_GEMV_OFF=1 routes one-row calls to the general decode kernel.
@@ -1397,6 +1565,42 @@ static int mp_gemv_env(int which) {
 static bool mp_gemv_mfma() {
   static const bool v = !(mp_knob("MP_W4_GEMV_MFMA") && atoi(mp_knob("MP_W4_GEMV_MFMA")) == 0);
   return v;
+}
+
+// MP_W4_BF16_SMALL=0 routes bf16 calls of 1 to 16 rows to the dequantising GEMM (for measurements).
+static bool mp_bf16_small() {
+  static const bool v = !(mp_knob("MP_W4_BF16_SMALL") && atoi(mp_knob("MP_W4_BF16_SMALL")) == 0);
+  return v;
+}
+
+// bf16 small-M kernel shape: waves per 16-row block, the fewest powers of two that give the grid
+// about 4096 waves (measured on the 7B / 70B decode shapes: 2048 to 8192 land within 5%), at most 16
+// and at least two rounds of two groups per wave; and its dynamic LDS (pair words + one-row slice).
+static int mp_bf16_small_waves(int64_t blocks, int ng) {
+  int w = 1;
+  while (w < 16 && blocks * w < 4096 && ng >= 4 * w) w *= 2;
+  return w;
+}
+static size_t mp_bf16_small_lds_for(int w, int gpw, bool one) {
+  return ((static_cast<size_t>(w) * 16 * (gpw + 1) + 3) / 4) * 16 + (one ? static_cast<size_t>(w) * gpw * 256 : 0);
+}
+// dynamic LDS bound: one row up to K of about 38900 (the 70B down projection, K = 28672, takes 72 KiB
+// at 8 waves), several rows far beyond any layer; above it the dequantising GEMM
+constexpr size_t kBf16SmallLds = 96 * 1024;
+
+template <int W, bool ONE, bool ZP>
+static int mp_bf16_small_launch(int64_t blocks, size_t lds, hipStream_t s, const uint16_t *x, int m, int k,
+                                const uint32_t *wq, int n, const uint16_t *sc, const uint16_t *zr, int ng, int gpw,
+                                const uint16_t *bias, uint16_t *y) {
+  // > 64 KiB of dynamic LDS must be allowed per kernel (idempotent, cheap)
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void *>(w4a16_bf16_small_kernel<W, ONE, ZP>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
+    return MP_ERR_HIP;
+  hipLaunchKernelGGL((w4a16_bf16_small_kernel<W, ONE, ZP>), dim3(static_cast<unsigned>(blocks)), dim3(W * 64), lds, s,
+                     x, m, k, wq, n, sc, zr, ng, gpw, bias, y);
+  MP_CHECK_LAUNCH();
+  return MP_OK;
 }
 
 // Batched-kernel shape knobs (for measurements): MP_W4_BATCH_NT (column tiles per
@@ -1697,7 +1901,42 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
   if (x_dtype == MP_BF16) {
     // bf16: every dequantised weight rounded to bf16 as the reference's pseudo-quantized
     // weight is (bf16 keeps 8 significant bits: factoring the group scale out of the sum, as
-    // the fp16 streaming kernels do, would miss the reference by ~1e-3)
+    // the fp16 streaming kernels do, would miss the reference by ~1e-3).  1 to 16 rows with
+    // group 128: the matrix-core small-M kernel; otherwise the dequantising GEMM.
+    if (m <= 16 && group_size == 128 && k % 128 == 0 && mp_bf16_small() && mp_aligned(x, 16) &&
+        mp_aligned(w_packed, 16) && mp_aligned(scales, 2) && (zeros == nullptr || mp_aligned(zeros, 2)) &&
+        (bias == nullptr || mp_aligned(bias, 2))) {
+      const int64_t blocks = mp_cdiv(n, 16);
+      const int ng = static_cast<int>(k / 128);
+      const int w = mp_bf16_small_waves(blocks, ng);
+      const int gpw = (ng + w - 1) / w;
+      const size_t lds = mp_bf16_small_lds_for(w, gpw, m == 1);
+      if (lds <= kBf16SmallLds) {
+        const auto *xp = static_cast<const uint16_t *>(x);
+        const auto *wp = reinterpret_cast<const uint32_t *>(w_packed);
+        const auto *sp = static_cast<const uint16_t *>(scales);
+        const auto *zp = static_cast<const uint16_t *>(zeros);
+        const auto *bp = static_cast<const uint16_t *>(bias);
+        auto *yp = static_cast<uint16_t *>(y);
+        const bool one = m == 1;
+        const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
+        int rc = MP_ERR_ARG;
+#define MP_W4_BF16_W(W_)                                                                                        \
+  do {                                                                                                          \
+    if (one) rc = zp ? mp_bf16_small_launch<W_, true, true>(blocks, lds, s, xp, mi, ki, wp, ni, sp, zp, ng, gpw, bp, yp) \
+                     : mp_bf16_small_launch<W_, true, false>(blocks, lds, s, xp, mi, ki, wp, ni, sp, zp, ng, gpw, bp, yp); \
+    else rc = zp ? mp_bf16_small_launch<W_, false, true>(blocks, lds, s, xp, mi, ki, wp, ni, sp, zp, ng, gpw, bp, yp) \
+                 : mp_bf16_small_launch<W_, false, false>(blocks, lds, s, xp, mi, ki, wp, ni, sp, zp, ng, gpw, bp, yp); \
+  } while (0)
+        if (w == 1) MP_W4_BF16_W(1);
+        else if (w == 2) MP_W4_BF16_W(2);
+        else if (w == 4) MP_W4_BF16_W(4);
+        else if (w == 8) MP_W4_BF16_W(8);
+        else MP_W4_BF16_W(16);
+#undef MP_W4_BF16_W
+        return rc;
+      }
+    }
     mp_dq_args a{};
     a.dt = MP_BF16;
     a.a = x;

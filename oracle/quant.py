@@ -291,6 +291,21 @@ def dequant_w4_fp16(packed, scales, zeros, k, group_size):
     return _h(_f(_h(u - z)) * s)
 
 
+def dequant_w4_bf16(packed, scales, zeros, k, group_size):
+    """bf16 dequant ``R(R(u - z) * s)`` from the packed codes, the weight that AWQ's
+    ``pseudo_quantize_tensor`` returns in bf16 (``quantizer.py:95-105``: ``(q - zeros) * scales``,
+    each op rounded to bf16; ``R(u - z)`` is exact).  ``scales`` / ``zeros`` are bf16 bit patterns;
+    ``zeros=None`` is the symmetric export (stored nibble = int + 8, so z = 8).  Returns bf16 bits."""
+    u = unpack_uint4(packed, k).astype(np.float32)
+    n_rows = u.shape[0]
+    s = np.repeat(bf16_bits_to_f32(scales), group_size, axis=1)[:, :k]
+    if zeros is None:
+        z = np.full((n_rows, k), 8.0, np.float32)
+    else:
+        z = np.repeat(bf16_bits_to_f32(zeros), group_size, axis=1)[:, :k]
+    return f32_to_bf16_bits(_round_to(u - z, "bf16") * s)
+
+
 def dequant_w4_export_fp32(packed, scale, weight_shape):
     """``_dequantize_weight`` (``scripts/repro/evaluate_real_quant_export_dequant.py:46-64``):
     signed ints times the fp16 scale, in float32."""

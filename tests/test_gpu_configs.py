@@ -113,6 +113,36 @@ def test_w4a16_full_shape_symmetric_and_awq_agree_with_oracle(m, n, k):
         assert _rel(_np(y)[:, cols], _ref_cols(x, packed, s, z, cols, k)) <= 1e-3
 
 
+# bf16 (Llama-3 checkpoints are bf16): one-row and batched decode shapes of the 70B / 7B layers
+W4_BF16_FULL = [(1, 28672, 8192), (1, 8192, 28672), (16, 10240, 8192), (16, 8192, 28672), (1, 57344, 8192),
+                (1, 4096, 11008), (8, 22016, 4096), (16, 4096, 4096), (64, 28672, 8192)]
+
+
+@pytest.mark.parametrize("m,n,k", W4_BF16_FULL)
+def test_w4a16_bf16_full_shape_sampled(m, n, k):
+    """bf16 weight N(0, 0.02) quantized on the GPU in bf16 arithmetic (AWQ, asymmetric on most shapes
+    and the symmetric export on the rest); the oracle's bf16 dequant of the sampled rows' codes, then
+    F.linear (fp32 accumulation, one bf16 rounding).  Bar: rel. Frobenius error <= 1e-3."""
+    _say("w4a16 bf16 full", m, n, k)
+    ops = _ops()
+    zp = (m + n) % 2 == 0
+    g = torch.Generator(device=DEV).manual_seed(m + n + k)
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).bfloat16()
+    packed, s, z, _ = ops.w4_quantize_awq(w, 128, zp, return_deq=False)
+    del w
+    x = torch.randn(m, k, generator=torch.Generator(device=DEV).manual_seed(7), device=DEV).bfloat16()
+    bias = (torch.randn(n, generator=torch.Generator(device=DEV).manual_seed(3), device=DEV) * 0.1).bfloat16()
+    y = ops.w4a16_gemm(x, packed, s, z, 128, bias)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16
+    cols = _cols(n, seed=n)
+    idx = torch.as_tensor(cols, device=DEV)
+    bits = lambda t: _np(t.view(torch.int16)).view(np.uint16)  # noqa: E731
+    deq = O.dequant_w4_bf16(_np(packed[idx]), bits(s[idx]), None if z is None else bits(z[idx]), k, 128)
+    ref = O.bf16_bits_to_f32(O.w4a16_linear(bits(x), deq, bits(bias[idx]), dtype="bf16"))
+    assert _rel(_np(y.float())[:, cols], ref) <= 1e-3
+
+
 # fused gate/up: [2I, K] with the gate rows first; 70B (I = 28672) and 7B (I = 11008)
 SWIGLU_FULL = [(1, 28672, 8192), (16, 28672, 8192), (1, 11008, 4096), (8, 11008, 4096)]
 

@@ -296,12 +296,32 @@ def test_bf16_awq_and_fake_quant_match_reference():
     assert np.array_equal(d, _u16(EXT["awqb_deq"]))
     assert np.array_equal(s, _u16(EXT["awqb_s"])) and np.array_equal(z, _u16(EXT["awqb_z"]))
     assert c.min() >= 0 and c.max() <= 15
-    d2, _, _, _ = O.pseudo_quantize_tensor(w, 4, False, 128, dtype="bf16")
+    d2, s2, _, c2 = O.pseudo_quantize_tensor(w, 4, False, 128, dtype="bf16")
     assert np.array_equal(d2, _u16(EXT["awqb_sym_deq"]))
+    # the packed codes dequantize to the reference's bf16 weights bit for bit (both zero-point forms)
+    k = w.shape[1]
+    assert np.array_equal(O.dequant_w4_bf16(O.pack_uint4(c), s, z, k, 128), _u16(EXT["awqb_deq"]))
+    assert np.array_equal(O.dequant_w4_bf16(O.pack_int4_signed(c2), s2, None, k, 128), _u16(EXT["awqb_sym_deq"]))
     _, _, fx = O.quantize_activation_per_token_fake(_u16(EXT["sqb_x"]), 8, "bf16")
     assert np.array_equal(fx, _u16(EXT["sqb_x_fq"]))
     _, _, fw = O.quantize_weight_per_channel_fake(_u16(EXT["sqb_w"]), 8, "bf16")
     assert np.array_equal(fw, _u16(EXT["sqb_w_fq"]))
+
+
+def test_bf16_packed_dequant_matches_pseudo_quantize_on_random_groups():
+    """dequant_w4_bf16 of the packed codes equals pseudo_quantize_tensor's bf16 weight bit for bit on
+    random rows (every group its own scale / zero, wide scale range), and a planted mistake (the
+    product not rounded to bf16) does not."""
+    rng = np.random.default_rng(5)
+    w32 = (rng.standard_normal((24, 512)) * np.exp(rng.uniform(-6, 2, (24, 1)))).astype(np.float32)
+    w = O.f32_to_bf16_bits(w32)
+    for zp in (True, False):
+        d, s, z, c = O.pseudo_quantize_tensor(w, 4, zp, 128, dtype="bf16")
+        packed = O.pack_uint4(c) if zp else O.pack_int4_signed(c)
+        assert np.array_equal(O.dequant_w4_bf16(packed, s, z, 512, 128), d)
+    u = O.unpack_uint4(packed, 512).astype(np.float32)
+    unrounded = (u - 8.0) * np.repeat(O.bf16_bits_to_f32(s), 128, axis=1)
+    assert not np.array_equal(unrounded, O.bf16_bits_to_f32(d))
 
 
 @pytest.mark.parametrize("tag,dt", [("f16", "fp16"), ("bf16", "bf16")])
