@@ -18,7 +18,8 @@ stated in each ``sample``).
 
 ``--profile NAME`` runs one kernel mix for rocprofv3 (the commands in ``profiles/``):
 ``w4gemv`` (the headline loop), ``readfloor`` (one-launch reads of 8.9 MB, rotated),
-``w4shapes`` (M=16 and the 70B GEMV shapes), ``w8big`` (the M=4096 int8 GEMM), and
+``w4shapes`` (M=16 and the 70B GEMV shapes), ``w4bf16`` (the bf16 W4A16 legs), ``w4batch8`` (7B
+gate/up and down at M = 1 and 8), ``dec7b`` (the 7B decode step), ``w8big`` (the M=4096 int8 GEMM), and
 ``--traffic-probe`` the kernel mix of ``profiles/traffic.json``.
 """
 from __future__ import annotations
@@ -91,20 +92,21 @@ def _roof(bound, achieved, peak, unit, traffic=None):
             "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
-def _w4_copies(ops, n, k, copies, g=128):
+def _w4_copies(ops, n, k, copies, g=128, dtype=torch.float16):
     gen = torch.Generator(device="cuda").manual_seed(1)
-    w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).half()
+    w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).to(dtype)
     packed, s, z, _ = ops.w4_quantize_awq(w, g, True, return_deq=False)
     del w
     return [packed.clone() for _ in range(copies)], [s.clone() for _ in range(copies)], \
         [z.clone() for _ in range(copies)]
 
 
-def leg_w4a16(ops, m, n, k, steps, warmup, copies=64, g=128):
-    """W4A16 at M x K x N: one step = ``copies`` launches, each on its own weight copy."""
-    pk, sc, zr = _w4_copies(ops, n, k, copies, g)
+def leg_w4a16(ops, m, n, k, steps, warmup, copies=64, g=128, dtype=torch.float16):
+    """W4A16 at M x K x N: one step = ``copies`` launches, each on its own weight copy.  ``dtype``:
+    the activation / scale / zero / output dtype (bf16: weights quantized in bf16 arithmetic)."""
+    pk, sc, zr = _w4_copies(ops, n, k, copies, g, dtype)
     gx = torch.Generator(device="cuda").manual_seed(0)
-    x = torch.randn(m, k, generator=gx, device="cuda").half()
+    x = torch.randn(m, k, generator=gx, device="cuda").to(dtype)
     y = ops.w4a16_gemm(x, pk[0], sc[0], zr[0], g, None)
     ms_step = _time_graph(lambda i: ops.w4a16_gemm(x, pk[i], sc[i], zr[i], g, None), copies, steps, warmup)
     ms = ms_step / copies
@@ -112,7 +114,8 @@ def leg_w4a16(ops, m, n, k, steps, warmup, copies=64, g=128):
     gbs = nbytes / (ms * 1e-3) / 1e9
     del pk, sc, zr
     torch.cuda.empty_cache()
-    return {"m": m, "n": n, "k": k, "group": g, "ms_per_call": ms, "ms_per_step": ms_step,
+    return {"m": m, "n": n, "k": k, "group": g, "dtype": "u4*bf16->bf16" if dtype == torch.bfloat16 else "u4*f16->f16",
+            "ms_per_call": ms, "ms_per_step": ms_step,
             "bytes_per_call": nbytes, "tb_s": gbs / 1000.0, "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s"),
             "weight_copies": copies, "working_set_bytes": copies * (n * k // 2 + 2 * n * (k // g) * 2)}, y
 
@@ -309,6 +312,16 @@ def profile_mix(ops, name, steps):
             print(f"w4 m={m} n={n} k={k}: {ms / c * 1e3:.3f} us per launch")
             del pk, sc, zr
             torch.cuda.empty_cache()
+    elif name == "w4bf16":
+        # bf16 W4A16 (the matrix-core small-M kernel) at the bench's bf16 legs: M = 1 and 16 at
+        # 4096 x 4096 (64 rotated copies) and the 70B gate/up GEMV (8 copies)
+        for m, n, k, c in ((1, 4096, 4096, 64), (16, 4096, 4096, 64), (1, 28672, 8192, 8)):
+            pk, sc, zr = _w4_copies(ops, n, k, c, dtype=torch.bfloat16)
+            x = torch.randn(m, k, device="cuda").bfloat16()
+            ms = _time_graph(lambda i: ops.w4a16_gemm(x, pk[i], sc[i], zr[i], 128, None), c, steps, 3)
+            print(f"w4bf16 m={m} n={n} k={k}: {ms / c * 1e3:.3f} us per launch")
+            del pk, sc, zr
+            torch.cuda.empty_cache()
     elif name == "w4batch8":
         # the 7B gate/up (fused SiLU-up, N = 2 x 11008, K = 4096) and down (N = 4096, K = 11008)
         # linears at M = 1 (one-row GEMV) and M = 8 (batched kernel), 4 eager launches each
@@ -449,6 +462,13 @@ def main():
         for m, n, k in ((1, 28672, 8192), (1, 8192, 28672)):
             key = f"w4a16_m{m}_k{k}_n{n}"
             out_legs[key], _ = leg_w4a16(ops, m, n, k, small, max(1, warmup // 2), copies=8)
+            out_legs[key]["roofline"]["traffic"] = _traffic(key)
+        _log("leg w4a16 bf16")
+        for m, n, k in ((1, 4096, 4096), (16, 4096, 4096), (1, 28672, 8192)):
+            key = f"w4a16_bf16_m{m}_k{k}_n{n}"
+            cp = 64 if n * k <= 4096 * 4096 else 8
+            out_legs[key], _ = leg_w4a16(ops, m, n, k, steps if cp == 64 else small, max(1, warmup // 2), copies=cp,
+                                         dtype=torch.bfloat16)
             out_legs[key]["roofline"]["traffic"] = _traffic(key)
     if "w8" in legs:
         for m in (4096, 256, 16, 1):
