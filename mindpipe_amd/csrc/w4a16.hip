@@ -1417,7 +1417,7 @@ __device__ __forceinline__ uint4 w4_bf16x8(uint32_t w, float s, float s16, float
 //  * Scale / zero: before the first round the wave copies the (s, z) pairs of its 16 rows x gpw
 //    groups into LDS with coalesced loads (consecutive lanes, consecutive groups of a row); the
 //    rounds read one 32-bit pair per group.  Per-group 16-bit loads scattered over 16 rows cost
-//    more than the weight stream itself.
+//    more than the weight stream itself.  The copy's first batch shares round 0's round trip.
 //  * Weights: per group one 16-byte load per lane, words 4 g .. 4 g + 3 of row n's group (K 32 g ..
 //    32 g + 31 of the group); word j, dequantised by w4_bf16x8, is the B operand of MFMA j.
 //  * Activations: the A operand of MFMA j is x[token][32 g + 8 j .. + 7] of the group, in natural
@@ -1495,18 +1495,78 @@ __global__ __launch_bounds__(W * 64) void w4a16_bf16_small_kernel(
     }
   };
   if (nr > 0) {
-    // (s, z) pairs of the 16 rows x cnt groups, element e = row r * cnt + group c
-    for (int e = lane; e < 16 * cnt; e += 64) {
-      const int r = e / cnt, c = e - r * cnt;
+    // Prologue.  The wave's (s, z) pairs (16 cnt elements, element e = row r * cnt + group c) and, for one
+    // row, its activation slice (cnt chunks of 16 bytes per lane row) are copied into LDS.  The first
+    // batch -- four pair loads per lane and four chunk loads per lane group -- is issued before round 0's
+    // weights and stored after them, so one memory round trip covers the prologue and the first round;
+    // a load-then-store loop costs one round trip per iteration, and every wave of the grid sits in
+    // that prologue at once.  A wave with at least 16 groups fills every slot of the batch; shorter
+    // ranges skip the slots without data (wave-uniform).  Longer ranges take further batches.
+    const float rcp = 1.0f / static_cast<float>(cnt);  // (e + 0.5) / cnt rounds to the exact quotient
+    auto sz_load = [&](int e) {
+      const int ec = e < 16 * cnt ? e : 16 * cnt - 1;
+      const int r = static_cast<int>((static_cast<float>(ec) + 0.5f) * rcp), c = ec - r * cnt;
       const int rr = row0 + r < n_rows ? row0 + r : n_rows - 1;
       const int64_t gi = static_cast<int64_t>(rr) * n_groups + gb + c;
-      szw[r * szst + c] = static_cast<uint32_t>(sc[gi]) | (static_cast<uint32_t>(ZP ? zr[gi] : 0x4100u) << 16);
+      return static_cast<uint32_t>(sc[gi]) | (static_cast<uint32_t>(ZP ? zr[gi] : 0x4100u) << 16);
+    };
+    auto sz_store = [&](int e, uint32_t v) {
+      if (e < 16 * cnt) {
+        const int r = static_cast<int>((static_cast<float>(e) + 0.5f) * rcp), c = e - r * cnt;
+        szw[r * szst + c] = v;
+      }
+    };
+    auto x_load = [&](int c) {
+      const int cc = c < cnt ? c : cnt - 1;
+      return *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(gb + cc) * 128 + 8 * n);
+    };
+    uint32_t szv0[4];
+    uint4 xv0[4];
+    const bool fullb = cnt >= 16;
+    if (fullb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) szv0[i] = sz_load(lane + 64 * i);
+      if constexpr (ONE) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xv0[i] = x_load(g + 4 * i);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (64 * i < 16 * cnt) szv0[i] = sz_load(lane + 64 * i);
+      if constexpr (ONE) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * i < cnt) xv0[i] = x_load(g + 4 * i);
+      }
     }
     Round A, B;
     load(A, 0);
-    if constexpr (ONE) {  // the wave's activation slice: lane group g copies groups g, g + 4, ...
-      for (int c = g; c < cnt; c += 4)
-        xw[c * 16 + n] = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(gb + c) * 128 + 8 * n);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (fullb || 64 * i < 16 * cnt) sz_store(lane + 64 * i, szv0[i]);
+    if constexpr (ONE) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (g + 4 * i < cnt) xw[(g + 4 * i) * 16 + n] = xv0[i];
+    }
+    for (int e0 = 256; e0 < 16 * cnt; e0 += 256) {  // wave-uniform
+      uint32_t v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = sz_load(e0 + lane + 64 * i);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sz_store(e0 + lane + 64 * i, v[i]);
+    }
+    if constexpr (ONE) {
+      for (int c0 = 16; c0 < cnt; c0 += 16) {  // wave-uniform
+        uint4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = x_load(c0 + g + 4 * i);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (c0 + g + 4 * i < cnt) xw[(c0 + g + 4 * i) * 16 + n] = v[i];
+      }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes land before its reads
     __builtin_amdgcn_wave_barrier();
