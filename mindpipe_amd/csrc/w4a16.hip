@@ -11,6 +11,39 @@ namespace {
 
 constexpr uint32_t kMagic = 0x64006400u;  // fp16 1024.0 in both halves
 
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2_t mp_as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+
+typedef __bf16 bf8w_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf2w_t __attribute__((ext_vector_type(2)));
+
+// The eight weights of one packed word (K positions 0..7, natural order) as bf16 pairs, each
+// R_bf16((u - z) s): the reference's bf16 pseudo-quantized weight, (q - z) exact and one rounding of
+// the product (awq/quantize/quantizer.py:95-105 in bf16 arithmetic).  (w & 0x000F000F) | 0x64006400
+// is the fp16 pair (1024 + u0, 1024 + u4) and the 0x00F000F0 mask gives (1024 + 16 u1, 1024 + 16 u5).
+// Each v_fma_mix computes (1024 + u) s - (1024 + z) s, resp. (1024 + 16 u) (s / 16) - (64 + z) s,
+// in one fp32 rounding that is exact: both subtracted products are exact in fp32 (at most 19
+// significant bits) and so is the difference (u - z) s (at most 12).  v_cvt_pk_bf16_f32 then rounds
+// to nearest even once.
+__device__ __forceinline__ uint4 w4_bf16x8(uint32_t w, float s, float s16, float nce, float nco, uint32_t m0,
+                                           uint32_t m1, uint32_t magic) {
+  const uint32_t w8 = w >> 8;
+  const h2_t e0 = mp_as_h2((w & m0) | magic), o0 = mp_as_h2((w & m1) | magic);
+  const h2_t e1 = mp_as_h2((w8 & m0) | magic), o1 = mp_as_h2((w8 & m1) | magic);
+  const bf2w_t p0 = {static_cast<__bf16>(fmaf(static_cast<float>(e0[0]), s, nce)),
+                     static_cast<__bf16>(fmaf(static_cast<float>(o0[0]), s16, nco))};
+  const bf2w_t p1 = {static_cast<__bf16>(fmaf(static_cast<float>(e1[0]), s, nce)),
+                     static_cast<__bf16>(fmaf(static_cast<float>(o1[0]), s16, nco))};
+  const bf2w_t p2 = {static_cast<__bf16>(fmaf(static_cast<float>(e0[1]), s, nce)),
+                     static_cast<__bf16>(fmaf(static_cast<float>(o0[1]), s16, nco))};
+  const bf2w_t p3 = {static_cast<__bf16>(fmaf(static_cast<float>(e1[1]), s, nce)),
+                     static_cast<__bf16>(fmaf(static_cast<float>(o1[1]), s16, nco))};
+  return make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                    __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
+}
+
+
 // Eight nibbles of one packed word -> fp16 (1024 + u) in the order
 // [k0, k4, k1, k5, k2, k6, k3, k7]: the "or 1024" trick turns a 4-bit integer
 // into an fp16 bit pattern with one AND-OR per pair.
@@ -478,7 +511,12 @@ __global__ __launch_bounds__(512) void w4a16_decode_kernel(
 // join makes the compiler wait for every outstanding load).  Each block pair's
 // activation loads are issued before the next pair's weight prefetch, so a
 // compute step waits for its own data only.
-template <int MT, int NT, int S, bool ZP, bool SWI = false, bool XDB_ON = true>
+//
+// BF: bf16 activations, scales, zeros and output.  Every weight is rounded to bf16 as the reference's
+// pseudo-quantized weight is (w4_bf16x8, natural K order), so the activation pieces go to the MFMA
+// (f32_16x16x32_bf16) as they lie, the group scale is inside each weight and no sum against ones
+// is needed.  No SwiGLU form.
+template <int MT, int NT, int S, bool ZP, bool SWI = false, bool XDB_ON = true, bool BF = false>
 __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
@@ -518,8 +556,9 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   const int st_lo = (nst * wave) / S;
   const int nsteps = (nst * (wave + 1)) / S - st_lo;
   const int lo = st_lo * STEP;
-  uint32_t magic_v = kMagic, mask_v = 0x000F000Fu;
-  asm volatile("" : "+v"(magic_v), "+v"(mask_v));
+  static_assert(!(BF && SWI), "the bf16 form has no SwiGLU epilogue");
+  uint32_t magic_v = kMagic, mask_v = 0x000F000Fu, mask1_v = 0x00F000F0u;
+  asm volatile("" : "+v"(magic_v), "+v"(mask_v), "+v"(mask1_v));
   const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
 
   // buffer resources (the host checks that every size fits 32 bits)
@@ -596,6 +635,32 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
       for (int i = 0; i < XI; ++i) {
         const int r = 4 * i + (lane >> 4);
         xsw[r * 16 + ((lane & 15) ^ (r & 15))] = xbuf[u][i];
+      }
+      if constexpr (BF) {
+        uint4 ab[MT][4];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const int r = 16 * t + (lane & 15);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ab[t][q] = xsw[r * 16 + ((4 * kq + q) ^ (r & 15))];
+        }
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const float su = mp_bf2f(static_cast<uint16_t>(swd[j] >> (16 * u)));
+          const float zr_ = ZP ? mp_bf2f(static_cast<uint16_t>(zwd[j] >> (16 * u))) : 8.0f;
+          const float s16 = su * 0.0625f, nce = -((1024.f + zr_) * su), nco = -((64.f + zr_) * su);
+          const uint32_t wsel[4] = {w[u][j].x, w[u][j].y, w[u][j].z, w[u][j].w};
+          uint4 bq[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) bq[q] = w4_bf16x8(wsel[q], su, s16, nce, nco, mask_v, mask1_v, magic_v);
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8w_t, ab[t][q]),
+                                                                  __builtin_bit_cast(bf8w_t, bq[q]), acc[t][j], 0, 0, 0);
+        }
+        continue;
       }
       h8_t af[MT][4];
       f4_t cs[MT];
@@ -723,7 +788,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   for (int j = 0; j < NO; ++j) {
     int col = col0 + j * 16 + (lane & 15);
     col = col < n_out ? col : n_out - 1;
-    bg[j] = bias ? mp_h2f(bias[col]) : 0.f;
+    bg[j] = bias ? (BF ? mp_bf2f(bias[col]) : mp_h2f(bias[col])) : 0.f;
     bu[j] = (SWI && bias) ? mp_h2f(bias[n_out + col]) : 0.f;
   }
   auto emit = [&](int m, int j, float v, float u) {
@@ -737,7 +802,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
         y[static_cast<int64_t>(m) * n_out + col] = mp_swiglu_h(mp_rh(v), mp_rh(u));
       } else {
         if (bias) v += bg[j];
-        y[static_cast<int64_t>(m) * n_out + col] = mp_f2h(v);
+        y[static_cast<int64_t>(m) * n_out + col] = BF ? mp_f2bf(v) : mp_f2h(v);
       }
     }
   };
@@ -976,9 +1041,6 @@ __global__ void w4a16_simple_kernel(const uint16_t *__restrict__ x, int64_t m_ro
 // Scale / zero pairs of the R rows x 16 groups are loaded by one coalesced
 // load per 64 entries and handed to the lanes that use them by ds_bpermute.
 // The R per-lane partials are reduced across the wave by a halving butterfly.
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ h2_t mp_as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 
 // NRM: the activation row is h = RMSNorm(x + residual) * w, computed by every
 // workgroup in its prologue into LDS (the arithmetic of add_rmsnorm_quant_kernel
@@ -1379,34 +1441,6 @@ __global__ __launch_bounds__(W * 64) void w4a16_gemv_mfma_kernel(
   }
 }
 
-typedef __bf16 bf8w_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf2w_t __attribute__((ext_vector_type(2)));
-
-// The eight weights of one packed word (K positions 0..7, natural order) as bf16 pairs, each
-// R_bf16((u - z) s): the reference's bf16 pseudo-quantized weight, (q - z) exact and one rounding of
-// the product (awq/quantize/quantizer.py:95-105 in bf16 arithmetic).  (w & 0x000F000F) | 0x64006400
-// is the fp16 pair (1024 + u0, 1024 + u4) and the 0x00F000F0 mask gives (1024 + 16 u1, 1024 + 16 u5).
-// Each v_fma_mix computes (1024 + u) s - (1024 + z) s, resp. (1024 + 16 u) (s / 16) - (64 + z) s,
-// in one fp32 rounding that is exact: both subtracted products are exact in fp32 (at most 19
-// significant bits) and so is the difference (u - z) s (at most 12).  v_cvt_pk_bf16_f32 then rounds
-// to nearest even once.
-__device__ __forceinline__ uint4 w4_bf16x8(uint32_t w, float s, float s16, float nce, float nco, uint32_t m0,
-                                           uint32_t m1, uint32_t magic) {
-  const uint32_t w8 = w >> 8;
-  const h2_t e0 = mp_as_h2((w & m0) | magic), o0 = mp_as_h2((w & m1) | magic);
-  const h2_t e1 = mp_as_h2((w8 & m0) | magic), o1 = mp_as_h2((w8 & m1) | magic);
-  const bf2w_t p0 = {static_cast<__bf16>(fmaf(static_cast<float>(e0[0]), s, nce)),
-                     static_cast<__bf16>(fmaf(static_cast<float>(o0[0]), s16, nco))};
-  const bf2w_t p1 = {static_cast<__bf16>(fmaf(static_cast<float>(e1[0]), s, nce)),
-                     static_cast<__bf16>(fmaf(static_cast<float>(o1[0]), s16, nco))};
-  const bf2w_t p2 = {static_cast<__bf16>(fmaf(static_cast<float>(e0[1]), s, nce)),
-                     static_cast<__bf16>(fmaf(static_cast<float>(o0[1]), s16, nco))};
-  const bf2w_t p3 = {static_cast<__bf16>(fmaf(static_cast<float>(e1[1]), s, nce)),
-                     static_cast<__bf16>(fmaf(static_cast<float>(o1[1]), s16, nco))};
-  return make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
-                    __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
-}
-
 // bf16 W4A16 for 1 to 16 activation rows on the matrix cores (group size 128):
 // y[m][n] = sum_k x[m][k] R_bf16((u(n, k) - z(n, g)) s(n, g)) (+ bias[n]), F.linear on the
 // reference's bf16 pseudo-quantized weight (fp32 accumulation, one rounding of the output).
@@ -1627,9 +1661,19 @@ static bool mp_gemv_mfma() {
   return v;
 }
 
-// MP_W4_BF16_SMALL=0 routes bf16 calls of 1 to 16 rows to the dequantising GEMM (for measurements).
+// MP_W4_BF16_SMALL=0 routes bf16 calls of 1 to 64 rows to the dequantising GEMM (for measurements).
 static bool mp_bf16_small() {
   static const bool v = !(mp_knob("MP_W4_BF16_SMALL") && atoi(mp_knob("MP_W4_BF16_SMALL")) == 0);
+  return v;
+}
+
+// bf16 rows above which the batched kernel's bf16 form runs.  Default 1: measured against the small-M
+// kernel at 2 to 16 rows on the 7B / 70B decode shapes, the batched form is faster from 4 rows on (at 16
+// rows 6.0 against 8.0 us at 4096 x 4096, 38 against 66 us on the 70B gate/up GEMV) and at 2 rows on
+// 4096 x 4096 and the 70B GEMV (5.5 / 32.8 against 5.9 / 38.8 us), 5% slower at 2 rows on the 7B gate/up
+// and down projections.  MP_W4_BF16_BATCH_MIN_M overrides it, for measurements.
+static int mp_bf16_batch_min_m() {
+  static const int v = mp_knob("MP_W4_BF16_BATCH_MIN_M") ? atoi(mp_knob("MP_W4_BF16_BATCH_MIN_M")) : 1;
   return v;
 }
 
@@ -1948,6 +1992,75 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
   return MP_OK;
 }
 
+// Launch of the batched kernel (fp16, or BF: bf16) with the shape rules measured on the 7B / 70B
+// decode shapes; the caller has checked 2 <= m <= 64, K % 256 == 0, group 128, an even group count,
+// 16-byte alignment and the 32-bit buffer sizes.
+template <bool BF>
+static void mp_launch_w4_batch(hipStream_t s, const uint16_t *xp, int64_t m, int64_t k, const uint32_t *wp,
+                               int64_t n, const uint16_t *sp, const uint16_t *zp, int n_groups_i, const uint16_t *bp,
+                               uint16_t *yp) {
+  const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
+  const int nblk = ki / 128;
+  const int mt = BF && mp_batch_part_mt(m) > 2 ? 2 : mp_batch_part_mt(m);
+  const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
+  const bool xdb = mp_batch_xdb();
+  // column tiles per wave (measured on the 7B decode shapes, M = 8..64): one for N <= 4096
+  // (enough workgroups), four from N = 12288 (activation loads shared by more tiles); the
+  // 64-row tiling takes at most 2 (registers)
+  int nt = n <= 4096 ? 1 : (n >= 12288 && mt < 4 ? 4 : 2);
+  if (mp_batch_env(0) > 0) nt = mp_batch_env(0) >= 4 ? 4 : mp_batch_env(0);
+  const int smax = mt * nt >= 8 ? 4 : (mt * nt > 1 ? 8 : 16);  // register budget per wave count
+  const int64_t groups = mp_cdiv(n, 16 * nt);
+  const int nsteps = (nblk + 7) / 8;                 // 8-block steps (one scale vector each)
+  // waves splitting K, >= 1 step each, up to ~1024 waves (~2048 for one-tile waves of <= 16 rows,
+  // measured on the 7B down projection at M = 8: 11.6 -> 10.2 us)
+  const int64_t target = mp_batch_env(2) > 0 ? mp_batch_env(2) : (mt == 1 && nt == 1 ? 2048 : 1024);
+  const int64_t wgs = groups * parts;
+  int split = 1;
+  while (split < smax && wgs * split < target && nsteps / (split * 2) >= 1) split *= 2;
+  if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
+  const dim3 grid(static_cast<unsigned>(parts > 1 ? mp_cdiv(groups, 8) * 8 * parts : groups));
+  const int hv = parts;
+#define MP_W4_BATCH(MT_, NT_, S_)                                                                            \
+do {                                                                                                       \
+  if (zp && (xdb || MT_ != 1))                                                                             \
+    hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, false, true, BF>), grid, dim3(S_ * 64), 0, s, xp, \
+                       mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                    \
+  else if (xdb || MT_ != 1)                                                                                \
+    hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, false, true, BF>), grid, dim3(S_ * 64), 0, s, xp, \
+                       mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                    \
+  else if (zp)                                                                                             \
+    hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, false, false, BF>), grid, dim3(S_ * 64), 0, s, xp, \
+                       mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                    \
+  else                                                                                                     \
+    hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, false, false, BF>), grid, dim3(S_ * 64), 0, s, xp, \
+                       mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                    \
+} while (0)
+#define MP_W4_BATCH_S(MT_, NT_)                    \
+do {                                             \
+  if (split == 1) MP_W4_BATCH(MT_, NT_, 1);      \
+  else if (split == 2) MP_W4_BATCH(MT_, NT_, 2); \
+  else if (split == 4) MP_W4_BATCH(MT_, NT_, 4); \
+  else if (split == 8 || MT_ * NT_ > 1) MP_W4_BATCH(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : 8)); \
+  else MP_W4_BATCH(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : (MT_ * NT_ > 1 ? 8 : 16))); \
+} while (0)
+  if (mt == 1) {
+    if (nt == 1) MP_W4_BATCH_S(1, 1);
+    else if (nt == 2) MP_W4_BATCH_S(1, 2);
+    else MP_W4_BATCH_S(1, 4);
+  } else if (mt == 2) {
+    if (nt == 1) MP_W4_BATCH_S(2, 1);
+    else if (nt == 2) MP_W4_BATCH_S(2, 2);
+    else MP_W4_BATCH_S(2, 4);
+  } else if constexpr (!BF) {  // the bf16 form takes 16- and 32-row parts only
+    if (nt == 1) MP_W4_BATCH_S(4, 1);
+    else if (nt == 2) MP_W4_BATCH_S(4, 2);
+    else MP_W4_BATCH_S(4, 4);
+  }
+#undef MP_W4_BATCH_S
+#undef MP_W4_BATCH
+}
+
 extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n,
                              const void *scales, const void *zeros, int group_size, const void *bias,
                              void *y, int x_dtype, mp_stream_t stream) {
@@ -1961,8 +2074,21 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
   if (x_dtype == MP_BF16) {
     // bf16: every dequantised weight rounded to bf16 as the reference's pseudo-quantized
     // weight is (bf16 keeps 8 significant bits: factoring the group scale out of the sum, as
-    // the fp16 streaming kernels do, would miss the reference by ~1e-3).  1 to 16 rows with
-    // group 128: the matrix-core small-M kernel; otherwise the dequantising GEMM.
+    // the fp16 streaming kernels do, would miss the reference by ~1e-3).  Group 128: the batched
+    // kernel's bf16 form for 2 to 64 rows (activation loads shared by column tiles; K % 256 == 0, an
+    // even group count), the matrix-core small-M kernel for one row and the other shapes of up to 16
+    // rows; otherwise the dequantising GEMM.
+    if (m > mp_bf16_batch_min_m() && m <= 64 && mp_bf16_small() && k % 256 == 0 && group_size == 128 && ((k / 128) % 2) == 0 &&
+        mp_aligned(x, 16) && mp_aligned(w_packed, 16) && mp_aligned(scales, 4) &&
+        (zeros == nullptr || mp_aligned(zeros, 4)) && n * (k / 2) < (int64_t(1) << 32) &&
+        m * k * 2 < (int64_t(1) << 32)) {
+      mp_launch_w4_batch<true>(s, static_cast<const uint16_t *>(x), m, k, reinterpret_cast<const uint32_t *>(w_packed),
+                               n, static_cast<const uint16_t *>(scales), static_cast<const uint16_t *>(zeros),
+                               static_cast<int>(k / group_size), static_cast<const uint16_t *>(bias),
+                               static_cast<uint16_t *>(y));
+      MP_CHECK_LAUNCH();
+      return MP_OK;
+    }
     if (m <= 16 && group_size == 128 && k % 128 == 0 && mp_bf16_small() && mp_aligned(x, 16) &&
         mp_aligned(w_packed, 16) && mp_aligned(scales, 2) && (zeros == nullptr || mp_aligned(zeros, 2)) &&
         (bias == nullptr || mp_aligned(bias, 2))) {
@@ -2102,66 +2228,7 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
 #undef MP_W4_GEMV
   } else if (m > batch_min_m && batch_shape && m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 &&
       aligned && n * (k / 2) < (int64_t(1) << 32) && m * k * 2 < (int64_t(1) << 32)) {
-    const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
-    const int nblk = ki / 128;
-    const int mt = mp_batch_part_mt(m);
-    const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
-    const bool xdb = mp_batch_xdb();
-    // column tiles per wave (measured on the 7B decode shapes, M = 8..64): one for N <= 4096
-    // (enough workgroups), four from N = 12288 (activation loads shared by more tiles); the
-    // 64-row tiling takes at most 2 (registers)
-    int nt = n <= 4096 ? 1 : (n >= 12288 && mt < 4 ? 4 : 2);
-    if (mp_batch_env(0) > 0) nt = mp_batch_env(0) >= 4 ? 4 : mp_batch_env(0);
-    const int smax = mt * nt >= 8 ? 4 : (mt * nt > 1 ? 8 : 16);  // register budget per wave count
-    const int64_t groups = mp_cdiv(n, 16 * nt);
-    const int nsteps = (nblk + 7) / 8;                 // 8-block steps (one scale vector each)
-    // waves splitting K, >= 1 step each, up to ~1024 waves (~2048 for one-tile waves of <= 16 rows,
-    // measured on the 7B down projection at M = 8: 11.6 -> 10.2 us)
-    const int64_t target = mp_batch_env(2) > 0 ? mp_batch_env(2) : (mt == 1 && nt == 1 ? 2048 : 1024);
-    const int64_t wgs = groups * parts;
-    int split = 1;
-    while (split < smax && wgs * split < target && nsteps / (split * 2) >= 1) split *= 2;
-    if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
-    const dim3 grid(static_cast<unsigned>(parts > 1 ? mp_cdiv(groups, 8) * 8 * parts : groups));
-    const int hv = parts;
-#define MP_W4_BATCH(MT_, NT_, S_)                                                                            \
-  do {                                                                                                       \
-    if (zp && (xdb || MT_ != 1))                                                                             \
-      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, wp, \
-                         ni, sp, zp, n_groups_i, bp, yp, hv);                                                \
-    else if (xdb || MT_ != 1)                                                                                \
-      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, wp, \
-                         ni, sp, zp, n_groups_i, bp, yp, hv);                                                \
-    else if (zp)                                                                                             \
-      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, false, false>), grid, dim3(S_ * 64), 0, s, xp,  \
-                         mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                    \
-    else                                                                                                     \
-      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, false, false>), grid, dim3(S_ * 64), 0, s, xp, \
-                         mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                    \
-  } while (0)
-#define MP_W4_BATCH_S(MT_, NT_)                    \
-  do {                                             \
-    if (split == 1) MP_W4_BATCH(MT_, NT_, 1);      \
-    else if (split == 2) MP_W4_BATCH(MT_, NT_, 2); \
-    else if (split == 4) MP_W4_BATCH(MT_, NT_, 4); \
-    else if (split == 8 || MT_ * NT_ > 1) MP_W4_BATCH(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : 8)); \
-    else MP_W4_BATCH(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : (MT_ * NT_ > 1 ? 8 : 16))); \
-  } while (0)
-    if (mt == 1) {
-      if (nt == 1) MP_W4_BATCH_S(1, 1);
-      else if (nt == 2) MP_W4_BATCH_S(1, 2);
-      else MP_W4_BATCH_S(1, 4);
-    } else if (mt == 2) {
-      if (nt == 1) MP_W4_BATCH_S(2, 1);
-      else if (nt == 2) MP_W4_BATCH_S(2, 2);
-      else MP_W4_BATCH_S(2, 4);
-    } else {
-      if (nt == 1) MP_W4_BATCH_S(4, 1);
-      else if (nt == 2) MP_W4_BATCH_S(4, 2);
-      else MP_W4_BATCH_S(4, 4);
-    }
-#undef MP_W4_BATCH_S
-#undef MP_W4_BATCH
+    mp_launch_w4_batch<false>(s, xp, m, k, wp, n, sp, zp, n_groups_i, bp, yp);
   } else if (m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {
     const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
     const int nblk = ki / 128;

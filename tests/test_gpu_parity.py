@@ -203,12 +203,16 @@ def test_awq_quantize_bf16_matches_reference():
 # several, ragged N, one to sixteen waves per row block, odd group counts (K = 640: five groups, a
 # round with one group; K = 11008: 86 groups over sixteen waves, the last one idle) and a long K
 # (K = 30720: 240 groups; K = 36864 / 40064: 18 / 20 groups per wave, so the prologue's first batch is
-# full and a second one follows, and the last wave of K = 40064 has 13).  One row past its LDS bound
-# (K = 40960), above 16 rows or with another group size: the dequantising MFMA GEMM, tiled (K % 64 == 0)
-# incl. ragged M / N, and the any-K kernel.
+# full and a second one follows, and the last wave of K = 40064 has 13).  2 to 64 rows with K % 256 == 0
+# and an even group count: the batched kernel's bf16 form (16- and 32-row parts, one to four column
+# tiles per wave, ragged N, 86 groups); other K with up to 16 rows (640, 1152, 40064) stay on the small-M
+# kernel.  One row past its LDS bound (K = 40960), above 64 rows or with another group size: the
+# dequantising MFMA GEMM, tiled (K % 64 == 0) incl. ragged M / N, and the any-K kernel.
 W4_BF16_CASES = [(1, 4096, 4096), (16, 4096, 4096), (3, 1000, 1024), (1, 17, 128), (7, 33, 640),
                  (1, 4096, 11008), (12, 300, 2048), (16, 520, 11008), (9, 2048, 8192), (1, 2050, 2048),
                  (1, 300, 30720), (4, 64, 30720), (1, 37, 36864), (2, 100, 40064), (1, 48, 40960),
+                 (24, 4096, 4096), (33, 12288, 4096), (40, 520, 2048), (48, 4096, 11008), (64, 8200, 1024),
+                 (16, 300, 1152), (2, 22016, 4096),
                  (17, 96, 512), (64, 384, 512), (200, 320, 1024), (300, 12288, 4096), (5, 256, 8192),
                  (2, 100, 96)]
 
