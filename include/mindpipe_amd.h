@@ -308,8 +308,9 @@ int mp_decode_rope_attention(const void *qkv, int64_t batch, int nh, int kvh, in
  * rules.  No counterpart in the reference. */
 int mp_argmax_rows(const void *x, int64_t rows, int64_t n, int64_t *idx, mp_stream_t stream);
 
-/* act [rows, I] = round(round(silu(gate)) * up) of gate_up [rows, 2I] (gate | up), fp16. */
-int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, mp_stream_t stream);
+/* act [rows, I] = round(round(silu(gate)) * up) of gate_up [rows, 2I] (gate | up), in dtype
+ * (MP_F16 / MP_BF16; every round is to that dtype). */
+int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, int dtype, mp_stream_t stream);
 
 /* ---- SmoothQuant smoothing (offline) ----
  * colmax [k] fp32 = max(colmax, max over rows |x[r, :]|) for x [rows, k] row-major (fp16 / bf16 /

@@ -38,7 +38,7 @@ SIGNATURES = {
                                    _vp]),
     "mp_decode_rope_attention": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _vp, _i32, C.c_float,
                                         _vp, _vp, _sz, _vp]),
-    "mp_silu_mul": (_i32, [_vp, _i64, _i64, _vp, _vp]),
+    "mp_silu_mul": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
     "mp_argmax_rows": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "mp_w8a8_gemm_quant_out_workspace_bytes": (_sz, [_i64, _i64]),
     "mp_w8a8_gemm_quant_out": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp,

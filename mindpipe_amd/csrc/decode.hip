@@ -673,12 +673,14 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const uint16_t *__res
 
 // ---------------------------------------------------------------- SiLU * up
 // gu [B, 2I] (gate | up) -> act [B, I] = round(round(silu(gate)) * up).
+template <bool BF>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ gu, int inter, int64_t total,
                                                        uint16_t *__restrict__ act) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= total) return;
   const int64_t b = i / inter, c = i % inter;
-  act[i] = mp_swiglu_h(mp_h2f(gu[b * 2 * inter + c]), mp_h2f(gu[b * 2 * inter + inter + c]));
+  const uint16_t g = gu[b * 2 * inter + c], u = gu[b * 2 * inter + inter + c];
+  act[i] = BF ? mp_swiglu_bf(mp_bf2f(g), mp_bf2f(u)) : mp_swiglu_h(mp_h2f(g), mp_h2f(u));
 }
 
 }  // namespace
@@ -815,15 +817,23 @@ extern "C" int mp_argmax_rows(const void *x, int64_t rows, int64_t n, int64_t *i
   return MP_OK;
 }
 
-extern "C" int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, mp_stream_t stream) {
+extern "C" int mp_silu_mul(const void *gate_up, int64_t rows, int64_t inter, void *act, int dtype,
+                           mp_stream_t stream) {
   if (!gate_up || !act) return MP_ERR_ARG;
+  if (dtype != MP_F16 && dtype != MP_BF16) return MP_ERR_DTYPE;
   if (rows < 0 || inter <= 0 || inter > INT32_MAX) return MP_ERR_SHAPE;
   const int64_t total = rows * inter;
   if (total == 0) return MP_OK;
   if (mp_cdiv(total, 256) > UINT32_MAX) return MP_ERR_SHAPE;
-  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(mp_cdiv(total, 256))), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t *>(gate_up),
-                     static_cast<int>(inter), total, static_cast<uint16_t *>(act));
+  const dim3 grid(static_cast<unsigned>(mp_cdiv(total, 256)));
+  const auto *gp = static_cast<const uint16_t *>(gate_up);
+  auto *ap = static_cast<uint16_t *>(act);
+  if (dtype == MP_BF16)
+    hipLaunchKernelGGL(silu_mul_kernel<true>, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), gp,
+                       static_cast<int>(inter), total, ap);
+  else
+    hipLaunchKernelGGL(silu_mul_kernel<false>, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), gp,
+                       static_cast<int>(inter), total, ap);
   MP_CHECK_LAUNCH();
   return MP_OK;
 }

@@ -140,6 +140,12 @@ __device__ __forceinline__ uint16_t mp_swiglu_h(float g, float u) {
   return mp_f2h(sg * u);
 }
 
+// The same for bf16 values: round(round(silu(g)) * u) in bf16.
+__device__ __forceinline__ uint16_t mp_swiglu_bf(float g, float u) {
+  const float sg = mp_rbf(g / (1.0f + expf(-g)));
+  return mp_f2bf(sg * u);
+}
+
 // SwiGLU of the grouped GEMM1 epilogue, h = silu(g) * u for the fp32 products g, u.  mode
 // kRoundNone keeps fp32 (the runtime rule); kRoundF16 / kRoundBF16 round as the reference's
 // fake path (fake_quant.py:184-185): gate and up as F.linear's output, silu(gate), and the

@@ -515,7 +515,7 @@ __global__ __launch_bounds__(512) void w4a16_decode_kernel(
 // BF: bf16 activations, scales, zeros and output.  Every weight is rounded to bf16 as the reference's
 // pseudo-quantized weight is (w4_bf16x8, natural K order), so the activation pieces go to the MFMA
 // (f32_16x16x32_bf16) as they lie, the group scale is inside each weight and no sum against ones
-// is needed.  No SwiGLU form.
+// is needed.  The SwiGLU form rounds gate, up, silu and the product to bf16.
 template <int MT, int NT, int S, bool ZP, bool SWI = false, bool XDB_ON = true, bool BF = false>
 __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
@@ -556,7 +556,6 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   const int st_lo = (nst * wave) / S;
   const int nsteps = (nst * (wave + 1)) / S - st_lo;
   const int lo = st_lo * STEP;
-  static_assert(!(BF && SWI), "the bf16 form has no SwiGLU epilogue");
   uint32_t magic_v = kMagic, mask_v = 0x000F000Fu, mask1_v = 0x00F000F0u;
   asm volatile("" : "+v"(magic_v), "+v"(mask_v), "+v"(mask1_v));
   const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
@@ -789,7 +788,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     int col = col0 + j * 16 + (lane & 15);
     col = col < n_out ? col : n_out - 1;
     bg[j] = bias ? (BF ? mp_bf2f(bias[col]) : mp_h2f(bias[col])) : 0.f;
-    bu[j] = (SWI && bias) ? mp_h2f(bias[n_out + col]) : 0.f;
+    bu[j] = (SWI && bias) ? (BF ? mp_bf2f(bias[n_out + col]) : mp_h2f(bias[n_out + col])) : 0.f;
   }
   auto emit = [&](int m, int j, float v, float u) {
     const int col = col0 + j * 16 + (lane & 15);
@@ -799,7 +798,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
           v += bg[j];
           u += bu[j];
         }
-        y[static_cast<int64_t>(m) * n_out + col] = mp_swiglu_h(mp_rh(v), mp_rh(u));
+        y[static_cast<int64_t>(m) * n_out + col] = BF ? mp_swiglu_bf(mp_rbf(v), mp_rbf(u)) : mp_swiglu_h(mp_rh(v), mp_rh(u));
       } else {
         if (bias) v += bg[j];
         y[static_cast<int64_t>(m) * n_out + col] = BF ? mp_f2bf(v) : mp_f2h(v);
@@ -1883,10 +1882,73 @@ extern "C" int mp_w4a16_gemv_rmsnorm(const void *x, const void *residual, const 
   return MP_OK;
 }
 
+// Launch of the batched kernel's SwiGLU form (fp16, or BF: bf16): NT/2 gate tiles paired with NT/2 up
+// tiles per wave.  The caller has checked 1 <= m <= 64, K % 256 == 0, group 128, an even group count,
+// the alignments and the 32-bit buffer sizes.
+template <bool BF>
+static void mp_launch_w4_batch_swiglu(hipStream_t s, const uint16_t *xp, int64_t m, int64_t k, const uint32_t *wp,
+                                      int64_t n2, const uint16_t *sp, const uint16_t *zp, int n_groups,
+                                      const uint16_t *bp, uint16_t *yp) {
+  const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n2);
+  const int64_t half = n2 / 2;
+  const int mt = BF && mp_batch_part_mt(m) > 2 ? 2 : mp_batch_part_mt(m);
+  const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
+  const bool xdb = mp_batch_xdb();
+  // column tiles per wave: 4 for 17..32 rows from I = 8192, else 2 (<= 16 rows: measured on the
+  // 7B gate/up at M = 8, 17.4 -> 16.3 us; the 64-row tiling: registers)
+  int nt = half >= 8192 && mt == 2 ? 4 : 2;
+  if (mp_batch_env(0) >= 2) nt = mp_batch_env(0) >= 4 ? 4 : 2;
+  const int smax = mt * nt >= 8 ? 4 : 8;
+  const int nblk = ki / 128;
+  const int nsteps = (nblk + 7) / 8;
+  const int64_t groups = mp_cdiv(half, 16 * (nt / 2));
+  const int64_t wgs = groups * parts;
+  int split = 1;
+  while (split < smax && wgs * split < (mp_batch_env(2) > 0 ? mp_batch_env(2) : 1024) && nsteps / (split * 2) >= 1)
+    split *= 2;
+  if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
+  const dim3 grid(static_cast<unsigned>(parts > 1 ? mp_cdiv(groups, 8) * 8 * parts : groups));
+  const int hv = parts;
+#define MP_W4_BSWI(MT_, NT_, S_)                                                                              \
+  do {                                                                                                       \
+    if (zp && (xdb || MT_ != 1))                                                                             \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, true, true, BF>), grid, dim3(S_ * 64), 0, s, xp, mi, ki,  \
+                         wp, ni, sp, zp, n_groups, bp, yp, hv);                                              \
+    else if (xdb || MT_ != 1)                                                                                \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, true, true, BF>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, \
+                         wp, ni, sp, zp, n_groups, bp, yp, hv);                                              \
+    else if (zp)                                                                                             \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, true, false, BF>), grid, dim3(S_ * 64), 0, s, xp, mi, \
+                         ki, wp, ni, sp, zp, n_groups, bp, yp, hv);                                          \
+    else                                                                                                     \
+      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, true, false, BF>), grid, dim3(S_ * 64), 0, s, xp,   \
+                         mi, ki, wp, ni, sp, zp, n_groups, bp, yp, hv);                                      \
+  } while (0)
+#define MP_W4_BSWI_S(MT_, NT_)                                                  \
+  do {                                                                          \
+    if (split == 1) MP_W4_BSWI(MT_, NT_, 1);                                    \
+    else if (split == 2) MP_W4_BSWI(MT_, NT_, 2);                               \
+    else if (split == 4) MP_W4_BSWI(MT_, NT_, 4);                               \
+    else MP_W4_BSWI(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : 8));                        \
+  } while (0)
+  if (mt == 1) {
+    if (nt == 2) MP_W4_BSWI_S(1, 2);
+    else MP_W4_BSWI_S(1, 4);
+  } else if (mt == 2) {
+    if (nt == 2) MP_W4_BSWI_S(2, 2);
+    else MP_W4_BSWI_S(2, 4);
+  } else if constexpr (!BF) {  // the bf16 form takes 16- and 32-row parts only
+    if (nt == 2) MP_W4_BSWI_S(4, 2);
+    else MP_W4_BSWI_S(4, 4);
+  }
+#undef MP_W4_BSWI_S
+#undef MP_W4_BSWI
+}
+
 extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n2,
                                     const void *scales, const void *zeros, int group_size, const void *bias,
                                     void *act, int x_dtype, mp_stream_t stream) {
-  if (x_dtype != MP_F16) return MP_ERR_DTYPE;
+  if (x_dtype != MP_F16 && x_dtype != MP_BF16) return MP_ERR_DTYPE;
   if (m < 0 || n2 <= 0 || (n2 & 1) || k <= 0 || group_size != 128 || k % 256 != 0) return MP_ERR_SHAPE;
   if (m == 0) return MP_OK;
   if (!x || !w_packed || !scales || !act) return MP_ERR_ARG;
@@ -1904,9 +1966,10 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
   const auto *zp = static_cast<const uint16_t *>(zeros);
   const auto *bp = static_cast<const uint16_t *>(bias);
   auto *yp = static_cast<uint16_t *>(act);
-  const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n2);
+  const int ki = static_cast<int>(k), ni = static_cast<int>(n2);
   const int64_t half = n2 / 2;
-  if (m == 1) {
+  // one row, fp16: the VALU GEMV's SwiGLU form; otherwise the batched kernel's
+  if (m == 1 && x_dtype == MP_F16) {
     // two gate rows and the matching two up rows per wave; chunk / split choice as the GEMV
     const int nch = (ki + 2047) / 2048;
     int c = 1, sk = 1;
@@ -1935,59 +1998,10 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
     MP_CHECK_LAUNCH();
     return MP_OK;
   }
-  // batched kernel: NT/2 gate tiles paired with NT/2 up tiles per wave
-  const int mt = mp_batch_part_mt(m);
-  const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
-  const bool xdb = mp_batch_xdb();
-  // column tiles per wave: 4 for 17..32 rows from I = 8192, else 2 (<= 16 rows: measured on the
-  // 7B gate/up at M = 8, 17.4 -> 16.3 us; the 64-row tiling: registers)
-  int nt = half >= 8192 && mt == 2 ? 4 : 2;
-  if (mp_batch_env(0) >= 2) nt = mp_batch_env(0) >= 4 ? 4 : 2;
-  const int smax = mt * nt >= 8 ? 4 : 8;
-  const int nblk = ki / 128;
-  const int nsteps = (nblk + 7) / 8;
-  const int64_t groups = mp_cdiv(half, 16 * (nt / 2));
-  const int64_t wgs = groups * parts;
-  int split = 1;
-  while (split < smax && wgs * split < (mp_batch_env(2) > 0 ? mp_batch_env(2) : 1024) && nsteps / (split * 2) >= 1)
-    split *= 2;
-  if (mp_batch_env(1) > 0) split = mp_batch_env(1) < smax ? mp_batch_env(1) : smax;
-  const dim3 grid(static_cast<unsigned>(parts > 1 ? mp_cdiv(groups, 8) * 8 * parts : groups));
-  const int hv = parts;
-#define MP_W4_BSWI(MT_, NT_, S_)                                                                              \
-  do {                                                                                                       \
-    if (zp && (xdb || MT_ != 1))                                                                             \
-      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki,  \
-                         wp, ni, sp, zp, n_groups, bp, yp, hv);                                              \
-    else if (xdb || MT_ != 1)                                                                                \
-      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, true>), grid, dim3(S_ * 64), 0, s, xp, mi, ki, \
-                         wp, ni, sp, zp, n_groups, bp, yp, hv);                                              \
-    else if (zp)                                                                                             \
-      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, true, true, false>), grid, dim3(S_ * 64), 0, s, xp, mi, \
-                         ki, wp, ni, sp, zp, n_groups, bp, yp, hv);                                          \
-    else                                                                                                     \
-      hipLaunchKernelGGL((w4a16_batch_kernel<MT_, NT_, S_, false, true, false>), grid, dim3(S_ * 64), 0, s, xp,   \
-                         mi, ki, wp, ni, sp, zp, n_groups, bp, yp, hv);                                      \
-  } while (0)
-#define MP_W4_BSWI_S(MT_, NT_)                                                  \
-  do {                                                                          \
-    if (split == 1) MP_W4_BSWI(MT_, NT_, 1);                                    \
-    else if (split == 2) MP_W4_BSWI(MT_, NT_, 2);                               \
-    else if (split == 4) MP_W4_BSWI(MT_, NT_, 4);                               \
-    else MP_W4_BSWI(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : 8));                        \
-  } while (0)
-  if (mt == 1) {
-    if (nt == 2) MP_W4_BSWI_S(1, 2);
-    else MP_W4_BSWI_S(1, 4);
-  } else if (mt == 2) {
-    if (nt == 2) MP_W4_BSWI_S(2, 2);
-    else MP_W4_BSWI_S(2, 4);
-  } else {
-    if (nt == 2) MP_W4_BSWI_S(4, 2);
-    else MP_W4_BSWI_S(4, 4);
-  }
-#undef MP_W4_BSWI_S
-#undef MP_W4_BSWI
+  if (x_dtype == MP_BF16)
+    mp_launch_w4_batch_swiglu<true>(s, xp, m, k, wp, n2, sp, zp, n_groups, bp, yp);
+  else
+    mp_launch_w4_batch_swiglu<false>(s, xp, m, k, wp, n2, sp, zp, n_groups, bp, yp);
   MP_CHECK_LAUNCH();
   return MP_OK;
 }

@@ -597,29 +597,31 @@ def group_offsets_from_list(group_list: torch.Tensor, group_list_type: int) -> t
 def w4a16_gemm_swiglu(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor],
                       group_size: int, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``silu(G) * U`` with ``[G | U] = X . dequant(W)^T (+ bias)`` for the fused gate/up weight
-    ``w_packed [2I, K/8]`` (gate rows first): ``[..., I]`` fp16, rounded as ``silu_mul`` of the
-    ``w4a16_gemm`` output.  One launch for M <= 64 (group 128, K % 256 == 0); otherwise the two
-    launches."""
+    ``w_packed [2I, K/8]`` (gate rows first): ``[..., I]`` in ``x``'s dtype (fp16 or bf16), rounded as
+    ``silu_mul`` of the ``w4a16_gemm`` output.  One launch for M <= 64 (group 128, K % 256 == 0);
+    otherwise the two launches."""
     k = x.shape[-1]
     n2 = w_packed.shape[0]
     x2 = x.reshape(-1, k)
     m = x2.shape[0]
     if m > 64 or group_size != 128 or k % 256 or n2 % 2:
         return silu_mul(w4a16_gemm(x2, w_packed, scales, zeros, group_size, bias)).reshape(*x.shape[:-1], n2 // 2)
-    _need(x, "x", torch.float16)
+    _need(x, "x", (torch.float16, torch.bfloat16))
     _need(w_packed, "w_packed", torch.int32, 2)
-    _need(scales, "scales", torch.float16, 2)
+    _need(scales, "scales", x.dtype, 2)
     if w_packed.shape[1] * 8 != k or scales.shape != (n2, k // group_size):
         raise RuntimeError(f"w_packed {tuple(w_packed.shape)} / scales {tuple(scales.shape)} do not match K={k}")
-    if zeros is not None and zeros.shape != scales.shape:
-        raise RuntimeError("zeros must have the shape of scales")
+    if zeros is not None and (zeros.shape != scales.shape or zeros.dtype != x.dtype):
+        raise RuntimeError("zeros must have the shape and dtype of scales")
     if bias is not None and bias.shape != (n2,):
         raise RuntimeError("bias must be [2I]")
-    act = torch.empty((m, n2 // 2), dtype=torch.float16, device=x.device)
+    if bias is not None and bias.dtype != x.dtype:
+        raise RuntimeError("bias must have the activation dtype")
+    act = torch.empty((m, n2 // 2), dtype=x.dtype, device=x.device)
     with _dev(x):
         _lib.check(_lib.load().mp_w4a16_gemm_swiglu(
             x2.data_ptr(), m, k, w_packed.data_ptr(), n2, scales.data_ptr(), _ptr(zeros), group_size,
-            _ptr(bias), act.data_ptr(), MP_F16, _stream()), "mp_w4a16_gemm_swiglu")
+            _ptr(bias), act.data_ptr(), _DT[x.dtype], _stream()), "mp_w4a16_gemm_swiglu")
     return act.reshape(*x.shape[:-1], n2 // 2)
 
 
@@ -769,14 +771,15 @@ def argmax_rows(x: torch.Tensor) -> torch.Tensor:
 
 
 def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``round(round(silu(gate)) * up)`` of ``gate_up [B, 2I]`` (gate | up), fp16."""
-    _need(gate_up, "gate_up", torch.float16, 2)
+    """``round(round(silu(gate)) * up)`` of ``gate_up [B, 2I]`` (gate | up), fp16 or bf16 (every round
+    to that dtype)."""
+    _need(gate_up, "gate_up", (torch.float16, torch.bfloat16), 2)
     rows, two_i = gate_up.shape
     if out is None:
-        out = torch.empty((rows, two_i // 2), dtype=torch.float16, device=gate_up.device)
+        out = torch.empty((rows, two_i // 2), dtype=gate_up.dtype, device=gate_up.device)
     with _dev(gate_up):
-        _lib.check(_lib.load().mp_silu_mul(gate_up.data_ptr(), rows, two_i // 2, out.data_ptr(), _stream()),
-                   "mp_silu_mul")
+        _lib.check(_lib.load().mp_silu_mul(gate_up.data_ptr(), rows, two_i // 2, out.data_ptr(), _DT[gate_up.dtype],
+                                           _stream()), "mp_silu_mul")
     return out
 
 

@@ -168,6 +168,18 @@ def test_silu_mul_within_one_ulp():
     assert int(d.max()) <= 1 and float((d == 0).float().mean()) >= 0.99
 
 
+def test_silu_mul_bf16_within_one_ulp():
+    """bf16 silu_mul against torch's bf16 ops (silu in fp32 rounded to bf16, the product rounded)."""
+    _say("silu_mul bf16")
+    from mindpipe_amd import ops
+    gu = (torch.randn(5, 2 * 1000, device=DEV, generator=torch.Generator(device=DEV).manual_seed(4)) * 3).bfloat16()
+    act = ops.silu_mul(gu)
+    assert act.dtype == torch.bfloat16
+    ref = torch.nn.functional.silu(gu[:, :1000]) * gu[:, 1000:]
+    d = (act.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+    assert int(d.max()) <= 1 and float((d == 0).float().mean()) >= 0.99
+
+
 @pytest.mark.parametrize("heads,kv_heads", [(2, 2), (4, 1)])
 def test_decoder_prefill_matches_torch_prefill(heads, kv_heads):
     _say("decoder prefill", heads, kv_heads)

@@ -182,6 +182,37 @@ def test_w4a16_gemm_swiglu_matches_two_step(m, i, k, zp):
     assert _rel(_np(act).astype(np.float32), ref) <= 1e-3   # bar: ||act - ref||_F / ||ref||_F <= 1e-3
 
 
+@pytest.mark.parametrize("m,i,k", [(1, 2048, 4096), (1, 300, 11008), (8, 2048, 4096), (16, 1000, 1024),
+                                   (40, 520, 2048), (64, 256, 1024), (3, 1001, 2304), (100, 300, 1024)])
+@pytest.mark.parametrize("zp", [True, False])
+def test_w4a16_gemm_swiglu_bf16_matches_oracle(m, i, k, zp):
+    """bf16 fused gate/up GEMM + SiLU-mul (the batched kernel's bf16 SwiGLU form for M <= 64, the bf16
+    GEMM then silu_mul above) against the oracle: gate and up = F.linear on the bf16 pseudo-quantized
+    weight, each rounded to bf16, then round(round(silu(gate)) * up) in bf16; rel. error <= 1e-3.
+    Against silu_mul(w4a16_gemm) in bf16: <= 1 bf16 ulp (their K splits differ), >= 99% equal."""
+    _say("w4a16 swiglu bf16", m, i, k, zp)
+    ops = _ops()
+    n2 = 2 * i
+    rng = np.random.default_rng(m + i + k)
+    w = O.f32_to_bf16_bits((rng.standard_normal((n2, k)) * 0.02).astype(np.float32))
+    x = O.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    bias = O.f32_to_bf16_bits((rng.standard_normal(n2) * 0.1).astype(np.float32))
+    rdeq, rs, rz, codes = O.pseudo_quantize_tensor(w, 4, zp, 128, dtype="bf16")
+    packed = O.pack_uint4(codes) if zp else O.pack_int4_signed(codes)
+    tb = lambda a: _t(a.view(np.int16), torch.bfloat16)  # noqa: E731
+    args = (_t(packed), tb(rs), None if rz is None else tb(rz), 128, tb(bias))
+    act = ops.w4a16_gemm_swiglu(tb(x), *args)
+    assert act.dtype == torch.bfloat16 and act.shape == (m, i)
+    two = ops.silu_mul(ops.w4a16_gemm(tb(x), *args))
+    d = (act.view(torch.int16).int() - two.view(torch.int16).int()).abs()
+    assert int(d.max()) <= 1 and float((d == 0).float().mean()) >= 0.99
+    gu = O.bf16_bits_to_f32(O.w4a16_linear(x, rdeq, bias, dtype="bf16"))
+    g, u = gu[:, :i], gu[:, i:]
+    rb = lambda v: O.bf16_bits_to_f32(O.f32_to_bf16_bits(v.astype(np.float32)))  # noqa: E731
+    ref = rb(rb(g / (np.float32(1.0) + np.exp(-g))) * u)
+    assert _rel(_np(act.float()), ref) <= 1e-3   # bar: ||act - ref||_F / ||ref||_F <= 1e-3
+
+
 def test_awq_quantize_bf16_matches_reference():
     """AWQ pseudo_quantize_tensor in bf16 arithmetic (asym with a constant group; sym): the
     dequantized weight, scales and zeros bit-exact to the reference's bf16 outputs."""
