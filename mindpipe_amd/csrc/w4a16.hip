@@ -851,7 +851,9 @@ constexpr int kPrefillStages = 4;  // register stages of K tiles
 
 // NTH = 512: a 256 x 128 tile of 8 waves (4 x 2 of 64 x 64): the weight tile is dequantised
 // once per 256 rows, each thread two of its words.
-template <int D, int NTH = 256>
+// BF: bf16 activations, scales, zeros and output; each weight is dequantised to R_bf16((u - z) s) (the
+// reference's bf16 pseudo-quantized weight, w4_bf16x8) and the MFMA is f32_32x32x16_bf16.
+template <int D, int NTH = 256, bool BF = false>
 __global__ __launch_bounds__(NTH) void w4a16_prefill_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups, int gs,
@@ -910,6 +912,16 @@ __global__ __launch_bounds__(NTH) void w4a16_prefill_kernel(
       const int r = c >> 3, cc = c & 7;
       *reinterpret_cast<uint4 *>(&sa[buf][r * kPLD + cc * 8]) = areg[set][i];
     }
+    if constexpr (BF) {
+      const float s_f = mp_bf2f(static_cast<uint16_t>(sz[set] & 0xFFFFu));
+      const float z_f = zr ? mp_bf2f(static_cast<uint16_t>(sz[set] >> 16)) : 8.0f;
+      const float s16 = s_f * 0.0625f, nce = -((1024.f + z_f) * s_f), nco = -((64.f + z_f) * s_f);
+#pragma unroll
+      for (int q = 0; q < BW; ++q)
+        *reinterpret_cast<uint4 *>(&sb[buf][brow * kPLD + bhalf * 8 * BW + q * 8]) =
+            w4_bf16x8(breg[set][q], s_f, s16, nce, nco, 0x000F000Fu, 0x00F000F0u, kMagic);
+      return;
+    }
     // exact fp16 dequant: (1024+u) - (1024+z) is exact, times s rounds once
     const float bz = zr ? mp_h2f(static_cast<uint16_t>(sz[set] >> 16)) : 8.0f;
     const __half2 off = __float2half2_rn(1024.0f + bz);
@@ -954,7 +966,11 @@ __global__ __launch_bounds__(NTH) void w4a16_prefill_kernel(
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          if constexpr (BF)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8w_t, af[i]),
+                                                                 __builtin_bit_cast(bf8w_t, bf[j]), acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
   };
 
@@ -987,14 +1003,15 @@ __global__ __launch_bounds__(NTH) void w4a16_prefill_kernel(
   for (int j = 0; j < 2; ++j) {
     const int col = n0 + wn * 64 + j * 32 + (lane & 31);
     const bool cval = col < n_cols;
-    const float bv = bias ? mp_h2f(bias[cval ? col : n_cols - 1]) : 0.f;
+    const uint16_t bb = bias ? bias[cval ? col : n_cols - 1] : 0;
+    const float bv = bias ? (BF ? mp_bf2f(bb) : mp_h2f(bb)) : 0.f;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const uint32_t o = (cval && m < m_rows) ? (static_cast<uint32_t>(m) * static_cast<uint32_t>(n_cols) + col) * 2 : kOob;
-        mp_buf_store2(yr, o, mp_f2h(acc[i][j][r] + bv));
+        mp_buf_store2(yr, o, BF ? mp_f2bf(acc[i][j][r] + bv) : mp_f2h(acc[i][j][r] + bv));
       }
   }
 }
@@ -2091,7 +2108,8 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     // the fp16 streaming kernels do, would miss the reference by ~1e-3).  Group 128: the batched
     // kernel's bf16 form for 2 to 64 rows (activation loads shared by column tiles; K % 256 == 0, an
     // even group count), the matrix-core small-M kernel for one row and the other shapes of up to 16
-    // rows; otherwise the dequantising GEMM.
+    // rows, the prefill kernel's bf16 form above 64 rows (K % 64 == 0, group % 32 == 0); otherwise
+    // the dequantising GEMM.
     if (m > mp_bf16_batch_min_m() && m <= 64 && mp_bf16_small() && k % 256 == 0 && group_size == 128 && ((k / 128) % 2) == 0 &&
         mp_aligned(x, 16) && mp_aligned(w_packed, 16) && mp_aligned(scales, 4) &&
         (zeros == nullptr || mp_aligned(zeros, 4)) && n * (k / 2) < (int64_t(1) << 32) &&
@@ -2136,6 +2154,31 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
 #undef MP_W4_BF16_W
         return rc;
       }
+    }
+    // above 64 rows: the prefill kernel's bf16 form
+    if (m > 64 && k % kPBK == 0 && group_size % 32 == 0 && mp_aligned(x, 16) && mp_aligned(w_packed, 16) &&
+        mp_aligned(scales, 2) && (zeros == nullptr || mp_aligned(zeros, 2)) && m * k * 2 < (int64_t(1) << 31) &&
+        m * n * 2 < (int64_t(1) << 31) && n <= INT32_MAX && k <= INT32_MAX) {
+      const auto *xp = static_cast<const uint16_t *>(x);
+      const auto *wp = reinterpret_cast<const uint32_t *>(w_packed);
+      const auto *sp = static_cast<const uint16_t *>(scales);
+      const auto *zp = static_cast<const uint16_t *>(zeros);
+      const auto *bp = static_cast<const uint16_t *>(bias);
+      auto *yp = static_cast<uint16_t *>(y);
+      const int ng = static_cast<int>(k / group_size);
+      if (m >= 256) {
+        const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, 256)));
+        hipLaunchKernelGGL((w4a16_prefill_kernel<kPrefillStages - 1, 512, true>), grid, dim3(512), 0, s, xp,
+                           static_cast<int>(m), static_cast<int>(k), wp, static_cast<int>(n), sp, zp, ng, group_size,
+                           bp, yp);
+      } else {
+        const dim3 grid(static_cast<unsigned>(mp_cdiv(n, kPBN)), static_cast<unsigned>(mp_cdiv(m, kPBM)));
+        hipLaunchKernelGGL((w4a16_prefill_kernel<kPrefillStages - 1, 256, true>), grid, dim3(256), 0, s, xp,
+                           static_cast<int>(m), static_cast<int>(k), wp, static_cast<int>(n), sp, zp, ng, group_size,
+                           bp, yp);
+      }
+      MP_CHECK_LAUNCH();
+      return MP_OK;
     }
     mp_dq_args a{};
     a.dt = MP_BF16;

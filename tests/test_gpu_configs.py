@@ -113,9 +113,11 @@ def test_w4a16_full_shape_symmetric_and_awq_agree_with_oracle(m, n, k):
         assert _rel(_np(y)[:, cols], _ref_cols(x, packed, s, z, cols, k)) <= 1e-3
 
 
-# bf16 (Llama-3 checkpoints are bf16): one-row and batched decode shapes of the 70B / 7B layers
+# bf16 (Llama-3 checkpoints are bf16): one-row and batched decode shapes of the 70B / 7B layers and
+# 7B prefill linears at M = 2048
 W4_BF16_FULL = [(1, 28672, 8192), (1, 8192, 28672), (16, 10240, 8192), (16, 8192, 28672), (1, 57344, 8192),
-                (1, 4096, 11008), (8, 22016, 4096), (16, 4096, 4096), (64, 28672, 8192)]
+                (1, 4096, 11008), (8, 22016, 4096), (16, 4096, 4096), (64, 28672, 8192), (2048, 12288, 4096),
+                (2048, 4096, 11008)]
 
 
 @pytest.mark.parametrize("m,n,k", W4_BF16_FULL)

@@ -237,13 +237,14 @@ def test_awq_quantize_bf16_matches_reference():
 # full and a second one follows, and the last wave of K = 40064 has 13).  2 to 64 rows with K % 256 == 0
 # and an even group count: the batched kernel's bf16 form (16- and 32-row parts, one to four column
 # tiles per wave, ragged N, 86 groups); other K with up to 16 rows (640, 1152, 40064) stay on the small-M
-# kernel.  One row past its LDS bound (K = 40960), above 64 rows or with another group size: the
-# dequantising MFMA GEMM, tiled (K % 64 == 0) incl. ragged M / N, and the any-K kernel.
+# kernel.  Above 64 rows with K % 64 == 0 and a group of 32 or 128: the prefill kernel's bf16 form (128-
+# and 256-row tiles, ragged M / N).  One row past its LDS bound (K = 40960) and the other shapes: the
+# dequantising MFMA GEMM (tiled) and its any-K kernel (K = 96).
 W4_BF16_CASES = [(1, 4096, 4096), (16, 4096, 4096), (3, 1000, 1024), (1, 17, 128), (7, 33, 640),
                  (1, 4096, 11008), (12, 300, 2048), (16, 520, 11008), (9, 2048, 8192), (1, 2050, 2048),
                  (1, 300, 30720), (4, 64, 30720), (1, 37, 36864), (2, 100, 40064), (1, 48, 40960),
                  (24, 4096, 4096), (33, 12288, 4096), (40, 520, 2048), (48, 4096, 11008), (64, 8200, 1024),
-                 (16, 300, 1152), (2, 22016, 4096),
+                 (16, 300, 1152), (2, 22016, 4096), (130, 1000, 1024), (80, 130, 320), (700, 520, 2048),
                  (17, 96, 512), (64, 384, 512), (200, 320, 1024), (300, 12288, 4096), (5, 256, 8192),
                  (2, 100, 96)]
 
