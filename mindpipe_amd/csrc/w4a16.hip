@@ -1762,6 +1762,21 @@ static int mp_batch_min_m() {
   return v;
 }
 
+// Whether the batched kernel (in 16- or 32-row parts) takes m rows of an n-column output: every
+// m <= 64, and 64 < m <= 512 where the prefill kernel's grid (128 columns x 128 or 256 rows per
+// workgroup) would fill at most half the CUs.  Measured at 96 to 512 rows (fp16 / bf16): 32 / 29 against
+// 68 / 70 us at M = 256 and 4096 x 4096, 80 against 187 us at M = 256 and N = 4096, K = 11008, 37 against
+// 59 us at M = 96 and N = 12288; the prefill kernel wins from grids of ~170 workgroups (N = 22016, M = 256:
+// 77 against 97 us).  MP_W4_BATCH_MAX_M (a row limit) overrides it, for measurements.
+static bool mp_batch_takes(int64_t m, int64_t n) {
+  static const int forced = mp_knob("MP_W4_BATCH_MAX_M") ? atoi(mp_knob("MP_W4_BATCH_MAX_M")) : -1;
+  if (forced >= 0) return m <= forced;
+  if (m <= 64) return true;
+  if (m > 512) return false;
+  const int64_t wgs = mp_cdiv(n, 128) * (m >= 256 ? mp_cdiv(m, 256) : mp_cdiv(m, 128));
+  return wgs <= 128;
+}
+
 // Prefill GEMM workgroup: 256 x 128 tiles of 8 waves from M = 256 (measured 8-13% faster than
 // 128 x 128 tiles of 4 waves on the 7B linears at M = 2048); MP_W4_PREFILL_THREADS=256 selects the
 // smaller tile (for measurements).
@@ -2024,7 +2039,7 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
 }
 
 // Launch of the batched kernel (fp16, or BF: bf16) with the shape rules measured on the 7B / 70B
-// decode shapes; the caller has checked 2 <= m <= 64, K % 256 == 0, group 128, an even group count,
+// decode shapes; the caller has checked 2 <= m <= 512 (mp_batch_takes), K % 256 == 0, group 128, an even group count,
 // 16-byte alignment and the 32-bit buffer sizes.
 template <bool BF>
 static void mp_launch_w4_batch(hipStream_t s, const uint16_t *xp, int64_t m, int64_t k, const uint32_t *wp,
@@ -2106,11 +2121,12 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     // bf16: every dequantised weight rounded to bf16 as the reference's pseudo-quantized
     // weight is (bf16 keeps 8 significant bits: factoring the group scale out of the sum, as
     // the fp16 streaming kernels do, would miss the reference by ~1e-3).  Group 128: the batched
-    // kernel's bf16 form for 2 to 64 rows (activation loads shared by column tiles; K % 256 == 0, an
-    // even group count), the matrix-core small-M kernel for one row and the other shapes of up to 16
-    // rows, the prefill kernel's bf16 form above 64 rows (K % 64 == 0, group % 32 == 0); otherwise
-    // the dequantising GEMM.
-    if (m > mp_bf16_batch_min_m() && m <= 64 && mp_bf16_small() && k % 256 == 0 && group_size == 128 && ((k / 128) % 2) == 0 &&
+    // kernel's bf16 form for 2 to 64 rows and the mid-M shapes it takes (mp_batch_takes; activation
+    // loads shared by column tiles; K % 256 == 0, an even group count), the matrix-core small-M kernel
+    // for one row and the other shapes of up to 16 rows, the prefill kernel's bf16 form above 64 rows
+    // (K % 64 == 0, group % 32 == 0); otherwise the dequantising GEMM.
+    if (m > mp_bf16_batch_min_m() && mp_batch_takes(m, n) && mp_bf16_small() && k % 256 == 0 && group_size == 128 &&
+        ((k / 128) % 2) == 0 &&
         mp_aligned(x, 16) && mp_aligned(w_packed, 16) && mp_aligned(scales, 4) &&
         (zeros == nullptr || mp_aligned(zeros, 4)) && n * (k / 2) < (int64_t(1) << 32) &&
         m * k * 2 < (int64_t(1) << 32)) {
@@ -2283,7 +2299,7 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
 #undef MP_W4_GEMV_S
 #undef MP_W4_GEMV_C
 #undef MP_W4_GEMV
-  } else if (m > batch_min_m && batch_shape && m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 &&
+  } else if (m > batch_min_m && batch_shape && mp_batch_takes(m, n) && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 &&
       aligned && n * (k / 2) < (int64_t(1) << 32) && m * k * 2 < (int64_t(1) << 32)) {
     mp_launch_w4_batch<false>(s, xp, m, k, wp, n, sp, zp, n_groups_i, bp, yp);
   } else if (m <= 64 && k % 256 == 0 && group_size == 128 && (n_groups_i % 2) == 0 && aligned) {

@@ -118,8 +118,11 @@ W4_CASES = [(1, 4096, 4096), (16, 4096, 4096), (3, 512, 1024), (17, 256, 2048), 
             (2, 4096, 4096), (4, 1000, 2304), (5, 4096, 11008), (8, 12288, 4096), (7, 300, 1280), (6, 72, 512),
             # 33..64 rows as two 32-row halves of one grid: padding workgroups, 4 / 2 / 1 column tiles
             (48, 12288, 4096), (64, 8192, 2048), (37, 1000, 1024), (57, 4096, 1280),
-            # prefill tiles: ragged rows and columns
-            (600, 1000, 1024), (2048, 384, 512)]
+            # 65..512 rows where the prefill grid would fill at most half the CUs: batched kernel in 32-row
+            # parts (up to 12), ragged last part
+            (96, 4096, 4096), (384, 1024, 2048), (130, 520, 1024),
+            # prefill tiles: ragged rows and columns; mid-M with a large grid (N = 12288, 24000)
+            (600, 1000, 1024), (2048, 384, 512), (300, 12288, 1024), (129, 24000, 512)]
 
 
 @pytest.mark.parametrize("m,n,k", W4_CASES)
@@ -237,8 +240,9 @@ def test_awq_quantize_bf16_matches_reference():
 # full and a second one follows, and the last wave of K = 40064 has 13).  2 to 64 rows with K % 256 == 0
 # and an even group count: the batched kernel's bf16 form (16- and 32-row parts, one to four column
 # tiles per wave, ragged N, 86 groups); other K with up to 16 rows (640, 1152, 40064) stay on the small-M
-# kernel.  Above 64 rows with K % 64 == 0 and a group of 32 or 128: the prefill kernel's bf16 form (128-
-# and 256-row tiles, ragged M / N).  One row past its LDS bound (K = 40960) and the other shapes: the
+# kernel.  65 to 512 rows where the prefill grid is small (130 / 200 rows): the batched form in parts.
+# Above that, with K % 64 == 0 and a group of 32 or 128: the prefill kernel's bf16 form (128- and 256-row
+# tiles, ragged M / N).  One row past its LDS bound (K = 40960) and the other shapes: the
 # dequantising MFMA GEMM (tiled) and its any-K kernel (K = 96).
 W4_BF16_CASES = [(1, 4096, 4096), (16, 4096, 4096), (3, 1000, 1024), (1, 17, 128), (7, 33, 640),
                  (1, 4096, 11008), (12, 300, 2048), (16, 520, 11008), (9, 2048, 8192), (1, 2050, 2048),
