@@ -1721,6 +1721,18 @@ static int mp_tiled_variant(int64_t k, int64_t wgs) {
   return 0;
 }
 
+// Whether the skinny kernel takes m (<= 64) rows of an n-column output: up to 32 rows, and up to 64
+// where the tiled kernel's 128-column grid is small (<= 64 column tiles).  Measured at K = 4096: N = 11008
+// (86 tiles) 30.2 against 38.6 us at 64 rows on the tiled kernel, even at 40; N = 4096 (32 tiles) the
+// skinny kernel 19.3 against 29.5 us at 64 rows.  MP_W8_SKINNY_MAX_M (a row limit) overrides it, for
+// measurements.
+static bool mp_skinny_takes(int64_t m, int64_t n) {
+  static const int forced = mp_knob("MP_W8_SKINNY_MAX_M") ? atoi(mp_knob("MP_W8_SKINNY_MAX_M")) : -1;
+  if (m > 64) return false;
+  if (forced >= 0) return m <= forced;
+  return m <= 32 || mp_cdiv(n, 128) <= 64;
+}
+
 static bool mp_skinny_one_chunk() {
   static const bool v = !(mp_knob("MP_W8_SKINNY_ONE_CHUNK") && atoi(mp_knob("MP_W8_SKINNY_ONE_CHUNK")) == 0);
   return v;
@@ -1874,8 +1886,8 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
     else if (rsel == 4) MP_I8_GEMV(4);
     else MP_I8_GEMV(2);
 #undef MP_I8_GEMV
-  } else if (a.rows <= 64 && a.k % 64 == 0 && aligned && epilogue == MP_EPI_DENSE && a.k <= INT32_MAX &&
-      a.n <= INT32_MAX) {
+  } else if (mp_skinny_takes(a.rows, a.n) && a.k % 64 == 0 && aligned && epilogue == MP_EPI_DENSE &&
+             a.k <= INT32_MAX && a.n <= INT32_MAX) {
     const int mi = static_cast<int>(a.rows);
     const int mt = mi <= 16 ? 1 : (mi <= 32 ? 2 : 4);
     const int nw = mt == 4 ? 4 : 8;
