@@ -31,6 +31,8 @@ struct mp_i8_args {
   int epi_round;             // SWIGLU: mp_round_mode of g, u, silu(g) and h (kRoundNone: fp32)
   int shared_b;              // grouped launches: every group multiplies the same b / s_b (a dense
                              // GEMM run as 256-row groups); 0: group e uses expert e's rows
+  int xcd_row_tiles;         // dense tiled launches on a 1-D grid: the row tiles of a column tile sit
+                             // 8 apart in dispatch order (one XCD); 0: the 2-D grid (x: columns, y: rows)
 };
 
 int mp_launch_i8_gemm(const mp_i8_args &args, int epilogue, hipStream_t stream);

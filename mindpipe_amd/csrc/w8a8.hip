@@ -340,6 +340,7 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
 
   int64_t row_begin, row_end;
   int e = 0;
+  int tile_n = blockIdx.x;
   if (p.offsets) {
     int64_t slot = blockIdx.y;
     bool found = false;
@@ -355,6 +356,14 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
       slot -= tiles;
     }
     if (!found) return;
+  } else if (p.xcd_row_tiles > 0) {
+    // 1-D grid: row tile (x / 8) % T of column tile (x / 8T) * 8 + x % 8, so the T row tiles of a
+    // column tile run on one XCD at nearly the same time and share its weight rows in L2
+    const int tr = p.xcd_row_tiles, bx = blockIdx.x;
+    tile_n = (bx / (8 * tr)) * 8 + (bx & 7);
+    row_begin = static_cast<int64_t>((bx >> 3) % tr) * BM;
+    if (static_cast<int64_t>(tile_n) * BN >= p.n || row_begin >= p.rows) return;  // padding; uniform
+    row_end = p.rows < row_begin + BM ? p.rows : row_begin + BM;
   } else {
     row_begin = static_cast<int64_t>(blockIdx.y) * BM;
     row_end = p.rows < row_begin + BM ? p.rows : row_begin + BM;
@@ -364,7 +373,7 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
   const int64_t nb_rows = (EPI == MP_EPI_SWIGLU) ? 2 * n_out : n_out;  // weight rows per expert
   const int8_t *bexp = p.b + static_cast<int64_t>(e) * nb_rows * k;
   const float *sbexp = p.s_b + static_cast<int64_t>(e) * nb_rows;
-  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * ((EPI == MP_EPI_SWIGLU) ? BN / 2 : BN);
+  const int64_t col0 = static_cast<int64_t>(tile_n) * ((EPI == MP_EPI_SWIGLU) ? BN / 2 : BN);
 
   // source rows of this thread's chunks
   const int8_t *asrc[CA];
@@ -522,7 +531,7 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
         if ((lane & 31) == 0 && mval)
-          p.amax_partial[m * p.n_partial + static_cast<int64_t>(blockIdx.x) * 2 + wn] = a;
+          p.amax_partial[m * p.n_partial + static_cast<int64_t>(tile_n) * 2 + wn] = a;
       }
     }
   } else {
@@ -1733,6 +1742,13 @@ static bool mp_skinny_takes(int64_t m, int64_t n) {
   return m <= 32 || mp_cdiv(n, 128) <= 64;
 }
 
+// Dense tiled launches with several row tiles on the XCD-paired 1-D grid (default); MP_W8_TILED_XCD=0
+// keeps the 2-D grid, for measurements.
+static bool mp_tiled_xcd() {
+  static const bool v = !(mp_knob("MP_W8_TILED_XCD") && atoi(mp_knob("MP_W8_TILED_XCD")) == 0);
+  return v;
+}
+
 static bool mp_skinny_one_chunk() {
   static const bool v = !(mp_knob("MP_W8_SKINNY_ONE_CHUNK") && atoi(mp_knob("MP_W8_SKINNY_ONE_CHUNK")) == 0);
   return v;
@@ -1955,21 +1971,30 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
         hipLaunchKernelGGL((i8_gemm_big_kernel<MP_F32, MP_EPI_DENSE>), pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
     }
   } else if (aligned && mp_tiled_variant(a.k, mp_cdiv(a.n, kTBN) * mp_cdiv(a.rows, kTBM)) > 0) {
-    const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));
-    const int tv = mp_tiled_variant(a.k, static_cast<int64_t>(grid.x) * grid.y);
+    // several row tiles: a 1-D grid whose row tiles of one column tile share an XCD (mp_tiled_xcd)
+    const int64_t tn = mp_cdiv(a.n, kTBN), tm = mp_cdiv(a.rows, kTBM);
+    mp_i8_args ax = a;
+    ax.xcd_row_tiles = (tm > 1 && mp_tiled_xcd()) ? static_cast<int>(tm) : 0;
+    const dim3 grid = ax.xcd_row_tiles ? dim3(static_cast<unsigned>(mp_cdiv(tn, 8) * 8 * tm))
+                                       : dim3(static_cast<unsigned>(tn), static_cast<unsigned>(tm));
+    const int tv = mp_tiled_variant(a.k, tn * tm);
     if (epilogue == MP_EPI_F32) {
-      if (tv == 2) hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_F32, 3>), grid, dim3(256), 0, stream, a);
-      else hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_F32, 0>), grid, dim3(256), 0, stream, a);
+      if (tv == 2) hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_F32, 3>), grid, dim3(256), 0, stream, ax);
+      else hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_F32, 0>), grid, dim3(256), 0, stream, ax);
     } else {
-      if (tv == 2) hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_DENSE, 3>), grid, dim3(256), 0, stream, a);
-      else hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_DENSE, 0>), grid, dim3(256), 0, stream, a);
+      if (tv == 2) hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_DENSE, 3>), grid, dim3(256), 0, stream, ax);
+      else hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK2, MP_EPI_DENSE, 0>), grid, dim3(256), 0, stream, ax);
     }
   } else if (a.k % kTBK == 0 && aligned) {
-    const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, kTBN)), static_cast<unsigned>(mp_cdiv(a.rows, kTBM)));
+    const int64_t tn = mp_cdiv(a.n, kTBN), tm = mp_cdiv(a.rows, kTBM);
+    mp_i8_args ax = a;
+    ax.xcd_row_tiles = (tm > 1 && mp_tiled_xcd()) ? static_cast<int>(tm) : 0;
+    const dim3 grid = ax.xcd_row_tiles ? dim3(static_cast<unsigned>(mp_cdiv(tn, 8) * 8 * tm))
+                                       : dim3(static_cast<unsigned>(tn), static_cast<unsigned>(tm));
     if (epilogue == MP_EPI_F32)
-      hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_F32>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_F32>), grid, dim3(256), 0, stream, ax);
     else
-      hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_DENSE>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((i8_tiled_kernel<kTBM, kTBN, kTBK, MP_EPI_DENSE>), grid, dim3(256), 0, stream, ax);
   } else {
     if (epilogue != MP_EPI_DENSE) return MP_ERR_SHAPE;
     hipLaunchKernelGGL(i8_simple_kernel, dim3(static_cast<unsigned>(mp_cdiv(a.rows * a.n, 256))), dim3(256), 0,
