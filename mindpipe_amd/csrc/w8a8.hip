@@ -375,15 +375,17 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
   const float *sbexp = p.s_b + static_cast<int64_t>(e) * nb_rows;
   const int64_t col0 = static_cast<int64_t>(tile_n) * ((EPI == MP_EPI_SWIGLU) ? BN / 2 : BN);
 
-  // source rows of this thread's chunks
-  const int8_t *asrc[CA];
-  bool aval[CA];
+  // A chunks through a descriptor over the tile's rows: a chunk of a row past row_end sits
+  // past the descriptor and reads zeros, so every thread issues the same loads with no branch
+  // (a branch around a load makes the compiler's waits count only the loads every path issues,
+  // which drains the register stages early).  The launcher bounds BM * K below 2^31.
+  const __amdgpu_buffer_rsrc_t arsrc = mp_rsrc(p.a + row_begin * p.k, static_cast<uint32_t>((row_end - row_begin) * p.k));
+  uint32_t aoff[CA];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
     const int c = tid + i * 256;
-    const int64_t r = row_begin + c / CPR;
-    aval[i] = r < row_end;
-    asrc[i] = p.a + (aval[i] ? r : row_begin) * k + (c % CPR) * 16;
+    const int64_t lr = c / CPR;
+    aoff[i] = row_begin + lr < row_end ? static_cast<uint32_t>(lr * p.k + (c % CPR) * 16) : 0x80000000u;
   }
   const int8_t *bsrc[CB];
 #pragma unroll
@@ -430,8 +432,7 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
     kt = kt < nkt ? kt : nkt - 1;
     const int64_t off = kt * BK;
 #pragma unroll
-    for (int i = 0; i < CA; ++i)
-      areg[set][i] = aval[i] ? *reinterpret_cast<const i4_t *>(asrc[i] + off) : i4_t{0, 0, 0, 0};
+    for (int i = 0; i < CA; ++i) areg[set][i] = mp_buf_load16i(arsrc, aoff[i], static_cast<uint32_t>(off));
 #pragma unroll
     for (int i = 0; i < CB; ++i) breg[set][i] = *reinterpret_cast<const i4_t *>(bsrc[i] + off);
   };
@@ -1800,8 +1801,10 @@ static int mp_launch_moe(const mp_i8_args &a, hipStream_t stream) {
 
 // Shared launcher (dense + grouped).
 int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
-  // the tiled kernel addresses a tile's 128 output rows through one descriptor
-  const bool aligned = mp_aligned(a.a, 16) && mp_aligned(a.b, 16) && a.ldy < (int64_t(1) << 23);
+  // the tiled kernel addresses a tile's 128 output rows, and its 128 activation rows, through one
+  // descriptor each
+  const bool aligned = mp_aligned(a.a, 16) && mp_aligned(a.b, 16) && a.ldy < (int64_t(1) << 23) &&
+                       a.k < (int64_t(1) << 23);
   if (a.offsets) {
     // experts of a few hundred rows (serving-size MoE): one workgroup per 256 rows of an
     // expert and weight slice, so each slice streams once per expert
