@@ -545,6 +545,58 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
     const __amdgpu_buffer_rsrc_t yr = mp_rsrc(static_cast<char *>(p.y) + row_begin * p.ldy * esz,
                                               static_cast<uint32_t>(row_end - row_begin) * ldy * esz);
     const int lm0 = wm * WM + 4 * (lane >> 5);
+    // a wave's 8 KB region in the A buffers (128-byte K steps; 64-byte steps leave too little room)
+    constexpr bool STAGE_FITS = WN * 2 * WM <= 8192 && 4 * 8192 <= 2 * BM * LD;
+    if (STAGE_FITS && EPI != MP_EPI_F32 && p.staged_epilogue && esz == 2) {  // workgroup-uniform
+      // 16-bit outputs through LDS: the wave converts its WM x WN tile into a private row-major
+      // region of the A buffers (free after the K loop's last barrier; lane pairs exchange
+      // halves so each lane writes 32-bit words of two adjacent columns), then reads it back
+      // as 16-byte chunks: 8 global stores per lane instead of 64 two-byte ones.  The launcher
+      // sets staged_epilogue only with N and the row stride multiples of 8 and y 16-byte
+      // aligned, so a chunk lies wholly inside or wholly outside the output.
+      int8_t *stage = &sa[0][0] + wave * 8192;
+      const bool odd = lane & 1;
+      const uint32_t sel_lo = odd ? 0x01000504u : 0x05040100u;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int cl = wn * WN + j * 32 + (lane & 31);
+        const float sbv = tscale[BM + cl], bv = tscale[BM + BN + cl];
+        const int cb = (j * 32 + (lane & 31)) & ~1;  // even column of the lane pair, within the wave tile
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f4_t s4 = *reinterpret_cast<const f4_t *>(tscale + lm0 + i * 32 + 8 * q);
+            uint32_t hv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][4 * q + e]), s4[e]), sbv);
+              if (hb) v = mp_add(v, bv);
+              hv[e] = bf ? mp_f2bf(v) : mp_f2h(v);
+            }
+            const uint32_t p01 = hv[0] | (hv[1] << 16), p23 = hv[2] | (hv[3] << 16);
+            const uint32_t recv = __shfl_xor(odd ? p01 : p23, 1, 64);
+            const uint32_t mine = odd ? p23 : p01;
+            const int r = i * 32 + 4 * (lane >> 5) + 8 * q + (odd ? 2 : 0);  // row within the wave tile
+            *reinterpret_cast<uint32_t *>(stage + r * (2 * WN) + cb * 2) = __builtin_amdgcn_perm(recv, mine, sel_lo);
+            *reinterpret_cast<uint32_t *>(stage + (r + 1) * (2 * WN) + cb * 2) =
+                __builtin_amdgcn_perm(recv, mine, sel_lo + 0x02020202u);
+          }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // wave-private region: own writes first
+      constexpr int CPR16 = WN / 8;                         // 16-byte chunks per tile row
+#pragma unroll
+      for (int t = 0; t < WM * CPR16 / 64; ++t) {
+        const int c = t * 64 + lane;
+        const int lr = c / CPR16, cc = (c % CPR16) * 8;
+        const uint4 v = *reinterpret_cast<const uint4 *>(stage + lr * (2 * WN) + cc * 2);
+        const int64_t col = col0 + wn * WN + cc;
+        const uint32_t off = col < n_out ? (static_cast<uint32_t>(wm * WM + lr) * ldy + static_cast<uint32_t>(col)) * 2
+                                         : 0x80000000u;
+        mp_buf_store16(yr, off, v);
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int cl = wn * WN + j * 32 + (lane & 31);
@@ -1755,6 +1807,13 @@ static bool mp_skinny_one_chunk() {
   return v;
 }
 
+// Dense 16-bit outputs of the tiled kernel through its LDS-staged 16-byte-store epilogue: N and the row
+// stride multiples of 8 elements, y 16-byte aligned (MP_W8_STAGED=0 turns it off, for measurements).
+static int mp_tiled_staged_ok(const mp_i8_args &a, int epilogue) {
+  return mp_staged_epilogue() && epilogue == MP_EPI_DENSE && a.out_dtype != MP_F32 && a.n % 8 == 0 &&
+         a.ldy % 8 == 0 && mp_aligned(a.y, 16);
+}
+
 // Persistent large-M launch (MP_W8_PERSIST=0 turns it off, for measurements).
 static int mp_persist() {
   static int v = [] {
@@ -1978,6 +2037,7 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
     const int64_t tn = mp_cdiv(a.n, kTBN), tm = mp_cdiv(a.rows, kTBM);
     mp_i8_args ax = a;
     ax.xcd_row_tiles = (tm > 1 && mp_tiled_xcd()) ? static_cast<int>(tm) : 0;
+    ax.staged_epilogue = mp_tiled_staged_ok(a, epilogue);
     const dim3 grid = ax.xcd_row_tiles ? dim3(static_cast<unsigned>(mp_cdiv(tn, 8) * 8 * tm))
                                        : dim3(static_cast<unsigned>(tn), static_cast<unsigned>(tm));
     const int tv = mp_tiled_variant(a.k, tn * tm);
@@ -1992,6 +2052,7 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
     const int64_t tn = mp_cdiv(a.n, kTBN), tm = mp_cdiv(a.rows, kTBM);
     mp_i8_args ax = a;
     ax.xcd_row_tiles = (tm > 1 && mp_tiled_xcd()) ? static_cast<int>(tm) : 0;
+    ax.staged_epilogue = mp_tiled_staged_ok(a, epilogue);
     const dim3 grid = ax.xcd_row_tiles ? dim3(static_cast<unsigned>(mp_cdiv(tn, 8) * 8 * tm))
                                        : dim3(static_cast<unsigned>(tn), static_cast<unsigned>(tm));
     if (epilogue == MP_EPI_F32)

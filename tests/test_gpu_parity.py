@@ -422,6 +422,9 @@ W8_CASES = [(1, 11008, 4096), (16, 11008, 4096), (5, 1000, 256), (17, 512, 1024)
             (17, 512, 4096), (18, 300, 4096), (7, 256, 11008), (5, 256, 14336), (33, 256, 2048),
             # C2 sweep at M = 256 (tiled kernel) on the full N x K
             (256, 11008, 4096),
+            # tiled kernel: the LDS-staged 16-byte-store epilogue with partial row and column tiles
+            # (N % 8 == 0), and the two-byte-store epilogue (N % 8 != 0)
+            (200, 1000, 512), (100, 333, 512),
             # 33..64 rows: the tiled kernel where its grid is large (N = 11008), the skinny kernel where
             # it is small (N = 4096)
             (48, 11008, 4096), (64, 11008, 1024), (40, 4096, 1024)]
