@@ -19,7 +19,8 @@ stated in each ``sample``).
 ``--profile NAME`` runs one kernel mix for rocprofv3 (the commands in ``profiles/``):
 ``w4gemv`` (the headline loop), ``readfloor`` (one-launch reads of 8.9 MB, rotated),
 ``w4shapes`` (M=16 and the 70B GEMV shapes), ``w4bf16`` (the bf16 W4A16 legs), ``w4batch8`` (7B
-gate/up and down at M = 1 and 8), ``dec7b`` (the 7B decode step), ``w8big`` (the M=4096 int8 GEMM), and
+gate/up and down at M = 1 and 8), ``dec7b`` (the 7B decode step), ``dec70b`` (four layers of the 70B
+decode step), ``w8big`` (the M=4096 int8 GEMM), and
 ``--traffic-probe`` the kernel mix of ``profiles/traffic.json``.
 """
 from __future__ import annotations
@@ -361,6 +362,26 @@ def profile_mix(ops, name, steps):
             del model
             torch.cuda.empty_cache()
         print("dec7b done")
+    elif name == "dec70b":
+        # four layers of the Llama-3-70B decode step at B = 1 and B = 16 with a 4096-token context
+        # (random KV values), 4 eager steps each: the per-layer kernels of the bench's 70B leg
+        import dataclasses
+        from mindpipe_amd.decoder import DecoderConfig, W4Decoder
+        cfg = dataclasses.replace(DecoderConfig.llama3_70b(), layers=4)
+        for b in (1, 16):
+            model = W4Decoder(cfg, max_batch=b, max_len=4096 + 8)
+            g = torch.Generator(device="cuda").manual_seed(5)
+            model.k_cache.normal_(0, 1, generator=g)
+            model.v_cache.normal_(0, 1, generator=g)
+            tok = torch.randint(0, cfg.vocab, (b,), device="cuda", generator=g)
+            cur = torch.tensor([4096], device="cuda", dtype=torch.int64)
+            for _ in range(4):
+                tok = model.decode_step(tok, cur)
+                cur.add_(1)
+            torch.cuda.synchronize()
+            del model
+            torch.cuda.empty_cache()
+        print("dec70b done")
     elif name == "w8big":
         gen = torch.Generator(device="cuda").manual_seed(1)
         qx = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device="cuda", generator=gen)
