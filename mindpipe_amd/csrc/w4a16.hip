@@ -2050,10 +2050,12 @@ static void mp_launch_w4_batch(hipStream_t s, const uint16_t *xp, int64_t m, int
   const int mt = BF && mp_batch_part_mt(m) > 2 ? 2 : mp_batch_part_mt(m);
   const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
   const bool xdb = mp_batch_xdb();
-  // column tiles per wave (measured on the 7B decode shapes, M = 8..64): one for N <= 4096
-  // (enough workgroups), four from N = 12288 (activation loads shared by more tiles); the
-  // 64-row tiling takes at most 2 (registers)
-  int nt = n <= 4096 ? 1 : (n >= 12288 && mt < 4 ? 4 : 2);
+  // column tiles per wave (measured on the 7B / 70B decode shapes, M = 8..64): one for N <= 4096
+  // (enough workgroups), four from N = 12288 (activation loads shared by more tiles), and from
+  // N = 10240 up to 16 rows (the 70B q/k/v at M = 16: 21.7 -> 19.3 us, where two tiles leave 320
+  // workgroups for 256 CUs; at M = 64 four tiles are slower, 40.1 -> 42.3 us); the 64-row tiling
+  // takes at most 2 (registers)
+  int nt = n <= 4096 ? 1 : ((n >= 12288 || (n >= 10240 && m <= 16)) && mt < 4 ? 4 : 2);
   if (mp_batch_env(0) > 0) nt = mp_batch_env(0) >= 4 ? 4 : mp_batch_env(0);
   const int smax = mt * nt >= 8 ? 4 : (mt * nt > 1 ? 8 : 16);  // register budget per wave count
   const int64_t groups = mp_cdiv(n, 16 * nt);

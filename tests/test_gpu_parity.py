@@ -110,6 +110,8 @@ W4_CASES = [(1, 4096, 4096), (16, 4096, 4096), (3, 512, 1024), (17, 256, 2048), 
             (65, 256, 512), (200, 320, 1024), (256, 4096, 4096),
             # batched small-M kernel: 17..32 rows with 4 column tiles per wave, 8 split waves, tail columns
             (24, 8192, 1024), (32, 1024, 2048), (40, 400, 1024), (12, 20480, 512),
+            # four column tiles from N = 10240 up to 16 rows (the 70B q/k/v), ragged last tile
+            (16, 10240, 1024), (12, 10300, 512),
             # one-row GEMV: partial 2048-wide K chunk, N not a multiple of the rows per wave, odd chunk count
             (1, 37, 768), (1, 301, 2304), (1, 1001, 11008), (1, 64, 6144),
             # one-row matrix-core GEMV (K = 2048, 4096): N not a multiple of its 16-row tiles
