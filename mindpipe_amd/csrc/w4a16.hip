@@ -1926,9 +1926,10 @@ static void mp_launch_w4_batch_swiglu(hipStream_t s, const uint16_t *xp, int64_t
   const int mt = BF && mp_batch_part_mt(m) > 2 ? 2 : mp_batch_part_mt(m);
   const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
   const bool xdb = mp_batch_xdb();
-  // column tiles per wave: 4 for 17..32 rows from I = 8192, else 2 (<= 16 rows: measured on the
-  // 7B gate/up at M = 8, 17.4 -> 16.3 us; the 64-row tiling: registers)
-  int nt = half >= 8192 && mt == 2 ? 4 : 2;
+  // column tiles per wave: 4 for 17..32 rows from I = 8192 and up to 16 rows from I = 16384, else 2
+  // (<= 16 rows: measured on the 7B gate/up, I = 11008, at M = 8, 17.4 -> 16.3 us with 2; on the 70B
+  // one, I = 28672, at M = 16, 74.3 -> 68.0 us with 4; the 64-row tiling: registers)
+  int nt = (half >= 8192 && mt == 2) || (half >= 16384 && mt == 1) ? 4 : 2;
   if (mp_batch_env(0) >= 2) nt = mp_batch_env(0) >= 4 ? 4 : 2;
   const int smax = mt * nt >= 8 ? 4 : 8;
   const int nblk = ki / 128;
