@@ -1750,6 +1750,10 @@ static int mp_batch_part_mt(int64_t m) {
   if (v == 1 || v == 2 || v == 4) return v;
   return m <= 16 ? 1 : 2;
 }
+static bool mp_batch_part_mt_forced() {
+  static const bool v = mp_knob("MP_W4_BATCH_PART_MT") != nullptr;
+  return v;
+}
 
 // The batched kernel takes M > this value (default 1: every 2 <= M <= 64, measured faster than
 // the LDS-staged kernel at 2..4 rows too, and the fused SwiGLU path then shares its sums);
@@ -2048,7 +2052,11 @@ static void mp_launch_w4_batch(hipStream_t s, const uint16_t *xp, int64_t m, int
                                uint16_t *yp) {
   const int mi = static_cast<int>(m), ki = static_cast<int>(k), ni = static_cast<int>(n);
   const int nblk = ki / 128;
-  const int mt = BF && mp_batch_part_mt(m) > 2 ? 2 : mp_batch_part_mt(m);
+  // 33..64 rows: one 64-row tile (fp16) where N <= 8192, else two 32-row parts (measured on the 70B
+  // shapes at M = 64: o 34.4 -> 27.7 us and down 106.9 -> 80.0 us with the 64-row tile; q/k/v,
+  // N = 10240, 40.1 -> 51.0 us)
+  int mt = BF && mp_batch_part_mt(m) > 2 ? 2 : mp_batch_part_mt(m);
+  if (!BF && mt == 2 && m > 32 && m <= 64 && n <= 8192 && !mp_batch_part_mt_forced()) mt = 4;
   const int parts = static_cast<int>(mp_cdiv(m, 16 * mt));
   const bool xdb = mp_batch_xdb();
   // column tiles per wave (measured on the 7B / 70B decode shapes, M = 8..64): one for N <= 4096
