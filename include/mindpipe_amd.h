@@ -282,6 +282,15 @@ int mp_decode_rope_append(const void *qkv, int64_t batch, int nh, int kvh, int h
                           const void *sin_t, const int64_t *pos, int64_t capacity, void *q_out, void *k_cache,
                           void *v_cache, mp_stream_t stream);
 
+/* Prefill counterpart of mp_decode_rope_append for positions 0 .. t_len - 1: qkv is
+ * [B * t_len, (nh + 2 kvh) * 128] (token rows of each sequence in order); writes the
+ * rotated queries q_out [B, nh, t_len, 128] and the rotated keys and the values into
+ * the caches [B, kvh, capacity, 128] at positions 0 .. t_len - 1 (t_len <= capacity).
+ * 16-byte aligned buffers; cos_t / sin_t fp16 [capacity, 64], 8-byte aligned. */
+int mp_prefill_rope_split(const void *qkv, int64_t batch, int64_t t_len, int nh, int kvh, int head_dim,
+                          const void *cos_t, const void *sin_t, int64_t capacity, void *q_out, void *k_cache,
+                          void *v_cache, mp_stream_t stream);
+
 /* Split-K decode attention (flash decoding) over positions [0, *pos] of one
  * layer's cache: out [B, nh, 128] fp16 = softmax(q k^T * scale) v, fp32 inside;
  * nh / kvh in {1, 2, 4, 8}.  splits workgroups per (row, kv head), each over

@@ -33,6 +33,7 @@ SIGNATURES = {
     "mp_quant_per_token_i8": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _i32, _vp]),
     "mp_add_rms_norm_quant": (_i32, [_vp, _vp, _vp, C.c_float, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp]),
     "mp_decode_rope_append": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "mp_prefill_rope_split": (_i32, [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "mp_decode_attention_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "mp_decode_attention": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _i32, C.c_float, _vp, _vp, _sz,
                                    _vp]),

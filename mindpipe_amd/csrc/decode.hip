@@ -704,6 +704,71 @@ extern "C" int mp_decode_rope_append(const void *qkv, int64_t batch, int nh, int
   return MP_OK;
 }
 
+namespace {
+
+// Prefill split: one thread per 16-byte piece (8 dims) of one head of one token row of the fused
+// qkv output [B * T, (nh + 2 kvh) * 128].  Query and key pieces are rotated with the cos / sin rows
+// of their position t (rope8: the reference's fp16 ops, each product and sum rounded), queries go
+// to q_out [B, nh, T, 128] (the attention's layout), keys and values to the caches [B, kvh, cap, 128]
+// at position t.  Replaces the slicing, rotation and cache-copy elementwise passes of a prefill.
+__global__ __launch_bounds__(256) void prefill_rope_split_kernel(
+    const uint16_t *__restrict__ qkv, int t_len, int nh, int kvh, const uint16_t *__restrict__ cos_t,
+    const uint16_t *__restrict__ sin_t, int cap, uint16_t *__restrict__ q_out, uint16_t *__restrict__ k_cache,
+    uint16_t *__restrict__ v_cache, int64_t pieces) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= pieces) return;
+  const int heads = nh + 2 * kvh;
+  const int d8 = static_cast<int>(i & 15);                      // 8-dim slice of the head
+  const int64_t hrow = i >> 4;                                  // (row, head)
+  const int h = static_cast<int>(hrow % heads);
+  const int64_t row = hrow / heads;                             // b * T + t
+  const int b = static_cast<int>(row / t_len), t = static_cast<int>(row % t_len);
+  const uint4 x = *reinterpret_cast<const uint4 *>(qkv + (row * heads + h) * kHd + d8 * 8);
+  uint4 o = x;
+  if (h < nh + kvh) {
+    const uint2 c = *reinterpret_cast<const uint2 *>(cos_t + static_cast<int64_t>(t) * (kHd / 2) + d8 * 4);
+    const uint2 sn = *reinterpret_cast<const uint2 *>(sin_t + static_cast<int64_t>(t) * (kHd / 2) + d8 * 4);
+    float f[8];
+    rope8(x, c, sn, f);
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(mp_f2h(f[2 * j])) | (static_cast<uint32_t>(mp_f2h(f[2 * j + 1])) << 16);
+    o = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  uint16_t *dst;
+  if (h < nh)
+    dst = q_out + ((static_cast<int64_t>(b) * nh + h) * t_len + t) * kHd;
+  else if (h < nh + kvh)
+    dst = k_cache + ((static_cast<int64_t>(b) * kvh + (h - nh)) * cap + t) * kHd;
+  else
+    dst = v_cache + ((static_cast<int64_t>(b) * kvh + (h - nh - kvh)) * cap + t) * kHd;
+  *reinterpret_cast<uint4 *>(dst + d8 * 8) = o;
+}
+
+}  // namespace
+
+extern "C" int mp_prefill_rope_split(const void *qkv, int64_t batch, int64_t t_len, int nh, int kvh, int head_dim,
+                                     const void *cos_t, const void *sin_t, int64_t capacity, void *q_out,
+                                     void *k_cache, void *v_cache, mp_stream_t stream) {
+  if (!qkv || !cos_t || !sin_t || !q_out || !k_cache || !v_cache) return MP_ERR_ARG;
+  if (head_dim != kHd) return MP_ERR_SHAPE;
+  if (batch <= 0 || t_len <= 0 || nh <= 0 || kvh <= 0 || nh % kvh != 0 || capacity <= 0 || t_len > capacity ||
+      capacity > INT32_MAX)
+    return MP_ERR_SHAPE;
+  if (!mp_aligned(qkv, 16) || !mp_aligned(q_out, 16) || !mp_aligned(k_cache, 16) || !mp_aligned(v_cache, 16) ||
+      !mp_aligned(cos_t, 8) || !mp_aligned(sin_t, 8))
+    return MP_ERR_ALIGN;
+  const int64_t pieces = batch * t_len * (nh + 2 * kvh) * (kHd / 8);
+  if (mp_cdiv(pieces, 256) > INT32_MAX) return MP_ERR_SHAPE;
+  hipLaunchKernelGGL(prefill_rope_split_kernel, dim3(static_cast<unsigned>(mp_cdiv(pieces, 256))), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t *>(qkv),
+                     static_cast<int>(t_len), nh, kvh, static_cast<const uint16_t *>(cos_t),
+                     static_cast<const uint16_t *>(sin_t), static_cast<int>(capacity), static_cast<uint16_t *>(q_out),
+                     static_cast<uint16_t *>(k_cache), static_cast<uint16_t *>(v_cache), pieces);
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
 // Workspace: partial o [B, nh, splits, 128] fp32 | partial (m, l) [B, nh, splits, 2] fp32.
 extern "C" size_t mp_decode_attention_workspace_bytes(int64_t batch, int nh, int splits) {
   if (batch <= 0 || nh <= 0 || splits <= 0) return 0;

@@ -144,27 +144,25 @@ class W4Decoder:
     def prefill(self, tokens, return_logits=False):
         """tokens [B, T] int64; fills the cache at positions [0, T); returns next-token ids [B]
         (or the last position's logits).  The residual adds, RMSNorms and SiLU-mul run on the
-        fused kernels (one launch each); attention is PyTorch SDPA."""
+        fused kernels (one launch each), RoPE and the cache writes in one launch; attention is
+        PyTorch SDPA."""
         cfg = self.cfg
         b, t = tokens.shape
         hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
         x = self.embed[tokens].reshape(b * t, -1)                  # [B*T, H] residual stream
-        pos = torch.arange(t, device=tokens.device)
         delta = None
         for li, l in enumerate(self.layers):
             if delta is None:
                 hn = ops.add_rms_norm_quant(x, None, l["ln1"], cfg.eps, quant=False)[0]
             else:
                 hn, _, _, x = ops.add_rms_norm_quant(delta, x, l["ln1"], cfg.eps, quant=False)
-            qkv = l["qkv"](hn).reshape(b, t, nh + 2 * kvh, hd).transpose(1, 2)
-            q, k, v = qkv[:, :nh], qkv[:, nh:nh + kvh], qkv[:, nh + kvh:]
-            q, k = self._rope(q, pos), self._rope(k, pos)
-            self.k_cache[li, :b, :, :t] = k
-            self.v_cache[li, :b, :, :t] = v
+            # one launch: RoPE on q / k, q to [B, nh, T, hd], k / v into the cache rows 0 .. T-1
+            q = ops.prefill_rope_split(l["qkv"](hn), b, nh, kvh, self.cos, self.sin, self.k_cache[li, :b],
+                                       self.v_cache[li, :b])
+            k, v = self.k_cache[li, :b, :, :t], self.v_cache[li, :b, :, :t]
             kk = k.repeat_interleave(nh // kvh, dim=1) if kvh != nh else k
             vv = v.repeat_interleave(nh // kvh, dim=1) if kvh != nh else v
-            att = torch.nn.functional.scaled_dot_product_attention(q.contiguous(), kk.contiguous(), vv.contiguous(),
-                                                                   is_causal=True)
+            att = torch.nn.functional.scaled_dot_product_attention(q, kk.contiguous(), vv.contiguous(), is_causal=True)
             o = l["o"](att.transpose(1, 2).reshape(b * t, nh * hd))
             hn, _, _, x = ops.add_rms_norm_quant(o, x, l["ln2"], cfg.eps, quant=False)
             delta = l["down"](ops.silu_mul(l["gate_up"](hn)))

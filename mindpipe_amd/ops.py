@@ -715,6 +715,33 @@ def decode_rope_append(qkv: torch.Tensor, nh: int, kvh: int, cos_t: torch.Tensor
     return q_out
 
 
+def prefill_rope_split(qkv: torch.Tensor, batch: int, nh: int, kvh: int, cos_t: torch.Tensor, sin_t: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor) -> torch.Tensor:
+    """Prefill of positions ``0 .. T-1``: ``qkv [B*T, (nh+2kvh)*128]`` fp16 (each sequence's token rows
+    in order).  RoPE on the q / k heads (the fp16 ops of ``decode_rope_append``), the rotated keys and
+    the values written into ``k_cache`` / ``v_cache [B, kvh, cap, 128]`` at positions ``0 .. T-1``;
+    returns the rotated queries ``[B, nh, T, 128]``."""
+    _need(qkv, "qkv", torch.float16, 2)
+    _need(cos_t, "cos_t", torch.float16, 2)
+    _need(sin_t, "sin_t", torch.float16, 2)
+    if qkv.shape[0] % batch != 0 or qkv.shape[1] != (nh + 2 * kvh) * 128:
+        raise RuntimeError(f"qkv must be [B*T, {(nh + 2 * kvh) * 128}], got {tuple(qkv.shape)}")
+    t = qkv.shape[0] // batch
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, torch.float16, 4)
+        if c.shape[0] != batch or c.shape[1] != kvh or c.shape[3] != 128 or not c.is_contiguous():
+            raise RuntimeError(f"{name} must be a contiguous [{batch}, {kvh}, cap, 128], got {tuple(c.shape)}")
+    cap = k_cache.shape[2]
+    if v_cache.shape[2] != cap or t > cap or cos_t.shape != (cap, 64) or sin_t.shape != (cap, 64):
+        raise RuntimeError("cache capacity, cos / sin rows and T do not match")
+    q = torch.empty((batch, nh, t, 128), dtype=torch.float16, device=qkv.device)
+    with _dev(qkv):
+        _lib.check(_lib.load().mp_prefill_rope_split(
+            qkv.data_ptr(), batch, t, nh, kvh, 128, cos_t.data_ptr(), sin_t.data_ptr(), cap, q.data_ptr(),
+            k_cache.data_ptr(), v_cache.data_ptr(), _stream()), "mp_prefill_rope_split")
+    return q
+
+
 def decode_attention_workspace(batch: int, nh: int, splits: int, device) -> torch.Tensor:
     """Workspace of the decode attention: the splits' partial outputs and statistics."""
     nbytes = _lib.load().mp_decode_attention_workspace_bytes(batch, nh, splits)

@@ -68,6 +68,27 @@ def test_rope_append_bit_exact(b, nh, kvh, pos):
     assert torch.equal(kc, k0) and torch.equal(vc, v0)
 
 
+@pytest.mark.parametrize("b,t,nh,kvh,cap", [(1, 5, 4, 4, 8), (2, 37, 8, 2, 64), (3, 64, 8, 1, 64), (1, 300, 32, 32, 301)])
+def test_prefill_rope_split_bit_exact(b, t, nh, kvh, cap):
+    """The prefill split of the fused qkv rows: rotated queries in [B, nh, T, 128], rotated keys and the
+    values in cache rows 0 .. T-1 (rows past T untouched), against the torch fp16 RoPE."""
+    _say("prefill_rope_split", b, t, nh, kvh, cap)
+    from mindpipe_amd import ops
+    hd = 128
+    g = torch.Generator(device=DEV).manual_seed(3)
+    qkv = torch.randn(b * t, (nh + 2 * kvh) * hd, device=DEV, generator=g).half()
+    cos, sin = _tables(cap)
+    kc = torch.full((b, kvh, cap, hd), 7.0, device=DEV, dtype=torch.float16)
+    vc = torch.full_like(kc, -7.0)
+    q = ops.prefill_rope_split(qkv, b, nh, kvh, cos, sin, kc, vc)
+    heads = qkv.reshape(b, t, nh + 2 * kvh, hd).transpose(1, 2)  # [B, heads, T, hd]
+    c, s_ = cos[:t].unsqueeze(0).unsqueeze(0), sin[:t].unsqueeze(0).unsqueeze(0)
+    assert torch.equal(q, _rope_torch(heads[:, :nh], c, s_))
+    assert torch.equal(kc[:, :, :t], _rope_torch(heads[:, nh:nh + kvh], c, s_))
+    assert torch.equal(vc[:, :, :t], heads[:, nh + kvh:])
+    assert bool((kc[:, :, t:] == 7.0).all()) and bool((vc[:, :, t:] == -7.0).all())
+
+
 @pytest.mark.parametrize("b,nh,kvh,cap,pos,splits", [(1, 4, 4, 300, 0, 8), (2, 8, 2, 300, 299, 1),
                                                      (3, 8, 1, 257, 130, 5), (1, 16, 2, 2304, 2200, 32),
                                                      (2, 4, 4, 1000, 511, 3)])
