@@ -853,7 +853,11 @@ constexpr int kPrefillStages = 4;  // register stages of K tiles
 // once per 256 rows, each thread two of its words.
 // BF: bf16 activations, scales, zeros and output; each weight is dequantised to R_bf16((u - z) s) (the
 // reference's bf16 pseudo-quantized weight, w4_bf16x8) and the MFMA is f32_32x32x16_bf16.
-template <int D, int NTH = 256, bool BF = false>
+// SWI: the fused gate/up weight [2I, K] (n_cols = 2I): a workgroup's 128 weight rows are 64 gate
+// rows and the matching 64 up rows, wave column half wn multiplies gate rows [32 wn, +32) (tile j = 0)
+// and their up rows (j = 1), and the epilogue writes act [M, I] = silu(gate) * up with the rounding of
+// the two-step path (gate and up rounded to the output type first).
+template <int D, int NTH = 256, bool BF = false, bool SWI = false>
 __global__ __launch_bounds__(NTH) void w4a16_prefill_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups, int gs,
@@ -881,7 +885,16 @@ __global__ __launch_bounds__(NTH) void w4a16_prefill_kernel(
     aoff[i] = m < m_rows ? (static_cast<uint32_t>(m) * static_cast<uint32_t>(k) + (c & 7) * 8) * 2 : kOob;
   }
   const int brow = tid / TPR, bhalf = tid % TPR;  // each thread: BW words = 8 BW columns
-  const int bn = n0 + brow < n_cols ? n0 + brow : n_cols - 1;
+  const int n_out = SWI ? n_cols / 2 : n_cols;
+  const int oc0 = SWI ? blockIdx.x * (kPBN / 2) : n0;  // first output column of the workgroup
+  int bn;
+  if constexpr (SWI) {
+    const int oc = oc0 + (brow & (kPBN / 2 - 1));
+    const int occ = oc < n_out ? oc : n_out - 1;
+    bn = brow < kPBN / 2 ? occ : n_out + occ;
+  } else {
+    bn = n0 + brow < n_cols ? n0 + brow : n_cols - 1;
+  }
   const uint32_t *bsrc = wq + static_cast<int64_t>(bn) * kw + BW * bhalf;
   const uint16_t *zsrc = zr ? zr : sc;  // (no zeros: the scale is read again and 8 used)
 
@@ -959,7 +972,7 @@ __global__ __launch_bounds__(NTH) void w4a16_prefill_kernel(
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int r = wn * 64 + j * 32 + (lane & 31);
+        const int r = SWI ? j * 64 + wn * 32 + (lane & 31) : wn * 64 + j * 32 + (lane & 31);
         bf[j] = *reinterpret_cast<const h8_t *>(&sb[cur][r * kPLD + ks * 16 + 8 * (lane >> 5)]);
       }
 #pragma unroll
@@ -998,7 +1011,25 @@ __global__ __launch_bounds__(NTH) void w4a16_prefill_kernel(
 
   // epilogue: biases first, then stores through a descriptor (rows past M and columns past
   // N dropped without a branch)
-  const auto yr = mp_rsrc(y, static_cast<uint32_t>(m_rows) * static_cast<uint32_t>(n_cols) * 2);
+  const auto yr = mp_rsrc(y, static_cast<uint32_t>(m_rows) * static_cast<uint32_t>(n_out) * 2);
+  if constexpr (SWI) {
+    const int col = oc0 + wn * 32 + (lane & 31);
+    const bool cval = col < n_out;
+    const int cc = cval ? col : n_out - 1;
+    const float bg = bias ? (BF ? mp_bf2f(bias[cc]) : mp_h2f(bias[cc])) : 0.f;
+    const float bu = bias ? (BF ? mp_bf2f(bias[n_out + cc]) : mp_h2f(bias[n_out + cc])) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const float g = acc[i][0][r] + bg, u = acc[i][1][r] + bu;
+        const uint16_t a = BF ? mp_swiglu_bf(mp_rbf(g), mp_rbf(u)) : mp_swiglu_h(mp_rh(g), mp_rh(u));
+        const uint32_t o = (cval && m < m_rows) ? (static_cast<uint32_t>(m) * static_cast<uint32_t>(n_out) + col) * 2 : kOob;
+        mp_buf_store2(yr, o, a);
+      }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int col = n0 + wn * 64 + j * 32 + (lane & 31);
@@ -1989,7 +2020,7 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
   if (m < 0 || n2 <= 0 || (n2 & 1) || k <= 0 || group_size != 128 || k % 256 != 0) return MP_ERR_SHAPE;
   if (m == 0) return MP_OK;
   if (!x || !w_packed || !scales || !act) return MP_ERR_ARG;
-  if (m > 64 || n2 > INT32_MAX || k > INT32_MAX) return MP_ERR_SHAPE;
+  if (n2 > INT32_MAX || k > INT32_MAX) return MP_ERR_SHAPE;
   const int n_groups = static_cast<int>(k / group_size);
   if (n_groups % 2 != 0) return MP_ERR_SHAPE;
   if (!mp_aligned(x, 16) || !mp_aligned(w_packed, 16) || !mp_aligned(scales, 4) ||
@@ -2005,6 +2036,27 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
   auto *yp = static_cast<uint16_t *>(act);
   const int ki = static_cast<int>(k), ni = static_cast<int>(n2);
   const int64_t half = n2 / 2;
+  if (m > 64) {
+    // the prefill kernel's SwiGLU form: 64 output columns (their gate and up rows) per workgroup;
+    // its descriptors cover the activation rows and the output (sizes < 2^31)
+    if (m * k * 2 >= (int64_t(1) << 31) || m * half * 2 >= (int64_t(1) << 31) || m > INT32_MAX) return MP_ERR_SHAPE;
+    const bool wide = mp_prefill_threads() == 512 && m >= 256;
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(half, kPBN / 2)), static_cast<unsigned>(mp_cdiv(m, wide ? 256 : kPBM)));
+    const int mi = static_cast<int>(m);
+#define MP_W4_PF_SWI(NTH_, BF_)                                                                                \
+  hipLaunchKernelGGL((w4a16_prefill_kernel<kPrefillStages - 1, NTH_, BF_, true>), grid, dim3(NTH_), 0, s, xp, mi, ki, \
+                     wp, ni, sp, zp, n_groups, group_size, bp, yp)
+    if (x_dtype == MP_BF16) {
+      if (wide) MP_W4_PF_SWI(512, true);
+      else MP_W4_PF_SWI(256, true);
+    } else {
+      if (wide) MP_W4_PF_SWI(512, false);
+      else MP_W4_PF_SWI(256, false);
+    }
+#undef MP_W4_PF_SWI
+    MP_CHECK_LAUNCH();
+    return MP_OK;
+  }
   // one row, fp16: the VALU GEMV's SwiGLU form; otherwise the batched kernel's
   if (m == 1 && x_dtype == MP_F16) {
     // two gate rows and the matching two up rows per wave; chunk / split choice as the GEMV

@@ -143,9 +143,9 @@ class W4Decoder:
     @torch.no_grad()
     def prefill(self, tokens, return_logits=False):
         """tokens [B, T] int64; fills the cache at positions [0, T); returns next-token ids [B]
-        (or the last position's logits).  The residual adds, RMSNorms and SiLU-mul run on the
-        fused kernels (one launch each), RoPE and the cache writes in one launch; attention is
-        PyTorch SDPA."""
+        (or the last position's logits).  The residual adds and RMSNorms run on the fused
+        kernels (one launch each), the SiLU-mul in the gate/up GEMM's epilogue, RoPE and the
+        cache writes in one launch; attention is PyTorch SDPA."""
         cfg = self.cfg
         b, t = tokens.shape
         hd, nh, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
@@ -165,7 +165,7 @@ class W4Decoder:
             att = torch.nn.functional.scaled_dot_product_attention(q, kk.contiguous(), vv.contiguous(), is_causal=True)
             o = l["o"](att.transpose(1, 2).reshape(b * t, nh * hd))
             hn, _, _, x = ops.add_rms_norm_quant(o, x, l["ln2"], cfg.eps, quant=False)
-            delta = l["down"](ops.silu_mul(l["gate_up"](hn)))
+            delta = l["down"](l["gate_up"].swiglu(hn))  # gate/up GEMM with SiLU-mul in its epilogue
         # the last position of each sequence only
         d_last = delta.reshape(b, t, -1)[:, -1].contiguous()
         x_last = x.reshape(b, t, -1)[:, -1].contiguous()

@@ -598,13 +598,13 @@ def w4a16_gemm_swiglu(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Ten
                       group_size: int, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``silu(G) * U`` with ``[G | U] = X . dequant(W)^T (+ bias)`` for the fused gate/up weight
     ``w_packed [2I, K/8]`` (gate rows first): ``[..., I]`` in ``x``'s dtype (fp16 or bf16), rounded as
-    ``silu_mul`` of the ``w4a16_gemm`` output.  One launch for M <= 64 (group 128, K % 256 == 0);
-    otherwise the two launches."""
+    ``silu_mul`` of the ``w4a16_gemm`` output.  One launch (group 128, K % 256 == 0, M * K and M * I
+    below 2^30); otherwise the two launches."""
     k = x.shape[-1]
     n2 = w_packed.shape[0]
     x2 = x.reshape(-1, k)
     m = x2.shape[0]
-    if m > 64 or group_size != 128 or k % 256 or n2 % 2:
+    if group_size != 128 or k % 256 or n2 % 2 or m * k >= (1 << 30) or m * (n2 // 2) >= (1 << 30):
         return silu_mul(w4a16_gemm(x2, w_packed, scales, zeros, group_size, bias)).reshape(*x.shape[:-1], n2 // 2)
     _need(x, "x", (torch.float16, torch.bfloat16))
     _need(w_packed, "w_packed", torch.int32, 2)
