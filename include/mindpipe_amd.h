@@ -110,8 +110,9 @@ int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t *w_packed, 
  * of the SwiGLU MLP (act_fn(gate_up) in the HF / vLLM Llama MLP the W4A16 export
  * serves) in one launch.  Every value is rounded as the two-step path rounds it
  * (fp16 / bf16 gate and up, then the rounded silu times up).  Group 128,
- * K % 256 == 0; fp16 or bf16.  Up to 64 rows the decode kernels, above that the
- * prefill kernel's SwiGLU form (M * K and M * I below 2^30). */
+ * K % 256 == 0; fp16 or bf16.  The row ranges of mp_w4a16_gemm: the decode kernels up
+ * to 64 rows and the batched kernel's row parts where its grid fills the chip better,
+ * else the prefill kernel's SwiGLU form (M * K and M * I below 2^30). */
 int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const int32_t *w_packed, int64_t n2,
                          const void *scales, const void *zeros, int group_size, const void *bias, void *act,
                          int x_dtype, mp_stream_t stream);

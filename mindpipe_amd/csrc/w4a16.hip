@@ -2036,9 +2036,10 @@ extern "C" int mp_w4a16_gemm_swiglu(const void *x, int64_t m, int64_t k, const i
   auto *yp = static_cast<uint16_t *>(act);
   const int ki = static_cast<int>(k), ni = static_cast<int>(n2);
   const int64_t half = n2 / 2;
-  if (m > 64) {
-    // the prefill kernel's SwiGLU form: 64 output columns (their gate and up rows) per workgroup;
-    // its descriptors cover the activation rows and the output (sizes < 2^31)
+  if (m > 64 && !mp_batch_takes(m, n2)) {
+    // the prefill kernel's SwiGLU form where w4a16_gemm takes the prefill kernel (else the batched
+    // kernel's SwiGLU form in row parts, below): 64 output columns (their gate and up rows) per
+    // workgroup; its descriptors cover the activation rows and the output (sizes < 2^31)
     if (m * k * 2 >= (int64_t(1) << 31) || m * half * 2 >= (int64_t(1) << 31) || m > INT32_MAX) return MP_ERR_SHAPE;
     const bool wide = mp_prefill_threads() == 512 && m >= 256;
     const dim3 grid(static_cast<unsigned>(mp_cdiv(half, kPBN / 2)), static_cast<unsigned>(mp_cdiv(m, wide ? 256 : kPBM)));

@@ -151,8 +151,10 @@ def test_w4a16_gemm_matches_dequant_matmul(m, n, k, zp):
 @pytest.mark.parametrize("m,i,k", [(1, 2048, 4096), (1, 1001, 2304), (1, 300, 11008), (8, 2048, 4096), (16, 1000, 1024),
                                    (24, 4096, 512), (40, 520, 2048), (64, 256, 1024), (3, 1001, 2304),
                                    (6, 300, 11008), (64, 8192, 2048), (45, 1000, 1024), (8, 16400, 512),
-                                   # above 64 rows: the prefill kernel's SwiGLU form (128- and 256-row tiles)
-                                   (100, 1000, 1024), (300, 520, 512), (65, 64, 256)])
+                                   # above 64 rows: the batched kernel's SwiGLU form in row parts, and the
+                                   # prefill kernel's (128- and 256-row tiles) where w4a16_gemm takes it
+                                   (100, 1000, 1024), (300, 520, 512), (65, 64, 256), (130, 8200, 256),
+                                   (520, 300, 512)])
 @pytest.mark.parametrize("zp", [True, False])
 def test_w4a16_gemm_swiglu_matches_two_step(m, i, k, zp):
     """Fused gate/up GEMM + SiLU-mul against silu_mul(w4a16_gemm) (bit-exact where both run the
@@ -194,7 +196,7 @@ def test_w4a16_gemm_swiglu_matches_two_step(m, i, k, zp):
 
 @pytest.mark.parametrize("m,i,k", [(1, 2048, 4096), (1, 300, 11008), (8, 2048, 4096), (16, 1000, 1024),
                                    (40, 520, 2048), (64, 256, 1024), (3, 1001, 2304), (100, 300, 1024),
-                                   (12, 16400, 512), (300, 520, 512)])
+                                   (12, 16400, 512), (300, 520, 512), (520, 300, 512)])
 @pytest.mark.parametrize("zp", [True, False])
 def test_w4a16_gemm_swiglu_bf16_matches_oracle(m, i, k, zp):
     """bf16 fused gate/up GEMM + SiLU-mul (the batched kernel's bf16 SwiGLU form for M <= 64, the bf16
