@@ -5,7 +5,8 @@ MindPipe (``acceleration/runtime_patches/vllm_ascend.patch:3935-4033``): per-tok
 dynamic int8 quant (fp32 scale, the ``npu_dynamic_quant`` contract) then the int8
 GEMM with the per-token x per-channel epilogue (``npu_quant_matmul``).
 ``fused_experts_w8a8`` replaces the MoE expert chain of ``_run_expert_tile``
-(``vllm_ascend.patch:2356-2423``).  ``add_rms_norm_forward`` replaces the
+(``vllm_ascend.patch:2356-2423``) and ``W8A8DynamicFusedMoEMethod`` the fused-MoE method's weight
+processing and ``apply`` (``:4278-4482``).  ``add_rms_norm_forward`` replaces the
 add-RMSNorm(-dynamic-quant) step in front of a W8A8 linear
 (``_addrmsnorm_forward_oot``, ``vllm_ascend.patch:740-792``), and
 ``prepare_dense_mlp_w8a8`` / ``dense_mlp_w8a8`` the chunked dense-MLP chain
@@ -23,7 +24,8 @@ import torch
 
 from . import ops
 
-__all__ = ["W8A8DynamicLinearMethod", "fused_experts_w8a8", "grouped_apply_mlp_w8a8", "dynamic_quant",
+__all__ = ["W8A8DynamicLinearMethod", "W8A8DynamicFusedMoEMethod", "fused_experts_w8a8", "grouped_apply_mlp_w8a8",
+           "layout_conversions", "dynamic_quant",
            "add_rms_norm_forward", "prepare_dense_mlp_w8a8", "dense_mlp_w8a8"]
 
 
@@ -78,52 +80,63 @@ class W8A8DynamicLinearMethod:
         return (output, dynamic_scale) if config.get("return_scale", False) else output
 
 
-_KERNEL_LAYOUT_CACHE = {}
+_LAYOUT_CONVERSIONS = [0]
 
 
-def _kernel_layout(w: torch.Tensor, cache_key: str) -> torch.Tensor:
-    """``[E, A, B]`` runtime weight -> contiguous ``[E, B, A]`` kernel layout, cached per source
-    tensor (version-checked), so a layer's transposed weights are materialised once."""
-    key = (cache_key, w.data_ptr(), tuple(w.shape), w._version)
-    t = _KERNEL_LAYOUT_CACHE.get(key)
-    if t is None:
-        t = w.transpose(1, 2).contiguous()
-        if len(_KERNEL_LAYOUT_CACHE) >= 64:
-            _KERNEL_LAYOUT_CACHE.clear()
-        _KERNEL_LAYOUT_CACHE[key] = t
-    return t
+def layout_conversions() -> int:
+    """How many weight tensors ``fused_experts_w8a8`` / ``grouped_apply_mlp_w8a8`` have re-laid in
+    place so far (each at most once: afterwards the tensor's own strides give the kernel view)."""
+    return _LAYOUT_CONVERSIONS[0]
 
 
-def _expert_weights(w1, w1_scale, w2, w2_scale, layout):
-    """Weights and fp32 per-row scales in the kernel layout ``w13 [E, 2I, H]`` / ``w2 [E, H, I]``.
-    ``layout="runtime"``: the loaded runtime layout ``w13 [E, H, 2I]`` / ``w2 [E, I, H]``
-    (``vllm_ascend.patch:2278-2291``); scales ``[E, 2I]`` / ``[E, H]`` (or ``[E, N, 1]``) in any
-    float dtype."""
-    if layout == "runtime":
-        w1 = _kernel_layout(w1, "w13")
-        w2 = _kernel_layout(w2, "w2")
-    elif layout != "kernel":
-        raise ValueError(f"layout must be 'kernel' or 'runtime', got {layout!r}")
+def _kernel_view(w: torch.Tensor, name: str) -> torch.Tensor:
+    """The kernel layout ``[E, N, K]`` (each output row's K bytes contiguous, the int8 MFMA
+    operand) of a runtime-layout expert weight ``w [E, K, N]`` (``vllm_ascend.patch:2278-2291``).
+
+    After ``W8A8DynamicFusedMoEMethod.process_weights_after_loading`` the layer's ``[E, K, N]``
+    weight is a strided view of ``[E, N, K]`` storage, so this is ``w.transpose(1, 2)`` with no
+    copy.  A contiguous ``[E, K, N]`` tensor (laid out by some other loader) has its storage
+    re-laid once, in place: its values, shape, dtype and device are unchanged and its strides
+    become the kernel view's, so later calls find that view; nothing is cached beside it."""
+    if w.dim() != 3 or w.dtype != torch.int8:
+        raise ValueError(f"{name} must be an int8 [E, K, N] expert weight, got {w.dtype} {tuple(w.shape)}")
+    kv = w.transpose(1, 2)
+    if kv.is_contiguous():
+        return kv
+    with torch.no_grad():
+        w.data = w.data.transpose(1, 2).contiguous().transpose(1, 2)
+    _LAYOUT_CONVERSIONS[0] += 1
+    return w.transpose(1, 2)
+
+
+def _expert_weights(w1, w1_scale, w2, w2_scale, hidden):
+    """Kernel views ``w13 [E, 2I, H]`` / ``w2 [E, H, I]`` of the runtime-layout weights
+    ``w1 [E, H, 2I]`` / ``w2 [E, I, H]``, and fp32 per-row scales ``[E, 2I]`` / ``[E, H]`` from
+    scales of any float dtype shaped ``[E, N]`` or ``[E, N, 1]``."""
+    if w1.dim() != 3 or w2.dim() != 3 or w1.shape[1] != hidden or w2.shape[2] != hidden or \
+            w1.shape[0] != w2.shape[0] or w1.shape[2] != 2 * w2.shape[1]:
+        raise ValueError(f"expected w1 [E, {hidden}, 2I] and w2 [E, I, {hidden}], got {tuple(w1.shape)} "
+                         f"and {tuple(w2.shape)}")
+    k1, k2 = _kernel_view(w1, "w1"), _kernel_view(w2, "w2")
     e = w1.shape[0]
     s1 = w1_scale.reshape(e, -1).to(torch.float32).contiguous()
     s2 = w2_scale.reshape(e, -1).to(torch.float32).contiguous()
-    return w1, s1, w2, s2
+    return k1, s1, k2, s2
 
 
 def fused_experts_w8a8(hidden_states: torch.Tensor, w1: torch.Tensor, w1_scale: torch.Tensor, w2: torch.Tensor,
                        w2_scale: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
                        row_idx: Optional[torch.Tensor] = None, use_int8_w8a8: bool = True,
                        pertoken_scale: Optional[torch.Tensor] = None, expert_map: Optional[torch.Tensor] = None,
-                       output_dtype: Optional[torch.dtype] = None, layout: str = "kernel",
-                       **_unused) -> torch.Tensor:
+                       output_dtype: Optional[torch.dtype] = None, **_unused) -> torch.Tensor:
     """The runtime's ``fused_experts(hidden_states, w1, w1_scale, w2, w2_scale, topk_weights,
     topk_ids, row_idx, use_int8_w8a8=True, pertoken_scale, expert_map, ..., output_dtype)``
     (``vllm_ascend.patch:4447-4468``) on the gfx950 chain: routing quant -> grouped GEMM1 +
     SwiGLU + requant -> grouped GEMM2 -> weighted un-permute.
 
-    * ``layout="kernel"``: ``w1`` int8 ``[E, 2I, H]`` (gate rows first), ``w2`` int8 ``[E, H, I]``;
-      ``layout="runtime"``: the loaded runtime layout ``[E, H, 2I]`` / ``[E, I, H]`` (transposed
-      once per weight tensor and cached).
+    * ``w1`` int8 ``[E, H, 2I]`` (gate columns first) and ``w2`` int8 ``[E, I, H]``: the runtime's
+      loaded layout, read through the kernel view of ``_kernel_view``;
+      ``w1_scale [E, 2I]`` / ``w2_scale [E, H]`` in any float dtype.
     * ``pertoken_scale``: ``hidden_states`` is already int8 with these fp32 per-token scales
       (routed without re-quantizing); ``output_dtype`` then defaults to fp16.
     * ``expert_map`` (expert parallelism: global -> local id, -1 = not on this rank): ids are
@@ -132,37 +145,82 @@ def fused_experts_w8a8(hidden_states: torch.Tensor, w1: torch.Tensor, w1_scale: 
     """
     if not use_int8_w8a8:
         raise NotImplementedError("fused_experts_w8a8 is the int8 W8A8 path")
-    w1, s1, w2, s2 = _expert_weights(w1, w1_scale, w2, w2_scale, layout)
+    k1, s1, k2, s2 = _expert_weights(w1, w1_scale, w2, w2_scale, hidden_states.shape[-1])
     ids = topk_ids.to(torch.int32)
     if expert_map is not None:
         ids = expert_map.to(device=ids.device, dtype=torch.int32)[ids.long()]
     if pertoken_scale is not None:
-        return ops.moe_w8a8_forward(hidden_states.contiguous(), ids.contiguous(), topk_weights, w1, s1, w2, s2,
+        return ops.moe_w8a8_forward(hidden_states.contiguous(), ids.contiguous(), topk_weights, k1, s1, k2, s2,
                                     out_dtype=output_dtype or torch.float16, rule="runtime",
                                     x_scale=pertoken_scale.reshape(-1).to(torch.float32).contiguous())
-    return ops.moe_w8a8_forward(hidden_states.contiguous(), ids.contiguous(), topk_weights, w1, s1, w2, s2,
+    return ops.moe_w8a8_forward(hidden_states.contiguous(), ids.contiguous(), topk_weights, k1, s1, k2, s2,
                                 out_dtype=output_dtype or hidden_states.dtype, rule="runtime")
 
 
 def grouped_apply_mlp_w8a8(hidden_states: torch.Tensor, w1: torch.Tensor, w1_scale: torch.Tensor, w2: torch.Tensor,
                            w2_scale: torch.Tensor, group_list: torch.Tensor, group_list_type: int = 0,
-                           dynamic_scale: Optional[torch.Tensor] = None, output_dtype: Optional[torch.dtype] = None,
-                           layout: str = "kernel") -> torch.Tensor:
+                           dynamic_scale: Optional[torch.Tensor] = None,
+                           output_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """The runtime's ``quant_apply_mlp`` on already-permuted rows (``vllm_ascend.patch:2895-2964``):
     ``hidden_states [R, H]`` grouped by expert with ``group_list`` cumulative endpoints
     (``group_list_type=0``) or raw counts (``1``) (``:2015-2031``); quantized here unless
-    ``dynamic_scale`` marks it as int8 codes.  GEMM1 + SwiGLU + requant, then GEMM2 with the
-    per-token scale, output ``output_dtype`` (default fp16; the reference's default is the down
-    scale's dtype).  There is no 10240-column limit (``_can_use_fused_swiglu_quant``)."""
-    w1, s1, w2, s2 = _expert_weights(w1, w1_scale, w2, w2_scale, layout)
+    ``dynamic_scale`` marks it as int8 codes.  Weights in the runtime layout as for
+    ``fused_experts_w8a8``.  GEMM1 + SwiGLU + requant, then GEMM2 with the per-token scale,
+    output ``output_dtype`` (default fp16; the reference's default is the down scale's dtype).
+    There is no 10240-column limit (``_can_use_fused_swiglu_quant``)."""
+    k1, s1, k2, s2 = _expert_weights(w1, w1_scale, w2, w2_scale, hidden_states.shape[-1])
     offsets = ops.group_offsets_from_list(group_list.to(hidden_states.device), group_list_type)
     if dynamic_scale is None:
         qx, sx = dynamic_quant(hidden_states)
     else:
         qx, sx = hidden_states.contiguous(), dynamic_scale.reshape(-1).to(torch.float32).contiguous()
-    inter = w2.shape[2]
-    qh, sh = ops.moe_gmm1_swiglu_quant(qx, sx, w1, s1, offsets, inter)
-    return ops.moe_gmm2(qh, sh, w2, s2, offsets, output_dtype or torch.float16)
+    inter = k2.shape[2]
+    qh, sh = ops.moe_gmm1_swiglu_quant(qx, sx, k1, s1, offsets, inter)
+    return ops.moe_gmm2(qh, sh, k2, s2, offsets, output_dtype or torch.float16)
+
+
+class W8A8DynamicFusedMoEMethod:
+    """Replaces ``AscendW8A8DynamicFusedMoEMethod`` (``vllm_ascend.patch:4278-4482``): weight
+    processing after loading, and ``apply`` on already-selected experts.
+
+    ``process_weights_after_loading``: the checkpoint loads ``w13_weight [E, 2I, H]`` and
+    ``w2_weight [E, H, I]``; the reference transposes them to ``[E, H, 2I]`` / ``[E, I, H]`` for
+    its NPU kernels.  Here the layer's tensors take that shape as strided views of the loaded
+    storage (no copy, no second buffer): the gfx950 grouped GEMMs read the loaded rows directly,
+    and ``fused_experts_w8a8`` recovers them from the view.  Scales are flattened to ``[E, N]``
+    with fp32 copies ``w13_weight_scale_fp32`` / ``w2_weight_scale_fp32``, offsets to ``[E, N]``,
+    under the reference's attribute names."""
+
+    def __init__(self, in_dtype: torch.dtype = torch.float16):
+        self.transpose_weight = True
+        self.in_dtype = in_dtype
+
+    def process_weights_after_loading(self, layer) -> None:
+        if self.transpose_weight:
+            layer.w13_weight.data = layer.w13_weight.data.transpose(1, 2)
+            layer.w2_weight.data = layer.w2_weight.data.transpose(1, 2)
+        for name in ("w13", "w2"):
+            sc = getattr(layer, f"{name}_weight_scale")
+            sc.data = sc.data.view(sc.data.shape[0], -1)
+            setattr(layer, f"{name}_weight_scale_fp32", sc.data.to(torch.float32))
+            off = getattr(layer, f"{name}_weight_offset", None)
+            if off is not None:
+                off.data = off.data.view(off.data.shape[0], -1)
+
+    def apply(self, layer, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+              expert_map: Optional[torch.Tensor] = None, pertoken_scale: Optional[torch.Tensor] = None,
+              row_idx: Optional[torch.Tensor] = None, **_unused) -> torch.Tensor:
+        """The expert chain of ``apply`` once experts are selected (``:4430-4468``): fp32 weight
+        scales under fp16 models, the stored scales otherwise; ``topk_weights`` cast to the model
+        dtype; output in the model dtype."""
+        if self.in_dtype == torch.float16:
+            w1_scale, w2_scale = layer.w13_weight_scale_fp32, layer.w2_weight_scale_fp32
+        else:
+            w1_scale, w2_scale = layer.w13_weight_scale, layer.w2_weight_scale
+        return fused_experts_w8a8(hidden_states=x, w1=layer.w13_weight, w1_scale=w1_scale, w2=layer.w2_weight,
+                                  w2_scale=w2_scale, topk_weights=topk_weights.to(self.in_dtype), topk_ids=topk_ids,
+                                  row_idx=row_idx, use_int8_w8a8=True, pertoken_scale=pertoken_scale,
+                                  expert_map=expert_map, output_dtype=self.in_dtype)
 
 
 # ---------------------------------------------------------------- add + RMSNorm (+ dynamic quant)

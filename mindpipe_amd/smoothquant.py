@@ -348,13 +348,20 @@ def _layers_of(root):
 
 def quantize_llama_like(model, weight_bits=8, activation_bits=8, act_quant="per_token", quantize_bmm_input=True,
                         scale_rule="fake", *, allow_extension_models=False) -> List[str]:
-    """Module-swap router (``fake_quant.py:226-438``): per decoder layer, q/k/v (output quant
-    when ``quantize_bmm_input``) and o; for Qwen3.5 linear-attention layers ``in_proj_qkv /
-    in_proj_z / in_proj_a / in_proj_b`` (output quant) and ``out_proj``; the Qwen3.5-MoE
-    ``shared_expert`` gate/up/down and ``shared_expert_gate``; packed experts become
-    ``SmoothQuantPackedMoeExperts`` (per-expert ``nn.ModuleList`` experts of qwen3_moe swap
-    their linears); every other model's MLP gate/up/down.  Returns the qualified names in
-    the reference's order."""
+    """Module-swap router (``fake_quant.py:226-438``), per decoder layer:
+
+    * attention: q/k/v (output quant when ``quantize_bmm_input``) and o; for Qwen3.5 and
+      Qwen3.5-MoE linear-attention layers ``in_proj_qkv / in_proj_z / in_proj_a / in_proj_b``
+      (output quant) and ``out_proj`` instead (``:249-293``);
+    * MLP: none for ``qwen3_5`` (its dense MLP stays in floating point, ``:249-293``); the
+      Qwen3.5-MoE ``shared_expert`` gate/up/down, ``shared_expert_gate`` and the packed experts
+      (``:294-362``); for ``qwen3_moe`` layers with experts, the per-expert linears of an
+      ``nn.ModuleList`` or the packed experts (``:363-406``); gate/up/down for every other
+      layer, including ``qwen3_moe``'s dense layers (``:407-437``).
+
+    The token-mixer kind of a Qwen3.5 layer is its ``layer_type`` (the attribute the reference
+    reads, as named by the transformers it pins) or, on later transformers, ``block_type``.
+    Returns the qualified names in the order the reference appends them."""
     model_type = getattr(getattr(model, "config", None), "model_type", None)
     allowed = SUPPORTED_MODEL_TYPES | (EXTENSION_MODEL_TYPES if allow_extension_models else frozenset())
     if model_type not in allowed:
@@ -367,9 +374,12 @@ def quantize_llama_like(model, weight_bits=8, activation_bits=8, act_quant="per_
         setattr(parent, attr, SmoothQuantLinear.from_float(getattr(parent, attr), quantize_output=qout, **kw))
         names.append(qualified)
 
+    def mixer_kind(layer):
+        kind = getattr(layer, "layer_type", None)
+        return getattr(layer, "block_type", None) if kind is None else kind
+
     def attention(layer, lp):
-        if model_type in ("qwen3_5", "qwen3_5_moe", "qwen3_5_moe_text") and \
-                getattr(layer, "layer_type", None) == "linear_attention":
+        if model_type in ("qwen3_5", "qwen3_5_moe", "qwen3_5_moe_text") and mixer_kind(layer) == "linear_attention":
             la = layer.linear_attn
             for p in ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b"):
                 swap(la, p, f"{lp}.linear_attn.{p}", quantize_bmm_input)
@@ -388,6 +398,8 @@ def quantize_llama_like(model, weight_bits=8, activation_bits=8, act_quant="per_
     for li, layer in enumerate(_layers_of(root)):
         lp = f"{prefix}.layers.{li}"
         attention(layer, lp)
+        if model_type == "qwen3_5":
+            continue
         mlp = layer.mlp
         if model_type in ("qwen3_5_moe", "qwen3_5_moe_text"):
             for p in ("gate_proj", "up_proj", "down_proj"):

@@ -599,7 +599,7 @@ def dense_mlp_runtime(x, qw13, s13, qw2, s2, chunks=1, out_dtype="fp16", qx=None
     return _to_out(out, out_dtype)
 
 
-def moe_fake(x, topk_ids, topk_w, gate_up_proj, down_proj, dtype="fp16"):
+def moe_fake(x, topk_ids, topk_w, gate_up_proj, down_proj, dtype="fp16", prequantized=False):
     """``SmoothQuantPackedMoeExperts`` construction + ``forward`` fake path
     (``fake_quant.py:124-191``) with SiLU: per-channel fake-quant weights
     ``gate_up_proj [E,2I,H]`` / ``down_proj [E,H,I]``; for each hit expert in ascending
@@ -607,13 +607,22 @@ def moe_fake(x, topk_ids, topk_w, gate_up_proj, down_proj, dtype="fp16"):
     rounding), ``chunk(2)``, ``silu(gate) * up`` (two roundings), per-token fake quant,
     ``F.linear``, times the fp32 router weight (rounded once), ``index_add_`` (one
     rounding per add).  Every rounding is to ``dtype``; fp16 arrays, or bf16 bit
-    patterns for ``dtype="bf16"`` (router weights fp32 in both cases)."""
+    patterns for ``dtype="bf16"`` (router weights fp32 in both cases).
+
+    ``prequantized=True``: the weights given are already the fake-quant weights (the
+    construction step ``:140-142`` done elsewhere), so only the forward is computed.
+    Each token's output depends on its own row and experts alone, so the forward may be
+    given any subset of the tokens."""
     R = lambda v: _round_to(v, dtype)  # noqa: E731
     F32 = lambda a: _in_f32(np.asarray(a), dtype)  # noqa: E731
     xf = F32(x)
     n_exp = gate_up_proj.shape[0]
-    wq13 = [F32(quantize_weight_per_channel_fake(gate_up_proj[e], 8, dtype)[2]) for e in range(n_exp)]
-    wq2 = [F32(quantize_weight_per_channel_fake(down_proj[e], 8, dtype)[2]) for e in range(n_exp)]
+    if prequantized:
+        wq13 = [F32(gate_up_proj[e]) for e in range(n_exp)]
+        wq2 = [F32(down_proj[e]) for e in range(n_exp)]
+    else:
+        wq13 = [F32(quantize_weight_per_channel_fake(gate_up_proj[e], 8, dtype)[2]) for e in range(n_exp)]
+        wq2 = [F32(quantize_weight_per_channel_fake(down_proj[e], 8, dtype)[2]) for e in range(n_exp)]
     out = np.zeros_like(xf)
     inter = down_proj.shape[2]
     for e in range(n_exp):

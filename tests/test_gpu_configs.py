@@ -146,21 +146,91 @@ def test_w4a16_bf16_full_shape_sampled(m, n, k):
 
 
 # fused gate/up: [2I, K] with the gate rows first; 70B (I = 28672) and 7B (I = 11008)
-SWIGLU_FULL = [(1, 28672, 8192), (16, 28672, 8192), (1, 11008, 4096), (8, 11008, 4096)]
+# M = 1 / 16 / 64: 70B decode at B = 1 / 16 / 64 (one-row GEMV and batched kernel forms); M = 1 / 8 / 32:
+# 7B decode at B = 1 / 8 / 32; M = 2048: the 7B prefill (the prefill kernel's SwiGLU form)
+SWIGLU_FULL = [(1, 28672, 8192), (16, 28672, 8192), (64, 28672, 8192), (1, 11008, 4096), (8, 11008, 4096),
+               (32, 11008, 4096), (2048, 11008, 4096)]
 
 
+@pytest.mark.parametrize("dt", ["fp16", "bf16"])
 @pytest.mark.parametrize("m,i,k", SWIGLU_FULL)
-def test_w4a16_swiglu_full_shape_sampled(m, i, k):
-    """``silu(G) * U`` of the fused gate/up GEMM against the oracle's dequant -> matmul (fp16 G, U) ->
-    SiLU-mul on sampled intermediate columns."""
-    _say("w4a16 swiglu full", m, i, k)
+def test_w4a16_swiglu_full_shape_sampled(m, i, k, dt):
+    """``silu(G) * U`` of the fused gate/up GEMM against the oracle's dequant -> matmul (G, U rounded
+    to the activation dtype) -> SiLU-mul (silu rounded, then the product) on sampled intermediate
+    columns, in fp16 and bf16.  Bar: rel. Frobenius error <= 1e-3."""
+    _say("w4a16 swiglu full", m, i, k, dt)
     ops = _ops()
-    packed, s, z = _quant_gpu(2 * i, k, seed=i + k, zp=True)
-    x = _x(m, k, seed=9)
+    if dt == "fp16":
+        packed, s, z = _quant_gpu(2 * i, k, seed=i + k, zp=True)
+        x = _x(m, k, seed=9)
+        act = ops.w4a16_gemm_swiglu(x, packed, s, z, 128, None)
+        torch.cuda.synchronize()
+        cols = _cols(i, seed=i)
+        g = _ref_cols(x, packed, s, z, cols, k).astype(np.float32)
+        u = _ref_cols(x, packed, s, z, cols + i, k).astype(np.float32)
+        sg = (g / (1.0 + np.exp(-g))).astype(np.float16).astype(np.float32)
+        ref = (sg * u).astype(np.float16)
+        assert _rel(_np(act)[:, cols], ref) <= 1e-3
+        return
+    g_ = torch.Generator(device=DEV).manual_seed(i + k)
+    w = (torch.randn(2 * i, k, generator=g_, device=DEV) * 0.02).bfloat16()
+    packed, s, z, _ = ops.w4_quantize_awq(w, 128, True, return_deq=False)
+    del w
+    x = torch.randn(m, k, generator=torch.Generator(device=DEV).manual_seed(9), device=DEV).bfloat16()
     act = ops.w4a16_gemm_swiglu(x, packed, s, z, 128, None)
     torch.cuda.synchronize()
+    assert act.dtype == torch.bfloat16
     cols = _cols(i, seed=i)
-    g = _ref_cols(x, packed, s, z, cols, k).astype(np.float32)
-    u = _ref_cols(x, packed, s, z, cols + i, k).astype(np.float32)
-    ref = (g / (1.0 + np.exp(-g)) * u).astype(np.float16)
-    assert _rel(_np(act)[:, cols], ref) <= 1e-3
+    bits = lambda t: _np(t.view(torch.int16)).view(np.uint16)  # noqa: E731
+
+    def half(c):
+        idx = torch.as_tensor(c, device=DEV)
+        deq = O.dequant_w4_bf16(_np(packed[idx]), bits(s[idx]), bits(z[idx]), k, 128)
+        return O.bf16_bits_to_f32(O.w4a16_linear(bits(x), deq, None, dtype="bf16"))
+
+    g, u = half(cols), half(cols + i)
+    sg = O.bf16_bits_to_f32(O.f32_to_bf16_bits((g / (1.0 + np.exp(-g))).astype(np.float32)))
+    ref = O.bf16_bits_to_f32(O.f32_to_bf16_bits((sg * u).astype(np.float32)))
+    assert _rel(_np(act.float())[:, cols], ref) <= 1e-3
+
+
+@pytest.mark.parametrize("dt", ["fp16", "bf16"])
+def test_moe_fake_rule_mixtral_shape_sampled(dt):
+    """Config 4 at full size with the module's default (fake) rule: ``SmoothQuantPackedMoeExperts``
+    over T = 512 tokens, H = 4096, I = 14336, E = 8, top-2 (``fake_quant.py:124-191``).  All 512
+    tokens run through the GPU chain (expert groups of their real size); 32 sampled tokens are
+    recomputed by ``oracle.moe_fake``, whose per-token forward needs only those rows.  The fake-
+    quant weights it uses are the module's codes times scales, after 64 sampled rows of each
+    expert's codes and scales are checked bit-exact against the oracle's quantizer.  Bar: rel.
+    Frobenius error <= 1e-3 over the sampled tokens."""
+    _say("moe fake mixtral shape", dt)
+    from mindpipe_amd.smoothquant import SmoothQuantPackedMoeExperts
+    t, h, inter, e = 512, 4096, 14336, 8
+    tdt = torch.float16 if dt == "fp16" else torch.bfloat16
+    gen = torch.Generator(device=DEV).manual_seed(1)
+    gu = (torch.randn(e, 2 * inter, h, generator=gen, device=DEV) * 0.02).to(tdt)
+    dn = (torch.randn(e, h, inter, generator=gen, device=DEV) * 0.02).to(tdt)
+    mod = SmoothQuantPackedMoeExperts(gu, dn, torch.nn.SiLU())
+    x = torch.randn(t, h, generator=torch.Generator(device=DEV).manual_seed(0), device=DEV)
+    x[:, torch.randperm(h, generator=torch.Generator().manual_seed(2))[:41].to(DEV)] *= 20
+    x = x.to(tdt)
+    logits = torch.randn(t, e, generator=torch.Generator().manual_seed(3)).numpy()
+    ids, tw = O.mixtral_router(logits, 2)
+    y = mod(x, torch.from_numpy(ids).to(DEV), torch.from_numpy(tw).to(DEV))
+    torch.cuda.synchronize()
+    bits = (lambda a: _np(a)) if dt == "fp16" else (lambda a: _np(a.view(torch.int16)).view(np.uint16))
+    rng = np.random.default_rng(5)
+    gq, dq = mod.dequantized_weights()
+    val = (lambda b: b.astype(np.float32)) if dt == "fp16" else O.bf16_bits_to_f32
+    for ex in range(e):   # the construction step on sampled rows: fake-quant weights exact
+        for w, wq in ((gu[ex], gq[ex]), (dn[ex], dq[ex])):
+            rows = torch.as_tensor(np.sort(rng.choice(w.shape[0], 64, replace=False)), device=DEV)
+            _, _, rfake = O.quantize_weight_per_channel_fake(bits(w[rows]), 8, dt)
+            # equal values (q * s gives +0 where the reference's round(w / s) * s gives -0)
+            assert np.array_equal(val(bits(wq[rows])), val(rfake))
+    toks = np.sort(rng.choice(t, 32, replace=False))
+    ref = O.moe_fake(bits(x[torch.as_tensor(toks, device=DEV)]), ids[toks], tw[toks], bits(gq), bits(dq), dt,
+                     prequantized=True)
+    rv = ref.astype(np.float32) if dt == "fp16" else O.bf16_bits_to_f32(ref)
+    err = _rel(_np(y.float())[toks], rv)
+    assert err <= 1e-3, err

@@ -212,19 +212,17 @@ def test_runtime_fused_experts_contract():
     sc13 = torch.from_numpy(s13).to(DEV).bfloat16()
     sc2 = torch.from_numpy(s2).to(DEV).bfloat16()
     xt, idt, twt = torch.from_numpy(x).to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(tw).to(DEV)
-    y = fused_experts_w8a8(xt, w13_rt, sc13, w2_rt, sc2, twt, idt, layout="runtime")
+    y = fused_experts_w8a8(xt, w13_rt, sc13, w2_rt, sc2, twt, idt)
     ref = O.moe_runtime(x, ids, tw, q13, s13b, q2, s2b)
     assert np.array_equal(y.cpu().numpy().view(np.uint16), ref.view(np.uint16)) or \
         _rel(y.float().cpu().numpy(), ref.astype(np.float32)) <= 1e-3
     # pre-quantized input: the same bits as quantizing inside
     qx, sx = dynamic_quant(xt)
-    y2 = fused_experts_w8a8(qx, w13_rt, sc13, w2_rt, sc2, twt, idt, pertoken_scale=sx, layout="runtime",
-                            output_dtype=torch.float16)
+    y2 = fused_experts_w8a8(qx, w13_rt, sc13, w2_rt, sc2, twt, idt, pertoken_scale=sx, output_dtype=torch.float16)
     assert torch.equal(y, y2)
     # expert_map: experts 2, 3 live elsewhere (-1); their assignments contribute nothing
     emap = torch.tensor([0, 1, -1, -1], dtype=torch.int32, device=DEV)
-    y3 = fused_experts_w8a8(xt, w13_rt[:2], sc13[:2], w2_rt[:2], sc2[:2], twt, idt, expert_map=emap,
-                            layout="runtime")
+    y3 = fused_experts_w8a8(xt, w13_rt[:2], sc13[:2], w2_rt[:2], sc2[:2], twt, idt, expert_map=emap)
     tw_loc = np.where(ids < 2, tw, 0).astype(np.float32)
     ref3 = O.moe_runtime(x, np.where(ids < 2, ids, 0).astype(np.int32), tw_loc, q13, s13b, q2, s2b)
     assert _rel(y3.float().cpu().numpy(), ref3.astype(np.float32)) <= 1e-3
@@ -232,7 +230,7 @@ def test_runtime_fused_experts_contract():
     routed, rscale, row_of_slot, offs = ops.moe_permute_quant(xt, idt, e)
     counts = torch.diff(offs)
     outs = [grouped_apply_mlp_w8a8(routed, w13_rt, sc13, w2_rt, sc2, gl, glt, dynamic_scale=rscale,
-                                   output_dtype=torch.float32, layout="runtime")
+                                   output_dtype=torch.float32)
             for gl, glt in ((offs[1:], 0), (counts, 1))]
     assert torch.equal(outs[0], outs[1])
     yk = ops.moe_gmm2(*ops.moe_gmm1_swiglu_quant(routed, rscale, torch.from_numpy(q13).to(DEV),
@@ -240,7 +238,83 @@ def test_runtime_fused_experts_contract():
                       torch.from_numpy(q2).to(DEV), torch.from_numpy(s2b).to(DEV), offs)
     assert torch.equal(outs[0], yk)
     with pytest.raises(ValueError):
-        grouped_apply_mlp_w8a8(routed, w13_rt, sc13, w2_rt, sc2, counts, 2, dynamic_scale=rscale, layout="runtime")
+        grouped_apply_mlp_w8a8(routed, w13_rt, sc13, w2_rt, sc2, counts, 2, dynamic_scale=rscale)
+
+
+def test_runtime_moe_layers_convert_each_weight_once():
+    """48 MoE layers' worth of distinct weights (Qwen3-30B-A3B has 48), called as the reference
+    runtime calls ``fused_experts`` (``vllm_ascend.patch:4447-4468``: ``w1 [E,H,2I]``,
+    ``w2 [E,I,H]``, no layout argument), twice per layer: each weight is re-laid at most once
+    and every output is bit-exact against the oracle's runtime chain.  Layers processed by
+    ``W8A8DynamicFusedMoEMethod.process_weights_after_loading`` (loaded ``[E,2I,H]`` /
+    ``[E,H,I]``) convert nothing, and their ``apply`` gives the same bits."""
+    _say("runtime moe 48 layers")
+    from mindpipe_amd.runtime import W8A8DynamicFusedMoEMethod, fused_experts_w8a8, layout_conversions
+    rng = np.random.default_rng(48)
+    t, h, inter, e, layers = 40, 128, 192, 4, 48
+    x = rng.standard_normal((t, h)).astype(np.float16)
+    ids, tw = O.mixtral_router(rng.standard_normal((t, e)).astype(np.float32), 2)
+    xt, idt, twt = torch.from_numpy(x).to(DEV), torch.from_numpy(ids).to(DEV), torch.from_numpy(tw).to(DEV)
+
+    class Layer(nn.Module):
+        pass
+
+    stack = []
+    for li in range(layers):
+        gu = (rng.standard_normal((e, 2 * inter, h)) * 0.02).astype(np.float16)
+        dn = (rng.standard_normal((e, h, inter)) * 0.02).astype(np.float16)
+        q13, s13 = (np.stack(v) for v in zip(*[O.quantize_weight_per_channel_export(gu[i])[:2] for i in range(e)]))
+        q2, s2 = (np.stack(v) for v in zip(*[O.quantize_weight_per_channel_export(dn[i])[:2] for i in range(e)]))
+        stack.append((q13, s13, q2, s2))
+    base = layout_conversions()
+    w_rt = [(torch.from_numpy(np.ascontiguousarray(q13.transpose(0, 2, 1))).to(DEV),
+             torch.from_numpy(np.ascontiguousarray(q2.transpose(0, 2, 1))).to(DEV)) for q13, _, q2, _ in stack]
+    first, exact = [], 0
+    for rep in range(2):
+        for li, (q13, s13, q2, s2) in enumerate(stack):
+            w13, w2 = w_rt[li]
+            y = fused_experts_w8a8(xt, w13, torch.from_numpy(s13).to(DEV), w2, torch.from_numpy(s2).to(DEV), twt, idt)
+            yn = y.cpu().numpy()
+            if rep == 0:
+                ref = O.moe_runtime(x, ids, tw, q13, s13, q2, s2)
+                # silu's exp is correctly rounded on neither side: a requant code may differ by one
+                same = np.array_equal(yn.view(np.uint16), ref.view(np.uint16))
+                exact += same
+                assert same or _rel(yn.astype(np.float32), ref.astype(np.float32)) <= 1e-3, li
+                first.append(yn)
+            else:   # the re-laid weights give the same bits as the first call
+                assert np.array_equal(yn.view(np.uint16), first[li].view(np.uint16)), li
+            assert w13.shape == (e, h, 2 * inter) and torch.equal(w13.cpu(), torch.from_numpy(q13.transpose(0, 2, 1)))
+        assert layout_conversions() - base == 2 * layers
+    _say("bit-exact layers", exact, "of", layers)
+    assert exact >= layers // 2
+    # the method's own loading path: no conversion at all
+    meth = W8A8DynamicFusedMoEMethod(torch.float16)
+    base = layout_conversions()
+    for li, (q13, s13, q2, s2) in enumerate(stack[:4]):
+        layer = Layer()
+        layer.w13_weight = nn.Parameter(torch.from_numpy(q13).to(DEV), requires_grad=False)
+        layer.w2_weight = nn.Parameter(torch.from_numpy(q2).to(DEV), requires_grad=False)
+        layer.w13_weight_scale = nn.Parameter(torch.from_numpy(s13).half().reshape(e, -1, 1).to(DEV),
+                                              requires_grad=False)
+        layer.w2_weight_scale = nn.Parameter(torch.from_numpy(s2).half().reshape(e, -1, 1).to(DEV),
+                                             requires_grad=False)
+        layer.w13_weight_offset = nn.Parameter(torch.zeros(e, 2 * inter, 1, device=DEV), requires_grad=False)
+        layer.w2_weight_offset = nn.Parameter(torch.zeros(e, h, 1, device=DEV), requires_grad=False)
+        meth.process_weights_after_loading(layer)
+        assert layer.w13_weight.shape == (e, h, 2 * inter) and layer.w2_weight.shape == (e, inter, h)
+        assert layer.w13_weight_scale.shape == (e, 2 * inter) and layer.w2_weight_scale_fp32.dtype == torch.float32
+        y = meth.apply(layer, xt, twt, idt)
+        s13h = layer.w13_weight_scale_fp32.cpu().numpy()
+        s2h = layer.w2_weight_scale_fp32.cpu().numpy()
+        ref = O.moe_runtime(x, ids, tw.astype(np.float16).astype(np.float32), q13, s13h, q2, s2h)
+        yn = y.cpu().numpy()
+        assert np.array_equal(yn.view(np.uint16), ref.view(np.uint16)) or \
+            _rel(yn.astype(np.float32), ref.astype(np.float32)) <= 1e-3, li
+    assert layout_conversions() == base
+    with pytest.raises(ValueError):   # kernel-layout weights are not the runtime contract
+        fused_experts_w8a8(xt, torch.from_numpy(stack[0][0]).to(DEV), torch.from_numpy(stack[0][1]).to(DEV),
+                           torch.from_numpy(stack[0][2]).to(DEV), torch.from_numpy(stack[0][3]).to(DEV), twt, idt)
 
 
 def test_runtime_apply_contract():
