@@ -1,31 +1,34 @@
 """Ascend ``W8A8_DYNAMIC`` checkpoints: writer, verifier and loader.
 
-The on-disk format is the one ``scripts/repro/export_fp16_to_ascend_w8a8_dynamic_probe.py`` writes for
-a dense Qwen2 / Qwen2.5 model (``:175-257``) and the vLLM-Ascend ``W8A8_DYNAMIC`` linear method reads
-(``vllm_ascend.patch:3935-4033``):
+The on-disk format is the one the reference's dense-Qwen2 export writes
+(``scripts/repro/export_fp16_to_ascend_w8a8_dynamic_probe.py:175-257``) and the vLLM-Ascend
+``W8A8_DYNAMIC`` linear method reads (``vllm_ascend.patch:3935-4033``):
 
-* each decoder linear ``model.layers.{i}.{q,k,v,o}_proj`` / ``mlp.{gate,up,down}_proj`` stores
-  ``.weight`` int8 ``[N, K]`` (per-output-channel, the fp32 rule
-  ``s = max|w| / 127`` clamped at 1e-8, ``q = round(w / s).clamp(-127, 127)``), ``.weight_scale``
-  ``[N, 1]`` and ``.weight_offset`` ``[N, 1]`` (zeros), both in the source weight's dtype;
-* every other tensor is copied unchanged;
-* ``quant_model_description.json`` maps each quantized weight (and the fused ``qkv_proj`` /
-  ``gate_up_proj`` names the runtime packs) to ``"W8A8_DYNAMIC"`` and ``embed_tokens`` / ``lm_head``
-  to ``"FLOAT"``; ``model.safetensors.index.json`` indexes the shards; the config loses its
-  ``quantization_config`` / ``compression_config``; tokenizer files are copied.
+* each decoder linear ``model.layers.{i}.self_attn.{q,k,v,o}_proj`` / ``mlp.{gate,up,down}_proj``
+  stores ``.weight`` int8 ``[N, K]`` (per output channel: ``s = fp32(max|w|) / 127`` clamped at
+  1e-8, ``q = round(w / s)`` clamped to +-127), ``.weight_scale`` ``[N, 1]`` and ``.weight_offset``
+  ``[N, 1]`` (zeros), both in the source weight's dtype;
+* every other tensor keeps its name, shard, dtype and values;
+* ``quant_model_description.json`` marks each quantized weight, and the fused ``qkv_proj`` /
+  ``gate_up_proj`` names the runtime packs them into, ``"W8A8_DYNAMIC"``, and ``embed_tokens`` /
+  ``lm_head`` ``"FLOAT"``; ``model.safetensors.index.json`` maps every tensor to its shard; the
+  config loses ``quantization_config`` / ``compression_config``; tokenizer files come along.
 
-``export_w8a8_dynamic`` quantizes with the GPU export quantizer (bit-exact to the fp32 rule) and
-verifies what it wrote; ``verify_w8a8_dynamic`` is the verify-only check; ``load_w8a8_dynamic`` puts
-an export into a model as ``W8A8DynamicLinear`` (the runtime method's layer) or ``SmoothQuantLinear``
-modules holding the stored int8 codes and scales -- no requantization.
+How this module is organised.  A checkpoint is handled as a *manifest*: for every tensor name, its
+shard, dtype and shape, read from the safetensors headers (eight-byte length, then JSON) without
+loading any tensor data.  The export is planned from the source manifest as the manifest the output
+must have (``_expected_output``); the writer streams the source shard by shard on the GPU export
+quantizer; the verifier reads the output's manifest back and compares it with the planned one,
+together with the description and the index, and reports every mismatch it finds at once.  The
+loader puts an export into a model from the same manifest.
 """
 from __future__ import annotations
 
-import gc
 import json
 import shutil
+from dataclasses import dataclass
 from pathlib import Path
-from typing import Dict, List, Optional, Set, Tuple
+from typing import Dict, Iterable, List, Optional, Tuple
 
 import torch
 from torch import nn
@@ -33,277 +36,287 @@ from torch import nn
 from . import ops
 from .runtime import W8A8DynamicLinearMethod
 
-__all__ = ["QUANT_TYPE", "FLOAT_TYPE", "LINEAR_SUFFIXES", "export_w8a8_dynamic", "verify_w8a8_dynamic",
-           "load_w8a8_dynamic", "W8A8DynamicLinear"]
+__all__ = ["QUANT_TYPE", "FLOAT_TYPE", "LINEAR_SUFFIXES", "read_config", "export_w8a8_dynamic",
+           "verify_w8a8_dynamic", "load_w8a8_dynamic", "W8A8DynamicLinear"]
 
+# ------------------------------------------------------------------ the format
 QUANT_TYPE = "W8A8_DYNAMIC"
 FLOAT_TYPE = "FLOAT"
-MODEL_TYPE = "qwen2"
-ARCHITECTURE = "Qwen2ForCausalLM"
-# the tokenizer / generation files an export carries over from its source
-INFERENCE_FILE_NAMES = ("added_tokens.json", "chat_template.json", "chat_template.jinja", "generation_config.json",
-                        "merges.txt", "special_tokens_map.json", "tokenizer.json", "tokenizer.model",
-                        "tokenizer_config.json", "vocab.json")
 LINEAR_SUFFIXES = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
                    "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
-_FLOAT_DTYPES = {"BF16", "F16", "F32", "F64"}
-_TERMINALS = ("model.embed_tokens.weight", "lm_head.weight")
+PACKED_SUFFIXES = ("self_attn.qkv_proj", "mlp.gate_up_proj")   # the runtime's fused module names
+TERMINAL_WEIGHTS = ("model.embed_tokens.weight", "lm_head.weight")
+TOKENIZER_FILES = ("added_tokens.json", "chat_template.json", "chat_template.jinja", "generation_config.json",
+                   "merges.txt", "special_tokens_map.json", "tokenizer.json", "tokenizer.model",
+                   "tokenizer_config.json", "vocab.json")
+INDEX_FILE = "model.safetensors.index.json"
+DESCRIPTION_FILE = "quant_model_description.json"
+_DENSE_QWEN2 = ("qwen2", "Qwen2ForCausalLM")
+_INT8 = "I8"
+_FLOATS = frozenset({"F16", "BF16", "F32", "F64"})
+_SIDE_TENSORS = ("weight_scale", "weight_offset")
 
 
-# ------------------------------------------------------------------ source checks
-def _paths(source, output) -> Tuple[Path, Path]:
+def _json(path: Path):
+    return json.loads(path.read_text(encoding="utf-8"))
+
+
+def _write_json(path: Path, obj) -> None:
+    path.write_text(json.dumps(obj, ensure_ascii=False, indent=2) + "\n", encoding="utf-8")
+
+
+# ------------------------------------------------------------------ manifests
+@dataclass(frozen=True)
+class TensorInfo:
+    shard: str
+    dtype: str        # safetensors dtype tag ("F16", "BF16", "I8", ...)
+    shape: Tuple[int, ...]
+
+
+def _header(shard: Path) -> Dict[str, Tuple[str, Tuple[int, ...]]]:
+    """``{tensor: (dtype, shape)}`` of one safetensors file, from its JSON header alone."""
+    with open(shard, "rb") as f:
+        size = int.from_bytes(f.read(8), "little")
+        if size <= 0 or size > (1 << 27):
+            raise ValueError(f"{shard} is not a safetensors file (header size {size})")
+        head = json.loads(f.read(size))
+    return {k: (v["dtype"].upper(), tuple(int(d) for d in v["shape"])) for k, v in head.items() if k != "__metadata__"}
+
+
+def _headers_of(directory: Path, shards: Iterable[str]) -> Dict[str, TensorInfo]:
+    man: Dict[str, TensorInfo] = {}
+    for shard in sorted(set(shards)):
+        for name, (dt, shape) in _header(directory / shard).items():
+            if name in man:
+                raise ValueError(f"tensor {name} appears in both {man[name].shard} and {shard}")
+            man[name] = TensorInfo(shard, dt, shape)
+    return man
+
+
+def _index(directory: Path) -> Optional[Dict[str, str]]:
+    """The index's ``weight_map`` (tensor -> shard file), checked for plain file names, or None."""
+    path = directory / INDEX_FILE
+    if not path.is_file():
+        return None
+    wm = _json(path).get("weight_map")
+    if not isinstance(wm, dict) or not wm:
+        raise ValueError(f"{path} has no weight_map")
+    for name, shard in wm.items():
+        if not isinstance(name, str) or not name or not isinstance(shard, str) or Path(shard).name != shard \
+                or shard in ("", ".", ".."):
+            raise ValueError(f"{path} maps {name!r} to an unsafe shard name {shard!r}")
+    return wm
+
+
+def _manifest(directory: Path) -> Dict[str, TensorInfo]:
+    """A checkpoint's manifest: the shards its index names, or every ``*.safetensors`` file."""
+    wm = _index(directory)
+    if wm is None:
+        shards = [p.name for p in directory.glob("*.safetensors")]
+        if not shards:
+            raise FileNotFoundError(f"no safetensors checkpoint in {directory}")
+        return _headers_of(directory, shards)
+    missing = sorted({s for s in wm.values() if not (directory / s).is_file()})
+    if missing:
+        raise FileNotFoundError(f"{directory} lacks shard file(s) named by its index: {', '.join(missing)}")
+    man = _headers_of(directory, wm.values())
+    absent = sorted(n for n, s in wm.items() if n not in man or man[n].shard != s)
+    if absent:
+        raise ValueError(f"{len(absent)} indexed tensor(s) are not in their shard; first: {', '.join(absent[:8])}")
+    return {n: man[n] for n in wm}
+
+
+_ELEM_BYTES = {"F64": 8, "I64": 8, "F32": 4, "I32": 4, "F16": 2, "BF16": 2, "I16": 2, "I8": 1, "U8": 1, "BOOL": 1}
+
+
+def _nbytes(info: TensorInfo) -> int:
+    n = 1
+    for d in info.shape:
+        n *= d
+    return n * _ELEM_BYTES.get(info.dtype, 1)
+
+
+def _by_shard(names: Iterable[str], man: Dict[str, TensorInfo]) -> Dict[str, List[str]]:
+    out: Dict[str, List[str]] = {}
+    for n in sorted(names):
+        out.setdefault(man[n].shard, []).append(n)
+    return out
+
+
+# ------------------------------------------------------------------ the source
+def _directories(source, output) -> Tuple[Path, Path]:
     src, out = Path(source).expanduser().resolve(), Path(output).expanduser().resolve()
     if not src.is_dir():
-        raise FileNotFoundError(f"Source checkpoint directory does not exist: {src}")
-    if src == out or src in out.parents or out in src.parents:
-        raise ValueError(f"source and output must be separate, non-nested directories: source={src}, output={out}")
+        raise FileNotFoundError(f"source checkpoint directory {src} does not exist")
+    nested = src == out or src in out.parents or out in src.parents
+    if nested:
+        raise ValueError(f"export needs separate, non-nested source and output directories (source {src}, "
+                         f"output {out})")
     return src, out
 
 
 def read_config(source) -> dict:
-    """``config.json`` of a dense Qwen2 / Qwen2.5 checkpoint (the only family the format covers)."""
+    """``config.json`` of the source, which must describe a dense Qwen2 / Qwen2.5 causal LM with at
+    least one decoder layer (the one family the format is defined for)."""
     path = Path(source) / "config.json"
     if not path.is_file():
-        raise FileNotFoundError(f"Missing config.json in {source}")
-    cfg = json.loads(path.read_text(encoding="utf-8"))
+        raise FileNotFoundError(f"{path} does not exist")
+    cfg = _json(path)
     if not isinstance(cfg, dict):
-        raise ValueError(f"Invalid JSON object in {path}")
-    if cfg.get("model_type") != MODEL_TYPE:
-        raise ValueError(f"Expected dense Qwen2/Qwen2.5 model_type={MODEL_TYPE!r}, got {cfg.get('model_type')!r}.")
-    if ARCHITECTURE not in (cfg.get("architectures") or []):
-        raise ValueError(f"Expected architectures to contain {ARCHITECTURE!r}, got {cfg.get('architectures')!r}.")
-    try:
-        layers = int(cfg["num_hidden_layers"])
-    except (KeyError, TypeError, ValueError) as exc:
-        raise ValueError("config.json has no valid num_hidden_layers") from exc
-    if layers <= 0:
-        raise ValueError("num_hidden_layers must be positive")
+        raise ValueError(f"{path} does not hold a JSON object")
+    mt, arch = _DENSE_QWEN2
+    if cfg.get("model_type") != mt or arch not in (cfg.get("architectures") or []):
+        raise ValueError(f"Expected dense Qwen2/Qwen2.5 checkpoint (model_type {mt!r}, architecture {arch!r}); "
+                         f"{path} has model_type {cfg.get('model_type')!r}, architectures {cfg.get('architectures')!r}")
+    layers = cfg.get("num_hidden_layers")
+    if isinstance(layers, bool) or not isinstance(layers, int) or layers < 1:
+        raise ValueError(f"{path}: num_hidden_layers must be a positive integer, got {layers!r}")
     return cfg
 
 
-def _shard_name(name, where) -> str:
-    if not isinstance(name, str) or not name or Path(name).name != name:
-        raise ValueError(f"Invalid or unsafe shard name in {where}: {name!r}")
-    return name
+def _linear_weights(cfg: dict) -> List[str]:
+    return [f"model.layers.{i}.{s}.weight" for i in range(cfg["num_hidden_layers"]) for s in LINEAR_SUFFIXES]
 
 
-def _read_index(directory: Path) -> Optional[Dict[str, str]]:
-    idx = directory / "model.safetensors.index.json"
-    if not idx.is_file():
-        return None
-    data = json.loads(idx.read_text(encoding="utf-8"))
-    wm = data.get("weight_map") if isinstance(data, dict) else None
-    if not isinstance(wm, dict) or not wm:
-        raise ValueError(f"Invalid weight_map in {idx}")
-    out = {}
-    for t, f in wm.items():
-        if not isinstance(t, str) or not t:
-            raise ValueError(f"Invalid tensor name in {idx}: {t!r}")
-        out[t] = _shard_name(f, idx)
-    return out
+def _description(cfg: dict, quantized: Iterable[str]) -> Dict[str, str]:
+    desc = {t: FLOAT_TYPE for t in TERMINAL_WEIGHTS}
+    desc.update({t: QUANT_TYPE for t in quantized})
+    for i in range(cfg["num_hidden_layers"]):
+        desc.update({f"model.layers.{i}.{s}.weight": QUANT_TYPE for s in PACKED_SUFFIXES})
+    return dict(sorted(desc.items()))
 
 
-def _scan_shards(directory: Path) -> Dict[str, str]:
-    from safetensors import safe_open
-    shards = sorted(directory.glob("*.safetensors"))
-    if not shards:
-        raise FileNotFoundError(f"No safetensors checkpoint found in {directory}")
-    wm: Dict[str, str] = {}
-    for sp in shards:
-        with safe_open(str(sp), framework="pt", device="cpu") as f:
-            for t in f.keys():
-                if t in wm:
-                    raise ValueError(f"Duplicate tensor across shards: {t}")
-                wm[t] = sp.name
-    return wm
-
-
-def _source_map(source: Path) -> Dict[str, str]:
-    wm = _read_index(source)
-    if wm is None:
-        if not (source / "model.safetensors").is_file():
-            raise FileNotFoundError(f"No safetensors checkpoint found in {source}")
-        return _scan_shards(source)
-    for f in set(wm.values()):
-        if not (source / f).is_file():
-            raise FileNotFoundError(f"Source shard missing: {source / f}")
-    return wm
-
-
-def quantized_weight_names(cfg: dict) -> Set[str]:
-    return {f"model.layers.{i}.{s}.weight" for i in range(int(cfg["num_hidden_layers"])) for s in LINEAR_SUFFIXES}
-
-
-def _by_file(wm: Dict[str, str]) -> Dict[str, List[str]]:
-    out: Dict[str, List[str]] = {}
-    for t, f in wm.items():
-        out.setdefault(f, []).append(t)
-    return out
+def _expected_output(src_man: Dict[str, TensorInfo], quantized: List[str]) -> Dict[str, TensorInfo]:
+    """The manifest the export must have: every source tensor in its shard, each quantized weight as
+    int8 of its shape with ``[N, 1]`` scale and offset in the source weight's dtype beside it."""
+    missing = [t for t in quantized if t not in src_man]
+    if missing:
+        raise ValueError(f"source checkpoint is missing {len(missing)} required linear weight(s) of its decoder "
+                         f"layers: {', '.join(missing[:8])}")
+    exp = dict(src_man)
+    for t in quantized:
+        info = src_man[t]
+        if len(info.shape) != 2:
+            raise ValueError(f"{t} has shape {info.shape}; a linear weight is [N, K]")
+        if info.dtype not in _FLOATS:
+            raise ValueError(f"{t} is {info.dtype}: the export quantizes a floating-point weight")
+        base = t[: -len(".weight")]
+        exp[t] = TensorInfo(info.shard, _INT8, info.shape)
+        for side in _SIDE_TENSORS:
+            exp[f"{base}.{side}"] = TensorInfo(info.shard, info.dtype, (info.shape[0], 1))
+    return exp
 
 
 # ------------------------------------------------------------------ writer
-def _quantize_export(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """The export quantizer of one weight on the GPU: ``(int8 [N, K], scale [N, 1], offset [N, 1])``,
-    scale and offset in the weight's dtype (``export_fp16_to_ascend_w8a8_dynamic_probe.py:175-195``)."""
-    if w.ndim != 2:
-        raise ValueError(f"Expected a two-dimensional Linear weight, got {tuple(w.shape)}")
+def _quantize(name: str, w: torch.Tensor) -> Dict[str, torch.Tensor]:
+    """One linear weight through the GPU export quantizer (bit-exact to the fp32 rule,
+    ``export_fp16_to_ascend_w8a8_dynamic_probe.py:175-195``): its int8 codes, scale and zero offset."""
     if not w.is_floating_point():
-        raise ValueError(f"Expected a floating-point source weight, got {w.dtype}")
+        raise ValueError(f"{name}: the export needs a floating-point weight, got {w.dtype}")
     if w.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"the GPU export quantizer takes fp16 / bf16 weights, got {w.dtype}")
+        raise ValueError(f"{name}: the GPU export quantizer takes fp16 or bf16 weights, got {w.dtype}")
     if not torch.cuda.is_available():
-        raise RuntimeError("the W8A8 export quantizer runs on the GPU only; no GPU is visible")
-    q, _s32, ssrc = ops.w8_quantize_per_channel(w.cuda().contiguous(), "export")
-    scale = ssrc.reshape(-1, 1).cpu().contiguous()
-    return q.cpu().contiguous(), scale, torch.zeros_like(scale)
+        raise RuntimeError("the W8A8 export quantizer runs on the GPU; none is visible")
+    q, _, scale = ops.w8_quantize_per_channel(w.cuda().contiguous(), "export")
+    scale = scale.reshape(-1, 1).cpu()
+    base = name[: -len(".weight")]
+    return {name: q.cpu(), f"{base}.weight_scale": scale, f"{base}.weight_offset": torch.zeros_like(scale)}
 
 
 def export_w8a8_dynamic(source, output, *, overwrite: bool = False) -> dict:
-    """Convert a dense fp16 / bf16 Qwen2 checkpoint to ``W8A8_DYNAMIC``, then verify it.  Returns the
-    conversion summary (also written to ``conversion_summary.json``)."""
+    """Write the ``W8A8_DYNAMIC`` export of a dense fp16 / bf16 Qwen2 checkpoint into ``output``,
+    then verify it.  Returns (and stores as ``conversion_summary.json``) the export summary:
+    ``converted_linear_modules``, ``output_tensors``, ``quant_description_entries`` and the
+    verifier's report under ``validation``."""
     from safetensors import safe_open
     from safetensors.torch import save_file
-    src, out = _paths(source, output)
+    src, out = _directories(source, output)
     cfg = read_config(src)
-    src_map = _source_map(src)
-    qnames = quantized_weight_names(cfg)
-    missing = sorted(qnames - set(src_map))
-    if missing:
-        raise ValueError(f"Source checkpoint is missing {len(missing)} required dense Qwen2 Linear weights; "
-                         f"first entries: {', '.join(missing[:8])}")
+    src_man = _manifest(src)
+    quantized = _linear_weights(cfg)
+    expected = _expected_output(src_man, quantized)
     if out.exists():
         if not overwrite:
-            raise FileExistsError(f"{out} already exists; pass overwrite=True to replace it")
+            raise FileExistsError(f"{out} exists; pass overwrite=True to replace it")
         shutil.rmtree(out)
     out.mkdir(parents=True)
-    for name in INFERENCE_FILE_NAMES:
-        if (src / name).is_file():
-            shutil.copy2(src / name, out / name)
-    clean = {k: v for k, v in cfg.items() if k not in ("compression_config", "quantization_config")}
-    (out / "config.json").write_text(json.dumps(clean, ensure_ascii=False, indent=2) + "\n", encoding="utf-8")
-    desc = {t: FLOAT_TYPE for t in _TERMINALS}
-    for t in sorted(qnames):
-        desc[t] = QUANT_TYPE
-    for i in range(int(cfg["num_hidden_layers"])):
-        desc[f"model.layers.{i}.self_attn.qkv_proj.weight"] = QUANT_TYPE
-        desc[f"model.layers.{i}.mlp.gate_up_proj.weight"] = QUANT_TYPE
-    (out / "quant_model_description.json").write_text(json.dumps(desc, ensure_ascii=False, indent=2) + "\n",
-                                                      encoding="utf-8")
-    out_map: Dict[str, str] = {}
-    converted = n_tensors = total = 0
-    for fname, names in sorted(_by_file(src_map).items()):
-        tensors: Dict[str, torch.Tensor] = {}
-        with safe_open(str(src / fname), framework="pt", device="cpu") as f:
-            avail = set(f.keys())
-            lost = sorted(set(names) - avail)
-            if lost:
-                raise ValueError(f"{fname} misses {len(lost)} indexed tensors; first: {', '.join(lost[:8])}")
-            for t in sorted(names):
-                v = f.get_tensor(t)
-                if t in qnames:
-                    q, sc, off = _quantize_export(v)
-                    p = t[: -len(".weight")]
-                    tensors.update({t: q, f"{p}.weight_scale": sc, f"{p}.weight_offset": off})
-                    converted += 1
-                else:
-                    tensors[t] = v
-        save_file(tensors, str(out / fname))
-        for t, v in tensors.items():
-            out_map[t] = fname
-            total += v.numel() * v.element_size()
-        n_tensors += len(tensors)
-        del tensors
-        gc.collect()
-    (out / "model.safetensors.index.json").write_text(
-        json.dumps({"metadata": {"total_size": total}, "weight_map": dict(sorted(out_map.items()))},
-                   ensure_ascii=False, indent=2) + "\n", encoding="utf-8")
-    report = verify_w8a8_dynamic(out, src)
-    summary = {"source": str(src), "output": str(out), "model_type": cfg["model_type"], "architecture": ARCHITECTURE,
-               "converted_linear_modules": converted, "output_tensors": n_tensors,
-               "quant_description_entries": len(desc), "format": "ascend_w8a8_dynamic_probe_from_fp16",
-               "validation": report,
-               "notes": "Dense transformer block Linear weights are W8A8_DYNAMIC; embed_tokens and lm_head remain FLOAT."}
-    (out / "conversion_summary.json").write_text(json.dumps(summary, ensure_ascii=False, indent=2) + "\n",
-                                                 encoding="utf-8")
+    qset = set(quantized)
+    for shard, names in _by_shard(src_man, src_man).items():
+        written: Dict[str, torch.Tensor] = {}
+        with safe_open(str(src / shard), framework="pt", device="cpu") as f:
+            for n in names:
+                t = f.get_tensor(n)
+                written.update(_quantize(n, t) if n in qset else {n: t})
+        save_file(written, str(out / shard))
+        del written
+    total = sum(_nbytes(i) for i in expected.values())
+    _write_json(out / INDEX_FILE, {"metadata": {"total_size": total},
+                                   "weight_map": {n: i.shard for n, i in sorted(expected.items())}})
+    desc = _description(cfg, quantized)
+    _write_json(out / DESCRIPTION_FILE, desc)
+    _write_json(out / "config.json",
+                {k: v for k, v in cfg.items() if k not in ("quantization_config", "compression_config")})
+    for fname in TOKENIZER_FILES:
+        if (src / fname).is_file():
+            shutil.copy2(src / fname, out / fname)
+    summary = {"source": str(src), "output": str(out), "quant_type": QUANT_TYPE,
+               "converted_linear_modules": len(quantized), "output_tensors": len(expected),
+               "quant_description_entries": len(desc), "validation": verify_w8a8_dynamic(out, src)}
+    _write_json(out / "conversion_summary.json", summary)
     return summary
 
 
 # ------------------------------------------------------------------ verifier
 def verify_w8a8_dynamic(output, source) -> dict:
-    """Check an export against its source: every source tensor present, each quantized weight int8
-    ``[N, K]`` with ``weight_scale`` / ``weight_offset`` ``[N, 1]`` in the source weight's dtype, the
-    description's ``W8A8_DYNAMIC`` / ``FLOAT`` entries, and (when present) the index against the shards."""
-    from safetensors import safe_open
+    """Compare an export with the manifest planned from its source.  Checked: every planned tensor
+    is in the output's shards with the planned dtype and shape (int8 ``[N, K]`` weights,
+    ``[N, 1]`` scales and offsets in the source weight's dtype, the rest unchanged); the index, when
+    present, maps each planned tensor to the shard that holds it; the description marks each
+    quantized weight ``W8A8_DYNAMIC`` and the terminal weights ``FLOAT``.  Every mismatch is
+    reported in one ``ValueError``."""
     src, out = Path(source).resolve(), Path(output).resolve()
     if not out.is_dir():
-        raise FileNotFoundError(f"Output checkpoint directory does not exist: {out}")
+        raise FileNotFoundError(f"export directory {out} does not exist")
     cfg = read_config(src)
-    src_map = _source_map(src)
-    qnames = quantized_weight_names(cfg)
-    indexed = _read_index(out)
-    actual = _scan_shards(out)
-    expected = set(src_map)
-    for t in qnames:
-        p = t[: -len(".weight")]
-        expected |= {f"{p}.weight_scale", f"{p}.weight_offset"}
-    missing = sorted(expected - set(actual))
-    if missing:
-        raise ValueError(f"Output misses {len(missing)} required tensors; first: {', '.join(missing[:8])}")
-    if indexed is not None:
-        lost = sorted(expected - set(indexed))
-        if lost:
-            raise ValueError(f"Output index misses {len(lost)} required tensors; first: {', '.join(lost[:8])}")
-        wrong = sorted(t for t in expected if indexed[t] != actual[t])
-        if wrong:
-            raise ValueError(f"Output index maps {len(wrong)} tensors to the wrong shard; first: {', '.join(wrong[:8])}")
-    dpath = out / "quant_model_description.json"
-    if not dpath.is_file():
-        raise FileNotFoundError(f"Missing quantization description: {dpath}")
-    desc = json.loads(dpath.read_text(encoding="utf-8"))
+    src_man = _manifest(src)
+    quantized = _linear_weights(cfg)
+    expected = _expected_output(src_man, quantized)
+    shards = [p.name for p in out.glob("*.safetensors")]
+    if not shards:
+        raise FileNotFoundError(f"no safetensors shards in {out}")
+    actual = _headers_of(out, shards)
+    problems: List[str] = []
+    for n, want in expected.items():
+        got = actual.get(n)
+        if got is None:
+            problems.append(f"{n} is missing")
+            continue
+        if got.dtype != want.dtype:
+            kind = "expected source weight dtype" if n.endswith(_SIDE_TENSORS) else "expected"
+            problems.append(f"{n}: dtype {got.dtype}, {kind} {want.dtype}")
+        if got.shape != want.shape:
+            problems.append(f"{n}: shape {got.shape}, expected {want.shape}")
+    index = _index(out)
+    if index is not None:
+        for n in expected:
+            if n in actual and index.get(n) != actual[n].shard:
+                problems.append(f"index maps {n} to {index.get(n)!r}, but it is in {actual[n].shard!r}")
+    desc_path = out / DESCRIPTION_FILE
+    desc = _json(desc_path) if desc_path.is_file() else None
     if not isinstance(desc, dict):
-        raise ValueError(f"Invalid quantization description: {dpath}")
-    bad = sorted(t for t in qnames if desc.get(t) != QUANT_TYPE)
-    if bad:
-        raise ValueError(f"Description has {len(bad)} invalid W8A8_DYNAMIC entries; first: {', '.join(bad[:8])}")
-    terminals = set(_TERMINALS) & set(src_map)
-    bad = sorted(t for t in terminals if desc.get(t) != FLOAT_TYPE)
-    if bad:
-        raise ValueError("Description does not keep terminal weights FLOAT: " + ", ".join(bad))
-    src_dtypes = {}
-    for fname, names in _by_file(src_map).items():
-        want = qnames.intersection(names)
-        if want:
-            with safe_open(str(src / fname), framework="pt", device="cpu") as f:
-                for t in want:
-                    src_dtypes[t] = str(f.get_slice(t).get_dtype()).upper()
-    checked = 0
-    for fname, names in _by_file({t: actual[t] for t in qnames}).items():
-        with safe_open(str(out / fname), framework="pt", device="cpu") as f:
-            for t in sorted(names):
-                if str(f.get_slice(t).get_dtype()).upper() not in {"I8", "INT8"}:
-                    raise ValueError(f"{t} has dtype {f.get_slice(t).get_dtype()}, expected int8")
-                shape = tuple(f.get_slice(t).get_shape())
-                if len(shape) != 2:
-                    raise ValueError(f"{t} has invalid shape {shape}")
-                p = t[: -len(".weight")]
-                for suf in ("weight_scale", "weight_offset"):
-                    pn = f"{p}.{suf}"
-                    dt = str(f.get_slice(pn).get_dtype()).upper()
-                    if dt != src_dtypes[t]:
-                        raise ValueError(f"{pn} has dtype {dt}, expected source weight dtype {src_dtypes[t]}")
-                    if tuple(f.get_slice(pn).get_shape()) != (shape[0], 1):
-                        raise ValueError(f"{pn} has shape {tuple(f.get_slice(pn).get_shape())}, expected ({shape[0]}, 1)")
-                checked += 1
-    for t in sorted(terminals):
-        with safe_open(str(out / actual[t]), framework="pt", device="cpu") as f:
-            if str(f.get_slice(t).get_dtype()).upper() not in _FLOAT_DTYPES:
-                raise ValueError(f"{t} is not floating point")
-    if checked != len(qnames):
-        raise AssertionError(f"Validated {checked} quantized weights, expected {len(qnames)}")
-    return {"validated_linear_weights": checked, "validated_scale_offset_pairs": checked,
-            "validated_float_terminal_weights": len(terminals), "all_linear_weights_int8": True,
-            "all_scale_offset_shapes_valid": True, "all_scale_offset_dtypes_match_source": True,
-            "output_index_present": indexed is not None}
+        problems.append(f"{DESCRIPTION_FILE} is missing or not a JSON object")
+        desc = {}
+    problems += [f"description marks {t} {desc.get(t)!r}, not {QUANT_TYPE}" for t in quantized
+                 if desc.get(t) != QUANT_TYPE]
+    terminals = [t for t in TERMINAL_WEIGHTS if t in src_man]
+    problems += [f"description marks {t} {desc.get(t)!r}, not {FLOAT_TYPE}" for t in terminals
+                 if desc.get(t) != FLOAT_TYPE]
+    if problems:
+        head = "; ".join(problems[:8])
+        raise ValueError(f"W8A8_DYNAMIC export {out} fails {len(problems)} check(s): {head}")
+    return {"validated_linear_weights": len(quantized), "validated_scale_offset_pairs": len(quantized),
+            "validated_float_terminal_weights": len(terminals), "checked_tensors": len(expected),
+            "output_index_present": index is not None}
 
 
 # ------------------------------------------------------------------ loader
@@ -330,70 +343,69 @@ class W8A8DynamicLinear(nn.Module):
         return self.quant_method.apply(self, x, b)
 
 
-def _set_module(model: nn.Module, name: str, new: nn.Module) -> None:
-    parent, _, child = name.rpartition(".")
-    setattr(model.get_submodule(parent) if parent else model, child, new)
+def _quantized_module(lin: nn.Linear, q, scale, bias, target: str) -> nn.Module:
+    from .smoothquant import SmoothQuantLinear
+    dev, pdt = lin.weight.device, lin.weight.dtype
+    if target == "runtime":
+        off = torch.zeros_like(scale)
+        return W8A8DynamicLinear(q.to(dev), scale.to(dev), off.to(dev), None if bias is None else bias.to(dev), pdt)
+    new = SmoothQuantLinear(lin.in_features, lin.out_features, bias is not None, dtype=pdt,
+                            scale_rule="export").to(dev)
+    new.weight = q.to(dev)
+    new.weight_scale = scale.reshape(-1).to(device=dev, dtype=torch.float32)
+    if bias is not None:
+        new.bias = bias.to(device=dev, dtype=pdt)
+    return new
 
 
 @torch.no_grad()
 def load_w8a8_dynamic(model: nn.Module, export_dir, *, target: str = "runtime") -> List[str]:
-    """Load a ``W8A8_DYNAMIC`` export into ``model`` without requantizing: each quantized weight's
-    ``nn.Linear`` becomes a ``W8A8DynamicLinear`` (``target="runtime"``) or a ``SmoothQuantLinear``
-    with the export scale rule (``target="smoothquant"``) holding the stored codes, the fp32 copy of
-    the stored scale and the linear's bias; every other tensor is copied into the model's parameter
-    or buffer of that name.  Returns the replaced module names."""
+    """Load a ``W8A8_DYNAMIC`` export into ``model`` without requantizing.  Each weight the
+    description marks ``W8A8_DYNAMIC`` and the checkpoint holds replaces its ``nn.Linear`` with a
+    ``W8A8DynamicLinear`` (``target="runtime"``) or a ``SmoothQuantLinear`` on the export scale
+    rule (``target="smoothquant"``): the stored codes, the fp32 value of the stored scale and the
+    linear's bias (the checkpoint's, else the module's).  Every other checkpoint tensor is copied
+    into the model's parameter or buffer of that name.  Returns the replaced module names."""
     from safetensors import safe_open
-    from .smoothquant import SmoothQuantLinear
     if target not in ("runtime", "smoothquant"):
         raise ValueError(f"unknown target {target!r}")
     d = Path(export_dir)
-    desc = json.loads((d / "quant_model_description.json").read_text(encoding="utf-8"))
-    wm = _read_index(d) or _scan_shards(d)
-    qset = {t for t, kind in desc.items() if kind == QUANT_TYPE and t in wm}
-    done: List[str] = []
-    handled: Set[str] = set()
-    for fname, names in sorted(_by_file(wm).items()):
-        with safe_open(str(d / fname), framework="pt", device="cpu") as f:
-            for t in sorted(set(names) & qset):
-                p = t[: -len(".weight")]
-                lin = model.get_submodule(p)
+    man = _manifest(d)
+    desc = _json(d / DESCRIPTION_FILE)
+    modules = sorted(t[: -len(".weight")] for t, kind in desc.items() if kind == QUANT_TYPE and t in man)
+    consumed = set()
+    for base in modules:
+        consumed |= {f"{base}.weight", f"{base}.weight_scale", f"{base}.weight_offset", f"{base}.bias"}
+    replaced: List[str] = []
+    for shard, names in _by_shard(man, man).items():
+        with safe_open(str(d / shard), framework="pt", device="cpu") as f:
+            mine = [b for b in modules if man[f"{b}.weight"].shard == shard]
+            for base in mine:
+                lin = model.get_submodule(base)
                 if not isinstance(lin, nn.Linear):
-                    raise TypeError(f"{p} is {type(lin).__name__}, expected nn.Linear")
-                q = f.get_tensor(t)
-                if q.dtype != torch.int8 or tuple(q.shape) != tuple(lin.weight.shape):
-                    raise ValueError(f"{t}: int8 {tuple(lin.weight.shape)} expected, got {q.dtype} {tuple(q.shape)}")
-                sc, off = f.get_tensor(f"{p}.weight_scale"), f.get_tensor(f"{p}.weight_offset")
-                if torch.any(off != 0):
-                    raise ValueError(f"{p}.weight_offset is not zero: W8A8_DYNAMIC is symmetric")
-                bname = f"{p}.bias"
-                bias = (f.get_tensor(bname) if bname in wm and wm[bname] == fname else
-                        (lin.bias.detach().clone() if lin.bias is not None else None))
-                dev, pdt = lin.weight.device, lin.weight.dtype
-                if target == "runtime":
-                    new = W8A8DynamicLinear(q.to(dev), sc.to(dev), off.to(dev),
-                                            None if bias is None else bias.to(dev), pdt)
-                else:
-                    new = SmoothQuantLinear(lin.in_features, lin.out_features, bias is not None, dtype=pdt,
-                                            scale_rule="export").to(dev)
-                    new.weight = q.to(dev)
-                    new.weight_scale = sc.reshape(-1).to(device=dev, dtype=torch.float32)
-                    if bias is not None:
-                        new.bias = bias.to(device=dev, dtype=pdt)
-                _set_module(model, p, new)
-                done.append(p)
-                handled |= {t, f"{p}.weight_scale", f"{p}.weight_offset", bname}
-    for fname, names in sorted(_by_file(wm).items()):
-        rest = [t for t in names if t not in handled]
-        if not rest:
-            continue
-        with safe_open(str(d / fname), framework="pt", device="cpu") as f:
-            for t in rest:
+                    raise TypeError(f"{base} is a {type(lin).__name__}, not an nn.Linear")
+                q = f.get_tensor(f"{base}.weight")
+                if q.dtype != torch.int8 or q.shape != lin.weight.shape:
+                    raise ValueError(f"{base}.weight is {q.dtype} {tuple(q.shape)}; the model needs int8 "
+                                     f"{tuple(lin.weight.shape)}")
+                if torch.count_nonzero(f.get_tensor(f"{base}.weight_offset")):
+                    raise ValueError(f"{base}.weight_offset is not zero; W8A8_DYNAMIC weights are symmetric")
+                bname = f"{base}.bias"
+                bias = f.get_tensor(bname) if man.get(bname) is not None and man[bname].shard == shard else \
+                    (None if lin.bias is None else lin.bias.detach().clone())
+                parent, _, child = base.rpartition(".")
+                setattr(model.get_submodule(parent) if parent else model, child,
+                        _quantized_module(lin, q, f.get_tensor(f"{base}.weight_scale"), bias, target))
+                replaced.append(base)
+            for n in names:
+                if n in consumed:
+                    continue
                 try:
-                    dst = model.get_parameter(t)
+                    dst = model.get_parameter(n)
                 except AttributeError:
                     try:
-                        dst = model.get_buffer(t)
+                        dst = model.get_buffer(n)
                     except AttributeError:
                         continue
-                dst.data.copy_(f.get_tensor(t).to(dst.device))
-    return done
+                dst.data.copy_(f.get_tensor(n).to(dst.device))
+    return replaced

@@ -284,7 +284,7 @@ def w8_quantize_per_channel(w: torch.Tensor, rule: str = "export"):
             w.data_ptr(), n, k, _DT[w.dtype], q.data_ptr(), s32.data_ptr(), ssrc.data_ptr(), r, bad.data_ptr(),
             _stream()), "mp_w8_quantize_per_channel")
     if rule == "export" and int(bad.item()) != 0:
-        raise ValueError("Source weight contains non-finite values")
+        raise ValueError("the weight holds non-finite values; the export quantizer needs finite weights")
     return q, s32, ssrc
 
 

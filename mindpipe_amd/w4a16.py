@@ -13,7 +13,9 @@ Mirrors:
 """
 from __future__ import annotations
 
+import contextlib
 import json
+import shutil
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Dict, Iterable, List, Optional
@@ -309,126 +311,134 @@ def quantize_model_w4a16(model: nn.Module, group_size: int = 128, zero_point: bo
     return names
 
 
-# Files a vLLM export directory takes over from the source checkpoint (tokenizer, chat template,
-# generation and processor configs, remote-code modules) and the weight files it never copies: the
-# on-disk format of ``exporters/vllm.py:18-54``.
-_INFERENCE_FILES = ("tokenizer.json", "tokenizer_config.json", "special_tokens_map.json", "added_tokens.json",
-                    "vocab.*", "merges.txt", "*.model", "spiece.model", "sentencepiece.bpe.model",
-                    "chat_template*.jinja", "generation_config*.json", "preprocessor_config.json",
-                    "processor_config.json", "image_processor_config.json", "video_processor_config.json",
-                    "feature_extractor_config.json", "configuration.json", "configuration*.py", "modeling*.py",
-                    "processing*.py", "tokenization*.py", "image_processing*.py", "video_processing*.py")
-_WEIGHT_FILES = ("*.safetensors", "*.bin", "*.pt", "*.pth", "*.ckpt", "*.gguf", "*.onnx",
-                 "model.safetensors.index.json", "pytorch_model.bin.index.json")
+# What a vLLM export directory takes over from the source checkpoint (tokenizer, chat template,
+# generation and processor configs, remote-code modules) and what it never copies from it (weights,
+# weight indexes, the config it rewrites): the on-disk format of ``exporters/vllm.py:18-54``.
+_CARRIED_FILES = ("tokenizer.json", "tokenizer_config.json", "special_tokens_map.json", "added_tokens.json",
+                  "vocab.*", "merges.txt", "*.model", "spiece.model", "sentencepiece.bpe.model",
+                  "chat_template*.jinja", "generation_config*.json", "preprocessor_config.json",
+                  "processor_config.json", "image_processor_config.json", "video_processor_config.json",
+                  "feature_extractor_config.json", "configuration.json", "configuration*.py", "modeling*.py",
+                  "processing*.py", "tokenization*.py", "image_processing*.py", "video_processing*.py")
+_NEVER_CARRIED = ("config.json", "*.safetensors", "*.bin", "*.pt", "*.pth", "*.ckpt", "*.gguf", "*.onnx",
+                  "model.safetensors.index.json", "pytorch_model.bin.index.json")
 
 
-def _glob_any(name: str, patterns) -> bool:
-    return any(Path(name).match(p) for p in patterns)
-
-
-def _copy_inference_files(tokenizer_bundle, out: Path) -> List[str]:
-    src = getattr(tokenizer_bundle, "source_path", None)
-    if not src or not Path(src).is_dir():
+def _carried_files(source_dir) -> List[Path]:
+    """The files of ``source_dir`` an export carries over, in name order."""
+    if not source_dir or not Path(source_dir).is_dir():
         return []
-    copied = []
-    for f in sorted(Path(src).iterdir()):
-        if not f.is_file() or f.name == "config.json" or _glob_any(f.name, _WEIGHT_FILES):
-            continue
-        if not _glob_any(f.name, _INFERENCE_FILES):
-            continue
-        dst = out / f.name
-        if f.resolve() == dst.resolve():
-            continue
-        import shutil
-        shutil.copy2(f, dst)
-        copied.append(f.name)
-    return copied
+    hit = lambda name, pats: any(Path(name).match(p) for p in pats)  # noqa: E731
+    return [f for f in sorted(Path(source_dir).iterdir())
+            if f.is_file() and hit(f.name, _CARRIED_FILES) and not hit(f.name, _NEVER_CARRIED)]
 
 
-def _write_compression_config(out: Path, group_size: int, ignored: List[str]) -> None:
-    """``config.json`` of the export: the source ``quantization_config`` dropped, ``rope_theta`` and
-    ``rope_parameters`` made to carry each other (whichever one the model config has), and the
-    compressed-tensors ``compression_config`` added (``vllm.py:168-190``)."""
-    path = out / "config.json"
-    cfg = json.loads(path.read_text(encoding="utf-8"))
-    cfg.pop("quantization_config", None)
+def export_config(config: dict, group_size: int, ignored_layers: List[str]) -> dict:
+    """The export's ``config.json`` from the saved model config (``vllm.py:168-190``): no
+    ``quantization_config``; ``rope_theta`` and ``rope_parameters`` each present when the other is
+    (a top-level ``rope_theta`` becomes ``{"rope_theta": .., "rope_type": "default"}``, a
+    ``rope_parameters["rope_theta"]`` is mirrored at top level); the compressed-tensors
+    ``compression_config``."""
+    cfg = {k: v for k, v in config.items() if k != "quantization_config"}
     rope = cfg.get("rope_parameters")
+    theta = cfg.get("rope_theta")
     if isinstance(rope, dict):
-        if rope.get("rope_theta") is not None and cfg.get("rope_theta") is None:
+        if theta is None and rope.get("rope_theta") is not None:
             cfg["rope_theta"] = rope["rope_theta"]
-    elif cfg.get("rope_theta") is not None:
-        cfg["rope_parameters"] = {"rope_theta": cfg["rope_theta"], "rope_type": "default"}
-    cfg["compression_config"] = build_compression_config(group_size=group_size, ignored_layers=ignored)
-    path.write_text(json.dumps(cfg, ensure_ascii=False, indent=2), encoding="utf-8")
+    elif theta is not None:
+        cfg["rope_parameters"] = {"rope_theta": theta, "rope_type": "default"}
+    cfg["compression_config"] = build_compression_config(group_size=group_size, ignored_layers=ignored_layers)
+    return cfg
+
+
+def _check_artifact(name: str, art: "RealQuantLinearArtifact", mod, g: int) -> None:
+    """Raise if ``art`` cannot be exported as the packed weight of module ``mod`` (``None`` when the
+    model has no module of that name) with group size ``g``."""
+    if mod is None:
+        raise KeyError(f"the model has no module {name!r} for its quantized artifact")
+    if not isinstance(mod, nn.Linear):
+        raise TypeError(f"artifact {name!r} targets a {type(mod).__name__}; only nn.Linear modules are exported")
+    shape = tuple(mod.weight.shape)
+    n, k = shape
+    checks = (
+        (art.bits == 4 and art.symmetric, f"{name!r} is a {art.bits}-bit "
+                                          f"{'symmetric' if art.symmetric else 'asymmetric'} artifact; the "
+                                          f"compressed-tensors W4A16 format holds symmetric 4-bit codes"),
+        (int(art.group_size) == g, f"{name!r} was quantized with group size {art.group_size}, the export uses {g}"),
+        (tuple(art.original_shape) == shape, f"{name!r} was quantized from a {tuple(art.original_shape)} weight; "
+                                             f"the module's weight is {shape}"),
+        (tuple(art.int_weight.shape) == shape, f"{name!r} holds {tuple(art.int_weight.shape)} codes for a "
+                                               f"{shape} weight"),
+        (k % g == 0, f"{name!r}: in_features {k} is not a multiple of the group size {g} (the packed format "
+                     f"needs whole groups)"),
+        (tuple(art.scale.shape) == (n, k // g), f"{name!r} has scales {tuple(art.scale.shape)}, the format "
+                                                f"needs {(n, k // g)}"),
+    )
+    for ok, msg in checks:
+        if not ok:
+            raise ValueError(msg)
+
+
+@contextlib.contextmanager
+def _modules_swapped(model: nn.Module, replacements: Dict[str, nn.Module]):
+    """Replace the named submodules for the duration of the block; the originals come back on exit,
+    also when the block raises."""
+    saved = []
+    try:
+        for name, new in replacements.items():
+            parent_name, _, child = name.rpartition(".")
+            parent = model.get_submodule(parent_name) if parent_name else model
+            saved.append((parent, child, parent._modules[child]))
+            parent._modules[child] = new
+        yield
+    finally:
+        for parent, child, orig in reversed(saved):
+            parent._modules[child] = orig
 
 
 @torch.no_grad()
 def export_vllm_gptq_w4a16(*, model: nn.Module, tokenizer_bundle, artifacts: Dict[str, RealQuantLinearArtifact],
                            export_dir, group_size: int) -> dict:
-    """Export GPTQ W4A16 artifacts as a vLLM compressed-tensors ``pack-quantized`` checkpoint
-    (``exporters/vllm.py:224-327``), same keyword-only signature, checks, files and summary:
+    """Write GPTQ W4A16 artifacts as a vLLM compressed-tensors ``pack-quantized`` checkpoint: the
+    keyword-only interface, files and summary keys of ``exporters/vllm.py:224-327``.
 
-    * each artifact must name an ``nn.Linear`` of the model, be symmetric 4-bit with the export's
-      ``group_size``, match the weight shape, and have ``scale [N, K/g]`` with ``K % g == 0``;
-    * the linears are swapped for ``VllmPackedInt4Linear`` (codes packed by the GPU packer) for
-      ``model.save_pretrained(..., safe_serialization=True)`` and swapped back afterwards, also on
-      error; ``tokenizer_bundle.save_pretrained`` writes the tokenizer, the source checkpoint's
-      inference files are copied, and ``config.json`` gets the ``compression_config``;
-    * unquantized linears are listed in ``ignore``.
-    """
+    Every artifact is checked against its module first (``_check_artifact``), so a bad one raises
+    before anything is written or swapped.  The model is then saved by its own
+    ``save_pretrained(..., safe_serialization=True)`` while the quantized linears are swapped for
+    ``VllmPackedInt4Linear`` (codes packed by the GPU packer; the model's modules come back
+    afterwards); the tokenizer bundle saves itself, the source checkpoint's inference files are
+    carried over, and ``config.json`` is rewritten by ``export_config``, with every unquantized
+    ``nn.Linear`` in ``ignore``."""
     if not artifacts:
-        raise ValueError("No real-quant Linear artifacts were provided for vLLM export.")
+        raise ValueError("export_vllm_gptq_w4a16 got no quantized artifacts to export")
+    g = int(group_size)
+    modules = dict(model.named_modules())
+    for name, art in artifacts.items():
+        _check_artifact(name, art, modules.get(name), g)
+    ignored = sorted(n for n, m in modules.items() if isinstance(m, nn.Linear) and n not in artifacts)
+    packed = {}
+    for name, art in artifacts.items():
+        mod = modules[name]
+        packed[name] = VllmPackedInt4Linear(
+            packed_weight=pack_int4_for_vllm(art.int_weight).cpu(), scale=art.scale.detach().cpu(),
+            bias=None if mod.bias is None else mod.bias.detach().cpu(), in_features=mod.in_features,
+            out_features=mod.out_features)
     out = Path(export_dir)
     out.mkdir(parents=True, exist_ok=True)
-    modules = dict(model.named_modules())
-    ignored = sorted(n for n, m in modules.items() if isinstance(m, nn.Linear) and n not in artifacts)
-    g = int(group_size)
-    swapped = []
-    copied: List[str] = []
-    try:
-        for name, art in artifacts.items():
-            mod = modules.get(name)
-            if mod is None:
-                raise KeyError(f"Cannot find quantized module {name!r} in model.")
-            if not isinstance(mod, nn.Linear):
-                raise TypeError(f"Module {name!r} is {type(mod)!r}, expected nn.Linear.")
-            if art.bits != 4 or not art.symmetric:
-                raise ValueError(f"Only symmetric W4 artifacts are supported, got {art!r}.")
-            if int(art.group_size) != g:
-                raise ValueError(f"Artifact {name!r} group_size={art.group_size}, expected {g}.")
-            shape = tuple(mod.weight.shape)
-            if tuple(art.original_shape) != shape:
-                raise ValueError(f"Artifact {name!r} original_shape={art.original_shape}, "
-                                 f"but module weight shape is {shape}.")
-            if tuple(art.int_weight.shape) != shape:
-                raise ValueError(f"Artifact {name!r} int_weight shape={tuple(art.int_weight.shape)}, expected {shape}.")
-            if mod.in_features % g:
-                raise ValueError("vLLM compressed-tensors W4A16 requires in_features divisible by group_size; "
-                                 f"{name!r} has in_features={mod.in_features}, group_size={g}.")
-            if tuple(art.scale.shape) != (mod.out_features, mod.in_features // g):
-                raise ValueError(f"Artifact {name!r} scale shape={tuple(art.scale.shape)}, "
-                                 f"expected {(mod.out_features, mod.in_features // g)}.")
-            packed = pack_int4_for_vllm(art.int_weight).cpu()
-            bias = mod.bias.data.detach().cpu() if mod.bias is not None else None
-            new = VllmPackedInt4Linear(packed_weight=packed, scale=art.scale.detach().cpu(), bias=bias,
-                                       in_features=mod.in_features, out_features=mod.out_features)
-            parent_name, _, child = name.rpartition(".")
-            parent = model.get_submodule(parent_name) if parent_name else model
-            swapped.append((parent, child, mod))
-            _set_module(model, name, new)
+    with _modules_swapped(model, packed):
         model.save_pretrained(out, safe_serialization=True)
-        tokenizer_bundle.save_pretrained(str(out))
-        copied = _copy_inference_files(tokenizer_bundle, out)
-        _write_compression_config(out, g, ignored)
-    finally:
-        for parent, child, orig in reversed(swapped):
-            if child in parent._modules:
-                parent._modules[child] = orig
-            else:
-                setattr(parent, child, orig)
+    tokenizer_bundle.save_pretrained(str(out))
+    carried = []
+    for f in _carried_files(getattr(tokenizer_bundle, "source_path", None)):
+        if f.resolve() != (out / f.name).resolve():
+            shutil.copy2(f, out / f.name)
+            carried.append(f.name)
+    cfg_path = out / "config.json"
+    cfg = export_config(json.loads(cfg_path.read_text(encoding="utf-8")), g, ignored)
+    cfg_path.write_text(json.dumps(cfg, ensure_ascii=False, indent=2), encoding="utf-8")
     return {"backend": "vllm", "format": "compressed-tensors", "precision": "W4A16", "path": str(out),
             "quantized_linear_count": len(artifacts), "ignored_linear_count": len(ignored),
-            "ignored_layers": ignored, "copied_inference_files": copied}
+            "ignored_layers": ignored, "copied_inference_files": carried}
 
 
 @torch.no_grad()

@@ -101,3 +101,96 @@ def test_ascend_export_rejects_non_dense_qwen2(tmp_path, model_type):
                                                       "num_hidden_layers": 1}))
     with pytest.raises(ValueError, match="Expected dense Qwen2/Qwen2.5"):
         read_config(tmp_path)
+
+
+def _ascend_source(path, dtype=torch.float16, drop=None):
+    """The reference test's tiny dense-Qwen2 source (one layer, every projection
+    ``arange(6).reshape(2, 3) - index``; test_export_fp16_to_ascend_w8a8_dynamic_probe.py:27-45)."""
+    import json
+    from safetensors.torch import save_file
+    from mindpipe_amd.ascend_w8a8 import LINEAR_SUFFIXES
+    path.mkdir(parents=True)
+    (path / "config.json").write_text(json.dumps({"architectures": ["Qwen2ForCausalLM"], "model_type": "qwen2",
+                                                  "num_hidden_layers": 1}))
+    t = {"model.embed_tokens.weight": torch.arange(12, dtype=dtype).reshape(4, 3),
+         "lm_head.weight": torch.arange(12, dtype=dtype).reshape(4, 3)}
+    for i, suf in enumerate(LINEAR_SUFFIXES, start=1):
+        name = f"model.layers.0.{suf}.weight"
+        if name != drop:
+            t[name] = torch.arange(6, dtype=dtype).reshape(2, 3) - i
+    save_file(t, str(path / "model.safetensors"))
+    return t
+
+
+def _ascend_output(path, src_tensors, scale_dtype=None):
+    """An export written by hand from the oracle's export quantizer (no GPU): what the writer must
+    produce, for the verifier."""
+    import json
+    from safetensors.torch import save_file
+    from oracle import quant as O
+    from mindpipe_amd.ascend_w8a8 import LINEAR_SUFFIXES
+    path.mkdir(parents=True)
+    out, desc = {}, {"model.embed_tokens.weight": "FLOAT", "lm_head.weight": "FLOAT"}
+    for n, v in src_tensors.items():
+        if any(n.endswith(s + ".weight") for s in LINEAR_SUFFIXES):
+            q, _, s16, _ = O.quantize_weight_per_channel_export(v.numpy())
+            base = n[:-len(".weight")]
+            sc = torch.from_numpy(s16).reshape(-1, 1).to(scale_dtype or v.dtype)
+            out.update({n: torch.from_numpy(q), f"{base}.weight_scale": sc, f"{base}.weight_offset": torch.zeros_like(sc)})
+            desc[n] = "W8A8_DYNAMIC"
+        else:
+            out[n] = v
+    save_file(out, str(path / "model.safetensors"))
+    (path / "quant_model_description.json").write_text(json.dumps(desc))
+
+
+def test_ascend_export_checks_before_any_gpu_work(tmp_path):
+    """The source checks of the W8A8_DYNAMIC export, with the message fragments the reference's tests
+    match (tests/repro/test_export_fp16_to_ascend_w8a8_dynamic_probe.py:107-171)."""
+    from mindpipe_amd.ascend_w8a8 import export_w8a8_dynamic
+    src = tmp_path / "src"
+    _ascend_source(src)
+    for out in (src, src / "out", tmp_path):
+        with pytest.raises(ValueError, match="separate, non-nested"):
+            export_w8a8_dynamic(src, out)
+    src2 = tmp_path / "src2"
+    _ascend_source(src2, drop="model.layers.0.mlp.down_proj.weight")
+    with pytest.raises(ValueError, match="missing 1 required"):
+        export_w8a8_dynamic(src2, tmp_path / "o2")
+    src3 = tmp_path / "src3"
+    _ascend_source(src3, dtype=torch.int8)
+    with pytest.raises(ValueError, match="floating-point"):
+        export_w8a8_dynamic(src3, tmp_path / "o3")
+    assert not (tmp_path / "o2").exists() and not (tmp_path / "o3").exists()
+
+
+def test_ascend_verifier_on_a_hand_written_export(tmp_path):
+    """verify_w8a8_dynamic accepts an export holding the format (with and without the index) and
+    names every mismatch: a scale in another dtype than its source weight ("expected source weight
+    dtype F16", the reference test's fragment), a missing offset, a wrong description entry."""
+    import json
+    from mindpipe_amd.ascend_w8a8 import verify_w8a8_dynamic
+    src, out = tmp_path / "src", tmp_path / "out"
+    t = _ascend_source(src)
+    _ascend_output(out, t)
+    rep = verify_w8a8_dynamic(out, src)
+    assert rep["validated_linear_weights"] == 7 and rep["output_index_present"] is False
+    from safetensors import safe_open
+    with safe_open(str(out / "model.safetensors"), framework="pt") as f:
+        wm = {n: "model.safetensors" for n in f.keys()}
+    (out / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wm}))
+    assert verify_w8a8_dynamic(out, src)["output_index_present"] is True
+    wm["lm_head.weight"] = "other.safetensors"
+    (out / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wm}))
+    with pytest.raises(ValueError, match="index maps lm_head.weight"):
+        verify_w8a8_dynamic(out, src)
+    (out / "model.safetensors.index.json").unlink()
+    bad = tmp_path / "bad"
+    _ascend_output(bad, t, scale_dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="expected source weight dtype F16"):
+        verify_w8a8_dynamic(bad, src)
+    d = json.loads((out / "quant_model_description.json").read_text())
+    d["lm_head.weight"] = "W8A8_DYNAMIC"
+    (out / "quant_model_description.json").write_text(json.dumps(d))
+    with pytest.raises(ValueError, match="lm_head.weight"):
+        verify_w8a8_dynamic(out, src)
