@@ -17,7 +17,9 @@ by ``torch.cuda.synchronize()``.
 stated in each ``sample``).
 
 ``--profile NAME`` runs one kernel mix for rocprofv3 (the commands in ``profiles/``):
-``w4gemv`` (the headline loop), ``readfloor`` (one-launch reads of 8.9 MB, rotated),
+``w4gemv`` (the headline loop), ``readfloor`` (one-launch reads of 8.9 MB, rotated), ``readsweep``
+(read probes of several launch shapes at 8.9 MB and 1 GiB), ``w8sweep`` (the W8A8 sweep's GEMMs),
+``moe`` (the Mixtral MoE chain), ``prefill`` (the 7B prefill linears at M = 2048),
 ``w4shapes`` (M=16 and the 70B GEMV shapes), ``w4bf16`` (the bf16 W4A16 legs), ``w4batch8`` (7B
 gate/up and down at M = 1 and 8), ``dec7b`` (the 7B decode step), ``dec70b`` (four layers of the 70B
 decode step), ``w8big`` (the M=4096 int8 GEMM), and
@@ -151,20 +153,22 @@ def leg_w8a8(ops, m, n, k, steps, warmup):
     out = {"m": m, "n": n, "k": k, "smoothing_alpha": 0.5, "ms_gemm": ms, "ms_quant": ms_q, "ms_e2e": ms + ms_q, "tops": tops,
            "tops_e2e": ops_count / ((ms + ms_q) * 1e-3) / 1e12, "gb_s": gbs,
            "weight_copies": len({id(t) for t in qws})}
+    traffic = _traffic(f"w8a8_gemm_m{m}_k{k}_n{n}")
     if m >= 1024:
-        out["roofline"] = _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS",
-                                _traffic(f"w8a8_gemm_m{m}_k{k}_n{n}"))
+        out["roofline"] = _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS", traffic)
     elif m <= 16:
-        out["roofline"] = _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s")
+        out["roofline"] = _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", traffic)
     else:
-        out["roofline"] = _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s")
-        out["roofline_mfma"] = _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS")
+        out["roofline"] = _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", traffic)
+        out["roofline_mfma"] = _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS", traffic)
     del qws
     torch.cuda.empty_cache()
     return out
 
 
-def leg_moe(ops, steps, warmup, t=512, h=4096, inter=14336, e=8, top_k=2):
+def _moe_inputs(ops, t=512, h=4096, inter=14336, e=8, top_k=2):
+    """Config 4's inputs: tokens ~ N(0, 1), router logits ~ N(0, 1) routed by fp32 softmax -> top-k
+    -> renormalise, expert weights ~ N(0, 0.02) quantized per row to int8 (export rule)."""
     gen = torch.Generator(device="cuda").manual_seed(1)
     q13 = torch.empty((e, 2 * inter, h), dtype=torch.int8, device="cuda")
     s13 = torch.empty((e, 2 * inter), dtype=torch.float32, device="cuda")
@@ -183,16 +187,25 @@ def leg_moe(ops, steps, warmup, t=512, h=4096, inter=14336, e=8, top_k=2):
     tw, ids = torch.topk(p, top_k, dim=-1)
     tw = (tw / tw.sum(-1, keepdim=True)).float().cuda()
     ids = ids.to(torch.int32).cuda()
-    ms = _time_graph(lambda i: ops.moe_w8a8_forward(x, ids, tw, q13, s13, q2, s2), 1, steps, warmup)
+    return x, ids, tw, q13, s13, q2, s2
+
+
+def _moe_chain_ms(ops, steps, warmup=3):
+    x, ids, tw, q13, s13, q2, s2 = _moe_inputs(ops)
+    return _time_graph(lambda i: ops.moe_w8a8_forward(x, ids, tw, q13, s13, q2, s2), 1, steps, warmup)
+
+
+def leg_moe(ops, steps, warmup, t=512, h=4096, inter=14336, e=8, top_k=2):
+    ms = _moe_chain_ms(ops, steps, warmup)
     wbytes = e * (2 * inter * h + h * inter)
     ops_count = 2.0 * t * top_k * (2 * inter * h + h * inter)
     gbs = wbytes / (ms * 1e-3) / 1e9
     tops = ops_count / (ms * 1e-3) / 1e12
-    t1, t2 = _traffic("moe_gmm1_mixtral_t512"), _traffic("moe_gmm2_mixtral_t512")
+    chain = _traffic("moe_chain_mixtral_t512")
     return {"tokens": t, "experts": e, "top_k": top_k, "hidden": h, "inter": inter, "ms_chain": ms,
             "weight_bytes": wbytes, "gb_s": gbs, "tops": tops,
-            "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", t1 + t2 if t1 and t2 else None),
-            "roofline_mfma": _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS")}
+            "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", chain),
+            "roofline_mfma": _roof("mfma", tops, INT8_PEAK_TOPS, "TOPS", chain)}
 
 
 def leg_decoder(cfg_name, batches, prompt, gen_tokens, prefill_batch=1):
@@ -304,12 +317,71 @@ def profile_mix(ops, name, steps):
         ms = _time_graph(lambda i: ops.w4a16_gemm(x, pk[i], sc[i], zr[i], 128, None), 64, steps, 5)
         print(f"w4gemv: {ms / 64 * 1e3:.3f} us per launch")
     elif name == "readfloor":
-        # the library's read probe over the headline GEMV's 8,929,280 bytes (64 rotated buffers):
-        # launch + latency + transfer with no dequant or dot work
+        # the measurement library's read probe over the headline GEMV's 8,929,280 bytes (64 rotated
+        # buffers): launch + latency + transfer with no dequant or dot work
+        from mindpipe_amd.measure import probe_read
         bufs = [torch.ones(8929280 // 4, dtype=torch.int32, device="cuda") for _ in range(64)]
-        sinks = [ops.probe_read(b) for b in bufs]
-        ms = _time_graph(lambda i: ops.probe_read(bufs[i], sinks[i]), 64, steps, 5)
+        sinks = [probe_read(b) for b in bufs]
+        ms = _time_graph(lambda i: probe_read(bufs[i], sinks[i]), 64, steps, 5)
         print(f"readfloor: {ms / 64 * 1e3:.3f} us per 8.9 MB read launch")
+    elif name == "readsweep":
+        # read probes of several launch shapes (threads per workgroup, 16-byte loads per lane,
+        # one-shot workgroups or a fixed strided grid), graph-replayed: at the headline's 8.9 MB over
+        # 64 rotated buffers and at 1 GiB (one buffer, four times the Infinity Cache)
+        from mindpipe_amd.measure import probe_read
+        small = [torch.ones(8929280 // 4, dtype=torch.int32, device="cuda") for _ in range(64)]
+        shapes_small = [(256, 1, 0), (256, 2, 0), (256, 4, 0), (256, 8, 0), (512, 2, 0), (512, 4, 0),
+                        (256, 4, 256), (256, 8, 256), (512, 4, 256), (512, 4, 512), (256, 4, 1024), (512, 2, 1024)]
+        for th, ld, gr in shapes_small:
+            sinks = [probe_read(b, None, th, ld, gr) for b in small]
+            ms = _time_graph(lambda i: probe_read(small[i], sinks[i], th, ld, gr), 64, steps, 3)
+            us = ms / 64 * 1e3
+            print(f"readsweep 8.9MB threads={th} loads={ld} grid={gr or 'one-shot'}: {us:.3f} us per launch, "
+                  f"{8929280 / (us * 1e-6) / 1e12:.2f} TB/s", flush=True)
+        del small
+        torch.cuda.empty_cache()
+        big = torch.ones((1 << 30) // 4, dtype=torch.int32, device="cuda")
+        shapes_big = [(256, 4, 0), (512, 8, 0), (512, 4, 256), (512, 8, 256), (512, 4, 512), (512, 8, 512),
+                      (512, 4, 1024), (512, 4, 2048), (256, 4, 4096)]
+        for th, ld, gr in shapes_big:
+            sink = probe_read(big, None, th, ld, gr)
+            ms = _time_graph(lambda i: probe_read(big, sink, th, ld, gr), 4, steps, 3)
+            us = ms / 4 * 1e3
+            print(f"readsweep 1GiB threads={th} loads={ld} grid={gr or 'one-shot'}: {us:.1f} us per launch, "
+                  f"{(1 << 30) / (us * 1e-6) / 1e12:.2f} TB/s", flush=True)
+    elif name == "w8sweep":
+        # the W8A8 sweep legs' GEMMs (M = 1, 16, 256, 4096; N = 11008, K = 4096) on random int8 data,
+        # M <= 256 over 13 rotated weight copies as in the bench
+        gen = torch.Generator(device="cuda").manual_seed(1)
+        copies = [torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device="cuda", generator=gen)
+                  for _ in range(13)]
+        sw = torch.rand(11008, device="cuda") * 1e-3
+        for m in (1, 16, 256, 4096):
+            qx = torch.randint(-127, 128, (m, 4096), dtype=torch.int8, device="cuda", generator=gen)
+            st = torch.rand(m, device="cuda") * 1e-2
+            c = 13 if m <= 256 else 1
+            ms = _time_graph(lambda i: ops.w8a8_gemm(qx, st, copies[i], sw, None, torch.float16), c, steps, 3) / c
+            print(f"w8sweep m={m}: {ms * 1e3:.2f} us per launch", flush=True)
+    elif name == "moe":
+        # the Mixtral MoE leg's chain (route + quant, GEMM1 + SwiGLU + requant, GEMM2, combine) on the
+        # bench leg's inputs
+        ms = _moe_chain_ms(ops, steps)
+        print(f"moe chain: {ms * 1e3:.1f} us per call", flush=True)
+    elif name == "prefill":
+        # the 7B prefill linears at M = 2048 (fp16): q/k/v (N = 12288), o (4096), fused gate/up with
+        # SiLU-mul (2 x 11008), down (K = 11008)
+        for n, k, swi in ((12288, 4096, False), (4096, 4096, False), (2 * 11008, 4096, True), (4096, 11008, False)):
+            pk, sc, zr = _w4_copies(ops, n, k, 1)
+            x = torch.randn(2048, k, device="cuda").half()
+            if swi:
+                f = lambda i: ops.w4a16_gemm_swiglu(x, pk[0], sc[0], zr[0], 128, None)  # noqa: E731
+            else:
+                f = lambda i: ops.w4a16_gemm(x, pk[0], sc[0], zr[0], 128, None)  # noqa: E731
+            ms = _time_graph(f, 2, steps, 3) / 2
+            print(f"prefill n={n} k={k}{' swiglu' if swi else ''}: {ms * 1e3:.1f} us, "
+                  f"{2 * 2048 * n * k / (ms * 1e-3) / 1e12:.0f} TFLOP/s", flush=True)
+            del pk, sc, zr
+            torch.cuda.empty_cache()
     elif name == "w4shapes":
         for m, n, k, c in ((16, 4096, 4096, 64), (1, 28672, 8192, 8), (1, 8192, 28672, 8), (16, 28672, 8192, 8),
                            (64, 28672, 8192, 8)):
@@ -423,27 +495,29 @@ def traffic_probe(ops):
         for i in range(8):
             ops.w4a16_gemm(xk, pk[i % 4], sc[i % 4], zr[i % 4], 128, None)
         del pk, sc, zr
-    qx = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device="cuda")
-    qw = torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device="cuda")
-    st = torch.rand(4096, device="cuda")
+    # the W8A8 sweep: M = 1, 16, 256 over 13 rotated weight copies (3 rounds), M = 4096 three times
+    gen8 = torch.Generator(device="cuda").manual_seed(1)
+    wcopies = [torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device="cuda", generator=gen8)
+               for _ in range(13)]
     sw = torch.rand(11008, device="cuda")
+    for m in (1, 16, 256, 4096):
+        qx = torch.randint(-127, 128, (m, 4096), dtype=torch.int8, device="cuda", generator=gen8)
+        st = torch.rand(m, device="cuda")
+        for i in range(39 if m <= 256 else 3):
+            ops.w8a8_gemm(qx, st, wcopies[i % 13], sw, None, torch.float16)
+    del wcopies, qx
+    # the 7B prefill's fused gate/up + SiLU-mul at M = 2048 (the prefill kernel's SwiGLU form)
+    pk, sc, zr = _w4_copies(ops, 2 * 11008, 4096, 1)
+    xp = torch.randn(2048, 4096, device="cuda").half()
     for _ in range(3):
-        ops.w8a8_gemm(qx, st, qw, sw, None, torch.float16)
-    del qx, qw
-    # the Mixtral MoE leg's grouped GEMMs (routing of the bench leg: 512 tokens, top-2 of 8)
-    e, h, inter = 8, 4096, 14336
-    counts = [126, 117, 122, 140, 133, 124, 133, 129]
-    offs = torch.tensor([0] + [sum(counts[:i + 1]) for i in range(e)], dtype=torch.int64, device="cuda")
-    rows = sum(counts)
-    routed = torch.randint(-127, 128, (rows, h), dtype=torch.int8, device="cuda")
-    rs = torch.rand(rows, device="cuda") * 0.01
-    w13 = torch.randint(-127, 128, (e, 2 * inter, h), dtype=torch.int8, device="cuda")
-    s13 = torch.rand(e, 2 * inter, device="cuda") * 1e-3
-    w2 = torch.randint(-127, 128, (e, h, inter), dtype=torch.int8, device="cuda")
-    s2 = torch.rand(e, h, device="cuda") * 1e-3
+        ops.w4a16_gemm_swiglu(xp, pk[0], sc[0], zr[0], 128, None)
+    del pk, sc, zr, xp
+    # the Mixtral MoE leg's whole chain on the bench leg's inputs (route + quant, GEMM1 + SwiGLU +
+    # requant, GEMM2, combine), three calls
+    mx = _moe_inputs(ops)
     for _ in range(3):
-        q, s = ops.moe_gmm1_swiglu_quant(routed, rs, w13, s13, offs, inter)
-        ops.moe_gmm2(q, s, w2, s2, offs)
+        ops.moe_w8a8_forward(*mx)
+    del mx
     torch.cuda.synchronize()
     print("traffic probe done")
 

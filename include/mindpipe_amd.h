@@ -345,13 +345,6 @@ int mp_smooth_scales(const float *act_max, const float *w_colmax, int64_t k, dou
  * (smooth_ln_fcs_llama_like, smooth.py:91-101). */
 int mp_scale_columns(void *w, int dtype, int64_t rows, int64_t k, const void *scales, int divide, mp_stream_t stream);
 
-/* Measurement probe (no counterpart in the reference): one launch that reads `bytes` (a multiple
- * of 16, 16-byte aligned buf) with the one-row GEMVs' launch shape and no other work, so its
- * duration is the read floor the kernels' roofline fractions are read against.  sink: uint32
- * [mp_probe_read_sink_words(bytes)], written at most once per workgroup. */
-size_t mp_probe_read_sink_words(int64_t bytes);
-int mp_probe_read(const void *buf, int64_t bytes, uint32_t *sink, mp_stream_t stream);
-
 #ifdef __cplusplus
 }
 #endif

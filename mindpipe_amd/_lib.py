@@ -47,8 +47,6 @@ SIGNATURES = {
     "mp_colmax_abs": (_i32, [_vp, _i32, _i64, _i64, _i32, _vp, _vp]),
     "mp_smooth_scales": (_i32, [_vp, _vp, _i64, C.c_double, _i32, _vp, _vp]),
     "mp_scale_columns": (_i32, [_vp, _i32, _i64, _i64, _vp, _i32, _vp]),
-    "mp_probe_read_sink_words": (C.c_size_t, [_i64]),
-    "mp_probe_read": (_i32, [_vp, _i64, _vp, _vp]),
     "mp_w8_quantize_per_channel": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "mp_w8a8_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp]),
     "mp_moe_route_workspace_bytes": (_sz, [_i64, _i64, _i32]),

@@ -74,6 +74,24 @@ def _stale(src: Path) -> bool:
     return any(d.stat().st_mtime > obj.stat().st_mtime for d in deps if d.exists())
 
 
+MEASURE_DIR = PKG / "measure"
+MEASURE_LIB = MEASURE_DIR / "libmindpipe_measure.so"
+
+
+def build_measure(verbose: bool = True) -> Path:
+    """The measurement-only probe library (``measure/probe.hip``), outside the product ABI."""
+    src = MEASURE_DIR / "probe.hip"
+    tmp = MEASURE_LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, *FLAGS, "-shared", str(src), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, MEASURE_LIB)
+    if verbose:
+        print(f"built {MEASURE_LIB}")
+    return MEASURE_LIB
+
+
 def build(verbose: bool = True, incremental: bool = False) -> Path:
     """Compile every ``csrc/*.hip`` and link the library.  ``incremental=True`` (a development
     aid) recompiles only sources whose object is stale."""
@@ -93,6 +111,9 @@ def build(verbose: bool = True, incremental: bool = False) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {[s.name for s in srcs]}")
+    if not incremental or not MEASURE_LIB.exists() or \
+            (MEASURE_DIR / "probe.hip").stat().st_mtime > MEASURE_LIB.stat().st_mtime:
+        build_measure(verbose)
     return LIB
 
 

@@ -1,0 +1,46 @@
+"""Measurement-only read probes (``libmindpipe_measure.so``, built from ``probe.hip`` beside this
+file).  Not part of the product path or its C ABI: ``bench.py --profile readfloor`` and
+``--profile readsweep`` use them to measure what a launch that only reads costs on this GPU."""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libmindpipe_measure.so"
+_LIB = None
+
+
+def _load() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise ImportError(f"{LIB_PATH} is not built (python -m mindpipe_amd.build)")
+        lib = C.CDLL(str(LIB_PATH))
+        lib.mp_probe_read_grid.restype = C.c_int64
+        lib.mp_probe_read_grid.argtypes = [C.c_int64, C.c_int, C.c_int, C.c_int64]
+        lib.mp_probe_read_shape.restype = C.c_int
+        lib.mp_probe_read_shape.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_int64, C.c_void_p,
+                                            C.c_void_p]
+        _LIB = lib
+    return _LIB
+
+
+def probe_read(buf: torch.Tensor, sink: Optional[torch.Tensor] = None, threads: int = 256, loads: int = 4,
+               grid: int = 0) -> torch.Tensor:
+    """One launch that reads all of ``buf`` (contiguous, 16-byte multiple) and nothing else.
+    ``grid`` = 0: one-shot workgroups of ``threads`` x ``loads`` 16-byte pieces (the one-row GEMVs'
+    shape at the defaults); ``grid`` > 0: that many workgroups striding over the buffer.  Returns
+    the sink the launch may write (pass it back in to reuse it)."""
+    lib = _load()
+    nbytes = buf.numel() * buf.element_size()
+    if sink is None:
+        words = max(1, int(lib.mp_probe_read_grid(nbytes, threads, loads, grid)))
+        sink = torch.zeros(words, dtype=torch.int32, device=buf.device)
+    rc = lib.mp_probe_read_shape(buf.data_ptr(), nbytes, threads, loads, grid, sink.data_ptr(),
+                                 torch.cuda.current_stream(buf.device).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"mp_probe_read_shape failed with status {rc}")
+    return sink

@@ -868,16 +868,3 @@ def scale_columns_(w: torch.Tensor, scales: torch.Tensor, divide: bool = False) 
                                                 int(divide), _stream()), "mp_scale_columns")
     return w
 
-
-def probe_read(buf: torch.Tensor, sink: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """One launch reading all of ``buf`` with the one-row GEMVs' launch shape and no other work (the
-    read floor of a one-launch kernel; a measurement probe).  Returns the sink it may write."""
-    if not buf.is_cuda or not buf.is_contiguous():
-        raise RuntimeError("buf must be a contiguous device tensor")
-    nbytes = buf.numel() * buf.element_size()
-    lib = _lib.load()
-    if sink is None:
-        sink = torch.zeros(max(1, int(lib.mp_probe_read_sink_words(nbytes))), dtype=torch.int32, device=buf.device)
-    with _dev(buf):
-        _lib.check(lib.mp_probe_read(buf.data_ptr(), nbytes, sink.data_ptr(), _stream()), "mp_probe_read")
-    return sink
