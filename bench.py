@@ -349,6 +349,22 @@ def profile_mix(ops, name, steps):
             us = ms / 4 * 1e3
             print(f"readsweep 1GiB threads={th} loads={ld} grid={gr or 'one-shot'}: {us:.1f} us per launch, "
                   f"{(1 << 30) / (us * 1e-6) / 1e12:.2f} TB/s", flush=True)
+    elif name == "tileread":
+        # the W8A8 weight operand (N = 11008 rows of K = 4096 bytes, 13 rotated copies) read in a
+        # tiled GEMM's order (a workgroup per tile of rows, step_bytes of each row per step, depth steps
+        # in flight) against the same bytes read contiguously
+        from mindpipe_amd.measure import probe_read, probe_read_tiles
+        n, kb = 11008, 4096
+        bufs = [torch.ones(n * kb // 4, dtype=torch.int32, device="cuda") for _ in range(13)]
+        sinks = [probe_read(b, None, 256, 4, 0) for b in bufs]
+        ms = _time_graph(lambda i: probe_read(bufs[i], sinks[i], 256, 4, 0), 13, steps, 3) / 13
+        print(f"tileread contiguous: {ms * 1e3:.2f} us, {n * kb / (ms * 1e-3) / 1e12:.2f} TB/s", flush=True)
+        for tr, sb, d in ((128, 128, 1), (128, 128, 4), (64, 256, 4), (32, 512, 4), (16, 1024, 4), (8, 2048, 2),
+                          (32, 128, 4), (16, 256, 4), (128, 512, 1), (64, 1024, 1), (16, 4096, 1)):
+            tsinks = [probe_read_tiles(b, n, kb, tr, sb, d) for b in bufs]
+            ms = _time_graph(lambda i: probe_read_tiles(bufs[i], n, kb, tr, sb, d, tsinks[i]), 13, steps, 3) / 13
+            print(f"tileread tile_rows={tr} step_bytes={sb} depth={d}: {ms * 1e3:.2f} us, "
+                  f"{n * kb / (ms * 1e-3) / 1e12:.2f} TB/s", flush=True)
     elif name == "w8sweep":
         # the W8A8 sweep legs' GEMMs (M = 1, 16, 256, 4096; N = 11008, K = 4096) on random int8 data,
         # M <= 256 over 13 rotated weight copies as in the bench

@@ -2325,6 +2325,14 @@ extern "C" int mp_w4a16_gemm(const void *x, int64_t m, int64_t k, const int32_t 
     int r = 4, c = 1, sk = 1;
     if (nch <= 2) {
       c = nch;
+    } else if (n >= 16384 && nch % 2 == 0) {
+      // wide layers (the 70B gate/up, down and LM head): 8 rows per wave, two waves splitting K,
+      // two chunks per iteration: 26.8 / 44.2 / 27.8 us against 27.8 / 47.2 / 29.0 us with the
+      // 4-row forms at K = 8192, N = 28672 / 57344 and K = 28672, N = 8192 (graph-timed, 8 rotated
+      // copies, one box)
+      r = 8;
+      c = 2;
+      sk = 2;
     } else if (nch % 4 == 0) {
       c = 2;
       sk = 2;

@@ -1,6 +1,7 @@
 // W8A8 for gfx950: per-token / per-channel int8 quantizers and the int8 MFMA
 // GEMM with the per-token x per-channel scale epilogue (dense and grouped).
 #include "dq_gemm.h"
+#include <type_traits>
 
 namespace {
 
@@ -633,11 +634,14 @@ __global__ __launch_bounds__(256) void i8_tiled_kernel(mp_i8_args p) {
 // a slice's row chunks share its weights) in that XCD's L2.  The launch is
 // persistent (one workgroup per CU): the next item's first K tiles are loaded before
 // the current item's epilogue.
-// Eight waves: wave (wm, wn) loads and multiplies the 64-row slab wm and owns the 64
-// columns wn.  A slab past the expert's rows is inactive: its two waves load no A
-// rows and skip their MFMAs and epilogue (the K loop is instantiated for both cases;
-// every wave runs the same barriers).  128-byte K steps (a 64-lane load covers 8 rows
-// x 128 B), D + 1 register stages in flight, LDS double buffer of 144-byte rows.
+// Eight waves: wave w loads the 32-row A slab w; wave (wr, wn) = (w >> 1, w & 1)
+// multiplies the 32-row tiles wr and 4 + wr (rows [32 wr, +32) and [128 + 32 wr, +32))
+// and owns the 64 columns wn, so an expert of up to 128 rows keeps all eight waves busy
+// (two per SIMD) and one of up to 256 rows gives each wave both tiles.  A slab or tile
+// past the expert's rows is inactive: its wave loads no A rows for it and skips its
+// MFMAs (the K loop is instantiated for one and for two tiles; every wave runs the same
+// barriers).  128-byte K steps (a 64-lane load covers 8 rows x 128 B), D + 1 register
+// stages in flight, LDS double buffer of 144-byte rows.
 constexpr int kMoeBM = 256, kMoeBN = 128, kMoeBK = 128, kMoeLD = kMoeBK + 16, kMoeThreads = 512;
 constexpr int kMoeMaxExperts = 1024;
 // LDS: double-buffered A and B tiles; two buffers each of the item's per-token scales and
@@ -701,7 +705,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
   constexpr int CPR = BK / 16;          // 16-byte chunks per tile row
   constexpr int CA = 4;                 // A loads per lane per K step (its wave's 32 rows)
   constexpr int CB = BN * CPR / NT;     // B loads (2)
-  constexpr int TM = 2, TN = 2;         // 32x32 MFMA tiles per wave: 64 x 64
+  constexpr int TM = 2, TN = 2;         // 32x32 MFMA tiles per wave: rows 32 wr, 128 + 32 wr; 64 columns
   constexpr bool SWI = EPI == MP_EPI_SWIGLU;
   extern __shared__ __attribute__((aligned(16))) int8_t smem_moe[];
   int8_t *sa = smem_moe;                // [2][BM * LD]
@@ -710,7 +714,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
   float *ssc = ssa + 2 * BM;                                              // [2][BN] column scales
   int64_t *soff = reinterpret_cast<int64_t *>(ssc + 2 * BN);             // [E + 1] group offsets
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wr = wave >> 1, wn = wave & 1;
 
   // ---- this workgroup's items (every wave derives the same ones).  The offsets are read
   // from an LDS copy, so finding the next item never waits on the tile loads in flight.
@@ -738,9 +742,9 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
   const int64_t nb_rows = SWI ? 2 * n_out : n_out;  // weight rows per expert
   const int64_t nkt = k / BK;
 
-  // A: lane's rows 64 wm + 32 wn + 8 i + lane / 8 (i < CA), chunk lane % 8, through a
+  // A: lane's rows 32 wave + 8 i + lane / 8 (i < CA), chunk lane % 8, through a
   // buffer descriptor that ends at row_end (rows past it read as zeros, no traffic)
-  const int arow0 = 64 * wm + 32 * wn + (lane >> 3);
+  const int arow0 = 32 * wave + (lane >> 3);
   const uint32_t aoff0 = static_cast<uint32_t>(arow0 * k + (lane & 7) * 16);
   // B: chunk c = tid + i * NT of the 128 x 128 tile
   int boff_row[CB];
@@ -752,7 +756,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
   int64_t row_begin, row_end;
   __amdgpu_buffer_rsrc_t arsrc;
   const int8_t *bsrc[CB];
-  bool act;
+  bool lact, mact0, mact1;  // the wave's A slab loads; its tiles 0 and 1 multiply
   // next item's scale held by this thread: tid < BM per-token scale of row tid, BM <= tid <
   // BM + BN the scale of weight row tid - BM of the tile
   float scale_a = 0.f, scale_b = 0.f;
@@ -760,7 +764,9 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
   auto set_item = [&](int g) {
     moe_find_item(off, ne, n_slices, g, lane, e, slice, row_begin, row_end);
     arsrc = mp_rsrc(p.a + row_begin * k, static_cast<uint32_t>((row_end - row_begin) * k));
-    act = row_begin + 64 * wm < row_end;
+    lact = row_begin + 32 * wave < row_end;
+    mact0 = row_begin + 32 * wr < row_end;
+    mact1 = row_begin + 128 + 32 * wr < row_end;
     const int8_t *bexp = p.b + (p.shared_b ? 0 : static_cast<int64_t>(e) * nb_rows * k);
     const int64_t col0 = static_cast<int64_t>(slice) * (SWI ? BN / 2 : BN);
 #pragma unroll
@@ -812,14 +818,14 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
   auto load_tile = [&](int set, int64_t kt) {
     kt = kt < 0 ? 0 : (kt < nkt ? kt : nkt - 1);  // every load stays inside the item's K range
     const uint32_t koff = static_cast<uint32_t>(kt * BK);
-    const uint32_t ab = act ? aoff0 : 0x80000000u;
+    const uint32_t ab = lact ? aoff0 : 0x80000000u;
 #pragma unroll
     for (int i = 0; i < CA; ++i) areg[set][i] = mp_buf_load16i(arsrc, ab + static_cast<uint32_t>(8 * i * k), koff);
 #pragma unroll
     for (int i = 0; i < CB; ++i) breg[set][i] = *reinterpret_cast<const i4_t *>(bsrc[i] + kt * BK);
   };
   auto store_tile = [&](int set, int buf) {
-    if (act) {  // wave-uniform
+    if (lact) {  // wave-uniform
 #pragma unroll
       for (int i = 0; i < CA; ++i)
         *reinterpret_cast<i4_t *>(sa + buf * BM * LD + (arow0 + 8 * i) * LD + (lane & 7) * 16) = areg[set][i];
@@ -832,24 +838,26 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
   i16_t acc[TM][TN];
   int arow_l[TM], brow_l[TN];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) arow_l[i] = (wm * 64 + i * 32 + (lane & 31)) * LD + 16 * (lane >> 5);
+  for (int i = 0; i < TM; ++i) arow_l[i] = (32 * wr + 128 * i + (lane & 31)) * LD + 16 * (lane >> 5);
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int lr = SWI ? (j * (BN / 2) + wn * 32 + (lane & 31)) : (wn * 64 + j * 32 + (lane & 31));
     brow_l[j] = lr * LD + 16 * (lane >> 5);
   }
-  auto mma = [&](int cur) {
+  // the wave's active tiles: TA = 1 (tile 0) or 2 (both)
+  auto mma = [&](int cur, auto ta_tag) {
+    constexpr int TA = decltype(ta_tag)::value;
     const int8_t *ca = sa + cur * BM * LD;
     const int8_t *cb = sb + cur * BN * LD;
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
-      i4_t af[TM], bf[TN];
+      i4_t af[TA], bf[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i4_t *>(ca + arow_l[i] + ks * 32);
+      for (int i = 0; i < TA; ++i) af[i] = *reinterpret_cast<const i4_t *>(ca + arow_l[i] + ks * 32);
 #pragma unroll
       for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const i4_t *>(cb + brow_l[j] + ks * 32);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TA; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
@@ -873,7 +881,8 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
         const int64_t kt = kt0 + d;
         const int nxt = (d + 1) % (D + 1);
         if (kt < nkt) {  // workgroup-uniform
-          if (act) mma(static_cast<int>(kt & 1));
+          if (mact1) mma(static_cast<int>(kt & 1), std::integral_constant<int, 2>{});
+          else if (mact0) mma(static_cast<int>(kt & 1), std::integral_constant<int, 1>{});
           if (kt + 1 < nkt) store_tile(nxt, static_cast<int>((kt + 1) & 1));
         }
         load_tile(nxt, kt + D + 2);
@@ -902,7 +911,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
 
     // the current item's epilogue parameters, then the next item's first tiles (the
     // loop's last barrier has passed: LDS is free, the register stages are consumed)
-    const bool cur_act = act;
+    const bool cur_act = mact0;
     const int cur_slice = slice;
     const int64_t cur_begin = row_begin, cur_end = row_end;
     idx += stride;
@@ -911,21 +920,21 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
     prologue(has_next ? 0 : nkt - 1);
 
     if (cur_act) {
-      // element r of tile (i, j): local row 64 wm + 32 i + 8 (r >> 2) + 4 (lane >> 5) + (r & 3).
+      // element r of tile (i, j): local row 32 wr + 128 i + 8 (r >> 2) + 4 (lane >> 5) + (r & 3).
       // Stores go through buffer descriptors over the item's rows: rows past cur_end and
       // columns past n_out (offset kOob) are dropped without a branch.  (Guarding each
       // store with a branch makes the compiler wait for every earlier store.)
       constexpr uint32_t kOob = 0x80000000u;
       const uint32_t nrows = static_cast<uint32_t>(cur_end - cur_begin);
       const uint32_t ldy = static_cast<uint32_t>(p.ldy);
-      const int lm0 = wm * 64 + 4 * (lane >> 5);
-      // the lane's per-token scales: rows lm0 + 32 i + 8 q + (0..3)
+      const int lm0 = 32 * wr + 4 * (lane >> 5);
+      // the lane's per-token scales: rows lm0 + 128 i + 8 q + (0..3)
       float sa_r[TM][16];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const f4_t s4 = *reinterpret_cast<const f4_t *>(ssa + par * BM + lm0 + 32 * i + 8 * q);
+          const f4_t s4 = *reinterpret_cast<const f4_t *>(ssa + par * BM + lm0 + 128 * i + 8 * q);
 #pragma unroll
           for (int c = 0; c < 4; ++c) sa_r[i][4 * q + c] = s4[c];
         }
@@ -943,7 +952,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int lm = lm0 + i * 32 + 8 * (r >> 2) + (r & 3);
+            const int lm = lm0 + i * 128 + 8 * (r >> 2) + (r & 3);
             const float gv = mp_mul(mp_mul(static_cast<float>(acc[i][0][r]), sa_r[i][r]), sg);
             const float uv = mp_mul(mp_mul(static_cast<float>(acc[i][1][r]), sa_r[i][r]), su);
             const float h = mp_swiglu_epi(gv, uv, p.epi_round);
@@ -957,7 +966,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
         moe_max_step<2>(v, lane);
         moe_max_step<1>(v, lane);
         const int jv = lane & 31;
-        const int lm = lm0 + (jv >> 4) * 32 + 8 * ((jv & 15) >> 2) + (jv & 3);
+        const int lm = lm0 + (jv >> 4) * 128 + 8 * ((jv & 15) >> 2) + (jv & 3);
         const uint32_t np = static_cast<uint32_t>(p.n_partial);
         const __amdgpu_buffer_rsrc_t pr = mp_rsrc(p.amax_partial + cur_begin * p.n_partial, nrows * np * 4);
         mp_buf_store4(pr, (static_cast<uint32_t>(lm) * np + static_cast<uint32_t>(cur_slice * 2 + wn)) * 4,
@@ -983,7 +992,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
           for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int lm = lm0 + i * 32 + 8 * (r >> 2) + (r & 3);
+              const int lm = lm0 + i * 128 + 8 * (r >> 2) + (r & 3);
               float yv = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), sa_r[i][r]), scj);
               yv = hb ? mp_add(yv, bj) : yv;
               const uint16_t hv = bf ? mp_f2bf(yv) : mp_f2h(yv);
@@ -1000,7 +1009,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
         moe_max_step<2>(v, lane);
         moe_max_step<1>(v, lane);
         const int jv = lane & 31;
-        const int lm = lm0 + (jv >> 4) * 32 + 8 * ((jv & 15) >> 2) + (jv & 3);
+        const int lm = lm0 + (jv >> 4) * 128 + 8 * ((jv & 15) >> 2) + (jv & 3);
         const uint32_t np = static_cast<uint32_t>(p.n_partial);
         const __amdgpu_buffer_rsrc_t pr = mp_rsrc(p.amax_partial + cur_begin * p.n_partial, nrows * np * 4);
         mp_buf_store4(pr, (static_cast<uint32_t>(lm) * np + static_cast<uint32_t>(cur_slice * 2 + wn)) * 4,
@@ -1019,7 +1028,7 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
           for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int lm = lm0 + i * 32 + 8 * (r >> 2) + (r & 3);
+              const int lm = lm0 + i * 128 + 8 * (r >> 2) + (r & 3);
               const float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), sa_r[i][r]), scj);
               const uint32_t off =
                   cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * esz : kOob;

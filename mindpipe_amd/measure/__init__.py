@@ -24,6 +24,9 @@ def _load() -> C.CDLL:
         lib.mp_probe_read_shape.restype = C.c_int
         lib.mp_probe_read_shape.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_int64, C.c_void_p,
                                             C.c_void_p]
+        lib.mp_probe_read_tiles.restype = C.c_int
+        lib.mp_probe_read_tiles.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                            C.c_void_p]
         _LIB = lib
     return _LIB
 
@@ -43,4 +46,19 @@ def probe_read(buf: torch.Tensor, sink: Optional[torch.Tensor] = None, threads: 
                                  torch.cuda.current_stream(buf.device).cuda_stream)
     if rc != 0:
         raise RuntimeError(f"mp_probe_read_shape failed with status {rc}")
+    return sink
+
+
+def probe_read_tiles(buf: torch.Tensor, rows: int, row_bytes: int, tile_rows: int, step_bytes: int, depth: int,
+                     sink: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One launch reading a row-major ``[rows, row_bytes]`` matrix in a tiled GEMM's weight order:
+    a workgroup per ``tile_rows`` rows, ``step_bytes`` of each of its rows per step, ``depth`` steps
+    in flight.  Returns the sink the launch may write."""
+    lib = _load()
+    if sink is None:
+        sink = torch.zeros(max(1, -(-rows // tile_rows)), dtype=torch.int32, device=buf.device)
+    rc = lib.mp_probe_read_tiles(buf.data_ptr(), rows, row_bytes, tile_rows, step_bytes, depth, sink.data_ptr(),
+                                 torch.cuda.current_stream(buf.device).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"mp_probe_read_tiles failed with status {rc}")
     return sink

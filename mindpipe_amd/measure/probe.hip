@@ -9,6 +9,10 @@
 //    THREADS = 256, LOADS = 4);
 //  * strided: a fixed grid; workgroup w reads pieces w * THREADS * LOADS + j * grid * THREADS *
 //    LOADS, j = 0, 1, ... (a persistent streaming kernel).
+// A third probe reads a row-major [rows, row_bytes] matrix in the order a tiled GEMM streams its
+// weight operand: workgroup w owns rows [w * tile_rows, +tile_rows) and walks the row length in
+// steps of step_bytes, each step reading step_bytes of every one of its rows, DEPTH steps' loads
+// issued before any is used.
 #include "../csrc/mp_common.h"
 
 namespace {
@@ -56,7 +60,68 @@ int launch_loads(int loads, const void *buf, int64_t n16, int64_t grid, int64_t 
   }
 }
 
+// tile-order read: 256 threads; per step tile_rows * step_bytes / 16 pieces, piece q = row
+// q / (step_bytes / 16) of the tile, 16-byte column q % (step_bytes / 16) of the step
+template <int DEPTH, int PPT>
+__global__ __launch_bounds__(256) void probe_tiles_kernel(const uint4 *__restrict__ p, int64_t rows, int64_t row16,
+                                                          int tile_rows, int step16, uint32_t *__restrict__ sink) {
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * tile_rows;
+  const int64_t steps = row16 / step16;
+  uint32_t x = 0;
+  for (int64_t s0 = 0; s0 < steps; s0 += DEPTH) {
+    uint4 v[DEPTH][PPT];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const int q = static_cast<int>(threadIdx.x) + 256 * i;
+        int64_t row = r0 + q / step16;
+        row = row < rows ? row : rows - 1;
+        int64_t st = s0 + d;
+        st = st < steps ? st : steps - 1;
+        v[d][i] = p[row * row16 + st * step16 + q % step16];
+      }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) x ^= v[d][i].x ^ v[d][i].y ^ v[d][i].z ^ v[d][i].w;
+  }
+  if (x == 0x9E3779B9u) sink[blockIdx.x] = x;
+}
+
 }  // namespace
+
+// Tile-order read of a row-major [rows, row_bytes] matrix (row_bytes a multiple of step_bytes,
+// tile_rows * step_bytes / 16 a multiple of 256 and at most 4096): one workgroup per tile_rows
+// rows, depth in {1, 2, 4} steps in flight; sink: uint32 [ceil(rows / tile_rows)].
+extern "C" int mp_probe_read_tiles(const void *buf, int64_t rows, int64_t row_bytes, int tile_rows, int step_bytes,
+                                   int depth, uint32_t *sink, mp_stream_t stream) {
+  if (!buf || !sink || rows <= 0 || tile_rows <= 0 || step_bytes < 16 || step_bytes % 16 || row_bytes % step_bytes)
+    return MP_ERR_ARG;
+  if (!mp_aligned(buf, 16)) return MP_ERR_ALIGN;
+  const int64_t pieces = static_cast<int64_t>(tile_rows) * (step_bytes / 16);
+  if (pieces % 256 || pieces > 4096) return MP_ERR_SHAPE;
+  const int ppt = static_cast<int>(pieces / 256);
+  const int64_t grid = mp_cdiv(rows, tile_rows);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const auto *pp = static_cast<const uint4 *>(buf);
+  const int64_t row16 = row_bytes / 16;
+  const int step16 = step_bytes / 16;
+#define MP_PT(D_, P_) hipLaunchKernelGGL((probe_tiles_kernel<D_, P_>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, pp, rows, row16, tile_rows, step16, sink)
+#define MP_PT_D(P_) do { if (depth == 1) MP_PT(1, P_); else if (depth == 2) MP_PT(2, P_); else if (depth == 4) MP_PT(4, P_); else return MP_ERR_ARG; } while (0)
+  switch (ppt) {
+    case 1: MP_PT_D(1); break;
+    case 2: MP_PT_D(2); break;
+    case 4: MP_PT_D(4); break;
+    case 8: MP_PT_D(8); break;
+    case 16: MP_PT_D(16); break;
+    default: return MP_ERR_SHAPE;
+  }
+#undef MP_PT_D
+#undef MP_PT
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
 
 // Workgroups of a read of `bytes` with `threads` threads and `loads` 16-byte loads per lane:
 // `grid` > 0 fixes the grid (strided form), grid = 0 gives one-shot workgroups.

@@ -234,3 +234,27 @@ def test_moe_fake_rule_mixtral_shape_sampled(dt):
     rv = ref.astype(np.float32) if dt == "fp16" else O.bf16_bits_to_f32(ref)
     err = _rel(_np(y.float())[toks], rv)
     assert err <= 1e-3, err
+
+
+# the one-row VALU GEMV off the 2048 / 4096 K of the matrix-core GEMV: row counts that leave a partial
+# row group (of 4, or of 8 at N >= 16384), a K that leaves a partial 2048-wide chunk, AWQ zeros and the
+# symmetric export, with and without bias
+ROW_GEMV_EDGES = [(8195, 8192, True, True), (6000, 11008, False, False), (16389, 8192, True, False),
+                  (4099, 16384, False, True)]
+
+
+@pytest.mark.parametrize("n,k,zp,with_bias", ROW_GEMV_EDGES)
+def test_w4a16_one_row_gemv_edges(n, k, zp, with_bias):
+    _say("w4a16 one-row gemv", n, k, zp, with_bias)
+    ops = _ops()
+    packed, s, z = _quant_gpu(n, k, seed=n + k, zp=zp)
+    x = _x(1, k, seed=13)
+    bias = (torch.randn(n, generator=torch.Generator(device=DEV).manual_seed(3), device=DEV) * 0.1).half() \
+        if with_bias else None
+    y = ops.w4a16_gemm(x, packed, s, z, 128, bias)
+    torch.cuda.synchronize()
+    cols = _cols(n, seed=n)
+    assert _rel(_np(y)[:, cols], _ref_cols(x, packed, s, z, cols, k, bias)) <= 1e-3
+    # every output row, against the same kernel run twice (no state left between launches)
+    y2 = ops.w4a16_gemm(x, packed, s, z, 128, bias)
+    assert torch.equal(y, y2)
