@@ -511,6 +511,19 @@ def traffic_probe(ops):
         for i in range(8):
             ops.w4a16_gemm(xk, pk[i % 4], sc[i % 4], zr[i % 4], 128, None)
         del pk, sc, zr
+    # the bf16 legs: M = 1 and M = 16 at K = N = 4096 (64 launches over 64 copies each), then
+    # K = 8192, N = 28672 (8 launches over 4 copies)
+    pk, sc, zr = _w4_copies(ops, 4096, 4096, 64, dtype=torch.bfloat16)
+    for m in (1, 16):
+        xb = torch.randn(m, 4096, device="cuda").bfloat16()
+        for i in range(64):
+            ops.w4a16_gemm(xb, pk[i], sc[i], zr[i], 128, None)
+    del pk, sc, zr
+    pk, sc, zr = _w4_copies(ops, 28672, 8192, 4, dtype=torch.bfloat16)
+    xb = torch.randn(1, 8192, device="cuda").bfloat16()
+    for i in range(8):
+        ops.w4a16_gemm(xb, pk[i % 4], sc[i % 4], zr[i % 4], 128, None)
+    del pk, sc, zr
     # the W8A8 sweep: M = 1, 16, 256 over 13 rotated weight copies (3 rounds), M = 4096 three times
     gen8 = torch.Generator(device="cuda").manual_seed(1)
     wcopies = [torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device="cuda", generator=gen8)
