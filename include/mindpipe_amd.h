@@ -73,6 +73,14 @@ int mp_abi_version(void);
 int mp_w4_quantize_awq(const void *w, int w_dtype, int64_t n, int64_t k, int group_size, int zero_point,
                        int32_t *packed, void *scales, void *zeros, void *w_deq, mp_stream_t stream);
 
+/* pseudo_quantize_tensor(w, n_bit, zero_point, q_group_size, get_scale_zp=True) at any
+ * code width n_bit = 1..8 (2..8 without a zero point) in the arithmetic of w's dtype;
+ * replaces quantizer.py:63-105 for n_bit != 4.  Codes in [0, 2^n - 1] with a zero point,
+ * else [-2^(n-1), 2^(n-1) - 1].  Outputs: scales [N, K/g_eff], zeros [N, K/g_eff]
+ * (zero_point only), w_deq [N,K] (required); no packed codes. */
+int mp_awq_pseudo_quantize(const void *w, int w_dtype, int64_t n, int64_t k, int group_size, int zero_point,
+                           int n_bit, void *scales, void *zeros, void *w_deq, mp_stream_t stream);
+
 /* GPTQ symmetric round-to-nearest group quantizer in fp32: Quantizer.find_params
  * (perchannel, sym) per group + quantize_with_qint and the signed export
  * q - 8; replaces algorithm/quantization/ptq/gptq/source/quant.py:13-17,44-82
@@ -181,6 +189,25 @@ int mp_w8a8_gemm(const int8_t *qx, const float *s_tok, const int8_t *w, const fl
 int mp_w8a8_gemm_fake(const int8_t *qx, const float *s_tok, const int8_t *w, const float *s_ch,
                       const void *bias, int act_dtype, void *y, int64_t m, int64_t n, int64_t k,
                       mp_stream_t stream);
+
+/* The fake-quant linear at any operand widths (fake_quant.py:85-88 with weight_bits /
+ * activation_bits other than 8, SmoothQuantLinear of fake_quant.py:38-113): y[M,N] =
+ * F.linear(A, B, bias) in dtype (fp16 / bf16) where A is int8 codes [M,K] with a_scale
+ * [M] (the value r(q * s) of quantize_activation_per_token_absmax) or, with a_scale NULL,
+ * plain values [M,K] in dtype (activation_bits >= 16); B likewise int8 [N,K] with
+ * b_scale [N] or plain values (weight_bits >= 16).  fp32 accumulation, bias (dtype, or
+ * NULL) added in fp32, one rounding. */
+int mp_dq_linear(const void *a, const float *a_scale, const void *b, const float *b_scale, const void *bias,
+                 int dtype, void *y, int64_t m, int64_t n, int64_t k, mp_stream_t stream);
+
+/* quantize_activation_per_token_absmax / quantize_weight_per_channel_absmax
+ * (fake_quant.py:10-31) at n_bits = 2..7, per row of x [rows, K] (fp16 / bf16), in the
+ * arithmetic of x's dtype: q_max = 2^(n-1) - 1, s = r(r(max(amax, 1e-5)) / q_max),
+ * q = rint(r(x / s)).  Outputs int8 codes [rows, K] (|q| <= q_max + 1) and scale fp32
+ * [rows] (a value of x's dtype); the fake value is r(q * s).  8 bits: MP_SCALE_FAKE of
+ * mp_quant_per_token_i8 / mp_w8_quantize_per_channel. */
+int mp_fake_quant_rows(const void *x, int x_dtype, int64_t rows, int64_t k, int n_bits, int8_t *q, float *scale,
+                       mp_stream_t stream);
 
 /* Output-quant W8A8 linear: y[M,N] = mp_w8a8_gemm's output (out_dtype fp16 / bf16, bias in
  * bias_dtype or NULL) together with its per-token int8 codes q_out[M,N] and scale s_out[M]:

@@ -23,6 +23,7 @@ SIGNATURES = {
     "mp_strerror": (C.c_char_p, [_i32]),
     "mp_abi_version": (_i32, []),
     "mp_w4_quantize_awq": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "mp_awq_pseudo_quantize": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "mp_w4_quantize_gptq_rtn": (_i32, [_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _vp]),
     "mp_pack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "mp_unpack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp]),
@@ -59,6 +60,8 @@ SIGNATURES = {
                                                  _vp, _vp]),
     "mp_w8a8_grouped_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp]),
     "mp_w8a8_gemm_fake": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
+    "mp_dq_linear": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
+    "mp_fake_quant_rows": (_i32, [_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp]),
     "mp_moe_unpermute_combine": (_i32, [_vp, _vp, _vp, _i64, _i32, _i64, _i32, _vp, _i32, _vp]),
 }
 

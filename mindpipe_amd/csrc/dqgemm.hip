@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void dq_gemm_kernel(mp_dq_args p) {
   __shared__ __attribute__((aligned(16))) uint16_t sb[2][kDBN * kDLD];
   constexpr bool SWI = EPI == MP_EPI_SWIGLU;
   constexpr int ACH = AF == MP_DQ_DT ? 4 : 2;  // 16-byte A pieces per thread per K tile
-  constexpr int BCH = BF == MP_DQ_U4GRP ? 1 : 2;
+  constexpr int BCH = BF == MP_DQ_U4GRP ? 1 : (BF == MP_DQ_DT ? 4 : 2);
   int64_t rb, re;
   int expert;
   if (!dq_rows(p, rb, re, expert)) return;  // workgroup-uniform
@@ -154,8 +154,8 @@ __global__ __launch_bounds__(256) void dq_gemm_kernel(mp_dq_args p) {
 #pragma unroll
   for (int i = 0; i < BCH; ++i) {
     const int c = tid + i * 256;
-    brow[i] = BF == MP_DQ_U4GRP ? (c >> 1) : (c >> 2);
-    bcol[i] = BF == MP_DQ_U4GRP ? (c & 1) * 32 : (c & 3) * 16;
+    brow[i] = BF == MP_DQ_U4GRP ? (c >> 1) : (BF == MP_DQ_DT ? (c >> 3) : (c >> 2));
+    bcol[i] = BF == MP_DQ_U4GRP ? (c & 1) * 32 : (BF == MP_DQ_DT ? (c & 7) * 8 : (c & 3) * 16);
     int64_t n;
     if (SWI) {
       const int64_t cc = col0 + (brow[i] & 63);
@@ -166,6 +166,10 @@ __global__ __launch_bounds__(256) void dq_gemm_kernel(mp_dq_args p) {
     bn[i] = n;
     if (BF == MP_DQ_U4GRP) {
       bptr[i] = static_cast<const uint8_t *>(p.b) + n * (k / 2) + bcol[i] / 2;
+      bscale[i] = 0.f;
+    } else if (BF == MP_DQ_DT) {
+      const int64_t rowg = static_cast<int64_t>(expert) * nb_rows + n;
+      bptr[i] = static_cast<const uint8_t *>(p.b) + (rowg * k + bcol[i]) * 2;
       bscale[i] = 0.f;
     } else {
       const int64_t rowg = static_cast<int64_t>(expert) * nb_rows + n;
@@ -190,7 +194,7 @@ __global__ __launch_bounds__(256) void dq_gemm_kernel(mp_dq_args p) {
         bs[i] = dq_to_f32<DT>(p.b_gscale[gi]);
         bz[i] = p.b_gzero ? dq_to_f32<DT>(p.b_gzero[gi]) : 8.0f;
       } else {
-        breg[i] = *reinterpret_cast<const uint4 *>(bptr[i] + kb);
+        breg[i] = *reinterpret_cast<const uint4 *>(bptr[i] + kb * (BF == MP_DQ_DT ? 2 : 1));
       }
     }
   };
@@ -214,6 +218,8 @@ __global__ __launch_bounds__(256) void dq_gemm_kernel(mp_dq_args p) {
         const uint32_t w[4] = {breg[i].x, breg[i].y, breg[i].z, breg[i].w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4 *>(dst + 8 * q) = dq_u4x8<DT>(w[q], bz[i], bs[i]);
+      } else if (BF == MP_DQ_DT) {
+        *reinterpret_cast<uint4 *>(dst) = breg[i];
       } else {
         uint4 lo, hi;
         dq_i8x16<DT>(breg[i], bscale[i], lo, hi);
@@ -339,6 +345,8 @@ __global__ __launch_bounds__(256) void dq_simple_kernel(mp_dq_args p) {
         const float s = dq_to_f32<DT>(p.b_gscale[gi]);
         const float z = p.b_gzero ? dq_to_f32<DT>(p.b_gzero[gi]) : 8.0f;
         w = (static_cast<float>(u) - z) * s;
+      } else if (BF == MP_DQ_DT) {
+        w = dq_to_f32<DT>(static_cast<const uint16_t *>(p.b)[rowg * k + kk]);
       } else {
         w = static_cast<float>(static_cast<const int8_t *>(p.b)[rowg * k + kk]) * p.b_scale[rowg];
       }
@@ -401,7 +409,8 @@ int mp_launch_dq_gemm(const mp_dq_args &p, int epi, hipStream_t stream) {
   if (p.rows == 0) return MP_OK;
   const bool u4 = p.b_fmt == MP_DQ_U4GRP;
   if (u4 && (p.offsets || !p.b_gscale || p.group <= 0 || p.k % p.group || p.k % 8)) return MP_ERR_SHAPE;
-  if (!u4 && (p.b_fmt != MP_DQ_I8ROW || !p.b_scale)) return MP_ERR_ARG;
+  if (p.b_fmt == MP_DQ_I8ROW && !p.b_scale) return MP_ERR_ARG;
+  if (p.b_fmt != MP_DQ_I8ROW && p.b_fmt != MP_DQ_DT && !u4) return MP_ERR_ARG;
   if (p.a_fmt == MP_DQ_I8ROW && !p.a_scale) return MP_ERR_ARG;
   if (p.a_fmt != MP_DQ_DT && p.a_fmt != MP_DQ_I8ROW) return MP_ERR_ARG;
   if (epi == MP_EPI_SWIGLU && (!p.amax_partial || p.n_partial < 2 * mp_cdiv(p.n, 64))) return MP_ERR_ARG;
@@ -409,13 +418,45 @@ int mp_launch_dq_gemm(const mp_dq_args &p, int epi, hipStream_t stream) {
   // 32-bit descriptor offsets over A and 32-bit tile arithmetic
   if (p.rows * p.k * (p.a_fmt == MP_DQ_DT ? 2 : 1) >= (int64_t(1) << 31) || p.k > (1 << 20)) return MP_ERR_SHAPE;
   if (p.k % kDBK == 0 && (!mp_aligned(p.a, 16) || !mp_aligned(p.b, 16))) return MP_ERR_ALIGN;  // tiled loads
-  const bool a8 = p.a_fmt == MP_DQ_I8ROW;
+  const bool a8 = p.a_fmt == MP_DQ_I8ROW, b8 = p.b_fmt == MP_DQ_I8ROW;
+  if (u4 && a8) return MP_ERR_ARG;  // packed weights multiply plain activations only
   if (p.dt == MP_F16) {
-    if (u4 && !a8) return dq_launch_fmt<MP_F16, MP_DQ_DT, MP_DQ_U4GRP>(p, epi, stream);
-    if (!u4 && a8) return dq_launch_fmt<MP_F16, MP_DQ_I8ROW, MP_DQ_I8ROW>(p, epi, stream);
-  } else {
-    if (u4 && !a8) return dq_launch_fmt<MP_BF16, MP_DQ_DT, MP_DQ_U4GRP>(p, epi, stream);
-    if (!u4 && a8) return dq_launch_fmt<MP_BF16, MP_DQ_I8ROW, MP_DQ_I8ROW>(p, epi, stream);
+    if (u4) return dq_launch_fmt<MP_F16, MP_DQ_DT, MP_DQ_U4GRP>(p, epi, stream);
+    if (a8 && b8) return dq_launch_fmt<MP_F16, MP_DQ_I8ROW, MP_DQ_I8ROW>(p, epi, stream);
+    if (b8) return dq_launch_fmt<MP_F16, MP_DQ_DT, MP_DQ_I8ROW>(p, epi, stream);
+    if (a8) return dq_launch_fmt<MP_F16, MP_DQ_I8ROW, MP_DQ_DT>(p, epi, stream);
+    return dq_launch_fmt<MP_F16, MP_DQ_DT, MP_DQ_DT>(p, epi, stream);
   }
-  return MP_ERR_ARG;  // the combinations the callers use are the two above
+  if (u4) return dq_launch_fmt<MP_BF16, MP_DQ_DT, MP_DQ_U4GRP>(p, epi, stream);
+  if (a8 && b8) return dq_launch_fmt<MP_BF16, MP_DQ_I8ROW, MP_DQ_I8ROW>(p, epi, stream);
+  if (b8) return dq_launch_fmt<MP_BF16, MP_DQ_DT, MP_DQ_I8ROW>(p, epi, stream);
+  if (a8) return dq_launch_fmt<MP_BF16, MP_DQ_I8ROW, MP_DQ_DT>(p, epi, stream);
+  return dq_launch_fmt<MP_BF16, MP_DQ_DT, MP_DQ_DT>(p, epi, stream);
+}
+
+// The fake-quant linear at any operand widths: y = F.linear(dq(a), dq(b), bias) with each operand
+// either plain values in the dtype (a width of 16 bits or more: not quantized) or int8 codes with
+// a per-row scale, rounded to the dtype as the reference's fake-quant tensors are.
+extern "C" int mp_dq_linear(const void *a, const float *a_scale, const void *b, const float *b_scale,
+                            const void *bias, int dtype, void *y, int64_t m, int64_t n, int64_t k,
+                            mp_stream_t stream) {
+  if (!a || !b || !y) return MP_ERR_ARG;
+  if (dtype != MP_F16 && dtype != MP_BF16) return MP_ERR_DTYPE;
+  mp_dq_args d{};
+  d.dt = dtype;
+  d.a = a;
+  d.a_fmt = a_scale ? MP_DQ_I8ROW : MP_DQ_DT;
+  d.a_scale = a_scale;
+  d.b = b;
+  d.b_fmt = b_scale ? MP_DQ_I8ROW : MP_DQ_DT;
+  d.b_scale = b_scale;
+  d.bias = bias;
+  d.bias_dtype = dtype;
+  d.y = y;
+  d.out_dtype = dtype;
+  d.ldy = n;
+  d.rows = m;
+  d.n = n;
+  d.k = k;
+  return mp_launch_dq_gemm(d, MP_EPI_DENSE, reinterpret_cast<hipStream_t>(stream));
 }

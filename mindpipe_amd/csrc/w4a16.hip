@@ -97,7 +97,7 @@ __device__ __forceinline__ uint16_t awq_st(float v) { return DT == MP_F16 ? mp_f
 
 template <int DT>
 __global__ __launch_bounds__(256) void awq_quantize_kernel(
-    const uint16_t *__restrict__ w, int64_t n_rows, int64_t k, int gs, int n_groups, int zero_point,
+    const uint16_t *__restrict__ w, int64_t n_rows, int64_t k, int gs, int n_groups, int zero_point, int n_bit,
     uint32_t *__restrict__ packed, int64_t kw, uint16_t *__restrict__ scales,
     uint16_t *__restrict__ zeros, uint16_t *__restrict__ wdeq) {
   const int lane = threadIdx.x & 63;
@@ -117,29 +117,32 @@ __global__ __launch_bounds__(256) void awq_quantize_kernel(
   mx = mp_wave_max(mx);
   mn = mp_wave_min(mn);
 
+  // n_bit-wide codes (1..8): [0, 2^n - 1] with a zero point, else [-2^(n-1), 2^(n-1) - 1];
+  // every bound is exact in fp16 and bf16
   float s, z, qmin, qmax;
   if (zero_point) {
+    qmin = 0.0f;
+    qmax = static_cast<float>((1 << n_bit) - 1);
     float d = awq_r<DT>(mx - mn);
     if (d < 1e-5f) d = awq_r<DT>(1e-5f);
-    s = awq_r<DT>(d / 15.0f);
+    s = awq_r<DT>(d / qmax);
     z = -rintf(awq_r<DT>(mn / s));
     if (z < 0.0f) z = 0.0f;   // keeps -0.0 like torch.clamp_
-    if (z > 15.0f) z = 15.0f;
-    qmin = 0.0f;
-    qmax = 15.0f;
+    if (z > qmax) z = qmax;
   } else {
+    qmin = -static_cast<float>(1 << (n_bit - 1));
+    qmax = static_cast<float>((1 << (n_bit - 1)) - 1);
     float a = mx;
     if (a < 1e-5f) a = awq_r<DT>(1e-5f);
-    s = awq_r<DT>(a / 7.0f);
+    s = awq_r<DT>(a / qmax);
     z = 0.0f;
-    qmin = -8.0f;
-    qmax = 7.0f;
   }
   if (lane == 0) {
     scales[row * n_groups + gi] = awq_st<DT>(s);
     if (zero_point) zeros[row * n_groups + gi] = awq_st<DT>(z);
   }
-  // pass 2: one packed word (8 consecutive columns) per lane iteration
+  // pass 2: one packed word (8 consecutive columns) per lane iteration (4-bit codes only;
+  // packed is null for other widths)
   const int nwords = (gs + 7) / 8;
   for (int c = lane; c < nwords; c += 64) {
     uint32_t word = 0;
@@ -157,7 +160,7 @@ __global__ __launch_bounds__(256) void awq_quantize_kernel(
       const uint32_t u = static_cast<uint32_t>(static_cast<int>(q) + (zero_point ? 0 : 8));
       word |= u << (4 * j);
     }
-    packed[row * kw + e0 / 8 + c] = word;
+    if (packed) packed[row * kw + e0 / 8 + c] = word;
   }
 }
 
@@ -1822,6 +1825,24 @@ static int mp_prefill_threads() {
 
 // ====================================================================== C ABI
 
+static int mp_launch_awq(const void *w, int w_dtype, int64_t n, int64_t k, int64_t gs, int zero_point, int n_bit,
+                         int32_t *packed, void *scales, void *zeros, void *w_deq, mp_stream_t stream) {
+  const int64_t n_groups = k / gs;
+  const int64_t total = n * n_groups;
+  const int64_t kw = mp_cdiv(k, 8);
+#define MP_AWQ(DT_)                                                                                          \
+  hipLaunchKernelGGL(awq_quantize_kernel<DT_>, dim3(static_cast<unsigned>(mp_cdiv(total, 4))), dim3(256), 0,  \
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t *>(w), n, k,         \
+                     static_cast<int>(gs), static_cast<int>(n_groups), zero_point, n_bit,                   \
+                     reinterpret_cast<uint32_t *>(packed), kw, static_cast<uint16_t *>(scales),             \
+                     static_cast<uint16_t *>(zeros), static_cast<uint16_t *>(w_deq))
+  if (w_dtype == MP_F16) MP_AWQ(MP_F16);
+  else MP_AWQ(MP_BF16);
+#undef MP_AWQ
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
 extern "C" int mp_w4_quantize_awq(const void *w, int w_dtype, int64_t n, int64_t k, int group_size, int zero_point,
                                   int32_t *packed, void *scales, void *zeros, void *w_deq,
                                   mp_stream_t stream) {
@@ -1831,20 +1852,21 @@ extern "C" int mp_w4_quantize_awq(const void *w, int w_dtype, int64_t n, int64_t
   const int64_t gs = (group_size > 0 && k % group_size == 0) ? group_size : k;
   if (gs % 8 != 0 && gs != k) return MP_ERR_SHAPE;
   if (gs > (1 << 30)) return MP_ERR_SHAPE;
-  const int64_t n_groups = k / gs;
-  const int64_t total = n * n_groups;
-  const int64_t kw = mp_cdiv(k, 8);
-#define MP_AWQ(DT_)                                                                                          \
-  hipLaunchKernelGGL(awq_quantize_kernel<DT_>, dim3(static_cast<unsigned>(mp_cdiv(total, 4))), dim3(256), 0,  \
-                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t *>(w), n, k,         \
-                     static_cast<int>(gs), static_cast<int>(n_groups), zero_point,                          \
-                     reinterpret_cast<uint32_t *>(packed), kw, static_cast<uint16_t *>(scales),             \
-                     static_cast<uint16_t *>(zeros), static_cast<uint16_t *>(w_deq))
-  if (w_dtype == MP_F16) MP_AWQ(MP_F16);
-  else MP_AWQ(MP_BF16);
-#undef MP_AWQ
-  MP_CHECK_LAUNCH();
-  return MP_OK;
+  return mp_launch_awq(w, w_dtype, n, k, gs, zero_point, 4, packed, scales, zeros, w_deq, stream);
+}
+
+// Pseudo-quantization at any code width from 1 to 8 bits: the dequantized weight and, with a
+// zero point, the group scales / zeros (no packed codes).
+extern "C" int mp_awq_pseudo_quantize(const void *w, int w_dtype, int64_t n, int64_t k, int group_size,
+                                      int zero_point, int n_bit, void *scales, void *zeros, void *w_deq,
+                                      mp_stream_t stream) {
+  if (!w || !scales || !w_deq || (zero_point && !zeros)) return MP_ERR_ARG;
+  if (w_dtype != MP_F16 && w_dtype != MP_BF16) return MP_ERR_DTYPE;
+  if (n_bit < 1 || n_bit > 8 || (!zero_point && n_bit < 2)) return MP_ERR_ARG;
+  if (n <= 0 || k <= 0) return MP_ERR_SHAPE;
+  const int64_t gs = (group_size > 0 && k % group_size == 0) ? group_size : k;
+  if (gs > (1 << 30)) return MP_ERR_SHAPE;
+  return mp_launch_awq(w, w_dtype, n, k, gs, zero_point, n_bit, nullptr, scales, zeros, w_deq, stream);
 }
 
 extern "C" int mp_w4_quantize_gptq_rtn(const void *w, int w_dtype, int64_t n, int64_t k, int group_size,

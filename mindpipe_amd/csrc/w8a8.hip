@@ -43,6 +43,33 @@ __global__ __launch_bounds__(256) void rowquant_kernel(const void *__restrict__ 
   }
 }
 
+// The fake per-row rule at a code width of 2..7 bits (quantize_*_absmax with n_bits < 8,
+// fake_quant.py:10-31): q_max = 2^(n-1) - 1, s = r(r(max(amax, 1e-5)) / q_max), code =
+// rint(r(v / s)), every op rounded to the input dtype.  |r(v / s)| stays below q_max + 1 (s is
+// within half an ulp of amax / q_max), so the codes fit int8 and need no sign rule.
+__global__ __launch_bounds__(256) void fake_rows_nbit_kernel(const void *__restrict__ x, int x_dtype, int64_t k,
+                                                             float q_max, int8_t *__restrict__ q,
+                                                             float *__restrict__ s_out) {
+  __shared__ float red[3][4];
+  __shared__ int wbad[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t base = row * k;
+  const int mode = mp_round_mode_of(x_dtype);
+  mp_rowstat st{0.f, 0.f, 0.f, 0};
+  for (int64_t c = tid; c < k; c += 256) st.amax = fmaxf(st.amax, fabsf(mp_load_as_f32(x, base + c, x_dtype)));
+  st = mp_block_rowstat(st, red, wbad);
+  float a = mp_round_mode_apply(st.amax, mode);
+  if (a < 1e-5f) a = mp_round_mode_apply(1e-5f, mode);
+  const float s = mp_round_mode_apply(a / q_max, mode);
+  if (tid == 0) s_out[row] = s;
+  for (int64_t c = tid; c < k; c += 256) {
+    const float v = mp_load_as_f32(x, base + c, x_dtype);
+    const float code = rintf(mp_round_mode_apply(v / s, mode));
+    q[base + c] = static_cast<int8_t>(static_cast<int>(fminf(fmaxf(code, -128.f), 127.f)));
+  }
+}
+
 // The same quantizer with 16-byte loads and 4- or 8-byte code stores (k a multiple of the
 // values per 16 bytes, 16-byte aligned rows); the per-element arithmetic is the same.
 template <int RULE, int DT>
@@ -2118,6 +2145,21 @@ extern "C" int mp_quant_per_token_i8(const void *x, int64_t m, int64_t k, int x_
   } else {
     return MP_ERR_ARG;
   }
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
+
+extern "C" int mp_fake_quant_rows(const void *x, int x_dtype, int64_t rows, int64_t k, int n_bits, int8_t *q,
+                                  float *scale, mp_stream_t stream) {
+  if (!x || !q || !scale) return MP_ERR_ARG;
+  if (x_dtype != MP_F16 && x_dtype != MP_BF16) return MP_ERR_DTYPE;
+  if (n_bits < 2 || n_bits > 7) return MP_ERR_ARG;
+  if (rows < 0 || k <= 0) return MP_ERR_SHAPE;
+  if (rows == 0) return MP_OK;
+  if (rows > INT32_MAX) return MP_ERR_SHAPE;
+  hipLaunchKernelGGL(fake_rows_nbit_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), x, x_dtype, k,
+                     static_cast<float>((1 << (n_bits - 1)) - 1), q, scale);
   MP_CHECK_LAUNCH();
   return MP_OK;
 }

@@ -65,6 +65,22 @@ def w4_quantize_awq(w: torch.Tensor, group_size: int = 128, zero_point: bool = T
     return packed, scales, zeros, deq
 
 
+def awq_pseudo_quantize(w: torch.Tensor, n_bit: int, group_size: int = 128, zero_point: bool = True):
+    """AWQ ``pseudo_quantize_tensor`` at any code width ``n_bit`` (1..8; 2..8 without a zero point) in
+    the arithmetic of ``w``'s dtype: returns ``(scales, zeros, w_deq)`` (zeros ``None`` when symmetric)."""
+    _need(w, "w", (torch.float16, torch.bfloat16), 2)
+    n, k = w.shape
+    g = group_size if (group_size > 0 and k % group_size == 0) else k
+    scales = torch.empty((n, k // g), dtype=w.dtype, device=w.device)
+    zeros = torch.empty_like(scales) if zero_point else None
+    deq = torch.empty_like(w)
+    with _dev(w):
+        _lib.check(_lib.load().mp_awq_pseudo_quantize(
+            w.data_ptr(), _DT[w.dtype], n, k, group_size, int(zero_point), int(n_bit), scales.data_ptr(),
+            _ptr(zeros), deq.data_ptr(), _stream()), "mp_awq_pseudo_quantize")
+    return scales, zeros, deq
+
+
 def w4_quantize_gptq_rtn(w: torch.Tensor, group_size: int = 128):
     """GPTQ symmetric RTN group quantizer: returns ``(int_weight int8, packed int32, scale fp16)``."""
     _need(w, "w", (torch.float32, torch.float16, torch.bfloat16), 2)
@@ -357,6 +373,53 @@ def _(qx, s_tok, w, s_ch, bias, act_dtype):
 
 # ---------------------------------------------------------------- MoE
 _RULES = {"runtime": MP_SCALE_FP32, "fake": MP_SCALE_FAKE}
+
+
+def fake_quant_rows(x: torch.Tensor, n_bits: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row fake quant at ``n_bits`` = 2..7 (``quantize_*_absmax`` with ``n_bits < 8``) in the
+    arithmetic of ``x``'s dtype (fp16 / bf16): ``(int8 codes [.., K], fp32 scale [..])``; the fake
+    value is ``r(q * s)``."""
+    _need(x, "x", (torch.float16, torch.bfloat16))
+    k = x.shape[-1]
+    x2 = x.reshape(-1, k)
+    q = torch.empty(x2.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty((x2.shape[0],), dtype=torch.float32, device=x.device)
+    with _dev(x):
+        _lib.check(_lib.load().mp_fake_quant_rows(x2.data_ptr(), _DT[x.dtype], x2.shape[0], k, int(n_bits),
+                                                  q.data_ptr(), s.data_ptr(), _stream()), "mp_fake_quant_rows")
+    return q.reshape(x.shape), s.reshape(x.shape[:-1])
+
+
+def dq_linear(a: torch.Tensor, a_scale: Optional[torch.Tensor], b: torch.Tensor, b_scale: Optional[torch.Tensor],
+              bias: Optional[torch.Tensor], dtype: torch.dtype) -> torch.Tensor:
+    """``F.linear(A, B, bias)`` in ``dtype`` (fp16 / bf16) where A is int8 codes with a per-row fp32
+    scale (the fake value ``r(q * s)``) or, with ``a_scale`` None, plain values in ``dtype``; B
+    likewise ([N, K]).  fp32 accumulation, one rounding: the fake-quant linear at any operand widths."""
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError("the fake-quant linear runs in fp16 or bf16")
+    k = a.shape[-1]
+    a2 = a.reshape(-1, k)
+    m = a2.shape[0]
+    _need(a2, "a", torch.int8 if a_scale is not None else dtype, 2)
+    _need(b, "b", torch.int8 if b_scale is not None else dtype, 2)
+    n = b.shape[0]
+    if b.shape[1] != k:
+        raise RuntimeError(f"b {tuple(b.shape)} does not match K={k}")
+    if a_scale is not None:
+        _need(a_scale, "a_scale", torch.float32)
+        if a_scale.numel() != m:
+            raise RuntimeError("a_scale does not match the rows of a")
+    if b_scale is not None:
+        _need(b_scale, "b_scale", torch.float32, 1)
+        if b_scale.numel() != n:
+            raise RuntimeError("b_scale does not match the rows of b")
+    if bias is not None:
+        _need(bias, "bias", dtype, 1)
+    y = torch.empty((m, n), dtype=dtype, device=a.device)
+    with _dev(a):
+        _lib.check(_lib.load().mp_dq_linear(a2.data_ptr(), _ptr(a_scale), b.data_ptr(), _ptr(b_scale), _ptr(bias),
+                                            _DT[dtype], y.data_ptr(), m, n, k, _stream()), "mp_dq_linear")
+    return y.reshape(*a.shape[:-1], n)
 
 
 @torch.library.custom_op("mindpipe_amd::w8a8_gemm_quant_out", mutates_args=())

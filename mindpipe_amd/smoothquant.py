@@ -9,6 +9,12 @@ Mirrors ``algorithm/quantization/ptq/smoothquant/source/smoothquant/fake_quant.p
 codes with per-row scales and ``forward`` runs the per-token int8 quantizer and the
 int8 MFMA GEMM (or the MoE chain) instead of fake-quant ``F.linear``.
 
+Widths: ``weight_bits`` / ``activation_bits`` of 8 run the int8 path above; 2..7 keep int8
+codes of the narrower rule (``q_max = 2^(n-1) - 1``) and >= 16 leave the operand unquantized, as
+the reference does; those combinations multiply on the dequantising GEMM, which rounds each
+operand element as the reference's fake-quant tensors are.  9..15 bits would need codes wider
+than int8 and raise ``NotImplementedError``.
+
 Scale rule (``scale_rule``):
   * ``"fake"`` (default for the modules): the arithmetic of the reference's
     ``quantize_*_absmax`` in the module dtype (fp16 or bf16) -- ``q * s`` is the value the
@@ -57,6 +63,23 @@ def _require_gpu(t: torch.Tensor, what: str) -> None:
 _FAKE_DTYPES = (torch.float16, torch.bfloat16)
 
 
+def _width(bits, what: str) -> int:
+    """The code width of a quantizer argument: 2..8, or >= 16 for no quantization."""
+    b = int(bits)
+    if b >= 16 or 2 <= b <= 8:
+        return b
+    raise NotImplementedError(f"{what}={b}: this build quantizes to 2..8-bit int8 codes (or >= 16: none)")
+
+
+def _row_codes(t2: torch.Tensor, n_bits: int):
+    """Fake-rule codes of the rows of a 2-D fp16 / bf16 tensor at ``n_bits`` (2..8): ``(int8 q,
+    fp32 s)`` with ``r(q * s)`` the reference's fake-quant value."""
+    if n_bits == 8:
+        q, s = ops.quant_per_token_i8(t2, True)
+        return q, s.float()
+    return ops.fake_quant_rows(t2, n_bits)
+
+
 @torch.no_grad()
 def quantize_weight_per_channel_absmax(weight: torch.Tensor, n_bits: int = 8) -> torch.Tensor:
     """Fake-quantized weight (``q * s`` in the weight dtype), as ``fake_quant.py:10-19`` returns it.
@@ -65,29 +88,32 @@ def quantize_weight_per_channel_absmax(weight: torch.Tensor, n_bits: int = 8) ->
     the returned tensor holds the same values as the reference's (the sign of an exact zero
     is not carried by int8 codes).  ``n_bits >= 16`` returns a copy, like the reference.
     """
-    if int(n_bits) >= 16:
+    n_bits = _width(n_bits, "n_bits")
+    if n_bits >= 16:
         return weight.detach().clone()
-    if int(n_bits) != 8:
-        raise NotImplementedError("mindpipe_amd quantizes weights to 8 bits per channel")
     _require_gpu(weight, "quantize_weight_per_channel_absmax")
     shape = weight.shape
     w2 = weight.detach().reshape(-1, shape[-1]).contiguous()
     if w2.dtype not in _FAKE_DTYPES:
         raise NotImplementedError("the fake-quant rule takes fp16 or bf16 weights")
-    q, s32, _ = ops.w8_quantize_per_channel(w2, "fake")
+    if n_bits == 8:
+        q, s32, _ = ops.w8_quantize_per_channel(w2, "fake")
+    else:
+        q, s32 = ops.fake_quant_rows(w2, n_bits)
     return (q.float() * s32[:, None]).to(weight.dtype).reshape(shape)
 
 
 @torch.no_grad()
 def quantize_activation_per_token_absmax(tensor: torch.Tensor, n_bits: int = 8) -> torch.Tensor:
     """Fake-quantized activation (``q * s`` in the input dtype), as ``fake_quant.py:22-31`` returns it."""
-    if int(n_bits) >= 16:
+    n_bits = _width(n_bits, "n_bits")
+    if n_bits >= 16:
         return tensor
-    if int(n_bits) != 8:
-        raise NotImplementedError("mindpipe_amd quantizes activations to 8 bits per token")
     _require_gpu(tensor, "quantize_activation_per_token_absmax")
-    q, s = ops.quant_per_token_i8(tensor.contiguous(), True)
-    return (q.float() * s.float().unsqueeze(-1)).to(tensor.dtype)
+    if tensor.dtype not in _FAKE_DTYPES:
+        raise NotImplementedError("the fake-quant rule takes fp16 or bf16 activations")
+    q, s = _row_codes(tensor.contiguous(), n_bits)
+    return (q.float() * s.unsqueeze(-1)).to(tensor.dtype)
 
 
 class SmoothQuantLinear(nn.Module):
@@ -103,16 +129,14 @@ class SmoothQuantLinear(nn.Module):
         super().__init__()
         self.in_features = in_features
         self.out_features = out_features
-        self.weight_bits = int(weight_bits)
-        self.activation_bits = int(activation_bits)
+        self.weight_bits = _width(weight_bits, "weight_bits")
+        self.activation_bits = _width(activation_bits, "activation_bits")
         if act_quant != "per_token":
             raise ValueError(f"Invalid act_quant: {act_quant}")
-        if self.weight_bits < 16 and self.weight_bits != 8:
-            raise NotImplementedError("weight_bits must be 8 (or >= 16 for no quantization)")
-        if self.activation_bits < 16 and self.activation_bits != 8:
-            raise NotImplementedError("activation_bits must be 8 (or >= 16 for no quantization)")
         if scale_rule not in ("fake", "export"):
             raise ValueError(f"Invalid scale_rule: {scale_rule}")
+        if scale_rule == "export" and (self.weight_bits, self.activation_bits) != (8, 8):
+            raise ValueError("scale_rule='export' is the W8A8 runtime rule (8-bit weights and activations)")
         self.scale_rule = scale_rule
         self.dtype = dtype
         wdt = torch.int8 if self.weight_bits < 16 else dtype
@@ -143,11 +167,35 @@ class SmoothQuantLinear(nn.Module):
             return self.weight
         return (self.weight.float() * self.weight_scale[:, None]).to(self.dtype)
 
+    @property
+    def _w8a8(self) -> bool:
+        return self.weight_bits == 8 and self.activation_bits == 8
+
+    def _linear_any_width(self, x):
+        """``F.linear(act_quant(x), weight, bias)`` at widths other than W8A8 on the dequantising
+        GEMM: each operand int8 codes of its width (rounded as ``r(q * s)``) or plain values."""
+        if x.dtype not in _FAKE_DTYPES:
+            raise NotImplementedError("the fake-quant linear runs in fp16 or bf16")
+        x2 = x.reshape(-1, self.in_features).contiguous()
+        if self.activation_bits < 16:
+            qa, sa = _row_codes(x2, self.activation_bits)
+        else:
+            qa, sa = x2, None
+        if self.weight_bits < 16:
+            qb, sb = self.weight, self.weight_scale
+        else:
+            if self.weight.dtype != x.dtype:
+                raise RuntimeError(f"input dtype {x.dtype} does not match the weight's {self.weight.dtype}")
+            qb, sb = self.weight, None
+        bias = None if self.bias is None else self.bias.to(x.dtype)
+        y = ops.dq_linear(qa, sa, qb, sb, bias, x.dtype)
+        return y.reshape(*x.shape[:-1], self.out_features)
+
     @torch.no_grad()
     def forward(self, x):
         _require_gpu(x, "SmoothQuantLinear")
-        if self.weight_bits >= 16:
-            return self.output_quant(F.linear(self.act_quant(x), self.weight, self.bias))
+        if not self._w8a8:
+            return self.output_quant(self._linear_any_width(x))
         fake, q, s = self._input_codes(x)
         if self._fused_output_quant(x, fake):
             qo, so = self._output_codes(q, s, x.dtype)
@@ -155,8 +203,6 @@ class SmoothQuantLinear(nn.Module):
         return self.output_quant(self._linear(x, fake, q, s))
 
     def _input_codes(self, x):
-        if self.activation_bits >= 16:
-            raise NotImplementedError("W8A16 is not a path of this build (weights int8 need int8 activations)")
         fake = self.scale_rule == "fake"
         if fake and x.dtype not in _FAKE_DTYPES:
             raise NotImplementedError("the fake scale rule takes fp16 or bf16 activations")
@@ -193,8 +239,11 @@ class SmoothQuantLinear(nn.Module):
         and per-token scale of the reference's output fake quant (``fake_quant.py:77-82``), from the
         GEMM epilogue, for consumers that take quantized q/k/v (the ``return_scale`` form)."""
         _require_gpu(x, "SmoothQuantLinear")
-        if self.output_quant_name == "none" or self.weight_bits >= 16:
-            raise RuntimeError("quantized_output needs an int8 linear with quantize_output=True")
+        if self.output_quant_name == "none":
+            raise RuntimeError("quantized_output needs quantize_output=True")
+        if not self._w8a8:
+            y = self._linear_any_width(x)
+            return _row_codes(y.reshape(-1, self.out_features).contiguous(), self.activation_bits)
         fake, q, s = self._input_codes(x)
         if self._fused_output_quant(x, fake):
             return self._output_codes(q, s, x.dtype)
@@ -211,7 +260,13 @@ class SmoothQuantLinear(nn.Module):
         new = new.to(device=module.weight.device)
         if new.weight_bits < 16:
             _require_gpu(module.weight, "SmoothQuantLinear.from_float")
-            q, s32, _ = ops.w8_quantize_per_channel(module.weight.detach().contiguous(), scale_rule)
+            w = module.weight.detach().contiguous()
+            if new.weight_bits == 8:
+                q, s32, _ = ops.w8_quantize_per_channel(w, scale_rule)
+            else:
+                if w.dtype not in _FAKE_DTYPES:
+                    raise NotImplementedError("the fake-quant rule takes fp16 or bf16 weights")
+                q, s32 = ops.fake_quant_rows(w, new.weight_bits)
             new.weight = q
             new.weight_scale = s32
         else:
@@ -240,28 +295,32 @@ class SmoothQuantPackedMoeExperts(nn.Module):
     SwiGLU + requant -> grouped GEMM2 -> un-permute (one launch each).  With
     ``scale_rule="fake"`` (default) every step rounds as the reference module does, in the
     weight dtype (fp16 / bf16); ``"export"`` is the fp32-scale runtime chain of
-    ``vllm_ascend.patch:2356-2423``.  ``act_fn`` must be SiLU (the fused SwiGLU)."""
+    ``vllm_ascend.patch:2356-2423``.
+
+    W8A8 with a SiLU ``act_fn`` runs the fused chain above.  Other widths (2..8, or >= 16 for
+    none) and other activations run the reference's expert loop (``fake_quant.py:166-191``) with
+    every linear on the dequantising GEMM and ``act_fn`` applied to its fp16 / bf16 output."""
 
     def __init__(self, gate_up_proj, down_proj, act_fn, *, weight_bits=8, activation_bits=8, scale_rule="fake"):
         super().__init__()
         self.num_experts = int(gate_up_proj.shape[0])
         self.hidden_dim = int(gate_up_proj.shape[2])
         self.intermediate_dim = int(down_proj.shape[2])
-        self.weight_bits = int(weight_bits)
-        self.activation_bits = int(activation_bits)
-        if self.weight_bits != 8 or self.activation_bits != 8:
-            raise NotImplementedError("the packed MoE path is W8A8")
-        if not _is_silu(act_fn):
-            raise NotImplementedError(f"the fused expert kernel computes SiLU(gate) * up; got {act_fn!r}")
+        self.weight_bits = _width(weight_bits, "weight_bits")
+        self.activation_bits = _width(activation_bits, "activation_bits")
         if scale_rule not in ("fake", "export"):
             raise ValueError(f"Invalid scale_rule: {scale_rule}")
-        if scale_rule == "fake" and gate_up_proj.dtype not in _FAKE_DTYPES:
+        # the fused chain: W8A8 with SiLU(gate) * up; anything else takes the expert loop
+        self._fused = self.weight_bits == 8 and self.activation_bits == 8 and _is_silu(act_fn)
+        if scale_rule == "export" and not self._fused:
+            raise ValueError("scale_rule='export' is the W8A8 SiLU runtime chain")
+        if gate_up_proj.dtype not in _FAKE_DTYPES and (scale_rule == "fake" or not self._fused):
             raise NotImplementedError("the fake scale rule takes fp16 or bf16 expert weights")
         self.act_fn = act_fn
         self.scale_rule = scale_rule
         _require_gpu(gate_up_proj, "SmoothQuantPackedMoeExperts")
-        q13, s13 = self._quant3d(gate_up_proj, scale_rule)
-        q2, s2 = self._quant3d(down_proj, scale_rule)
+        q13, s13 = self._quant3d(gate_up_proj, scale_rule, self.weight_bits)
+        q2, s2 = self._quant3d(down_proj, scale_rule, self.weight_bits)
         self.register_buffer("gate_up_proj", q13)
         self.register_buffer("gate_up_scale", s13)
         self.register_buffer("down_proj", q2)
@@ -269,9 +328,17 @@ class SmoothQuantPackedMoeExperts(nn.Module):
         self.dtype = gate_up_proj.dtype
 
     @staticmethod
-    def _quant3d(w, rule):
+    def _quant3d(w, rule, bits=8):
+        """Per-row codes and fp32 scales of a packed [E, N, K] weight at ``bits`` (>= 16: the weight
+        itself and no scale)."""
         e, n, k = w.shape
-        q, s32, _ = ops.w8_quantize_per_channel(w.detach().reshape(e * n, k).contiguous(), rule)
+        w2 = w.detach().reshape(e * n, k).contiguous()
+        if bits >= 16:
+            return w2.clone().reshape(e, n, k), None
+        if bits == 8:
+            q, s32, _ = ops.w8_quantize_per_channel(w2, rule)
+        else:
+            q, s32 = ops.fake_quant_rows(w2, bits)
         return q.reshape(e, n, k), s32.reshape(e, n)
 
     @staticmethod
@@ -282,13 +349,48 @@ class SmoothQuantPackedMoeExperts(nn.Module):
 
     def dequantized_weights(self):
         """The fake-quant ``(gate_up_proj, down_proj)`` the reference module holds (``q * s``)."""
+        if self.gate_up_scale is None:
+            return self.gate_up_proj, self.down_proj
         return ((self.gate_up_proj.float() * self.gate_up_scale[..., None]).to(self.dtype),
                 (self.down_proj.float() * self.down_scale[..., None]).to(self.dtype))
+
+    def _codes(self, t2):
+        if self.activation_bits >= 16:
+            return t2, None
+        return _row_codes(t2, self.activation_bits)
+
+    def _forward_expert_loop(self, hidden_states, top_k_index, top_k_weights):
+        """The reference's expert loop (``fake_quant.py:166-191``): for each expert hit, gather its
+        tokens, quantize, gate/up linear, ``act_fn(gate) * up``, quantize, down linear, scale by
+        the routing weight and accumulate into the token rows -- each linear on the dequantising
+        GEMM, the elementwise steps in the activation dtype."""
+        dt = hidden_states.dtype
+        if dt not in _FAKE_DTYPES:
+            raise NotImplementedError("the expert loop runs in fp16 or bf16")
+        out = torch.zeros_like(hidden_states)
+        hits = torch.nn.functional.one_hot(top_k_index, num_classes=self.num_experts).permute(2, 1, 0)
+        experts = torch.greater(hits.sum(dim=(-1, -2)), 0).nonzero()
+        for row in experts.tolist():
+            e = row[0]
+            pos, tok = torch.where(hits[e])
+            qa, sa = self._codes(hidden_states[tok].contiguous())
+            gate_up = ops.dq_linear(qa, sa, self.gate_up_proj[e],
+                                    None if self.gate_up_scale is None else self.gate_up_scale[e], None, dt)
+            gate, up = gate_up.chunk(2, dim=-1)
+            h = self.act_fn(gate) * up
+            qh, sh = self._codes(h.contiguous())
+            y = ops.dq_linear(qh, sh, self.down_proj[e], None if self.down_scale is None else self.down_scale[e],
+                              None, dt)
+            y = y * top_k_weights[tok, pos, None]
+            out.index_add_(0, tok, y.to(out.dtype))
+        return out
 
     @torch.no_grad()
     def forward(self, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
                 top_k_weights: torch.Tensor) -> torch.Tensor:
         _require_gpu(hidden_states, "SmoothQuantPackedMoeExperts")
+        if not self._fused:
+            return self._forward_expert_loop(hidden_states, top_k_index, top_k_weights)
         rule = "fake" if self.scale_rule == "fake" else "runtime"
         return ops.moe_w8a8_forward(hidden_states.contiguous(), top_k_index, top_k_weights, self.gate_up_proj,
                                     self.gate_up_scale, self.down_proj, self.down_scale,

@@ -68,13 +68,15 @@ class RealQuantLinearArtifact:
 def pseudo_quantize_tensor(w, n_bit=8, zero_point=True, q_group_size=-1, inplace=False, get_scale_zp=False):
     """AWQ pseudo-quantization on the GPU, same signature and results as the reference.
 
-    Only ``n_bit=4`` is a kernel of this build; fp16 and bf16 weights are quantized in their
-    own arithmetic.  Returns the dequantized weight (bit-identical to the reference's), plus
-    ``scales``/``zeros`` ``[N, K/g]`` when ``get_scale_zp`` (zero_point only, as in the
-    reference).
+    Code widths ``n_bit`` 1..8 (2..8 without a zero point); fp16 and bf16 weights are quantized
+    in their own arithmetic.  Returns the dequantized weight (bit-identical to the reference's),
+    plus ``scales``/``zeros`` ``[N, K/g]`` when ``get_scale_zp`` (zero_point only, as in the
+    reference).  ``n_bit=4`` runs the quantizer that also packs the codes for the W4A16 GEMMs.
     """
-    if n_bit != 4:
-        raise NotImplementedError("mindpipe_amd implements the 4-bit AWQ quantizer")
+    n_bit = int(n_bit)
+    if not (1 <= n_bit <= 8) or (n_bit == 1 and not zero_point):
+        raise NotImplementedError(f"n_bit={n_bit}: this build's AWQ quantizer takes 1..8-bit codes "
+                                  "(2..8 without a zero point)")
     if get_scale_zp and not zero_point:
         raise ValueError("get_scale_zp needs zero_point=True (the reference's symmetric branch has no zeros)")
     src = _gpu(w.detach())
@@ -82,7 +84,10 @@ def pseudo_quantize_tensor(w, n_bit=8, zero_point=True, q_group_size=-1, inplace
     w2 = src.reshape(-1, shape[-1]).contiguous()
     if w2.dtype not in (torch.float16, torch.bfloat16):
         raise NotImplementedError("the AWQ quantizer takes fp16 or bf16 weights (the reference's arithmetic)")
-    packed, s, z, deq = ops.w4_quantize_awq(w2, q_group_size, zero_point, return_deq=True)
+    if n_bit == 4:
+        _, s, z, deq = ops.w4_quantize_awq(w2, q_group_size, zero_point, return_deq=True)
+    else:
+        s, z, deq = ops.awq_pseudo_quantize(w2, n_bit, q_group_size, zero_point)
     deq = deq.reshape(shape).to(w.device)
     if inplace:
         w.data.copy_(deq)

@@ -22,9 +22,14 @@ def test_smoothquant_linear_rejects_bad_args():
     with pytest.raises(ValueError):
         SQ.SmoothQuantLinear(8, 8, act_quant="per_tensor")
     with pytest.raises(NotImplementedError):
-        SQ.SmoothQuantLinear(8, 8, weight_bits=4)
+        SQ.SmoothQuantLinear(8, 8, weight_bits=12)  # codes wider than int8
+    with pytest.raises(NotImplementedError):
+        SQ.SmoothQuantLinear(8, 8, activation_bits=1)
     with pytest.raises(ValueError):
         SQ.SmoothQuantLinear(8, 8, scale_rule="other")
+    with pytest.raises(ValueError):
+        SQ.SmoothQuantLinear(8, 8, weight_bits=4, scale_rule="export")
+    assert "weight_bits=4, activation_bits=16" in repr(SQ.SmoothQuantLinear(8, 8, weight_bits=4, activation_bits=16))
 
 
 def test_module_forward_refuses_cpu_tensors():
@@ -54,7 +59,9 @@ def test_w4_module_buffers_and_shapes():
     assert mod.weight_shape.tolist() == [64, 256]
     with pytest.raises(ValueError):
         W4.W4A16Linear(100, 8, group_size=128)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(NotImplementedError):  # codes wider than 8 bits
+        W4.pseudo_quantize_tensor(torch.zeros(4, 128, dtype=torch.float16), n_bit=9)
+    with pytest.raises(RuntimeError, match="GPU"):  # other widths run on the GPU too
         W4.pseudo_quantize_tensor(torch.zeros(4, 128, dtype=torch.float16), n_bit=8)
 
 

@@ -404,3 +404,34 @@ def test_dense_mlp_single_chunk_equals_one_expert_moe():
                                          O.bf16_bits_to_f32(O.f32_to_bf16_bits(s2)), chunks=1, out_dtype="fp32"))
     y2 = O.dense_mlp_runtime(x, qw13, s13, qw2, s2, chunks=2, out_dtype="fp32")
     assert y2.tobytes() == (np.float32(0) + parts[0] + parts[1]).astype(np.float32).tobytes()
+
+
+WID = np.load(Path(__file__).parent / "golden" / "reference_width_vectors.npz")
+
+
+@pytest.mark.parametrize("tag,dt", [("f16", "fp16"), ("bf16", "bf16")])
+def test_quantizers_match_reference_at_other_widths(tag, dt):
+    """AWQ at 2, 3 and 8 bits (zero point and symmetric, group 128 and per row) and the
+    per-token / per-channel fake quantizers at 3, 4 and 6 bits, against the reference's own
+    outputs (``make_width_vectors.py``): bit-exact in fp16 and bf16."""
+    cv = _cv(dt)
+    w = cv(WID[f"awq_{tag}_w"])
+    checked = 0
+    for n_bit in (2, 3, 8):
+        for zp in (True, False):
+            for g in (128, -1):
+                key = f"awq_{tag}_n{n_bit}_zp{int(zp)}_g{g}"
+                if key + "_deq" not in WID.files:
+                    continue
+                d, s, z, _ = O.pseudo_quantize_tensor(w, n_bit, zp, g, dt)
+                assert np.array_equal(_u16(d), _u16(WID[key + "_deq"])), key
+                if zp:
+                    assert np.array_equal(_u16(s), _u16(WID[key + "_s"])), key
+                    assert np.array_equal(_u16(z), _u16(WID[key + "_z"])), key
+                checked += 1
+    assert checked == 8
+    for n in (3, 4, 6):
+        _, _, fx = O.quantize_activation_per_token_fake(cv(WID[f"fq_{tag}_x"]), n, dt)
+        assert np.array_equal(_u16(fx), _u16(WID[f"fq_{tag}_x_n{n}"])), n
+        _, _, fw = O.quantize_weight_per_channel_fake(cv(WID[f"fq_{tag}_w"]), n, dt)
+        assert np.array_equal(_u16(fw), _u16(WID[f"fq_{tag}_w_n{n}"])), n
