@@ -671,6 +671,94 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const uint16_t *__res
   if (lane == 0) idx[blockIdx.x] = bi;
 }
 
+// Split form for long rows (the LM head's vocabulary): a workgroup per 4096-value span of a row
+// finds the span's best (value, index) and merges it into idx[row] by a 64-bit atomic max of a key
+// that orders like am_better: the value's bits mapped to an unsigned order in the high word (NaN
+// above everything, -0 as +0), the complement of the index in the low word (equal values: the
+// smaller index wins).  idx[row] is cleared first and decoded after (three launches, no workspace).
+__device__ __forceinline__ unsigned long long am_key(float v, int i) {
+  uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+  u = (v != v) ? 0xFFFFFFFFu : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+  return (static_cast<unsigned long long>(u) << 32) | static_cast<uint32_t>(0xFFFFFFFFu - static_cast<uint32_t>(i));
+}
+
+__global__ void argmax_clear_kernel(int64_t *__restrict__ idx, int64_t rows) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r < rows) idx[r] = 0;
+}
+
+constexpr int kArgmaxSpan = 4096;
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void argmax_span_kernel(const uint16_t *__restrict__ x, int n,
+                                                          int64_t *__restrict__ idx) {
+  __shared__ unsigned long long sk[4];
+  const uint16_t *row = x + static_cast<int64_t>(blockIdx.y) * n;
+  const int lo = blockIdx.x * kArgmaxSpan;
+  const int hi = lo + kArgmaxSpan < n ? lo + kArgmaxSpan : n;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  unsigned long long best = 0;
+  if (VEC) {
+    // 16 values per thread: two 16-byte chunks, both loaded before any comparison
+    constexpr int C = kArgmaxSpan / 8 / 256;
+    const uint4 *r4 = reinterpret_cast<const uint4 *>(row);
+    uint4 c[C];
+#pragma unroll
+    for (int u = 0; u < C; ++u) {
+      const int j = lo / 8 + threadIdx.x + u * 256;
+      c[u] = 8 * j < hi ? r4[j] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < C; ++u) {
+      const int j = lo / 8 + threadIdx.x + u * 256;
+      if (8 * j >= hi) break;
+      const uint32_t w[4] = {c[u].x, c[u].y, c[u].z, c[u].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const unsigned long long k =
+            am_key(mp_h2f(static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu))), 8 * j + e);
+        best = k > best ? k : best;
+      }
+    }
+  } else {
+    constexpr int C = kArgmaxSpan / 256;
+    uint16_t c[C];
+#pragma unroll
+    for (int u = 0; u < C; ++u) {
+      const int j = lo + threadIdx.x + u * 256;
+      c[u] = j < hi ? row[j] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < C; ++u) {
+      const int j = lo + threadIdx.x + u * 256;
+      if (j >= hi) break;
+      const unsigned long long k = am_key(mp_h2f(c[u]), j);
+      best = k > best ? k : best;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long k = __shfl_xor(best, o, 64);
+    best = k > best ? k : best;
+  }
+  if (lane == 0) sk[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = sk[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) k = sk[w] > k ? sk[w] : k;
+    atomicMax(reinterpret_cast<unsigned long long *>(idx + blockIdx.y), k);
+  }
+}
+
+__global__ void argmax_decode_kernel(int64_t *__restrict__ idx, int64_t rows) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r < rows) {
+    const unsigned long long k = static_cast<unsigned long long>(idx[r]);
+    idx[r] = static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(k & 0xFFFFFFFFull));
+  }
+}
+
 // ---------------------------------------------------------------- SiLU * up
 // gu [B, 2I] (gate | up) -> act [B, I] = round(round(silu(gate)) * up).
 template <bool BF>
@@ -870,6 +958,21 @@ extern "C" int mp_argmax_rows(const void *x, int64_t rows, int64_t n, int64_t *i
   if (rows < 0 || rows > UINT32_MAX || n <= 0 || n > INT32_MAX - 1024) return MP_ERR_SHAPE;
   if (rows == 0) return MP_OK;
   const bool vec = n % 8 == 0 && mp_aligned(x, 16);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t spans = mp_cdiv(n, kArgmaxSpan);
+  if (spans >= 4 && rows <= 65535) {
+    // long rows: spans of one row on many CUs (a single workgroup per row is bound by one CU's
+    // outstanding loads)
+    const dim3 g1(static_cast<unsigned>(mp_cdiv(rows, 256)));
+    hipLaunchKernelGGL(argmax_clear_kernel, g1, dim3(256), 0, s, idx, rows);
+    const dim3 g2(static_cast<unsigned>(spans), static_cast<unsigned>(rows));
+    const auto *xp = static_cast<const uint16_t *>(x);
+    if (vec) hipLaunchKernelGGL(argmax_span_kernel<true>, g2, dim3(256), 0, s, xp, static_cast<int>(n), idx);
+    else hipLaunchKernelGGL(argmax_span_kernel<false>, g2, dim3(256), 0, s, xp, static_cast<int>(n), idx);
+    hipLaunchKernelGGL(argmax_decode_kernel, g1, dim3(256), 0, s, idx, rows);
+    MP_CHECK_LAUNCH();
+    return MP_OK;
+  }
   if (vec)
     hipLaunchKernelGGL(argmax_rows_kernel<true>, dim3(static_cast<unsigned>(rows)), dim3(1024), 0,
                        reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t *>(x), static_cast<int>(n),

@@ -1972,8 +1972,9 @@ extern "C" int mp_w4a16_gemv_rmsnorm(const void *x, const void *residual, const 
 }
 
 // Launch of the batched kernel's SwiGLU form (fp16, or BF: bf16): NT/2 gate tiles paired with NT/2 up
-// tiles per wave.  The caller has checked 1 <= m <= 64, K % 256 == 0, group 128, an even group count,
-// the alignments and the 32-bit buffer sizes.
+// tiles per wave.  The caller has checked 1 <= m <= 512 (mp_batch_takes; above 64 rows it calls this
+// once per 32-row part), K % 256 == 0, group 128, an even group count, the alignments and the 32-bit
+// buffer sizes.
 template <bool BF>
 static void mp_launch_w4_batch_swiglu(hipStream_t s, const uint16_t *xp, int64_t m, int64_t k, const uint32_t *wp,
                                       int64_t n2, const uint16_t *sp, const uint16_t *zp, int n_groups,

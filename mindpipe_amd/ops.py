@@ -787,6 +787,11 @@ def prefill_rope_split(qkv: torch.Tensor, batch: int, nh: int, kvh: int, cos_t: 
     _need(qkv, "qkv", torch.float16, 2)
     _need(cos_t, "cos_t", torch.float16, 2)
     _need(sin_t, "sin_t", torch.float16, 2)
+    if batch < 1:
+        raise RuntimeError(f"batch must be >= 1, got {batch}")
+    for name, c in (("cos_t", cos_t), ("sin_t", sin_t), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if c.device != qkv.device:
+            raise RuntimeError(f"{name} is on {c.device}, qkv on {qkv.device}")
     if qkv.shape[0] % batch != 0 or qkv.shape[1] != (nh + 2 * kvh) * 128:
         raise RuntimeError(f"qkv must be [B*T, {(nh + 2 * kvh) * 128}], got {tuple(qkv.shape)}")
     t = qkv.shape[0] // batch

@@ -306,9 +306,12 @@ def test_decoder_one_row_step_fused_norm():
     assert _rel(lf.float(), lt.float()) <= 2e-2
 
 
-@pytest.mark.parametrize("rows,n", [(1, 32000), (8, 128256), (3, 1), (5, 1500)])
+@pytest.mark.parametrize("rows,n", [(1, 32000), (8, 128256), (3, 1), (5, 1500), (4, 20001), (2, 16384),
+                                    (6, 16383)])
 def test_argmax_rows_matches_torch(rows, n):
-    """Row argmax equals torch.argmax, including ties (first index), all -inf rows and NaN."""
+    """Row argmax equals torch.argmax, including ties (first index; across the 4096-value spans of
+    the split form), all -inf rows, NaN, and +0 / -0 ties.  Rows of 16384+ values take the split
+    form (16-byte loads when n % 8 == 0, scalar loads otherwise); shorter rows one workgroup each."""
     _say("argmax_rows", rows, n)
     from mindpipe_amd import ops
     g = torch.Generator(device=DEV).manual_seed(rows * 7 + n)
@@ -319,6 +322,10 @@ def test_argmax_rows_matches_torch(rows, n):
     if rows > 2:
         x[1] = float("-inf")                     # all equal: index 0
         x[2, n // 2] = float("nan")              # NaN counts as the maximum
+    if rows > 3:
+        x[2, n - 1] = float("nan")               # a later NaN loses to the first
+        x[3] = 0.0
+        x[3, : n // 2] = -0.0                    # -0 and +0 are equal: index 0
     assert torch.equal(ops.argmax_rows(x), torch.argmax(x, dim=-1))
 
 

@@ -118,7 +118,8 @@ W4_CASES = [(1, 4096, 4096), (16, 4096, 4096), (3, 512, 1024), (17, 256, 2048), 
             (1, 2048, 2048), (1, 1000, 4096), (1, 24, 2048), (1, 4097, 4096), (1, 8, 2048),
             # 2..8 rows (four-row MFMA kernel): half-filled last K chunk, N not a multiple of 16, split-K waves
             (2, 4096, 4096), (4, 1000, 2304), (5, 4096, 11008), (8, 12288, 4096), (7, 300, 1280), (6, 72, 512),
-            # 33..64 rows as two 32-row halves of one grid: padding workgroups, 4 / 2 / 1 column tiles
+            # 33..64 rows: one 64-row tile where N <= 8192 (fp16), else two 32-row parts of one grid
+            # (padding workgroups, 4 / 2 / 1 column tiles)
             (48, 12288, 4096), (64, 8192, 2048), (37, 1000, 1024), (57, 4096, 1280),
             # 65..512 rows where the prefill grid would fill at most half the CUs: batched kernel in 32-row
             # parts (up to 12), ragged last part

@@ -70,7 +70,21 @@ def test_noalloc_gmm1_matches_workspace_entry(rule, act):
 def test_noalloc_gmm1_refuses_oversized_shape():
     from mindpipe_amd import _lib
     lib = _lib.load()
-    # 4096 rows x 8192 intermediate columns of fp32 rows: 128 MiB > 64 MiB; refused on the host
-    rc = lib.mp_i8_gemm_swiglu_requant_noalloc(1, 1, 1, 1, 1, 8, 4096, 128, 8192, 0, 0, 1, 1, None)
+    # 4096 rows x 8192 intermediate columns of fp32 rows: 128 MiB > 64 MiB; refused on the host before
+    # any launch.  Every operand is a real buffer of its full size, so only the scratch is too small.
+    t, h, inter, e = 4096, 128, 8192, 8
+    dev = "cuda:0"
+    routed = torch.zeros((t, h), dtype=torch.int8, device=dev)
+    rscale = torch.ones((t,), dtype=torch.float32, device=dev)
+    w13 = torch.zeros((e, 2 * inter, h), dtype=torch.int8, device=dev)
+    s13 = torch.ones((e, 2 * inter), dtype=torch.float32, device=dev)
+    offsets = torch.arange(0, t + 1, t // e, dtype=torch.int64, device=dev)
+    q = torch.empty((t, inter), dtype=torch.int8, device=dev)
+    s = torch.empty((t,), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    rc = lib.mp_i8_gemm_swiglu_requant_noalloc(routed.data_ptr(), rscale.data_ptr(), w13.data_ptr(), s13.data_ptr(),
+                                               offsets.data_ptr(), e, t, h, inter, 0, 0, q.data_ptr(), s.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
     assert rc == 6   # MP_ERR_WORKSPACE
     assert lib.mp_moe_gmm1_workspace_bytes(4096, 8192) > (64 << 20)
