@@ -19,10 +19,11 @@ stated in each ``sample``).
 ``--profile NAME`` runs one kernel mix for rocprofv3 (the commands in ``profiles/``):
 ``w4gemv`` (the headline loop), ``readfloor`` (one-launch reads of 8.9 MB, rotated), ``readsweep``
 (read probes of several launch shapes at 8.9 MB and 1 GiB), ``w8sweep`` (the W8A8 sweep's GEMMs),
-``moe`` (the Mixtral MoE chain), ``prefill`` (the 7B prefill linears at M = 2048),
+``moe`` (the Mixtral MoE chain), ``moesmall`` (the same chain at an expert FFN of 1792), ``prefill`` (the 7B prefill linears at M = 2048),
 ``w4shapes`` (M=16 and the 70B GEMV shapes), ``w4bf16`` (the bf16 W4A16 legs), ``w4batch8`` (7B
 gate/up and down at M = 1 and 8), ``dec7b`` (the 7B decode step), ``dec70b`` (four layers of the 70B
 decode step), ``w8big`` (the M=4096 int8 GEMM), and
+``curead`` (per-CU read rates from L2 and from HBM, into registers or LDS), and
 ``--traffic-probe`` the kernel mix of ``profiles/traffic.json``.
 """
 from __future__ import annotations
@@ -365,6 +366,29 @@ def profile_mix(ops, name, steps):
             ms = _time_graph(lambda i: probe_read_tiles(bufs[i], n, kb, tr, sb, d, tsinks[i]), 13, steps, 3) / 13
             print(f"tileread tile_rows={tr} step_bytes={sb} depth={d}: {ms * 1e3:.2f} us, "
                   f"{n * kb / (ms * 1e-3) / 1e12:.2f} TB/s", flush=True)
+    elif name == "curead":
+        # per-CU read rate: every workgroup re-reads a 1 MB region shared by its XCD (L2 hits after
+        # the first pass; 32 passes), or one workgroup per distinct 4 MB / 2 MB region of 1 GiB (HBM),
+        # into registers or straight into LDS, at several launch shapes
+        from mindpipe_amd.measure import probe_cu_read
+        buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+        for mode in ("l2", "hbm"):
+            for grid in (256, 512):
+                for threads, loads in ((256, 4), (256, 8), (512, 4), (512, 8)):
+                    for dma in (False, True):
+                        if dma and threads * loads * 32 > 65536:
+                            continue
+                        if mode == "l2":
+                            region, nreg, passes = 1 << 20, 8, 32
+                        else:
+                            region, nreg, passes = (1 << 30) // grid, grid, 1
+                        sink = probe_cu_read(buf, region, nreg, passes, grid, threads, loads, dma)
+                        ms = _time_graph(lambda i: probe_cu_read(buf, region, nreg, passes, grid, threads, loads, dma,
+                                                                 sink), 1, steps, 2)
+                        total = region * passes * grid
+                        print(f"curead {mode} grid={grid} threads={threads} loads={loads} dma={int(dma)}: "
+                              f"{ms * 1e3:.1f} us, {total / (ms * 1e-3) / 1e12:.2f} TB/s, "
+                              f"{total / (ms * 1e-3) / 1e9 / 256:.1f} GB/s per CU", flush=True)
     elif name == "w8sweep":
         # the W8A8 sweep legs' GEMMs (M = 1, 16, 256, 4096; N = 11008, K = 4096) on random int8 data,
         # M <= 256 over 13 rotated weight copies as in the bench
@@ -383,6 +407,12 @@ def profile_mix(ops, name, steps):
         # bench leg's inputs
         ms = _moe_chain_ms(ops, steps)
         print(f"moe chain: {ms * 1e3:.1f} us per call", flush=True)
+    elif name == "moesmall":
+        # the same chain with an expert FFN of 1792 (8x smaller): its 176 MB of expert weights stay in
+        # the Infinity Cache across calls, so the GEMMs' rate per byte shows whether HBM sets it
+        x, ids, tw, q13, s13, q2, s2 = _moe_inputs(ops, inter=1792)
+        ms = _time_graph(lambda i: ops.moe_w8a8_forward(x, ids, tw, q13, s13, q2, s2), 1, steps, 3)
+        print(f"moe chain (I = 1792): {ms * 1e3:.1f} us per call", flush=True)
     elif name == "prefill":
         # the 7B prefill linears at M = 2048 (fp16): q/k/v (N = 12288), o (4096), fused gate/up with
         # SiLU-mul (2 x 11008), down (K = 11008)

@@ -27,6 +27,19 @@ static inline bool mp_aligned(const void *p, size_t a) {
 
 static inline int64_t mp_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Compute units of the current device (cached per device id).
+static inline int mp_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
 // Measurement knobs: the environment variables that steer a kernel choice (MP_W4_*, MP_W8_*) are
 // read only by a library compiled with -DMP_MEASUREMENT_KNOBS (python -m mindpipe_amd.build
 // --knobs).  The default build ignores the environment, so every call takes the tested default.

@@ -1750,19 +1750,6 @@ static int mp_big_variant() {
   return v;
 }
 
-// Compute units of the current device (cached per device id).
-static int mp_cu_count() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cache[dev] = v;
-  }
-  return cache[dev];
-}
-
 // LDS-staged 16-byte-store epilogue (MP_W8_STAGED=0 turns it off, for measurements).
 static int mp_staged_epilogue() {
   static int v = [] {

@@ -27,6 +27,9 @@ def _load() -> C.CDLL:
         lib.mp_probe_read_tiles.restype = C.c_int
         lib.mp_probe_read_tiles.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                             C.c_void_p]
+        lib.mp_probe_cu_read.restype = C.c_int
+        lib.mp_probe_cu_read.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                         C.c_void_p, C.c_void_p]
         _LIB = lib
     return _LIB
 
@@ -61,4 +64,22 @@ def probe_read_tiles(buf: torch.Tensor, rows: int, row_bytes: int, tile_rows: in
                                  torch.cuda.current_stream(buf.device).cuda_stream)
     if rc != 0:
         raise RuntimeError(f"mp_probe_read_tiles failed with status {rc}")
+    return sink
+
+
+def probe_cu_read(buf: torch.Tensor, region_bytes: int, nreg: int, passes: int, grid: int, threads: int = 256,
+                  loads: int = 8, dma: bool = False, sink: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One launch of ``grid`` workgroups, workgroup w reading region ``w % nreg`` of ``buf``
+    (``nreg`` regions of ``region_bytes``) ``passes`` times: the per-CU read rate from L2
+    (``nreg`` = 8, one small region per XCD) or from HBM (large distinct regions).  ``dma``: the
+    loads go straight to LDS.  Returns the sink the launch may write."""
+    lib = _load()
+    if buf.numel() * buf.element_size() < region_bytes * nreg:
+        raise ValueError("buf is smaller than nreg regions")
+    if sink is None:
+        sink = torch.zeros(grid, dtype=torch.int32, device=buf.device)
+    rc = lib.mp_probe_cu_read(buf.data_ptr(), region_bytes, nreg, passes, threads, loads, 1 if dma else 0, grid,
+                              sink.data_ptr(), torch.cuda.current_stream(buf.device).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"mp_probe_cu_read failed with status {rc}")
     return sink

@@ -89,7 +89,97 @@ __global__ __launch_bounds__(256) void probe_tiles_kernel(const uint4 *__restric
   if (x == 0x9E3779B9u) sink[blockIdx.x] = x;
 }
 
+// Per-CU read rate: every workgroup reads the region (blockIdx.x % nreg) of region16 16-byte pieces
+// `passes` times, LOADS 16-byte loads per lane per step, two steps in flight.  With nreg = 8 and a
+// grid that is a multiple of 8, the workgroups of one XCD share one region, which stays in that
+// XCD's L2 after the first pass; large distinct regions come from HBM.  DMA: the loads go straight
+// to LDS (buffer_load ... lds) instead of registers.
+template <int THREADS, int LOADS, bool DMA>
+__global__ __launch_bounds__(THREADS) void probe_cu_read_kernel(const uint4 *__restrict__ p, int64_t region16,
+                                                               int nreg, int passes, uint32_t *__restrict__ sink) {
+  constexpr int64_t kStep = static_cast<int64_t>(THREADS) * LOADS;
+  __shared__ uint4 lds[DMA ? 2 * kStep : 1];
+  const uint4 *base = p + static_cast<int64_t>(blockIdx.x % nreg) * region16;
+  const uint32_t rbytes = static_cast<uint32_t>(region16 * 16);
+  const auto rs = mp_rsrc(base, rbytes);
+  const int wave = threadIdx.x >> 6;
+  const int64_t steps = region16 / kStep;  // host: region16 a multiple of kStep, >= 2 steps
+  uint32_t x = 0;
+  uint4 v[2][LOADS];
+  auto issue = [&](int64_t st, int slot) {
+    const uint32_t off0 = static_cast<uint32_t>((st * kStep + threadIdx.x) * 16);
+#pragma unroll
+    for (int l = 0; l < LOADS; ++l) {
+      const uint32_t off = off0 + static_cast<uint32_t>(l * THREADS * 16);
+      if constexpr (DMA)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, reinterpret_cast<__attribute__((address_space(3))) void *>(
+                    reinterpret_cast<uintptr_t>(&lds[slot * kStep + l * THREADS + wave * 64])),
+            16, off, 0, 0, 0);
+      else
+        v[slot][l] = mp_buf_load16(rs, off, 0);
+    }
+  };
+  for (int ps = 0; ps < passes; ++ps) {
+    issue(0, 0);
+    for (int64_t st = 0; st < steps; st += 2) {
+      issue(st + 1 < steps ? st + 1 : st, 1);
+      if constexpr (DMA) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS) : "memory");
+      } else {
+#pragma unroll
+        for (int l = 0; l < LOADS; ++l) x ^= v[0][l].x ^ v[0][l].w;
+      }
+      issue(st + 2 < steps ? st + 2 : st, 0);
+      if constexpr (DMA) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS) : "memory");
+      } else {
+#pragma unroll
+        for (int l = 0; l < LOADS; ++l) x ^= v[1][l].x ^ v[1][l].w;
+      }
+    }
+    if constexpr (DMA) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+#pragma unroll
+      for (int l = 0; l < LOADS; ++l) x ^= v[0][l].x ^ v[0][l].w;
+    }
+  }
+  if constexpr (DMA) {
+    __syncthreads();
+    x = lds[threadIdx.x].x;
+  }
+  if (x == 0x9E3779B9u) sink[blockIdx.x] = x;
+}
+
 }  // namespace
+
+// Per-CU read rate (probe_cu_read_kernel): `grid` workgroups of `threads` (256 / 512), `loads` (4 / 8)
+// 16-byte loads per lane per step, each reading the region (w % nreg) of `region_bytes` bytes
+// `passes` times; dma: loads straight into LDS.  buf holds nreg regions; region_bytes a multiple of
+// 2 * threads * loads * 16 and below 4 GiB; sink: uint32 [grid].
+extern "C" int mp_probe_cu_read(const void *buf, int64_t region_bytes, int nreg, int passes, int threads, int loads,
+                                int dma, int grid, uint32_t *sink, mp_stream_t stream) {
+  if (!buf || !sink || nreg <= 0 || passes <= 0 || grid <= 0) return MP_ERR_ARG;
+  if (!mp_aligned(buf, 16)) return MP_ERR_ALIGN;
+  const int64_t step = static_cast<int64_t>(threads) * loads * 16;
+  if (region_bytes <= 0 || region_bytes % (2 * step) || region_bytes >= (int64_t(1) << 32)) return MP_ERR_SHAPE;
+  if (dma && 2 * step > 64 * 1024) return MP_ERR_SHAPE;  // the two LDS steps fit 64 KB
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const auto *pp = static_cast<const uint4 *>(buf);
+  const int64_t r16 = region_bytes / 16;
+#define MP_PC(T_, L_, D_) hipLaunchKernelGGL((probe_cu_read_kernel<T_, L_, D_>), dim3(static_cast<unsigned>(grid)), dim3(T_), 0, s, pp, r16, nreg, passes, sink)
+#define MP_PC_D(T_, L_) do { if (dma) MP_PC(T_, L_, true); else MP_PC(T_, L_, false); } while (0)
+  if (threads == 256 && loads == 4) MP_PC_D(256, 4);
+  else if (threads == 256 && loads == 8) MP_PC_D(256, 8);
+  else if (threads == 512 && loads == 4) MP_PC_D(512, 4);
+  else if (threads == 512 && loads == 8) MP_PC_D(512, 8);
+  else return MP_ERR_ARG;
+#undef MP_PC_D
+#undef MP_PC
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
 
 // Tile-order read of a row-major [rows, row_bytes] matrix (row_bytes a multiple of step_bytes,
 // tile_rows * step_bytes / 16 a multiple of 256 and at most 4096): one workgroup per tile_rows

@@ -258,3 +258,45 @@ def test_w4a16_one_row_gemv_edges(n, k, zp, with_bias):
     # every output row, against the same kernel run twice (no state left between launches)
     y2 = ops.w4a16_gemm(x, packed, s, z, 128, bias)
     assert torch.equal(y, y2)
+
+
+# Edges of the one-row VALU GEMV at 34 MB layers (its 8-row, two-wave form from N = 16384): row groups
+# that do not divide N (the last group clamps its rows), a partial last K chunk (K = 11008: 5.375
+# chunks of 2048; K = 30720: 15 chunks), long K (16384), no zero points, a bias, and the SwiGLU form
+# with an odd intermediate width.
+GEMV_LARGE_EDGES = [(8200, 8192, True, True), (6104, 11008, True, False), (16400, 4096, False, True),
+                (2200, 30720, True, True), (4100, 16384, False, False)]
+
+
+@pytest.mark.parametrize("n,k,zp,bias", GEMV_LARGE_EDGES)
+def test_w4a16_gemv_large_edges(n, k, zp, bias):
+    _say("w4a16 gemv large edges", n, k, zp, bias)
+    ops = _ops()
+    packed, s, z = _quant_gpu(n, k, seed=n + k, zp=zp)
+    x = _x(1, k, seed=13)
+    b = (torch.randn(n, generator=torch.Generator(device=DEV).manual_seed(4), device=DEV) * 0.1).half() \
+        if bias else None
+    y = ops.w4a16_gemm(x, packed, s, z, 128, b)
+    y2 = ops.w4a16_gemm(x, packed, s, z, 128, b)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)  # fixed summation order: the same bits on every call
+    cols = _cols(n, seed=n, count=96)
+    assert _rel(_np(y)[:, cols], _ref_cols(x, packed, s, z, cols, k, b)) <= 1e-3
+
+
+@pytest.mark.parametrize("i,k,bias", [(8197, 4096, True), (4100, 8192, False)])
+def test_w4a16_gemv_large_swiglu_edges(i, k, bias):
+    _say("w4a16 gemv large swiglu edges", i, k, bias)
+    ops = _ops()
+    packed, s, z = _quant_gpu(2 * i, k, seed=i + k, zp=True)
+    x = _x(1, k, seed=17)
+    b = (torch.randn(2 * i, generator=torch.Generator(device=DEV).manual_seed(5), device=DEV) * 0.1).half() \
+        if bias else None
+    act = ops.w4a16_gemm_swiglu(x, packed, s, z, 128, b)
+    torch.cuda.synchronize()
+    cols = _cols(i, seed=i, count=96)
+    g = _ref_cols(x, packed, s, z, cols, k, b).astype(np.float32)
+    u = _ref_cols(x, packed, s, z, cols + i, k, b).astype(np.float32)
+    sg = (g / (1.0 + np.exp(-g))).astype(np.float16).astype(np.float32)
+    ref = (sg * u).astype(np.float16)
+    assert _rel(_np(act)[:, cols], ref) <= 1e-3

@@ -429,6 +429,8 @@ W8_CASES = [(1, 11008, 4096), (16, 11008, 4096), (5, 1000, 256), (17, 512, 1024)
             (1024, 640, 768), (1300, 700, 384),
             # large-M kernel with odd N: the unpaired store path
             (1024, 333, 256),
+            # large-M kernel: twenty loop trips, partial row and column tiles
+            (1100, 600, 2560),
             # row-contiguous GEMV (M <= 2): K past the last 1 KB chunk, M = 2, tiny K, K = 11008
             (2, 300, 1040), (1, 257, 4112), (2, 64, 16), (1, 100, 11008),
             # skinny kernel where the whole K fits the 76 KB LDS budget but not the staging
@@ -478,6 +480,28 @@ def test_w8a8_gemm_large_rows_subset():
     rows = np.concatenate([rows, [0, 127, 128, m - 1]])
     ref = O.w8a8_linear_runtime(_np(qx)[rows], _np(sx)[rows], _np(qw), _np(sw))
     assert np.array_equal(_np(y)[rows].view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("out", ["fp16", "bf16"])
+def test_w8a8_gemm_persistent_partial_tiles(out):
+    """M = 4100, N = 5000, K = 512: 17 x 20 tiles of 256 x 256 over a persistent grid (more tiles than
+    CUs), with a partial last row tile (4 rows) and column tile (136 columns); bit-exact on sampled
+    rows (those of the partial tile included) x all columns."""
+    _say("w8a8 persistent partial tiles", out)
+    m, n, k = 4100, 5000, 512
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    qx = torch.randint(-127, 128, (m, k), generator=gen, device=DEV, dtype=torch.int8)
+    qw = torch.randint(-127, 128, (n, k), generator=gen, device=DEV, dtype=torch.int8)
+    sx = torch.rand(m, generator=gen, device=DEV) * 0.01
+    sw = torch.rand(n, generator=gen, device=DEV) * 0.001
+    bias = (torch.randn(n, generator=gen, device=DEV) * 0.1).half()
+    odt = torch.float16 if out == "fp16" else torch.bfloat16
+    y = _ops().w8a8_gemm(qx, sx, qw, sw, bias, odt)
+    rows = np.random.default_rng(1).choice(m, 64, replace=False)
+    rows = np.unique(np.concatenate([rows, [0, 255, 256, 4095, 4096, 4097, 4098, 4099]]))
+    ref = O.w8a8_linear_runtime(_np(qx)[rows], _np(sx)[rows], _np(qw), _np(sw), _np(bias), out_dtype=out)
+    got = _np(y.view(torch.int16)).view(np.uint16) if out == "bf16" else _np(y).view(np.uint16)
+    assert np.array_equal(got[rows], ref.view(np.uint16))
 
 
 def test_w8a8_end_to_end_vs_fake_reference():
