@@ -18,13 +18,14 @@ stated in each ``sample``).
 
 ``--profile NAME`` runs one kernel mix for rocprofv3 (the commands in ``profiles/``):
 ``w4gemv`` (the headline loop), ``readfloor`` (one-launch reads of 8.9 MB, rotated), ``readsweep``
-(read probes of several launch shapes at 8.9 MB and 1 GiB), ``w8sweep`` (the W8A8 sweep's GEMMs),
-``moe`` (the Mixtral MoE chain), ``moesmall`` (the same chain at an expert FFN of 1792), ``prefill`` (the 7B prefill linears at M = 2048),
-``w4shapes`` (M=16 and the 70B GEMV shapes), ``w4bf16`` (the bf16 W4A16 legs), ``w4batch8`` (7B
-gate/up and down at M = 1 and 8), ``dec7b`` (the 7B decode step), ``dec70b`` (four layers of the 70B
-decode step), ``w8big`` (the M=4096 int8 GEMM), and
-``curead`` (per-CU read rates from L2 and from HBM, into registers or LDS), and
-``--traffic-probe`` the kernel mix of ``profiles/traffic.json``.
+(read probes of several launch shapes at 8.9 MB and 1 GiB), ``curead`` (per-CU read rates from L2 and
+from HBM, into registers or LDS), ``w8sweep`` (the W8A8 sweep's GEMMs), ``moe`` (the Mixtral MoE
+chain), ``moesmall`` (the same chain at an expert FFN of 1792), ``prefill`` (the 7B prefill linears at
+M = 2048), ``w4shapes`` (M=16 and the 70B GEMV shapes), ``w4bf16`` (the bf16 W4A16 legs),
+``w4batch8`` (7B gate/up and down at M = 1 and 8), ``dec7b`` (the 7B decode step), ``dec70b`` (four
+layers of the 70B decode step), ``decsteps`` (two full-depth steps of every decode leg, for their
+traffic) and ``w8big`` (the M=4096 int8 GEMM); ``--traffic-probe`` runs the kernel mix of
+``profiles/traffic.json``.
 """
 from __future__ import annotations
 
@@ -274,7 +275,8 @@ def leg_decoder(cfg_name, batches, prompt, gen_tokens, prefill_batch=1):
         alg_bytes = wbytes + kv_bytes
         out["decode"][str(b)] = {"ms_per_step": ms, "tok_s": b / (ms * 1e-3), "weight_bytes": wbytes,
                                  "kv_bytes_per_step_read": kv_bytes,
-                                 "roofline": _roof("hbm", alg_bytes / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s")}
+                                 "roofline": _roof("hbm", alg_bytes / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s",
+                                                   _traffic(f"decode_{cfg_name}_b{b}"))}
         del graph, model
         torch.cuda.empty_cache()
     return out
@@ -500,6 +502,34 @@ def profile_mix(ops, name, steps):
             del model
             torch.cuda.empty_cache()
         print("dec70b done")
+    elif name == "decsteps":
+        # the bench's decode legs at full depth (Llama-2-7B at B = 1 / 8 / 32 after a 2048-token prompt,
+        # Llama-3-70B at B = 1 / 16 / 64 after 4096 tokens; random KV), two eager steps each at the leg's
+        # middle position (prompt + half the generated tokens: the leg's mean KV length), every step
+        # preceded by a one-row silu_mul launch (a kernel no decode step runs) that marks the step's
+        # first dispatch for the FETCH_SIZE / WRITE_SIZE passes of profiles/decode_step_traffic.md
+        from mindpipe_amd.decoder import DecoderConfig, W4Decoder
+        mark = torch.zeros(1, 2, dtype=torch.float16, device="cuda")
+        for cfg_name, batches, prompt, gen in (("llama2_7b", (1, 8, 32), 2048, 256),
+                                               ("llama3_70b", (1, 16, 64), 4096, 64)):
+            cfg = getattr(DecoderConfig, cfg_name)()
+            for b in batches:
+                model = W4Decoder(cfg, max_batch=b, max_len=prompt + gen + 8)
+                g = torch.Generator(device="cuda").manual_seed(5)
+                model.k_cache.normal_(0, 1, generator=g)
+                model.v_cache.normal_(0, 1, generator=g)
+                tok = torch.randint(0, cfg.vocab, (b,), device="cuda", generator=g)
+                cur = torch.tensor([prompt + gen // 2], device="cuda", dtype=torch.int64)
+                torch.cuda.synchronize()
+                for _ in range(2):
+                    ops.silu_mul(mark)
+                    tok = model.decode_step(tok, cur)
+                    cur.add_(1)
+                ops.silu_mul(mark)
+                torch.cuda.synchronize()
+                print(f"decsteps {cfg_name} B={b} done", flush=True)
+                del model
+                torch.cuda.empty_cache()
     elif name == "w8big":
         gen = torch.Generator(device="cuda").manual_seed(1)
         qx = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device="cuda", generator=gen)
