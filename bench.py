@@ -19,7 +19,7 @@ stated in each ``sample``).
 ``--profile NAME`` runs one kernel mix for rocprofv3 (the commands in ``profiles/``):
 ``w4gemv`` (the headline loop), ``readfloor`` (one-launch reads of 8.9 MB, rotated), ``readsweep``
 (read probes of several launch shapes at 8.9 MB and 1 GiB), ``curead`` (per-CU read rates from L2 and
-from HBM, into registers or LDS), ``w8sweep`` (the W8A8 sweep's GEMMs), ``moe`` (the Mixtral MoE
+from HBM, into registers or LDS), ``mfmabread`` (the MoE weights read in an MFMA B operand's lane order), ``w8sweep`` (the W8A8 sweep's GEMMs), ``moe`` (the Mixtral MoE
 chain), ``moesmall`` (the same chain at an expert FFN of 1792), ``prefill`` (the 7B prefill linears at
 M = 2048), ``w4shapes`` (M=16 and the 70B GEMV shapes), ``w4bf16`` (the bf16 W4A16 legs),
 ``w4batch8`` (7B gate/up and down at M = 1 and 8), ``dec7b`` (the 7B decode step), ``dec70b`` (four
@@ -391,6 +391,25 @@ def profile_mix(ops, name, steps):
                         print(f"curead {mode} grid={grid} threads={threads} loads={loads} dma={int(dma)}: "
                               f"{ms * 1e3:.1f} us, {total / (ms * 1e-3) / 1e12:.2f} TB/s, "
                               f"{total / (ms * 1e-3) / 1e9 / 256:.1f} GB/s per CU", flush=True)
+    elif name == "mfmabread":
+        # the MoE expert weights read in an MFMA B operand's lane order straight from memory (32 rows x
+        # 32 bytes per load instruction), against the same bytes read contiguously: GEMM1's
+        # [8 x 28672, 4096] and GEMM2's [8 x 4096, 14336]
+        from mindpipe_amd.measure import probe_read, probe_read_mfma_b
+        for rows, kb, kps in ((8 * 28672, 4096, (1, 2, 4)), (8 * 4096, 14336, (1, 2, 4, 7))):
+            buf = torch.ones(rows * kb // 4, dtype=torch.int32, device="cuda")
+            sink = probe_read(buf, None, 256, 4, 0)
+            ms = _time_graph(lambda i: probe_read(buf, sink, 256, 4, 0), 1, steps, 2)
+            print(f"mfmabread [{rows}, {kb}] contiguous: {ms * 1e3:.1f} us, {rows * kb / (ms * 1e-3) / 1e12:.2f} TB/s",
+                  flush=True)
+            for kp in kps:
+                for d in (1, 2, 4, 8):
+                    bs = probe_read_mfma_b(buf, rows, kb, kp, d)
+                    ms = _time_graph(lambda i: probe_read_mfma_b(buf, rows, kb, kp, d, bs), 1, steps, 2)
+                    print(f"mfmabread [{rows}, {kb}] kparts={kp} depth={d}: {ms * 1e3:.1f} us, "
+                          f"{rows * kb / (ms * 1e-3) / 1e12:.2f} TB/s", flush=True)
+            del buf
+            torch.cuda.empty_cache()
     elif name == "w8sweep":
         # the W8A8 sweep legs' GEMMs (M = 1, 16, 256, 4096; N = 11008, K = 4096) on random int8 data,
         # M <= 256 over 13 rotated weight copies as in the bench

@@ -30,6 +30,9 @@ def _load() -> C.CDLL:
         lib.mp_probe_cu_read.restype = C.c_int
         lib.mp_probe_cu_read.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.c_void_p, C.c_void_p]
+        lib.mp_probe_read_mfma_b.restype = C.c_int
+        lib.mp_probe_read_mfma_b.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int, C.c_int, C.c_void_p,
+                                             C.c_void_p]
         _LIB = lib
     return _LIB
 
@@ -82,4 +85,19 @@ def probe_cu_read(buf: torch.Tensor, region_bytes: int, nreg: int, passes: int, 
                               sink.data_ptr(), torch.cuda.current_stream(buf.device).cuda_stream)
     if rc != 0:
         raise RuntimeError(f"mp_probe_cu_read failed with status {rc}")
+    return sink
+
+
+def probe_read_mfma_b(buf: torch.Tensor, rows: int, row_bytes: int, kparts: int, depth: int,
+                      sink: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One launch reading an int8 ``[rows, row_bytes]`` matrix in the lane order of an MFMA B operand
+    loaded straight from memory (32 rows x 32 bytes per load instruction), ``kparts`` workgroups per 32
+    rows splitting K, ``depth`` 128-byte K steps in flight.  Returns the sink the launch may write."""
+    lib = _load()
+    if sink is None:
+        sink = torch.zeros(-(-rows // 32) * kparts, dtype=torch.int32, device=buf.device)
+    rc = lib.mp_probe_read_mfma_b(buf.data_ptr(), rows, row_bytes, kparts, depth, sink.data_ptr(),
+                                  torch.cuda.current_stream(buf.device).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"mp_probe_read_mfma_b failed with status {rc}")
     return sink

@@ -152,7 +152,64 @@ __global__ __launch_bounds__(THREADS) void probe_cu_read_kernel(const uint4 *__r
   if (x == 0x9E3779B9u) sink[blockIdx.x] = x;
 }
 
+// MFMA-operand weight read: an int8 [rows, row_bytes] matrix read the way a wave feeds it to
+// v_mfma_i32_32x32x32_i8 as the B operand straight from memory.  A workgroup of four waves owns 32
+// rows and a K range (kparts workgroups per 32 rows split K); wave w takes the w-th quarter of it.  Per
+// 128-byte K step lane l loads 4 x 16 bytes of row l % 32 at K offset 64 (l / 32) + 16 i: each load
+// instruction touches 32 rows x 32 bytes, the four of a step the same 32 cache lines.  DEPTH steps in
+// flight.
+template <int DEPTH>
+__global__ __launch_bounds__(256) void probe_mfma_b_kernel(const int8_t *__restrict__ p, int64_t rows,
+                                                          int64_t row_bytes, int kparts, uint32_t *__restrict__ sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t rblk = blockIdx.x / kparts, kp = blockIdx.x % kparts;
+  int64_t row = rblk * 32 + (lane & 31);
+  row = row < rows ? row : rows - 1;
+  const int64_t kspan = row_bytes / kparts / 4;  // bytes of K per wave (a multiple of 128)
+  const int64_t k0 = kp * (row_bytes / kparts) + wave * kspan;
+  const int8_t *src = p + row * row_bytes + k0 + 64 * (lane >> 5);
+  const int64_t steps = kspan / 128;
+  uint32_t x = 0;
+  for (int64_t s0 = 0; s0 < steps; s0 += DEPTH) {
+    uint4 v[DEPTH][4];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int64_t st = s0 + d < steps ? s0 + d : steps - 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[d][i] = *reinterpret_cast<const uint4 *>(src + st * 128 + 16 * i);
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x ^= v[d][i].x ^ v[d][i].w;
+  }
+  if (x == 0x9E3779B9u) sink[blockIdx.x] = x;
+}
+
 }  // namespace
+
+// MFMA-operand weight read (probe_mfma_b_kernel) of an int8 [rows, row_bytes] matrix: ceil(rows / 32) x
+// kparts workgroups of 256 threads, depth in {1, 2, 4, 8}; row_bytes a multiple of 512 kparts; sink:
+// uint32 [ceil(rows / 32) * kparts].
+extern "C" int mp_probe_read_mfma_b(const void *buf, int64_t rows, int64_t row_bytes, int kparts, int depth,
+                                    uint32_t *sink, mp_stream_t stream) {
+  if (!buf || !sink || rows <= 0 || kparts <= 0) return MP_ERR_ARG;
+  if (!mp_aligned(buf, 16)) return MP_ERR_ALIGN;
+  if (row_bytes <= 0 || row_bytes % (512 * static_cast<int64_t>(kparts))) return MP_ERR_SHAPE;
+  const int64_t grid = mp_cdiv(rows, 32) * kparts;
+  if (grid > INT32_MAX) return MP_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const auto *pp = static_cast<const int8_t *>(buf);
+#define MP_PB(D_) hipLaunchKernelGGL((probe_mfma_b_kernel<D_>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, pp, rows, row_bytes, kparts, sink)
+  if (depth == 1) MP_PB(1);
+  else if (depth == 2) MP_PB(2);
+  else if (depth == 4) MP_PB(4);
+  else if (depth == 8) MP_PB(8);
+  else return MP_ERR_ARG;
+#undef MP_PB
+  MP_CHECK_LAUNCH();
+  return MP_OK;
+}
 
 // Per-CU read rate (probe_cu_read_kernel): `grid` workgroups of `threads` (256 / 512), `loads` (4 / 8)
 // 16-byte loads per lane per step, each reading the region (w % nreg) of `region_bytes` bytes

@@ -534,7 +534,7 @@ def _moe_case(t, h, inter, e, seed=0):
 # (t, h, inter, e): experts of up to ~300 rows (two 256-row chunks on the grouped large-M kernel),
 # an intermediate size that is not a multiple of 128 (tiled kernel), a nearly empty batch
 @pytest.mark.parametrize("t,h,inter,e", [(64, 256, 512, 8), (200, 512, 384, 4), (3, 128, 128, 8),
-                                         (600, 256, 256, 4), (64, 256, 320, 4)])
+                                         (600, 256, 256, 4), (64, 256, 320, 4), (256, 1024, 512, 8)])
 def test_moe_chain_matches_oracle(t, h, inter, e):
     _say("moe", t, h, inter, e)
     x, ids, tw, q13, s13, q2, s2 = _moe_case(t, h, inter, e)
@@ -669,7 +669,12 @@ def test_moe_mixtral_full_shape_sampled_tokens():
 # kernel): empty experts, one-row experts, experts of several 256-row chunks, more than 64
 # experts, output widths that are not tile multiples.  (counts, k, n, inter)
 GROUPED_CASES = [([0, 300, 1, 0, 130, 64], 256, 320, 96), ([128] * 4, 512, 256, 128), ([0, 0, 700], 128, 128, 64),
-                 ([int(c) for c in np.random.default_rng(7).integers(0, 10, 70)], 256, 128, 64)]
+                 ([int(c) for c in np.random.default_rng(7).integers(0, 10, 70)], 256, 128, 64),
+                 # longer K: experts of every size around the 32-row tile and 256-row chunk edges, weight
+                 # slices past N and I, 70 experts, a K of 12 steps
+                 ([0, 300, 1, 0, 130, 64, 257, 33, 31, 32, 256, 255], 512, 320, 96), ([128] * 4, 1024, 256, 128),
+                 ([0, 0, 700], 512, 128, 64), ([int(c) for c in np.random.default_rng(8).integers(0, 10, 70)], 512, 128, 64),
+                 ([31, 200, 17], 1536, 200, 200)]
 
 
 @pytest.mark.parametrize("counts,k,n,inter", GROUPED_CASES)
