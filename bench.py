@@ -19,7 +19,7 @@ stated in each ``sample``).
 ``--profile NAME`` runs one kernel mix for rocprofv3 (the commands in ``profiles/``):
 ``w4gemv`` (the headline loop), ``readfloor`` (one-launch reads of 8.9 MB, rotated), ``readsweep``
 (read probes of several launch shapes at 8.9 MB and 1 GiB), ``curead`` (per-CU read rates from L2 and
-from HBM, into registers or LDS), ``mfmabread`` (the MoE weights read in an MFMA B operand's lane order), ``w8sweep`` (the W8A8 sweep's GEMMs), ``moe`` (the Mixtral MoE
+from HBM, into registers or LDS), ``cufew`` (the HBM read rate of one CU when 8 to 128 read), ``mfmabread`` (the MoE weights read in an MFMA B operand's lane order), ``w8sweep`` (the W8A8 sweep's GEMMs), ``moe`` (the Mixtral MoE
 chain), ``moesmall`` (the same chain at an expert FFN of 1792), ``prefill`` (the 7B prefill linears at
 M = 2048), ``w4shapes`` (M=16 and the 70B GEMV shapes), ``w4bf16`` (the bf16 W4A16 legs),
 ``w4batch8`` (7B gate/up and down at M = 1 and 8), ``dec7b`` (the 7B decode step), ``dec70b`` (four
@@ -391,6 +391,21 @@ def profile_mix(ops, name, steps):
                         print(f"curead {mode} grid={grid} threads={threads} loads={loads} dma={int(dma)}: "
                               f"{ms * 1e3:.1f} us, {total / (ms * 1e-3) / 1e12:.2f} TB/s, "
                               f"{total / (ms * 1e-3) / 1e9 / 256:.1f} GB/s per CU", flush=True)
+    elif name == "cufew":
+        # the HBM read rate one workgroup (one CU) reaches when few CUs read: 8 to 128 workgroups, each
+        # streaming its own region of 1 GiB (at most 64 MB) once, into registers or straight into LDS
+        from mindpipe_amd.measure import probe_cu_read
+        buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+        for grid in (8, 32, 64, 128):
+            for threads, loads, dma in ((256, 4, False), (256, 8, False), (512, 8, False), (256, 8, True)):
+                region = min((1 << 30) // grid, 64 << 20)
+                sink = probe_cu_read(buf, region, grid, 1, grid, threads, loads, dma)
+                ms = _time_graph(lambda i: probe_cu_read(buf, region, grid, 1, grid, threads, loads, dma, sink), 1,
+                                 steps, 2)
+                total = region * grid
+                print(f"cufew grid={grid} threads={threads} loads={loads} dma={int(dma)}: {ms * 1e3:.1f} us, "
+                      f"{total / (ms * 1e-3) / 1e12:.2f} TB/s, {total / (ms * 1e-3) / 1e9 / grid:.1f} GB/s per "
+                      f"workgroup", flush=True)
     elif name == "mfmabread":
         # the MoE expert weights read in an MFMA B operand's lane order straight from memory (32 rows x
         # 32 bytes per load instruction), against the same bytes read contiguously: GEMM1's

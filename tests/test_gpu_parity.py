@@ -436,8 +436,11 @@ W8_CASES = [(1, 11008, 4096), (16, 11008, 4096), (5, 1000, 256), (17, 512, 1024)
             # skinny kernel where the whole K fits the 76 KB LDS budget but not the staging
             # registers (more than 4096 sixteen-byte pieces): K split into chunks
             (17, 512, 4096), (18, 300, 4096), (7, 256, 11008), (5, 256, 14336), (33, 256, 2048),
-            # C2 sweep at M = 256 (tiled kernel) on the full N x K
+            # C2 sweep at M = 256 (mid-M direct-to-LDS kernel) on the full N x K
             (256, 11008, 4096),
+            # mid-M kernel (64 .. 256 tiles of 128 x 128): partial row and column tiles, K of 1 to 9
+            # steps of 128 (partial four-step loop groups), odd N (the unpaired store path)
+            (200, 8200, 512), (65, 8320, 1152), (384, 2700, 640), (1000, 2048, 128), (129, 12001, 256),
             # tiled kernel: the LDS-staged 16-byte-store epilogue with partial row and column tiles
             # (N % 8 == 0), and the two-byte-store epilogue (N % 8 != 0)
             (200, 1000, 512), (100, 333, 512),
