@@ -36,6 +36,3 @@ struct mp_i8_args {
 };
 
 int mp_launch_i8_gemm(const mp_i8_args &args, int epilogue, hipStream_t stream);
-// Whether a grouped launch with this epilogue runs on the weight-streaming kernel, whose SwiGLU
-// epilogue writes 4 * ceil(n / 64) abs-max partials per row (the other grouped kernels 2 * ceil(n / 64)).
-bool mp_moe_stream_takes(const mp_i8_args &args, int epilogue);

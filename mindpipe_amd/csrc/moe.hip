@@ -387,9 +387,7 @@ extern "C" int mp_moe_permute_quant(const void *x, int x_dtype, const float *x_s
   return MP_OK;
 }
 
-// abs-max partials per row of the GMM1 workspace: the most any GEMM1 kernel writes (the weight-streaming
-// kernel: one per 16 output columns; the others one per 32)
-static int64_t gmm1_partials(int64_t inter) { return 4 * mp_cdiv(inter, 64); }
+static int64_t gmm1_partials(int64_t inter) { return 2 * mp_cdiv(inter, 64); }
 
 extern "C" size_t mp_moe_gmm1_workspace_bytes(int64_t rows, int64_t inter) {
   const size_t hbytes = static_cast<size_t>(rows) * static_cast<size_t>(inter) * sizeof(float);
@@ -415,7 +413,7 @@ extern "C" int mp_i8_gemm_swiglu_requant(const int8_t *routed, const float *rout
   const size_t hbytes = static_cast<size_t>(rows) * static_cast<size_t>(inter) * sizeof(float);
   float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + ((hbytes + 255) & ~static_cast<size_t>(255)));
   const int mode = scale_rule == MP_SCALE_FAKE ? mp_round_mode_of(act_dtype) : kRoundNone;
-  int n_partial = static_cast<int>(2 * mp_cdiv(inter, 64));
+  const int n_partial = static_cast<int>(gmm1_partials(inter));
   int rc;
   if (scale_rule == MP_SCALE_FAKE) {
     // the reference's F.linear on the fake-quant tensors: fp16 / bf16 MFMA on r(q * s) values
@@ -457,8 +455,6 @@ extern "C" int mp_i8_gemm_swiglu_requant(const int8_t *routed, const float *rout
     a.k = h;
     a.ldy = inter;
     a.epi_round = mode;
-    if (mp_moe_stream_takes(a, MP_EPI_SWIGLU)) n_partial = static_cast<int>(gmm1_partials(inter));
-    a.n_partial = n_partial;
     rc = mp_launch_i8_gemm(a, MP_EPI_SWIGLU, s);
   }
   if (rc != MP_OK) return rc;

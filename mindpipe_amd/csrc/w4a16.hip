@@ -519,7 +519,7 @@ __global__ __launch_bounds__(512) void w4a16_decode_kernel(
 // pseudo-quantized weight is (w4_bf16x8, natural K order), so the activation pieces go to the MFMA
 // (f32_16x16x32_bf16) as they lie, the group scale is inside each weight and no sum against ones
 // is needed.  The SwiGLU form rounds gate, up, silu and the product to bf16.
-template <int MT, int NT, int S, bool ZP, bool SWI = false, bool XDB_ON = true, bool BF = false, bool ONE = false>
+template <int MT, int NT, int S, bool ZP, bool SWI = false, bool XDB_ON = true, bool BF = false>
 __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
     const uint16_t *__restrict__ x, int m_rows, int k, const uint32_t *__restrict__ wq, int n_cols,
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ zr, int n_groups,
@@ -714,27 +714,7 @@ __global__ __launch_bounds__(S * 64) void w4a16_batch_kernel(
   // basic block that issues it; scheduling barriers keep every group of loads
   // where it is written.  Dead blocks (past nblk) read zeros: zero scale, no
   // contribution.
-  if constexpr (ONE) {
-    // every wave owns one 8-block step of K or none (the launcher checks): the step's scales,
-    // activations and weights are all loaded before any arithmetic, so the step costs one memory
-    // round trip (a wave without a step loads dead blocks: zeros, no memory access)
-    static_assert(MT == 1 && XDB, "one-step form: 16-row tiles with the activation double buffer");
-    uint4 wall[4][U][NT], xall[4][U][XI];
-    const int b0 = nsteps > 0 ? lo : nblk;
-    load_sz(b0);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      load_x_to(xall[q], b0 + 2 * q);
-      issue_w(wall[q], b0 + 2 * q);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t swd[NT], zwd[NT];
-      words(q, swd, zwd);
-      compute_x(wall[q], xall[q], swd, zwd);
-    }
-  } else if constexpr (XDB) {
+  if constexpr (XDB) {
     // activations one pair ahead in two buffers, the next step's scales during the
     // current step's last pair (its words copied out first): a pair waits only for loads
     // issued a pair or more before it
@@ -1796,13 +1776,6 @@ static bool mp_batch_xdb() {
   return v;
 }
 
-// One-step form of the batched kernel (16-row tiles, one column tile, every wave at most one 8-block
-// step of K): 1 = on, 0 = off (MP_W4_BATCH_ONE, for measurements).
-static bool mp_batch_one() {
-  static const bool v = mp_knob("MP_W4_BATCH_ONE") && atoi(mp_knob("MP_W4_BATCH_ONE")) == 1;
-  return v;
-}
-
 // Row tiling of the batched kernel: MT 16-row tiles per wave, and parts = ceil(M / 16 MT)
 // workgroups per column group when M exceeds them.  Default: MT = 1 up to 16 rows, 2 above
 // (33..64 rows in two parts).  MP_W4_BATCH_PART_MT=1 / 2 / 4 fixes MT (for measurements).
@@ -2204,22 +2177,7 @@ do {                                             \
   else if (split == 8 || MT_ * NT_ > 1) MP_W4_BATCH(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : 8)); \
   else MP_W4_BATCH(MT_, NT_, (MT_ * NT_ >= 8 ? 4 : (MT_ * NT_ > 1 ? 8 : 16))); \
 } while (0)
-#define MP_W4_BATCH_ONE(S_)                                                                                      \
-  do {                                                                                                           \
-    if (zp)                                                                                                      \
-      hipLaunchKernelGGL((w4a16_batch_kernel<1, 1, S_, true, false, true, BF, true>), grid, dim3(S_ * 64), 0, s, xp, \
-                         mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                        \
-    else                                                                                                         \
-      hipLaunchKernelGGL((w4a16_batch_kernel<1, 1, S_, false, false, true, BF, true>), grid, dim3(S_ * 64), 0, s, xp, \
-                         mi, ki, wp, ni, sp, zp, n_groups_i, bp, yp, hv);                                        \
-  } while (0)
-  if (mt == 1 && nt == 1 && xdb && nsteps <= split && mp_batch_one()) {
-    if (split == 1) MP_W4_BATCH_ONE(1);
-    else if (split == 2) MP_W4_BATCH_ONE(2);
-    else if (split == 4) MP_W4_BATCH_ONE(4);
-    else if (split == 8) MP_W4_BATCH_ONE(8);
-    else MP_W4_BATCH_ONE(16);
-  } else if (mt == 1) {
+  if (mt == 1) {
     if (nt == 1) MP_W4_BATCH_S(1, 1);
     else if (nt == 2) MP_W4_BATCH_S(1, 2);
     else MP_W4_BATCH_S(1, 4);
@@ -2232,7 +2190,6 @@ do {                                             \
     else if (nt == 2) MP_W4_BATCH_S(4, 2);
     else MP_W4_BATCH_S(4, 4);
   }
-#undef MP_W4_BATCH_ONE
 #undef MP_W4_BATCH_S
 #undef MP_W4_BATCH
 }

@@ -726,134 +726,6 @@ __device__ __forceinline__ void moe_max_step(float (&v)[32], int lane) {
   }
 }
 
-// Epilogue of one grouped-GEMM work item for a wave of the grouped kernels' 8-wave layout (wave (wr, wn)
-// holds 32x32 accumulator tiles i = 0, 1 at item rows 32 wr + 128 i and j = 0, 1 at its 64 columns:
-// SwiGLU gate / up, else columns 32 j), with the item's per-token scales sab[256] and the scales of its
-// 128 weight rows scb[128] in LDS.  Element r of tile (i, j): local row 32 wr + 128 i + 8 (r >> 2) +
-// 4 (lane >> 5) + (r & 3).  Stores go through buffer descriptors over the item's rows: rows past
-// row_end and columns past N (offset kOob) are dropped without a branch.  (Guarding each store with a
-// branch makes the compiler wait for every earlier store.)
-template <int EPI>
-__device__ __forceinline__ void moe_item_epilogue(const mp_i8_args &p, const i16_t (&acc)[2][2], int lane, int wr,
-                                                  int wn, int slice, int64_t row_begin, int64_t row_end,
-                                                  const float *sab, const float *scb) {
-  constexpr int BN = kMoeBN, TM = 2, TN = 2;
-  constexpr bool SWI = EPI == MP_EPI_SWIGLU;
-  constexpr uint32_t kOob = 0x80000000u;
-  const uint32_t nrows = static_cast<uint32_t>(row_end - row_begin);
-  const uint32_t ldy = static_cast<uint32_t>(p.ldy);
-  const int lm0 = 32 * wr + 4 * (lane >> 5);
-  // the lane's per-token scales: rows lm0 + 128 i + 8 q + (0..3)
-  float sa_r[TM][16];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f4_t s4 = *reinterpret_cast<const f4_t *>(sab + lm0 + 128 * i + 8 * q);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) sa_r[i][4 * q + c] = s4[c];
-    }
-  if (SWI) {
-    // h = silu((acc_g * s_tok) * s_g) * ((acc_u * s_tok) * s_u), and the abs-max of
-    // each row over the wave's 32 columns: the 32 row values of a lane are reduced
-    // across the 32 lanes of its half by a transposing butterfly (31 exchanges; after
-    // it lane l holds the maximum of row value l % 32)
-    const int64_t col = static_cast<int64_t>(slice) * (BN / 2) + wn * 32 + (lane & 31);
-    const bool cval = col < p.n;
-    const float sg = scb[wn * 32 + (lane & 31)], su = scb[BN / 2 + wn * 32 + (lane & 31)];
-    const __amdgpu_buffer_rsrc_t hr = mp_rsrc(static_cast<float *>(p.y) + row_begin * p.ldy, nrows * ldy * 4);
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lm = lm0 + i * 128 + 8 * (r >> 2) + (r & 3);
-        const float gv = mp_mul(mp_mul(static_cast<float>(acc[i][0][r]), sa_r[i][r]), sg);
-        const float uv = mp_mul(mp_mul(static_cast<float>(acc[i][1][r]), sa_r[i][r]), su);
-        const float h = mp_swiglu_epi(gv, uv, p.epi_round);
-        mp_buf_store4(hr, cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * 4 : kOob,
-                      __float_as_uint(h));
-        v[i * 16 + r] = (cval && static_cast<uint32_t>(lm) < nrows) ? fabsf(h) : 0.f;
-      }
-    moe_max_step<16>(v, lane);
-    moe_max_step<8>(v, lane);
-    moe_max_step<4>(v, lane);
-    moe_max_step<2>(v, lane);
-    moe_max_step<1>(v, lane);
-    const int jv = lane & 31;
-    const int lm = lm0 + (jv >> 4) * 128 + 8 * ((jv & 15) >> 2) + (jv & 3);
-    const uint32_t np = static_cast<uint32_t>(p.n_partial);
-    const __amdgpu_buffer_rsrc_t pr = mp_rsrc(p.amax_partial + row_begin * p.n_partial, nrows * np * 4);
-    mp_buf_store4(pr, (static_cast<uint32_t>(lm) * np + static_cast<uint32_t>(slice * 2 + wn)) * 4,
-                  __float_as_uint(v[0]));
-  } else if (EPI == MP_EPI_AMAX) {
-    // y = (acc * s_tok) * s_ch (+ bias), rounded to the 16-bit output and stored (the
-    // arithmetic and order of the dense epilogues), and the abs-max of each row's rounded
-    // values over the wave's 64 columns, reduced as in the SwiGLU epilogue, into
-    // amax_partial[row][2 * slice + wave column]
-    const bool bf = p.out_dtype == MP_BF16, hb = p.bias != nullptr;
-    const __amdgpu_buffer_rsrc_t yr =
-        mp_rsrc(static_cast<char *>(p.y) + row_begin * p.ldy * 2, nrows * ldy * 2);
-    float v[32];
-#pragma unroll
-    for (int t = 0; t < 32; ++t) v[t] = 0.f;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = static_cast<int64_t>(slice) * BN + wn * 64 + j * 32 + (lane & 31);
-      const bool cval = col < p.n;
-      const float scj = scb[wn * 64 + j * 32 + (lane & 31)];
-      const float bj = hb ? mp_load_as_f32(p.bias, cval ? col : p.n - 1, p.bias_dtype) : 0.f;
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int lm = lm0 + i * 128 + 8 * (r >> 2) + (r & 3);
-          float yv = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), sa_r[i][r]), scj);
-          yv = hb ? mp_add(yv, bj) : yv;
-          const uint16_t hv = bf ? mp_f2bf(yv) : mp_f2h(yv);
-          const uint32_t off =
-              cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * 2 : kOob;
-          mp_buf_store2(yr, off, hv);
-          const float rv = bf ? mp_bf2f(hv) : mp_h2f(hv);
-          v[i * 16 + r] = fmaxf(v[i * 16 + r], (cval && static_cast<uint32_t>(lm) < nrows) ? fabsf(rv) : 0.f);
-        }
-    }
-    moe_max_step<16>(v, lane);
-    moe_max_step<8>(v, lane);
-    moe_max_step<4>(v, lane);
-    moe_max_step<2>(v, lane);
-    moe_max_step<1>(v, lane);
-    const int jv = lane & 31;
-    const int lm = lm0 + (jv >> 4) * 128 + 8 * ((jv & 15) >> 2) + (jv & 3);
-    const uint32_t np = static_cast<uint32_t>(p.n_partial);
-    const __amdgpu_buffer_rsrc_t pr = mp_rsrc(p.amax_partial + row_begin * p.n_partial, nrows * np * 4);
-    mp_buf_store4(pr, (static_cast<uint32_t>(lm) * np + static_cast<uint32_t>(slice * 2 + wn)) * 4,
-                  __float_as_uint(v[0]));
-  } else {
-    const uint32_t esz = EPI == MP_EPI_F32 ? 4 : 2;
-    const bool bf = p.out_dtype == MP_BF16;
-    const __amdgpu_buffer_rsrc_t yr =
-        mp_rsrc(static_cast<char *>(p.y) + row_begin * p.ldy * esz, nrows * ldy * esz);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = static_cast<int64_t>(slice) * BN + wn * 64 + j * 32 + (lane & 31);
-      const bool cval = col < p.n;
-      const float scj = scb[wn * 64 + j * 32 + (lane & 31)];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int lm = lm0 + i * 128 + 8 * (r >> 2) + (r & 3);
-          const float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), sa_r[i][r]), scj);
-          const uint32_t off =
-              cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * esz : kOob;
-          if (EPI == MP_EPI_F32) mp_buf_store4(yr, off, __float_as_uint(v));
-          else mp_buf_store2(yr, off, bf ? mp_f2bf(v) : mp_f2h(v));
-        }
-    }
-  }
-}
-
 template <int EPI, int D>
 __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n_slices) {
   constexpr int BM = kMoeBM, BN = kMoeBN, BK = kMoeBK, LD = kMoeLD, NT = kMoeThreads;
@@ -1074,503 +946,129 @@ __global__ __launch_bounds__(kMoeThreads) void i8_moe_kernel(mp_i8_args p, int n
     if (has_next) set_item(xcd * share + idx);
     prologue(has_next ? 0 : nkt - 1);
 
-    if (cur_act) moe_item_epilogue<EPI>(p, acc, lane, wr, wn, cur_slice, cur_begin, cur_end, ssa + par * BM, ssc + par * BN);
+    if (cur_act) {
+      // element r of tile (i, j): local row 32 wr + 128 i + 8 (r >> 2) + 4 (lane >> 5) + (r & 3).
+      // Stores go through buffer descriptors over the item's rows: rows past cur_end and
+      // columns past n_out (offset kOob) are dropped without a branch.  (Guarding each
+      // store with a branch makes the compiler wait for every earlier store.)
+      constexpr uint32_t kOob = 0x80000000u;
+      const uint32_t nrows = static_cast<uint32_t>(cur_end - cur_begin);
+      const uint32_t ldy = static_cast<uint32_t>(p.ldy);
+      const int lm0 = 32 * wr + 4 * (lane >> 5);
+      // the lane's per-token scales: rows lm0 + 128 i + 8 q + (0..3)
+      float sa_r[TM][16];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f4_t s4 = *reinterpret_cast<const f4_t *>(ssa + par * BM + lm0 + 128 * i + 8 * q);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) sa_r[i][4 * q + c] = s4[c];
+        }
+      if (SWI) {
+        // h = silu((acc_g * s_tok) * s_g) * ((acc_u * s_tok) * s_u), and the abs-max of
+        // each row over the wave's 32 columns: the 32 row values of a lane are reduced
+        // across the 32 lanes of its half by a transposing butterfly (31 exchanges; after
+        // it lane l holds the maximum of row value l % 32)
+        const int64_t col = static_cast<int64_t>(cur_slice) * (BN / 2) + wn * 32 + (lane & 31);
+        const bool cval = col < n_out;
+        const float sg = ssc[par * BN + wn * 32 + (lane & 31)], su = ssc[par * BN + BN / 2 + wn * 32 + (lane & 31)];
+        const __amdgpu_buffer_rsrc_t hr = mp_rsrc(static_cast<float *>(p.y) + cur_begin * p.ldy, nrows * ldy * 4);
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int lm = lm0 + i * 128 + 8 * (r >> 2) + (r & 3);
+            const float gv = mp_mul(mp_mul(static_cast<float>(acc[i][0][r]), sa_r[i][r]), sg);
+            const float uv = mp_mul(mp_mul(static_cast<float>(acc[i][1][r]), sa_r[i][r]), su);
+            const float h = mp_swiglu_epi(gv, uv, p.epi_round);
+            mp_buf_store4(hr, cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * 4 : kOob,
+                          __float_as_uint(h));
+            v[i * 16 + r] = (cval && static_cast<uint32_t>(lm) < nrows) ? fabsf(h) : 0.f;
+          }
+        moe_max_step<16>(v, lane);
+        moe_max_step<8>(v, lane);
+        moe_max_step<4>(v, lane);
+        moe_max_step<2>(v, lane);
+        moe_max_step<1>(v, lane);
+        const int jv = lane & 31;
+        const int lm = lm0 + (jv >> 4) * 128 + 8 * ((jv & 15) >> 2) + (jv & 3);
+        const uint32_t np = static_cast<uint32_t>(p.n_partial);
+        const __amdgpu_buffer_rsrc_t pr = mp_rsrc(p.amax_partial + cur_begin * p.n_partial, nrows * np * 4);
+        mp_buf_store4(pr, (static_cast<uint32_t>(lm) * np + static_cast<uint32_t>(cur_slice * 2 + wn)) * 4,
+                      __float_as_uint(v[0]));
+      } else if (EPI == MP_EPI_AMAX) {
+        // y = (acc * s_tok) * s_ch (+ bias), rounded to the 16-bit output and stored (the
+        // arithmetic and order of the dense epilogues), and the abs-max of each row's rounded
+        // values over the wave's 64 columns, reduced as in the SwiGLU epilogue, into
+        // amax_partial[row][2 * slice + wave column]
+        const bool bf = p.out_dtype == MP_BF16, hb = p.bias != nullptr;
+        const __amdgpu_buffer_rsrc_t yr =
+            mp_rsrc(static_cast<char *>(p.y) + cur_begin * p.ldy * 2, nrows * ldy * 2);
+        float v[32];
+#pragma unroll
+        for (int t = 0; t < 32; ++t) v[t] = 0.f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int64_t col = static_cast<int64_t>(cur_slice) * BN + wn * 64 + j * 32 + (lane & 31);
+          const bool cval = col < n_out;
+          const float scj = ssc[par * BN + wn * 64 + j * 32 + (lane & 31)];
+          const float bj = hb ? mp_load_as_f32(p.bias, cval ? col : n_out - 1, p.bias_dtype) : 0.f;
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int lm = lm0 + i * 128 + 8 * (r >> 2) + (r & 3);
+              float yv = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), sa_r[i][r]), scj);
+              yv = hb ? mp_add(yv, bj) : yv;
+              const uint16_t hv = bf ? mp_f2bf(yv) : mp_f2h(yv);
+              const uint32_t off =
+                  cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * 2 : kOob;
+              mp_buf_store2(yr, off, hv);
+              const float rv = bf ? mp_bf2f(hv) : mp_h2f(hv);
+              v[i * 16 + r] = fmaxf(v[i * 16 + r], (cval && static_cast<uint32_t>(lm) < nrows) ? fabsf(rv) : 0.f);
+            }
+        }
+        moe_max_step<16>(v, lane);
+        moe_max_step<8>(v, lane);
+        moe_max_step<4>(v, lane);
+        moe_max_step<2>(v, lane);
+        moe_max_step<1>(v, lane);
+        const int jv = lane & 31;
+        const int lm = lm0 + (jv >> 4) * 128 + 8 * ((jv & 15) >> 2) + (jv & 3);
+        const uint32_t np = static_cast<uint32_t>(p.n_partial);
+        const __amdgpu_buffer_rsrc_t pr = mp_rsrc(p.amax_partial + cur_begin * p.n_partial, nrows * np * 4);
+        mp_buf_store4(pr, (static_cast<uint32_t>(lm) * np + static_cast<uint32_t>(cur_slice * 2 + wn)) * 4,
+                      __float_as_uint(v[0]));
+      } else {
+        const uint32_t esz = EPI == MP_EPI_F32 ? 4 : 2;
+        const bool bf = p.out_dtype == MP_BF16;
+        const __amdgpu_buffer_rsrc_t yr =
+            mp_rsrc(static_cast<char *>(p.y) + cur_begin * p.ldy * esz, nrows * ldy * esz);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int64_t col = static_cast<int64_t>(cur_slice) * BN + wn * 64 + j * 32 + (lane & 31);
+          const bool cval = col < n_out;
+          const float scj = ssc[par * BN + wn * 64 + j * 32 + (lane & 31)];
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int lm = lm0 + i * 128 + 8 * (r >> 2) + (r & 3);
+              const float v = mp_mul(mp_mul(static_cast<float>(acc[i][j][r]), sa_r[i][r]), scj);
+              const uint32_t off =
+                  cval ? (static_cast<uint32_t>(lm) * ldy + static_cast<uint32_t>(col)) * esz : kOob;
+              if (EPI == MP_EPI_F32) mp_buf_store4(yr, off, __float_as_uint(v));
+              else mp_buf_store2(yr, off, bf ? mp_f2bf(v) : mp_f2h(v));
+            }
+        }
+      }
+    }
     load_scales();  // (the next item's, or again the current one's at the end)
     if (!has_next) break;
     par ^= 1;
   }
-}
-
-// Grouped (MoE) GEMM with direct global->LDS loads: the work items, item walk, waves and epilogues of
-// i8_moe_kernel (rows of one expert, at most 256, against 128 weight rows; eight waves; 128-byte K
-// steps), with the tiles loaded by `buffer_load_dwordx4 ... lds` into three LDS stages of 48 KB (A rows
-// 0..255, then B rows 0..127, 128 bytes each; chunk c of row r at slot c ^ ((r >> 1) & 7)) two K steps
-// ahead.  A runs through a descriptor over the item's rows (rows past the expert's end move nothing),
-// B through one over the expert's weight.  The load cursor runs ahead of the compute cursor across
-// work items: the next item's first two steps are in flight while the current item's epilogue runs,
-// and the next item's scales go to the other parity's LDS buffers with its first step.  Every wave
-// issues the same seven loads per step (four A, two B, one scale load, which falls past its descriptor
-// into a per-wave junk slot on the other steps, as every load does past the last item), so one static
-// vmcnt per step waits for the step about to be multiplied.  Needs two or more K steps per item (the
-// scale buffers of item j + 2 are rewritten after item j's epilogue).
-constexpr int kMdStages = 3;
-constexpr int kMdStage = (kMoeBM + kMoeBN) * kMoeBK;
-constexpr size_t kMdSmem = static_cast<size_t>(kMdStages) * kMdStage + 2 * (kMoeBM + kMoeBN) * sizeof(float) +
-                           8 * 64 * sizeof(float) + (kMoeMaxExperts + 1) * sizeof(int64_t);
-
-__device__ __forceinline__ void md_lds_load(__amdgpu_buffer_rsrc_t r, void *lds_wave_base, uint32_t voff, int size) {
-  if (size == 16)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds_wave_base)), 16,
-        voff, 0, 0, 0);
-  else
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds_wave_base)), 4,
-        voff, 0, 0, 0);
-}
-
-template <int EPI>
-__global__ __launch_bounds__(kMoeThreads) void i8_moe_dma_kernel(mp_i8_args p, int n_slices) {
-  constexpr int BM = kMoeBM, BN = kMoeBN, BK = kMoeBK, S = kMdStages, NT = kMoeThreads;
-  constexpr bool SWI = EPI == MP_EPI_SWIGLU;
-  constexpr uint32_t kOob = 0x80000000u;
-  extern __shared__ __attribute__((aligned(16))) int8_t smem_md[];
-  int8_t *ring = smem_md;                                                 // [S][(BM + BN) * BK]
-  float *ssa = reinterpret_cast<float *>(smem_md + S * kMdStage);         // [2][BM] per-token scales
-  float *ssc = ssa + 2 * BM;                                              // [2][BN] weight-row scales
-  float *junk = ssc + 2 * BN;                                             // [8][64] dummy scale loads
-  int64_t *soff = reinterpret_cast<int64_t *>(junk + 8 * 64);             // [E + 1] group offsets
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wn = wave & 1;
-
-  const int ne = p.n_experts;
-  for (int i = tid; i <= ne; i += NT) soff[i] = p.offsets[i];
-  mp_lds_barrier();
-  const int64_t *off = soff;
-  int total = 0;
-  for (int c0 = 0; c0 < ne; c0 += 64) {
-    int it = c0 + lane < ne ? moe_row_chunks(off, c0 + lane) * n_slices : 0;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) it += __shfl_xor(it, o, 64);
-    total += it;
-  }
-  total = __builtin_amdgcn_readfirstlane(total);
-  const int share = (total + 7) / 8;
-  const int xcd = static_cast<int>(blockIdx.x) % 8, stride = static_cast<int>(gridDim.x) / 8;
-  const int idx0 = static_cast<int>(blockIdx.x) / 8;
-  if (idx0 >= share || xcd * share + idx0 >= total) return;  // workgroup-uniform, before any barrier
-
-  const int64_t k = p.k;
-  const int64_t n_out = p.n;
-  const int64_t nb_rows = SWI ? 2 * n_out : n_out;  // weight rows per expert
-  const int nkt = static_cast<int>(k / BK);
-  // weight row of the item's local B row lr (SwiGLU: gate rows, then the matching up rows), clamped
-  auto weight_row = [&](int slice, int lr) -> int64_t {
-    if (SWI) {
-      int64_t oc = static_cast<int64_t>(slice) * (BN / 2) + lr % (BN / 2);
-      oc = oc < n_out ? oc : n_out - 1;
-      return lr < BN / 2 ? oc : n_out + oc;
-    }
-    const int64_t oc = static_cast<int64_t>(slice) * BN + lr;
-    return oc < n_out ? oc : n_out - 1;
-  };
-
-  // ---- load cursor: the item of the step being issued
-  int ld_idx = idx0, ld_kt = 0, ld_seq = 0;
-  bool ld_live = true;
-  __amdgpu_buffer_rsrc_t arsrc, brsrc, sarsrc, sbrsrc;
-  uint32_t voff[6], soff_lane;  // load q < 4: A rows (4 wave + q) * 8 ..; else B rows (2 wave + q - 4) * 8 ..
-  auto set_load_item = [&]() {
-    ld_live = ld_idx < share && xcd * share + ld_idx < total;  // workgroup-uniform
-    int e = 0, slice = 0;
-    int64_t rb = 0, re = 0;
-    if (ld_live) moe_find_item(off, ne, n_slices, xcd * share + ld_idx, lane, e, slice, rb, re);
-    const int64_t nrows = re - rb;
-    const int64_t wbase = p.shared_b ? 0 : static_cast<int64_t>(e) * nb_rows;
-    arsrc = mp_rsrc(p.a + rb * k, static_cast<uint32_t>(nrows * k));
-    brsrc = mp_rsrc(p.b + wbase * k, ld_live ? static_cast<uint32_t>(nb_rows * k) : 0u);
-    sarsrc = mp_rsrc(p.s_a + rb, static_cast<uint32_t>(nrows * 4));
-    sbrsrc = mp_rsrc(p.s_b + wbase, ld_live ? static_cast<uint32_t>(nb_rows * 4) : 0u);
-#pragma unroll
-    for (int q = 0; q < 6; ++q) {
-      const int r = (q < 4 ? (4 * wave + q) : (2 * wave + q - 4)) * 8 + lane / 8;
-      const int c = (lane & 7) ^ ((r >> 1) & 7);
-      voff[q] = q < 4 ? (r < nrows ? static_cast<uint32_t>(r * k + 16 * c) : kOob)
-                      : static_cast<uint32_t>(weight_row(slice, r) * k + 16 * c);
-    }
-    // scales: waves 0-3 the per-token scales of rows 64 wave + lane, waves 4-7 the scales of B rows
-    // 64 (wave & 1) + lane (waves 6-7 repeat waves 4-5: the same values to the same words)
-    if (wave < 4) soff_lane = 64 * wave + lane < nrows ? static_cast<uint32_t>(64 * wave + lane) * 4 : kOob;
-    else soff_lane = static_cast<uint32_t>(weight_row(slice, 64 * (wave & 1) + lane) * 4);
-  };
-  auto issue = [&](int stage) {
-    const uint32_t kb = static_cast<uint32_t>(ld_kt) * BK;
-    int8_t *st = ring + stage * kMdStage;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      md_lds_load(arsrc, st + (4 * wave + q) * 8 * BK, voff[q] == kOob ? kOob : voff[q] + kb, 16);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) md_lds_load(brsrc, st + BM * BK + (2 * wave + q) * 8 * BK, voff[4 + q] + kb, 16);
-    const bool first = ld_kt == 0 && ld_live;
-    const int par = ld_seq & 1;
-    if (wave < 4)
-      md_lds_load(sarsrc, first ? ssa + par * BM + 64 * wave : junk + 64 * wave, first ? soff_lane : kOob, 4);
-    else
-      md_lds_load(sbrsrc, first ? ssc + par * BN + 64 * (wave & 1) : junk + 64 * wave, first ? soff_lane : kOob, 4);
-    if (++ld_kt == nkt) {
-      ld_kt = 0;
-      ld_idx += stride;
-      ++ld_seq;
-      set_load_item();
-    }
-  };
-
-  // ---- compute cursor
-  int c_idx = idx0, c_seq = 0, c_kt = 0;
-  int c_slice = 0;
-  int64_t c_rb = 0, c_re = 0;
-  bool mact0 = false, mact1 = false;  // the wave's tiles 0 (rows 32 wr ..) and 1 (rows 128 + 32 wr ..) multiply
-  auto set_compute_item = [&]() {
-    int e;
-    moe_find_item(off, ne, n_slices, xcd * share + c_idx, lane, e, c_slice, c_rb, c_re);
-    mact0 = c_rb + 32 * wr < c_re;
-    mact1 = c_rb + 128 + 32 * wr < c_re;
-  };
-  i16_t acc[2][2];
-  auto clear = [&]() {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-  };
-  const int swz = (lane >> 1) & 7, half = lane >> 5;
-  int arow_l[2], brow_l[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) arow_l[i] = (32 * wr + 128 * i + (lane & 31)) * BK;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int lr = SWI ? (j * (BN / 2) + wn * 32 + (lane & 31)) : (wn * 64 + j * 32 + (lane & 31));
-    brow_l[j] = BM * BK + lr * BK;
-  }
-  auto mma = [&](int stage, auto ta_tag) {
-    constexpr int TA = decltype(ta_tag)::value;
-    const int8_t *st = ring + stage * kMdStage;
-    i4_t af[4][TA], bf[4][2];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int sl = 16 * ((2 * ks + half) ^ swz);
-#pragma unroll
-      for (int i = 0; i < TA; ++i) af[ks][i] = *reinterpret_cast<const i4_t *>(st + arow_l[i] + sl);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(st + brow_l[j] + sl);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int i = 0; i < TA; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
-  };
-
-  set_load_item();
-  set_compute_item();
-  clear();
-  issue(0);
-  issue(1);
-  int cs = 0;  // stage of the step being multiplied
-  while (true) {
-    // own loads of this step landed (the next step's seven may remain) and own reads of the stage
-    // refilled next are done, then the barrier makes both hold for every wave
-    asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    issue(cs == 0 ? 2 : cs - 1);
-    if (mact1) mma(cs, std::integral_constant<int, 2>{});
-    else if (mact0) mma(cs, std::integral_constant<int, 1>{});
-    cs = cs == S - 1 ? 0 : cs + 1;
-    if (++c_kt == nkt) {
-      if (mact0)
-        moe_item_epilogue<EPI>(p, acc, lane, wr, wn, c_slice, c_rb, c_re, ssa + (c_seq & 1) * BM,
-                               ssc + (c_seq & 1) * BN);
-      c_kt = 0;
-      ++c_seq;
-      c_idx += stride;
-      if (!(c_idx < share && xcd * share + c_idx < total)) break;  // workgroup-uniform
-      set_compute_item();
-      clear();
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS DMA outstanding at exit
-}
-
-// ------------------------------------------------------------------ weight-streaming grouped GEMM
-// Expert-grouped int8 GEMM (GEMM1 + SwiGLU, GEMM2 with fp32 outputs) whose weights go from HBM straight
-// into the matrix cores: no LDS round trip for the weight operand, so each wave's weight loads stay
-// in flight while the matrix cores run and the expert weights stream at the read rate of the box.
-//  * Work item: up to 256 routed rows of one expert (a 256-row chunk) against a slice of weight rows:
-//    SwiGLU 64 output columns (wave w: gate rows 16 w .. 16 w + 15 of the slice and the matching up
-//    rows), fp32 128 output columns (wave w: 32 weight rows).  Four waves, one per SIMD; items are
-//    numbered expert-major with the row chunk fastest and walked XCD-major (as i8_moe_kernel), the
-//    launch persistent.
-//  * K steps of 128 bytes.  The weight operand of v_mfma_i32_32x32x32_i8 comes from four 16-byte loads
-//    per lane per step: lane l reads bytes 64 (l / 32) + 16 j of its weight row (l % 32), and slice j of
-//    the step is the B operand of MFMA j.  That is a permutation of K; the activations are read under
-//    the same permutation (chunk 4 (l / 32) + j of the row), and int32 sums do not depend on the order.
-//  * Activations: the chunk's 256 rows x 128 bytes of a step go to an LDS ring of four stages by direct
-//    loads (buffer_load ... lds; rows past the chunk read as zeros, without memory traffic); the 16-byte
-//    chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the fragment reads are conflict-free.
-//  * A step multiplies the chunk's first four 32-row tiles (chunks of up to 128 rows) or all eight;
-//    rows past the chunk are zeros and their results are dropped.
-//  * Pipeline: three steps in flight.  Step g waits for its own loads, passes a barrier (every wave's
-//    activation loads of step g are in LDS, every read of the stage refilled next is done), issues the
-//    loads of step g + 3 (possibly of the next item: load and compute cursors are separate), then runs
-//    its MFMAs.  A step issues the same loads on every path (those past the last item read nothing),
-//    so one vmcnt wait fits all.
-//  * Epilogue at an item's last step, while the next item's first steps are in flight: the per-token
-//    and weight-row scales were copied to LDS by the item's first loads.  SwiGLU: lane l (l % 32 < 16)
-//    pairs its gate column with the up column of lane l ^ 16 and writes h = silu(g) * u (fp32) with
-//    g = (acc * s_tok) * s_gate, u = (acc * s_tok) * s_up (the arithmetic of i8_moe_kernel); the abs-max
-//    of each row over the wave's 16 columns goes to amax_partial[row][4 * slice + wave].  fp32: y =
-//    (acc * s_tok) * s_b.
-constexpr int kMsBM = 256, kMsBK = 128, kMsInFlight = 3, kMsRing = kMsInFlight + 1, kMsThreads = 256;
-constexpr int kMsMaxExperts = 1024;
-constexpr size_t kMsStage = static_cast<size_t>(kMsBM) * kMsBK;  // 32 KB
-// LDS: the activation ring; per-token scales [2][256] and weight-row scales [2][4 waves][64] (by item
-// parity); the group offsets
-constexpr size_t kMsSmem = kMsRing * kMsStage + (2 * kMsBM + 2 * 4 * 64) * sizeof(float) +
-                           (kMsMaxExperts + 1) * sizeof(int64_t);
-
-__device__ __forceinline__ void ms_lds_load16(__amdgpu_buffer_rsrc_t r, void *lds_wave_base, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      r, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds_wave_base)), 16,
-      voff, 0, 0, 0);
-}
-__device__ __forceinline__ void ms_lds_load4(__amdgpu_buffer_rsrc_t r, void *lds_wave_base, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      r, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds_wave_base)), 4,
-      voff, 0, 0, 0);
-}
-
-template <int EPI>
-__global__ __launch_bounds__(kMsThreads) void i8_moe_stream_kernel(mp_i8_args p, int n_slices) {
-  constexpr bool SWI = EPI == MP_EPI_SWIGLU;
-  constexpr int OUTC = SWI ? 64 : 128;          // output columns per item
-  constexpr uint32_t kOob = 0xFFFFFFF0u;        // a load offset past every buffer
-  extern __shared__ __attribute__((aligned(16))) int8_t smem_ms[];
-  int8_t *ring = smem_ms;                                                   // [kMsRing][256 x 128]
-  float *sca = reinterpret_cast<float *>(smem_ms + kMsRing * kMsStage);   // [2][256]
-  float *scb = sca + 2 * kMsBM;                                             // [2][4][64]
-  int64_t *soff = reinterpret_cast<int64_t *>(scb + 2 * 4 * 64);           // [E + 1]
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-  const int ne = p.n_experts;
-  for (int i = tid; i <= ne; i += kMsThreads) soff[i] = p.offsets[i];
-  mp_lds_barrier();
-  const int64_t *off = soff;
-  int total = 0;
-  for (int c0 = 0; c0 < ne; c0 += 64) {
-    int it = c0 + lane < ne ? moe_row_chunks(off, c0 + lane) * n_slices : 0;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) it += __shfl_xor(it, o, 64);
-    total += it;
-  }
-  total = __builtin_amdgcn_readfirstlane(total);
-  const int share = (total + 7) / 8;
-  const int xcd = static_cast<int>(blockIdx.x) % 8, stride = static_cast<int>(gridDim.x) / 8;
-  const int idx0 = static_cast<int>(blockIdx.x) / 8;
-  if (idx0 >= share || xcd * share + idx0 >= total) return;  // workgroup-uniform, before any later barrier
-
-  const int64_t k = p.k, n_out = p.n;
-  const int64_t nb_rows = SWI ? 2 * n_out : n_out;  // weight rows per expert
-  const int nkt = static_cast<int>(k / kMsBK);      // host: k % (kMsRing * kMsBK) == 0
-  const auto arsrc = mp_rsrc(p.a, static_cast<uint32_t>(p.rows * k));
-  const auto brsrc = mp_rsrc(p.b, static_cast<uint32_t>(static_cast<int64_t>(ne) * nb_rows * k));
-  const auto sarsrc = mp_rsrc(p.s_a, static_cast<uint32_t>(p.rows * 4));
-  const auto sbrsrc = mp_rsrc(p.s_b, static_cast<uint32_t>(static_cast<int64_t>(ne) * nb_rows * 4));
-  const int hl = lane & 31, hh = lane >> 5;
-
-  // ---- load cursor: item of the steps being issued
-  int ld_idx = idx0, ld_kt = 0, ld_seq = 0;
-  bool ld_live = true;
-  uint32_t a_voff[8];   // activation piece q of this thread: row 32 q + tid / 8, chunk (tid % 8) ^ swizzle
-  uint32_t b_voff;      // weight row of this lane, byte 64 hh of the step
-  auto set_load_item = [&]() {
-    int e, slice;
-    int64_t rb, re;
-    ld_live = ld_idx < share && xcd * share + ld_idx < total;
-    if (ld_live) {
-      moe_find_item(off, ne, n_slices, xcd * share + ld_idx, lane, e, slice, rb, re);
-    } else {
-      e = 0; slice = 0; rb = 0; re = 0;
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int r = 32 * q + tid / 8;
-      const int c = (tid & 7) ^ ((r >> 1) & 7);
-      a_voff[q] = rb + r < re ? static_cast<uint32_t>((rb + r) * k + 16 * c) : kOob;
-    }
-    int64_t wrow;
-    if (SWI) {
-      int64_t oc = static_cast<int64_t>(slice) * OUTC + wave * 16 + (hl & 15);
-      oc = oc < n_out ? oc : n_out - 1;
-      wrow = hl < 16 ? oc : n_out + oc;
-    } else {
-      int64_t oc = static_cast<int64_t>(slice) * OUTC + wave * 32 + hl;
-      wrow = oc < n_out ? oc : n_out - 1;
-    }
-    const int64_t gb = static_cast<int64_t>(e) * nb_rows + wrow;
-    b_voff = ld_live ? static_cast<uint32_t>(gb * k + 64 * hh) : kOob;
-    // the item's scales, into the LDS buffers of its parity (read by its epilogue)
-    const int par = ld_seq & 1;
-    const uint32_t sa_off = ld_live && rb + 64 * wave + lane < re ? static_cast<uint32_t>((rb + 64 * wave + lane) * 4) : kOob;
-    ms_lds_load4(sarsrc, sca + par * kMsBM + 64 * wave, sa_off);
-    ms_lds_load4(sbrsrc, scb + (par * 4 + wave) * 64, ld_live ? static_cast<uint32_t>(gb * 4) : kOob);
-  };
-  auto issue = [&](int slot_lds, i4_t (&b)[4]) {
-    const uint32_t kb = static_cast<uint32_t>(ld_kt) * kMsBK;
-    int8_t *stage = ring + slot_lds * kMsStage;
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      ms_lds_load16(arsrc, stage + q * 4096 + wave * 1024, a_voff[q] == kOob ? kOob : a_voff[q] + kb);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      b[j] = mp_buf_load16i(brsrc, b_voff == kOob ? kOob : b_voff + kb + 16 * j, 0);
-    if (++ld_kt == nkt) {
-      ld_kt = 0;
-      ld_idx += stride;
-      ++ld_seq;
-      set_load_item();
-    }
-  };
-
-  // ---- compute cursor
-  int cp_idx = idx0, cp_seq = 0;
-  int cp_slice = 0;
-  bool cp_ta4 = true;  // the chunk holds at most 128 rows: four row tiles
-  int64_t cp_rb = 0, cp_re = 0;
-  auto set_compute_item = [&]() {
-    int e;
-    moe_find_item(off, ne, n_slices, xcd * share + cp_idx, lane, e, cp_slice, cp_rb, cp_re);
-    cp_ta4 = cp_re - cp_rb <= 128;
-  };
-
-  i16_t acc[8];
-#pragma unroll
-  for (int t = 0; t < 8; ++t)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[t][r] = 0;
-  // activation fragment of slice j: row hl (+ 32 t), chunk 4 hh + j, swizzled
-  const int afrag = hl * kMsBK + (((4 * hh) ^ ((hl >> 1) & 7)) * 16);
-  // one K step over the item's first TA row tiles (TA = 4: chunks of up to 128 rows): the fragments
-  // of slice j + 1 are read while slice j is multiplied
-  auto compute = [&](int slot_lds, const i4_t (&b)[4], auto ta_tag) {
-    constexpr int TA = decltype(ta_tag)::value;
-    const int8_t *stage = ring + slot_lds * kMsStage;
-    i4_t af[2][TA];
-#pragma unroll
-    for (int t = 0; t < TA; ++t) af[0][t] = *reinterpret_cast<const i4_t *>(stage + t * 32 * kMsBK + afrag);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < 3) {
-#pragma unroll
-        for (int t = 0; t < TA; ++t)
-          af[(j + 1) & 1][t] = *reinterpret_cast<const i4_t *>(stage + t * 32 * kMsBK + (afrag ^ (16 * (j + 1))));
-      }
-#pragma unroll
-      for (int t = 0; t < TA; ++t)
-        acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[j & 1][t], b[j], acc[t], 0, 0, 0);
-      if (j < 3) {
-        // interleave the next slice's reads with this slice's MFMAs
-#pragma unroll
-        for (int t = 0; t < TA; ++t) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        }
-      }
-    }
-  };
-  auto epilogue = [&](auto ta_tag) {
-    constexpr int TA = decltype(ta_tag)::value;
-    constexpr uint32_t kOobS = 0x80000000u;
-    const int par = cp_seq & 1;
-    const uint32_t nrows = static_cast<uint32_t>(cp_re - cp_rb);
-    // opaque here: the per-element offsets below stay in the epilogue instead of being hoisted out
-    // of the K loop into registers the loop needs
-    uint32_t ldy = static_cast<uint32_t>(p.ldy);
-    int hhv = hh;
-    asm volatile("" : "+s"(ldy), "+v"(hhv));
-    const float sbv = scb[(par * 4 + wave) * 64 + hl];
-    if (SWI) {
-      const float su = __shfl_xor(sbv, 16, 64);  // lane l ^ 16 holds the matching up row's scale
-      const int64_t col = static_cast<int64_t>(cp_slice) * OUTC + wave * 16 + (hl & 15);
-      const bool cval = hl < 16 && col < n_out;
-      const __amdgpu_buffer_rsrc_t hr = mp_rsrc(static_cast<float *>(p.y) + cp_rb * p.ldy, nrows * ldy * 4);
-      const uint32_t np = static_cast<uint32_t>(p.n_partial);
-      const __amdgpu_buffer_rsrc_t pr = mp_rsrc(p.amax_partial + cp_rb * p.n_partial, nrows * np * 4);
-      const uint32_t cbase = cval ? static_cast<uint32_t>(col) * 4 : kOobS;
-#pragma unroll
-      for (int t = 0; t < TA; ++t) {
-        float v[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int lm = 32 * t + 8 * (r >> 2) + 4 * hhv + (r & 3);
-          const float sa = sca[par * kMsBM + lm];
-          const int up_acc = __shfl_xor(acc[t][r], 16, 64);
-          const float gv = mp_mul(mp_mul(static_cast<float>(acc[t][r]), sa), sbv);
-          const float uv = mp_mul(mp_mul(static_cast<float>(up_acc), sa), su);
-          const float h = mp_swiglu_epi(gv, uv, kRoundNone);  // host: runtime rule only
-          mp_buf_store4(hr, cbase + static_cast<uint32_t>(lm) * ldy * 4, __float_as_uint(h));
-          v[r] = (cval && static_cast<uint32_t>(lm) < nrows) ? fabsf(h) : 0.f;
-        }
-        // transposing max butterfly over the 16 gate lanes of each half: lane hl < 16 ends with the
-        // maximum of row value hl
-#pragma unroll
-        for (int bb = 8; bb >= 1; bb >>= 1) {
-          const bool hi = (lane & bb) != 0;
-#pragma unroll
-          for (int q = 0; q < bb; ++q) {
-            const float send = hi ? v[q] : v[q + bb];
-            const float keep = hi ? v[q + bb] : v[q];
-            v[q] = fmaxf(keep, __shfl_xor(send, bb, 64));
-          }
-        }
-        const int lm = 32 * t + 8 * ((hl & 15) >> 2) + 4 * hhv + (hl & 3);
-        mp_buf_store4(pr, hl < 16 ? (static_cast<uint32_t>(lm) * np + static_cast<uint32_t>(cp_slice * 4 + wave)) * 4
-                                  : kOobS,
-                      __float_as_uint(v[0]));
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    } else {
-      const int64_t col = static_cast<int64_t>(cp_slice) * OUTC + wave * 32 + hl;
-      const uint32_t cbase = col < n_out ? static_cast<uint32_t>(col) * 4 : kOobS;
-      const __amdgpu_buffer_rsrc_t yr = mp_rsrc(static_cast<float *>(p.y) + cp_rb * p.ldy, nrows * ldy * 4);
-#pragma unroll
-      for (int t = 0; t < TA; ++t) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int lm = 32 * t + 8 * (r >> 2) + 4 * hhv + (r & 3);
-          const float vv = mp_mul(mp_mul(static_cast<float>(acc[t][r]), sca[par * kMsBM + lm]), sbv);
-          mp_buf_store4(yr, cbase + static_cast<uint32_t>(lm) * ldy * 4, __float_as_uint(vv));
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[t][r] = 0;
-  };
-
-  set_load_item();
-  set_compute_item();
-  i4_t breg[kMsRing][4];  // weight operand of step g in register set g % 4
-  issue(0, breg[0]);
-  issue(1, breg[1]);
-  issue(2, breg[2]);
-  // step g (ring slot and register set g % 4): wait for its loads (the 2 newer steps' 12 + 12 loads
-  // may remain, more at item starts), barrier, issue step g + 3 into slot (g + 3) % 4 (read at step
-  // g - 1), compute.  Four steps per trip keep the register sets fixed.
-  for (int g0 = 0;; g0 += kMsRing) {
-#pragma unroll
-    for (int u = 0; u < kMsRing; ++u) {
-      asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      issue((u + 3) % kMsRing, breg[(u + 3) % kMsRing]);
-      if (cp_ta4) compute(u, breg[u], std::integral_constant<int, 4>{});
-      else compute(u, breg[u], std::integral_constant<int, 8>{});
-    }
-    // items hold a multiple of kMsRing steps (host check): an item ends only here
-    if ((g0 + kMsRing) % nkt == 0) {
-      if (cp_ta4) epilogue(std::integral_constant<int, 4>{});
-      else epilogue(std::integral_constant<int, 8>{});
-      cp_idx += stride;
-      ++cp_seq;
-      if (!(cp_idx < share && xcd * share + cp_idx < total)) break;  // workgroup-uniform
-      set_compute_item();
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS load outstanding at exit
 }
 
 // ------------------------------------------------------------------ large-M dense GEMM
@@ -2520,79 +2018,8 @@ static int mp_launch_moe_d(const mp_i8_args &a, hipStream_t stream) {
   return MP_OK;
 }
 
-// Grouped GEMMs of i8_moe_kernel's shapes on the direct-to-LDS form i8_moe_dma_kernel: 1 = on, 0 = off
-// (MP_W8_MOE_DMA, for measurements).
-static int mp_moe_dma() {
-  static int v = [] {
-    const char *e = mp_knob("MP_W8_MOE_DMA");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
-
-template <int EPI>
-static int mp_launch_moe_dma(const mp_i8_args &a, hipStream_t stream) {
-  const int64_t n_slices = mp_cdiv(a.n, EPI == MP_EPI_SWIGLU ? kMoeBN / 2 : kMoeBN);
-  const int64_t items_ub = n_slices * (mp_cdiv(a.rows, kMoeBM) + a.n_experts);
-  if (items_ub > INT32_MAX / 2) return MP_ERR_SHAPE;
-  const int64_t cus = mp_cu_count() >= 8 ? mp_cu_count() / 8 * 8 : 256;
-  const int64_t wgs = mp_cdiv(items_ub, 8) * 8;
-  const dim3 grid(static_cast<unsigned>(wgs < cus ? wgs : cus));
-  if (hipFuncSetAttribute(reinterpret_cast<const void *>(i8_moe_dma_kernel<EPI>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMdSmem)) != hipSuccess)
-    return MP_ERR_HIP;
-  hipLaunchKernelGGL((i8_moe_dma_kernel<EPI>), grid, dim3(kMoeThreads), kMdSmem, stream, a, static_cast<int>(n_slices));
-  MP_CHECK_LAUNCH();
-  return MP_OK;
-}
-
-// Grouped GEMMs on the weight-streaming kernel (i8_moe_stream_kernel): 1 = on, 0 = off (default)
-// (MP_W8_MOE_STREAM, for measurements).
-static int mp_moe_stream() {
-  static int v = [] {
-    const char *e = mp_knob("MP_W8_MOE_STREAM");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
-
-bool mp_moe_stream_takes(const mp_i8_args &a, int epilogue) {
-  if (!mp_moe_stream() || !a.offsets || a.shared_b) return false;
-  if (epilogue != MP_EPI_SWIGLU && epilogue != MP_EPI_F32) return false;
-  if (epilogue == MP_EPI_SWIGLU && a.epi_round != kRoundNone) return false;  // the runtime rule only
-  if (a.k <= 0 || a.k % (kMsRing * kMsBK) != 0 || a.n_experts <= 0 || a.n_experts > kMsMaxExperts) return false;
-  if (a.rows > static_cast<int64_t>(kMsBM) * a.n_experts) return false;  // experts averaging <= 256 rows
-  if (!mp_aligned(a.a, 16) || !mp_aligned(a.b, 16) || a.ldy > (int64_t(1) << 21)) return false;
-  const int64_t nb_rows = epilogue == MP_EPI_SWIGLU ? 2 * a.n : a.n;
-  return a.rows * a.k < (int64_t(1) << 32) && static_cast<int64_t>(a.n_experts) * nb_rows * a.k < (int64_t(1) << 32) &&
-         static_cast<int64_t>(a.n_experts) * nb_rows * 4 < (int64_t(1) << 32);
-}
-
-template <int EPI>
-static int mp_launch_moe_stream(const mp_i8_args &a, hipStream_t stream) {
-  const int64_t n_slices = mp_cdiv(a.n, EPI == MP_EPI_SWIGLU ? 64 : 128);
-  if (EPI == MP_EPI_SWIGLU && a.n_partial < 4 * n_slices) return MP_ERR_ARG;
-  const int64_t items_ub = n_slices * (mp_cdiv(a.rows, kMsBM) + a.n_experts);
-  if (items_ub > INT32_MAX / 2) return MP_ERR_SHAPE;
-  const int64_t cus = mp_cu_count() >= 8 ? mp_cu_count() / 8 * 8 : 256;
-  const int64_t wgs = mp_cdiv(items_ub, 8) * 8;
-  const dim3 grid(static_cast<unsigned>(wgs < cus ? wgs : cus));
-  if (hipFuncSetAttribute(reinterpret_cast<const void *>(i8_moe_stream_kernel<EPI>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMsSmem)) != hipSuccess)
-    return MP_ERR_HIP;
-  hipLaunchKernelGGL((i8_moe_stream_kernel<EPI>), grid, dim3(kMsThreads), kMsSmem, stream, a,
-                     static_cast<int>(n_slices));
-  MP_CHECK_LAUNCH();
-  return MP_OK;
-}
-
 template <int EPI>
 static int mp_launch_moe(const mp_i8_args &a, hipStream_t stream) {
-  // the direct-to-LDS form: two or more K steps per item, each expert's weight under 4 GiB (one
-  // buffer descriptor)
-  const int64_t nb_rows = EPI == MP_EPI_SWIGLU ? 2 * a.n : a.n;
-  if (mp_moe_dma() && a.k >= 2 * kMoeBK && nb_rows * a.k < (int64_t(1) << 32))
-    return mp_launch_moe_dma<EPI>(a, stream);
   if (mp_moe_kernel() == 2) return mp_launch_moe_d<EPI, 2>(a, stream);
   return mp_launch_moe_d<EPI, 1>(a, stream);
 }
@@ -2604,11 +2031,6 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
   const bool aligned = mp_aligned(a.a, 16) && mp_aligned(a.b, 16) && a.ldy < (int64_t(1) << 23) &&
                        a.k < (int64_t(1) << 23);
   if (a.offsets) {
-    // expert weights streamed straight into the matrix cores (SwiGLU and fp32 outputs)
-    if (mp_moe_stream_takes(a, epilogue)) {
-      if (epilogue == MP_EPI_SWIGLU) return mp_launch_moe_stream<MP_EPI_SWIGLU>(a, stream);
-      return mp_launch_moe_stream<MP_EPI_F32>(a, stream);
-    }
     // experts of a few hundred rows (serving-size MoE): one workgroup per 256 rows of an
     // expert and weight slice, so each slice streams once per expert
     if (mp_moe_kernel() && aligned && a.k % kMoeBK == 0 && a.k <= (1 << 17) && a.n_experts <= kMoeMaxExperts &&
