@@ -1720,27 +1720,40 @@ __global__ __launch_bounds__(512) void i8_gemm_dma_kernel(mp_i8_args p, int tile
     big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
 }
 
-// Mid-M dense GEMM with direct global->LDS loads: a 128x128 output tile per workgroup of
-// four waves (2 x 2, each 64x64 from 2 x 2 MFMA i32_32x32x32_i8 tiles), 128-byte K steps,
-// four LDS stages of 32 KB (A rows 0..127, then B rows 0..127, 128 bytes each).  Tile kt+3
-// is loaded straight into stage (kt+3) % 4 while tile kt is multiplied: three K tiles
-// (96 KB) in flight per workgroup with no staging registers and no LDS store
-// instructions.  A load instruction fills 1 KB (8 rows x 128 B, lane l at byte 16 l);
-// chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the 16 lanes of a ds_read_b128
-// quarter (16 rows, one logical chunk) hit 16 distinct 16-byte bank groups.  One barrier
-// per step: after it every wave's loads of tile kt have landed and every read of the
-// stage refilled next is done.  The grid is 1-D: the row tiles of a column tile run on
-// one XCD (blocks x and x + 8 ...), so their shared weight rows come from that XCD's L2.
+// Mid-M dense GEMM with direct global->LDS loads: a 128 x BN output tile per workgroup of four
+// waves (BN = 128: 2 x 2 waves of 64x64; BN = 96: 4 x 1 waves of 32x96; MFMA i32_32x32x32_i8
+// tiles), 128-byte K steps, four LDS stages (A rows 0..127, then B rows 0..BN-1, 128 bytes each).
+// Tile kt+3 is loaded straight into stage (kt+3) % 4 while tile kt is multiplied: three K tiles in
+// flight per workgroup with no staging registers and no LDS store instructions.  A load instruction
+// fills 1 KB (8 rows x 128 B, lane l at byte 16 l); chunk c of row r sits at slot c ^ ((r >> 1) & 7),
+// so the 16 lanes of a ds_read_b128 quarter (16 rows, one logical chunk) hit 16 distinct 16-byte bank
+// groups.  One barrier per step: after it every wave's loads of tile kt have landed and every read of
+// the stage refilled next is done.  The grid is 1-D: the row tiles of a column tile run on one XCD
+// (blocks x and x + 8 ...), so their shared weight rows come from that XCD's L2.  BN = 96 gives a
+// launch more tiles (more CUs streaming) for a quarter less weight per tile.
 constexpr int kMidStages = 4, kMidBK = 128;
-constexpr size_t kMidSmem = static_cast<size_t>(kMidStages) * 256 * kMidBK;
+constexpr size_t mid_smem(int bn) { return static_cast<size_t>(kMidStages) * (128 + bn) * kMidBK; }
 
-template <int OUT_DT>
+// 16 bytes per lane from a buffer into LDS (lane l at byte 16 l of the wave-uniform lds address).  The
+// cast to an LDS pointer stays in this non-template function: inside a kernel template, with an operand
+// that depends on a template parameter, it makes the host pass drop the kernel's launch stub.
+__device__ __forceinline__ void mid_lds_load16(__amdgpu_buffer_rsrc_t r, int8_t *lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds)), 16, voff, 0, 0,
+      0);
+}
+
+template <int OUT_DT, int BN>
 __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) {
-  constexpr int BM = 128, BN = 128, BK = kMidBK, TM = 2, TN = 2, S = kMidStages;
+  constexpr int BM = 128, BK = kMidBK, S = kMidStages;
+  constexpr int WN = BN == 128 ? 2 : 1, WM = 4 / WN;  // waves along M and N
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // 32x32 tiles per wave
+  constexpr int QW = (BM + BN) / 8 / 4;                // load instructions per wave per stage
   constexpr int STAGE = (BM + BN) * BK;
+  static_assert((BN == 128 || BN == 96) && (BM + BN) % 32 == 0, "tile shapes");
   extern __shared__ __attribute__((aligned(16))) int8_t smem_mid[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int bx = static_cast<int>(blockIdx.x);
   const int tile_n = (bx / (8 * tiles_m)) * 8 + (bx & 7);
   const int64_t m0 = static_cast<int64_t>((bx >> 3) % tiles_m) * BM;
@@ -1748,21 +1761,22 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
   if (n0 >= p.n || m0 >= p.rows) return;  // grid padding; workgroup-uniform, before any barrier
   const int64_t k = p.k;
 
-  // load instruction q (0..7) of this wave: q < 4 -> A rows (4 wave + q) * 8 .. + 8, else B rows
-  // (4 wave + q - 4) * 8 .. + 8.  Lane l: row + l / 8, slot l % 8, global chunk slot ^ ((row >> 1) & 7).
-  // Through buffer descriptors over the tile's valid A and B rows: a row past M or N sits past its
-  // descriptor, reads zeros and moves no memory (the epilogue drops its outputs).  The launcher
-  // bounds K below 2^23, so 128 K bytes of rows and the 0x80000000 dead offset stay apart.
+  // load instruction q of this wave fills 8-row group g = 4 q + wave of the stage: q < 4 (g < 16) -> A
+  // rows 8 g .. + 8, else B rows 8 (g - 16) .. + 8.  Lane l: row + l / 8, slot l % 8, global chunk
+  // slot ^ ((row >> 1) & 7).  Through buffer descriptors over the tile's valid A and B rows: a row
+  // past M or N sits past its descriptor, reads zeros and moves no memory (the epilogue drops its
+  // outputs).  The launcher bounds K below 2^23, so 128 K bytes of rows and the 0x80000000 dead
+  // offset stay apart.
   constexpr uint32_t kOob = 0x80000000u;
   const int64_t a_rows = p.rows - m0 < BM ? p.rows - m0 : BM, b_rows = p.n - n0 < BN ? p.n - n0 : BN;
   const __amdgpu_buffer_rsrc_t arsrc = mp_rsrc(p.a + m0 * k, static_cast<uint32_t>(a_rows * k));
   const __amdgpu_buffer_rsrc_t brsrc = mp_rsrc(p.b + n0 * k, static_cast<uint32_t>(b_rows * k));
-  uint32_t voff[8];
-  int ldst[8];
+  uint32_t voff[QW];
+  int ldst[QW];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const bool is_a = q < 4;
-    const int r0 = (4 * wave + (q & 3)) * 8;
+  for (int q = 0; q < QW; ++q) {
+    const bool is_a = q < BM / 32;
+    const int r0 = (4 * q + wave - (is_a ? 0 : BM / 8)) * 8;
     const int r = r0 + lane / 8;
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     voff[q] = r < (is_a ? a_rows : b_rows) ? static_cast<uint32_t>(r * k + 16 * c) : kOob;
@@ -1771,12 +1785,9 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
   auto issue = [&](int64_t kt, int stage) {
     const uint32_t kb = static_cast<uint32_t>(kt * BK);
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          q < 4 ? arsrc : brsrc,
-          reinterpret_cast<__attribute__((address_space(3))) void *>(
-              reinterpret_cast<uintptr_t>(smem_mid + stage * STAGE + ldst[q])),
-          16, voff[q] == kOob ? kOob : voff[q] + kb, 0, 0, 0);
+    for (int q = 0; q < QW; ++q)
+      mid_lds_load16(q < BM / 32 ? arsrc : brsrc, smem_mid + stage * STAGE + ldst[q],
+                     voff[q] == kOob ? kOob : voff[q] + kb);
   };
 
   i16_t acc[TM][TN];
@@ -1790,8 +1801,8 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
   // 2 ks + l / 32, stored at slot (2 ks + l / 32) ^ ((l >> 1) & 7) (the tile's first row is a multiple
   // of 32, so the row's swizzle is that of l % 32)
   const int swz = (lane >> 1) & 7, half = lane >> 5;
-  const int arow = (wm * 64 + (lane & 31)) * BK;
-  const int brow = BM * BK + (wn * 64 + (lane & 31)) * BK;
+  const int arow = (wm * TM * 32 + (lane & 31)) * BK;
+  const int brow = BM * BK + (wn * TN * 32 + (lane & 31)) * BK;
   auto compute = [&](int stage) {
     const int8_t *st = smem_mid + stage * STAGE;
     i4_t af[4][TM], bf[4][TN];
@@ -1811,12 +1822,12 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
     // the fragments of K pieces ks + 1 (and 1 for ks = 0) are read while the MFMAs of piece ks run
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TM + TN), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * TM * TN, 0);
   };
 
   const int64_t nkt = k / BK;
@@ -1824,13 +1835,15 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
   issue(0, 0);
   issue(kc(1), 1);
   issue(kc(2), 2);
-  // step kt: own loads of tile kt done (16 newer load instructions may remain), barrier, refill
+  // step kt: own loads of tile kt done (2 QW newer load instructions may remain), barrier, refill
   // the stage read in step kt-1, compute.  Loads past the last tile re-read it (never used).
   for (int64_t kt0 = 0; kt0 < nkt; kt0 += S) {
 #pragma unroll
     for (int u = 0; u < S; ++u) {
       if (kt0 + u < nkt) {  // workgroup-uniform
-        asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if constexpr (QW == 8) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(14) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        static_assert(QW == 8 || QW == 7, "the wait counts two stages of loads");
         issue(kc(kt0 + u + 3), (u + 3) % S);
         compute(u);
       }
@@ -1838,7 +1851,8 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS DMA outstanding at exit
 
-  big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * 64 + 4 * (lane >> 5), n0 + wn * 64, m0 + BM <= p.rows, lane);
+  big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * TM * 32 + 4 * (lane >> 5), n0 + wn * TN * 32, m0 + BM <= p.rows,
+                               lane);
 }
 
 // Any-shape dense fallback: one thread per output.
@@ -1960,11 +1974,12 @@ static int mp_tiled_staged_ok(const mp_i8_args &a, int epilogue) {
 
 // Dense GEMMs below the large-M range on the direct-to-LDS mid-M kernel when its 128x128 tiles number
 // from 64 to three quarters of the CUs (MP_W8_MID=0 keeps the register-staged tiled kernel, for
-// measurements).  Measured at K = 4096 against the tiled kernel: M = 256 / 128, N = 11008 (172 / 86
-// tiles) 27.3 / 25.5 against 32.1 / 29.9 us; M = 256 / 512, N = 4096 (64 / 128 tiles) 21.5 / 23.4
-// against 28.3 / 30.8 us; M = 48 / 64 / 200 level with it (+-1 us).  With 32 tiles (M = 96, N = 4096)
-// it is slower (30 against 28 us), at 256 tiles (M = 1000, N = 4096) 34.0 against 33.0 us, and beyond
-// one tile per CU (M = 384 .. 1000, N = 11008) the tiled kernel's two workgroups per CU win.
+// measurements).  Measured at K = 4096 against the tiled kernel, with 128-column tiles: M = 256 / 128,
+// N = 11008 (172 / 86 tiles) 27.3 / 25.5 against 32.1 / 29.9 us; M = 256 / 512, N = 4096 (64 / 128
+// tiles) 21.5 / 23.4 against 28.3 / 30.8 us; M = 48 / 64 / 200 level with it (+-1 us), and faster with
+// 96-column tiles (mp_mid_bn).  With 32 tiles (M = 96, N = 4096) it is slower (30 against 28 us), at
+// 256 tiles (M = 1000, N = 4096) 34.0 against 33.0 us, and beyond one tile per CU (M = 384 .. 1000,
+// N = 11008) the tiled kernel's two workgroups per CU win.
 static int mp_mid_kernel() {
   static int v = [] {
     const char *e = mp_knob("MP_W8_MID");
@@ -1973,11 +1988,20 @@ static int mp_mid_kernel() {
   return v;
 }
 
-static bool mp_mid_takes(const mp_i8_args &a) {
+// The mid-M kernel's tile width for a launch, or 0 when it does not take it.  MP_W8_MID_BN=96 / 128
+// forces the width (for measurements).
+static int mp_mid_bn(const mp_i8_args &a) {
   const int64_t tiles = mp_cdiv(a.n, 128) * mp_cdiv(a.rows, 128);
   const int64_t cus = mp_cu_count() > 0 ? mp_cu_count() : 256;
-  return mp_mid_kernel() && a.k >= kMidBK && a.k % kMidBK == 0 && a.k < (int64_t(1) << 23) && tiles >= 64 &&
-         4 * tiles <= 3 * cus;
+  if (!(mp_mid_kernel() && a.k >= kMidBK && a.k % kMidBK == 0 && a.k < (int64_t(1) << 23) && tiles >= 64 &&
+        4 * tiles <= 3 * cus))
+    return 0;
+  static const int forced = mp_knob("MP_W8_MID_BN") ? atoi(mp_knob("MP_W8_MID_BN")) : 0;
+  if (forced == 96 || forced == 128) return forced;
+  // 96-column tiles where they still fit one per CU: measured at K = 4096 against 128-column ones,
+  // M = 256 / 128 / 64, N = 11008 25.2 / 22.5 / 25.9 against 27.2 / 25.5 / 29.5 us; M = 200, N = 8192
+  // 24.6 against 29.6 us; M = 256 / 512, N = 4096 18.8 / 20.1 against 21.9 / 24.1 us
+  return mp_cdiv(a.n, 96) * mp_cdiv(a.rows, 128) <= cus ? 96 : 128;
 }
 
 // Persistent large-M launch (MP_W8_PERSIST=0 turns it off, for measurements).
@@ -2198,23 +2222,30 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
       else
         hipLaunchKernelGGL((i8_gemm_big_kernel<MP_F32, MP_EPI_DENSE>), pgrid, dim3(kBigThreads), smem, stream, am, tiles_m, tiles_n);
     }
-  } else if (aligned && epilogue == MP_EPI_DENSE && mp_mid_takes(a)) {
-    const int64_t tn = mp_cdiv(a.n, 128), tm = mp_cdiv(a.rows, 128);
+  } else if (aligned && epilogue == MP_EPI_DENSE && mp_mid_bn(a) > 0) {
+    const int bn = mp_mid_bn(a);
+    const int64_t tn = mp_cdiv(a.n, bn), tm = mp_cdiv(a.rows, 128);
     const dim3 grid(static_cast<unsigned>(mp_cdiv(tn, 8) * 8 * tm));
-    const void *fk[3] = {reinterpret_cast<const void *>(i8_mid_kernel<MP_F16>),
-                         reinterpret_cast<const void *>(i8_mid_kernel<MP_BF16>),
-                         reinterpret_cast<const void *>(i8_mid_kernel<MP_F32>)};
-    for (const void *fn : fk)
-      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMidSmem)) !=
-          hipSuccess)
-        return MP_ERR_HIP;
     const int tmi = static_cast<int>(tm);
-    if (a.out_dtype == MP_F16)
-      hipLaunchKernelGGL((i8_mid_kernel<MP_F16>), grid, dim3(256), kMidSmem, stream, a, tmi);
-    else if (a.out_dtype == MP_BF16)
-      hipLaunchKernelGGL((i8_mid_kernel<MP_BF16>), grid, dim3(256), kMidSmem, stream, a, tmi);
-    else
-      hipLaunchKernelGGL((i8_mid_kernel<MP_F32>), grid, dim3(256), kMidSmem, stream, a, tmi);
+#define MP_MID(BN_)                                                                                          \
+  do {                                                                                                       \
+    const void *fk[3] = {reinterpret_cast<const void *>(i8_mid_kernel<MP_F16, BN_>),                         \
+                         reinterpret_cast<const void *>(i8_mid_kernel<MP_BF16, BN_>),                        \
+                         reinterpret_cast<const void *>(i8_mid_kernel<MP_F32, BN_>)};                        \
+    for (const void *fn : fk)                                                                                \
+      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mid_smem(BN_))) != \
+          hipSuccess)                                                                                        \
+        return MP_ERR_HIP;                                                                                   \
+    if (a.out_dtype == MP_F16)                                                                               \
+      hipLaunchKernelGGL((i8_mid_kernel<MP_F16, BN_>), grid, dim3(256), mid_smem(BN_), stream, a, tmi);       \
+    else if (a.out_dtype == MP_BF16)                                                                         \
+      hipLaunchKernelGGL((i8_mid_kernel<MP_BF16, BN_>), grid, dim3(256), mid_smem(BN_), stream, a, tmi);      \
+    else                                                                                                     \
+      hipLaunchKernelGGL((i8_mid_kernel<MP_F32, BN_>), grid, dim3(256), mid_smem(BN_), stream, a, tmi);       \
+  } while (0)
+    if (bn == 96) MP_MID(96);
+    else MP_MID(128);
+#undef MP_MID
   } else if (aligned && mp_tiled_variant(a.k, mp_cdiv(a.n, kTBN) * mp_cdiv(a.rows, kTBM)) > 0) {
     // several row tiles: a 1-D grid whose row tiles of one column tile share an XCD (mp_tiled_xcd)
     const int64_t tn = mp_cdiv(a.n, kTBN), tm = mp_cdiv(a.rows, kTBM);
