@@ -253,6 +253,131 @@ __global__ __launch_bounds__(NW * 64) void i8_skinny_kernel(mp_i8_args p, int cb
   }
 }
 
+// 16 bytes per lane from a buffer into LDS (lane l at byte 16 l of the wave-uniform lds address).  The
+// cast to an LDS pointer stays in this non-template function: inside a kernel template, with an operand
+// that depends on a template parameter, it makes the host pass drop the kernel's launch stub.
+__device__ __forceinline__ void mid_lds_load16(__amdgpu_buffer_rsrc_t r, int8_t *lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds)), 16, voff, 0, 0,
+      0);
+}
+
+// Skinny GEMM (M <= 32) with direct global->LDS loads: a workgroup of four waves per 16 NCT output
+// columns, each wave a contiguous quarter of K in 128-byte steps, streaming its activation rows (16 MT)
+// and the workgroup's weight rows (16 NCT) into a ring of three LDS stages of its own, two steps ahead,
+// by `buffer_load_dwordx4 ... lds` (lane l at byte 16 l of 8 rows x 128 B; chunk c of row r at slot
+// c ^ ((r >> 1) & 7)).  The rings are wave-private, so a step waits only for the wave's own loads and
+// LDS reads (no barrier in the K loop).  MFMA i32_16x16x64_i8 (A: activation row lane % 16, B: weight
+// row lane % 16, 16 bytes of a 64-byte K piece per lane).  Rows past M and N sit past their buffer
+// descriptors (zeros, no memory access).  The four waves' int32 sums meet in LDS; the epilogue is
+// i8_skinny_kernel's, so the outputs are the same bits.
+constexpr int kSdStages = 3;
+constexpr size_t skdma_smem(int mt, int nct) {
+  return static_cast<size_t>(4) * kSdStages * (16 * mt + 16 * nct) * 128;
+}
+
+template <int MT, int NCT>
+__global__ __launch_bounds__(256) void i8_skinny_dma_kernel(mp_i8_args p) {
+  constexpr int S = kSdStages, BK = 128;
+  constexpr int AR = 16 * MT, BR = 16 * NCT;                // activation / weight rows per stage
+  constexpr int QA = AR / 8, QB = BR / 8, QW = QA + QB;     // load instructions per stage
+  constexpr int STAGE = (AR + BR) * BK;
+  constexpr uint32_t kOob = 0x80000000u;
+  extern __shared__ __attribute__((aligned(16))) int8_t smem_sd[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int8_t *ring = smem_sd + wave * S * STAGE;
+  const int64_t k = p.k;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BR;
+  const int64_t b_rows = p.n - n0 < BR ? p.n - n0 : BR;
+  const __amdgpu_buffer_rsrc_t arsrc = mp_rsrc(p.a, static_cast<uint32_t>(p.rows * k));
+  const __amdgpu_buffer_rsrc_t brsrc = mp_rsrc(p.b + n0 * k, static_cast<uint32_t>(b_rows * k));
+  // this wave's K steps [s0, s1)
+  const int nkt = static_cast<int>(k / BK);
+  const int s0 = nkt * wave / 4, s1 = nkt * (wave + 1) / 4;
+  uint32_t voff[QW];
+#pragma unroll
+  for (int q = 0; q < QW; ++q) {
+    const bool is_a = q < QA;
+    const int r = (is_a ? q : q - QA) * 8 + lane / 8;
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    voff[q] = r < (is_a ? p.rows : b_rows) ? static_cast<uint32_t>(r * k + 16 * c) : kOob;
+  }
+  auto issue = [&](int step, int slot) {
+    const bool live = step < s1;
+    const uint32_t kb = static_cast<uint32_t>(step) * BK;
+#pragma unroll
+    for (int q = 0; q < QW; ++q)
+      mid_lds_load16(q < QA ? arsrc : brsrc, ring + slot * STAGE + (q < QA ? q * 8 : AR + (q - QA) * 8) * BK,
+                     live && voff[q] != kOob ? voff[q] + kb : kOob);
+  };
+  i4_t acc[NCT][MT];
+#pragma unroll
+  for (int j = 0; j < NCT; ++j)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[j][t] = i4_t{0, 0, 0, 0};
+  const int swz = (lane >> 1) & 7, kq = lane >> 4, row = lane & 15;
+  auto compute = [&](int slot) {
+    const int8_t *st = ring + slot * STAGE;
+    i4_t af[2][MT], bf[2][NCT];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int sl = 16 * ((4 * ks + kq) ^ swz);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) af[ks][t] = *reinterpret_cast<const i4_t *>(st + (16 * t + row) * BK + sl);
+#pragma unroll
+      for (int j = 0; j < NCT; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(st + (AR + 16 * j + row) * BK + sl);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < NCT; ++j)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          acc[j][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[ks][t], bf[ks][j], acc[j][t], 0, 0, 0);
+  };
+  issue(s0, 0);
+  issue(s0 + 1, 1);
+  int slot = 0;
+  for (int s = s0; s < s1; ++s) {
+    // own loads of step s landed (the next step's may remain) and own reads of the slot refilled next
+    // are done; the ring is this wave's alone
+    if constexpr (QW == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+    else if constexpr (QW == 6) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)" ::: "memory");
+    else if constexpr (QW == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+    else if constexpr (QW == 10) asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)" ::: "memory");
+    static_assert(QW >= 4 && QW <= 12 && QW % 2 == 0, "the wait counts one stage of loads");
+    issue(s + 2, slot == 0 ? 2 : slot - 1);
+    compute(slot);
+    slot = slot == S - 1 ? 0 : slot + 1;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS DMA outstanding past this point
+  mp_lds_barrier();                                 // every ring is done: reuse LDS for the sums
+  int *red = reinterpret_cast<int *>(smem_sd);      // [4][NCT * MT][4][64]
+#pragma unroll
+  for (int j = 0; j < NCT; ++j)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[((wave * NCT * MT + j * MT + t) * 4 + i) * 64 + lane] = acc[j][t][i];
+  mp_lds_barrier();
+  for (int o = tid; o < NCT * MT * 256; o += 256) {
+    const int jt = o >> 8, r = o & 255;
+    const int j = jt / MT, t = jt % MT;
+    const int l = r & 63, i = r >> 6;
+    int v = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v += red[((w * NCT * MT + jt) * 4 + i) * 64 + l];
+    const int64_t m = t * 16 + 4 * (l >> 4) + i;
+    const int64_t col = n0 + j * 16 + (l & 15);
+    if (m < p.rows && col < p.n) {
+      float yv = mp_mul(mp_mul(static_cast<float>(v), p.s_a[m]), p.s_b[col]);
+      if (p.bias) yv = mp_add(yv, mp_load_as_f32(p.bias, col, p.bias_dtype));
+      mp_store_from_f32(p.y, m * p.ldy + col, p.out_dtype, yv);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ GEMV (M <= 2)
 // A wave owns R weight rows over all of K.  In chunk j lane l covers K bytes
 // [1024 j + 16 l, +16), so each weight load reads 1 KB of one row contiguously
@@ -1734,15 +1859,6 @@ __global__ __launch_bounds__(512) void i8_gemm_dma_kernel(mp_i8_args p, int tile
 constexpr int kMidStages = 4, kMidBK = 128;
 constexpr size_t mid_smem(int bn) { return static_cast<size_t>(kMidStages) * (128 + bn) * kMidBK; }
 
-// 16 bytes per lane from a buffer into LDS (lane l at byte 16 l of the wave-uniform lds address).  The
-// cast to an LDS pointer stays in this non-template function: inside a kernel template, with an operand
-// that depends on a template parameter, it makes the host pass drop the kernel's launch stub.
-__device__ __forceinline__ void mid_lds_load16(__amdgpu_buffer_rsrc_t r, int8_t *lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      r, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds)), 16, voff, 0, 0,
-      0);
-}
-
 template <int OUT_DT, int BN>
 __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) {
   constexpr int BM = 128, BK = kMidBK, S = kMidStages;
@@ -1960,6 +2076,20 @@ static bool mp_tiled_xcd() {
   return v;
 }
 
+// Column tiles (16 each) per workgroup of the direct-to-LDS skinny kernel for 3..32 rows, or 0 when it
+// does not take the launch: the fewest that leave at most one workgroup per CU (MP_W8_SKDMA=0 keeps
+// i8_skinny_kernel, for measurements).  Measured at K = 4096, N = 11008 against i8_skinny_kernel:
+// M = 4 / 8 / 16 / 32 12.3 / 12.3 / 12.3 / 14.4 against 15.8 / 15.9 / 15.5 / 24.4 us; M = 16 at
+// N = 4096 5.6 against 7.1 us, at K = 11008 13.4 against 17.5 us.
+static int mp_skdma_nct(const mp_i8_args &a) {
+  static const bool on = !(mp_knob("MP_W8_SKDMA") && atoi(mp_knob("MP_W8_SKDMA")) == 0);
+  if (!on || a.rows < 3 || a.rows > 32 || a.k < 4 * 128 || a.k % 128 != 0 || a.k >= (int64_t(1) << 23)) return 0;
+  const int64_t cus = mp_cu_count() > 0 ? mp_cu_count() : 256;
+  for (int nct = 1; nct <= 4; ++nct)
+    if (mp_cdiv(a.n, 16 * nct) <= cus) return nct;
+  return 0;
+}
+
 static bool mp_skinny_one_chunk() {
   static const bool v = !(mp_knob("MP_W8_SKINNY_ONE_CHUNK") && atoi(mp_knob("MP_W8_SKINNY_ONE_CHUNK")) == 0);
   return v;
@@ -2154,6 +2284,30 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
     else if (rsel == 4) MP_I8_GEMV(4);
     else MP_I8_GEMV(2);
 #undef MP_I8_GEMV
+  } else if (mp_skdma_nct(a) > 0 && aligned && epilogue == MP_EPI_DENSE) {
+    const int nct = mp_skdma_nct(a);
+    const int mt = a.rows <= 16 ? 1 : 2;
+    const dim3 grid(static_cast<unsigned>(mp_cdiv(a.n, 16 * nct)));
+#define MP_SD(MT_, NCT_)                                                                                      \
+  do {                                                                                                       \
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(i8_skinny_dma_kernel<MT_, NCT_>),                 \
+                            hipFuncAttributeMaxDynamicSharedMemorySize,                                      \
+                            static_cast<int>(skdma_smem(MT_, NCT_))) != hipSuccess)                          \
+      return MP_ERR_HIP;                                                                                     \
+    hipLaunchKernelGGL((i8_skinny_dma_kernel<MT_, NCT_>), grid, dim3(256), skdma_smem(MT_, NCT_), stream, a); \
+  } while (0)
+    if (mt == 1) {
+      if (nct == 1) MP_SD(1, 1);
+      else if (nct == 2) MP_SD(1, 2);
+      else if (nct == 3) MP_SD(1, 3);
+      else MP_SD(1, 4);
+    } else {
+      if (nct == 1) MP_SD(2, 1);
+      else if (nct == 2) MP_SD(2, 2);
+      else if (nct == 3) MP_SD(2, 3);
+      else MP_SD(2, 4);
+    }
+#undef MP_SD
   } else if (mp_skinny_takes(a.rows, a.n) && a.k % 64 == 0 && aligned && epilogue == MP_EPI_DENSE &&
              a.k <= INT32_MAX && a.n <= INT32_MAX) {
     const int mi = static_cast<int>(a.rows);

@@ -441,6 +441,9 @@ W8_CASES = [(1, 11008, 4096), (16, 11008, 4096), (5, 1000, 256), (17, 512, 1024)
             # mid-M kernel (64 .. 256 tiles of 128 x 128): partial row and column tiles, K of 1 to 9
             # steps of 128 (partial four-step loop groups), odd N (the unpaired store path)
             (200, 8200, 512), (65, 8320, 1152), (384, 2700, 640), (1000, 2048, 128), (129, 12001, 256),
+            # direct-to-LDS skinny kernel (3..32 rows, 1 to 4 column tiles per workgroup): two 16-row
+            # tiles, waves with one and two K steps, odd N, partial column tiles
+            (32, 2000, 640), (3, 5000, 512), (24, 16000, 1024), (13, 12001, 768),
             # tiled kernel: the LDS-staged 16-byte-store epilogue with partial row and column tiles
             # (N % 8 == 0), and the two-byte-store epilogue (N % 8 != 0)
             (200, 1000, 512), (100, 333, 512),
