@@ -472,6 +472,35 @@ def test_w8a8_gemm_bitexact(m, n, k, out):
     assert np.array_equal(got, ref.view(np.uint16))   # bar: bit-exact
 
 
+def _random_w8_shapes(count=40, seed=11):
+    """Seeded shapes across every W8A8 routing range: rows 1..1100, N 1..13000 (odd included), K a
+    multiple of 16, 64 or 128 from 16 to 4608."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        m = int(rng.choice([1, 2, 3, 5, 8, 13, 16, 17, 24, 31, 32, 33, 48, 64, 65, 97, 128, 200, 256, 300, 511, 1100]))
+        n = int(rng.integers(1, 13000))
+        k = int(rng.choice([16, 64, 128])) * int(rng.integers(1, 37))
+        if m * n * k <= 6e9:
+            out.append((m, n, k))
+    return out
+
+
+@pytest.mark.parametrize("m,n,k", _random_w8_shapes())
+def test_w8a8_gemm_random_shapes(m, n, k):
+    """Seeded shapes over every routing range of mp_w8a8_gemm (GEMV, both skinny kernels, tiled, mid-M,
+    large-M, the any-shape fallback): fp16 output bit-exact against the oracle."""
+    _say("w8a8 random", m, n, k)
+    rng = np.random.default_rng(m * 131 + n * 7 + k)
+    qx = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    qw = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    sx = (rng.random(m) * 0.01).astype(np.float32)
+    sw = (rng.random(n) * 0.001).astype(np.float32)
+    y = _ops().w8a8_gemm(_t(qx), _t(sx), _t(qw), _t(sw), None, torch.float16)
+    ref = O.w8a8_linear_runtime(qx, sx, qw, sw, None, out_dtype="fp16")
+    assert np.array_equal(_np(y).view(np.uint16), ref.view(np.uint16))   # bar: bit-exact
+
+
 def test_w8a8_gemm_large_rows_subset():
     """M = 4096, N = 11008, K = 4096 (BASELINE config): bit-exact on 96 sampled rows x all columns."""
     _say("w8a8 full size")
