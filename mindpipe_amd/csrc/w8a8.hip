@@ -1344,7 +1344,7 @@ __device__ __forceinline__ void grouped_epilogue(const mp_i8_args &p, const i16_
     const bool cval = col < p.n;
     const int64_t colc = cval ? col : p.n - 1;
     const float sg = sbexp[colc], su = sbexp[p.n + colc];
-    const int64_t pidx = nbase / 32;  // the row's abs-max slot: its 32-column output block
+    const int64_t pidx = static_cast<int64_t>(blockIdx.x) * 4 + (nbase % 128) / 32;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -1859,13 +1859,9 @@ __global__ __launch_bounds__(512) void i8_gemm_dma_kernel(mp_i8_args p, int tile
 constexpr int kMidStages = 4, kMidBK = 128;
 constexpr size_t mid_smem(int bn) { return static_cast<size_t>(kMidStages) * (128 + bn) * kMidBK; }
 
-template <int OUT_DT, int BN, int EPI = MP_EPI_DENSE>
+template <int OUT_DT, int BN>
 __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) {
   constexpr int BM = 128, BK = kMidBK, S = kMidStages;
-  // grouped expert launches (F32: GEMM2; SWIGLU: GEMM1, 64 gate rows then the 64 matching up rows)
-  constexpr bool GROUPED = EPI != MP_EPI_DENSE, SWI = EPI == MP_EPI_SWIGLU;
-  constexpr int OUTC = SWI ? BN / 2 : BN;  // output columns per tile
-  static_assert(!GROUPED || BN == 128, "grouped launches: 128 weight rows per tile");
   constexpr int WN = BN == 128 ? 2 : 1, WM = 4 / WN;  // waves along M and N
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // 32x32 tiles per wave
   constexpr int QW = (BM + BN) / 8 / 4;                // load instructions per wave per stage
@@ -1874,37 +1870,12 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
   extern __shared__ __attribute__((aligned(16))) int8_t smem_mid[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
+  const int bx = static_cast<int>(blockIdx.x);
+  const int tile_n = (bx / (8 * tiles_m)) * 8 + (bx & 7);
+  const int64_t m0 = static_cast<int64_t>((bx >> 3) % tiles_m) * BM;
+  const int64_t n0 = static_cast<int64_t>(tile_n) * BN;
+  if (n0 >= p.n || m0 >= p.rows) return;  // grid padding; workgroup-uniform, before any barrier
   const int64_t k = p.k;
-  int64_t m0, n0, row_end;
-  int e = 0;
-  if constexpr (GROUPED) {
-    // blockIdx.y: the slot-th 128-row tile over the experts' row groups (surplus slots exit)
-    int64_t slot = blockIdx.y;
-    bool found = false;
-    for (e = 0; e < p.n_experts; ++e) {
-      const int64_t lo = p.offsets[e], hi = p.offsets[e + 1];
-      const int64_t tiles = (hi - lo + BM - 1) / BM;
-      if (slot < tiles) {
-        m0 = lo + slot * BM;
-        row_end = hi < m0 + BM ? hi : m0 + BM;
-        found = true;
-        break;
-      }
-      slot -= tiles;
-    }
-    if (!found) return;  // workgroup-uniform, before any barrier
-    n0 = static_cast<int64_t>(blockIdx.x) * OUTC;
-  } else {
-    const int bx = static_cast<int>(blockIdx.x);
-    const int tile_n = (bx / (8 * tiles_m)) * 8 + (bx & 7);
-    m0 = static_cast<int64_t>((bx >> 3) % tiles_m) * BM;
-    n0 = static_cast<int64_t>(tile_n) * BN;
-    if (n0 >= p.n || m0 >= p.rows) return;  // grid padding; workgroup-uniform, before any barrier
-    row_end = p.rows - m0 < BM ? p.rows : m0 + BM;
-  }
-  const int64_t nb_rows = SWI ? 2 * p.n : p.n;  // weight rows per expert
-  const int8_t *bexp = p.b + (GROUPED ? static_cast<int64_t>(e) * nb_rows * k : 0);
-  const float *sbexp = p.s_b + (GROUPED ? static_cast<int64_t>(e) * nb_rows : 0);
 
   // load instruction q of this wave fills 8-row group g = 4 q + wave of the stage: q < 4 (g < 16) -> A
   // rows 8 g .. + 8, else B rows 8 (g - 16) .. + 8.  Lane l: row + l / 8, slot l % 8, global chunk
@@ -1913,12 +1884,9 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
   // outputs).  The launcher bounds K below 2^23, so 128 K bytes of rows and the 0x80000000 dead
   // offset stay apart.
   constexpr uint32_t kOob = 0x80000000u;
-  // grouped: B through a descriptor over the expert's whole weight (the launcher bounds it below 4 GiB),
-  // weight rows past N clamped (their outputs are dropped)
-  const int64_t a_rows = row_end - m0, b_rows = GROUPED ? nb_rows : (p.n - n0 < BN ? p.n - n0 : BN);
+  const int64_t a_rows = p.rows - m0 < BM ? p.rows - m0 : BM, b_rows = p.n - n0 < BN ? p.n - n0 : BN;
   const __amdgpu_buffer_rsrc_t arsrc = mp_rsrc(p.a + m0 * k, static_cast<uint32_t>(a_rows * k));
-  const __amdgpu_buffer_rsrc_t brsrc =
-      mp_rsrc(GROUPED ? bexp : p.b + n0 * k, static_cast<uint32_t>(b_rows * k));
+  const __amdgpu_buffer_rsrc_t brsrc = mp_rsrc(p.b + n0 * k, static_cast<uint32_t>(b_rows * k));
   uint32_t voff[QW];
   int ldst[QW];
 #pragma unroll
@@ -1927,19 +1895,7 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
     const int r0 = (4 * q + wave - (is_a ? 0 : BM / 8)) * 8;
     const int r = r0 + lane / 8;
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    if (!GROUPED || is_a) {
-      voff[q] = r < (is_a ? a_rows : b_rows) ? static_cast<uint32_t>(r * k + 16 * c) : kOob;
-    } else {
-      int64_t w;
-      if (SWI) {
-        int64_t oc = n0 + r % (BN / 2);
-        oc = oc < p.n ? oc : p.n - 1;
-        w = r < BN / 2 ? oc : p.n + oc;
-      } else {
-        w = n0 + r < p.n ? n0 + r : p.n - 1;
-      }
-      voff[q] = static_cast<uint32_t>(w * k + 16 * c);
-    }
+    voff[q] = r < (is_a ? a_rows : b_rows) ? static_cast<uint32_t>(r * k + 16 * c) : kOob;
     ldst[q] = (is_a ? 0 : BM * BK) + r0 * BK;
   }
   auto issue = [&](int64_t kt, int stage) {
@@ -1962,9 +1918,7 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
   // of 32, so the row's swizzle is that of l % 32)
   const int swz = (lane >> 1) & 7, half = lane >> 5;
   const int arow = (wm * TM * 32 + (lane & 31)) * BK;
-  // SwiGLU: tile j = 0 the wave's 32 gate rows, j = 1 the matching up rows
-  const int brow = BM * BK + ((SWI ? wn * 32 : wn * TN * 32) + (lane & 31)) * BK;
-  constexpr int BJ = SWI ? BN / 2 : 32;  // B rows between the wave's tiles j and j + 1
+  const int brow = BM * BK + (wn * TN * 32 + (lane & 31)) * BK;
   auto compute = [&](int stage) {
     const int8_t *st = smem_mid + stage * STAGE;
     i4_t af[4][TM], bf[4][TN];
@@ -1974,7 +1928,7 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
 #pragma unroll
       for (int i = 0; i < TM; ++i) af[ks][i] = *reinterpret_cast<const i4_t *>(st + arow + i * 32 * BK + sl);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(st + brow + j * BJ * BK + sl);
+      for (int j = 0; j < TN; ++j) bf[ks][j] = *reinterpret_cast<const i4_t *>(st + brow + j * 32 * BK + sl);
     }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -2013,12 +1967,8 @@ __global__ __launch_bounds__(256) void i8_mid_kernel(mp_i8_args p, int tiles_m) 
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS DMA outstanding at exit
 
-  if constexpr (GROUPED)
-    grouped_epilogue<EPI, TM>(p, acc, m0 + wm * TM * 32 + 4 * (lane >> 5), row_end, n0 + wn * (SWI ? 32 : 64), sbexp,
-                              lane);
-  else
-    big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * TM * 32 + 4 * (lane >> 5), n0 + wn * TN * 32, m0 + BM <= p.rows,
-                                 lane);
+  big_epilogue<OUT_DT, TM, TN>(p, acc, m0 + wm * TM * 32 + 4 * (lane >> 5), n0 + wn * TN * 32, m0 + BM <= p.rows,
+                               lane);
 }
 
 // Any-shape dense fallback: one thread per output.
@@ -2152,15 +2102,6 @@ static int mp_tiled_staged_ok(const mp_i8_args &a, int epilogue) {
          a.ldy % 8 == 0 && mp_aligned(a.y, 16);
 }
 
-// Grouped GEMMs on the direct-to-LDS mid-M kernel: 1 = on, 0 = off (MP_W8_MOE_MID, for measurements).
-static int mp_moe_mid() {
-  static int v = [] {
-    const char *e = mp_knob("MP_W8_MOE_MID");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
-
 // Dense GEMMs below the large-M range on the direct-to-LDS mid-M kernel when its 128x128 tiles number
 // from 64 to three quarters of the CUs (MP_W8_MID=0 keeps the register-staged tiled kernel, for
 // measurements).  Measured at K = 4096 against the tiled kernel, with 128-column tiles: M = 256 / 128,
@@ -2244,27 +2185,6 @@ int mp_launch_i8_gemm(const mp_i8_args &a, int epilogue, hipStream_t stream) {
   const bool aligned = mp_aligned(a.a, 16) && mp_aligned(a.b, 16) && a.ldy < (int64_t(1) << 23) &&
                        a.k < (int64_t(1) << 23);
   if (a.offsets) {
-    // grouped launches on the direct-to-LDS mid-M kernel (MP_W8_MOE_MID=1, for measurements)
-    const int64_t nb_rows_g = epilogue == MP_EPI_SWIGLU ? 2 * a.n : a.n;
-    if (mp_moe_mid() && aligned && (epilogue == MP_EPI_SWIGLU || epilogue == MP_EPI_F32) && a.k >= kMidBK &&
-        a.k % kMidBK == 0 && a.k < (int64_t(1) << 23) && nb_rows_g * a.k < (int64_t(1) << 32) &&
-        !a.shared_b && a.n_experts > 0) {
-      const bool swi = epilogue == MP_EPI_SWIGLU;
-      const int64_t n_tiles = mp_cdiv(a.n, swi ? 64 : 128);
-      const int64_t m_slots = mp_cdiv(a.rows, 128) + a.n_experts;
-      const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(m_slots));
-      const void *fn = swi ? reinterpret_cast<const void *>(i8_mid_kernel<MP_F32, 128, MP_EPI_SWIGLU>)
-                           : reinterpret_cast<const void *>(i8_mid_kernel<MP_F32, 128, MP_EPI_F32>);
-      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mid_smem(128))) !=
-          hipSuccess)
-        return MP_ERR_HIP;
-      if (swi)
-        hipLaunchKernelGGL((i8_mid_kernel<MP_F32, 128, MP_EPI_SWIGLU>), grid, dim3(256), mid_smem(128), stream, a, 1);
-      else
-        hipLaunchKernelGGL((i8_mid_kernel<MP_F32, 128, MP_EPI_F32>), grid, dim3(256), mid_smem(128), stream, a, 1);
-      MP_CHECK_LAUNCH();
-      return MP_OK;
-    }
     // experts of a few hundred rows (serving-size MoE): one workgroup per 256 rows of an
     // expert and weight slice, so each slice streams once per expert
     if (mp_moe_kernel() && aligned && a.k % kMoeBK == 0 && a.k <= (1 << 17) && a.n_experts <= kMoeMaxExperts &&
